@@ -1,0 +1,183 @@
+/*
+ * jit_moe.h -- C-ABI of the MI355X (gfx950) ragged-batch MoE decode step.
+ *
+ * One shared library (jitengine_amd/_lib/libjit_moe.so) exports these entry
+ * points.  They replace the Metal kernels of JITEngine's hot path; each
+ * declaration names the reference interface it stands in for (paths relative to
+ * the reference repository; Q36 = engines/qwen3.6-35b-a3b-m4pro/src/
+ * jitengine_qwen3_6_35b_a3b_m4pro, FN = engines/qwen3.8-flash-next-m4pro/src/
+ * jitengine_qwen3_8_flash_next_m4pro, FL = engines/flint-m4pro/src/
+ * jitengine_flint_m4pro).
+ *
+ * Conventions
+ *  - Every pointer argument is a device pointer unless its name ends in _host.
+ *  - bf16 tensors are uint16_t bit patterns; all tensors are dense row-major.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *  - Entry points check their scalar contract on the host before any launch and
+ *    return JIT_EINVAL (contract break, the reference's ValueError) or
+ *    JIT_EUNSUPPORTED (a shape outside the kernel's coverage, where the
+ *    reference would take its stock MLX fallback); JIT_ELAUNCH reports a HIP
+ *    launch failure.  jit_last_error() describes the last failure on the
+ *    calling thread.
+ *  - No entry point allocates device memory: workspaces are arguments.
+ *  - Calls are asynchronous on `stream`; device-side contents (expert ids,
+ *    page ids) are trusted, as the reference's kernels trust theirs
+ *    ("entry points validate nothing; callers gate them", FN/kernels/README.md:4).
+ *
+ * MLX 4-bit affine layout (Q36/linear.py:101-128): a quantized matrix [N, K] is
+ * w uint32 [N, K/8] (element j = nibble j%8 of word j/8, low nibble first),
+ * scales and biases bf16 [N, K/64]; value = scale * q + bias.  An expert stack
+ * prepends an expert axis [E, N, ...].
+ */
+#ifndef JIT_MOE_H
+#define JIT_MOE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JIT_OK 0
+#define JIT_EINVAL (-1)
+#define JIT_EUNSUPPORTED (-2)
+#define JIT_ELAUNCH (-3)
+
+/* Paged KV pool geometry fixed by the kernels. */
+#define JIT_PAGE_TOKENS 16
+#define JIT_HEAD_DIM 128
+
+/* Human-readable description of the last error returned on this thread. */
+const char *jit_last_error(void);
+
+/* Library version (monotonic integer). */
+int jit_version(void);
+
+/* ---------------------------------------------------------------- router --
+ * router_topk(logits[..., N] bf16, k, norm) -> (inds uint32[..., k],
+ * scores bf16[..., k]): softmax (fp32, stored bf16), exact top-k by rank in
+ * ascending (value, index) order, gathered gates, optional renormalisation by
+ * their sequential bf16 sum.
+ * Replaces Q36/kernels/router_topk.py:177-192 (router_topk) and the stock chain
+ * of Q36/model/moe.py:304-315.  Contract: rows >= 0, 0 < k <= N (else
+ * JIT_EINVAL, Q36/kernels/router_topk.py:41-42); N % 32 == 0 and N <= 1024
+ * (else JIT_EUNSUPPORTED, router_supported :171-174).
+ * gates_out (optional, may be NULL): the bf16 gates [rows, N]. */
+int jit_router_topk(const uint16_t *logits, int rows, int N, int k, int norm, uint32_t *inds,
+                    uint16_t *scores, uint16_t *gates_out, void *stream);
+
+/* topk(gates, k): the rank top-k alone on given bf16 gates [rows, N].
+ * Replaces Q36/kernels/router_topk.py:36-66 (topk / topk_stable).
+ * Contract: 0 < k <= N (JIT_EINVAL); N <= 1024 (JIT_EUNSUPPORTED). */
+int jit_topk(const uint16_t *gates, int rows, int N, int k, uint32_t *inds, void *stream);
+
+/* --------------------------------------------------------------- packing --
+ * Token-to-expert packing of the P = rows*k flat (row, slot) pairs of inds:
+ * a stable sort by expert id.  Replaces Q36/model/moe.py:151-159 (_sort_pairs:
+ * argsort, inverse argsort, order // k) and FN/model/moe/expert_mlp.py:39-49,
+ * 147-163 (stable argsort + np.unique -> seg_slot, seg_start, seg_cnt,
+ * pair_row).  Outputs (int32):
+ *   order[P]      flat pair index at sorted position p
+ *   pair_row[P]   order[p] / k (the activation row of sorted position p)
+ *   inv[P]        sorted position of flat pair f
+ *   expert_cnt[E], expert_off[E]    pairs per expert and first sorted position
+ *   seg_expert[E], seg_start[E], seg_cnt[E]   the first meta[0] entries list
+ *                 the non-empty experts in ascending order
+ *   meta[4]       {n_seg, max_cnt, bad_ids, 0}; bad_ids counts ids >= E (such
+ *                 pairs are dropped: they appear in no segment)
+ * Contract: P >= 0, k > 0, 0 < E <= 1024. */
+int jit_moe_pack(const uint32_t *inds, int P, int k, int E, int32_t *order, int32_t *pair_row,
+                 int32_t *inv, int32_t *expert_cnt, int32_t *expert_off, int32_t *seg_expert,
+                 int32_t *seg_start, int32_t *seg_cnt, int32_t *meta, void *stream);
+
+/* ------------------------------------------------ quantized projections --
+ * Dense 4-bit projection y[T, N] = x[T, K] . dequant(W[N, K])^T, fp32
+ * accumulation, bf16 out: QLinear.__call__ / .rows (Q36/linear.py:219-313,
+ * the qmv arithmetic of Q36/kernels/qmv_mrow.py), used for the router logits
+ * (Q36/model/moe.py:296-302) and the attention projections.
+ * Contract: T >= 0, N % 64 == 0, K % 256 == 0 (JIT_EUNSUPPORTED otherwise). */
+int jit_qmm(const uint16_t *x, int T, int K, const uint32_t *w, const uint16_t *scales,
+            const uint16_t *biases, int N, uint16_t *y, void *stream);
+
+/* Grouped gate||up projection with fused SwiGLU over packed pairs:
+ * for every sorted pair p of expert e, g, u = x[pair_row[p]] . dequant(Wgu_e)^T
+ * (gate rows [0, I), up rows [I, 2I) of the fused [E, 2I, K] stack),
+ * h[p] = bf16(bf16(g * sigmoid(g)) * u) with g, u and sigmoid(g) rounded to bf16.
+ * Replaces expert_gate_up_exact(_rows) (Q36/kernels/expert_solo.py:67-116,
+ * 213-232,359-401), the stock gate_up.gather + swiglu (Q36/model/moe.py:
+ * 191-193, Q36/kernels/elementwise.py:14-15) and FN's grouped_swiglu
+ * (FN/kernels/grouped_expert_qmv.py:345-371).  x [B, K] bf16; h [P, I] bf16 in
+ * sorted pair order.  Contract: I % 64 == 0, K % 256 == 0, 0 < E. */
+int jit_moe_gate_up_swiglu(const uint16_t *x, int K, const int32_t *pair_row,
+                           const int32_t *expert_cnt, const int32_t *expert_off, int E,
+                           const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
+                           int I, int P, uint16_t *h, void *stream);
+
+/* Grouped down projection over packed pairs: r[p] = bf16(h[p] . dequant(Wd_e)^T)
+ * for every sorted pair p of expert e (the down gather of Q36/model/moe.py:193;
+ * the per-expert GEMV inside expert_down_exact(_par),
+ * Q36/kernels/expert_solo.py:118-164,262-356).  h [P, I], r [P, D] bf16.
+ * Contract: D % 64 == 0, I % 256 == 0. */
+int jit_moe_down(const uint16_t *h, int I, const int32_t *expert_cnt, const int32_t *expert_off,
+                 int E, const uint32_t *w, const uint16_t *scales, const uint16_t *biases, int D,
+                 int P, uint16_t *r, void *stream);
+
+/* Weighted combine in slot order: y[b] = sum_j bf16(r[inv[b*k+j]] * score[b, j])
+ * with each product rounded to bf16 and a sequential bf16 sum over j = 0..k-1
+ * (Q36/kernels/expert_solo.py:1-6,155-163,307-315; stock
+ * (e * scores[..., None]).sum(-2), Q36/model/moe.py:286).  With resid != NULL,
+ * y[b] = bf16(resid[b] + that sum) (with_residual, Q36/model/moe.py:119-123). */
+int jit_moe_combine(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int B, int k,
+                    int D, const uint16_t *resid, uint16_t *y, void *stream);
+
+/* --------------------------------------------------------- paged KV pool --
+ * Pool layout (the build's design; the reference keeps one contiguous
+ * [1, Hkv, cap, Dh] buffer per request, Q36/kvcache/kv_cache.py:27-85):
+ * pool [num_pages, 2, Hkv, 16 * 128] bf16 per layer; part 0 of a page holds K
+ * slot-major ([slot][d]), part 1 holds V dim-major ([d][slot]).  Token t of
+ * sequence b is at page page_table[b * max_pages + t / 16], slot t % 16.
+ *
+ * KV append: write k, v [B, Hkv, 128] of row b at position pos[b]
+ * (KVSlot.append, Q36/kvcache/kv_cache.py:76-85).  Contract: Dh == 128. */
+int jit_kv_append_paged(const uint16_t *k, const uint16_t *v, int B, int Hkv, const int32_t *pos,
+                        const int32_t *page_table, int max_pages, uint16_t *pool, void *stream);
+
+/* Host-only split plan for paged decode attention: sequence b is cut into
+ * ceil(lens_host[b] / chunk) chunks of jit_attn_chunk_tokens(lens_host[b])
+ * keys, a pure function of the sequence's own length, so a row's result never
+ * depends on the rest of the batch (the property of FL/kernels/plan.py:50-57
+ * and Q36T/metal/engine/test_engine_consistency.py:43).  Fills
+ * chunk_start_host[B + 1] (exclusive prefix) and, when chunk_seq_host is not
+ * NULL, chunk_seq_host[c] = the sequence of chunk c (at most seq_cap entries);
+ * returns the total chunk count, negative on a contract break (lens < 1, or
+ * seq_cap too small). */
+int jit_attn_chunk_tokens(int len);
+int jit_attn_plan(const int32_t *lens_host, int B, int32_t *chunk_start_host,
+                  int32_t *chunk_seq_host, int seq_cap);
+
+/* Workspace bytes jit_paged_decode_attn needs for `total_chunks` chunks. */
+int64_t jit_attn_workspace_bytes(int total_chunks, int H);
+
+/* Paged GQA decode attention, one query per row: out[b, h] =
+ * softmax(scale * q[b, h] . K_b^T) . V_b over the first lens[b] tokens of
+ * sequence b, q head h reading kv head h / (H / Hkv).  Split-K over the key
+ * length with fp32 (max, sum, o) partials merged in chunk order.
+ * Replaces sdpa_decode / sdpa_decode_rows (Q36/kernels/sdpa_decode.py:448-476,
+ * the one- and two-pass kernels :16-74,217-315) and the split-K attention phase
+ * of Flint (FL/kernels/plan.py:42-59).  q, out [B, H, 128] bf16; chunk_start
+ * [B + 1] and chunk_seq [total_chunks] int32 (device copies of jit_attn_plan's
+ * output for these lens); workspace of jit_attn_workspace_bytes(total_chunks, H)
+ * bytes.  The pool must hold finite values in every slot of the pages read
+ * (the build's pool is zero-initialised).
+ * Contract: H % Hkv == 0, H / Hkv <= 16, Dh == 128, B >= 0 (JIT_EINVAL /
+ * JIT_EUNSUPPORTED, the checks of Q36/kernels/sdpa_decode.py:77-116). */
+int jit_paged_decode_attn(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,
+                          int max_pages, const int32_t *lens, const int32_t *chunk_start,
+                          const int32_t *chunk_seq, int B, int H, int Hkv, float scale,
+                          int total_chunks, void *workspace, uint16_t *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JIT_MOE_H */

@@ -1,0 +1,90 @@
+"""Loader of the C-ABI library libjit_moe.so (include/jit_moe.h) through ctypes.
+
+The library is the only compute path: if it is missing this module raises, it never falls back to
+anything else.  Build it with `python -m jitengine_amd.build` (or `__graft_entry__.build()`).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+from . import build as _build
+
+JIT_OK = 0
+JIT_EINVAL = -1
+JIT_EUNSUPPORTED = -2
+JIT_ELAUNCH = -3
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> argtypes (restype int unless listed in _RESTYPES)
+_SIGNATURES = {
+    "jit_last_error": [],
+    "jit_version": [],
+    "jit_router_topk": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
+    "jit_topk": [_P, _I, _I, _I, _P, _P],
+    "jit_moe_pack": [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "jit_qmm": [_P, _I, _I, _P, _P, _P, _I, _P, _P],
+    "jit_moe_gate_up_swiglu": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _P, _P],
+    "jit_moe_down": [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _P, _P],
+    "jit_moe_combine": [_P, _P, _P, _I, _I, _I, _P, _P, _P],
+    "jit_kv_append_paged": [_P, _P, _I, _I, _P, _P, _I, _P, _P],
+    "jit_attn_chunk_tokens": [_I],
+    "jit_attn_plan": [_P, _I, _P, _P, _I],
+    "jit_attn_workspace_bytes": [_I, _I],
+    "jit_paged_decode_attn": [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P, _P],
+}
+_RESTYPES = {"jit_last_error": ctypes.c_char_p, "jit_attn_workspace_bytes": ctypes.c_int64}
+
+_lib = None
+
+
+class JitError(RuntimeError):
+    """A HIP launch failure reported by the library."""
+
+
+class UnsupportedShape(ValueError):
+    """The shape is outside the kernel's coverage (where the reference takes its stock MLX op)."""
+
+
+def library_path() -> str:
+    return _build.LIB
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        path = _build.LIB
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"{path} is missing: the HIP extension is the only compute path; build it with "
+                "`python -m jitengine_amd.build`"
+            )
+        h = ctypes.CDLL(path)
+        for name, args in _SIGNATURES.items():
+            fn = getattr(h, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, _I)
+        _lib = h
+    return _lib
+
+
+def exported_symbols() -> list:
+    """The C-ABI entry points this module binds (each must exist in the library)."""
+    return sorted(_SIGNATURES)
+
+
+def check(rc: int, what: str) -> int:
+    """Turn a negative status into the matching Python exception."""
+    if rc >= 0:
+        return rc
+    msg = lib().jit_last_error().decode(errors="replace")
+    if rc == JIT_EINVAL:
+        raise ValueError(f"{what}: {msg}")
+    if rc == JIT_EUNSUPPORTED:
+        raise UnsupportedShape(f"{what}: {msg}")
+    raise JitError(f"{what}: {msg} (status {rc})")

@@ -1,0 +1,54 @@
+// Shared device helpers for the gfx950 kernels: bf16 conversion, MFMA operand
+// types, wave-level exchange, and the error plumbing of the C-ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "jit_moe.h"
+
+// ------------------------------------------------------------------ types
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+union Frag8 {  // 8 bf16 = one MFMA 16x16x32 operand fragment of one lane
+  bf16x8_t v;
+  uint32_t u[4];
+  uint4 q;
+};
+
+// ------------------------------------------------------------------ bf16
+__device__ __forceinline__ float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
+__device__ __forceinline__ float bf2f_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16 round-to-nearest-even (NaN kept quiet), the rounding of MLX's bf16 type.
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f2bf(lo) | (f2bf(hi) << 16);
+}
+
+// ------------------------------------------------------------------ wave
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+__device__ __forceinline__ float shfl_f(float v, int src) { return __shfl(v, src, 64); }
+
+__device__ __forceinline__ f32x4 mfma16x16x32(const Frag8 &a, const Frag8 &b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------------ host error plumbing
+namespace jit {
+void set_error(const char *fmt, ...);
+int fail(int code, const char *fmt, ...);
+int check_launch(const char *what);
+}  // namespace jit

@@ -1,0 +1,306 @@
+// Router top-k and token-to-expert packing for gfx950.
+//
+// Compiled with -ffp-contract=off: the softmax must produce the same fp32 bits
+// as the CPU restatement, because the expert indices derived from it are
+// compared bit for bit.  Every floating-point step below is a single IEEE
+// operation (add, multiply, divide, fused multiply-add, round-to-integer) in a
+// fixed order.
+#pragma clang fp contract(off)
+
+#include "common.hpp"
+
+namespace {
+
+// e^x for x <= 0: Cody-Waite reduction x = n ln2 + r with fdlibm's two-part ln2,
+// degree-7 Taylor polynomial of e^r in Horner form (|r| <= ln2/2), scaling by 2^n
+// through the exponent field; x <= -64 gives 0 so no subnormal is ever formed.
+__device__ __forceinline__ float exp_neg(float x) {
+  if (!(x > -64.0f)) return 0.0f;
+  const float t = x * 1.44269504088896341f;
+  const float n = __builtin_rintf(t);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.42860682030941723e-6f, r);
+  float p = 1.98412698412698413e-4f;
+  p = __builtin_fmaf(p, r, 1.38888888888888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666666666666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666666666666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int e = (int)n;
+  const float sc = __uint_as_float((uint32_t)(e + 127) << 23);
+  return p * sc;
+}
+
+constexpr int kRowsPerBlock = 4;  // one wave64 per token row
+constexpr int kMaxN = 1024;
+
+// One wave per row.  Lane l owns experts l, l+64, ...: it sums their exps in that
+// order, the wave adds the 64 partial sums by a butterfly over offsets 32..1
+// (every lane ends with the same total), then every gate is e_i * (1 / total)
+// rounded to bf16.  The top-k is the rank rule of the reference: the rank of
+// gate i counts the gates below it, ties broken by index, and ranks >= N-k fill
+// slots rank-(N-k) in ascending (value, index) order.
+template <int NPL, bool FROM_GATES>
+__global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t *__restrict__ src, int rows,
+                                                          int N, int k, int norm,
+                                                          uint32_t *__restrict__ inds,
+                                                          uint16_t *__restrict__ scores,
+                                                          uint16_t *__restrict__ gates_out) {
+  __shared__ float sg[kRowsPerBlock][kMaxN];
+  __shared__ int sidx[kRowsPerBlock][kMaxN];
+  const int w = threadIdx.x >> 6, l = lane_id();
+  const int row = blockIdx.x * kRowsPerBlock + w;
+  const bool valid = row < rows;
+  const uint16_t *lg = src + (size_t)(valid ? row : 0) * N;
+
+  if (FROM_GATES) {
+#pragma unroll
+    for (int j = 0; j < NPL; j++) {
+      const int i = l + 64 * j;
+      if (valid && i < N) sg[w][i] = bf2f(lg[i]);
+    }
+  } else {
+    float v[NPL], e[NPL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NPL; j++) {
+      const int i = l + 64 * j;
+      v[j] = (valid && i < N) ? bf2f(lg[i]) : -INFINITY;
+      mx = v[j] > mx ? v[j] : mx;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float y = shfl_xor_f(mx, o);
+      mx = y > mx ? y : mx;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPL; j++) {
+      const int i = l + 64 * j;
+      e[j] = (i < N) ? exp_neg(v[j] - mx) : 0.0f;
+      s = s + e[j];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s = s + shfl_xor_f(s, o);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int j = 0; j < NPL; j++) {
+      const int i = l + 64 * j;
+      if (valid && i < N) {
+        const uint32_t g = f2bf(e[j] * inv);
+        sg[w][i] = bf2f(g);
+        if (gates_out) gates_out[(size_t)row * N + i] = (uint16_t)g;
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < NPL; j++) {
+    const int i = l + 64 * j;
+    if (valid && i < N) {
+      const float v = sg[w][i];
+      int rank = 0;
+      for (int jj = 0; jj < N; jj++) {
+        const float u = sg[w][jj];
+        rank += (u < v) || (u == v && jj < i);
+      }
+      if (rank >= N - k) sidx[w][rank - (N - k)] = i;
+    }
+  }
+  __syncthreads();
+  if (valid && l == 0) {
+    if (scores == nullptr) {
+      for (int j = 0; j < k; j++) inds[(size_t)row * k + j] = (uint32_t)sidx[w][j];
+    } else {
+      float tot = 0.0f;
+      for (int j = 0; j < k; j++) {
+        const int e = sidx[w][j];
+        inds[(size_t)row * k + j] = (uint32_t)e;
+        tot = bf2f(f2bf(tot + sg[w][e]));
+      }
+      for (int j = 0; j < k; j++) {
+        const float sc = sg[w][sidx[w][j]];
+        scores[(size_t)row * k + j] = (uint16_t)(norm ? f2bf(sc / tot) : f2bf(sc));
+      }
+    }
+  }
+}
+
+template <bool FROM_GATES>
+int launch_router(const uint16_t *src, int rows, int N, int k, int norm, uint32_t *inds,
+                  uint16_t *scores, uint16_t *gates_out, hipStream_t st) {
+  const dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock), block(256);
+  const int npl = (N + 63) / 64;
+  if (npl <= 1)
+    router_topk_kernel<1, FROM_GATES><<<grid, block, 0, st>>>(src, rows, N, k, norm, inds, scores, gates_out);
+  else if (npl <= 2)
+    router_topk_kernel<2, FROM_GATES><<<grid, block, 0, st>>>(src, rows, N, k, norm, inds, scores, gates_out);
+  else if (npl <= 4)
+    router_topk_kernel<4, FROM_GATES><<<grid, block, 0, st>>>(src, rows, N, k, norm, inds, scores, gates_out);
+  else if (npl <= 8)
+    router_topk_kernel<8, FROM_GATES><<<grid, block, 0, st>>>(src, rows, N, k, norm, inds, scores, gates_out);
+  else
+    router_topk_kernel<16, FROM_GATES><<<grid, block, 0, st>>>(src, rows, N, k, norm, inds, scores, gates_out);
+  return jit::check_launch(FROM_GATES ? "jit_topk" : "jit_router_topk");
+}
+
+// --------------------------------------------------------------- packing
+// One workgroup of 1024 threads.  (1) per-expert counts in LDS; (2) exclusive
+// scans give each expert's first sorted position and the ascending list of
+// non-empty experts; (3) pairs are placed in tiles of 1024 in flat order: within
+// a wave, lanes holding the same expert id find each other with ballots over
+// the id's bits, so a pair's position is its expert's running offset plus the
+// pairs of that expert in earlier waves of the tile plus its rank among its own
+// wave's lanes -- a stable counting sort.
+constexpr int kPackThreads = 1024;
+constexpr int kPackWaves = kPackThreads / 64;
+
+__device__ __forceinline__ int wave_incl_scan(int x, int l) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (l >= o) x += y;
+  }
+  return x;
+}
+
+__global__ __launch_bounds__(kPackThreads) void moe_pack_kernel(
+    const uint32_t *__restrict__ inds, int P, int k, int E, int32_t *__restrict__ order,
+    int32_t *__restrict__ pair_row, int32_t *__restrict__ inv, int32_t *__restrict__ expert_cnt,
+    int32_t *__restrict__ expert_off, int32_t *__restrict__ seg_expert,
+    int32_t *__restrict__ seg_start, int32_t *__restrict__ seg_cnt, int32_t *__restrict__ meta) {
+  __shared__ int cnt[kPackThreads];
+  __shared__ int nxt[kPackThreads];
+  __shared__ unsigned short wcnt[kPackWaves][kPackThreads];
+  __shared__ int wsum[kPackWaves], wflag[kPackWaves], wmax[kPackWaves];
+  __shared__ int bad;
+  const int t = threadIdx.x, w = t >> 6, l = t & 63;
+  cnt[t] = 0;
+  if (t == 0) bad = 0;
+  __syncthreads();
+  for (int p = t; p < P; p += kPackThreads) {
+    const uint32_t e = inds[p];
+    if (e < (uint32_t)E)
+      atomicAdd(&cnt[e], 1);
+    else
+      atomicAdd(&bad, 1);
+  }
+  __syncthreads();
+  const int c = cnt[t];
+  const int f = c > 0 ? 1 : 0;
+  const int cs = wave_incl_scan(c, l);
+  const int fs = wave_incl_scan(f, l);
+  int mx = c;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = max(mx, __shfl_xor(mx, o, 64));
+  if (l == 63) {
+    wsum[w] = cs;
+    wflag[w] = fs;
+    wmax[w] = mx;
+  }
+  __syncthreads();
+  int cbase = 0, fbase = 0, tot_f = 0, tot_m = 0;
+  for (int ww = 0; ww < kPackWaves; ww++) {
+    if (ww < w) {
+      cbase += wsum[ww];
+      fbase += wflag[ww];
+    }
+    tot_f += wflag[ww];
+    tot_m = max(tot_m, wmax[ww]);
+  }
+  const int off = cbase + cs - c;
+  nxt[t] = off;
+  if (t < E) {
+    expert_cnt[t] = c;
+    expert_off[t] = off;
+    if (f) {
+      const int u = fbase + fs - 1;
+      seg_expert[u] = t;
+      seg_start[u] = off;
+      seg_cnt[u] = c;
+    }
+  }
+  if (t == 0) {
+    meta[0] = tot_f;
+    meta[1] = tot_m;
+    meta[2] = bad;
+    meta[3] = 0;
+  }
+  const int nbits = 32 - __clz(E);  // enough bits for ids 0..E (E = "no expert")
+  for (int base = 0; base < P; base += kPackThreads) {
+    const int p = base + t;
+    uint32_t e = p < P ? inds[p] : (uint32_t)E;
+    if (e > (uint32_t)E) e = (uint32_t)E;
+    unsigned long long m = ~0ull;
+    for (int bt = 0; bt < nbits; bt++) {
+      const int bit = (e >> bt) & 1u;
+      const unsigned long long bal = __ballot(bit);
+      m &= bit ? bal : ~bal;
+    }
+    const int rank = __popcll(m & ((1ull << l) - 1ull));
+    const int total = __popcll(m);
+    for (int idx = t; idx < kPackWaves * E; idx += kPackThreads) wcnt[idx / E][idx % E] = 0;
+    __syncthreads();
+    if (e < (uint32_t)E && rank == total - 1) wcnt[w][e] = (unsigned short)total;
+    __syncthreads();
+    if (e < (uint32_t)E) {
+      int pos = nxt[e] + rank;
+      for (int ww = 0; ww < w; ww++) pos += wcnt[ww][e];
+      order[pos] = p;
+      pair_row[pos] = p / k;
+      inv[p] = pos;
+    } else if (p < P) {
+      inv[p] = -1;
+    }
+    __syncthreads();
+    if (t < E) {
+      int s = 0;
+      for (int ww = 0; ww < kPackWaves; ww++) s += wcnt[ww][t];
+      nxt[t] += s;
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+extern "C" int jit_router_topk(const uint16_t *logits, int rows, int N, int k, int norm,
+                               uint32_t *inds, uint16_t *scores, uint16_t *gates_out,
+                               void *stream) {
+  if (rows < 0 || N <= 0 || !(0 < k && k <= N))
+    return jit::fail(JIT_EINVAL, "router_topk takes rows >= 0 and 0 < k <= N, got rows=%d N=%d k=%d",
+                     rows, N, k);
+  if (N % 32 != 0 || N > kMaxN)
+    return jit::fail(JIT_EUNSUPPORTED, "router_topk covers N %% 32 == 0 and N <= %d, got N=%d", kMaxN, N);
+  if (rows == 0) return JIT_OK;
+  if (!logits || !inds || !scores) return jit::fail(JIT_EINVAL, "router_topk: null pointer");
+  return launch_router<false>(logits, rows, N, k, norm, inds, scores, gates_out, (hipStream_t)stream);
+}
+
+extern "C" int jit_topk(const uint16_t *gates, int rows, int N, int k, uint32_t *inds, void *stream) {
+  if (rows < 0 || N <= 0 || !(0 < k && k <= N))
+    return jit::fail(JIT_EINVAL, "top-k takes 0 < k <= %d gates, not k = %d", N, k);
+  if (N > kMaxN) return jit::fail(JIT_EUNSUPPORTED, "topk covers N <= %d, got N=%d", kMaxN, N);
+  if (rows == 0) return JIT_OK;
+  if (!gates || !inds) return jit::fail(JIT_EINVAL, "topk: null pointer");
+  return launch_router<true>(gates, rows, N, k, 0, inds, nullptr, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int jit_moe_pack(const uint32_t *inds, int P, int k, int E, int32_t *order,
+                            int32_t *pair_row, int32_t *inv, int32_t *expert_cnt,
+                            int32_t *expert_off, int32_t *seg_expert, int32_t *seg_start,
+                            int32_t *seg_cnt, int32_t *meta, void *stream) {
+  if (P < 0 || k <= 0 || E <= 0 || P % k != 0)
+    return jit::fail(JIT_EINVAL, "moe_pack takes P >= 0 pairs in rows of k > 0 and E > 0, got P=%d k=%d E=%d",
+                     P, k, E);
+  if (E > kPackThreads) return jit::fail(JIT_EUNSUPPORTED, "moe_pack covers E <= %d, got %d", kPackThreads, E);
+  if (!expert_cnt || !expert_off || !seg_expert || !seg_start || !seg_cnt || !meta)
+    return jit::fail(JIT_EINVAL, "moe_pack: null pointer");
+  if (P > 0 && (!inds || !order || !pair_row || !inv)) return jit::fail(JIT_EINVAL, "moe_pack: null pointer");
+  moe_pack_kernel<<<1, kPackThreads, 0, (hipStream_t)stream>>>(inds, P, k, E, order, pair_row, inv,
+                                                              expert_cnt, expert_off, seg_expert,
+                                                              seg_start, seg_cnt, meta);
+  return jit::check_launch("jit_moe_pack");
+}

@@ -1,0 +1,56 @@
+"""The MoE block's routed-expert path on the HIP kernels.
+
+Mirrors the call sites of Qwen3_5MoeSparseMoeBlock (Q36/model/moe.py): the router logits
+(`_route_logits`, :296-302), the fused router top-k (`_route_top_k`, :304-315), token-to-expert
+packing (`_sort_pairs`, :151-159), gate||up + SwiGLU and down over the packed pairs (:191-193), and
+the slot-order weighted combine (:286) with the residual (`with_residual`, :119-123).  The
+BASELINE geometry has no shared expert, so there is no shared branch.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from .quant import QLinear
+
+
+class MoEBlock:
+    """Router + routed experts over ragged token rows x [B, D] (bf16, on the GPU)."""
+
+    def __init__(self, router: QLinear, gate_up: QLinear, down: QLinear, top_k: int = 8,
+                 norm_topk: bool = True):
+        for lin in (router, gate_up, down):
+            lin.validate()
+        if gate_up.weight.dim() != 3 or down.weight.dim() != 3:
+            raise ValueError("gate_up and down must be expert stacks [E, N, K]")
+        E = gate_up.weight.shape[0]
+        if down.weight.shape[0] != E or router.out_dims != E:
+            raise ValueError("router, gate_up and down disagree on the number of experts")
+        if down.in_dims * 2 != gate_up.out_dims or down.out_dims != gate_up.in_dims:
+            raise ValueError("down must be [E, D, I] for a gate_up stack [E, 2I, D]")
+        self.router, self.gate_up, self.down = router, gate_up, down
+        self.top_k = int(top_k)
+        self.norm_topk = bool(norm_topk)
+        self.num_experts = E
+
+    def route(self, x: torch.Tensor):
+        """(inds int32 [B, k], scores bf16 [B, k]) for rows x [B, D]."""
+        logits = ops.qmm(x, self.router)
+        return ops.router_topk(logits, self.top_k, self.norm_topk)
+
+    def experts(self, x: torch.Tensor, inds: torch.Tensor, scores: torch.Tensor,
+                resid: torch.Tensor | None = None) -> torch.Tensor:
+        """Every selected expert applied and combined: y [B, D] (+ resid)."""
+        pk = ops.moe_pack(inds, self.num_experts)
+        h = ops.expert_gate_up(x, self.gate_up, pk)
+        r = ops.expert_down(h, self.down, pk)
+        return ops.moe_combine(r, pk, scores, resid)
+
+    def __call__(self, x: torch.Tensor, resid: torch.Tensor | None = None) -> torch.Tensor:
+        inds, scores = self.route(x)
+        return self.experts(x, inds, scores, resid)
+
+    def with_residual(self, x: torch.Tensor, resid: torch.Tensor) -> torch.Tensor:
+        """resid + moe(x)."""
+        return self(x, resid)

@@ -1,0 +1,280 @@
+"""Torch-facing operators of the hot path, each a thin call into the C-ABI (include/jit_moe.h).
+
+Every function here mirrors a reference kernel entry point (named in its docstring) and calls the
+HIP library on the current torch stream; contract breaks raise ValueError as the reference's do,
+shapes outside the kernels' coverage raise UnsupportedShape.  There is no other compute path.
+Tensors: bf16 as torch.bfloat16, packed 4-bit words and expert ids as torch.int32.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from .quant import QLinear
+
+PAGE = 16
+HEAD_DIM = 128
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _need(t: torch.Tensor, dtype, name: str) -> None:
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+# ----------------------------------------------------------------------------- router
+def router_topk(logits: torch.Tensor, k: int, norm: bool, gates_out: bool = False):
+    """logits [..., N] bf16 -> (inds int32 [..., k], scores bf16 [..., k][, gates bf16 [..., N]]).
+
+    The fused router of Q36/kernels/router_topk.py:177-192 (softmax, rank top-k in ascending
+    (value, index) order, gather, optional bf16 renormalisation)."""
+    _need(logits, torch.bfloat16, "logits")
+    n = logits.shape[-1]
+    rows = logits.numel() // n if n else 0
+    shp = (*logits.shape[:-1], k)
+    inds = torch.empty(shp, dtype=torch.int32, device=logits.device)
+    scores = torch.empty(shp, dtype=torch.bfloat16, device=logits.device)
+    gates = torch.empty_like(logits) if gates_out else None
+    _lib.check(
+        _lib.lib().jit_router_topk(
+            _p(logits), rows, n, int(k), int(bool(norm)), _p(inds), _p(scores), _p(gates), _stream()
+        ),
+        "router_topk",
+    )
+    return (inds, scores, gates) if gates_out else (inds, scores)
+
+
+def topk(gates: torch.Tensor, k: int) -> torch.Tensor:
+    """gates [..., N] bf16 -> int32 [..., k]: topk_stable (Q36/kernels/router_topk.py:36-66)."""
+    _need(gates, torch.bfloat16, "gates")
+    n = gates.shape[-1]
+    rows = gates.numel() // n if n else 0
+    out = torch.empty((*gates.shape[:-1], k), dtype=torch.int32, device=gates.device)
+    _lib.check(_lib.lib().jit_topk(_p(gates), rows, n, int(k), _p(out), _stream()), "topk")
+    return out
+
+
+# ----------------------------------------------------------------------------- packing
+@dataclass
+class Packing:
+    """Packing tables of P = B*k (row, slot) pairs sorted stably by expert (jit_moe_pack)."""
+
+    order: torch.Tensor
+    pair_row: torch.Tensor
+    inv: torch.Tensor
+    expert_cnt: torch.Tensor
+    expert_off: torch.Tensor
+    seg_expert: torch.Tensor
+    seg_start: torch.Tensor
+    seg_cnt: torch.Tensor
+    meta: torch.Tensor
+    P: int
+    k: int
+    E: int
+
+
+def moe_pack(inds: torch.Tensor, n_experts: int) -> Packing:
+    """inds [B, k] int32 -> Packing: Q36/model/moe.py:151-159 (_sort_pairs) and
+    FN/model/moe/expert_mlp.py:39-49,147-163 (segment tables) in one launch."""
+    _need(inds, torch.int32, "inds")
+    k = inds.shape[-1]
+    P = inds.numel()
+    E = int(n_experts)
+    buf = torch.empty(3 * P + 5 * E + 4, dtype=torch.int32, device=inds.device)
+    parts = torch.split(buf, [P, P, P, E, E, E, E, E, 4])
+    pk = Packing(*parts, P=P, k=k, E=E)
+    _lib.check(
+        _lib.lib().jit_moe_pack(
+            _p(inds), P, k, E, _p(pk.order), _p(pk.pair_row), _p(pk.inv), _p(pk.expert_cnt),
+            _p(pk.expert_off), _p(pk.seg_expert), _p(pk.seg_start), _p(pk.seg_cnt), _p(pk.meta),
+            _stream(),
+        ),
+        "moe_pack",
+    )
+    return pk
+
+
+# ----------------------------------------------------------------------------- projections
+def qmm(x: torch.Tensor, lin: QLinear) -> torch.Tensor:
+    """x [T, K] bf16 -> [T, N] bf16 against a 4-bit matrix [N, K]: QLinear.__call__ / .rows
+    (Q36/linear.py:219-313)."""
+    _need(x, torch.bfloat16, "x")
+    if lin.weight.dim() != 2:
+        raise ValueError("qmm takes one [N, K] matrix")
+    lin.validate()
+    T, K = x.shape
+    if K != lin.in_dims:
+        raise ValueError(f"x has K = {K}, the matrix takes {lin.in_dims}")
+    y = torch.empty((T, lin.out_dims), dtype=torch.bfloat16, device=x.device)
+    _lib.check(
+        _lib.lib().jit_qmm(
+            _p(x), T, K, _p(lin.weight), _p(lin.scales), _p(lin.biases), lin.out_dims, _p(y), _stream()
+        ),
+        "qmm",
+    )
+    return y
+
+
+def expert_gate_up(x: torch.Tensor, gate_up: QLinear, pk: Packing) -> torch.Tensor:
+    """x [B, K] bf16, fused stack [E, 2I, K] -> h [P, I] bf16 in sorted pair order: the grouped
+    gate||up + SwiGLU (expert_gate_up_exact(_rows), Q36/kernels/expert_solo.py:213-232,380-401)."""
+    _need(x, torch.bfloat16, "x")
+    gate_up.validate()
+    E, two_i = gate_up.weight.shape[0], gate_up.out_dims
+    if x.shape[-1] != gate_up.in_dims or E != pk.E:
+        raise ValueError("x / stack / packing disagree on K or E")
+    I = two_i // 2
+    h = torch.empty((pk.P, I), dtype=torch.bfloat16, device=x.device)
+    _lib.check(
+        _lib.lib().jit_moe_gate_up_swiglu(
+            _p(x), x.shape[-1], _p(pk.pair_row), _p(pk.expert_cnt), _p(pk.expert_off), E,
+            _p(gate_up.weight), _p(gate_up.scales), _p(gate_up.biases), I, pk.P, _p(h), _stream(),
+        ),
+        "moe_gate_up",
+    )
+    return h
+
+
+def expert_down(h: torch.Tensor, down: QLinear, pk: Packing) -> torch.Tensor:
+    """h [P, I] bf16, stack [E, D, I] -> r [P, D] bf16 (the down gather, Q36/model/moe.py:193)."""
+    _need(h, torch.bfloat16, "h")
+    down.validate()
+    E, D = down.weight.shape[0], down.out_dims
+    if h.shape[-1] != down.in_dims or E != pk.E or h.shape[0] != pk.P:
+        raise ValueError("h / stack / packing disagree on I, E or P")
+    r = torch.empty((pk.P, D), dtype=torch.bfloat16, device=h.device)
+    _lib.check(
+        _lib.lib().jit_moe_down(
+            _p(h), h.shape[-1], _p(pk.expert_cnt), _p(pk.expert_off), E, _p(down.weight),
+            _p(down.scales), _p(down.biases), D, pk.P, _p(r), _stream(),
+        ),
+        "moe_down",
+    )
+    return r
+
+
+def moe_combine(r: torch.Tensor, pk: Packing, scores: torch.Tensor, resid: torch.Tensor | None = None):
+    """y [B, D] = sum over slots of bf16(r * score), sequential bf16 in slot order
+    (Q36/kernels/expert_solo.py:155-163), plus resid if given (with_residual)."""
+    _need(r, torch.bfloat16, "r")
+    _need(scores, torch.bfloat16, "scores")
+    B, k = scores.shape
+    D = r.shape[-1]
+    if resid is not None:
+        _need(resid, torch.bfloat16, "resid")
+        if resid.shape != (B, D):
+            raise ValueError("resid must be [B, D]")
+    y = torch.empty((B, D), dtype=torch.bfloat16, device=r.device)
+    _lib.check(
+        _lib.lib().jit_moe_combine(_p(r), _p(pk.inv), _p(scores), B, k, D, _p(resid), _p(y), _stream()),
+        "moe_combine",
+    )
+    return y
+
+
+# ----------------------------------------------------------------------------- paged KV
+def kv_append_paged(pool: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor,
+                    page_table: torch.Tensor) -> None:
+    """Write k, v [B, Hkv, 128] at positions pos [B] (KVSlot.append, Q36/kvcache/kv_cache.py:76-85)."""
+    _need(pool, torch.bfloat16, "pool")
+    _need(k, torch.bfloat16, "k")
+    _need(v, torch.bfloat16, "v")
+    _need(pos, torch.int32, "pos")
+    _need(page_table, torch.int32, "page_table")
+    B, Hkv, Dh = k.shape
+    if Dh != HEAD_DIM or v.shape != k.shape or pool.shape[2] != Hkv or pool.shape[3] != PAGE * HEAD_DIM:
+        raise ValueError("kv_append_paged: k/v [B, Hkv, 128] must match the pool [pages, 2, Hkv, 2048]")
+    _lib.check(
+        _lib.lib().jit_kv_append_paged(
+            _p(k), _p(v), B, Hkv, _p(pos), _p(page_table), page_table.shape[1], _p(pool), _stream()
+        ),
+        "kv_append_paged",
+    )
+
+
+@dataclass
+class AttnPlan:
+    """Split-K plan of one decode step: chunk boundaries per sequence (host and device copies)."""
+
+    lens: torch.Tensor         # int32 [B] (device)
+    chunk_start: torch.Tensor  # int32 [B + 1] (device)
+    chunk_seq: torch.Tensor    # int32 [total] (device)
+    total: int
+    lens_host: np.ndarray
+
+
+def attn_chunk_tokens(length: int) -> int:
+    return int(_lib.lib().jit_attn_chunk_tokens(int(length)))
+
+
+def attn_plan(lens_host, device) -> AttnPlan:
+    """Plan the split of every sequence into key chunks (jit_attn_plan, host only)."""
+    ln = np.ascontiguousarray(np.asarray(lens_host, dtype=np.int32))
+    B = ln.size
+    cs = np.empty(B + 1, np.int32)
+    total = _lib.check(
+        _lib.lib().jit_attn_plan(ln.ctypes.data_as(ctypes.c_void_p), B, cs.ctypes.data_as(ctypes.c_void_p), None, 0),
+        "attn_plan",
+    )
+    seq = np.empty(max(total, 1), np.int32)
+    _lib.check(
+        _lib.lib().jit_attn_plan(
+            ln.ctypes.data_as(ctypes.c_void_p), B, cs.ctypes.data_as(ctypes.c_void_p),
+            seq.ctypes.data_as(ctypes.c_void_p), int(seq.size),
+        ),
+        "attn_plan",
+    )
+    dev = torch.from_numpy(np.concatenate([ln, cs, seq])).to(device)
+    return AttnPlan(dev[:B], dev[B:2 * B + 1], dev[2 * B + 1:], int(total), ln)
+
+
+def attn_workspace_bytes(total_chunks: int, H: int) -> int:
+    return int(_lib.lib().jit_attn_workspace_bytes(int(total_chunks), int(H)))
+
+
+def paged_decode_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor,
+                           plan: AttnPlan, scale: float, workspace: torch.Tensor | None = None):
+    """q [B, H, 128] bf16 -> out [B, H, 128] bf16 over each sequence's first lens[b] keys of the
+    paged pool: sdpa_decode(_rows) (Q36/kernels/sdpa_decode.py:448-476) with split-K."""
+    _need(q, torch.bfloat16, "q")
+    _need(pool, torch.bfloat16, "pool")
+    _need(page_table, torch.int32, "page_table")
+    B, H, Dh = q.shape
+    Hkv = pool.shape[2]
+    if Dh != HEAD_DIM:
+        raise _lib.UnsupportedShape(f"paged_decode_attention covers head_dim 128, got {Dh}")
+    if plan.lens.shape[0] != B or page_table.shape[0] != B:
+        raise ValueError("q, page_table and plan disagree on the number of sequences")
+    if B and int((plan.lens_host.max() + PAGE - 1) // PAGE) > page_table.shape[1]:
+        raise ValueError(f"page_table has {page_table.shape[1]} columns, the longest sequence needs "
+                         f"{int((plan.lens_host.max() + PAGE - 1) // PAGE)}")
+    if H % Hkv or pool.shape[3] != PAGE * HEAD_DIM:
+        raise ValueError(f"{H} query heads over a pool of {Hkv} kv heads / page width {pool.shape[3]}")
+    need = attn_workspace_bytes(plan.total, H)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    out = torch.empty_like(q)
+    _lib.check(
+        _lib.lib().jit_paged_decode_attn(
+            _p(q), _p(pool), _p(page_table), page_table.shape[1], _p(plan.lens), _p(plan.chunk_start),
+            _p(plan.chunk_seq), B, H, Hkv, float(scale), plan.total, _p(workspace), _p(out), _stream(),
+        ),
+        "paged_decode_attn",
+    )
+    return out

@@ -1,0 +1,288 @@
+"""CPU oracle for the ragged MoE decode step -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package, and
+only as the checker; the product path (jitengine_amd) never imports it.  The arithmetic lives in
+jit_oracle.c (a C restatement of the reference's algorithm, each function citing the reference
+lines it follows); this module wraps it with numpy.  bf16 arrays are numpy uint16 bit patterns.
+
+Parity status of each function (how it is pinned, see tests/test_oracle.py):
+  exp_neg, softmax_bf16   vs float64 math.exp / softmax (closed form), within the stated ulps
+  topk_from_gates         vs numpy's stable argsort tail (a library routine), brute force
+  router_topk             composition of the two above + bf16 sequential sum vs torch bf16 ops
+  moe_pack                vs numpy stable argsort + np.unique (the FN reference's own calls)
+  dequant4                known-answer words + an independent numpy unpack
+  qmm                     vs torch float64 matmul of independently dequantized weights
+  qmv_mlx_f32             vs float64 within fp32 accumulation bounds (it is only an error yardstick)
+  swiglu_bf16             vs float64 silu(g) * u within bf16 rounding bounds
+  moe_gate_up / moe_down  vs qmm + swiglu composed in numpy (different code path, same maths)
+  moe_combine             vs torch bf16 ops in slot order (a library routine)
+  kv_append_paged/gather  integer addressing: round trip, page-permutation invariance
+  paged_decode_attn       vs torch scaled_dot_product_attention in float64 on gathered KV
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from . import build as _build
+
+_LIB = None
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+
+
+def lib():
+    """The loaded oracle library, built on first use if it is missing."""
+    global _LIB
+    if _LIB is None:
+        path = _build.LIB
+        if not os.path.exists(path):
+            _build.build()
+        _LIB = ctypes.CDLL(path)
+        _LIB.jo_exp_neg.restype = ctypes.c_float
+        _LIB.jo_exp_neg.argtypes = [ctypes.c_float]
+        _LIB.jo_bf2f.restype = ctypes.c_float
+        _LIB.jo_bf2f.argtypes = [ctypes.c_uint16]
+        _LIB.jo_f2bf.restype = ctypes.c_uint16
+        _LIB.jo_f2bf.argtypes = [ctypes.c_float]
+        _LIB.jo_swiglu_bf16.restype = ctypes.c_uint16
+        _LIB.jo_swiglu_bf16.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
+        _LIB.jo_paged_decode_attn.argtypes = [_P, _P, _P, _I, _P, _I, _I, _I, _I, ctypes.c_float, _P]
+        _LIB.jo_num_threads.restype = _I
+    return _LIB
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _check(rc: int, name: str) -> None:
+    if rc != 0:
+        raise ValueError(f"oracle {name} rejected its arguments (rc={rc})")
+
+
+def _u16(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint16)
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+# ----------------------------------------------------------------------------- bf16 helpers
+def f32_to_bf16(x) -> np.ndarray:
+    """Round float32 values to bf16 bit patterns (nearest-even), as the oracle and kernels do."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def num_threads() -> int:
+    return int(lib().jo_num_threads())
+
+
+def set_num_threads(n: int) -> None:
+    lib().jo_set_num_threads(int(n))
+
+
+def exp_neg(x: float) -> float:
+    return float(lib().jo_exp_neg(float(x)))
+
+
+def swiglu_bf16(g: int, u: int) -> int:
+    return int(lib().jo_swiglu_bf16(int(g), int(u)))
+
+
+# ----------------------------------------------------------------------------- router
+def softmax_bf16(logits) -> np.ndarray:
+    lg = _u16(logits)
+    rows, n = lg.reshape(-1, lg.shape[-1]).shape
+    g = np.empty_like(lg)
+    _check(lib().jo_softmax_bf16(_p(lg), rows, n, _p(g)), "softmax_bf16")
+    return g
+
+
+def topk_from_gates(gates, k: int) -> np.ndarray:
+    g = _u16(gates)
+    n = g.shape[-1]
+    rows = g.size // n
+    out = np.empty((*g.shape[:-1], k), dtype=np.uint32)
+    _check(lib().jo_topk_from_gates(_p(g), rows, n, int(k), _p(out)), "topk_from_gates")
+    return out
+
+
+def router_topk(logits, k: int, norm: bool):
+    """(inds uint32 [..., k], scores bf16 [..., k], gates bf16 [..., N])."""
+    lg = _u16(logits)
+    n = lg.shape[-1]
+    rows = lg.size // n
+    inds = np.empty((*lg.shape[:-1], k), dtype=np.uint32)
+    scores = np.empty((*lg.shape[:-1], k), dtype=np.uint16)
+    gates = np.empty_like(lg)
+    _check(
+        lib().jo_router_topk(_p(lg), rows, n, int(k), int(bool(norm)), _p(inds), _p(scores), _p(gates)),
+        "router_topk",
+    )
+    return inds, scores, gates
+
+
+# ----------------------------------------------------------------------------- packing
+def moe_pack(inds, n_experts: int) -> dict:
+    """Packing tables of the flat (row, slot) pairs of inds [B, k] (see jit_oracle.c)."""
+    ind = _u32(inds)
+    k = ind.shape[-1]
+    P = ind.size
+    E = int(n_experts)
+    out = {
+        "order": np.empty(P, np.int32),
+        "pair_row": np.empty(P, np.int32),
+        "inv": np.empty(P, np.int32),
+        "expert_cnt": np.empty(E, np.int32),
+        "expert_off": np.empty(E, np.int32),
+        "seg_expert": np.zeros(E, np.int32),
+        "seg_start": np.zeros(E, np.int32),
+        "seg_cnt": np.zeros(E, np.int32),
+        "meta": np.zeros(2, np.int32),
+    }
+    _check(
+        lib().jo_moe_pack(
+            _p(ind), P, k, E, _p(out["order"]), _p(out["pair_row"]), _p(out["inv"]),
+            _p(out["expert_cnt"]), _p(out["expert_off"]), _p(out["seg_expert"]),
+            _p(out["seg_start"]), _p(out["seg_cnt"]), _p(out["meta"]),
+        ),
+        "moe_pack",
+    )
+    return out
+
+
+# ----------------------------------------------------------------------------- quantized maths
+def dequant4(w, s, b) -> np.ndarray:
+    w, s, b = _u32(w), _u16(s), _u16(b)
+    N, K = w.shape[0], w.shape[1] * 8
+    out = np.empty((N, K), np.float64)
+    _check(lib().jo_dequant4(_p(w), _p(s), _p(b), N, K, _p(out)), "dequant4")
+    return out
+
+
+def qmm(x, w, s, b):
+    """x [T, K] bf16 against one [N, K] quantized matrix -> (float64 [T, N], bf16 [T, N])."""
+    x, w, s, b = _u16(x), _u32(w), _u16(s), _u16(b)
+    T, K = x.shape
+    N = w.shape[0]
+    f = np.empty((T, N), np.float64)
+    h = np.empty((T, N), np.uint16)
+    _check(lib().jo_qmm(_p(x), T, _p(w), _p(s), _p(b), N, K, _p(f), _p(h)), "qmm")
+    return f, h
+
+
+def qmv_mlx_f32(x, w, s, b) -> np.ndarray:
+    x, w, s, b = _u16(x), _u32(w), _u16(s), _u16(b)
+    T, K = x.shape
+    N = w.shape[0]
+    out = np.empty((T, N), np.float32)
+    _check(lib().jo_qmv_mlx_f32(_p(x), T, _p(w), _p(s), _p(b), N, K, _p(out)), "qmv_mlx_f32")
+    return out
+
+
+# ----------------------------------------------------------------------------- experts
+def moe_gate_up(x, inds, pack: dict, w, s, b) -> np.ndarray:
+    """h [P, I] bf16 in sorted pair order; w [E, 2I, D/8], s/b [E, 2I, D/64]."""
+    x, ind, w, s, b = _u16(x), _u32(inds), _u32(w), _u16(s), _u16(b)
+    B, D = x.shape
+    E, two_i = w.shape[0], w.shape[1]
+    P = ind.size
+    h = np.empty((P, two_i // 2), np.uint16)
+    _check(
+        lib().jo_moe_gate_up(
+            _p(x), B, D, _p(ind), P, _p(pack["order"]), _p(pack["pair_row"]), _p(w), _p(s), _p(b),
+            E, two_i // 2, _p(h),
+        ),
+        "moe_gate_up",
+    )
+    return h
+
+
+def moe_down(h, inds, pack: dict, w, s, b) -> np.ndarray:
+    """r [P, D] bf16 in sorted pair order; w [E, D, I/8], s/b [E, D, I/64]."""
+    h, ind, w, s, b = _u16(h), _u32(inds), _u32(w), _u16(s), _u16(b)
+    P, I = h.shape
+    E, D = w.shape[0], w.shape[1]
+    r = np.empty((P, D), np.uint16)
+    _check(
+        lib().jo_moe_down(_p(h), P, I, _p(ind), _p(pack["order"]), _p(w), _p(s), _p(b), E, D, _p(r)),
+        "moe_down",
+    )
+    return r
+
+
+def moe_combine(r, inv, scores) -> np.ndarray:
+    r, inv, sc = _u16(r), _i32(inv), _u16(scores)
+    B, k = sc.shape
+    D = r.shape[1]
+    y = np.empty((B, D), np.uint16)
+    _check(lib().jo_moe_combine(_p(r), _p(inv), _p(sc), B, k, D, _p(y)), "moe_combine")
+    return y
+
+
+def moe_experts(x, inds, scores, gu: tuple, dn: tuple, n_experts: int) -> dict:
+    """The whole routed-expert chain for given routing: pack -> gate_up -> down -> combine."""
+    pack = moe_pack(inds, n_experts)
+    h = moe_gate_up(x, inds, pack, *gu)
+    r = moe_down(h, inds, pack, *dn)
+    y = moe_combine(r, pack["inv"], scores)
+    return {"pack": pack, "h": h, "r": r, "y": y}
+
+
+# ----------------------------------------------------------------------------- paged KV
+PAGE = 16
+
+
+def kv_append_paged(pool, k, v, pos, page_table) -> None:
+    """In place: pool [num_pages, 2, Hkv, 16*Dh] bf16; k, v [B, Hkv, Dh]; pos [B]."""
+    assert pool.flags["C_CONTIGUOUS"] and pool.dtype == np.uint16
+    k, v, pos, pt = _u16(k), _u16(v), _i32(pos), _i32(page_table)
+    B, Hkv, Dh = k.shape
+    _check(
+        lib().jo_kv_append_paged(
+            _p(k), _p(v), B, Hkv, Dh, _p(pos), _p(pt), pt.shape[1], pool.shape[0], _p(pool)
+        ),
+        "kv_append_paged",
+    )
+
+
+def kv_gather(pool, page_row, n: int, Hkv: int, Dh: int):
+    """Contiguous K, V [Hkv, n, Dh] of one sequence's first n tokens."""
+    pr = _i32(page_row)
+    kc = np.empty((Hkv, n, Dh), np.uint16)
+    vc = np.empty((Hkv, n, Dh), np.uint16)
+    _check(lib().jo_kv_gather(_p(_u16(pool)), Hkv, Dh, _p(pr), int(n), _p(kc), _p(vc)), "kv_gather")
+    return kc, vc
+
+
+def paged_decode_attn(q, pool, page_table, lens, scale: float) -> np.ndarray:
+    """q [B, H, Dh] bf16 -> out [B, H, Dh] bf16 (float64 softmax attention over lens[b] tokens)."""
+    q, pool, pt, ln = _u16(q), _u16(pool), _i32(page_table), _i32(lens)
+    B, H, Dh = q.shape
+    Hkv = pool.shape[2]
+    out = np.empty_like(q)
+    _check(
+        lib().jo_paged_decode_attn(
+            _p(q), _p(pool), _p(pt), pt.shape[1], _p(ln), B, H, Hkv, Dh, float(scale), _p(out)
+        ),
+        "paged_decode_attn",
+    )
+    return out

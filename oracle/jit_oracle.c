@@ -1,0 +1,553 @@
+/*
+ * jit_oracle.c -- CPU restatement of JITEngine's ragged-batch MoE decode step.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker the HIP path is compared
+ * against; it is linked by tests/, by __graft_entry__.smoke() and by bench.py's
+ * cpu_baseline leg, and by nothing the product ships.  Each function cites the
+ * reference lines it restates (paths relative to the reference repository;
+ * Q36 = engines/qwen3.6-35b-a3b-m4pro/src/jitengine_qwen3_6_35b_a3b_m4pro,
+ * FN  = engines/qwen3.8-flash-next-m4pro/src/jitengine_qwen3_8_flash_next_m4pro,
+ * FL  = engines/flint-m4pro/src/jitengine_flint_m4pro).
+ *
+ * Number formats: bf16 is carried as uint16_t bit patterns; every rounding to
+ * bf16 is round-to-nearest-even from fp32 (jo_f2bf), the conversion MLX's bf16
+ * type performs.  Dot products of the quantized projections and attention are
+ * accumulated in float64 ("exact" relative to the fp32 arithmetic of both the
+ * reference and the GPU) and then rounded at the points where the reference
+ * rounds.  Integer work (top-k ranks, pair packing, page addressing) is exact.
+ *
+ * Build: oracle/build.py (gcc -O2 -fopenmp -ffp-contract=off -shared).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define JO_OK 0
+#define JO_EINVAL -1
+#define JO_ENOMEM -2
+
+/* ------------------------------------------------------------------ bf16 */
+static inline float bf2f(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static inline uint16_t f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float jo_bf2f(uint16_t h) { return bf2f(h); }
+uint16_t jo_f2bf(float f) { return f2bf(f); }
+
+/* ------------------------------------------------------- exp for x <= 0
+ * The router softmax needs the same fp32 bits on CPU and GPU (the expert
+ * indices are compared bit for bit), so the build pins its own exp rather than
+ * a platform libm or MLX's fast::exp (Q36/kernels/router_topk.py:116).
+ * Method: Cody-Waite range reduction x = n ln2 + r with the two-part ln2 split
+ * of fdlibm's expf, then the degree-7 Taylor polynomial of e^r on |r| <= ln2/2
+ * in Horner form with fused multiply-adds, then scaling by 2^n through the
+ * exponent field.  Inputs below -64 return 0 (e^-64 < 2^-92, far below the
+ * resolution of a sum that contains e^0 = 1), so no subnormal is ever formed.
+ * The HIP kernel (router_topk.hip) executes the identical operation sequence.
+ */
+float jo_exp_neg(float x) {
+  if (!(x > -64.0f)) return 0.0f;
+  const float t = x * 1.44269504088896341f;
+  const float n = rintf(t);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, 1.42860682030941723e-6f, r);
+  float p = 1.98412698412698413e-4f;
+  p = fmaf(p, r, 1.38888888888888889e-3f);
+  p = fmaf(p, r, 8.33333333333333333e-3f);
+  p = fmaf(p, r, 4.16666666666666667e-2f);
+  p = fmaf(p, r, 1.66666666666666667e-1f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int e = (int)n;
+  const uint32_t bits = (uint32_t)(e + 127) << 23;
+  float sc;
+  memcpy(&sc, &bits, 4);
+  return p * sc;
+}
+
+/* ------------------------------------------------------------ a2 router
+ * Softmax of one row of bf16 logits, stored as bf16 gates.  Restates the
+ * precise softmax of Q36/kernels/router_topk.py:86-133: fp32 max, exp(x - max),
+ * fp32 sum, one reciprocal, multiply, round to bf16.  The reduction order is
+ * the build's (MLX's simd_sum order is a hardware detail): 64 lanes, lane l
+ * holds indices l, l+64, ... and sums them in that order, then a butterfly over
+ * lane offsets 32, 16, 8, 4, 2, 1.
+ */
+static void softmax_row(const uint16_t *lg, int N, float *e, uint16_t *g) {
+  float mx = -INFINITY;
+  for (int i = 0; i < N; i++) {
+    const float v = bf2f(lg[i]);
+    mx = v > mx ? v : mx;
+  }
+  float part[64];
+  for (int l = 0; l < 64; l++) {
+    float s = 0.0f;
+    for (int i = l; i < N; i += 64) {
+      e[i] = jo_exp_neg(bf2f(lg[i]) - mx);
+      s = s + e[i];
+    }
+    part[l] = s;
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    float nxt[64];
+    for (int l = 0; l < 64; l++) nxt[l] = part[l] + part[l ^ o];
+    memcpy(part, nxt, sizeof part);
+  }
+  const float inv = 1.0f / part[0];
+  for (int i = 0; i < N; i++) g[i] = f2bf(e[i] * inv);
+}
+
+/* Exact top-k by rank (Q36/kernels/router_topk.py:14-28,135-145): the rank of
+ * gate i is #{j : g_j < g_i or (g_j == g_i and j < i)}; gates of rank >= N-k
+ * are selected and stored at slot rank-(N-k), i.e. ascending (value, index)
+ * order, slot k-1 holding the largest gate, a boundary tie going to the higher
+ * index -- the order mx.argpartition(g, kth=-k)[..., -k:] returns on Metal. */
+static void topk_rank_row(const uint16_t *g, int N, int k, uint32_t *inds) {
+  for (int i = 0; i < N; i++) {
+    const float v = bf2f(g[i]);
+    int rank = 0;
+    for (int j = 0; j < N; j++) {
+      const float u = bf2f(g[j]);
+      rank += (u < v) || (u == v && j < i);
+    }
+    if (rank >= N - k) inds[rank - (N - k)] = (uint32_t)i;
+  }
+}
+
+int jo_topk_from_gates(const uint16_t *gates, int rows, int N, int k, uint32_t *inds) {
+  if (rows < 0 || N <= 0 || k <= 0 || k > N) return JO_EINVAL;
+  for (int r = 0; r < rows; r++) topk_rank_row(gates + (size_t)r * N, N, k, inds + (size_t)r * k);
+  return JO_OK;
+}
+
+int jo_softmax_bf16(const uint16_t *logits, int rows, int N, uint16_t *gates) {
+  if (rows < 0 || N <= 0) return JO_EINVAL;
+  float *e = (float *)malloc(sizeof(float) * (size_t)N);
+  if (!e) return JO_ENOMEM;
+  for (int r = 0; r < rows; r++) softmax_row(logits + (size_t)r * N, N, e, gates + (size_t)r * N);
+  free(e);
+  return JO_OK;
+}
+
+/* The fused router (Q36/kernels/router_topk.py:72-192; stock chain
+ * Q36/model/moe.py:304-315): softmax, rank top-k, gather the k gates and, with
+ * norm, divide them by their sum accumulated sequentially in bf16 in slot order
+ * (router_topk.py:147-157). */
+int jo_router_topk(const uint16_t *logits, int rows, int N, int k, int norm, uint32_t *inds,
+                   uint16_t *scores, uint16_t *gates_out) {
+  if (rows < 0 || N <= 0 || k <= 0 || k > N) return JO_EINVAL;
+  float *e = (float *)malloc(sizeof(float) * (size_t)N);
+  uint16_t *g = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)N);
+  if (!e || !g) {
+    free(e);
+    free(g);
+    return JO_ENOMEM;
+  }
+  for (int r = 0; r < rows; r++) {
+    softmax_row(logits + (size_t)r * N, N, e, g);
+    if (gates_out) memcpy(gates_out + (size_t)r * N, g, sizeof(uint16_t) * (size_t)N);
+    uint32_t *ind = inds + (size_t)r * k;
+    uint16_t *sc = scores + (size_t)r * k;
+    topk_rank_row(g, N, k, ind);
+    uint16_t tot = 0;
+    for (int j = 0; j < k; j++) {
+      sc[j] = g[ind[j]];
+      tot = f2bf(bf2f(tot) + bf2f(sc[j]));
+    }
+    if (norm)
+      for (int j = 0; j < k; j++) sc[j] = f2bf(bf2f(sc[j]) / bf2f(tot));
+  }
+  free(e);
+  free(g);
+  return JO_OK;
+}
+
+/* ------------------------------------------------------------ a3 packing
+ * Token-to-expert packing.  Canonical order = stable sort of the flat (row,
+ * slot) pairs by expert id (Q36/model/moe.py:151-159 argsort / argsort;
+ * FN/model/moe/expert_mlp.py:39-49,147-163 stable argsort, np.unique ->
+ * seg_slot, seg_start, seg_cnt, pair_row = pos // k).  Outputs:
+ *   order[p]      flat pair index at sorted position p
+ *   pair_row[p]   = order[p] / k, the activation row of sorted position p
+ *   inv[f]        sorted position of flat pair f (inv[order[p]] = p)
+ *   expert_cnt[e], expert_off[e]  pairs per expert and their first position
+ *   seg_expert/seg_start/seg_cnt[u], u < n_seg: the non-empty experts ascending
+ *   meta[0] = n_seg, meta[1] = max_cnt
+ */
+int jo_moe_pack(const uint32_t *inds, int P, int k, int E, int32_t *order, int32_t *pair_row,
+                int32_t *inv, int32_t *expert_cnt, int32_t *expert_off, int32_t *seg_expert,
+                int32_t *seg_start, int32_t *seg_cnt, int32_t *meta) {
+  if (P < 0 || k <= 0 || E <= 0 || (P % k) != 0) return JO_EINVAL;
+  for (int p = 0; p < P; p++)
+    if (inds[p] >= (uint32_t)E) return JO_EINVAL;
+  for (int e = 0; e < E; e++) expert_cnt[e] = 0;
+  for (int p = 0; p < P; p++) expert_cnt[inds[p]]++;
+  int run = 0, u = 0, mc = 0;
+  for (int e = 0; e < E; e++) {
+    expert_off[e] = run;
+    if (expert_cnt[e] > 0) {
+      seg_expert[u] = e;
+      seg_start[u] = run;
+      seg_cnt[u] = expert_cnt[e];
+      u++;
+    }
+    if (expert_cnt[e] > mc) mc = expert_cnt[e];
+    run += expert_cnt[e];
+  }
+  int32_t *next = (int32_t *)malloc(sizeof(int32_t) * (size_t)E);
+  if (!next) return JO_ENOMEM;
+  memcpy(next, expert_off, sizeof(int32_t) * (size_t)E);
+  for (int p = 0; p < P; p++) {
+    const int pos = next[inds[p]]++;
+    order[pos] = p;
+    pair_row[pos] = p / k;
+    inv[p] = pos;
+  }
+  free(next);
+  meta[0] = u;
+  meta[1] = mc;
+  return JO_OK;
+}
+
+/* ------------------------------------------------- a10 MLX 4-bit affine
+ * Layout (Q36/linear.py:101-128, FN/kernels/qmv_row_blocked.py:23-33): a
+ * matrix [N, K] is weight uint32 [N, K/8] (element j of row n = nibble j%8 of
+ * word j/8, low nibble first), scales and biases bf16 [N, K/64], and
+ * w = scale * q + bias.  Dequantize one row into float64. */
+static void dequant_row(const uint32_t *w, const uint16_t *s, const uint16_t *b, int K, double *out) {
+  for (int j = 0; j < K; j++) {
+    const uint32_t q = (w[j >> 3] >> (4 * (j & 7))) & 0xfu;
+    out[j] = (double)bf2f(s[j >> 6]) * (double)q + (double)bf2f(b[j >> 6]);
+  }
+}
+
+int jo_dequant4(const uint32_t *w, const uint16_t *s, const uint16_t *b, int N, int K, double *out) {
+  if (N < 0 || K <= 0 || (K % 64) != 0) return JO_EINVAL;
+  for (int n = 0; n < N; n++)
+    dequant_row(w + (size_t)n * (K / 8), s + (size_t)n * (K / 64), b + (size_t)n * (K / 64), K,
+                out + (size_t)n * K);
+  return JO_OK;
+}
+
+/* Quantized projection y[t, n] = sum_j x[t, j] * w(n, j) for T rows, exact
+ * (float64) accumulation; out_f64 gets the sums, out_bf16 (if given) their
+ * bf16 rounding -- the value QLinear's quantized_matmul returns
+ * (Q36/linear.py:146-157). */
+int jo_qmm(const uint16_t *x, int T, const uint32_t *w, const uint16_t *s, const uint16_t *b, int N,
+           int K, double *out_f64, uint16_t *out_bf16) {
+  if (T < 0 || N < 0 || K <= 0 || (K % 64) != 0) return JO_EINVAL;
+#pragma omp parallel
+  {
+    double *row = (double *)malloc(sizeof(double) * (size_t)K);
+#pragma omp for schedule(static)
+    for (int n = 0; n < N; n++) {
+      dequant_row(w + (size_t)n * (K / 8), s + (size_t)n * (K / 64), b + (size_t)n * (K / 64), K, row);
+      for (int t = 0; t < T; t++) {
+        const uint16_t *xr = x + (size_t)t * K;
+        double acc = 0.0;
+        for (int j = 0; j < K; j++) acc += (double)bf2f(xr[j]) * row[j];
+        if (out_f64) out_f64[(size_t)t * N + n] = acc;
+        if (out_bf16) out_bf16[(size_t)t * N + n] = f2bf((float)acc);
+      }
+    }
+    free(row);
+  }
+  return JO_OK;
+}
+
+/* MLX qmv_fast's per-lane fp32 arithmetic for 4-bit group-64 weights, the
+ * reference's "stock" numerics (Q36/kernels/qmv_mrow.py:52-59 load_vector,
+ * :103-122 qdot, :140-160 and :179-207 the k-block loop): 32 lanes, lane l
+ * covers values [16l, 16l+16) of each 512-wide block; x is pre-scaled by 1,
+ * 1/16, 1/256, 1/4096 and summed; the nibbles are masked in place; each block
+ * adds scale*accum + sum*bias to the lane's result; the 32 lane results are
+ * summed by a butterfly (the simd_sum order is the hardware's, unpinned).
+ * Used only as the error yardstick of the no-worse-than-stock criterion
+ * (FN/kernels/selfcheck.py:313-331). */
+int jo_qmv_mlx_f32(const uint16_t *x, int T, const uint32_t *w, const uint16_t *s,
+                   const uint16_t *b, int N, int K, float *out) {
+  if (T < 0 || N < 0 || K <= 0 || (K % 512) != 0) return JO_EINVAL;
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; n++) {
+    const uint8_t *wb = (const uint8_t *)(w + (size_t)n * (K / 8));
+    const uint16_t *sr = s + (size_t)n * (K / 64), *br = b + (size_t)n * (K / 64);
+    for (int t = 0; t < T; t++) {
+      const uint16_t *xr = x + (size_t)t * K;
+      float lane[32];
+      for (int l = 0; l < 32; l++) {
+        float res = 0.0f;
+        for (int kb = 0; kb < K; kb += 512) {
+          const int k0 = kb + 16 * l;
+          float xt[16], sum = 0.0f;
+          for (int i = 0; i < 16; i += 4) {
+            const float a0 = bf2f(xr[k0 + i]), a1 = bf2f(xr[k0 + i + 1]);
+            const float a2 = bf2f(xr[k0 + i + 2]), a3 = bf2f(xr[k0 + i + 3]);
+            sum += ((a0 + a1) + a2) + a3;
+            xt[i] = a0;
+            xt[i + 1] = a1 / 16.0f;
+            xt[i + 2] = a2 / 256.0f;
+            xt[i + 3] = a3 / 4096.0f;
+          }
+          float accum = 0.0f;
+          for (int i = 0; i < 4; i++) {
+            const uint32_t ws = (uint32_t)wb[k0 / 2 + 2 * i] | ((uint32_t)wb[k0 / 2 + 2 * i + 1] << 8);
+            accum += (((xt[4 * i] * (float)(ws & 0x000fu)) + xt[4 * i + 1] * (float)(ws & 0x00f0u)) +
+                      xt[4 * i + 2] * (float)(ws & 0x0f00u)) +
+                     xt[4 * i + 3] * (float)(ws & 0xf000u);
+          }
+          const float sc = bf2f(sr[k0 / 64]), bi = bf2f(br[k0 / 64]);
+          res += sc * accum + sum * bi;
+        }
+        lane[l] = res;
+      }
+      for (int o = 16; o >= 1; o >>= 1) {
+        float nxt[32];
+        for (int l = 0; l < 32; l++) nxt[l] = lane[l] + lane[l ^ o];
+        memcpy(lane, nxt, sizeof lane);
+      }
+      out[(size_t)t * N + n] = lane[0];
+    }
+  }
+  return JO_OK;
+}
+
+/* ------------------------------------------------ a4 gate||up + SwiGLU
+ * One pair p (sorted position) against expert e's fused gate||up stack
+ * [2I, D]: g, u = x . dequant(W)^T, rounded to bf16; then, as the exact kernel
+ * does in bf16 (Q36/kernels/expert_solo.py:56-62,106-115):
+ *   sg = sigmoid(g) (MLX SigmoidX: y = 1/(1+e^|g|), g<0 ? y : 1-y), rounded;
+ *   sl = bf16(g * sg); h = bf16(sl * u).
+ * The sigmoid is evaluated in float64 from the bf16 g and rounded once. */
+static inline uint16_t swiglu_bf16(uint16_t gt, uint16_t ut) {
+  const double g = (double)bf2f(gt);
+  const double y = 1.0 / (1.0 + exp(fabs(g)));
+  const uint16_t sg = f2bf((float)(g < 0 ? y : 1.0 - y));
+  const uint16_t sl = f2bf(bf2f(gt) * bf2f(sg));
+  return f2bf(bf2f(sl) * bf2f(ut));
+}
+
+uint16_t jo_swiglu_bf16(uint16_t g, uint16_t u) { return swiglu_bf16(g, u); }
+
+/* h[p, :] for every sorted pair p; x [B, D] bf16; stacks [E, 2I, D/8] u32 and
+ * [E, 2I, D/64] bf16; pair_row/order from jo_moe_pack; inds the flat expert ids. */
+int jo_moe_gate_up(const uint16_t *x, int B, int D, const uint32_t *inds, int P, const int32_t *order,
+                   const int32_t *pair_row, const uint32_t *w, const uint16_t *s, const uint16_t *b,
+                   int E, int I, uint16_t *h) {
+  if (B < 0 || P < 0 || D <= 0 || (D % 64) != 0 || I <= 0) return JO_EINVAL;
+  const size_t ws = (size_t)2 * I * (D / 8), gs = (size_t)2 * I * (D / 64);
+#pragma omp parallel
+  {
+    double *gr = (double *)malloc(sizeof(double) * (size_t)D);
+    double *ur = (double *)malloc(sizeof(double) * (size_t)D);
+#pragma omp for schedule(dynamic, 4)
+    for (int n = 0; n < I; n++) {
+      int last_e = -1;
+      for (int p = 0; p < P; p++) {
+        const int e = (int)inds[order[p]];
+        if (e < 0 || e >= E) continue;
+        if (e != last_e) {
+          dequant_row(w + e * ws + (size_t)n * (D / 8), s + e * gs + (size_t)n * (D / 64),
+                      b + e * gs + (size_t)n * (D / 64), D, gr);
+          dequant_row(w + e * ws + (size_t)(I + n) * (D / 8), s + e * gs + (size_t)(I + n) * (D / 64),
+                      b + e * gs + (size_t)(I + n) * (D / 64), D, ur);
+          last_e = e;
+        }
+        const uint16_t *xr = x + (size_t)pair_row[p] * D;
+        double ga = 0.0, ua = 0.0;
+        for (int j = 0; j < D; j++) {
+          const double xv = (double)bf2f(xr[j]);
+          ga += xv * gr[j];
+          ua += xv * ur[j];
+        }
+        h[(size_t)p * I + n] = swiglu_bf16(f2bf((float)ga), f2bf((float)ua));
+      }
+    }
+    free(gr);
+    free(ur);
+  }
+  return JO_OK;
+}
+
+/* ---------------------------------------------------- a5 down + combine
+ * r[p, :] = bf16(h[p] . dequant(Wd_e)^T) for every sorted pair (the down
+ * gather's bf16 output, Q36/model/moe.py:193). */
+int jo_moe_down(const uint16_t *h, int P, int I, const uint32_t *inds, const int32_t *order,
+                const uint32_t *w, const uint16_t *s, const uint16_t *b, int E, int D, uint16_t *r) {
+  if (P < 0 || I <= 0 || (I % 64) != 0 || D <= 0) return JO_EINVAL;
+  const size_t ws = (size_t)D * (I / 8), gs = (size_t)D * (I / 64);
+#pragma omp parallel
+  {
+    double *row = (double *)malloc(sizeof(double) * (size_t)I);
+#pragma omp for schedule(dynamic, 16)
+    for (int n = 0; n < D; n++) {
+      int last_e = -1;
+      for (int p = 0; p < P; p++) {
+        const int e = (int)inds[order[p]];
+        if (e < 0 || e >= E) continue;
+        if (e != last_e) {
+          dequant_row(w + e * ws + (size_t)n * (I / 8), s + e * gs + (size_t)n * (I / 64),
+                      b + e * gs + (size_t)n * (I / 64), I, row);
+          last_e = e;
+        }
+        const uint16_t *hr = h + (size_t)p * I;
+        double acc = 0.0;
+        for (int j = 0; j < I; j++) acc += (double)bf2f(hr[j]) * row[j];
+        r[(size_t)p * D + n] = f2bf((float)acc);
+      }
+    }
+    free(row);
+  }
+  return JO_OK;
+}
+
+/* y[b, n] = sum over slots j = 0..k-1 of bf16(r_j * score_j), each product
+ * rounded to bf16 and the sum accumulated sequentially in bf16 in slot order
+ * (Q36/kernels/expert_solo.py:1-6,155-163,307-315; the stock
+ * (e * scores[..., None]).sum(-2) of Q36/model/moe.py:286). */
+int jo_moe_combine(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int B, int k, int D,
+                   uint16_t *y) {
+  if (B < 0 || k <= 0 || D <= 0) return JO_EINVAL;
+#pragma omp parallel for schedule(static)
+  for (int t = 0; t < B; t++) {
+    for (int n = 0; n < D; n++) {
+      uint16_t acc = 0;
+      for (int j = 0; j < k; j++) {
+        const uint16_t rv = r[(size_t)inv[t * k + j] * D + n];
+        const uint16_t pr = f2bf(bf2f(rv) * bf2f(scores[t * k + j]));
+        acc = f2bf(bf2f(acc) + bf2f(pr));
+      }
+      y[(size_t)t * D + n] = acc;
+    }
+  }
+  return JO_OK;
+}
+
+/* ----------------------------------------------------- a6/a7 paged KV
+ * Paged pool layout (the build's design; the reference keeps one contiguous
+ * [1, Hkv, cap, Dh] buffer per request, Q36/kvcache/kv_cache.py:27-85):
+ * pool [num_pages, 2, Hkv, 16 * Dh] bf16; part 0 of a page is K slot-major
+ * ([slot][d]), part 1 is V dim-major ([d][slot]).  Token t of sequence b lives
+ * in page page_table[b * max_pages + t / 16], slot t % 16. */
+#define JO_PAGE 16
+
+static inline size_t k_index(int page, int Hkv, int Dh, int h, int slot, int d) {
+  return (((size_t)page * 2 + 0) * Hkv + h) * (size_t)(JO_PAGE * Dh) + (size_t)slot * Dh + d;
+}
+static inline size_t v_index(int page, int Hkv, int Dh, int h, int slot, int d) {
+  return (((size_t)page * 2 + 1) * Hkv + h) * (size_t)(JO_PAGE * Dh) + (size_t)d * JO_PAGE + slot;
+}
+
+/* KVSlot.append restated for pages (Q36/kvcache/kv_cache.py:76-85): the k, v
+ * of row b ([B, Hkv, Dh]) go to position pos[b]. */
+int jo_kv_append_paged(const uint16_t *k, const uint16_t *v, int B, int Hkv, int Dh,
+                       const int32_t *pos, const int32_t *page_table, int max_pages, int num_pages,
+                       uint16_t *pool) {
+  if (B < 0 || Hkv <= 0 || Dh <= 0) return JO_EINVAL;
+  for (int b = 0; b < B; b++) {
+    if (pos[b] < 0 || pos[b] / JO_PAGE >= max_pages) return JO_EINVAL;
+    const int page = page_table[(size_t)b * max_pages + pos[b] / JO_PAGE];
+    if (page < 0 || page >= num_pages) return JO_EINVAL;
+    const int slot = pos[b] % JO_PAGE;
+    for (int h = 0; h < Hkv; h++)
+      for (int d = 0; d < Dh; d++) {
+        pool[k_index(page, Hkv, Dh, h, slot, d)] = k[((size_t)b * Hkv + h) * Dh + d];
+        pool[v_index(page, Hkv, Dh, h, slot, d)] = v[((size_t)b * Hkv + h) * Dh + d];
+      }
+  }
+  return JO_OK;
+}
+
+/* Gather the first n tokens of sequence b into contiguous [Hkv, n, Dh] K and V
+ * (the reference's KVSlot layout, the parity contract of the paged pool). */
+int jo_kv_gather(const uint16_t *pool, int Hkv, int Dh, const int32_t *page_row, int n, uint16_t *kc,
+                 uint16_t *vc) {
+  for (int h = 0; h < Hkv; h++)
+    for (int t = 0; t < n; t++) {
+      const int page = page_row[t / JO_PAGE], slot = t % JO_PAGE;
+      for (int d = 0; d < Dh; d++) {
+        kc[((size_t)h * n + t) * Dh + d] = pool[k_index(page, Hkv, Dh, h, slot, d)];
+        vc[((size_t)h * n + t) * Dh + d] = pool[v_index(page, Hkv, Dh, h, slot, d)];
+      }
+    }
+  return JO_OK;
+}
+
+/* Decode attention, one query per row, GQA (q head h reads kv head h / G), over
+ * the first lens[b] tokens: softmax(scale * q . K^T) . V, the result of
+ * sdpa_decode / mx.fast.scaled_dot_product_attention with mask=None
+ * (Q36/kernels/sdpa_decode.py:16-74,448-476; Q36/model/attention.py:70-74),
+ * evaluated in float64 and rounded to bf16 once.  q [B, H, Dh], out [B, H, Dh]. */
+int jo_paged_decode_attn(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,
+                         int max_pages, const int32_t *lens, int B, int H, int Hkv, int Dh, float scale,
+                         uint16_t *out) {
+  if (B < 0 || H <= 0 || Hkv <= 0 || (H % Hkv) != 0 || Dh <= 0) return JO_EINVAL;
+  for (int b = 0; b < B; b++)
+    if (lens[b] < 1 || (lens[b] + JO_PAGE - 1) / JO_PAGE > max_pages) return JO_EINVAL;
+  const int G = H / Hkv;
+#pragma omp parallel for schedule(dynamic, 1) collapse(2)
+  for (int b = 0; b < B; b++) {
+    for (int h = 0; h < H; h++) {
+      const int n = lens[b], kvh = h / G;
+      const int32_t *prow = page_table + (size_t)b * max_pages;
+      double *sc = (double *)malloc(sizeof(double) * (size_t)n);
+      double *acc = (double *)calloc((size_t)Dh, sizeof(double));
+      const uint16_t *qh = q + ((size_t)b * H + h) * Dh;
+      double mx = -INFINITY;
+      for (int t = 0; t < n; t++) {
+        const int page = prow[t / JO_PAGE], slot = t % JO_PAGE;
+        double dot = 0.0;
+        for (int d = 0; d < Dh; d++)
+          dot += (double)bf2f(qh[d]) * (double)bf2f(pool[k_index(page, Hkv, Dh, kvh, slot, d)]);
+        sc[t] = dot * (double)scale;
+        if (sc[t] > mx) mx = sc[t];
+      }
+      double den = 0.0;
+      for (int t = 0; t < n; t++) {
+        sc[t] = exp(sc[t] - mx);
+        den += sc[t];
+      }
+      for (int t = 0; t < n; t++) {
+        const int page = prow[t / JO_PAGE], slot = t % JO_PAGE;
+        for (int d = 0; d < Dh; d++)
+          acc[d] += sc[t] * (double)bf2f(pool[v_index(page, Hkv, Dh, kvh, slot, d)]);
+      }
+      uint16_t *o = out + ((size_t)b * H + h) * Dh;
+      for (int d = 0; d < Dh; d++) o[d] = f2bf((float)(acc[d] / den));
+      free(sc);
+      free(acc);
+    }
+  }
+  return JO_OK;
+}
+
+int jo_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+void jo_set_num_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}

@@ -1,0 +1,76 @@
+"""The C-ABI library loads, exports every entry point include/jit_moe.h declares, and checks its
+scalar contract on the host (no GPU work: every call here returns before any launch)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from jitengine_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "jit_moe.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(jit_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    declared = _declared()
+    assert len(declared) >= 14
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_lib.exported_symbols())
+    assert lib.jit_version() >= 1
+
+
+def test_contract_breaks_return_einval_before_launch():
+    lib = _lib.lib()
+    assert lib.jit_router_topk(None, 4, 128, 0, 1, None, None, None, None) == _lib.JIT_EINVAL
+    assert lib.jit_router_topk(None, 4, 128, 129, 1, None, None, None, None) == _lib.JIT_EINVAL
+    assert b"0 < k <= N" in lib.jit_last_error()
+    assert lib.jit_router_topk(None, 4, 100, 8, 1, None, None, None, None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_router_topk(None, 4, 2048, 8, 1, None, None, None, None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_topk(None, 1, 8, 9, None, None) == _lib.JIT_EINVAL
+    assert lib.jit_moe_pack(None, 10, 8, 128, *([None] * 9), None) == _lib.JIT_EINVAL  # P % k
+    assert lib.jit_moe_pack(None, 16, 8, 2000, *([None] * 9), None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_qmm(None, 4, 100, None, None, None, 64, None, None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_moe_down(None, 768 + 64, None, None, 8, None, None, None, 2048, 16, None, None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_paged_decode_attn(None, None, None, 4, None, None, None, 2, 30, 4, 0.1, 4, None, None, None) == _lib.JIT_EINVAL
+    assert lib.jit_paged_decode_attn(None, None, None, 4, None, None, None, 2, 64, 2, 0.1, 4, None, None, None) == _lib.JIT_EUNSUPPORTED
+    # empty work is a no-op, not an error
+    assert lib.jit_router_topk(None, 0, 128, 8, 1, None, None, None, None) == _lib.JIT_OK
+    with pytest.raises(ValueError):
+        _lib.check(_lib.JIT_EINVAL, "x")
+    with pytest.raises(_lib.UnsupportedShape):
+        _lib.check(_lib.JIT_EUNSUPPORTED, "x")
+
+
+def test_attn_plan_is_a_function_of_each_length():
+    lib = _lib.lib()
+    lens = np.array([1, 255, 256, 257, 16384, 16385, 262144], np.int32)
+    cs = np.zeros(lens.size + 1, np.int32)
+    seq = np.zeros(2000, np.int32)
+    total = lib.jit_attn_plan(lens.ctypes.data_as(ctypes.c_void_p), lens.size, cs.ctypes.data_as(ctypes.c_void_p),
+                              seq.ctypes.data_as(ctypes.c_void_p), seq.size)
+    ck = [lib.jit_attn_chunk_tokens(int(L)) for L in lens]
+    n = [-(-int(L) // c) for L, c in zip(lens, ck)]
+    assert ck == [256, 256, 256, 256, 256, 512, 512]
+    assert total == sum(n)
+    assert list(cs) == list(np.concatenate([[0], np.cumsum(n)]))
+    for b in range(lens.size):
+        assert np.all(seq[cs[b]:cs[b + 1]] == b)
+    bad = np.array([5, 0], np.int32)
+    assert lib.jit_attn_plan(bad.ctypes.data_as(ctypes.c_void_p), 2, cs.ctypes.data_as(ctypes.c_void_p), None, 0) == _lib.JIT_EINVAL
+
+
+def test_workspace_bytes():
+    lib = _lib.lib()
+    assert lib.jit_attn_workspace_bytes(10, 32) == 10 * 32 * 130 * 4

@@ -1,0 +1,252 @@
+"""HIP path vs the CPU oracle on the same seeded inputs (MI355X only).
+
+Integer outputs (expert ids, packing tables, KV bytes) must be bit-exact; bf16 outputs must meet
+the north-star tolerance (max-abs <= 2e-2, cosine >= 0.9995) and, for the quantized projections,
+the reference's own criterion (FN/kernels/selfcheck.py:313-331): the kernel's largest error against
+the float64 result is at most 8x that of the reference's fp32 arithmetic (restated in
+oracle.qmv_mlx_f32, rounded to bf16 as the reference returns it) plus 4 fp32 ulps of the scale."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from jitengine_amd import ops
+from jitengine_amd.moe import MoEBlock
+from jitengine_amd.quant import QLinear
+from tests.helpers import (
+    assert_close_bf16, bf16_tensor, bf16_to_f32, make_stack, normal_bf16, router_logits, stack_np, tie_gates, u16,
+)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _i32(a) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(DEV)
+
+
+def _dev(q: QLinear) -> QLinear:
+    return q.to(DEV)
+
+
+# ----------------------------------------------------------------------------- router
+@pytest.mark.parametrize("N", [128, 256])
+@pytest.mark.parametrize("norm", [True, False])
+def test_router_topk_bit_exact(N, norm):
+    for t in range(24):
+        B = 1 + t % 8
+        lg = router_logits(t % 4, B, N, seed=3000 + t)
+        inds, scores, gates = ops.router_topk(bf16_tensor(lg, DEV), 8, norm, gates_out=True)
+        wi, ws, wg = oracle.router_topk(lg, 8, norm)
+        assert np.array_equal(u16(gates), wg), t
+        assert np.array_equal(inds.cpu().numpy().view(np.uint32), wi), t
+        assert np.array_equal(u16(scores), ws), t
+
+
+@pytest.mark.parametrize("B", [64, 32, 2108, 1])
+def test_router_topk_config_rows(B):
+    lg = router_logits(2 if B == 1 else 0, B, 128, seed=B)
+    inds, scores = ops.router_topk(bf16_tensor(lg, DEV), 8, True)
+    wi, ws, _ = oracle.router_topk(lg, 8, True)
+    assert np.array_equal(inds.cpu().numpy().view(np.uint32), wi)
+    assert np.array_equal(u16(scores), ws)
+
+
+@pytest.mark.parametrize("N,k", [(256, 8), (128, 8), (1024, 16), (64, 64)])
+def test_topk_from_gates_bit_exact(N, k):
+    for t in range(12):
+        g = tie_gates(3, N, seed=400 + t) if t % 2 else oracle.softmax_bf16(router_logits(t % 4, 3, N, seed=400 + t))
+        got = ops.topk(bf16_tensor(g, DEV), k).cpu().numpy().view(np.uint32)
+        assert np.array_equal(got, oracle.topk_from_gates(g, k)), t
+
+
+# ----------------------------------------------------------------------------- packing
+@pytest.mark.parametrize("B,k,E", [(64, 8, 128), (32, 8, 128), (1, 8, 128), (2108, 8, 128), (300, 5, 7), (3, 8, 1024)])
+def test_pack_bit_exact(B, k, E):
+    rng = np.random.default_rng(B + E)
+    if E < k:
+        inds = rng.integers(0, E, (B, k)).astype(np.uint32)
+    else:
+        inds = np.stack([rng.permutation(E)[:k] for _ in range(B)]).astype(np.uint32)
+    pk = ops.moe_pack(_i32(inds), E)
+    want = oracle.moe_pack(inds, E)
+    U = int(want["meta"][0])
+    for name in ("order", "pair_row", "inv", "expert_cnt", "expert_off"):
+        assert np.array_equal(getattr(pk, name).cpu().numpy(), want[name]), name
+    for name in ("seg_expert", "seg_start", "seg_cnt"):
+        assert np.array_equal(getattr(pk, name).cpu().numpy()[:U], want[name][:U]), name
+    meta = pk.meta.cpu().numpy()
+    assert meta[0] == U and meta[1] == want["meta"][1] and meta[2] == 0
+
+
+# ----------------------------------------------------------------------------- projections
+def _fn_criterion(got_u16, x, w, s, b, f64):
+    stock = oracle.f32_to_bf16(oracle.qmv_mlx_f32(x, w, s, b))
+    e_got = np.abs(bf16_to_f32(got_u16) - f64).max()
+    e_stock = np.abs(bf16_to_f32(stock) - f64).max()
+    scale = np.abs(f64).max()
+    assert e_stock <= 2.0**-6 * scale
+    assert e_got <= 8 * e_stock + 4 * 2.0**-24 * scale, (e_got, e_stock)
+
+
+@pytest.mark.parametrize("T", [1, 3, 16, 17, 40])
+@pytest.mark.parametrize("N,K", [(128, 2048), (512, 2048), (256, 4096), (2048, 768 + 256)])
+def test_qmm_parity(T, N, K):
+    q = make_stack((N, K), seed=N + K)
+    w, s, b = stack_np(q)
+    x = normal_bf16((T, K), seed=T)
+    y = ops.qmm(bf16_tensor(x, DEV), _dev(q))
+    f64, want = oracle.qmm(x, w, s, b)
+    assert_close_bf16(u16(y), want, what="qmm")
+    if K % 512 == 0:
+        _fn_criterion(u16(y), x, w, s, b, f64)
+
+
+def _moe_inputs(B, E, D, I, seed):
+    gu = make_stack((E, 2 * I, D), seed=seed + 1)
+    dn = make_stack((E, D, I), seed=seed + 2)
+    x = normal_bf16((B, D), seed=seed + 3)
+    inds, scores, _ = oracle.router_topk(router_logits(0, B, E, seed=seed + 4), 8, True)
+    return gu, dn, x, inds, scores
+
+
+@pytest.mark.parametrize("B,E", [(64, 16), (5, 16), (1, 128)])
+def test_gate_up_swiglu_parity(B, E):
+    gu, dn, x, inds, scores = _moe_inputs(B, E, 2048, 768, seed=50 + B)
+    pk = ops.moe_pack(_i32(inds), E)
+    h = ops.expert_gate_up(bf16_tensor(x, DEV), _dev(gu), pk)
+    want = oracle.moe_gate_up(x, inds, oracle.moe_pack(inds, E), *stack_np(gu))
+    st = assert_close_bf16(u16(h), want, what="gate_up")
+    assert st["bit_equal"] > 0.95, st
+
+
+@pytest.mark.parametrize("B,E", [(64, 16), (7, 128)])
+def test_down_parity(B, E):
+    gu, dn, x, inds, scores = _moe_inputs(B, E, 2048, 768, seed=70 + B)
+    opk = oracle.moe_pack(inds, E)
+    h = oracle.moe_gate_up(x, inds, opk, *stack_np(gu))
+    pk = ops.moe_pack(_i32(inds), E)
+    r = ops.expert_down(bf16_tensor(h, DEV), _dev(dn), pk)
+    want = oracle.moe_down(h, inds, opk, *stack_np(dn))
+    st = assert_close_bf16(u16(r), want, what="down")
+    assert st["bit_equal"] > 0.95, st
+
+
+@pytest.mark.parametrize("resid", [False, True])
+def test_combine_bit_exact(resid):
+    B, k, D, E = 33, 8, 2048, 128
+    rng = np.random.default_rng(5)
+    inds = np.stack([rng.permutation(E)[:k] for _ in range(B)]).astype(np.uint32)
+    scores = oracle.router_topk(router_logits(1, B, E, seed=6), k, True)[1]
+    r = normal_bf16((B * k, D), seed=7)
+    pk = ops.moe_pack(_i32(inds), E)
+    rs = normal_bf16((B, D), seed=8)
+    y = ops.moe_combine(bf16_tensor(r, DEV), pk, bf16_tensor(scores, DEV), bf16_tensor(rs, DEV) if resid else None)
+    want = oracle.moe_combine(r, oracle.moe_pack(inds, E)["inv"], scores)
+    if resid:
+        want = oracle.f32_to_bf16(bf16_to_f32(rs) + bf16_to_f32(want))
+    assert np.array_equal(u16(y), want)
+
+
+def test_moe_block_chain():
+    """Router logits -> top-k -> experts -> combine + residual, each stage checked against the
+    oracle applied to the GPU's own input of that stage (routing is bit-exact given the logits)."""
+    B, E, D, I = 48, 32, 2048, 768
+    router = make_stack((E, D), seed=91)
+    gu = make_stack((E, 2 * I, D), seed=92)
+    dn = make_stack((E, D, I), seed=93)
+    blk = MoEBlock(_dev(router), _dev(gu), _dev(dn), top_k=8)
+    x = normal_bf16((B, D), seed=94)
+    res = normal_bf16((B, D), seed=95)
+    xt = bf16_tensor(x, DEV)
+    logits = ops.qmm(xt, blk.router)
+    _, want_logits = oracle.qmm(x, *stack_np(router))
+    assert_close_bf16(u16(logits), want_logits, what="router logits")
+    inds, scores = ops.router_topk(logits, 8, True)
+    wi, ws, _ = oracle.router_topk(u16(logits), 8, True)
+    assert np.array_equal(inds.cpu().numpy().view(np.uint32), wi)
+    assert np.array_equal(u16(scores), ws)
+    y = blk.experts(xt, inds, scores, bf16_tensor(res, DEV))
+    out = oracle.moe_experts(x, wi, ws, stack_np(gu), stack_np(dn), E)
+    want = oracle.f32_to_bf16(bf16_to_f32(res) + bf16_to_f32(out["y"]))
+    assert_close_bf16(u16(y), want, what="moe block")
+    y2 = blk(xt, bf16_tensor(res, DEV))
+    assert torch.equal(y2, y)
+
+
+# ----------------------------------------------------------------------------- paged KV
+def _pool(lens, seed, Hkv=4, H=32, extra=5):
+    rng = np.random.default_rng(seed)
+    npg = [-(-L // 16) for L in lens]
+    total = sum(npg) + extra
+    perm = rng.permutation(total)
+    table = np.zeros((len(lens), max(npg)), np.int32)
+    at = 0
+    for i, n in enumerate(npg):
+        table[i, :n] = perm[at:at + n]
+        at += n
+    pool = normal_bf16((total, 2, Hkv, 16 * 128), seed=seed + 1)
+    q = normal_bf16((len(lens), H, 128), seed=seed + 2)
+    return q, pool, table
+
+
+def test_kv_append_bit_exact():
+    lens = [5, 40, 17, 1]
+    _, pool, table = _pool(lens, seed=11)
+    k = normal_bf16((4, 4, 128), seed=12)
+    v = normal_bf16((4, 4, 128), seed=13)
+    pos = np.array([4, 39, 16, 0], np.int32)
+    pt = bf16_tensor(pool, DEV)
+    ops.kv_append_paged(pt, bf16_tensor(k, DEV), bf16_tensor(v, DEV), _i32(pos), _i32(table))
+    want = pool.copy()
+    oracle.kv_append_paged(want, k, v, pos, table)
+    assert np.array_equal(u16(pt), want)
+
+
+LENS = [1, 7, 16, 17, 31, 32, 33, 255, 256, 257, 300, 1023, 1024, 1500, 4095, 4096, 6000, 9000, 16384, 16385, 20000]
+
+
+def _attn(q, pool, table, lens, scale=128 ** -0.5):
+    plan = ops.attn_plan(lens, DEV)
+    out = ops.paged_decode_attention(bf16_tensor(q, DEV), bf16_tensor(pool, DEV), _i32(table), plan, scale)
+    return u16(out)
+
+
+def test_paged_attention_parity():
+    q, pool, table = _pool(LENS, seed=21)
+    got = _attn(q, pool, table, LENS)
+    want = oracle.paged_decode_attn(q, pool, table, LENS, 128 ** -0.5)
+    for b, L in enumerate(LENS):
+        assert_close_bf16(got[b], want[b], max_abs=2e-2, min_cos=0.9995, what=f"attention L={L}")
+
+
+def test_paged_attention_one_key_is_its_value():
+    q, pool, table = _pool([1, 1], seed=31)
+    got = _attn(q, pool, table, [1, 1])
+    for b in range(2):
+        kc, vc = oracle.kv_gather(pool, table[b], 1, 4, 128)
+        assert np.array_equal(got[b].reshape(4, 8, 128), np.repeat(vc[:, :1], 8, 1))
+
+
+def test_paged_attention_batched_row_equals_solo_and_page_permutation():
+    lens = [300, 5000, 17, 20000]
+    q, pool, table = _pool(lens, seed=41)
+    batched = _attn(q, pool, table, lens)
+    for b in range(len(lens)):
+        solo = _attn(q[b:b + 1], pool, table[b:b + 1], lens[b:b + 1])
+        assert np.array_equal(solo[0], batched[b]), b
+    perm = np.random.default_rng(42).permutation(pool.shape[0])
+    pool2 = np.empty_like(pool)
+    pool2[perm] = pool
+    assert np.array_equal(_attn(q, pool2, perm[table].astype(np.int32), lens), batched)
+
+
+def test_paged_attention_gqa_shapes():
+    for H, Hkv in [(16, 2), (8, 8), (64, 4)]:
+        q, pool, table = _pool([70, 3000], seed=H + Hkv, H=H, Hkv=Hkv)
+        got = _attn(q, pool, table, [70, 3000])
+        want = oracle.paged_decode_attn(q, pool, table, [70, 3000], 128 ** -0.5)
+        assert_close_bf16(got, want, what=f"H={H} Hkv={Hkv}")

@@ -1,0 +1,289 @@
+"""Pins of the CPU oracle (oracle/jit_oracle.c) against what fixes each function independently:
+closed forms, library routines (numpy / torch float64 and bf16 ops), known-answer vectors and
+invariants.  The reference holds no golden vectors for this path (its tests recompute stock MLX
+live, Q36T/metal/kernels/*), so these are the oracle's anchors; the recipes (tie-heavy router
+draws, lengths either side of the split-K switch) follow the reference's tests."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import bf16_to_f32, f32_to_bf16, make_stack, normal_bf16, router_logits, stack_np, tie_gates
+
+
+# ----------------------------------------------------------------------------- bf16 + exp
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(50000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 50000),
+                        np.array([0.0, -0.0, np.inf, -np.inf, 1.0 + 2**-8, 1.0 + 3 * 2**-8], np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(f32_to_bf16(x), want)
+    lib = oracle.lib()
+    for v in x[:2000]:
+        assert lib.jo_f2bf(float(v)) == f32_to_bf16(np.array([v], np.float32))[0]
+
+
+def test_exp_neg_close_to_exp():
+    xs = np.concatenate([np.linspace(-63.99, 0.0, 20001), -np.geomspace(1e-8, 63.0, 2000), [0.0, -1e-30]])
+    worst = 0.0
+    for x in xs.astype(np.float32):
+        got = oracle.exp_neg(float(x))
+        want = math.exp(float(x))
+        worst = max(worst, abs(got - want) / want)
+    assert worst < 4 * 2.0**-24, worst  # within 2 ulp of e^x
+    assert oracle.exp_neg(0.0) == 1.0
+    assert oracle.exp_neg(-64.0) == 0.0 and oracle.exp_neg(-1e9) == 0.0
+
+
+# ----------------------------------------------------------------------------- router
+@pytest.mark.parametrize("N", [32, 128, 256, 1024])
+def test_softmax_within_one_ulp_of_float64(N):
+    for kind in range(4):
+        lg = router_logits(kind, 8, N, seed=10 + kind)
+        g = oracle.softmax_bf16(lg)
+        x = bf16_to_f32(lg).astype(np.float64)
+        p = np.exp(x - x.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        want = bf16_to_f32(f32_to_bf16(p.astype(np.float32))).astype(np.float64)
+        got = bf16_to_f32(g).astype(np.float64)
+        ulp = np.maximum(np.abs(want), 2.0**-126) * 2.0**-7
+        assert np.all(np.abs(got - want) <= ulp + 1e-30), kind
+
+
+def _argpartition_tail(g_u16: np.ndarray, k: int) -> np.ndarray:
+    """The ids MLX's stable argpartition puts last, in its order: a stable ascending sort by value
+    (ties keep index order), last k -- numpy's stable argsort is that sort."""
+    v = bf16_to_f32(g_u16)
+    return np.argsort(v, axis=-1, kind="stable")[..., -k:].astype(np.uint32)
+
+
+@pytest.mark.parametrize("N,k", [(256, 8), (128, 8), (128, 4), (64, 64), (32, 1)])
+def test_topk_rank_rule_equals_stable_sort_tail(N, k):
+    for t in range(60):
+        if t % 3 == 2:
+            g = tie_gates(2, N, seed=1000 + t)
+        else:
+            g = oracle.softmax_bf16(router_logits(t % 4, 2, N, seed=1000 + t))
+        assert np.array_equal(oracle.topk_from_gates(g, k), _argpartition_tail(g, k)), t
+
+
+def test_topk_contract():
+    with pytest.raises(ValueError):
+        oracle.topk_from_gates(np.zeros((1, 8), np.uint16), 0)
+    with pytest.raises(ValueError):
+        oracle.topk_from_gates(np.zeros((1, 8), np.uint16), 9)
+
+
+@pytest.mark.parametrize("norm", [True, False])
+def test_router_is_softmax_topk_gather_and_bf16_renorm(norm):
+    for t in range(24):
+        lg = router_logits(t % 4, 1 + t % 8, 128, seed=2000 + t)
+        inds, scores, gates = oracle.router_topk(lg, 8, norm)
+        assert np.array_equal(gates, oracle.softmax_bf16(lg))
+        assert np.array_equal(inds, _argpartition_tail(gates, 8))
+        sc = torch.from_numpy(np.take_along_axis(gates, inds.astype(np.int64), -1).view(np.int16)).view(torch.bfloat16)
+        if norm:
+            tot = torch.zeros(sc.shape[0], dtype=torch.bfloat16)
+            for j in range(8):  # sequential bf16 sum in slot order
+                tot = tot + sc[:, j]
+            sc = sc / tot[:, None]
+        assert np.array_equal(scores, sc.view(torch.int16).numpy().view(np.uint16))
+
+
+# ----------------------------------------------------------------------------- packing
+@pytest.mark.parametrize("B,k,E", [(64, 8, 128), (32, 8, 128), (1, 8, 128), (200, 8, 16), (5, 3, 7), (0, 8, 128)])
+def test_pack_equals_numpy_stable_argsort_and_unique(B, k, E):
+    rng = np.random.default_rng(B * 31 + E)
+    inds = np.stack([rng.permutation(E)[:k] for _ in range(B)]).astype(np.uint32) if B else np.zeros((0, k), np.uint32)
+    if E < 10 and B:
+        inds = rng.integers(0, E, (B, k)).astype(np.uint32)  # repeats inside a row too
+    pk = oracle.moe_pack(inds, E)
+    flat = inds.reshape(-1).astype(np.int64)
+    order = np.argsort(flat, kind="stable")
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    uniq, start, cnt = np.unique(flat[order], return_index=True, return_counts=True)
+    assert np.array_equal(pk["order"], order)
+    assert np.array_equal(pk["inv"], inv)
+    assert np.array_equal(pk["pair_row"], order // k)
+    U = int(pk["meta"][0])
+    assert U == uniq.size and int(pk["meta"][1]) == (int(cnt.max()) if cnt.size else 0)
+    assert np.array_equal(pk["seg_expert"][:U], uniq)
+    assert np.array_equal(pk["seg_start"][:U], start)
+    assert np.array_equal(pk["seg_cnt"][:U], cnt)
+    full = np.bincount(flat, minlength=E)
+    assert np.array_equal(pk["expert_cnt"], full)
+    assert np.array_equal(pk["expert_off"], np.concatenate([[0], np.cumsum(full)[:-1]]))
+
+
+def test_pack_rejects_bad_ids():
+    with pytest.raises(ValueError):
+        oracle.moe_pack(np.array([[0, 200]], np.uint32), 128)
+
+
+# ----------------------------------------------------------------------------- dequant / qmm
+def test_dequant_known_answer():
+    # word 0x76543210 holds nibbles 0..7 low first; scale 2, bias -1 -> 2q - 1
+    w = np.full((1, 8), 0x76543210, np.uint32)
+    s = f32_to_bf16(np.array([[2.0]], np.float32))
+    b = f32_to_bf16(np.array([[-1.0]], np.float32))
+    got = oracle.dequant4(w, s, b)
+    assert np.array_equal(got[0], np.tile(2.0 * np.arange(8) - 1.0, 8))
+    w2 = np.array([[0xF0000000] + [0] * 7], np.uint32)  # only element 7 is 15
+    got2 = oracle.dequant4(w2, f32_to_bf16(np.array([[1.0]], np.float32)), f32_to_bf16(np.array([[0.0]], np.float32)))
+    assert got2[0, 7] == 15.0 and got2[0].sum() == 15.0
+
+
+def test_dequant_matches_independent_unpack():
+    q = make_stack((40, 256), seed=3)
+    w, s, b = stack_np(q)
+    nib = (w.view(np.uint8)[..., None] >> np.array([0, 4], np.uint8)) & 0xF  # bytes, low nibble first
+    nib = nib.reshape(40, 256).astype(np.float64)
+    want = nib * np.repeat(bf16_to_f32(s), 64, -1) + np.repeat(bf16_to_f32(b), 64, -1)
+    assert np.array_equal(oracle.dequant4(w, s, b), want)
+
+
+def test_qmm_matches_torch_float64_matmul():
+    q = make_stack((96, 512), seed=4)
+    w, s, b = stack_np(q)
+    x = normal_bf16((5, 512), seed=5)
+    f, h = oracle.qmm(x, w, s, b)
+    nib = ((w.view(np.uint8)[..., None] >> np.array([0, 4], np.uint8)) & 0xF).reshape(96, 512)
+    dq = torch.from_numpy(nib.astype(np.float64) * np.repeat(bf16_to_f32(s), 64, -1) + np.repeat(bf16_to_f32(b), 64, -1))
+    want = torch.from_numpy(bf16_to_f32(x).astype(np.float64)) @ dq.T
+    assert np.allclose(f, want.numpy(), rtol=1e-12, atol=1e-12)
+    assert np.array_equal(h, f32_to_bf16(f.astype(np.float32)))
+
+
+def test_mlx_lane_order_is_fp32_accurate():
+    q = make_stack((64, 1024), seed=6)
+    w, s, b = stack_np(q)
+    x = normal_bf16((3, 1024), seed=7)
+    f, _ = oracle.qmm(x, w, s, b)
+    m = oracle.qmv_mlx_f32(x, w, s, b).astype(np.float64)
+    bound = 1024 * 2.0**-22 * (np.abs(bf16_to_f32(x)).astype(np.float64) @ np.abs(oracle.dequant4(w, s, b)).T)
+    assert np.all(np.abs(m - f) <= bound)
+    assert np.abs(m - f).max() > 0  # fp32, not float64
+
+
+# ----------------------------------------------------------------------------- experts
+def test_swiglu_within_bf16_rounding_of_exact():
+    rng = np.random.default_rng(8)
+    g = f32_to_bf16((rng.standard_normal(4000) * 3).astype(np.float32))
+    u = f32_to_bf16((rng.standard_normal(4000) * 3).astype(np.float32))
+    got = np.array([oracle.swiglu_bf16(a, c) for a, c in zip(g, u)], np.uint16)
+    gf, uf = bf16_to_f32(g).astype(np.float64), bf16_to_f32(u).astype(np.float64)
+    want = gf / (1 + np.exp(-gf)) * uf
+    err = np.abs(bf16_to_f32(got) - want)
+    assert np.all(err <= 4 * 2.0**-8 * np.abs(want) + 1e-30)  # three bf16 roundings
+
+
+def _moe_case(B=24, E=16, D=512, I=256, seed=0):
+    gu = make_stack((E, 2 * I, D), seed=seed + 1)
+    dn = make_stack((E, D, I), seed=seed + 2)
+    x = normal_bf16((B, D), seed=seed + 3)
+    lg = router_logits(0, B, E, seed=seed + 4)
+    inds, scores, _ = oracle.router_topk(lg, 8, True)
+    return x, inds, scores, stack_np(gu), stack_np(dn)
+
+
+def test_gate_up_equals_per_pair_qmm_and_swiglu():
+    x, inds, scores, gu, dn = _moe_case()
+    pk = oracle.moe_pack(inds, 16)
+    h = oracle.moe_gate_up(x, inds, pk, *gu)
+    I = h.shape[1]
+    flat = inds.reshape(-1)
+    for p in range(0, pk["order"].size, 7):
+        e, r = int(flat[pk["order"][p]]), int(pk["pair_row"][p])
+        _, g = oracle.qmm(x[r:r + 1], gu[0][e, :I], gu[1][e, :I], gu[2][e, :I])
+        _, u = oracle.qmm(x[r:r + 1], gu[0][e, I:], gu[1][e, I:], gu[2][e, I:])
+        want = np.array([oracle.swiglu_bf16(a, c) for a, c in zip(g[0], u[0])], np.uint16)
+        assert np.array_equal(h[p], want), p
+
+
+def test_down_and_combine_equal_torch_bf16_composition():
+    x, inds, scores, gu, dn = _moe_case(seed=10)
+    out = oracle.moe_experts(x, inds, scores, gu, dn, 16)
+    pk, h, r = out["pack"], out["h"], out["r"]
+    flat = inds.reshape(-1)
+    for p in range(0, pk["order"].size, 11):
+        e = int(flat[pk["order"][p]])
+        _, want = oracle.qmm(h[p:p + 1], dn[0][e], dn[1][e], dn[2][e])
+        assert np.array_equal(r[p], want[0])
+    rt = torch.from_numpy(r.view(np.int16)).view(torch.bfloat16)
+    st = torch.from_numpy(scores.view(np.int16)).view(torch.bfloat16)
+    B, k = scores.shape
+    y = torch.zeros((B, r.shape[1]), dtype=torch.bfloat16)
+    for j in range(k):  # products rounded to bf16, sequential bf16 sum in slot order
+        y = y + rt[pk["inv"].reshape(B, k)[:, j]] * st[:, j:j + 1]
+    assert np.array_equal(out["y"], y.view(torch.int16).numpy().view(np.uint16))
+
+
+# ----------------------------------------------------------------------------- paged KV / attention
+def _pool_case(lens, Hkv=4, H=32, seed=0, extra_pages=3):
+    rng = np.random.default_rng(seed)
+    pages_per = [-(-L // 16) for L in lens]
+    num_pages = sum(pages_per) + extra_pages
+    perm = rng.permutation(num_pages)
+    width = max(pages_per)
+    table = np.zeros((len(lens), width), np.int32)
+    at = 0
+    for i, n in enumerate(pages_per):
+        table[i, :n] = perm[at:at + n]
+        at += n
+    pool = normal_bf16((num_pages, 2, Hkv, 16 * 128), seed=seed + 1)
+    q = normal_bf16((len(lens), H, 128), seed=seed + 2)
+    return q, pool, table
+
+
+def test_kv_append_gather_round_trip():
+    lens = [5, 40, 17]
+    _, pool, table = _pool_case(lens, seed=3)
+    pool = np.ascontiguousarray(pool)
+    k = normal_bf16((3, 4, 128), seed=4)
+    v = normal_bf16((3, 4, 128), seed=5)
+    pos = np.array([4, 39, 16], np.int32)
+    oracle.kv_append_paged(pool, k, v, pos, table)
+    for b in range(3):
+        kc, vc = oracle.kv_gather(pool, table[b], lens[b], 4, 128)
+        assert np.array_equal(kc[:, pos[b]], k[b]) and np.array_equal(vc[:, pos[b]], v[b])
+        pg, sl = table[b, pos[b] // 16], pos[b] % 16
+        assert np.array_equal(pool[pg, 0, :, sl * 128:(sl + 1) * 128], k[b])  # K slot-major
+        assert np.array_equal(pool[pg, 1].reshape(4, 128, 16)[:, :, sl], v[b])  # V dim-major
+
+
+def test_attention_matches_torch_sdpa_float64():
+    lens = [1, 7, 16, 33, 300]
+    q, pool, table = _pool_case(lens, seed=6)
+    scale = 128 ** -0.5
+    out = oracle.paged_decode_attn(q, pool, table, lens, scale)
+    for b, L in enumerate(lens):
+        kc, vc = oracle.kv_gather(pool, table[b], L, 4, 128)
+        qt = torch.from_numpy(bf16_to_f32(q[b]).astype(np.float64)).reshape(1, 32, 1, 128)
+        kt = torch.from_numpy(bf16_to_f32(kc).astype(np.float64)).repeat_interleave(8, 0)[None]
+        vt = torch.from_numpy(bf16_to_f32(vc).astype(np.float64)).repeat_interleave(8, 0)[None]
+        want = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, scale=scale).reshape(32, 128)
+        wb = f32_to_bf16(want.numpy().astype(np.float32))
+        got = bf16_to_f32(out[b]).astype(np.float64)
+        ulp = np.maximum(np.abs(bf16_to_f32(wb)), 1e-30) * 2.0**-7  # one bf16 ulp (summation order)
+        assert np.all(np.abs(got - bf16_to_f32(wb)) <= ulp), b
+        assert np.mean(out[b] == wb) > 0.99
+    # one key: the output is that key's value row, exactly
+    kc, vc = oracle.kv_gather(pool, table[0], 1, 4, 128)
+    assert np.array_equal(out[0].reshape(4, 8, 128), np.repeat(vc[:, :1], 8, 1))
+
+
+def test_attention_page_permutation_invariance():
+    lens = [50, 130]
+    q, pool, table = _pool_case(lens, seed=9)
+    a = oracle.paged_decode_attn(q, pool, table, lens, 0.088)
+    perm = np.random.default_rng(10).permutation(pool.shape[0])
+    pool2 = np.empty_like(pool)
+    pool2[perm] = pool
+    b = oracle.paged_decode_attn(q, pool2, perm[table].astype(np.int32), lens, 0.088)
+    assert np.array_equal(a, b)
