@@ -95,9 +95,30 @@ int jit_moe_pack(const uint32_t *inds, int P, int k, int E, int32_t *order, int3
  * accumulation, bf16 out: QLinear.__call__ / .rows (Q36/linear.py:219-313,
  * the qmv arithmetic of Q36/kernels/qmv_mrow.py), used for the router logits
  * (Q36/model/moe.py:296-302) and the attention projections.
- * Contract: T >= 0, N % 64 == 0, K % 256 == 0 (JIT_EUNSUPPORTED otherwise). */
+ * Contract: T >= 0, N % 16 == 0, K % 256 == 0, K <= 4096 (JIT_EUNSUPPORTED
+ * otherwise). */
 int jit_qmm(const uint16_t *x, int T, int K, const uint32_t *w, const uint16_t *scales,
             const uint16_t *biases, int N, uint16_t *y, void *stream);
+
+/* Packed tile layout of a quantized stack (the build's MI355X layout; no
+ * counterpart in the reference, whose loader keeps the MLX layout,
+ * Q36/linear.py:101-128).  The same bytes as the MLX layout, reordered once at
+ * load time: per (expert, block of 16 rows, pair of groups) one 1152-byte tile,
+ * 64 lanes x 16 B of nibble words in the order the MFMA B operand consumes them
+ * (lane 16*j + r: words 2j, 2j+1 of the pair's first group and 2j, 2j+1 of its
+ * second group, row r), then 16 rows x (scale pair, bias pair) bf16.  A wave
+ * reads a tile with one fully coalesced 1 KB load (the MLX layout in MFMA
+ * fragment order is read in 32-byte pieces per row, which caps HBM reads well
+ * below the streaming rate).
+ * jit_q4_packed_bytes: bytes of the packed stack [E, N, K] (-1 if N % 16 or
+ * K % 128 != 0).  jit_q4_prepack: w, scales, biases (MLX layout) -> packed. */
+int64_t jit_q4_packed_bytes(int E, int N, int K);
+int jit_q4_prepack(const uint32_t *w, const uint16_t *scales, const uint16_t *biases, int E, int N,
+                   int K, void *packed, void *stream);
+
+/* jit_qmm on a packed matrix (bitwise jit_qmm's result on the same weights). */
+int jit_qmm_packed(const uint16_t *x, int T, int K, const void *packed, int N, uint16_t *y,
+                   void *stream);
 
 /* Grouped gate||up projection with fused SwiGLU over packed pairs:
  * for every sorted pair p of expert e, g, u = x[pair_row[p]] . dequant(Wgu_e)^T
@@ -107,20 +128,31 @@ int jit_qmm(const uint16_t *x, int T, int K, const uint32_t *w, const uint16_t *
  * 213-232,359-401), the stock gate_up.gather + swiglu (Q36/model/moe.py:
  * 191-193, Q36/kernels/elementwise.py:14-15) and FN's grouped_swiglu
  * (FN/kernels/grouped_expert_qmv.py:345-371).  x [B, K] bf16; h [P, I] bf16 in
- * sorted pair order.  Contract: I % 64 == 0, K % 256 == 0, 0 < E. */
+ * sorted pair order.  Contract: I % 16 == 0, K % 512 == 0, K <= 4096, 0 < E.
+ * Expert segments come from jit_moe_pack (expert_cnt, expert_off, pair_row). */
 int jit_moe_gate_up_swiglu(const uint16_t *x, int K, const int32_t *pair_row,
                            const int32_t *expert_cnt, const int32_t *expert_off, int E,
                            const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
                            int I, int P, uint16_t *h, void *stream);
 
+/* The same on a packed [E, 2I, K] stack (bitwise the unpacked call's result). */
+int jit_moe_gate_up_swiglu_packed(const uint16_t *x, int K, const int32_t *pair_row,
+                                  const int32_t *expert_cnt, const int32_t *expert_off, int E,
+                                  const void *packed, int I, int P, uint16_t *h, void *stream);
+
 /* Grouped down projection over packed pairs: r[p] = bf16(h[p] . dequant(Wd_e)^T)
  * for every sorted pair p of expert e (the down gather of Q36/model/moe.py:193;
  * the per-expert GEMV inside expert_down_exact(_par),
  * Q36/kernels/expert_solo.py:118-164,262-356).  h [P, I], r [P, D] bf16.
- * Contract: D % 64 == 0, I % 256 == 0. */
+ * Contract: D % 16 == 0, I % 256 == 0, I <= 2048. */
 int jit_moe_down(const uint16_t *h, int I, const int32_t *expert_cnt, const int32_t *expert_off,
                  int E, const uint32_t *w, const uint16_t *scales, const uint16_t *biases, int D,
                  int P, uint16_t *r, void *stream);
+
+/* The same on a packed [E, D, I] stack (bitwise the unpacked call's result). */
+int jit_moe_down_packed(const uint16_t *h, int I, const int32_t *expert_cnt,
+                        const int32_t *expert_off, int E, const void *packed, int D, int P,
+                        uint16_t *r, void *stream);
 
 /* Weighted combine in slot order: y[b] = sum_j bf16(r[inv[b*k+j]] * score[b, j])
  * with each product rounded to bf16 and a sequential bf16 sum over j = 0..k-1
@@ -129,6 +161,29 @@ int jit_moe_down(const uint16_t *h, int I, const int32_t *expert_cnt, const int3
  * y[b] = bf16(resid[b] + that sum) (with_residual, Q36/model/moe.py:119-123). */
 int jit_moe_combine(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int B, int k,
                     int D, const uint16_t *resid, uint16_t *y, void *stream);
+
+/* ----------------------------------------------------- decoder block glue --
+ * RMSNorm of rows x [rows, D] (mx.fast.rms_norm as the decoder layer applies it,
+ * Q36/model/model.py:65-80; Q36/model/attention.py:59-60): sum(x^2) in fp32,
+ * y = bf16(w * bf16(x * rsqrt(mean + eps))).  With resid != NULL the normed row
+ * is h = bf16(x + resid) (the residual add in front of the post-attention
+ * norm), written to h_out when that is not NULL.  Contract: D % 8 == 0,
+ * D <= 2048. */
+int jit_rmsnorm(const uint16_t *x, const uint16_t *resid, int rows, int D, const uint16_t *w,
+                float eps, uint16_t *h_out, uint16_t *y, void *stream);
+
+/* The attention block between the qkv projection and attention
+ * (Qwen3_5MoeAttention.step, Q36/model/attention.py:99-119, without the output
+ * gate, which the BASELINE geometry does not have): qkv [B, (H + 2 Hkv) * 128]
+ * (q heads, then k heads, then v heads); per head RMSNorm with q_norm_w /
+ * k_norm_w [128]; RoPE with traditional = False on q and k (pairs (i, i + 64),
+ * angle fp32(pos[b]) * inv_freq[i], inv_freq [64] fp32 = base^(-2i/128));
+ * q -> q_out [B, H, 128]; k, v -> the paged pool at position pos[b] (the KV
+ * append of KVSlot.append, Q36/kvcache/kv_cache.py:76-85). */
+int jit_qk_norm_rope_append(const uint16_t *qkv, int B, int H, int Hkv, const uint16_t *q_norm_w,
+                            const uint16_t *k_norm_w, float eps, const float *inv_freq,
+                            const int32_t *pos, const int32_t *page_table, int max_pages,
+                            uint16_t *pool, uint16_t *q_out, void *stream);
 
 /* --------------------------------------------------------- paged KV pool --
  * Pool layout (the build's design; the reference keeps one contiguous

@@ -27,17 +27,25 @@ _SIGNATURES = {
     "jit_router_topk": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "jit_topk": [_P, _I, _I, _I, _P, _P],
     "jit_moe_pack": [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "jit_q4_packed_bytes": [_I, _I, _I],
+    "jit_q4_prepack": [_P, _P, _P, _I, _I, _I, _P, _P],
     "jit_qmm": [_P, _I, _I, _P, _P, _P, _I, _P, _P],
+    "jit_qmm_packed": [_P, _I, _I, _P, _I, _P, _P],
     "jit_moe_gate_up_swiglu": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _P, _P],
+    "jit_moe_gate_up_swiglu_packed": [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P, _P],
     "jit_moe_down": [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _P, _P],
+    "jit_moe_down_packed": [_P, _I, _P, _P, _I, _P, _I, _I, _P, _P],
     "jit_moe_combine": [_P, _P, _P, _I, _I, _I, _P, _P, _P],
+    "jit_rmsnorm": [_P, _P, _I, _I, _P, _F, _P, _P, _P],
+    "jit_qk_norm_rope_append": [_P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _I, _P, _P, _P],
     "jit_kv_append_paged": [_P, _P, _I, _I, _P, _P, _I, _P, _P],
     "jit_attn_chunk_tokens": [_I],
     "jit_attn_plan": [_P, _I, _P, _P, _I],
     "jit_attn_workspace_bytes": [_I, _I],
     "jit_paged_decode_attn": [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P, _P],
 }
-_RESTYPES = {"jit_last_error": ctypes.c_char_p, "jit_attn_workspace_bytes": ctypes.c_int64}
+_RESTYPES = {"jit_last_error": ctypes.c_char_p, "jit_attn_workspace_bytes": ctypes.c_int64,
+             "jit_q4_packed_bytes": ctypes.c_int64}
 
 _lib = None
 

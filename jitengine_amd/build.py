@@ -26,6 +26,7 @@ SOURCES = {
     "router.hip": ["-ffp-contract=off"],
     "qmm.hip": [],
     "attention.hip": [],
+    "block.hip": [],
 }
 
 _COMMON = [

@@ -1,0 +1,159 @@
+// The decoder block's small fused kernels for gfx950: RMSNorm (with the residual
+// add fused in front) and the per-head q/k RMSNorm + RoPE + paged KV append that
+// sits between the qkv projection and decode attention.
+//
+// Arithmetic follows the reference's MLX ops (Q36/model/attention.py:42-68,
+// 99-119; Q36/model/model.py:65-80): RMSNorm accumulates sum(x^2) in fp32 and
+// returns bf16(w * bf16(x * rsqrt(mean + eps))); RoPE (traditional = False)
+// rotates the pairs (x[i], x[i + D/2]) by pos * inv_freq[i] in fp32.
+#include "common.hpp"
+
+namespace {
+
+constexpr int kD = JIT_HEAD_DIM;
+constexpr int kPage = JIT_PAGE_TOKENS;
+
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += shfl_xor_f(v, o);
+  const int w = threadIdx.x >> 6;
+  if (lane_id() == 0) red[w] = v;
+  __syncthreads();
+  const float s = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return s;
+}
+
+// One workgroup (256 threads) per row; each thread owns 8 consecutive elements.
+// With `resid`, the row is h = bf16(x + resid) (written to h_out) and h is normed.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict__ x,
+                                                      const uint16_t *__restrict__ resid, int D,
+                                                      const uint16_t *__restrict__ w, float eps,
+                                                      uint16_t *__restrict__ h_out,
+                                                      uint16_t *__restrict__ y) {
+  __shared__ float red[4];
+  const long long row = blockIdx.x;
+  float v[8];
+  float ss = 0.0f;
+  const int n = threadIdx.x * 8;
+  const bool on = n < D;
+  if (on) {
+    const uint4 a = *(const uint4 *)(x + row * D + n);
+    const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (i & 1) ? bf2f_hi(aw[i >> 1]) : bf2f(aw[i >> 1] & 0xffffu);
+    if (resid) {
+      const uint4 r = *(const uint4 *)(resid + row * D + n);
+      const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = bf2f(f2bf(v[i] + ((i & 1) ? bf2f_hi(rw[i >> 1]) : bf2f(rw[i >> 1] & 0xffffu))));
+      if (h_out) {
+        uint4 o;
+        o.x = f2bf(v[0]) | (f2bf(v[1]) << 16);
+        o.y = f2bf(v[2]) | (f2bf(v[3]) << 16);
+        o.z = f2bf(v[4]) | (f2bf(v[5]) << 16);
+        o.w = f2bf(v[6]) | (f2bf(v[7]) << 16);
+        *(uint4 *)(h_out + row * D + n) = o;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) ss = fmaf(v[i], v[i], ss);
+  }
+  const float tot = block_sum_256(ss, red);
+  const float r = rsqrtf(tot / (float)D + eps);
+  if (on) {
+    const uint4 wq = *(const uint4 *)(w + n);
+    const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float wi = (i & 1) ? bf2f_hi(ww[i >> 1]) : bf2f(ww[i >> 1] & 0xffffu);
+      o[i] = bf2f(f2bf(wi * bf2f(f2bf(v[i] * r))));
+    }
+    uint4 out;
+    out.x = f2bf(o[0]) | (f2bf(o[1]) << 16);
+    out.y = f2bf(o[2]) | (f2bf(o[3]) << 16);
+    out.z = f2bf(o[4]) | (f2bf(o[5]) << 16);
+    out.w = f2bf(o[6]) | (f2bf(o[7]) << 16);
+    *(uint4 *)(y + row * D + n) = out;
+  }
+}
+
+// One wave per (token, head) of the fused qkv row [q: H*128 | k: Hkv*128 | v: Hkv*128].
+// Lane l owns dims l and l + 64 -- exactly one RoPE pair -- so the per-head
+// RMSNorm is a wave butterfly and the rotation needs no exchange.  q heads go to
+// q_out; k heads are normed, rotated and written to the pool page slot of pos[b];
+// v heads are written to the pool's dim-major V part.
+__global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
+    const uint16_t *__restrict__ qkv, int H, int Hkv, const uint16_t *__restrict__ qn_w,
+    const uint16_t *__restrict__ kn_w, float eps, const float *__restrict__ inv_freq,
+    const int32_t *__restrict__ pos, const int32_t *__restrict__ page_table, int max_pages,
+    uint16_t *__restrict__ pool, uint16_t *__restrict__ q_out) {
+  const int b = blockIdx.y;
+  const int head = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int l = lane_id();
+  const int nh = H + 2 * Hkv;
+  if (head >= nh) return;
+  const uint16_t *src = qkv + ((long long)b * nh + head) * kD;
+  const int p = pos[b];
+  const int page = page_table[(long long)b * max_pages + p / kPage];
+  const int slot = p % kPage;
+  const long long part = (long long)Hkv * kPage * kD;  // bf16 elements of one (page, K or V)
+  float x1 = bf2f(src[l]), x2 = bf2f(src[l + 64]);
+  if (head >= H + Hkv) {  // v: copy into the dim-major V part
+    const int h = head - H - Hkv;
+    uint16_t *vp = pool + ((long long)page * 2 + 1) * part + (long long)h * kPage * kD;
+    vp[l * kPage + slot] = src[l];
+    vp[(l + 64) * kPage + slot] = src[l + 64];
+    return;
+  }
+  const uint16_t *nw = head < H ? qn_w : kn_w;
+  float ss = fmaf(x1, x1, x2 * x2);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += shfl_xor_f(ss, o);
+  const float r = rsqrtf(ss / (float)kD + eps);
+  x1 = bf2f(f2bf(bf2f(nw[l]) * bf2f(f2bf(x1 * r))));
+  x2 = bf2f(f2bf(bf2f(nw[l + 64]) * bf2f(f2bf(x2 * r))));
+  const float ang = (float)p * inv_freq[l];
+  float sn, cs;
+  sincosf(ang, &sn, &cs);
+  const uint32_t o1 = f2bf(x1 * cs - x2 * sn), o2 = f2bf(x1 * sn + x2 * cs);
+  if (head < H) {
+    uint16_t *qo = q_out + ((long long)b * H + head) * kD;
+    qo[l] = (uint16_t)o1;
+    qo[l + 64] = (uint16_t)o2;
+  } else {
+    const int h = head - H;
+    uint16_t *kp = pool + (long long)page * 2 * part + (long long)h * kPage * kD + slot * kD;
+    kp[l] = (uint16_t)o1;
+    kp[l + 64] = (uint16_t)o2;
+  }
+}
+
+}  // namespace
+
+extern "C" int jit_rmsnorm(const uint16_t *x, const uint16_t *resid, int rows, int D, const uint16_t *w,
+                           float eps, uint16_t *h_out, uint16_t *y, void *stream) {
+  if (rows < 0 || D <= 0) return jit::fail(JIT_EINVAL, "rmsnorm: bad dims rows=%d D=%d", rows, D);
+  if (D % 8 != 0 || D > 2048) return jit::fail(JIT_EUNSUPPORTED, "rmsnorm covers D %% 8 == 0 and D <= 2048, got %d", D);
+  if (rows == 0) return JIT_OK;
+  if (!x || !w || !y) return jit::fail(JIT_EINVAL, "rmsnorm: null pointer");
+  rmsnorm_kernel<<<rows, 256, 0, (hipStream_t)stream>>>(x, resid, D, w, eps, h_out, y);
+  return jit::check_launch("jit_rmsnorm");
+}
+
+extern "C" int jit_qk_norm_rope_append(const uint16_t *qkv, int B, int H, int Hkv, const uint16_t *q_norm_w,
+                                       const uint16_t *k_norm_w, float eps, const float *inv_freq,
+                                       const int32_t *pos, const int32_t *page_table, int max_pages,
+                                       uint16_t *pool, uint16_t *q_out, void *stream) {
+  if (B < 0 || H <= 0 || Hkv <= 0 || max_pages <= 0)
+    return jit::fail(JIT_EINVAL, "qk_norm_rope_append: bad dims B=%d H=%d Hkv=%d", B, H, Hkv);
+  if (H % Hkv != 0) return jit::fail(JIT_EINVAL, "%d query heads do not share %d KV heads evenly", H, Hkv);
+  if (B == 0) return JIT_OK;
+  if (!qkv || !q_norm_w || !k_norm_w || !inv_freq || !pos || !page_table || !pool || !q_out)
+    return jit::fail(JIT_EINVAL, "qk_norm_rope_append: null pointer");
+  const dim3 grid((H + 2 * Hkv + 3) / 4, B);
+  qk_norm_rope_append_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(qkv, H, Hkv, q_norm_w, k_norm_w, eps, inv_freq,
+                                                                    pos, page_table, max_pages, pool, q_out);
+  return jit::check_launch("jit_qk_norm_rope_append");
+}

@@ -1,19 +1,26 @@
 // 4-bit affine (MLX layout, group 64) quantized projections on gfx950 matrix
 // cores, for dense projections and for expert segments of packed pairs.
 //
-// Tile: one wave computes C[16 tokens x 16 weight rows] per row block with
-// v_mfma_f32_16x16x32_bf16, tokens on the M side (A operand = activations) and
-// weight rows on the N side (B operand = nibbles).  Each lane therefore owns one
-// weight row (l % 16) and, per quant group of 64 k, loads the two 32-bit words
-// (16 nibbles) its lane group (l / 16) feeds into the two MFMAs of that group --
-// every MFMA sees k values of a single group, so the group's scale and bias are
-// applied to the MFMA result, not per weight:
+// MFMA tile: v_mfma_f32_16x16x32_bf16 computes C[16 tokens x 16 weight rows],
+// tokens on the M side (A operand = activations), weight rows on the N side
+// (B operand = nibbles).  Each lane owns one weight row (l % 16) and, per quant
+// group of 64 k, the two 32-bit words (16 nibbles) its lane group (l / 16) feeds
+// into the group's two MFMAs -- every MFMA sees k values of a single group, so
+// the group's scale and bias apply to the MFMA result, not to each weight:
 //   sum_k x_k (s q_k + b) = s * sum_k x_k (q_k + 128) + (b - 128 s) * sum_k x_k.
-// A nibble q becomes the bf16 value 128 + q with one AND-OR (0x43pq bit pattern),
-// and sum_k x_k comes out of one more MFMA against an all-ones B operand, so the
-// per-weight vector work is 7 integer ops per 8 nibbles.  The two bf16 halves of
-// an unpacked word hold nibbles (i, i + 4), so the activation fragment is loaded
-// in the matching k order with byte permutes.
+// A nibble q becomes the bf16 value 128 + q with one AND-OR (bit pattern 0x43pq),
+// and sum_k x_k comes from one more MFMA against an all-ones B operand, so the
+// vector work per weight word is 7 integer ops.  The two bf16 halves of an
+// unpacked word hold nibbles (i, i + 4), so activations are permuted to match.
+//
+// Work split: a workgroup owns 16 * NB output rows of one expert (or of the dense
+// matrix) and splits K over its waves (KSPLIT = blockDim / 64); each wave owns
+// GPW consecutive groups.  A wave issues every weight, scale and bias load of its
+// K-slice before any math -- 16 KB in flight per wave for a 2048-wide gate||up
+// slice -- and keeps the slice in registers while it walks the expert's token
+// tiles of 16, so an expert's weights leave HBM once however many tokens it has.
+// The waves' partial sums meet in LDS and are added in wave order (a fixed
+// order: results do not depend on the batch).
 #include "common.hpp"
 
 namespace {
@@ -27,8 +34,17 @@ struct QmmArgs {
   const uint16_t *s, *b;      // scales, biases [E, rows_w, K / 64]
   uint16_t *out;              // [positions, N] bf16
   int K, N, T;
-  long long w_estride, g_estride;
+  long long w_estride, g_estride;  // per expert: 32-bit words and bf16 entries (MLX layout), or
+                                   // bytes of tiles (packed layout; g_estride unused)
+  int rows_w;                      // weight rows per expert (2N with SWIGLU)
 };
+
+// Packed tile layout (jit_q4_prepack): per (expert, 16-row block, pair of groups) one
+// 1152-byte tile -- 64 lanes x 16 B of nibble words in MFMA fragment order (lane
+// 16*lg + lr holds words 2lg, 2lg+1 of the pair's first group and 2lg, 2lg+1 of the
+// second, row lr), then 16 rows x (scale pair, bias pair) bf16.  A wave reads a tile
+// with one fully coalesced 1 KB load plus one 128-byte load.
+constexpr int kTileBytes = 1152;
 
 // bf16 fragment of 8 nibbles: elements (q0, q4, q1, q5, q2, q6, q3, q7) + 128.
 __device__ __forceinline__ Frag8 unpack_nibbles(uint32_t w) {
@@ -50,11 +66,6 @@ __device__ __forceinline__ Frag8 permute_x(uint4 d) {
   return f;
 }
 
-__device__ __forceinline__ float sel_bf16(uint2 v, int i) {
-  const uint32_t w = (i < 2) ? v.x : v.y;
-  return (i & 1) ? bf2f_hi(w) : bf2f(w & 0xffffu);
-}
-
 // SwiGLU with the reference's bf16 rounding points: g, u rounded; sigmoid(g)
 // rounded; bf16(g * sigmoid) * u rounded.
 __device__ __forceinline__ uint32_t swiglu_bf16(float gacc, float uacc) {
@@ -65,12 +76,12 @@ __device__ __forceinline__ uint32_t swiglu_bf16(float gacc, float uacc) {
   return f2bf(sl * u);
 }
 
-// NB output row blocks of 16 per wave, 4 waves per workgroup.  With SWIGLU each
-// output block reads a gate block (rows n) and an up block (rows N + n) of the
-// fused stack.
-template <int NB, bool SWIGLU>
-__global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
-  constexpr int NBW = SWIGLU ? 2 * NB : NB;
+template <int NB, int GPW, bool SWIGLU, bool PACKED>
+__global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
+  static_assert(!PACKED || GPW % 2 == 0, "packed tiles hold pairs of groups");
+  constexpr int NBW = SWIGLU ? 2 * NB : NB;  // weight row blocks (gate and up blocks with SWIGLU)
+  extern __shared__ float red[];             // [KSPLIT][NBW][4][64]
+  const int ksplit = blockDim.x >> 6;
   const int wave = threadIdx.x >> 6, l = lane_id();
   const int lr = l & 15, lg = l >> 4;
   const int e = blockIdx.y;
@@ -82,26 +93,49 @@ __global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
     cnt = a.T;
     off = 0;
   }
-  if (cnt <= 0) return;
-  const int n0 = (blockIdx.x * 4 + wave) * (16 * NB);
-  if (n0 >= a.N) return;
+  if (cnt <= 0) return;  // uniform over the workgroup
+  const int n0 = blockIdx.x * (16 * NB);
   const int G = a.K >> 6, KW = a.K >> 3;
-  const uint32_t *wb = a.w + (long long)e * a.w_estride;
-  const uint16_t *sb = a.s + (long long)e * a.g_estride;
-  const uint16_t *bb = a.b + (long long)e * a.g_estride;
+  const int g0 = wave * GPW;
 
-  const uint32_t *wrow[NBW];
-  const uint16_t *srow[NBW], *brow[NBW];
-  bool live[NBW];
+  // ---- the wave's whole weight slice: GPW groups x NBW row blocks
+  uint2 wv[GPW][NBW];
+  uint32_t sv[NBW][(GPW + 1) / 2], bv[NBW][(GPW + 1) / 2];  // bf16 pairs (groups 2j, 2j+1)
 #pragma unroll
   for (int rb = 0; rb < NBW; rb++) {
+    // rows past N (a partial last tile) read row block n0 instead; only stores are guarded
     const int ob = SWIGLU ? (rb % NB) : rb;
-    const int rowo = n0 + 16 * ob;
-    live[rb] = rowo < a.N;
-    const int row = (SWIGLU && rb >= NB ? a.N : 0) + (live[rb] ? rowo : n0) + lr;
-    wrow[rb] = wb + (long long)row * KW + 2 * lg;
-    srow[rb] = sb + (long long)row * G;
-    brow[rb] = bb + (long long)row * G;
+    const int rowo = n0 + 16 * ob < a.N ? n0 + 16 * ob : n0;
+    const int rowb = (SWIGLU && rb >= NB ? a.N : 0) + rowo;  // first row of the block
+    if (PACKED) {
+      const int GP = a.K >> 7;
+      const uint8_t *tb = (const uint8_t *)a.w + (long long)e * a.w_estride +
+                          ((long long)(rowb >> 4) * GP + (g0 >> 1)) * kTileBytes;
+#pragma unroll
+      for (int j = 0; j < GPW / 2; j++) {
+        const uint4 q = *(const uint4 *)(tb + j * kTileBytes + 16 * l);
+        const uint2 sb2 = *(const uint2 *)(tb + j * kTileBytes + 1024 + 8 * lr);
+        wv[2 * j][rb] = make_uint2(q.x, q.y);
+        wv[2 * j + 1][rb] = make_uint2(q.z, q.w);
+        sv[rb][j] = sb2.x;
+        bv[rb][j] = sb2.y;
+      }
+    } else {
+      const long long row = (long long)rowb + lr;
+      const uint32_t *wp = a.w + e * a.w_estride + row * KW + 8 * g0 + 2 * lg;
+      const uint16_t *sp = a.s + e * a.g_estride + row * G + g0;
+      const uint16_t *bp = a.b + e * a.g_estride + row * G + g0;
+#pragma unroll
+      for (int g = 0; g < GPW; g++) wv[g][rb] = *(const uint2 *)(wp + 8 * g);
+#pragma unroll
+      for (int j = 0; j < (GPW + 1) / 2; j++) {
+        const uint32_t s0 = sp[2 * j], b0 = bp[2 * j];
+        const uint32_t s1 = (2 * j + 1 < GPW) ? sp[2 * j + 1] : 0u;
+        const uint32_t b1 = (2 * j + 1 < GPW) ? bp[2 * j + 1] : 0u;
+        sv[rb][j] = s0 | (s1 << 16);
+        bv[rb][j] = b0 | (b1 << 16);
+      }
+    }
   }
   Frag8 ones;
 #pragma unroll
@@ -110,78 +144,136 @@ __global__ __launch_bounds__(256) void qmm_kernel(const QmmArgs a) {
   for (int t0 = 0; t0 < cnt; t0 += 16) {
     const int tok = t0 + lr;
     const bool tv = tok < cnt;
-    const uint16_t *xr = a.x;
+    Frag8 xa[GPW][2];  // activation fragments, permuted in place as they arrive
     if (tv) {
       const int pos = off + tok;
       const int xrow = a.row_index ? a.row_index[pos] : pos;
-      xr = a.x + (long long)xrow * a.K + 16 * lg;
+      const uint16_t *xr = a.x + (long long)xrow * a.K + 64 * g0 + 16 * lg;
+#pragma unroll
+      for (int g = 0; g < GPW; g++) {
+        xa[g][0].q = *(const uint4 *)(xr + 64 * g);
+        xa[g][1].q = *(const uint4 *)(xr + 64 * g + 8);
+      }
+#pragma unroll
+      for (int g = 0; g < GPW; g++) {
+        xa[g][0] = permute_x(xa[g][0].q);
+        xa[g][1] = permute_x(xa[g][1].q);
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < GPW; g++) xa[g][0].q = xa[g][1].q = make_uint4(0, 0, 0, 0);
     }
     f32x4 acc[NBW];
 #pragma unroll
     for (int rb = 0; rb < NBW; rb++) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    for (int g = 0; g < G; g += 4) {
-      uint2 s4[NBW], b4[NBW], wv[4][NBW];
-      uint4 xa[4][2];
+#pragma unroll
+    for (int g = 0; g < GPW; g++) {
+      const Frag8 &A0 = xa[g][0], &A1 = xa[g][1];
+      f32x4 X = mfma16x16x32(A0, ones, f32x4{0.f, 0.f, 0.f, 0.f});
+      X = mfma16x16x32(A1, ones, X);
 #pragma unroll
       for (int rb = 0; rb < NBW; rb++) {
-        s4[rb] = *(const uint2 *)(srow[rb] + g);
-        b4[rb] = *(const uint2 *)(brow[rb] + g);
+        // the packed words are loop-invariant across token tiles; this empty register
+        // constraint keeps their unpacking here instead of hoisted (8 VGPRs per word pair)
+        uint32_t w0 = wv[g][rb].x, w1 = wv[g][rb].y;
+        asm volatile("" : "+v"(w0), "+v"(w1));
+        const Frag8 B0 = unpack_nibbles(w0), B1 = unpack_nibbles(w1);
+        f32x4 C = mfma16x16x32(A0, B0, f32x4{0.f, 0.f, 0.f, 0.f});
+        C = mfma16x16x32(A1, B1, C);
+        const float sc = (g & 1) ? bf2f_hi(sv[rb][g >> 1]) : bf2f(sv[rb][g >> 1] & 0xffffu);
+        const float bi = (g & 1) ? bf2f_hi(bv[rb][g >> 1]) : bf2f(bv[rb][g >> 1] & 0xffffu);
+        const float bq = fmaf(-128.0f, sc, bi);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[rb][i] = fmaf(bq, X[i], fmaf(sc, C[i], acc[rb][i]));
       }
-#pragma unroll
-      for (int gg = 0; gg < 4; gg++) {
-#pragma unroll
-        for (int rb = 0; rb < NBW; rb++) wv[gg][rb] = *(const uint2 *)(wrow[rb] + 8 * (g + gg));
-        if (tv) {
-          xa[gg][0] = *(const uint4 *)(xr + 64 * (g + gg));
-          xa[gg][1] = *(const uint4 *)(xr + 64 * (g + gg) + 8);
-        } else {
-          xa[gg][0] = make_uint4(0, 0, 0, 0);
-          xa[gg][1] = make_uint4(0, 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int gg = 0; gg < 4; gg++) {
-        const Frag8 A0 = permute_x(xa[gg][0]), A1 = permute_x(xa[gg][1]);
-        f32x4 X = mfma16x16x32(A0, ones, f32x4{0.f, 0.f, 0.f, 0.f});
-        X = mfma16x16x32(A1, ones, X);
-#pragma unroll
-        for (int rb = 0; rb < NBW; rb++) {
-          if (!live[rb]) continue;
-          const Frag8 B0 = unpack_nibbles(wv[gg][rb].x), B1 = unpack_nibbles(wv[gg][rb].y);
-          f32x4 C = mfma16x16x32(A0, B0, f32x4{0.f, 0.f, 0.f, 0.f});
-          C = mfma16x16x32(A1, B1, C);
-          const float sc = sel_bf16(s4[rb], gg), bi = sel_bf16(b4[rb], gg);
-          const float bp = fmaf(-128.0f, sc, bi);
-#pragma unroll
-          for (int i = 0; i < 4; i++) acc[rb][i] = fmaf(bp, X[i], fmaf(sc, C[i], acc[rb][i]));
-        }
-      }
+      // keep each group's nibble unpacking next to its MFMAs (hoisting every group's
+      // unpacked fragments ahead would cost 8 registers per (group, block))
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // lane l holds C[token 4*lg + i][row lr] of each block
+    // ---- the waves' partial sums meet in LDS; lane l holds C[token 4*lg + i][row lr]
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int rb = 0; rb < NBW; rb++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) red[((wave * NBW + rb) * 4 + i) * 64 + l] = acc[rb][i];
+    __syncthreads();
+    // (output block, token row i) pairs are spread over the waves
+    for (int idx = wave; idx < 4 * NB; idx += ksplit) {
+      const int ob = idx >> 2, i = idx & 3;
       const int t = t0 + 4 * lg + i;
-      if (t >= cnt) continue;
-      uint16_t *orow = a.out + (long long)(off + t) * a.N + n0 + lr;
-#pragma unroll
-      for (int ob = 0; ob < NB; ob++) {
-        if (!live[ob]) continue;
-        if (SWIGLU)
-          orow[16 * ob] = (uint16_t)swiglu_bf16(acc[ob][i], acc[NB + ob][i]);
-        else
-          orow[16 * ob] = (uint16_t)f2bf(acc[ob][i]);
+      if (n0 + 16 * ob >= a.N) continue;
+      float v = 0.0f, u = 0.0f;
+      for (int ks = 0; ks < ksplit; ks++) {
+        v += red[((ks * NBW + ob) * 4 + i) * 64 + l];
+        if (SWIGLU) u += red[((ks * NBW + NB + ob) * 4 + i) * 64 + l];
+      }
+      if (t < cnt) {
+        uint16_t *o = a.out + (long long)(off + t) * a.N + n0 + 16 * ob + lr;
+        *o = (uint16_t)(SWIGLU ? swiglu_bf16(v, u) : f2bf(v));
       }
     }
+    __syncthreads();
   }
 }
 
-template <int NB, bool SWIGLU>
+template <int NB, int GPW, bool SWIGLU, bool PACKED>
 int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what) {
-  const int rows_per_wg = 4 * 16 * NB;
-  const dim3 grid((a.N + rows_per_wg - 1) / rows_per_wg, E), block(256);
-  qmm_kernel<NB, SWIGLU><<<grid, block, 0, st>>>(a);
+  constexpr int NBW = SWIGLU ? 2 * NB : NB;
+  const int G = a.K / 64;
+  const int ksplit = G / GPW;
+  if (ksplit * GPW != G || ksplit < 1 || ksplit > 8)
+    return jit::fail(JIT_EUNSUPPORTED, "%s: K=%d does not split into %d-group wave slices", what, a.K, GPW);
+  const dim3 grid((a.N + 16 * NB - 1) / (16 * NB), E), block(64 * ksplit);
+  const size_t lds = (size_t)ksplit * NBW * 4 * 64 * sizeof(float);
+  qmm_kernel<NB, GPW, SWIGLU, PACKED><<<grid, block, lds, st>>>(a);
   return jit::check_launch(what);
+}
+
+// Groups per wave for a dense projection: the smallest even slice that splits K over at
+// most 8 waves (the packed and direct layouts use the same split, so they agree bit for bit).
+int dense_gpw(int K) {
+  const int G = K / 64;
+  for (int gpw = 2; gpw <= 8; gpw += 2)
+    if (G % gpw == 0 && G / gpw <= 8) return gpw;
+  return 0;
+}
+
+template <bool PACKED>
+int launch_dense(const QmmArgs &a, hipStream_t st) {
+  const char *what = PACKED ? "jit_qmm_packed" : "jit_qmm";
+  switch (dense_gpw(a.K)) {
+    case 2: return launch_qmm<1, 2, false, PACKED>(a, 1, st, what);
+    case 4: return launch_qmm<1, 4, false, PACKED>(a, 1, st, what);
+    case 6: return launch_qmm<1, 6, false, PACKED>(a, 1, st, what);
+    case 8: return launch_qmm<1, 8, false, PACKED>(a, 1, st, what);
+    default: return jit::fail(JIT_EUNSUPPORTED, "%s covers K %% 256 == 0 and K <= 4096, got %d", what, a.K);
+  }
+}
+
+// One-time repack of an MLX-layout stack into the tile layout above: one wave per tile.
+__global__ __launch_bounds__(64) void q4_prepack_kernel(const uint32_t *__restrict__ w,
+                                                        const uint16_t *__restrict__ s,
+                                                        const uint16_t *__restrict__ b, int N, int K,
+                                                        uint8_t *__restrict__ out) {
+  const long long tile = blockIdx.x;
+  const int l = threadIdx.x, lr = l & 15, lg = l >> 4;
+  const int GP = K >> 7, NRB = N >> 4, G = K >> 6, KW = K >> 3;
+  const int gp = (int)(tile % GP);
+  const int rbi = (int)((tile / GP) % NRB);
+  const long long e = tile / ((long long)GP * NRB);
+  const long long row = e * N + rbi * 16 + lr;
+  const uint32_t *wr = w + row * KW + 16 * gp + 2 * lg;
+  uint4 q;
+  q.x = wr[0];
+  q.y = wr[1];
+  q.z = wr[8];
+  q.w = wr[9];
+  uint8_t *t = out + tile * kTileBytes;
+  *(uint4 *)(t + 16 * l) = q;
+  if (lg == 0) {
+    const uint16_t *sr = s + row * G + 2 * gp, *br = b + row * G + 2 * gp;
+    *(uint2 *)(t + 1024 + 8 * lr) = make_uint2((uint32_t)sr[0] | ((uint32_t)sr[1] << 16),
+                                               (uint32_t)br[0] | ((uint32_t)br[1] << 16));
+  }
 }
 
 // Weighted combine: one workgroup per token row, 8 outputs per thread; each
@@ -230,15 +322,59 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict
 
 }  // namespace
 
+extern "C" int64_t jit_q4_packed_bytes(int E, int N, int K) {
+  if (E <= 0 || N <= 0 || K <= 0 || N % 16 != 0 || K % 128 != 0) return -1;
+  return (int64_t)E * (N / 16) * (K / 128) * kTileBytes;
+}
+
+extern "C" int jit_q4_prepack(const uint32_t *w, const uint16_t *scales, const uint16_t *biases, int E,
+                              int N, int K, void *packed, void *stream) {
+  if (E <= 0 || N <= 0 || K <= 0) return jit::fail(JIT_EINVAL, "q4_prepack: bad dims E=%d N=%d K=%d", E, N, K);
+  if (N % 16 != 0 || K % 128 != 0)
+    return jit::fail(JIT_EUNSUPPORTED, "q4_prepack covers N %% 16 == 0 and K %% 128 == 0, got N=%d K=%d", N, K);
+  if (!w || !scales || !biases || !packed) return jit::fail(JIT_EINVAL, "q4_prepack: null pointer");
+  const long long tiles = (long long)E * (N / 16) * (K / 128);
+  if (tiles > 0x7fffffffLL) return jit::fail(JIT_EUNSUPPORTED, "q4_prepack: %lld tiles", tiles);
+  q4_prepack_kernel<<<(unsigned)tiles, 64, 0, (hipStream_t)stream>>>(w, scales, biases, N, K, (uint8_t *)packed);
+  return jit::check_launch("jit_q4_prepack");
+}
+
+static int qmm_common(const uint16_t *x, int T, int K, int N, uint16_t *y, const char *what) {
+  if (T < 0 || K <= 0 || N <= 0) return jit::fail(JIT_EINVAL, "%s: bad dims T=%d K=%d N=%d", what, T, K, N);
+  if (K % 256 != 0 || N % 16 != 0 || K > 4096)
+    return jit::fail(JIT_EUNSUPPORTED, "%s covers K %% 256 == 0, K <= 4096 and N %% 16 == 0, got K=%d N=%d",
+                     what, K, N);
+  if (T > 0 && (!x || !y)) return jit::fail(JIT_EINVAL, "%s: null pointer", what);
+  return JIT_OK;
+}
+
 extern "C" int jit_qmm(const uint16_t *x, int T, int K, const uint32_t *w, const uint16_t *scales,
                        const uint16_t *biases, int N, uint16_t *y, void *stream) {
-  if (T < 0 || K <= 0 || N <= 0) return jit::fail(JIT_EINVAL, "qmm: bad dims T=%d K=%d N=%d", T, K, N);
-  if (K % 256 != 0 || N % 16 != 0)
-    return jit::fail(JIT_EUNSUPPORTED, "qmm covers K %% 256 == 0 and N %% 16 == 0, got K=%d N=%d", K, N);
+  if (int rc = qmm_common(x, T, K, N, y, "qmm")) return rc;
   if (T == 0) return JIT_OK;
-  if (!x || !w || !scales || !biases || !y) return jit::fail(JIT_EINVAL, "qmm: null pointer");
-  QmmArgs a{x, nullptr, nullptr, nullptr, w, scales, biases, y, K, N, T, 0, 0};
-  return launch_qmm<1, false>(a, 1, (hipStream_t)stream, "jit_qmm");
+  if (!w || !scales || !biases) return jit::fail(JIT_EINVAL, "qmm: null pointer");
+  QmmArgs a{x, nullptr, nullptr, nullptr, w, scales, biases, y, K, N, T, 0, 0, N};
+  return launch_dense<false>(a, (hipStream_t)stream);
+}
+
+extern "C" int jit_qmm_packed(const uint16_t *x, int T, int K, const void *packed, int N, uint16_t *y,
+                              void *stream) {
+  if (int rc = qmm_common(x, T, K, N, y, "qmm_packed")) return rc;
+  if (T == 0) return JIT_OK;
+  if (!packed) return jit::fail(JIT_EINVAL, "qmm_packed: null pointer");
+  QmmArgs a{x, nullptr, nullptr, nullptr, (const uint32_t *)packed, nullptr, nullptr, y, K, N, T, 0, 0, N};
+  return launch_dense<true>(a, (hipStream_t)stream);
+}
+
+static int gate_up_check(const uint16_t *x, int K, const int32_t *pair_row, const int32_t *cnt,
+                         const int32_t *off, int E, int I, int P, uint16_t *h) {
+  if (K <= 0 || I <= 0 || E <= 0 || P < 0)
+    return jit::fail(JIT_EINVAL, "moe_gate_up: bad dims K=%d I=%d E=%d P=%d", K, I, E, P);
+  if (K % 512 != 0 || K > 4096 || I % 16 != 0)
+    return jit::fail(JIT_EUNSUPPORTED, "moe_gate_up covers K %% 512 == 0, K <= 4096 and I %% 16 == 0, got K=%d I=%d",
+                     K, I);
+  if (P > 0 && (!x || !pair_row || !cnt || !off || !h)) return jit::fail(JIT_EINVAL, "moe_gate_up: null pointer");
+  return JIT_OK;
 }
 
 extern "C" int jit_moe_gate_up_swiglu(const uint16_t *x, int K, const int32_t *pair_row,
@@ -246,32 +382,57 @@ extern "C" int jit_moe_gate_up_swiglu(const uint16_t *x, int K, const int32_t *p
                                       const uint32_t *w, const uint16_t *scales,
                                       const uint16_t *biases, int I, int P, uint16_t *h,
                                       void *stream) {
-  if (K <= 0 || I <= 0 || E <= 0 || P < 0)
-    return jit::fail(JIT_EINVAL, "moe_gate_up: bad dims K=%d I=%d E=%d P=%d", K, I, E, P);
-  if (K % 256 != 0 || I % 16 != 0)
-    return jit::fail(JIT_EUNSUPPORTED, "moe_gate_up covers K %% 256 == 0 and I %% 16 == 0, got K=%d I=%d", K, I);
+  if (int rc = gate_up_check(x, K, pair_row, expert_cnt, expert_off, E, I, P, h)) return rc;
   if (P == 0) return JIT_OK;
-  if (!x || !pair_row || !expert_cnt || !expert_off || !w || !scales || !biases || !h)
-    return jit::fail(JIT_EINVAL, "moe_gate_up: null pointer");
+  if (!w || !scales || !biases) return jit::fail(JIT_EINVAL, "moe_gate_up: null pointer");
   QmmArgs a{x, pair_row, expert_cnt, expert_off, w, scales, biases, h, K, I, 0,
-            (long long)2 * I * (K / 8), (long long)2 * I * (K / 64)};
-  return launch_qmm<1, true>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu");
+            (long long)2 * I * (K / 8), (long long)2 * I * (K / 64), 2 * I};
+  return launch_qmm<2, 8, true, false>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu");
+}
+
+extern "C" int jit_moe_gate_up_swiglu_packed(const uint16_t *x, int K, const int32_t *pair_row,
+                                             const int32_t *expert_cnt, const int32_t *expert_off, int E,
+                                             const void *packed, int I, int P, uint16_t *h, void *stream) {
+  if (int rc = gate_up_check(x, K, pair_row, expert_cnt, expert_off, E, I, P, h)) return rc;
+  if (P == 0) return JIT_OK;
+  if (!packed) return jit::fail(JIT_EINVAL, "moe_gate_up_packed: null pointer");
+  QmmArgs a{x, pair_row, expert_cnt, expert_off, (const uint32_t *)packed, nullptr, nullptr, h, K, I, 0,
+            jit_q4_packed_bytes(1, 2 * I, K), 0, 2 * I};
+  return launch_qmm<2, 8, true, true>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu_packed");
+}
+
+static int down_check(const uint16_t *h, int I, const int32_t *cnt, const int32_t *off, int E, int D, int P,
+                      uint16_t *r) {
+  if (I <= 0 || D <= 0 || E <= 0 || P < 0)
+    return jit::fail(JIT_EINVAL, "moe_down: bad dims I=%d D=%d E=%d P=%d", I, D, E, P);
+  if (I % 256 != 0 || I > 2048 || D % 16 != 0)
+    return jit::fail(JIT_EUNSUPPORTED, "moe_down covers I %% 256 == 0, I <= 2048 and D %% 16 == 0, got I=%d D=%d",
+                     I, D);
+  if (P > 0 && (!h || !cnt || !off || !r)) return jit::fail(JIT_EINVAL, "moe_down: null pointer");
+  return JIT_OK;
 }
 
 extern "C" int jit_moe_down(const uint16_t *h, int I, const int32_t *expert_cnt,
                             const int32_t *expert_off, int E, const uint32_t *w,
                             const uint16_t *scales, const uint16_t *biases, int D, int P, uint16_t *r,
                             void *stream) {
-  if (I <= 0 || D <= 0 || E <= 0 || P < 0)
-    return jit::fail(JIT_EINVAL, "moe_down: bad dims I=%d D=%d E=%d P=%d", I, D, E, P);
-  if (I % 256 != 0 || D % 16 != 0)
-    return jit::fail(JIT_EUNSUPPORTED, "moe_down covers I %% 256 == 0 and D %% 16 == 0, got I=%d D=%d", I, D);
+  if (int rc = down_check(h, I, expert_cnt, expert_off, E, D, P, r)) return rc;
   if (P == 0) return JIT_OK;
-  if (!h || !expert_cnt || !expert_off || !w || !scales || !biases || !r)
-    return jit::fail(JIT_EINVAL, "moe_down: null pointer");
+  if (!w || !scales || !biases) return jit::fail(JIT_EINVAL, "moe_down: null pointer");
   QmmArgs a{h, nullptr, expert_cnt, expert_off, w, scales, biases, r, I, D, 0,
-            (long long)D * (I / 8), (long long)D * (I / 64)};
-  return launch_qmm<2, false>(a, E, (hipStream_t)stream, "jit_moe_down");
+            (long long)D * (I / 8), (long long)D * (I / 64), D};
+  return launch_qmm<4, 4, false, false>(a, E, (hipStream_t)stream, "jit_moe_down");
+}
+
+extern "C" int jit_moe_down_packed(const uint16_t *h, int I, const int32_t *expert_cnt,
+                                   const int32_t *expert_off, int E, const void *packed, int D, int P,
+                                   uint16_t *r, void *stream) {
+  if (int rc = down_check(h, I, expert_cnt, expert_off, E, D, P, r)) return rc;
+  if (P == 0) return JIT_OK;
+  if (!packed) return jit::fail(JIT_EINVAL, "moe_down_packed: null pointer");
+  QmmArgs a{h, nullptr, expert_cnt, expert_off, (const uint32_t *)packed, nullptr, nullptr, r, I, D, 0,
+            jit_q4_packed_bytes(1, D, I), 0, D};
+  return launch_qmm<4, 4, false, true>(a, E, (hipStream_t)stream, "jit_moe_down_packed");
 }
 
 extern "C" int jit_moe_combine(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int B,

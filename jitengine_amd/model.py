@@ -1,0 +1,155 @@
+"""The decode step of the BASELINE geometry on the HIP kernels: decoder layers and decode_step.
+
+Mirrors the reference's batched decode call chain (Q36/model/model.py:504-517 `decode_step` ->
+`Qwen3_5MoeDecoderLayer.step` :77-80): input RMSNorm -> fused qkv projection -> q/k RMSNorm +
+RoPE + KV append (Q36/model/attention.py:99-119, here into the paged pool) -> decode attention
+(Q36/kernels/sdpa_decode.py:462-476, here paged split-K) -> o_proj -> residual -> post-attention
+RMSNorm -> MoE block (Q36/model/moe.py:255-289) with the residual.  The geometry (Qwen3-MoE-style:
+hidden 2048, 32 q / 4 kv heads of 128, 128 experts top-8 of intermediate 768, RoPE theta 1e6) has
+no output gate and no shared expert.  Embedding and lm_head are outside the step.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import ops
+from .moe import MoEBlock
+from .quant import QLinear, random_quantized
+
+
+@dataclass(frozen=True)
+class MoEConfig:
+    hidden: int = 2048
+    heads: int = 32
+    kv_heads: int = 4
+    head_dim: int = 128
+    experts: int = 128
+    top_k: int = 8
+    inter: int = 768
+    rope_theta: float = 1e6
+    eps: float = 1e-6
+    layers: int = 48
+    norm_topk: bool = True
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+
+def rope_inv_freq(theta: float, dims: int) -> np.ndarray:
+    """fp32 inverse frequencies theta^(-2i/dims), i < dims/2 (evaluated in float64, rounded)."""
+    return (float(theta) ** (-np.arange(0, dims, 2, dtype=np.float64) / dims)).astype(np.float32)
+
+
+def random_layer_weights(cfg: MoEConfig, seed: int, device, std: float = 0.02) -> dict:
+    """Synthetic weights of one layer: N(0, std) bf16 matrices quantized to 4-bit g64 (MLX
+    layout) and RMSNorm weights 1 + N(0, std) in bf16; seeded, generated on `device`."""
+    D, I, E = cfg.hidden, cfg.inter, cfg.experts
+    gen = torch.Generator(device=device)
+    gen.manual_seed(int(seed))
+
+    def norm_w(n):
+        return (1.0 + std * torch.randn(n, generator=gen, device=device)).to(torch.bfloat16)
+
+    def stack(shape, s):
+        parts = [random_quantized((min(16, shape[0] - e0), *shape[1:]), s * 1000 + e0, std, device)
+                 for e0 in range(0, shape[0], 16)]
+        return QLinear(torch.cat([p.weight for p in parts]), torch.cat([p.scales for p in parts]),
+                       torch.cat([p.biases for p in parts]))
+
+    return {
+        "input_norm": norm_w(D),
+        "qkv": random_quantized((cfg.qkv_rows, D), seed * 10 + 1, std, device),
+        "q_norm": norm_w(cfg.head_dim),
+        "k_norm": norm_w(cfg.head_dim),
+        "o": random_quantized((D, cfg.heads * cfg.head_dim), seed * 10 + 2, std, device),
+        "post_norm": norm_w(D),
+        "router": random_quantized((E, D), seed * 10 + 3, std, device),
+        "gate_up": stack((E, 2 * I, D), seed * 10 + 4),
+        "down": stack((E, D, I), seed * 10 + 5),
+    }
+
+
+@dataclass
+class StepState:
+    """Per-step inputs shared by every layer: positions, page table, split plan, buffers."""
+
+    pos: torch.Tensor          # int32 [B]: the position each row writes (its length so far)
+    page_table: torch.Tensor   # int32 [B, max_pages]
+    plan: ops.AttnPlan         # over lens = pos + 1
+    workspace: torch.Tensor    # attention partials
+
+
+def make_step_state(cfg: MoEConfig, pos_host, page_table: torch.Tensor) -> StepState:
+    """Plan one decode step: row b writes position pos_host[b] and attends to pos + 1 keys (the
+    plan and its workspace serve every layer of the step)."""
+    pos_host = np.asarray(pos_host, np.int32)
+    dev = page_table.device
+    plan = ops.attn_plan(pos_host + 1, dev)
+    ws = torch.empty(max(ops.attn_workspace_bytes(plan.total, cfg.heads), 4), dtype=torch.uint8, device=dev)
+    return StepState(torch.from_numpy(pos_host).to(dev), page_table, plan, ws)
+
+
+class DecoderLayer:
+    """One decoder layer over B ragged decode rows; weights stay resident (packed layout)."""
+
+    def __init__(self, cfg: MoEConfig, w: dict, prepack: bool = True):
+        self.cfg = cfg
+        pk = ops.prepack if prepack else (lambda q: q)
+        self.input_norm = w["input_norm"].contiguous()
+        self.qkv = pk(w["qkv"])
+        self.q_norm = w["q_norm"].contiguous()
+        self.k_norm = w["k_norm"].contiguous()
+        self.o = pk(w["o"])
+        self.post_norm = w["post_norm"].contiguous()
+        self.moe = MoEBlock(w["router"], w["gate_up"], w["down"], cfg.top_k, cfg.norm_topk, prepack=prepack)
+        self.inv_freq = torch.from_numpy(rope_inv_freq(cfg.rope_theta, cfg.head_dim)).to(self.input_norm.device)
+
+    def step(self, x: torch.Tensor, pool: torch.Tensor, st: StepState, debug: dict | None = None,
+             prof=None) -> torch.Tensor:
+        """x [B, D] -> the layer's output rows.  `prof(name, fn)`, if given, wraps each launch
+        (timing); `debug` receives every intermediate."""
+        cfg = self.cfg
+        B = x.shape[0]
+        run = prof if prof is not None else (lambda name, fn: fn())
+        moe = self.moe
+        xn = run("rmsnorm", lambda: ops.rmsnorm(x, self.input_norm, cfg.eps))
+        qkv = run("qkv_proj", lambda: ops.qmm(xn, self.qkv))
+        q = run("qk_norm_rope_append", lambda: ops.qk_norm_rope_append(
+            qkv, cfg.heads, cfg.kv_heads, self.q_norm, self.k_norm, cfg.eps, self.inv_freq, st.pos,
+            st.page_table, pool))
+        attn = run("paged_attention", lambda: ops.paged_decode_attention(
+            q, pool, st.page_table, st.plan, cfg.head_dim ** -0.5, st.workspace))
+        o = run("o_proj", lambda: ops.qmm(attn.view(B, -1), self.o))
+        hn, h = run("add_rmsnorm", lambda: ops.rmsnorm(o, self.post_norm, cfg.eps, resid=x, return_sum=True))
+        logits = run("router_proj", lambda: ops.qmm(hn, moe.router))
+        inds, scores = run("router_topk", lambda: ops.router_topk(logits, moe.top_k, moe.norm_topk))
+        pk = run("moe_pack", lambda: ops.moe_pack(inds, moe.num_experts))
+        hh = run("gate_up_swiglu", lambda: ops.expert_gate_up(hn, moe.gate_up, pk))
+        r = run("down", lambda: ops.expert_down(hh, moe.down, pk))
+        y = run("combine", lambda: ops.moe_combine(r, pk, scores, h))
+        if debug is not None:
+            debug.update(xn=xn, qkv=qkv, q=q, attn=attn, o=o, h=h, hn=hn, logits=logits, inds=inds,
+                         scores=scores, y=y)
+        return y
+
+
+class Model:
+    """A stack of decoder layers and the ragged batched decode step."""
+
+    def __init__(self, cfg: MoEConfig, layer_weights: list, prepack: bool = True):
+        self.cfg = cfg
+        self.layers = [DecoderLayer(cfg, w, prepack) for w in layer_weights]
+
+    def make_state(self, pos_host, page_table: torch.Tensor) -> StepState:
+        return make_step_state(self.cfg, pos_host, page_table)
+
+    def decode_step(self, x: torch.Tensor, pools: list, st: StepState, prof=None) -> torch.Tensor:
+        """x [B, D] bf16 hidden rows -> the last layer's output rows; pools[l] is layer l's KV pool."""
+        for layer, pool in zip(self.layers, pools):
+            x = layer.step(x, pool, st, prof=prof)
+        return x

@@ -19,7 +19,7 @@ class MoEBlock:
     """Router + routed experts over ragged token rows x [B, D] (bf16, on the GPU)."""
 
     def __init__(self, router: QLinear, gate_up: QLinear, down: QLinear, top_k: int = 8,
-                 norm_topk: bool = True):
+                 norm_topk: bool = True, prepack: bool = True):
         for lin in (router, gate_up, down):
             lin.validate()
         if gate_up.weight.dim() != 3 or down.weight.dim() != 3:
@@ -29,6 +29,8 @@ class MoEBlock:
             raise ValueError("router, gate_up and down disagree on the number of experts")
         if down.in_dims * 2 != gate_up.out_dims or down.out_dims != gate_up.in_dims:
             raise ValueError("down must be [E, D, I] for a gate_up stack [E, 2I, D]")
+        if prepack:  # one-time reorder into the MFMA tile layout (coalesced weight streaming)
+            router, gate_up, down = ops.prepack(router), ops.prepack(gate_up), ops.prepack(down)
         self.router, self.gate_up, self.down = router, gate_up, down
         self.top_k = int(top_k)
         self.norm_topk = bool(norm_topk)

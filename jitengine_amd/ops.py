@@ -110,18 +110,72 @@ def moe_pack(inds: torch.Tensor, n_experts: int) -> Packing:
     return pk
 
 
-# ----------------------------------------------------------------------------- projections
-def qmm(x: torch.Tensor, lin: QLinear) -> torch.Tensor:
-    """x [T, K] bf16 -> [T, N] bf16 against a 4-bit matrix [N, K]: QLinear.__call__ / .rows
-    (Q36/linear.py:219-313)."""
-    _need(x, torch.bfloat16, "x")
-    if lin.weight.dim() != 2:
-        raise ValueError("qmm takes one [N, K] matrix")
+# ----------------------------------------------------------------------------- packed layout
+@dataclass
+class PackedQ4:
+    """A quantized matrix or expert stack [E, N, K] reordered into the MFMA tile layout
+    (jit_q4_prepack): the same bytes as the MLX layout, read by the kernels with coalesced 1 KB
+    loads.  `data` is a uint8 device tensor."""
+
+    data: torch.Tensor
+    E: int
+    N: int
+    K: int
+    stacked: bool
+
+    @property
+    def in_dims(self) -> int:
+        return self.K
+
+    @property
+    def out_dims(self) -> int:
+        return self.N
+
+    @property
+    def nbytes(self) -> int:
+        return self.data.numel()
+
+
+def packed_bytes(E: int, N: int, K: int) -> int:
+    return int(_lib.lib().jit_q4_packed_bytes(int(E), int(N), int(K)))
+
+
+def prepack(lin: QLinear) -> PackedQ4:
+    """Reorder a device QLinear (matrix [N, K] or stack [E, N, K]) into the packed tile layout."""
     lin.validate()
+    if not lin.weight.is_cuda:
+        raise ValueError("prepack takes device tensors")
+    stacked = lin.weight.dim() == 3
+    E = lin.weight.shape[0] if stacked else 1
+    N, K = lin.out_dims, lin.in_dims
+    nbytes = packed_bytes(E, N, K)
+    if nbytes < 0:
+        raise _lib.UnsupportedShape(f"prepack covers N % 16 == 0 and K % 128 == 0, got N={N} K={K}")
+    out = torch.empty(nbytes, dtype=torch.uint8, device=lin.weight.device)
+    _lib.check(
+        _lib.lib().jit_q4_prepack(_p(lin.weight), _p(lin.scales), _p(lin.biases), E, N, K, _p(out), _stream()),
+        "q4_prepack",
+    )
+    return PackedQ4(out, E, N, K, stacked)
+
+
+# ----------------------------------------------------------------------------- projections
+def qmm(x: torch.Tensor, lin) -> torch.Tensor:
+    """x [T, K] bf16 -> [T, N] bf16 against a 4-bit matrix [N, K] (QLinear in the MLX layout or
+    PackedQ4): QLinear.__call__ / .rows (Q36/linear.py:219-313)."""
+    _need(x, torch.bfloat16, "x")
     T, K = x.shape
     if K != lin.in_dims:
         raise ValueError(f"x has K = {K}, the matrix takes {lin.in_dims}")
     y = torch.empty((T, lin.out_dims), dtype=torch.bfloat16, device=x.device)
+    if isinstance(lin, PackedQ4):
+        if lin.stacked:
+            raise ValueError("qmm takes one [N, K] matrix")
+        _lib.check(_lib.lib().jit_qmm_packed(_p(x), T, K, _p(lin.data), lin.N, _p(y), _stream()), "qmm_packed")
+        return y
+    if lin.weight.dim() != 2:
+        raise ValueError("qmm takes one [N, K] matrix")
+    lin.validate()
     _lib.check(
         _lib.lib().jit_qmm(
             _p(x), T, K, _p(lin.weight), _p(lin.scales), _p(lin.biases), lin.out_dims, _p(y), _stream()
@@ -131,41 +185,60 @@ def qmm(x: torch.Tensor, lin: QLinear) -> torch.Tensor:
     return y
 
 
-def expert_gate_up(x: torch.Tensor, gate_up: QLinear, pk: Packing) -> torch.Tensor:
+def _experts_of(lin) -> int:
+    if isinstance(lin, PackedQ4):
+        if not lin.stacked:
+            raise ValueError("expert projections take a stack [E, N, K]")
+        return lin.E
+    lin.validate()
+    if lin.weight.dim() != 3:
+        raise ValueError("expert projections take a stack [E, N, K]")
+    return lin.weight.shape[0]
+
+
+def expert_gate_up(x: torch.Tensor, gate_up, pk: Packing) -> torch.Tensor:
     """x [B, K] bf16, fused stack [E, 2I, K] -> h [P, I] bf16 in sorted pair order: the grouped
     gate||up + SwiGLU (expert_gate_up_exact(_rows), Q36/kernels/expert_solo.py:213-232,380-401)."""
     _need(x, torch.bfloat16, "x")
-    gate_up.validate()
-    E, two_i = gate_up.weight.shape[0], gate_up.out_dims
+    E = _experts_of(gate_up)
     if x.shape[-1] != gate_up.in_dims or E != pk.E:
         raise ValueError("x / stack / packing disagree on K or E")
-    I = two_i // 2
+    I = gate_up.out_dims // 2
     h = torch.empty((pk.P, I), dtype=torch.bfloat16, device=x.device)
-    _lib.check(
-        _lib.lib().jit_moe_gate_up_swiglu(
+    L = _lib.lib()
+    if isinstance(gate_up, PackedQ4):
+        rc = L.jit_moe_gate_up_swiglu_packed(
+            _p(x), x.shape[-1], _p(pk.pair_row), _p(pk.expert_cnt), _p(pk.expert_off), E, _p(gate_up.data),
+            I, pk.P, _p(h), _stream(),
+        )
+    else:
+        rc = L.jit_moe_gate_up_swiglu(
             _p(x), x.shape[-1], _p(pk.pair_row), _p(pk.expert_cnt), _p(pk.expert_off), E,
             _p(gate_up.weight), _p(gate_up.scales), _p(gate_up.biases), I, pk.P, _p(h), _stream(),
-        ),
-        "moe_gate_up",
-    )
+        )
+    _lib.check(rc, "moe_gate_up")
     return h
 
 
-def expert_down(h: torch.Tensor, down: QLinear, pk: Packing) -> torch.Tensor:
+def expert_down(h: torch.Tensor, down, pk: Packing) -> torch.Tensor:
     """h [P, I] bf16, stack [E, D, I] -> r [P, D] bf16 (the down gather, Q36/model/moe.py:193)."""
     _need(h, torch.bfloat16, "h")
-    down.validate()
-    E, D = down.weight.shape[0], down.out_dims
+    E = _experts_of(down)
+    D = down.out_dims
     if h.shape[-1] != down.in_dims or E != pk.E or h.shape[0] != pk.P:
         raise ValueError("h / stack / packing disagree on I, E or P")
     r = torch.empty((pk.P, D), dtype=torch.bfloat16, device=h.device)
-    _lib.check(
-        _lib.lib().jit_moe_down(
+    L = _lib.lib()
+    if isinstance(down, PackedQ4):
+        rc = L.jit_moe_down_packed(
+            _p(h), h.shape[-1], _p(pk.expert_cnt), _p(pk.expert_off), E, _p(down.data), D, pk.P, _p(r), _stream(),
+        )
+    else:
+        rc = L.jit_moe_down(
             _p(h), h.shape[-1], _p(pk.expert_cnt), _p(pk.expert_off), E, _p(down.weight),
             _p(down.scales), _p(down.biases), D, pk.P, _p(r), _stream(),
-        ),
-        "moe_down",
-    )
+        )
+    _lib.check(rc, "moe_down")
     return r
 
 
@@ -186,6 +259,54 @@ def moe_combine(r: torch.Tensor, pk: Packing, scores: torch.Tensor, resid: torch
         "moe_combine",
     )
     return y
+
+
+# ----------------------------------------------------------------------------- decoder block glue
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, resid: torch.Tensor | None = None,
+            return_sum: bool = False):
+    """RMSNorm rows of x (mx.fast.rms_norm, Q36/model/model.py:65-80); with resid the normed row
+    is h = x + resid, and return_sum=True returns (normed, h)."""
+    _need(x, torch.bfloat16, "x")
+    _need(w, torch.bfloat16, "w")
+    rows, D = x.shape
+    if w.shape != (D,):
+        raise ValueError(f"norm weight must be [{D}]")
+    if resid is not None:
+        _need(resid, torch.bfloat16, "resid")
+        if resid.shape != x.shape:
+            raise ValueError("resid must match x")
+    y = torch.empty_like(x)
+    h = torch.empty_like(x) if (resid is not None and return_sum) else None
+    _lib.check(
+        _lib.lib().jit_rmsnorm(_p(x), _p(resid), rows, D, _p(w), float(eps), _p(h), _p(y), _stream()), "rmsnorm"
+    )
+    if return_sum:
+        return y, (h if h is not None else x)
+    return y
+
+
+def qk_norm_rope_append(qkv: torch.Tensor, H: int, Hkv: int, q_norm: torch.Tensor, k_norm: torch.Tensor,
+                        eps: float, inv_freq: torch.Tensor, pos: torch.Tensor, page_table: torch.Tensor,
+                        pool: torch.Tensor) -> torch.Tensor:
+    """qkv [B, (H + 2 Hkv) * 128] -> q [B, H, 128] (normed, rotated); k, v appended to the pool at
+    pos (Q36/model/attention.py:99-119 + KVSlot.append)."""
+    _need(qkv, torch.bfloat16, "qkv")
+    _need(pool, torch.bfloat16, "pool")
+    _need(pos, torch.int32, "pos")
+    _need(page_table, torch.int32, "page_table")
+    _need(inv_freq, torch.float32, "inv_freq")
+    B = qkv.shape[0]
+    if qkv.shape[1] != (H + 2 * Hkv) * HEAD_DIM or pool.shape[2] != Hkv or inv_freq.numel() != HEAD_DIM // 2:
+        raise ValueError("qkv / pool / inv_freq do not match the head geometry")
+    q = torch.empty((B, H, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
+    _lib.check(
+        _lib.lib().jit_qk_norm_rope_append(
+            _p(qkv), B, H, Hkv, _p(q_norm), _p(k_norm), float(eps), _p(inv_freq), _p(pos), _p(page_table),
+            page_table.shape[1], _p(pool), _p(q), _stream(),
+        ),
+        "qk_norm_rope_append",
+    )
+    return q
 
 
 # ----------------------------------------------------------------------------- paged KV

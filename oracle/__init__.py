@@ -17,6 +17,8 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
   moe_gate_up / moe_down  vs qmm + swiglu composed in numpy (different code path, same maths)
   moe_combine             vs torch bf16 ops in slot order (a library routine)
   kv_append_paged/gather  integer addressing: round trip, page-permutation invariance
+  q4_prepack              a byte permutation (multiset of bytes preserved, every word placed once);
+                          on the GPU, GEMMs on packed and MLX layouts agree bit for bit
   paged_decode_attn       vs torch scaled_dot_product_attention in float64 on gathered KV
 """
 
@@ -178,6 +180,17 @@ def dequant4(w, s, b) -> np.ndarray:
     return out
 
 
+def q4_prepack(w, s, b) -> np.ndarray:
+    """The packed tile layout (uint8) of a stack w [E, N, K/8] (or a matrix [N, K/8])."""
+    w, s, b = _u32(w), _u16(s), _u16(b)
+    if w.ndim == 2:
+        w, s, b = w[None], s[None], b[None]
+    E, N, K = w.shape[0], w.shape[1], w.shape[2] * 8
+    out = np.empty(E * (N // 16) * (K // 128) * 1152, np.uint8)
+    _check(lib().jo_q4_prepack(_p(w), _p(s), _p(b), E, N, K, _p(out)), "q4_prepack")
+    return out
+
+
 def qmm(x, w, s, b):
     """x [T, K] bf16 against one [N, K] quantized matrix -> (float64 [T, N], bf16 [T, N])."""
     x, w, s, b = _u16(x), _u32(w), _u16(s), _u16(b)
@@ -245,6 +258,61 @@ def moe_experts(x, inds, scores, gu: tuple, dn: tuple, n_experts: int) -> dict:
     r = moe_down(h, inds, pack, *dn)
     y = moe_combine(r, pack["inv"], scores)
     return {"pack": pack, "h": h, "r": r, "y": y}
+
+
+# ----------------------------------------------------------------------------- decoder block
+def rmsnorm(x, w, eps: float, resid=None):
+    """(y, h): y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))) of h = x (+ resid)."""
+    x, w = _u16(x), _u16(w)
+    rows, D = x.shape
+    y = np.empty_like(x)
+    h = np.empty_like(x) if resid is not None else None
+    rs = _u16(resid) if resid is not None else None
+    lib().jo_rmsnorm.argtypes = [_P, _P, _I, _I, _P, ctypes.c_float, _P, _P]
+    _check(lib().jo_rmsnorm(_p(x), _p(rs) if rs is not None else None, rows, D, _p(w), float(eps),
+                            _p(h) if h is not None else None, _p(y)), "rmsnorm")
+    return y, (h if h is not None else x)
+
+
+def qk_norm_rope_append(qkv, H: int, Hkv: int, qn, kn, eps: float, inv_freq, pos, pool, page_table):
+    """q [B, H, 128] bf16; writes k, v into pool (in place) at positions pos."""
+    qkv, qn, kn = _u16(qkv), _u16(qn), _u16(kn)
+    invf = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    ps, pt = _i32(pos), _i32(page_table)
+    assert pool.flags["C_CONTIGUOUS"] and pool.dtype == np.uint16
+    B = qkv.shape[0]
+    q = np.empty((B, H, 128), np.uint16)
+    lib().jo_qk_norm_rope_append.argtypes = [_P, _I, _I, _I, _P, _P, ctypes.c_float, _P, _P, _P, _I, _I, _P, _P]
+    _check(lib().jo_qk_norm_rope_append(_p(qkv), B, H, Hkv, _p(qn), _p(kn), float(eps), _p(invf), _p(ps), _p(pt),
+                                        pt.shape[1], pool.shape[0], _p(pool), _p(q)), "qk_norm_rope_append")
+    return q
+
+
+def decoder_layer(x, layer: dict, pool, page_table, pos, cfg: dict, routing=None) -> dict:
+    """One decoder layer of the BASELINE geometry for rows x [B, D] (the reference's layer step,
+    Q36/model/model.py:77-80 with Qwen3_5MoeAttention.step and the MoE block): input RMSNorm ->
+    qkv -> q/k norm + RoPE + KV append -> attention over pos + 1 keys -> o_proj -> residual ->
+    post-attention RMSNorm -> router -> experts -> combine + residual.  `layer` holds numpy
+    weights (quantized ones as (w, s, b) triples); `pool` is updated in place.  `routing`
+    (inds, scores) overrides the router's choice (used to compare against another
+    implementation's routing).  Returns every intermediate."""
+    H, Hkv, E, k = cfg["heads"], cfg["kv_heads"], cfg["experts"], cfg["top_k"]
+    eps = cfg["eps"]
+    xn, _ = rmsnorm(x, layer["input_norm"], eps)
+    _, qkv = qmm(xn, *layer["qkv"])
+    q = qk_norm_rope_append(qkv, H, Hkv, layer["q_norm"], layer["k_norm"], eps, cfg["inv_freq"], pos, pool, page_table)
+    lens = np.asarray(pos, np.int64) + 1
+    attn = paged_decode_attn(q, pool, page_table, lens, 128 ** -0.5)
+    _, o = qmm(attn.reshape(x.shape[0], -1), *layer["o"])
+    hn, h = rmsnorm(o, layer["post_norm"], eps, resid=x)
+    _, logits = qmm(hn, *layer["router"])
+    inds, scores, _ = router_topk(logits, k, True)
+    if routing is not None:
+        inds, scores = routing
+    ex = moe_experts(hn, inds, scores, layer["gate_up"], layer["down"], E)
+    y = f32_to_bf16(bf16_to_f32(h) + bf16_to_f32(ex["y"]))
+    return {"xn": xn, "qkv": qkv, "q": q, "attn": attn, "o": o, "h": h, "hn": hn, "logits": logits,
+            "inds": inds, "scores": scores, "y": y}
 
 
 # ----------------------------------------------------------------------------- paged KV

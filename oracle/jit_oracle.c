@@ -551,3 +551,110 @@ void jo_set_num_threads(int n) {
   (void)n;
 #endif
 }
+
+/* ------------------------------------------------- decoder block glue
+ * RMSNorm as mx.fast.rms_norm computes it for the decoder layer
+ * (Q36/model/model.py:65-80, Q36/model/attention.py:59-60): r = 1/sqrt(mean(x^2)
+ * + eps) (float64 here), y = bf16(w * bf16(x * r)).  With resid, the normed row
+ * is h = bf16(x + resid) (written to h_out if given). */
+int jo_rmsnorm(const uint16_t *x, const uint16_t *resid, int rows, int D, const uint16_t *w, float eps,
+               uint16_t *h_out, uint16_t *y) {
+  if (rows < 0 || D <= 0) return JO_EINVAL;
+  float *v = (float *)malloc(sizeof(float) * (size_t)D);
+  if (!v) return JO_ENOMEM;
+  for (int r = 0; r < rows; r++) {
+    double ss = 0.0;
+    for (int i = 0; i < D; i++) {
+      float a = bf2f(x[(size_t)r * D + i]);
+      if (resid) a = bf2f(f2bf(a + bf2f(resid[(size_t)r * D + i])));
+      if (resid && h_out) h_out[(size_t)r * D + i] = f2bf(a);
+      v[i] = a;
+      ss += (double)a * (double)a;
+    }
+    const double rr = 1.0 / sqrt(ss / D + (double)eps);
+    for (int i = 0; i < D; i++)
+      y[(size_t)r * D + i] = f2bf(bf2f(w[i]) * bf2f(f2bf((float)((double)v[i] * rr))));
+  }
+  free(v);
+  return JO_OK;
+}
+
+/* q/k RMSNorm + RoPE + KV append (Qwen3_5MoeAttention.step without the output
+ * gate, Q36/model/attention.py:99-119): per head of 128 dims, RMSNorm with the
+ * q or k norm weight, then RoPE with traditional = False (mx.fast.rope): pairs
+ * (i, i + 64) rotated by angle = fp32(pos) * inv_freq[i] -- the fp32 product
+ * MLX forms -- with cos/sin and the rotation in float64, rounded to bf16 once.
+ * q -> q_out [B, H, 128]; k and v -> the pool at pos[b] (jo_kv_append_paged's
+ * layout). */
+int jo_qk_norm_rope_append(const uint16_t *qkv, int B, int H, int Hkv, const uint16_t *qn,
+                           const uint16_t *kn, float eps, const float *inv_freq, const int32_t *pos,
+                           const int32_t *page_table, int max_pages, int num_pages, uint16_t *pool,
+                           uint16_t *q_out) {
+  if (B < 0 || H <= 0 || Hkv <= 0) return JO_EINVAL;
+  const int Dh = 128, nh = H + 2 * Hkv;
+  for (int b = 0; b < B; b++) {
+    if (pos[b] < 0 || pos[b] / JO_PAGE >= max_pages) return JO_EINVAL;
+    const int page = page_table[(size_t)b * max_pages + pos[b] / JO_PAGE];
+    if (page < 0 || page >= num_pages) return JO_EINVAL;
+    const int slot = pos[b] % JO_PAGE;
+    for (int hd = 0; hd < nh; hd++) {
+      const uint16_t *src = qkv + ((size_t)b * nh + hd) * Dh;
+      if (hd >= H + Hkv) {
+        const int h = hd - H - Hkv;
+        for (int d = 0; d < Dh; d++) pool[v_index(page, Hkv, Dh, h, slot, d)] = src[d];
+        continue;
+      }
+      const uint16_t *nw = hd < H ? qn : kn;
+      double ss = 0.0;
+      for (int d = 0; d < Dh; d++) ss += (double)bf2f(src[d]) * (double)bf2f(src[d]);
+      const double rr = 1.0 / sqrt(ss / Dh + (double)eps);
+      float xn[128];
+      for (int d = 0; d < Dh; d++) xn[d] = bf2f(f2bf(bf2f(nw[d]) * bf2f(f2bf((float)((double)bf2f(src[d]) * rr)))));
+      uint16_t out[128];
+      for (int i = 0; i < 64; i++) {
+        const float ang = (float)pos[b] * inv_freq[i];
+        const double c = cos((double)ang), s = sin((double)ang);
+        out[i] = f2bf((float)(xn[i] * c - xn[i + 64] * s));
+        out[i + 64] = f2bf((float)(xn[i] * s + xn[i + 64] * c));
+      }
+      if (hd < H) {
+        memcpy(q_out + ((size_t)b * H + hd) * Dh, out, sizeof out);
+      } else {
+        for (int d = 0; d < Dh; d++) pool[k_index(page, Hkv, Dh, hd - H, slot, d)] = out[d];
+      }
+    }
+  }
+  return JO_OK;
+}
+
+/* ------------------------------------------------- packed tile layout
+ * The build's MI355X layout of a quantized stack [E, N, K] (no counterpart in
+ * the reference): per (expert, block of 16 rows, pair of groups) a 1152-byte
+ * tile; bytes 0..1023 hold, for lane l = 16 j + r (j = l / 16, r = l % 16),
+ * words 2j, 2j+1 of group 2gp and words 2j, 2j+1 of group 2gp+1 of row 16 rb + r
+ * (word w of group g = word 8g + w of the row); bytes 1024..1151 hold, for row
+ * r, (scale[2gp], scale[2gp+1], bias[2gp], bias[2gp+1]) bf16. */
+int jo_q4_prepack(const uint32_t *w, const uint16_t *s, const uint16_t *b, int E, int N, int K,
+                  uint8_t *out) {
+  if (E <= 0 || N <= 0 || K <= 0 || (N % 16) != 0 || (K % 128) != 0) return JO_EINVAL;
+  const int GP = K / 128, NRB = N / 16, G = K / 64, KW = K / 8;
+  for (int e = 0; e < E; e++)
+    for (int rb = 0; rb < NRB; rb++)
+      for (int gp = 0; gp < GP; gp++) {
+        uint8_t *t = out + (((size_t)e * NRB + rb) * GP + gp) * 1152;
+        for (int l = 0; l < 64; l++) {
+          const int j = l / 16, r = l % 16;
+          const uint32_t *wr = w + ((size_t)e * N + rb * 16 + r) * KW;
+          const uint32_t words[4] = {wr[8 * (2 * gp) + 2 * j], wr[8 * (2 * gp) + 2 * j + 1],
+                                     wr[8 * (2 * gp + 1) + 2 * j], wr[8 * (2 * gp + 1) + 2 * j + 1]};
+          memcpy(t + 16 * l, words, 16);
+        }
+        for (int r = 0; r < 16; r++) {
+          const size_t row = (size_t)e * N + rb * 16 + r;
+          const uint16_t v[4] = {s[row * G + 2 * gp], s[row * G + 2 * gp + 1], b[row * G + 2 * gp],
+                                 b[row * G + 2 * gp + 1]};
+          memcpy(t + 1024 + 8 * r, v, 8);
+        }
+      }
+  return JO_OK;
+}

@@ -1,0 +1,135 @@
+"""Decoder-block kernels and a whole decoder layer on the GPU vs the CPU oracle (MI355X only)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from jitengine_amd import ops
+from jitengine_amd.model import DecoderLayer, MoEConfig, Model, make_step_state, random_layer_weights, rope_inv_freq
+from tests.helpers import assert_close_bf16, bf16_tensor, bf16_to_f32, normal_bf16, u16
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _i32(a) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(DEV)
+
+
+@pytest.mark.parametrize("resid", [False, True])
+@pytest.mark.parametrize("rows", [1, 32, 300])
+def test_rmsnorm_parity(resid, rows):
+    x = normal_bf16((rows, 2048), seed=rows, scale=2.0)
+    r = normal_bf16((rows, 2048), seed=rows + 1)
+    w = oracle.f32_to_bf16((1 + 0.02 * np.random.default_rng(3).standard_normal(2048)).astype(np.float32))
+    y, h = ops.rmsnorm(bf16_tensor(x, DEV), bf16_tensor(w, DEV), 1e-6,
+                       resid=bf16_tensor(r, DEV) if resid else None, return_sum=True)
+    wy, wh = oracle.rmsnorm(x, w, 1e-6, resid=r if resid else None)
+    assert np.array_equal(u16(h), wh)
+    st = assert_close_bf16(u16(y), wy, what="rmsnorm")
+    assert st["bit_equal"] > 0.97, st
+
+
+@pytest.mark.parametrize("pos", [[0, 1, 15, 16, 17], [4096, 32767, 100000, 262143]])
+def test_qk_norm_rope_append_parity(pos):
+    H, Hkv, B = 32, 4, len(pos)
+    qkv = normal_bf16((B, (H + 2 * Hkv) * 128), seed=sum(pos) % 1000, scale=1.5)
+    rng = np.random.default_rng(7)
+    qn = oracle.f32_to_bf16((1 + 0.02 * rng.standard_normal(128)).astype(np.float32))
+    kn = oracle.f32_to_bf16((1 + 0.02 * rng.standard_normal(128)).astype(np.float32))
+    inv = rope_inv_freq(1e6, 128)
+    npg = max(p // 16 for p in pos) + 1
+    num_pages = B + 3
+    table = rng.integers(0, num_pages, (B, npg)).astype(np.int32)  # only the written page matters
+    for b, p in enumerate(pos):
+        table[b, p // 16] = b  # distinct pages for the written slots
+    pool = normal_bf16((num_pages, 2, Hkv, 2048), seed=9)
+    pt = bf16_tensor(pool, DEV)
+    q = ops.qk_norm_rope_append(bf16_tensor(qkv, DEV), H, Hkv, bf16_tensor(qn, DEV), bf16_tensor(kn, DEV), 1e-6,
+                                torch.from_numpy(inv).to(DEV), _i32(pos), _i32(table), pt)
+    want_pool = pool.copy()
+    wq = oracle.qk_norm_rope_append(qkv, H, Hkv, qn, kn, 1e-6, inv, np.array(pos, np.int32), want_pool, table)
+    st = assert_close_bf16(u16(q), wq, what="q")
+    assert st["bit_equal"] > 0.95, st
+    got_pool = u16(pt)
+    assert np.array_equal(got_pool[:, 1], want_pool[:, 1])  # V parts: copied verbatim, nothing else touched
+    kg = got_pool[:, 0].reshape(num_pages, Hkv, 16, 128).copy()
+    kw = want_pool[:, 0].reshape(num_pages, Hkv, 16, 128).copy()
+    for b, p in enumerate(pos):
+        assert_close_bf16(kg[b, :, p % 16], kw[b, :, p % 16], what="k")
+        kg[b, :, p % 16] = kw[b, :, p % 16]
+    assert np.array_equal(kg, kw)  # K parts: only the written slots changed
+
+
+def _layer_numpy(w: dict) -> dict:
+    def q(lin):
+        return (lin.weight.cpu().numpy().view(np.uint32), u16(lin.scales), u16(lin.biases))
+
+    return {"input_norm": u16(w["input_norm"]), "qkv": q(w["qkv"]), "q_norm": u16(w["q_norm"]),
+            "k_norm": u16(w["k_norm"]), "o": q(w["o"]), "post_norm": u16(w["post_norm"]),
+            "router": q(w["router"]), "gate_up": q(w["gate_up"]), "down": q(w["down"])}
+
+
+def _small_cfg():
+    return MoEConfig(experts=32, layers=2)
+
+
+def _ctx(lens, cfg, seed):
+    rng = np.random.default_rng(seed)
+    npg = [-(-(L + 1) // 16) for L in lens]
+    num_pages = sum(npg) + 3
+    perm = rng.permutation(num_pages)
+    table = np.zeros((len(lens), max(npg)), np.int32)
+    at = 0
+    for i, n in enumerate(npg):
+        table[i, :n] = perm[at:at + n]
+        at += n
+    pools = [normal_bf16((num_pages, 2, cfg.kv_heads, 2048), seed=seed + 10 + l) for l in range(cfg.layers)]
+    return table, pools
+
+
+def test_decoder_layer_parity():
+    """One layer, 12 ragged rows: every stage checked against the oracle's layer; the MoE half
+    is compared under the GPU's routing (routing is bit-exact given the router logits, and the
+    logits themselves are within tolerance), and rows whose float64 routing differs are counted."""
+    cfg = _small_cfg()
+    lens = [1, 15, 16, 100, 255, 256, 257, 1000, 3000, 4096, 5000, 20000]
+    w = random_layer_weights(cfg, seed=5, device=DEV)
+    layer = DecoderLayer(cfg, w)
+    table, pools = _ctx(lens, cfg, seed=6)
+    x = normal_bf16((len(lens), 2048), seed=7)
+    pool_t = bf16_tensor(pools[0], DEV)
+    st = make_step_state(cfg, np.array(lens), _i32(table))
+    dbg = {}
+    y = layer.step(bf16_tensor(x, DEV), pool_t, st, debug=dbg)
+    ref_pool = pools[0].copy()
+    ocfg = {"heads": cfg.heads, "kv_heads": cfg.kv_heads, "experts": cfg.experts, "top_k": cfg.top_k,
+            "eps": cfg.eps, "inv_freq": rope_inv_freq(cfg.rope_theta, 128)}
+    gi = dbg["inds"].cpu().numpy().view(np.uint32)
+    gs = u16(dbg["scores"])
+    ref = oracle.decoder_layer(x, _layer_numpy(w), ref_pool, table, np.array(lens, np.int32), ocfg, routing=(gi, gs))
+    for name in ("xn", "qkv", "q", "attn", "o", "h", "hn"):
+        assert_close_bf16(u16(dbg[name]).reshape(ref[name].shape), ref[name], what=name)
+    own = oracle.router_topk(ref["logits"], cfg.top_k, True)[0]
+    flips = int(np.sum(np.any(np.sort(own, -1) != np.sort(gi, -1), -1)))
+    assert flips <= 2, f"{flips} rows routed differently from the float64 logits"
+    assert_close_bf16(u16(y), ref["y"], what="layer output")
+
+
+def test_model_decode_step_rows_are_independent():
+    """A row's output does not depend on the other rows of the batch (the reference's
+    batched-row = solo-row property, Q36T/metal/engine/test_engine_consistency.py:43)."""
+    cfg = _small_cfg()
+    lens = [50, 3000, 17, 9000]
+    model = Model(cfg, [random_layer_weights(cfg, seed=20 + l, device=DEV) for l in range(cfg.layers)])
+    table, pools = _ctx(lens, cfg, seed=30)
+    x = normal_bf16((len(lens), 2048), seed=31)
+    st = model.make_state(np.array(lens), _i32(table))
+    batched = u16(model.decode_step(bf16_tensor(x, DEV), [bf16_tensor(p, DEV) for p in pools], st))
+    for b in range(len(lens)):
+        stb = model.make_state(np.array(lens[b:b + 1]), _i32(table[b:b + 1]))
+        solo = u16(model.decode_step(bf16_tensor(x[b:b + 1], DEV), [bf16_tensor(p, DEV) for p in pools], stb))
+        assert np.array_equal(solo[0], batched[b]), b

@@ -113,14 +113,70 @@ def _moe_inputs(B, E, D, I, seed):
     return gu, dn, x, inds, scores
 
 
-@pytest.mark.parametrize("B,E", [(64, 16), (5, 16), (1, 128)])
+def _sigmoid_bf16(g):
+    gf = bf16_to_f32(g).astype(np.float64)
+    y = 1.0 / (1.0 + np.exp(np.abs(gf)))
+    return oracle.f32_to_bf16(np.where(gf < 0, y, 1.0 - y).astype(np.float32))
+
+
+def _swiglu_np(g, u, sg=None):
+    """The oracle's SwiGLU rounding chain, vectorised (checked bit-exact against it below);
+    `sg` overrides the bf16 sigmoid(g)."""
+    sg = _sigmoid_bf16(g) if sg is None else sg
+    sl = oracle.f32_to_bf16(bf16_to_f32(g) * bf16_to_f32(sg))
+    return oracle.f32_to_bf16(bf16_to_f32(sl) * bf16_to_f32(u))
+
+
+def _bf16_neighbours(b):
+    """The bf16 values one ulp either side of each bit pattern (sign-magnitude order)."""
+    b = b.astype(np.int32)
+    mag, neg = b & 0x7FFF, (b & 0x8000) != 0
+    up = np.where(neg, np.where(mag > 0, b - 1, 0x0001), b + 1)      # towards +inf
+    dn = np.where(neg, b + 1, np.where(mag > 0, b - 1, 0x8001))      # towards -inf
+    return up.astype(np.uint16), dn.astype(np.uint16)
+
+
+@pytest.mark.parametrize("B,E", [(64, 16), (5, 16), (1, 128), (300, 8)])
 def test_gate_up_swiglu_parity(B, E):
+    """Every h is the reference's SwiGLU chain -- g, u (the float64 projections) rounded to
+    bf16, sigmoid(g) rounded, bf16(g * sigmoid) * u rounded -- with at most one bf16 ulp of
+    slack at each of the three roundings the kernel computes differently (g and u accumulate
+    in fp32; sigmoid uses the fp32 exp), so a rounding may land on the neighbouring bf16
+    value; (300, 8) gives experts more than 16 tokens (several token tiles per weight slice)."""
     gu, dn, x, inds, scores = _moe_inputs(B, E, 2048, 768, seed=50 + B)
     pk = ops.moe_pack(_i32(inds), E)
-    h = ops.expert_gate_up(bf16_tensor(x, DEV), _dev(gu), pk)
-    want = oracle.moe_gate_up(x, inds, oracle.moe_pack(inds, E), *stack_np(gu))
-    st = assert_close_bf16(u16(h), want, what="gate_up")
+    h = u16(ops.expert_gate_up(bf16_tensor(x, DEV), _dev(gu), pk))
+    opk = oracle.moe_pack(inds, E)
+    want = oracle.moe_gate_up(x, inds, opk, *stack_np(gu))
+    st = assert_close_bf16(h, want, what="gate_up", ulps=4.0)
     assert st["bit_equal"] > 0.95, st
+    w, s, b = stack_np(gu)
+    I = w.shape[1] // 2
+    flat = inds.reshape(-1)
+    g = np.empty_like(want)
+    u = np.empty_like(want)
+    for e in range(E):
+        ps = np.nonzero(flat[opk["order"]] == e)[0]
+        if ps.size == 0:
+            continue
+        rows = opk["pair_row"][ps]
+        g[ps] = oracle.qmm(x[rows], w[e, :I], s[e, :I], b[e, :I])[1]
+        u[ps] = oracle.qmm(x[rows], w[e, I:], s[e, I:], b[e, I:])[1]
+    assert np.array_equal(_swiglu_np(g, u), want)
+    ok = np.zeros(h.shape, bool)
+    for gg in (g, *_bf16_neighbours(g)):
+        sg = _sigmoid_bf16(gg)
+        for ss in (sg, *_bf16_neighbours(sg)):
+            for uu in (u, *_bf16_neighbours(u)):
+                ok |= _swiglu_np(gg, uu, ss) == h
+    # near zero (|g| or |u| ~ 1e-5) the fp32 accumulation's absolute error (~1e-6) spans many
+    # bf16 ulps: there the h values must agree to 2^-12 absolute instead
+    ok |= np.abs(bf16_to_f32(h).astype(np.float64) - bf16_to_f32(want)) <= 2.0**-12
+    bad = np.argwhere(~ok)[:6]
+    detail = [(tuple(i), float(bf16_to_f32(g[tuple(i)])), float(bf16_to_f32(u[tuple(i)])),
+               float(bf16_to_f32(h[tuple(i)])), float(bf16_to_f32(want[tuple(i)]))) for i in bad]
+    assert ok.all(), (f"{(~ok).sum()} of {ok.size} h values are neither within one ulp at each rounding point "
+                      f"nor within 2^-12 (index, g, u, h_gpu, h_oracle): {detail}")
 
 
 @pytest.mark.parametrize("B,E", [(64, 16), (7, 128)])
@@ -175,6 +231,34 @@ def test_moe_block_chain():
     assert_close_bf16(u16(y), want, what="moe block")
     y2 = blk(xt, bf16_tensor(res, DEV))
     assert torch.equal(y2, y)
+    direct = MoEBlock(_dev(router), _dev(gu), _dev(dn), top_k=8, prepack=False)
+    assert torch.equal(direct(xt, bf16_tensor(res, DEV)), y)
+
+
+# ----------------------------------------------------------------------------- packed layout
+@pytest.mark.parametrize("E,N,K", [(1, 128, 2048), (3, 1536, 2048), (2, 2048, 768), (1, 5120, 2048)])
+def test_prepack_bytes_match_oracle(E, N, K):
+    q = make_stack((E, N, K), seed=E + N)
+    got = ops.prepack(_dev(q)).data.cpu().numpy()
+    assert np.array_equal(got, oracle.q4_prepack(*stack_np(q)))
+
+
+@pytest.mark.parametrize("T,N,K", [(1, 128, 2048), (32, 5120, 2048), (17, 2048, 4096), (5, 256, 768)])
+def test_qmm_packed_equals_direct(T, N, K):
+    q = _dev(make_stack((N, K), seed=T + N))
+    x = bf16_tensor(normal_bf16((T, K), seed=T), DEV)
+    assert torch.equal(ops.qmm(x, ops.prepack(q)), ops.qmm(x, q))
+
+
+@pytest.mark.parametrize("B,E", [(64, 128), (300, 8), (1, 16)])
+def test_expert_paths_packed_equal_direct(B, E):
+    gu, dn, x, inds, scores = _moe_inputs(B, E, 2048, 768, seed=60 + B)
+    pk = ops.moe_pack(_i32(inds), E)
+    xt = bf16_tensor(x, DEV)
+    gud, dnd = _dev(gu), _dev(dn)
+    h = ops.expert_gate_up(xt, gud, pk)
+    assert torch.equal(ops.expert_gate_up(xt, ops.prepack(gud), pk), h)
+    assert torch.equal(ops.expert_down(h, ops.prepack(dnd), pk), ops.expert_down(h, dnd, pk))
 
 
 # ----------------------------------------------------------------------------- paged KV

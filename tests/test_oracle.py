@@ -287,3 +287,85 @@ def test_attention_page_permutation_invariance():
     pool2[perm] = pool
     b = oracle.paged_decode_attn(q, pool2, perm[table].astype(np.int32), lens, 0.088)
     assert np.array_equal(a, b)
+
+
+# ----------------------------------------------------------------------------- packed layout
+def test_prepack_is_a_permutation_of_words_and_scales():
+    E, N, K = 2, 32, 256
+    w = np.arange(E * N * K // 8, dtype=np.uint32).reshape(E, N, K // 8)  # every word distinct
+    s = np.arange(E * N * K // 64, dtype=np.uint16).reshape(E, N, K // 64)
+    b = (s + 40000).astype(np.uint16)
+    out = oracle.q4_prepack(w, s, b)
+    assert out.size == E * (N // 16) * (K // 128) * 1152
+    tiles = out.reshape(-1, 1152)
+    words = tiles[:, :1024].copy().view(np.uint32).ravel()
+    assert np.array_equal(np.sort(words), w.ravel())  # each word placed exactly once
+    sb = tiles[:, 1024:].copy().view(np.uint16).reshape(-1, 16, 4)
+    assert np.array_equal(np.sort(sb[..., :2].ravel()), s.ravel())
+    assert np.array_equal(np.sort(sb[..., 2:].ravel()), b.ravel())
+    # tile (e=1, rb=1, gp=1), lane 16*2 + 5: row 21, words 2*2, 2*2+1 of groups 2 and 3
+    t = tiles[(1 * 2 + 1) * 2 + 1]
+    lane = t[16 * (16 * 2 + 5):16 * (16 * 2 + 6)].view(np.uint32)
+    assert list(lane) == [w[1, 21, 8 * 2 + 4], w[1, 21, 8 * 2 + 5], w[1, 21, 8 * 3 + 4], w[1, 21, 8 * 3 + 5]]
+    assert list(t[1024 + 8 * 5:1024 + 8 * 6].view(np.uint16)) == [s[1, 21, 2], s[1, 21, 3], b[1, 21, 2], b[1, 21, 3]]
+
+
+# ----------------------------------------------------------------------------- decoder block glue
+def test_rmsnorm_matches_torch_rms_norm_float64():
+    x = normal_bf16((6, 2048), seed=70, scale=3.0)
+    w = f32_to_bf16((1 + 0.02 * np.random.default_rng(71).standard_normal(2048)).astype(np.float32))
+    y, _ = oracle.rmsnorm(x, w, 1e-6)
+    xt = torch.from_numpy(bf16_to_f32(x).astype(np.float64))
+    want = torch.nn.functional.rms_norm(xt, (2048,), weight=torch.from_numpy(bf16_to_f32(w).astype(np.float64)), eps=1e-6)
+    got = bf16_to_f32(y).astype(np.float64)
+    assert np.all(np.abs(got - want.numpy()) <= np.abs(want.numpy()) * 2.0**-7 + 1e-30)  # two bf16 roundings
+    # a power-of-two scale of x leaves the norm's output unchanged (closed form)
+    y4, _ = oracle.rmsnorm(f32_to_bf16(bf16_to_f32(x) * 4.0), w, 0.0)
+    y1, _ = oracle.rmsnorm(x, w, 0.0)
+    assert np.array_equal(y4, y1)
+    # the residual form normalises bf16(x + r) and returns that sum
+    r = normal_bf16((6, 2048), seed=72)
+    yr, h = oracle.rmsnorm(x, w, 1e-6, resid=r)
+    assert np.array_equal(h, f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(r)))
+    assert np.array_equal(yr, oracle.rmsnorm(h, w, 1e-6)[0])
+
+
+def _rope_case(pos, seed=80, H=2, Hkv=1):
+    qkv = normal_bf16((len(pos), (H + 2 * Hkv) * 128), seed=seed)
+    ones = f32_to_bf16(np.ones(128, np.float32))
+    inv = (1e6 ** (-np.arange(0, 128, 2) / 128)).astype(np.float32)
+    pages = max(p // 16 for p in pos) + 1
+    table = np.tile(np.arange(pages, dtype=np.int32), (len(pos), 1))
+    pool = np.zeros((pages, 2, Hkv, 2048), np.uint16)
+    q = oracle.qk_norm_rope_append(qkv, H, Hkv, ones, ones, 1e-6, inv, np.array(pos, np.int32), pool, table)
+    return qkv, q, pool, inv
+
+
+def test_rope_position_zero_is_the_norm_alone_and_rotation_keeps_pair_norms():
+    qkv, q, pool, inv = _rope_case([0, 5, 70000])
+    ones = f32_to_bf16(np.ones(128, np.float32))
+    normed, _ = oracle.rmsnorm(qkv[:, :256].reshape(-1, 128), ones, 1e-6)
+    assert np.array_equal(q[0].reshape(-1, 128), normed.reshape(3, 2, 128)[0])  # angle 0: identity
+    a = bf16_to_f32(normed.reshape(3, 2, 128)).astype(np.float64)
+    b = bf16_to_f32(q).astype(np.float64)
+    na = np.hypot(a[..., :64], a[..., 64:])
+    nb = np.hypot(b[..., :64], b[..., 64:])
+    assert np.all(np.abs(na - nb) <= na * 2.0**-6 + 1e-6)
+
+
+def test_rope_matches_complex_rotation():
+    qkv, q, pool, inv = _rope_case([12345], seed=81)
+    ones = f32_to_bf16(np.ones(128, np.float32))
+    xn = bf16_to_f32(oracle.rmsnorm(qkv[:, :128], ones, 1e-6)[0][0]).astype(np.float64)
+    ang = (np.float32(12345) * inv).astype(np.float64)  # the fp32 angle MLX forms
+    z = (xn[:64] + 1j * xn[64:]) * np.exp(1j * ang)
+    want = f32_to_bf16(np.concatenate([z.real, z.imag]).astype(np.float32))
+    assert np.array_equal(q[0, 0], want)
+
+
+def test_qk_append_writes_k_and_v_at_the_position():
+    qkv, q, pool, inv = _rope_case([3, 40], seed=82)
+    kc, vc = oracle.kv_gather(pool, np.array([0, 1, 2], np.int32), 41, 1, 128)
+    assert np.array_equal(vc[0, 40], qkv[1, 3 * 128:])  # v copied verbatim
+    assert np.array_equal(vc[0, 3], qkv[0, 3 * 128:])
+    assert not np.array_equal(kc[0, 40], qkv[1, 2 * 128:3 * 128])  # k normed + rotated
