@@ -189,7 +189,8 @@ int jit_qk_norm_rope_append(const uint16_t *qkv, int B, int H, int Hkv, const ui
  * Pool layout (the build's design; the reference keeps one contiguous
  * [1, Hkv, cap, Dh] buffer per request, Q36/kvcache/kv_cache.py:27-85):
  * pool [num_pages, 2, Hkv, 16 * 128] bf16 per layer; part 0 of a page holds K
- * slot-major ([slot][d]), part 1 holds V dim-major ([d][slot]).  Token t of
+ * chunk-major ([d / 32][slot][d % 32]: an MFMA fragment's 16 slots x 32 dims
+ * are 1 KB contiguous), part 1 holds V dim-major ([d][slot]).  Token t of
  * sequence b is at page page_table[b * max_pages + t / 16], slot t % 16.
  *
  * KV append: write k, v [B, Hkv, 128] of row b at position pos[b]

@@ -1,19 +1,26 @@
 // Paged KV pool append and split-K paged GQA decode attention for gfx950.
 //
-// Pool page (one layer): [2][Hkv][16 * 128] bf16 -- K slot-major ([slot][d],
-// 4 KiB per kv head), V dim-major ([d][slot], 4 KiB per kv head).
+// Pool page (one layer): [2][Hkv][16 * 128] bf16.  The K part of a (page, kv
+// head) is chunk-major -- [4 d-chunks][16 slots][32 dims], so the 16 slots x 32
+// dims one MFMA A fragment covers are 1 KB contiguous -- and the V part is
+// dim-major -- [128 dims][16 slots], so a B fragment's 16 dims x 4 slots per lane
+// group are 512 B contiguous.  Both are 4 KiB per (page, kv head).
 //
-// Attention work item: one workgroup per (chunk of one sequence, kv head); its 4
-// waves split the chunk's pages and each streams 2 pages (32 keys) per step:
-//   S^T[16 keys x 16 q heads] = K_page . Q^T     (4 MFMA 16x16x32 per page; the
-//        K page feeds the A operand directly: lane = slot, 16 B of d per MFMA)
+// Attention work item: one workgroup per 256-key chunk of one sequence, one wave per
+// kv head; a wave streams the chunk's keys two 16-key pages (32 keys) per step:
+//   S^T[16 keys x 16 q heads] = K_page . Q^T      (4 MFMA 16x16x32 per page)
 //   online softmax in the exp2 domain (fp32 running max / sum per q head)
-//   O[16 q heads x 128 d] += P . V               (8 MFMA 16x16x32 per 2 pages; the
-//        V page's dim-major rows feed the B operand with 8-byte loads)
-// so each K/V byte is read once for all G = H / Hkv query heads of its kv head
-// (G <= 16; rows G..15 of the tiles are padding).  The waves merge in LDS; a
-// sequence of one chunk writes its output directly, longer ones write fp32
-// (max, sum, o[128]) partials that attn_merge_kernel combines in chunk order.
+//   O^T[128 d x 16 q heads] += V^T . P^T           (8 MFMA 16x16x32, all 32 keys)
+// Every lane owns one q head (lane % 16) in the scores, the softmax state and the
+// output tile alike, so the rescale needs no lane exchange; the cross-lane max and
+// sum use the gfx950 permlane swaps.  Each K/V byte is read once for all
+// G = H / Hkv query heads of its kv head (G <= 16; tile columns G..15 are
+// padding).  A step's K registers are refilled for the next step as soon as its
+// scores are formed and its V registers as soon as P.V is issued, so the next
+// step's loads are in flight during the softmax and the MFMAs; the chunk's page
+// ids are fetched once up front.  A sequence of one chunk writes its output
+// directly, longer ones write fp32 (max, sum, o[128]) partials that
+// attn_merge_kernel combines in chunk order.
 #include "common.hpp"
 
 namespace {
@@ -21,14 +28,18 @@ namespace {
 constexpr int kD = JIT_HEAD_DIM;      // 128
 constexpr int kPage = JIT_PAGE_TOKENS;  // 16
 constexpr int kPageHead = kPage * kD;   // bf16 elements of one (page, part, kv head)
+constexpr int kChunk = 256;             // keys per work item (one wave per kv head)
+
+__device__ __forceinline__ int k_off(int slot, int d) { return k_page_offset(slot, d); }
 
 }  // namespace
 
-// Chunk length rule: a pure function of the sequence's own length (so results
-// do not depend on the batch), 256 keys up to 16K tokens, 512 beyond.
-extern "C" int jit_attn_chunk_tokens(int len) { return len <= 16384 ? 256 : 512; }
-
-__device__ __forceinline__ int chunk_tokens_dev(int len) { return len <= 16384 ? 256 : 512; }
+// Chunk length rule: a pure function of the sequence's own length (so results do
+// not depend on the batch); one size serves every length.
+extern "C" int jit_attn_chunk_tokens(int len) {
+  (void)len;
+  return kChunk;
+}
 
 namespace {
 
@@ -44,7 +55,7 @@ __global__ void kv_append_kernel(const uint16_t *__restrict__ k, const uint16_t 
   for (int t = threadIdx.x; t < Hkv * kD; t += blockDim.x) {
     const int h = t / kD, d = t % kD;
     const long long src = ((long long)b * Hkv + h) * kD + d;
-    pool[((long long)page * 2 * Hkv + h) * kPageHead + slot * kD + d] = k[src];
+    pool[((long long)page * 2 * Hkv + h) * kPageHead + k_off(slot, d)] = k[src];
     pool[(((long long)page * 2 + 1) * Hkv + h) * kPageHead + d * kPage + slot] = v[src];
   }
 }
@@ -63,24 +74,79 @@ struct AttnArgs {
   float qk_scale;  // scale * log2(e)
 };
 
-__global__ __launch_bounds__(256) void paged_attn_kernel(const AttnArgs a) {
-  __shared__ float sm[4][16], sl[4][16];
-  __shared__ float so[4][16][kD];
-  const int gc = blockIdx.x, kvh = blockIdx.y;
+// xor-16 / xor-32 lane exchanges, one VALU op each (gfx950 permlane swaps): with both
+// operands the same value, the two results are the even and the odd row (of each
+// row pair, resp. half) -- so any symmetric combination of them is the reduction.
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// K fragments of two pages: the A operand of S^T = K . Q^T (lane: slot lr, dims
+// 8*lg..8*lg+7 of each 32-dim chunk).
+__device__ __forceinline__ void load_k2(Frag8 (&k)[2][4], const uint16_t *pool, long long part_stride, int kvh,
+                                        int pg0, int pg1, int lr, int lg) {
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const uint16_t *kp = pool + (long long)(t ? pg1 : pg0) * part_stride + (long long)kvh * kPageHead;
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) k[t][cc].q = *(const uint4 *)(kp + cc * (kPage * 32) + lr * 32 + 8 * lg);
+  }
+}
+
+// V fragments of two pages: the A operand of O^T = V^T . P^T (lane: dim 16*cc + lr,
+// slots 4*lg..4*lg+3 of each page).
+__device__ __forceinline__ void load_v2(uint2 (&v)[2][8], const uint16_t *pool, long long part_stride, int kvh,
+                                        int Hkv, int pg0, int pg1, int lr, int lg) {
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const uint16_t *vp = pool + (long long)(t ? pg1 : pg0) * part_stride + (long long)(Hkv + kvh) * kPageHead;
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) v[t][cc] = *(const uint2 *)(vp + (16 * cc + lr) * kPage + 4 * lg);
+  }
+}
+
+// keep the bf16 halves of w whose key index (k, k + 1) is below L
+__device__ __forceinline__ uint32_t mask_pair(uint32_t w, int k, int L) {
+  return (k < L ? (w & 0xffffu) : 0u) | (k + 1 < L ? (w & 0xffff0000u) : 0u);
+}
+
+__global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
+  const int gc = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
+  const int kvh = blockIdx.y * (blockDim.x >> 6) + wave;
+  if (kvh >= a.Hkv) return;
   const int b = a.chunk_seq[gc];
   const int L = a.lens[b];
-  const int CK = chunk_tokens_dev(L);
   const int c = gc - a.chunk_start[b];
-  const int nchunks = (L + CK - 1) / CK;
-  const int wave = threadIdx.x >> 6, l = lane_id();
+  const int nchunks = (L + kChunk - 1) / kChunk;
   const int lr = l & 15, lg = l >> 4;
   const int G = a.G;
-  const int per_wave = CK / 4;
-  const int wk0 = c * CK + wave * per_wave;
-  const int wk1 = min(wk0 + per_wave, L);
-  const int32_t *prow = a.page_table + (long long)b * a.max_pages;
+  const int wk0 = c * kChunk;
+  const int wk1 = min(wk0 + kChunk, L);
+  const int npg = (wk1 - wk0 + kPage - 1) / kPage;  // >= 1: every chunk holds a key
+  const int nst = (npg + 1) >> 1;                     // 32-key steps
   const long long part_stride = (long long)2 * a.Hkv * kPageHead;  // bf16 per page
+  // the chunk's page ids, one per lane (at most kChunk / 16 = 16)
+  const int my_page = l < npg ? a.page_table[(long long)b * a.max_pages + (wk0 >> 4) + l] : 0;
+  const int last = npg - 1;
+  // page id i of the chunk (past the last page: the last page again, whose keys are
+  // masked, so prefetches need no branch)
+  auto page = [&](int i) { return __builtin_amdgcn_readlane(my_page, min(i, last)); };
 
+  // Q^T fragments (B operand of S^T = K . Q^T): q head lr, dims 8*lg.. of each chunk
   Frag8 qf[4];
   if (lr < G) {
     const uint16_t *qp = a.q + ((long long)b * a.H + kvh * G + lr) * kD + 8 * lg;
@@ -90,48 +156,38 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const AttnArgs a) {
 #pragma unroll
     for (int cc = 0; cc < 4; cc++) qf[cc].q = make_uint4(0, 0, 0, 0);
   }
+  // Lane (lr, lg) owns q head lr throughout: scores S^T[key 4*lg + i][head lr], the
+  // running max / sum of head lr, and O^T[dim 16*cc + 4*lg + i][head lr].
   float m_run = -INFINITY, l_run = 0.0f;
   f32x4 o[8];
 #pragma unroll
   for (int cc = 0; cc < 8; cc++) o[cc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = wk0; k0 < wk1; k0 += 32) {
-    const bool has1 = k0 + 16 < wk1;
-    const int pg0 = prow[k0 >> 4];
-    const int pg1 = has1 ? prow[(k0 >> 4) + 1] : pg0;
-    const uint16_t *kp0 = a.pool + (long long)pg0 * part_stride + (long long)kvh * kPageHead;
-    const uint16_t *kp1 = a.pool + (long long)pg1 * part_stride + (long long)kvh * kPageHead;
-    const uint16_t *vp0 = kp0 + (long long)a.Hkv * kPageHead;
-    const uint16_t *vp1 = kp1 + (long long)a.Hkv * kPageHead;
-    Frag8 kf0[4], kf1[4];
-#pragma unroll
-    for (int cc = 0; cc < 4; cc++) {
-      kf0[cc].q = *(const uint4 *)(kp0 + lr * kD + 32 * cc + 8 * lg);
-      kf1[cc].q = has1 ? *(const uint4 *)(kp1 + lr * kD + 32 * cc + 8 * lg) : make_uint4(0, 0, 0, 0);
-    }
-    uint2 va[8], vb[8];
-#pragma unroll
-    for (int cc = 0; cc < 8; cc++) {
-      va[cc] = *(const uint2 *)(vp0 + (16 * cc + lr) * kPage + 4 * lg);
-      vb[cc] = has1 ? *(const uint2 *)(vp1 + (16 * cc + lr) * kPage + 4 * lg) : make_uint2(0, 0);
-    }
+  Frag8 kf[2][4];
+  uint2 vv[2][8];
+  // K before V, as in the loop, so a step's K wait leaves its V loads in flight
+  load_k2(kf, a.pool, part_stride, kvh, page(0), page(1), lr, lg);
+  asm volatile("" ::: "memory");
+  load_v2(vv, a.pool, part_stride, kvh, a.Hkv, page(0), page(1), lr, lg);
+  for (int st = 0; st < nst; st++) {
+    const int k0 = wk0 + 32 * st;
     f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int cc = 0; cc < 4; cc++) {
-      s0 = mfma16x16x32(kf0[cc], qf[cc], s0);
-      s1 = mfma16x16x32(kf1[cc], qf[cc], s1);
+      s0 = mfma16x16x32(kf[0][cc], qf[cc], s0);
+      s1 = mfma16x16x32(kf[1][cc], qf[cc], s1);
     }
-    // lane holds S^T[key 4*lg + i][head lr] of both pages
+    // K registers are free: the next step's K is in flight during softmax and P.V
+    load_k2(kf, a.pool, part_stride, kvh, page(2 * st + 2), page(2 * st + 3), lr, lg);
     float p0[4], p1[4], tmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int key0 = k0 + 4 * lg + i, key1 = key0 + 16;
-      p0[i] = key0 < wk1 ? s0[i] * a.qk_scale : -INFINITY;
-      p1[i] = key1 < wk1 ? s1[i] * a.qk_scale : -INFINITY;
+      const int key = k0 + 4 * lg + i;
+      p0[i] = key < wk1 ? s0[i] * a.qk_scale : -INFINITY;
+      p1[i] = key + 16 < wk1 ? s1[i] * a.qk_scale : -INFINITY;
       tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
     }
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+    tmax = max_xor32(max_xor16(tmax));
     const float m_new = fmaxf(m_run, tmax);
     const float alpha = exp2f(m_run - m_new);
     float psum = 0.0f;
@@ -143,105 +199,137 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const AttnArgs a) {
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
+    // P^T fragment (B operand): head lr, k slots 8*lg + j = key 4*lg + j of the first
+    // page (j < 4) and of the second (j >= 4) -- the lane's own probabilities
     Frag8 pf;
-    if (lr < G) {
-      pf.u[0] = pack_bf16x2(p0[0], p0[1]);
-      pf.u[1] = pack_bf16x2(p0[2], p0[3]);
-      pf.u[2] = pack_bf16x2(p1[0], p1[1]);
-      pf.u[3] = pack_bf16x2(p1[2], p1[3]);
-    } else {
-      pf.q = make_uint4(0, 0, 0, 0);
-    }
+    pf.u[0] = pack_bf16x2(p0[0], p0[1]);
+    pf.u[1] = pack_bf16x2(p0[2], p0[3]);
+    pf.u[2] = pack_bf16x2(p1[0], p1[1]);
+    pf.u[3] = pack_bf16x2(p1[2], p1[3]);
+    if (lr >= G) pf.q = make_uint4(0, 0, 0, 0);
     // the tail page may hold stale slots past L: their p is 0, make their V 0 too
     if (k0 + 32 > L) {
+      const int kb = k0 + 4 * lg;
 #pragma unroll
       for (int cc = 0; cc < 8; cc++) {
-        const int kb0 = k0 + 4 * lg, kb1 = kb0 + 16;
-        va[cc].x = (kb0 + 0 < L ? (va[cc].x & 0xffffu) : 0u) | (kb0 + 1 < L ? (va[cc].x & 0xffff0000u) : 0u);
-        va[cc].y = (kb0 + 2 < L ? (va[cc].y & 0xffffu) : 0u) | (kb0 + 3 < L ? (va[cc].y & 0xffff0000u) : 0u);
-        vb[cc].x = (kb1 + 0 < L ? (vb[cc].x & 0xffffu) : 0u) | (kb1 + 1 < L ? (vb[cc].x & 0xffff0000u) : 0u);
-        vb[cc].y = (kb1 + 2 < L ? (vb[cc].y & 0xffffu) : 0u) | (kb1 + 3 < L ? (vb[cc].y & 0xffff0000u) : 0u);
+        vv[0][cc].x = mask_pair(vv[0][cc].x, kb, L);
+        vv[0][cc].y = mask_pair(vv[0][cc].y, kb + 2, L);
+        vv[1][cc].x = mask_pair(vv[1][cc].x, kb + 16, L);
+        vv[1][cc].y = mask_pair(vv[1][cc].y, kb + 18, L);
       }
     }
-    // O rows are q heads 4*lg + i: fetch their rescale factors from the lanes
-    // that own those heads in the score layout
-    float al[4];
+    // rescale only when some head's running max moved (alpha == 1 is a no-op)
+    if (__any(alpha != 1.0f)) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) al[i] = shfl_f(alpha, 4 * lg + i);
+      for (int cc = 0; cc < 8; cc++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[cc][i] *= alpha;
+    }
 #pragma unroll
     for (int cc = 0; cc < 8; cc++) {
       Frag8 vf;
-      vf.u[0] = va[cc].x;
-      vf.u[1] = va[cc].y;
-      vf.u[2] = vb[cc].x;
-      vf.u[3] = vb[cc].y;
-#pragma unroll
-      for (int i = 0; i < 4; i++) o[cc][i] *= al[i];
-      o[cc] = mfma16x16x32(pf, vf, o[cc]);
+      vf.u[0] = vv[0][cc].x;
+      vf.u[1] = vv[0][cc].y;
+      vf.u[2] = vv[1][cc].x;
+      vf.u[3] = vv[1][cc].y;
+      o[cc] = mfma16x16x32(vf, pf, o[cc]);
     }
+    load_v2(vv, a.pool, part_stride, kvh, a.Hkv, page(2 * st + 2), page(2 * st + 3), lr, lg);
+    // keep these loads in this step: sunk into the next step they would only be
+    // issued once that step's K has arrived
+    asm volatile("" ::: "memory");
   }
-  float l_tot = l_run + shfl_xor_f(l_run, 16);
-  l_tot = l_tot + shfl_xor_f(l_tot, 32);
-  if (lg == 0) {
-    sm[wave][lr] = m_run;
-    sl[wave][lr] = l_tot;
-  }
+  // per-head sum over the four lane groups
+  const float l_tot = sum_xor32(sum_xor16(l_run));
+  if (lr >= G) return;
+  const long long row = (long long)b * a.H + kvh * G + lr;  // this lane's q head
+  if (nchunks == 1) {
+    const float inv = 1.0f / l_tot;
 #pragma unroll
-  for (int cc = 0; cc < 8; cc++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int hh = 4 * lg + i;
-      if (hh < G) so[wave][hh][16 * cc + lr] = o[cc][i];
+    for (int cc = 0; cc < 8; cc++) {
+      uint2 w;
+      w.x = pack_bf16x2(o[cc][0] * inv, o[cc][1] * inv);
+      w.y = pack_bf16x2(o[cc][2] * inv, o[cc][3] * inv);
+      *(uint2 *)(a.out + row * kD + 16 * cc + 4 * lg) = w;
     }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < G * kD; idx += 256) {
-    const int hh = idx / kD, d = idx % kD;
-    float M = sm[0][hh];
+  } else {
+    const long long r = (long long)gc * a.H + kvh * G + lr;
 #pragma unroll
-    for (int w = 1; w < 4; w++) M = fmaxf(M, sm[w][hh]);
-    float Ls = 0.0f, O = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-      const float f = exp2f(sm[w][hh] - M);
-      Ls += sl[w][hh] * f;
-      O += so[w][hh][d] * f;
-    }
-    const int h = kvh * G + hh;
-    if (nchunks == 1) {
-      a.out[((long long)b * a.H + h) * kD + d] = (uint16_t)f2bf(O / Ls);
-    } else {
-      a.part_o[((long long)gc * a.H + h) * kD + d] = O;
-      if (d == 0) {
-        a.part_ml[((long long)gc * a.H + h) * 2 + 0] = M;
-        a.part_ml[((long long)gc * a.H + h) * 2 + 1] = Ls;
-      }
+    for (int cc = 0; cc < 8; cc++)
+      *(float4 *)(a.part_o + r * kD + 16 * cc + 4 * lg) = make_float4(o[cc][0], o[cc][1], o[cc][2], o[cc][3]);
+    if (lg == 0) {
+      a.part_ml[r * 2 + 0] = m_run;
+      a.part_ml[r * 2 + 1] = l_tot;
     }
   }
 }
 
-// Merge of a sequence's chunk partials in chunk order: one workgroup of 128
-// threads (one per d) per (sequence, q head).
-__global__ __launch_bounds__(128) void attn_merge_kernel(const int32_t *__restrict__ lens,
+// Merge of a sequence's chunk partials: one workgroup of 512 threads per (sequence,
+// q head).  The partials were written by workgroups on other XCDs, so every read
+// here misses this XCD's L2; the chunks are spread over 16 chunk lanes (thread =
+// chunk lane x 32 dim quads) so that many of those reads are in flight at once
+// instead of one per chunk in a serial chain.  Lane j sums chunks j, j + 16, ...
+// and the 16 lane sums are added in lane order: a fixed order that depends only on
+// the sequence's chunk count.
+constexpr int kMergeLanes = 16;
+
+__global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restrict__ lens,
                                                          const int32_t *__restrict__ chunk_start,
                                                          const float *__restrict__ part_o,
                                                          const float *__restrict__ part_ml, int H,
                                                          uint16_t *__restrict__ out) {
-  const int b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const int b = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
   const int L = lens[b];
-  const int CK = chunk_tokens_dev(L);
-  const int n = (L + CK - 1) / CK;
+  const int n = (L + kChunk - 1) / kChunk;
   if (n <= 1) return;
   const long long c0 = chunk_start[b];
+  __shared__ float s_max[512 / 64];
+  __shared__ float4 s_o[kMergeLanes][32];
+  __shared__ float s_l[kMergeLanes];
+  // the largest chunk max (max is exact, so any order)
   float M = -INFINITY;
-  for (int c = 0; c < n; c++) M = fmaxf(M, part_ml[((c0 + c) * H + h) * 2]);
-  float Ls = 0.0f, O = 0.0f;
-  for (int c = 0; c < n; c++) {
+  for (int c = t; c < n; c += 512) M = fmaxf(M, part_ml[((c0 + c) * H + h) * 2]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor_f(M, off));
+  if ((t & 63) == 0) s_max[t >> 6] = M;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < 512 / 64; w++) M = fmaxf(M, s_max[w]);
+  const int cl = t >> 5, dq = t & 31;
+  float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+  float Ls = 0.0f;
+#pragma unroll 4
+  for (int c = cl; c < n; c += kMergeLanes) {
     const long long r = (c0 + c) * H + h;
-    const float f = exp2f(part_ml[r * 2] - M);
-    Ls += part_ml[r * 2 + 1] * f;
-    O += part_o[r * kD + d] * f;
+    const float2 ml = *(const float2 *)(part_ml + r * 2);
+    const float4 o = *(const float4 *)(part_o + r * kD + 4 * dq);
+    const float f = exp2f(ml.x - M);
+    Ls += ml.y * f;
+    O.x += o.x * f;
+    O.y += o.y * f;
+    O.z += o.z * f;
+    O.w += o.w * f;
   }
-  out[((long long)b * H + h) * kD + d] = (uint16_t)f2bf(O / Ls);
+  s_o[cl][dq] = O;
+  if (dq == 0) s_l[cl] = Ls;
+  __syncthreads();
+  if (t >= 32) return;
+  float4 acc = s_o[0][t];
+  float lsum = s_l[0];
+#pragma unroll
+  for (int j = 1; j < kMergeLanes; j++) {
+    const float4 v = s_o[j][t];
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+    lsum += s_l[j];
+  }
+  const float inv = 1.0f / lsum;
+  uint2 w;
+  w.x = pack_bf16x2(acc.x * inv, acc.y * inv);
+  w.y = pack_bf16x2(acc.z * inv, acc.w * inv);
+  *(uint2 *)(out + ((long long)b * H + h) * kD + 4 * t) = w;
 }
 
 }  // namespace
@@ -299,9 +387,10 @@ extern "C" int jit_paged_decode_attn(const uint16_t *q, const uint16_t *pool,
   AttnArgs a{q, pool, page_table, lens, chunk_start, chunk_seq, part_o, part_ml, out,
              max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f};
   hipStream_t st = (hipStream_t)stream;
-  paged_attn_kernel<<<dim3(total_chunks, Hkv), 256, 0, st>>>(a);
+  const int hb = Hkv < 8 ? Hkv : 8;  // kv heads (waves) per workgroup
+  paged_attn_kernel<<<dim3(total_chunks, (Hkv + hb - 1) / hb), 64 * hb, 0, st>>>(a);
   int rc = jit::check_launch("jit_paged_decode_attn");
   if (rc) return rc;
-  attn_merge_kernel<<<dim3(B, H), 128, 0, st>>>(lens, chunk_start, part_o, part_ml, H, out);
+  attn_merge_kernel<<<dim3(B, H), 512, 0, st>>>(lens, chunk_start, part_o, part_ml, H, out);
   return jit::check_launch("jit_paged_decode_attn merge");
 }

@@ -124,9 +124,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
     qo[l + 64] = (uint16_t)o2;
   } else {
     const int h = head - H;
-    uint16_t *kp = pool + (long long)page * 2 * part + (long long)h * kPage * kD + slot * kD;
-    kp[l] = (uint16_t)o1;
-    kp[l + 64] = (uint16_t)o2;
+    uint16_t *kp = pool + (long long)page * 2 * part + (long long)h * kPage * kD;
+    kp[k_page_offset(slot, l)] = (uint16_t)o1;
+    kp[k_page_offset(slot, l + 64)] = (uint16_t)o2;
   }
 }
 

@@ -46,6 +46,14 @@ __device__ __forceinline__ f32x4 mfma16x16x32(const Frag8 &a, const Frag8 &b, f3
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, c, 0, 0, 0);
 }
 
+// ------------------------------------------------------------------ paged KV layout
+// Element offset of (slot, d) inside the K block of one (page, kv head): chunk-major
+// [4 d-chunks of 32][16 slots][32 dims], so one MFMA fragment's 16 slots x 32 dims
+// are 1 KB contiguous.  (The V block is dim-major: offset d * 16 + slot.)
+__device__ __forceinline__ int k_page_offset(int slot, int d) {
+  return (d >> 5) * (JIT_PAGE_TOKENS * 32) + slot * 32 + (d & 31);
+}
+
 // ------------------------------------------------------------------ host error plumbing
 namespace jit {
 void set_error(const char *fmt, ...);

@@ -82,7 +82,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   constexpr int NBW = SWIGLU ? 2 * NB : NB;  // weight row blocks (gate and up blocks with SWIGLU)
   extern __shared__ float red[];             // [KSPLIT][NBW][4][64]
   const int ksplit = blockDim.x >> 6;
-  const int wave = threadIdx.x >> 6, l = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
   const int lr = l & 15, lg = l >> 4;
   const int e = blockIdx.y;
   int cnt, off;
@@ -144,9 +144,11 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   for (int t0 = 0; t0 < cnt; t0 += 16) {
     const int tok = t0 + lr;
     const bool tv = tok < cnt;
-    Frag8 xa[GPW][2];  // activation fragments, permuted in place as they arrive
-    if (tv) {
-      const int pos = off + tok;
+    // activation fragments, permuted in place as they arrive; lanes past the last
+    // token load a valid row (no branch around the loads) and zero it
+    Frag8 xa[GPW][2];
+    {
+      const int pos = off + (tv ? tok : 0);
       const int xrow = a.row_index ? a.row_index[pos] : pos;
       const uint16_t *xr = a.x + (long long)xrow * a.K + 64 * g0 + 16 * lg;
 #pragma unroll
@@ -154,14 +156,16 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
         xa[g][0].q = *(const uint4 *)(xr + 64 * g);
         xa[g][1].q = *(const uint4 *)(xr + 64 * g + 8);
       }
+      const uint32_t keep = tv ? 0xffffffffu : 0u;
 #pragma unroll
-      for (int g = 0; g < GPW; g++) {
-        xa[g][0] = permute_x(xa[g][0].q);
-        xa[g][1] = permute_x(xa[g][1].q);
-      }
-    } else {
+      for (int g = 0; g < GPW; g++)
 #pragma unroll
-      for (int g = 0; g < GPW; g++) xa[g][0].q = xa[g][1].q = make_uint4(0, 0, 0, 0);
+        for (int h2 = 0; h2 < 2; h2++) {
+          Frag8 f = permute_x(xa[g][h2].q);
+#pragma unroll
+          for (int i = 0; i < 4; i++) f.u[i] &= keep;
+          xa[g][h2] = f;
+        }
     }
     f32x4 acc[NBW];
 #pragma unroll

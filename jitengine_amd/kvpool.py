@@ -2,8 +2,9 @@
 
 The reference keeps one contiguous growable [1, Hkv, cap, Dh] buffer per request and layer
 (KVSlot, Q36/kvcache/kv_cache.py:27-85).  The build replaces it with a pool of 16-token pages per
-layer, [num_pages, 2, Hkv, 16 * 128] bf16: part 0 of a page holds K slot-major, part 1 holds V
-dim-major (the operand layouts the attention kernel reads).  A sequence owns a list of pages, the
+layer, [num_pages, 2, Hkv, 16 * 128] bf16: part 0 of a page holds K chunk-major ([d / 32][slot]
+[d % 32]), part 1 holds V dim-major ([d][slot]) -- the operand layouts the attention kernel reads
+with contiguous loads.  A sequence owns a list of pages, the
 same page ids in every layer; token t sits in page pages[t // 16], slot t % 16.  The pool is
 zero-initialised, so every slot of an allocated page always holds finite values.
 """

@@ -56,11 +56,11 @@ def test_qk_norm_rope_append_parity(pos):
     assert st["bit_equal"] > 0.95, st
     got_pool = u16(pt)
     assert np.array_equal(got_pool[:, 1], want_pool[:, 1])  # V parts: copied verbatim, nothing else touched
-    kg = got_pool[:, 0].reshape(num_pages, Hkv, 16, 128).copy()
-    kw = want_pool[:, 0].reshape(num_pages, Hkv, 16, 128).copy()
+    kg = got_pool[:, 0].reshape(num_pages, Hkv, 4, 16, 32).copy()  # K chunk-major [d/32][slot][d%32]
+    kw = want_pool[:, 0].reshape(num_pages, Hkv, 4, 16, 32).copy()
     for b, p in enumerate(pos):
-        assert_close_bf16(kg[b, :, p % 16], kw[b, :, p % 16], what="k")
-        kg[b, :, p % 16] = kw[b, :, p % 16]
+        assert_close_bf16(kg[b, :, :, p % 16], kw[b, :, :, p % 16], what="k")
+        kg[b, :, :, p % 16] = kw[b, :, :, p % 16]
     assert np.array_equal(kg, kw)  # K parts: only the written slots changed
 
 
@@ -116,7 +116,10 @@ def test_decoder_layer_parity():
     own = oracle.router_topk(ref["logits"], cfg.top_k, True)[0]
     flips = int(np.sum(np.any(np.sort(own, -1) != np.sort(gi, -1), -1)))
     assert flips <= 2, f"{flips} rows routed differently from the float64 logits"
-    assert_close_bf16(u16(y), ref["y"], what="layer output")
+    # the layer output composes ~6 bf16 rounding stages (attention, o_proj, residual, experts,
+    # combine, residual): up to 4 ulps where that exceeds the absolute 2e-2 (|y| in [2, 4) has
+    # an ulp of 1.6e-2)
+    assert_close_bf16(u16(y), ref["y"], what="layer output", ulps=4.0)
 
 
 def test_model_decode_step_rows_are_independent():

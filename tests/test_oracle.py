@@ -253,7 +253,7 @@ def test_kv_append_gather_round_trip():
         kc, vc = oracle.kv_gather(pool, table[b], lens[b], 4, 128)
         assert np.array_equal(kc[:, pos[b]], k[b]) and np.array_equal(vc[:, pos[b]], v[b])
         pg, sl = table[b, pos[b] // 16], pos[b] % 16
-        assert np.array_equal(pool[pg, 0, :, sl * 128:(sl + 1) * 128], k[b])  # K slot-major
+        assert np.array_equal(pool[pg, 0].reshape(4, 4, 16, 32)[:, :, sl].reshape(4, 128), k[b])  # K chunk-major
         assert np.array_equal(pool[pg, 1].reshape(4, 128, 16)[:, :, sl], v[b])  # V dim-major
 
 
