@@ -45,23 +45,49 @@ def gen_stack(shape, seed, device):
                    torch.cat([p.biases for p in parts]))
 
 
-class Timer:
-    """Per-kernel HIP-event timing on the current stream."""
-
-    def __init__(self):
-        self.acc = {}
-
-    def run(self, name, fn):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        out = fn()
-        e.record()
-        self.acc.setdefault(name, []).append((s, e))
-        return out
-
-    def means_us(self):
+def time_ops(launches: dict, reps: int = 5) -> dict:
+    """Mean device time per launch of each op, in microseconds.  `launches[name]` is a list of
+    zero-argument callables, one launch each (for example the op on every layer's own weights and
+    inputs).  Each list is captured once as a HIP graph and replayed `reps` times between two HIP
+    events on the stream the launches run on, so host overhead between launches is not counted."""
+    out = {}
+    stream = torch.cuda.current_stream()
+    for name, fns in launches.items():
+        for f in fns:  # eager warm-up: the library is loaded and every allocation is cached
+            f()
         torch.cuda.synchronize()
-        return {k: 1e3 * float(np.mean([a.elapsed_time(b) for a, b in v])) for k, v in self.acc.items()}
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for f in fns:
+                f()
+        g.replay()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e.record(stream)
+        torch.cuda.synchronize()
+        out[name] = 1e3 * s.elapsed_time(e) / (reps * len(fns))
+        del g
+    return out
+
+
+def profile_traffic(name: str):
+    """HBM bytes per launch of a kernel from a committed rocprofv3 summary (FETCH_SIZE and
+    WRITE_SIZE, already scaled by the copy calibration): the line `traffic_bytes_per_launch: N`
+    of profiles/<name>.txt, or None when there is no such summary."""
+    path = os.path.join(ROOT, "profiles", name + ".txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_threads() -> int:
+    return len(os.sched_getaffinity(0))
 
 
 def bench_config1(steps: int, warmup: int, dev: str) -> dict:
@@ -98,14 +124,14 @@ def bench_config1(steps: int, warmup: int, dev: str) -> dict:
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
 
-    # per-kernel durations, same launches, events around each
-    tm = Timer()
-    for _ in range(max(steps, 10)):
-        pk = tm.run("moe_pack", lambda: ops.moe_pack(inds, E))
-        h = tm.run("gate_up_swiglu", lambda: ops.expert_gate_up(x, gu, pk))
-        r = tm.run("down", lambda: ops.expert_down(h, dn, pk))
-        tm.run("combine", lambda: ops.moe_combine(r, pk, scores))
-    kus = tm.means_us()
+    # per-op device time, each op replayed alone on the same inputs
+    pk = ops.moe_pack(inds, E)
+    h = ops.expert_gate_up(x, gu, pk)
+    r = ops.expert_down(h, dn, pk)
+    kus = time_ops({"moe_pack": [lambda: ops.moe_pack(inds, E)],
+                    "gate_up_swiglu": [lambda: ops.expert_gate_up(x, gu, pk)],
+                    "down": [lambda: ops.expert_down(h, dn, pk)],
+                    "combine": [lambda: ops.moe_combine(r, pk, scores)]}, reps=max(steps, 10))
 
     flat = inds.cpu().numpy().reshape(-1)
     U = int(np.unique(flat).size)
@@ -128,8 +154,10 @@ def bench_config1(steps: int, warmup: int, dev: str) -> dict:
                 q.biases.view(torch.int16).cpu().numpy().view(np.uint16))
 
     gu_h, dn_h = host(gu_mlx), host(dn_mlx)
+    oracle.set_num_threads(cpu_threads())
+    oracle.moe_experts(x_np[:nb], ind_np, sc_np, gu_h, dn_h, E)  # warm-up
     times = []
-    for _ in range(3):
+    for _ in range(5):
         c0 = time.perf_counter()
         oracle.moe_experts(x_np[:nb], ind_np, sc_np, gu_h, dn_h, E)
         times.append(time.perf_counter() - c0)
@@ -151,7 +179,7 @@ def bench_config1(steps: int, warmup: int, dev: str) -> dict:
                      "frac": achieved / HBM_PEAK_GBS, "alg_bytes_per_launch": alg_gate_up, "traffic": None},
         "cpu_baseline": {"value": cpu_tps, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
                          "sample": f"oracle expert chain (pack, gate_up, down, combine; float64 dots) on {nb} of "
-                                   f"the {B} tokens, median of 3"},
+                                   f"the {B} tokens, median of 5 after a warm-up"},
         "_y": y,
     }
 
@@ -197,13 +225,15 @@ def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int 
     st = make_step_state(cfg, lens, table_d)
     torch.cuda.synchronize()
 
-    # distinct experts per layer (for the algorithmic byte count), one eager step
-    U = []
+    # one eager step keeps every layer's intermediates: the distinct experts per layer (for the
+    # algorithmic byte count) and the inputs of the per-op timing below
+    dbg = []
     xx = x
     for l, layer in enumerate(model.layers):
         d = {}
         xx = layer.step(xx, pools[l], st, debug=d)
-        U.append(int(torch.unique(d["inds"]).numel()))
+        dbg.append(d)
+    U = [int(torch.unique(d["inds"]).numel()) for d in dbg]
     torch.cuda.synchronize()
 
     def step():
@@ -234,31 +264,48 @@ def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int 
         torch.cuda.synchronize()
         ms = t0.elapsed_time(t1) / steps
         y = yg
+        del g
 
-    # per-kernel durations over one eager step (events around each launch)
-    tm = Timer()
-    for _ in range(2):
-        model.decode_step(x, pools, st, prof=tm.run)
-    kus = {k: v * 1.0 for k, v in tm.means_us().items()}  # mean per launch
-    launches = {k: len(v) for k, v in tm.acc.items()}
-    total_us = {k: kus[k] * launches[k] / 2 for k in kus}  # per step
+    # per-op device time: each op over the 48 layers (each layer's own weights, pool and
+    # inputs from the eager step above), replayed alone
+    L_ = model.layers
+    E = cfg.experts
+    per_layer = {
+        "rmsnorm": lambda l: ops.rmsnorm(dbg[l]["x"], L_[l].input_norm, cfg.eps),
+        "qkv_proj": lambda l: ops.qmm(dbg[l]["xn"], L_[l].qkv),
+        "qk_norm_rope_append": lambda l: ops.qk_norm_rope_append(
+            dbg[l]["qkv"], cfg.heads, cfg.kv_heads, L_[l].q_norm, L_[l].k_norm, cfg.eps, L_[l].inv_freq, st.pos,
+            st.page_table, pools[l]),
+        "paged_attention": lambda l: ops.paged_decode_attention(
+            dbg[l]["q"], pools[l], st.page_table, st.plan, cfg.head_dim ** -0.5, st.workspace),
+        "o_proj": lambda l: ops.qmm(dbg[l]["attn"].view(B, -1), L_[l].o),
+        "add_rmsnorm": lambda l: ops.rmsnorm(dbg[l]["o"], L_[l].post_norm, cfg.eps, resid=dbg[l]["x"],
+                                             return_sum=True),
+        "router_proj": lambda l: ops.qmm(dbg[l]["hn"], L_[l].moe.router),
+        "router_topk": lambda l: ops.router_topk(dbg[l]["logits"], cfg.top_k, cfg.norm_topk),
+        "moe_pack": lambda l: ops.moe_pack(dbg[l]["inds"], E),
+        "gate_up_swiglu": lambda l: ops.expert_gate_up(dbg[l]["hn"], L_[l].moe.gate_up, dbg[l]["pk"]),
+        "down": lambda l: ops.expert_down(dbg[l]["hh"], L_[l].moe.down, dbg[l]["pk"]),
+        "combine": lambda l: ops.moe_combine(dbg[l]["r"], dbg[l]["pk"], dbg[l]["scores"], dbg[l]["h"]),
+    }
+    kus = time_ops({name: [(lambda f=f, l=l: f(l)) for l in range(n_layers)] for name, f in per_layer.items()},
+                   reps=3)
 
     dense = cfg.qkv_rows * cfg.hidden // 2 * 9 // 8 + cfg.hidden * cfg.heads * 128 // 2 * 9 // 8 \
         + cfg.experts * cfg.hidden // 2 * 9 // 8
-    per_expert = 2654208
-    kv = int((lens.astype(np.int64) + 1).sum()) * 2 * cfg.kv_heads * 128 * 2
+    per_expert = 2654208  # gate||up 1,769,472 + down 884,736 (weights, scales, biases)
+    kv = int((lens.astype(np.int64) + 1).sum()) * 2 * cfg.kv_heads * 128 * 2  # 2,048 B per key
     alg_step = n_layers * (dense + kv) + sum(U) * per_expert
-    # the dominant kernel by time in the step
-    dom = max(total_us, key=total_us.get)
-    alg_kernel = {
-        "paged_attention": kv + B * cfg.heads * 128 * 2 * 2,
-        "gate_up_swiglu": float(np.mean(U)) * 1769472,
-        "down": float(np.mean(U)) * 884736,
-    }
-    achieved = alg_kernel.get(dom, 0.0) / (kus[dom] * 1e-6) / 1e9 if dom in alg_kernel else None
+    # the dominant op by device time, and its algorithmic bytes per launch (the same for every layer
+    # for attention; the mean over layers for the experts)
+    alg_op = {"paged_attention": kv, "gate_up_swiglu": float(np.mean(U)) * 1769472,
+              "down": float(np.mean(U)) * 884736}
+    dom = max(kus, key=kus.get)
+    achieved = alg_op[dom] / (kus[dom] * 1e-6) / 1e9 if dom in alg_op else None
+    traffic = profile_traffic(f"{dom}_config2")
 
-    # CPU baseline: the oracle's decoder layer (layer 0) on a sample of rows, scaled to 48 layers
-    nb = 4
+    # CPU baseline: the oracle's decoder layer (layer 0's weights and pool) on all 32 rows, median
+    # of 5 after a warm-up, scaled to the 48 layers of a step
     def host_q(lin):
         return (lin.weight.cpu().numpy().view(np.uint32), lin.scales.view(torch.int16).cpu().numpy().view(np.uint16),
                 lin.biases.view(torch.int16).cpu().numpy().view(np.uint16))
@@ -266,37 +313,44 @@ def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int 
     lw = {"input_norm": u16(w0["input_norm"]), "qkv": host_q(w0["qkv"]), "q_norm": u16(w0["q_norm"]),
           "k_norm": u16(w0["k_norm"]), "o": host_q(w0["o"]), "post_norm": u16(w0["post_norm"]),
           "router": host_q(w0["router"]), "gate_up": host_q(w0["gate_up"]), "down": host_q(w0["down"])}
-    pool_h = u16(pools[0]).copy()
+    pool_h = u16(pools[0])
     ocfg = {"heads": cfg.heads, "kv_heads": cfg.kv_heads, "experts": cfg.experts, "top_k": cfg.top_k,
             "eps": cfg.eps, "inv_freq": rope_inv_freq(cfg.rope_theta, 128)}
-    xs = u16(x)[:nb]
-    c0 = time.perf_counter()
-    oracle.decoder_layer(xs, lw, pool_h, table[:nb], lens[:nb], ocfg)
-    t_cpu = time.perf_counter() - c0
-    cpu_tps = nb / (t_cpu * n_layers)
+    xs = u16(x)
+    oracle.set_num_threads(cpu_threads())
+    times = []
+    for i in range(6):
+        ph = pool_h.copy()
+        c0 = time.perf_counter()
+        oracle.decoder_layer(xs, lw, ph, table, lens, ocfg)
+        if i:
+            times.append(time.perf_counter() - c0)
+    cpu_tps = B / (float(np.median(times)) * n_layers)
 
     return {
         "metric": "decode tok/s (bs=1, ragged bs=32) + achieved HBM GB/s as % of MI355X peak",
         "value": B / (ms * 1e-3),
         "unit": "tokens/s",
         "ms_per_step": ms,
-        "dtype": "bf16 activations, 4-bit g64 weights, fp32 accumulate",
+        "dtype": "bf16",
         "config": {"workload": f"config2: ragged 32-sequence decode, {n_layers} layers of the Qwen3-MoE-style 4-bit "
                                "block, paged bf16 KV (16-token pages, permuted), lens log-uniform [128, 32768]",
+                   "weights": "MLX 4-bit affine g64 (bf16 scale/bias), dequantized in registers; fp32 accumulate",
                    "sequences": B, "layers": n_layers, "kv_tokens": int(lens.sum()), "lens_min": int(lens.min()),
                    "lens_max": int(lens.max()), "distinct_experts_mean": float(np.mean(U)),
                    "hip_graph": bool(graph), "ms_per_step_eager": ms_eager},
         "step_hbm": {"alg_bytes": alg_step, "GB_s": alg_step / (ms * 1e-3) / 1e9,
                      "frac": alg_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                      "split": {"experts": sum(U) * per_expert, "kv": n_layers * kv, "dense": n_layers * dense}},
-        "kernels_us": kus,
-        "kernels_us_per_step": total_us,
+        "op_us": kus,
+        "op_us_sum_per_step": n_layers * sum(kus.values()),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": (achieved / HBM_PEAK_GBS) if achieved else None,
-                     "alg_bytes_per_launch": alg_kernel.get(dom), "traffic": None},
-        "cpu_baseline": {"value": cpu_tps, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
-                         "sample": f"oracle decoder layer 0 (float64 dots) for {nb} of the {B} rows "
-                                   f"(lens {list(map(int, lens[:nb]))}), time x {n_layers} layers"},
+                     "frac": (achieved / HBM_PEAK_GBS) if achieved else None, "traffic": traffic,
+                     "alg_bytes_per_launch": alg_op.get(dom), "launch_us": kus[dom]},
+        "cpu_baseline": {"value": cpu_tps, "unit": "tokens/s", "cores": cpu_threads(), "kind": "port",
+                         "sample": f"oracle decoder layer (C, float64 dots, OpenMP) on all {B} rows with layer 0's "
+                                   f"weights and KV ({int(lens.sum())} keys), median of 5 after a warm-up, "
+                                   f"x {n_layers} layers"},
         "_y": y,
     }
 
@@ -320,6 +374,88 @@ def copy_calibration(dev: str) -> int:
     return 0
 
 
+OP_KERNELS = {  # the kernels one op launches (rocprofv3 kernel names contain these)
+    "paged_attention": ["paged_attn_kernel", "attn_merge_kernel"],
+    "gate_up_swiglu": ["qmm_kernel<2, 8, true, true>"],
+    "down": ["qmm_kernel<4, 4, false, true>"],
+}
+
+
+def rocprof_summary(args) -> int:
+    """Text summary of rocprofv3 CSV output for one op: per-kernel launch statistics (from
+    --kernel-trace --stats) and HBM traffic per launch (FETCH_SIZE and WRITE_SIZE from two --pmc
+    runs of the same command, each scaled by what the counter reads for a plain copy of known size
+    in a --copy-calibration run)."""
+    import csv
+    import collections
+
+    def per_kernel(path):
+        d = collections.defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            d[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+        return d
+
+    def match(d, frag):
+        hits = [k for k in d if frag in k]
+        if len(hits) != 1:
+            raise SystemExit(f"kernel fragment {frag!r} matches {len(hits)} names")
+        return hits[0]
+
+    d_dir = args.rocprof_summary
+    stats = {r["Name"]: r for r in csv.DictReader(open(os.path.join(d_dir, "kt", "kt_kernel_stats.csv")))}
+    print(f"# rocprofv3 summary of bench.py's default workload (config 2), op {args.op}")
+    print("# made on one MI355X from the repository root by:")
+    print("#   rocprofv3 --kernel-trace --stats -f csv -d prof/kt -o kt -- python3 bench.py --steps 10 --warmup 2")
+    if args.op == "step":
+        print("#   python3 bench.py --rocprof-summary prof --op step")
+        print("# this library's kernels over the whole run (48 layers x (warm-up + timed steps + per-op replays));")
+        print("# launches, average / min / max duration in us, share of this library's kernel time")
+        ours = [r for r in stats.values() if "(anonymous namespace)::" in r["Name"] and "at::" not in r["Name"]
+                and "prepack" not in r["Name"]]
+        ours.sort(key=lambda r: -float(r["TotalDurationNs"]))
+        tot = sum(float(r["TotalDurationNs"]) for r in ours)
+        for r in ours:
+            name = r["Name"].replace("(anonymous namespace)::", "").split("(")[0]
+            print(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:9.2f} "
+                  f"{float(r['MaxNs']) / 1e3:9.2f} {100 * float(r['TotalDurationNs']) / tot:6.1f}%  {name}")
+        return 0
+    for c in ("FETCH_SIZE -f csv -d prof/fetch -o fetch -- python3 bench.py --steps 1 --warmup 1 --no-graph",
+              "WRITE_SIZE -f csv -d prof/write -o write -- python3 bench.py --steps 1 --warmup 1 --no-graph",
+              "FETCH_SIZE -f csv -d prof/cfetch -o cfetch -- python3 bench.py --copy-calibration",
+              "WRITE_SIZE -f csv -d prof/cwrite -o cwrite -- python3 bench.py --copy-calibration"):
+        print(f"#   rocprofv3 --pmc {c}")
+    print(f"#   python3 bench.py --rocprof-summary prof --op {args.op}")
+    fetch = per_kernel(os.path.join(d_dir, "fetch", "fetch_counter_collection.csv"))
+    write = per_kernel(os.path.join(d_dir, "write", "write_counter_collection.csv"))
+    cfetch = per_kernel(os.path.join(d_dir, "cfetch", "cfetch_counter_collection.csv"))
+    cwrite = per_kernel(os.path.join(d_dir, "cwrite", "cwrite_counter_collection.csv"))
+    copy_kib = 256 * 1024  # the calibration copy reads and writes 256 MiB
+    ck = match(cfetch, "copyBuffer")
+    f_scale = copy_kib / float(np.mean(cfetch[ck]))
+    w_scale = copy_kib / float(np.mean(cwrite[match(cwrite, "copyBuffer")]))
+    print(f"op: {args.op}")
+    print(f"calibration: FETCH_SIZE x {f_scale:.4f}, WRITE_SIZE x {w_scale:.4f} "
+          f"(copy of 256 MiB reads {np.mean(cfetch[ck]):.1f} KiB by FETCH_SIZE)")
+    tot_us, tot_bytes = 0.0, 0.0
+    for frag in OP_KERNELS[args.op]:
+        name = match(stats, frag)
+        st = stats[name]
+        avg_us = float(st["AverageNs"]) / 1e3
+        fk, wk = match(fetch, frag), match(write, frag)
+        fb = float(np.mean(fetch[fk])) * 1024 * f_scale
+        wb = float(np.mean(write[wk])) * 1024 * w_scale
+        tot_us += avg_us
+        tot_bytes += fb + wb
+        print(f"kernel: {name[:120]}")
+        print(f"  launches {st['Calls']}, average {avg_us:.2f} us, min {float(st['MinNs']) / 1e3:.2f} us, "
+              f"max {float(st['MaxNs']) / 1e3:.2f} us")
+        print(f"  HBM read {fb / 1e6:.2f} MB, written {wb / 1e6:.2f} MB per launch "
+              f"({len(fetch[fk])} / {len(write[wk])} dispatches counted)")
+    print(f"op_average_us: {tot_us:.2f}")
+    print(f"traffic_bytes_per_launch: {tot_bytes:.0f}")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -329,7 +465,12 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph replay")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--rocprof-summary", metavar="DIR",
+                    help="summarise rocprofv3 CSV output under DIR (kt/, fetch/, write/, cfetch/, cwrite/)")
+    ap.add_argument("--op", default="paged_attention", choices=sorted(OP_KERNELS) + ["step"])
     args = ap.parse_args()
+    if args.rocprof_summary:
+        return rocprof_summary(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
@@ -351,7 +492,7 @@ def main() -> int:
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
             "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to MLX 4-bit g64)",
             "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"]}
-    for key in ("step_hbm", "kernels_us", "kernels_us_per_step"):
+    for key in ("step_hbm", "op_us", "op_us_sum_per_step", "kernels_us"):
         if key in res:
             line[key] = res[key]
     print(json.dumps(line), flush=True)

@@ -293,17 +293,30 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[i] = 0.0f;
-    for (int j = 0; j < k; j++) {
-      const int p = inv[bt * k + j];
-      if (p < 0) continue;  // a dropped pair (expert id >= E) contributes nothing
-      const float sc = bf2f(scores[bt * k + j]);
-      const uint4 rv = *(const uint4 *)(r + (long long)p * D + n);
-      const uint32_t wds[4] = {rv.x, rv.y, rv.z, rv.w};
+    // slots in groups of 8, every load of a group issued before any is used (a
+    // dropped pair, inv < 0, reads row 0 and contributes nothing)
+    for (int j0 = 0; j0 < k; j0 += 8) {
+      uint4 rv[8];
+      float sc[8];
+      bool use[8];
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float rr = (i & 1) ? bf2f_hi(wds[i >> 1]) : bf2f(wds[i >> 1] & 0xffffu);
-        const float pr = bf2f(f2bf(rr * sc));
-        acc[i] = bf2f(f2bf(acc[i] + pr));
+      for (int jj = 0; jj < 8; jj++) {
+        const int j = min(j0 + jj, k - 1);
+        const int p = inv[bt * k + j];
+        use[jj] = j0 + jj < k && p >= 0;
+        sc[jj] = bf2f(scores[bt * k + j]);
+        rv[jj] = *(const uint4 *)(r + (long long)(p < 0 ? 0 : p) * D + n);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++) {
+        if (!use[jj]) continue;
+        const uint32_t wds[4] = {rv[jj].x, rv[jj].y, rv[jj].z, rv[jj].w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float rr = (i & 1) ? bf2f_hi(wds[i >> 1]) : bf2f(wds[i >> 1] & 0xffffu);
+          const float pr = bf2f(f2bf(rr * sc[jj]));
+          acc[i] = bf2f(f2bf(acc[i] + pr));
+        }
       }
     }
     if (resid) {

@@ -36,30 +36,57 @@ __device__ __forceinline__ float exp_neg(float x) {
 constexpr int kRowsPerBlock = 4;  // one wave64 per token row
 constexpr int kMaxN = 1024;
 
+// Key of a bf16 value in the ascending (value, index) order of the rank rule: the
+// value's bits made monotonic as an unsigned integer (-0 ties +0, as the float
+// comparison does) above a 16-bit index.  Gates must not be NaN.
+__device__ __forceinline__ uint32_t order_key(uint32_t b, int i) {
+  b = b == 0x8000u ? 0u : b;
+  const uint32_t o = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  return (o << 16) | (uint32_t)i;
+}
+__device__ __forceinline__ uint32_t key_bf16(uint32_t key) {
+  const uint32_t o = key >> 16;
+  return (o & 0x8000u) ? (o & 0x7fffu) : (~o & 0xffffu);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    const uint32_t y = (uint32_t)__shfl_xor((int)v, o, 64);
+    v = y > v ? y : v;
+  }
+  auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = r[0] > r[1] ? r[0] : r[1];
+  r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return r[0] > r[1] ? r[0] : r[1];
+}
+
 // One wave per row.  Lane l owns experts l, l+64, ...: it sums their exps in that
 // order, the wave adds the 64 partial sums by a butterfly over offsets 32..1
 // (every lane ends with the same total), then every gate is e_i * (1 / total)
 // rounded to bf16.  The top-k is the rank rule of the reference: the rank of
 // gate i counts the gates below it, ties broken by index, and ranks >= N-k fill
-// slots rank-(N-k) in ascending (value, index) order.
+// slots rank-(N-k) in ascending (value, index) order.  The wave finds them as k
+// rounds of a maximum over (value, index) keys, round t filling slot k-1-t -- the
+// same slots the ranks give, with no pairwise comparison.
 template <int NPL, bool FROM_GATES>
 __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t *__restrict__ src, int rows,
                                                           int N, int k, int norm,
                                                           uint32_t *__restrict__ inds,
                                                           uint16_t *__restrict__ scores,
                                                           uint16_t *__restrict__ gates_out) {
-  __shared__ float sg[kRowsPerBlock][kMaxN];
-  __shared__ int sidx[kRowsPerBlock][kMaxN];
+  __shared__ uint32_t skey[kRowsPerBlock][kMaxN];
   const int w = threadIdx.x >> 6, l = lane_id();
   const int row = blockIdx.x * kRowsPerBlock + w;
-  const bool valid = row < rows;
-  const uint16_t *lg = src + (size_t)(valid ? row : 0) * N;
+  if (row >= rows) return;  // the whole wave: row is uniform
+  const uint16_t *lg = src + (size_t)row * N;
+  uint32_t key[NPL];
 
   if (FROM_GATES) {
 #pragma unroll
     for (int j = 0; j < NPL; j++) {
       const int i = l + 64 * j;
-      if (valid && i < N) sg[w][i] = bf2f(lg[i]);
+      key[j] = i < N ? order_key(lg[i], i) : 0u;
     }
   } else {
     float v[NPL], e[NPL];
@@ -67,7 +94,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t *__rest
 #pragma unroll
     for (int j = 0; j < NPL; j++) {
       const int i = l + 64 * j;
-      v[j] = (valid && i < N) ? bf2f(lg[i]) : -INFINITY;
+      v[j] = i < N ? bf2f(lg[i]) : -INFINITY;
       mx = v[j] > mx ? v[j] : mx;
     }
 #pragma unroll
@@ -88,42 +115,33 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t *__rest
 #pragma unroll
     for (int j = 0; j < NPL; j++) {
       const int i = l + 64 * j;
-      if (valid && i < N) {
-        const uint32_t g = f2bf(e[j] * inv);
-        sg[w][i] = bf2f(g);
-        if (gates_out) gates_out[(size_t)row * N + i] = (uint16_t)g;
-      }
+      const uint32_t g = f2bf(e[j] * inv);
+      key[j] = i < N ? order_key(g, i) : 0u;
+      if (gates_out && i < N) gates_out[(size_t)row * N + i] = (uint16_t)g;
     }
   }
-  __syncthreads();
+  // every valid key is > 0 (its value field is >= 0x007f); a taken key becomes 0
+  for (int t = 0; t < k; t++) {
+    uint32_t m = key[0];
 #pragma unroll
-  for (int j = 0; j < NPL; j++) {
-    const int i = l + 64 * j;
-    if (valid && i < N) {
-      const float v = sg[w][i];
-      int rank = 0;
-      for (int jj = 0; jj < N; jj++) {
-        const float u = sg[w][jj];
-        rank += (u < v) || (u == v && jj < i);
-      }
-      if (rank >= N - k) sidx[w][rank - (N - k)] = i;
-    }
+    for (int j = 1; j < NPL; j++) m = key[j] > m ? key[j] : m;
+    m = wave_max_u32(m);
+#pragma unroll
+    for (int j = 0; j < NPL; j++) key[j] = key[j] == m ? 0u : key[j];
+    if (l == 0) skey[w][k - 1 - t] = m;
   }
-  __syncthreads();
-  if (valid && l == 0) {
-    if (scores == nullptr) {
-      for (int j = 0; j < k; j++) inds[(size_t)row * k + j] = (uint32_t)sidx[w][j];
-    } else {
-      float tot = 0.0f;
-      for (int j = 0; j < k; j++) {
-        const int e = sidx[w][j];
-        inds[(size_t)row * k + j] = (uint32_t)e;
-        tot = bf2f(f2bf(tot + sg[w][e]));
-      }
-      for (int j = 0; j < k; j++) {
-        const float sc = sg[w][sidx[w][j]];
-        scores[(size_t)row * k + j] = (uint16_t)(norm ? f2bf(sc / tot) : f2bf(sc));
-      }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float tot = 0.0f;
+  if (scores != nullptr)
+    for (int j = 0; j < k; j++) tot = bf2f(f2bf(tot + bf2f(key_bf16(skey[w][j]))));
+  for (int j = l; j < k; j += 64) {
+    const uint32_t m = skey[w][j];
+    inds[(size_t)row * k + j] = m & 0xffffu;
+    if (scores != nullptr) {
+      const float sc = bf2f(key_bf16(m));
+      scores[(size_t)row * k + j] = (uint16_t)(norm ? f2bf(sc / tot) : f2bf(sc));
     }
   }
 }

@@ -109,32 +109,28 @@ class DecoderLayer:
         self.moe = MoEBlock(w["router"], w["gate_up"], w["down"], cfg.top_k, cfg.norm_topk, prepack=prepack)
         self.inv_freq = torch.from_numpy(rope_inv_freq(cfg.rope_theta, cfg.head_dim)).to(self.input_norm.device)
 
-    def step(self, x: torch.Tensor, pool: torch.Tensor, st: StepState, debug: dict | None = None,
-             prof=None) -> torch.Tensor:
-        """x [B, D] -> the layer's output rows.  `prof(name, fn)`, if given, wraps each launch
-        (timing); `debug` receives every intermediate."""
+    def step(self, x: torch.Tensor, pool: torch.Tensor, st: StepState, debug: dict | None = None) -> torch.Tensor:
+        """x [B, D] -> the layer's output rows (Q36/model/model.py:65-80 order: attention
+        sub-block, residual, MoE sub-block, residual); `debug` receives every intermediate."""
         cfg = self.cfg
         B = x.shape[0]
-        run = prof if prof is not None else (lambda name, fn: fn())
         moe = self.moe
-        xn = run("rmsnorm", lambda: ops.rmsnorm(x, self.input_norm, cfg.eps))
-        qkv = run("qkv_proj", lambda: ops.qmm(xn, self.qkv))
-        q = run("qk_norm_rope_append", lambda: ops.qk_norm_rope_append(
-            qkv, cfg.heads, cfg.kv_heads, self.q_norm, self.k_norm, cfg.eps, self.inv_freq, st.pos,
-            st.page_table, pool))
-        attn = run("paged_attention", lambda: ops.paged_decode_attention(
-            q, pool, st.page_table, st.plan, cfg.head_dim ** -0.5, st.workspace))
-        o = run("o_proj", lambda: ops.qmm(attn.view(B, -1), self.o))
-        hn, h = run("add_rmsnorm", lambda: ops.rmsnorm(o, self.post_norm, cfg.eps, resid=x, return_sum=True))
-        logits = run("router_proj", lambda: ops.qmm(hn, moe.router))
-        inds, scores = run("router_topk", lambda: ops.router_topk(logits, moe.top_k, moe.norm_topk))
-        pk = run("moe_pack", lambda: ops.moe_pack(inds, moe.num_experts))
-        hh = run("gate_up_swiglu", lambda: ops.expert_gate_up(hn, moe.gate_up, pk))
-        r = run("down", lambda: ops.expert_down(hh, moe.down, pk))
-        y = run("combine", lambda: ops.moe_combine(r, pk, scores, h))
+        xn = ops.rmsnorm(x, self.input_norm, cfg.eps)
+        qkv = ops.qmm(xn, self.qkv)
+        q = ops.qk_norm_rope_append(qkv, cfg.heads, cfg.kv_heads, self.q_norm, self.k_norm, cfg.eps,
+                                    self.inv_freq, st.pos, st.page_table, pool)
+        attn = ops.paged_decode_attention(q, pool, st.page_table, st.plan, cfg.head_dim ** -0.5, st.workspace)
+        o = ops.qmm(attn.view(B, -1), self.o)
+        hn, h = ops.rmsnorm(o, self.post_norm, cfg.eps, resid=x, return_sum=True)
+        logits = ops.qmm(hn, moe.router)
+        inds, scores = ops.router_topk(logits, moe.top_k, moe.norm_topk)
+        pk = ops.moe_pack(inds, moe.num_experts)
+        hh = ops.expert_gate_up(hn, moe.gate_up, pk)
+        r = ops.expert_down(hh, moe.down, pk)
+        y = ops.moe_combine(r, pk, scores, h)
         if debug is not None:
-            debug.update(xn=xn, qkv=qkv, q=q, attn=attn, o=o, h=h, hn=hn, logits=logits, inds=inds,
-                         scores=scores, y=y)
+            debug.update(x=x, xn=xn, qkv=qkv, q=q, attn=attn, o=o, h=h, hn=hn, logits=logits, inds=inds,
+                         scores=scores, pk=pk, hh=hh, r=r, y=y)
         return y
 
 
@@ -148,8 +144,8 @@ class Model:
     def make_state(self, pos_host, page_table: torch.Tensor) -> StepState:
         return make_step_state(self.cfg, pos_host, page_table)
 
-    def decode_step(self, x: torch.Tensor, pools: list, st: StepState, prof=None) -> torch.Tensor:
+    def decode_step(self, x: torch.Tensor, pools: list, st: StepState) -> torch.Tensor:
         """x [B, D] bf16 hidden rows -> the last layer's output rows; pools[l] is layer l's KV pool."""
         for layer, pool in zip(self.layers, pools):
-            x = layer.step(x, pool, st, prof=prof)
+            x = layer.step(x, pool, st)
         return x
