@@ -376,8 +376,8 @@ def copy_calibration(dev: str) -> int:
 
 OP_KERNELS = {  # the kernels one op launches (rocprofv3 kernel names contain these)
     "paged_attention": ["paged_attn_kernel", "attn_merge_kernel"],
-    "gate_up_swiglu": ["qmm_kernel<2, 8, true, true>"],
-    "down": ["qmm_kernel<4, 4, false, true>"],
+    "gate_up_swiglu": ["qmm_kernel<1, 8, true, true"],
+    "down": ["qmm_kernel<4, 4, false, true"],
 }
 
 

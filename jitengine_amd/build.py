@@ -2,7 +2,9 @@
 
 Every HIP translation unit is built with the packed-FP32 feature disabled (hipcc forms
 v_pk_{add,mul,fma}_f32 from ordinary float code otherwise).  router.hip is built with
--ffp-contract=off: its softmax must reproduce the CPU restatement bit for bit.
+-ffp-contract=off: its softmax must reproduce the CPU restatement bit for bit.  qmm.hip is
+built with MFMA results in ordinary VGPRs (-amdgpu-mfma-vgpr-form) instead of accumulation
+registers, which removes a register copy per MFMA result from its inner loops.
 """
 
 from __future__ import annotations
@@ -24,7 +26,7 @@ ARCH = "gfx950"
 SOURCES = {
     "errors.cpp": [],
     "router.hip": ["-ffp-contract=off"],
-    "qmm.hip": [],
+    "qmm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "attention.hip": [],
     "block.hip": [],
 }

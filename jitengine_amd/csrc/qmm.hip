@@ -10,14 +10,16 @@
 //   sum_k x_k (s q_k + b) = s * sum_k x_k (q_k + 128) + (b - 128 s) * sum_k x_k.
 // A nibble q becomes the bf16 value 128 + q with one AND-OR (bit pattern 0x43pq),
 // and sum_k x_k comes from one more MFMA against an all-ones B operand, so the
-// vector work per weight word is 7 integer ops.  The two bf16 halves of an
-// unpacked word hold nibbles (i, i + 4), so activations are permuted to match.
+// vector work per weight word is 7 integer ops.  Words are used in the packed
+// nibble order (nibbles_natural below), whose unpacking yields k in natural order,
+// so the activations are fed to the matrix cores as loaded.
 //
 // Work split: a workgroup owns 16 * NB output rows of one expert (or of the dense
 // matrix) and splits K over its waves (KSPLIT = blockDim / 64); each wave owns
 // GPW consecutive groups.  A wave issues every weight, scale and bias load of its
-// K-slice before any math -- 16 KB in flight per wave for a 2048-wide gate||up
-// slice -- and keeps the slice in registers while it walks the expert's token
+// K-slice before any math -- 9 KB in flight per wave for the gate||up shape (a
+// 16-row gate block and its up block, 8 groups) -- and keeps the slice in
+// registers while it walks the expert's token
 // tiles of 16, so an expert's weights leave HBM once however many tokens it has.
 // The waves' partial sums meet in LDS and are added in wave order (a fixed
 // order: results do not depend on the batch).
@@ -46,25 +48,36 @@ struct QmmArgs {
 // with one fully coalesced 1 KB load plus one 128-byte load.
 constexpr int kTileBytes = 1152;
 
-// bf16 fragment of 8 nibbles: elements (q0, q4, q1, q5, q2, q6, q3, q7) + 128.
-__device__ __forceinline__ Frag8 unpack_nibbles(uint32_t w) {
+// Nibble order inside a packed-layout word: the MLX word holds q0..q7 at bits 4i;
+// the packed word holds q0, q2, q4, q6 at nibble positions 0-3 and q1, q3, q5, q7 at
+// 4-7, so that unpacking yields the k values in natural order and the activations
+// need no shuffle.  jit_q4_prepack applies this once; the MLX-layout kernels apply it
+// in registers, so both feed the matrix cores the same operands.
+__device__ __forceinline__ uint32_t nibbles_natural(uint32_t w) {
+  uint32_t e = w & 0x0F0F0F0Fu, o = (w >> 4) & 0x0F0F0F0Fu;
+  e = (e | (e >> 4)) & 0x00FF00FFu;
+  o = (o | (o >> 4)) & 0x00FF00FFu;
+  e = (e | (e >> 8)) & 0x0000FFFFu;
+  o = (o | (o >> 8)) & 0x0000FFFFu;
+  return e | (o << 16);
+}
+
+// bf16 fragment of the 8 nibbles of a packed-order word: (q0, ..., q7) + 128, each
+// output one shift and one v_and_or_b32 (m = 0x000F000F and c = 0x43004300 are
+// passed in registers: the instruction takes no literal operands).
+__device__ __forceinline__ Frag8 unpack_nibbles(uint32_t w, uint32_t m, uint32_t c) {
   Frag8 f;
-  f.u[0] = (w & 0x000F000Fu) | 0x43004300u;
-  f.u[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  f.u[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  f.u[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  f.u[0] = (w & m) | c;
+  f.u[1] = ((w >> 4) & m) | c;
+  f.u[2] = ((w >> 8) & m) | c;
+  f.u[3] = ((w >> 12) & m) | c;
   return f;
 }
 
-// 8 consecutive bf16 x0..x7 -> the fragment order (x0, x4, x1, x5, x2, x6, x3, x7).
-__device__ __forceinline__ Frag8 permute_x(uint4 d) {
-  Frag8 f;
-  f.u[0] = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
-  f.u[1] = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
-  f.u[2] = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
-  f.u[3] = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
-  return f;
-}
+// The unpack masks as register values the compiler cannot fold back into literals.
+#define UNPACK_CONSTANTS(m, c)            \
+  uint32_t m = 0x000F000Fu, c = 0x43004300u; \
+  asm volatile("" : "+v"(m), "+v"(c))
 
 // SwiGLU with the reference's bf16 rounding points: g, u rounded; sigmoid(g)
 // rounded; bf16(g * sigmoid) * u rounded.
@@ -76,11 +89,11 @@ __device__ __forceinline__ uint32_t swiglu_bf16(float gacc, float uacc) {
   return f2bf(sl * u);
 }
 
-template <int NB, int GPW, bool SWIGLU, bool PACKED>
+template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1>
 __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   static_assert(!PACKED || GPW % 2 == 0, "packed tiles hold pairs of groups");
   constexpr int NBW = SWIGLU ? 2 * NB : NB;  // weight row blocks (gate and up blocks with SWIGLU)
-  extern __shared__ float red[];             // [KSPLIT][NBW][4][64]
+  extern __shared__ float red[];             // [KSPLIT][TT][NBW][4][64]
   const int ksplit = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
   const int lr = l & 15, lg = l >> 4;
@@ -126,7 +139,10 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
       const uint16_t *sp = a.s + e * a.g_estride + row * G + g0;
       const uint16_t *bp = a.b + e * a.g_estride + row * G + g0;
 #pragma unroll
-      for (int g = 0; g < GPW; g++) wv[g][rb] = *(const uint2 *)(wp + 8 * g);
+      for (int g = 0; g < GPW; g++) {
+        const uint2 wm = *(const uint2 *)(wp + 8 * g);
+        wv[g][rb] = make_uint2(nibbles_natural(wm.x), nibbles_natural(wm.y));
+      }
 #pragma unroll
       for (int j = 0; j < (GPW + 1) / 2; j++) {
         const uint32_t s0 = sp[2 * j], b0 = bp[2 * j];
@@ -140,55 +156,57 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   Frag8 ones;
 #pragma unroll
   for (int i = 0; i < 4; i++) ones.u[i] = 0x3F803F80u;
+  UNPACK_CONSTANTS(um, uc);
 
-  for (int t0 = 0; t0 < cnt; t0 += 16) {
-    const int tok = t0 + lr;
-    const bool tv = tok < cnt;
-    // activation fragments, permuted in place as they arrive; lanes past the last
-    // token load a valid row (no branch around the loads) and zero it
-    Frag8 xa[GPW][2];
-    {
-      const int pos = off + (tv ? tok : 0);
+  // TT token tiles of 16 per pass: their activations are loaded together, their
+  // partial sums meet in LDS once (one barrier round and one epilogue per pass)
+  for (int t0 = 0; t0 < cnt; t0 += 16 * TT) {
+    // activation fragments (natural k order, as the unpacked weights); lanes past the
+    // last token load a valid row (no branch around the loads): they only feed output
+    // rows of tokens that are never stored
+    Frag8 xa[TT][GPW][2];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+      const int tok = t0 + 16 * tt + lr;
+      const int pos = off + (tok < cnt ? tok : 0);
       const int xrow = a.row_index ? a.row_index[pos] : pos;
       const uint16_t *xr = a.x + (long long)xrow * a.K + 64 * g0 + 16 * lg;
 #pragma unroll
       for (int g = 0; g < GPW; g++) {
-        xa[g][0].q = *(const uint4 *)(xr + 64 * g);
-        xa[g][1].q = *(const uint4 *)(xr + 64 * g + 8);
+        xa[tt][g][0].q = *(const uint4 *)(xr + 64 * g);
+        xa[tt][g][1].q = *(const uint4 *)(xr + 64 * g + 8);
       }
-      const uint32_t keep = tv ? 0xffffffffu : 0u;
-#pragma unroll
-      for (int g = 0; g < GPW; g++)
-#pragma unroll
-        for (int h2 = 0; h2 < 2; h2++) {
-          Frag8 f = permute_x(xa[g][h2].q);
-#pragma unroll
-          for (int i = 0; i < 4; i++) f.u[i] &= keep;
-          xa[g][h2] = f;
-        }
     }
-    f32x4 acc[NBW];
+    f32x4 acc[TT][NBW];
 #pragma unroll
-    for (int rb = 0; rb < NBW; rb++) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+      for (int rb = 0; rb < NBW; rb++) acc[tt][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int g = 0; g < GPW; g++) {
-      const Frag8 &A0 = xa[g][0], &A1 = xa[g][1];
-      f32x4 X = mfma16x16x32(A0, ones, f32x4{0.f, 0.f, 0.f, 0.f});
-      X = mfma16x16x32(A1, ones, X);
+      f32x4 X[TT];
+#pragma unroll
+      for (int tt = 0; tt < TT; tt++) {
+        X[tt] = mfma16x16x32(xa[tt][g][0], ones, f32x4{0.f, 0.f, 0.f, 0.f});
+        X[tt] = mfma16x16x32(xa[tt][g][1], ones, X[tt]);
+      }
 #pragma unroll
       for (int rb = 0; rb < NBW; rb++) {
         // the packed words are loop-invariant across token tiles; this empty register
         // constraint keeps their unpacking here instead of hoisted (8 VGPRs per word pair)
         uint32_t w0 = wv[g][rb].x, w1 = wv[g][rb].y;
         asm volatile("" : "+v"(w0), "+v"(w1));
-        const Frag8 B0 = unpack_nibbles(w0), B1 = unpack_nibbles(w1);
-        f32x4 C = mfma16x16x32(A0, B0, f32x4{0.f, 0.f, 0.f, 0.f});
-        C = mfma16x16x32(A1, B1, C);
+        const Frag8 B0 = unpack_nibbles(w0, um, uc), B1 = unpack_nibbles(w1, um, uc);
         const float sc = (g & 1) ? bf2f_hi(sv[rb][g >> 1]) : bf2f(sv[rb][g >> 1] & 0xffffu);
         const float bi = (g & 1) ? bf2f_hi(bv[rb][g >> 1]) : bf2f(bv[rb][g >> 1] & 0xffffu);
         const float bq = fmaf(-128.0f, sc, bi);
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[rb][i] = fmaf(bq, X[i], fmaf(sc, C[i], acc[rb][i]));
+        for (int tt = 0; tt < TT; tt++) {
+          f32x4 C = mfma16x16x32(xa[tt][g][0], B0, f32x4{0.f, 0.f, 0.f, 0.f});
+          C = mfma16x16x32(xa[tt][g][1], B1, C);
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[tt][rb][i] = fmaf(bq, X[tt][i], fmaf(sc, C[i], acc[tt][rb][i]));
+        }
       }
       // keep each group's nibble unpacking next to its MFMAs (hoisting every group's
       // unpacked fragments ahead would cost 8 registers per (group, block))
@@ -196,19 +214,21 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     }
     // ---- the waves' partial sums meet in LDS; lane l holds C[token 4*lg + i][row lr]
 #pragma unroll
-    for (int rb = 0; rb < NBW; rb++)
+    for (int tt = 0; tt < TT; tt++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) red[((wave * NBW + rb) * 4 + i) * 64 + l] = acc[rb][i];
+      for (int rb = 0; rb < NBW; rb++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) red[(((wave * TT + tt) * NBW + rb) * 4 + i) * 64 + l] = acc[tt][rb][i];
     __syncthreads();
-    // (output block, token row i) pairs are spread over the waves
-    for (int idx = wave; idx < 4 * NB; idx += ksplit) {
-      const int ob = idx >> 2, i = idx & 3;
-      const int t = t0 + 4 * lg + i;
+    // (tile, output block, token row i) triples are spread over the waves
+    for (int idx = wave; idx < TT * 4 * NB; idx += ksplit) {
+      const int tt = idx / (4 * NB), ob = (idx >> 2) % NB, i = idx & 3;
+      const int t = t0 + 16 * tt + 4 * lg + i;
       if (n0 + 16 * ob >= a.N) continue;
       float v = 0.0f, u = 0.0f;
       for (int ks = 0; ks < ksplit; ks++) {
-        v += red[((ks * NBW + ob) * 4 + i) * 64 + l];
-        if (SWIGLU) u += red[((ks * NBW + NB + ob) * 4 + i) * 64 + l];
+        v += red[(((ks * TT + tt) * NBW + ob) * 4 + i) * 64 + l];
+        if (SWIGLU) u += red[(((ks * TT + tt) * NBW + NB + ob) * 4 + i) * 64 + l];
       }
       if (t < cnt) {
         uint16_t *o = a.out + (long long)(off + t) * a.N + n0 + 16 * ob + lr;
@@ -219,7 +239,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   }
 }
 
-template <int NB, int GPW, bool SWIGLU, bool PACKED>
+template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1>
 int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what) {
   constexpr int NBW = SWIGLU ? 2 * NB : NB;
   const int G = a.K / 64;
@@ -227,8 +247,8 @@ int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what) {
   if (ksplit * GPW != G || ksplit < 1 || ksplit > 8)
     return jit::fail(JIT_EUNSUPPORTED, "%s: K=%d does not split into %d-group wave slices", what, a.K, GPW);
   const dim3 grid((a.N + 16 * NB - 1) / (16 * NB), E), block(64 * ksplit);
-  const size_t lds = (size_t)ksplit * NBW * 4 * 64 * sizeof(float);
-  qmm_kernel<NB, GPW, SWIGLU, PACKED><<<grid, block, lds, st>>>(a);
+  const size_t lds = (size_t)ksplit * TT * NBW * 4 * 64 * sizeof(float);
+  qmm_kernel<NB, GPW, SWIGLU, PACKED, TT><<<grid, block, lds, st>>>(a);
   return jit::check_launch(what);
 }
 
@@ -241,14 +261,28 @@ int dense_gpw(int K) {
   return 0;
 }
 
+// Dense launch shape: up to two token tiles per pass (one reduction round for a
+// 32-row decode batch), and 32 output rows per workgroup for a wide matrix with a
+// short K-slice per wave (the activations each workgroup pulls through L2 then
+// serve twice the rows).  The shape never changes a result: each output sums the
+// same groups in the same order.
+template <bool PACKED, int GPW>
+int launch_dense_gpw(const QmmArgs &a, hipStream_t st, const char *what) {
+  const bool two_tiles = a.T > 16, wide = GPW <= 4 && a.N >= 4096;
+  if (wide) return two_tiles ? launch_qmm<2, GPW, false, PACKED, 2>(a, 1, st, what)
+                             : launch_qmm<2, GPW, false, PACKED, 1>(a, 1, st, what);
+  return two_tiles ? launch_qmm<1, GPW, false, PACKED, 2>(a, 1, st, what)
+                   : launch_qmm<1, GPW, false, PACKED, 1>(a, 1, st, what);
+}
+
 template <bool PACKED>
 int launch_dense(const QmmArgs &a, hipStream_t st) {
   const char *what = PACKED ? "jit_qmm_packed" : "jit_qmm";
   switch (dense_gpw(a.K)) {
-    case 2: return launch_qmm<1, 2, false, PACKED>(a, 1, st, what);
-    case 4: return launch_qmm<1, 4, false, PACKED>(a, 1, st, what);
-    case 6: return launch_qmm<1, 6, false, PACKED>(a, 1, st, what);
-    case 8: return launch_qmm<1, 8, false, PACKED>(a, 1, st, what);
+    case 2: return launch_dense_gpw<PACKED, 2>(a, st, what);
+    case 4: return launch_dense_gpw<PACKED, 4>(a, st, what);
+    case 6: return launch_dense_gpw<PACKED, 6>(a, st, what);
+    case 8: return launch_dense_gpw<PACKED, 8>(a, st, what);
     default: return jit::fail(JIT_EUNSUPPORTED, "%s covers K %% 256 == 0 and K <= 4096, got %d", what, a.K);
   }
 }
@@ -267,10 +301,10 @@ __global__ __launch_bounds__(64) void q4_prepack_kernel(const uint32_t *__restri
   const long long row = e * N + rbi * 16 + lr;
   const uint32_t *wr = w + row * KW + 16 * gp + 2 * lg;
   uint4 q;
-  q.x = wr[0];
-  q.y = wr[1];
-  q.z = wr[8];
-  q.w = wr[9];
+  q.x = nibbles_natural(wr[0]);
+  q.y = nibbles_natural(wr[1]);
+  q.z = nibbles_natural(wr[8]);
+  q.w = nibbles_natural(wr[9]);
   uint8_t *t = out + tile * kTileBytes;
   *(uint4 *)(t + 16 * l) = q;
   if (lg == 0) {
@@ -404,7 +438,7 @@ extern "C" int jit_moe_gate_up_swiglu(const uint16_t *x, int K, const int32_t *p
   if (!w || !scales || !biases) return jit::fail(JIT_EINVAL, "moe_gate_up: null pointer");
   QmmArgs a{x, pair_row, expert_cnt, expert_off, w, scales, biases, h, K, I, 0,
             (long long)2 * I * (K / 8), (long long)2 * I * (K / 64), 2 * I};
-  return launch_qmm<2, 8, true, false>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu");
+  return launch_qmm<1, 8, true, false>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu");
 }
 
 extern "C" int jit_moe_gate_up_swiglu_packed(const uint16_t *x, int K, const int32_t *pair_row,
@@ -415,7 +449,7 @@ extern "C" int jit_moe_gate_up_swiglu_packed(const uint16_t *x, int K, const int
   if (!packed) return jit::fail(JIT_EINVAL, "moe_gate_up_packed: null pointer");
   QmmArgs a{x, pair_row, expert_cnt, expert_off, (const uint32_t *)packed, nullptr, nullptr, h, K, I, 0,
             jit_q4_packed_bytes(1, 2 * I, K), 0, 2 * I};
-  return launch_qmm<2, 8, true, true>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu_packed");
+  return launch_qmm<1, 8, true, true>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu_packed");
 }
 
 static int down_check(const uint16_t *h, int I, const int32_t *cnt, const int32_t *off, int E, int D, int P,

@@ -636,6 +636,18 @@ int jo_qk_norm_rope_append(const uint16_t *qkv, int B, int H, int Hkv, const uin
  * words 2j, 2j+1 of group 2gp and words 2j, 2j+1 of group 2gp+1 of row 16 rb + r
  * (word w of group g = word 8g + w of the row); bytes 1024..1151 hold, for row
  * r, (scale[2gp], scale[2gp+1], bias[2gp], bias[2gp+1]) bf16. */
+/* Nibble order of a packed-layout word: q0, q2, q4, q6 at nibble positions 0-3 and
+ * q1, q3, q5, q7 at 4-7 (the MLX word holds q_i at position i). */
+static uint32_t nibbles_natural(uint32_t w) {
+  uint32_t r = 0;
+  for (int i = 0; i < 8; i++) {
+    const uint32_t q = (w >> (4 * i)) & 0xFu;
+    const int pos = (i % 2 == 0) ? i / 2 : 4 + i / 2;
+    r |= q << (4 * pos);
+  }
+  return r;
+}
+
 int jo_q4_prepack(const uint32_t *w, const uint16_t *s, const uint16_t *b, int E, int N, int K,
                   uint8_t *out) {
   if (E <= 0 || N <= 0 || K <= 0 || (N % 16) != 0 || (K % 128) != 0) return JO_EINVAL;
@@ -647,8 +659,10 @@ int jo_q4_prepack(const uint32_t *w, const uint16_t *s, const uint16_t *b, int E
         for (int l = 0; l < 64; l++) {
           const int j = l / 16, r = l % 16;
           const uint32_t *wr = w + ((size_t)e * N + rb * 16 + r) * KW;
-          const uint32_t words[4] = {wr[8 * (2 * gp) + 2 * j], wr[8 * (2 * gp) + 2 * j + 1],
-                                     wr[8 * (2 * gp + 1) + 2 * j], wr[8 * (2 * gp + 1) + 2 * j + 1]};
+          const uint32_t words[4] = {nibbles_natural(wr[8 * (2 * gp) + 2 * j]),
+                                     nibbles_natural(wr[8 * (2 * gp) + 2 * j + 1]),
+                                     nibbles_natural(wr[8 * (2 * gp + 1) + 2 * j]),
+                                     nibbles_natural(wr[8 * (2 * gp + 1) + 2 * j + 1])};
           memcpy(t + 16 * l, words, 16);
         }
         for (int r = 0; r < 16; r++) {
