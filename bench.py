@@ -53,6 +53,7 @@ def time_ops(launches: dict, reps: int = 5) -> dict:
     out = {}
     stream = torch.cuda.current_stream()
     for name, fns in launches.items():
+        fns = list(fns) * max(1, -(-16 // len(fns)))  # >= 16 launches: a graph's own launch is amortised
         for f in fns:  # eager warm-up: the library is loaded and every allocation is cached
             f()
         torch.cuda.synchronize()
@@ -218,7 +219,7 @@ def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int 
     model.cfg, model.layers = cfg, layers
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed + 7)
-    pools = [torch.randn((num_pages, 2, cfg.kv_heads, 16 * 128), generator=gen, device=dev, dtype=torch.bfloat16)
+    pools = [torch.randn((num_pages, cfg.kv_heads, 2, 16 * 128), generator=gen, device=dev, dtype=torch.bfloat16)
              for _ in range(n_layers)]
     x = torch.randn((B, cfg.hidden), generator=gen, device=dev, dtype=torch.bfloat16)
     table_d = torch.from_numpy(table).to(dev)
@@ -269,7 +270,11 @@ def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int 
     # per-op device time: each op over the 48 layers (each layer's own weights, pool and
     # inputs from the eager step above), replayed alone
     L_ = model.layers
-    E = cfg.experts
+
+    # the launches of one step, op by op: layer l's closing combine also norms layer l + 1's input,
+    # so the stand-alone input norm runs for layer 0 only and the plain combine for the last layer
+    last = n_layers - 1
+    step_layers = {"rmsnorm": [0], "combine_rmsnorm": list(range(last)), "combine": [last]}
     per_layer = {
         "rmsnorm": lambda l: ops.rmsnorm(dbg[l]["x"], L_[l].input_norm, cfg.eps),
         "qkv_proj": lambda l: ops.qmm(dbg[l]["xn"], L_[l].qkv),
@@ -283,13 +288,17 @@ def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int 
                                              return_sum=True),
         "router_proj": lambda l: ops.qmm(dbg[l]["hn"], L_[l].moe.router),
         "router_topk": lambda l: ops.router_topk(dbg[l]["logits"], cfg.top_k, cfg.norm_topk),
-        "moe_pack": lambda l: ops.moe_pack(dbg[l]["inds"], E),
+        "moe_pack": lambda l: ops.moe_pack(dbg[l]["inds"], cfg.experts),
         "gate_up_swiglu": lambda l: ops.expert_gate_up(dbg[l]["hn"], L_[l].moe.gate_up, dbg[l]["pk"]),
         "down": lambda l: ops.expert_down(dbg[l]["hh"], L_[l].moe.down, dbg[l]["pk"]),
+        "combine_rmsnorm": lambda l: ops.moe_combine_rmsnorm(dbg[l]["r"], dbg[l]["pk"], dbg[l]["scores"],
+                                                             dbg[l]["h"], L_[l + 1].input_norm, cfg.eps),
         "combine": lambda l: ops.moe_combine(dbg[l]["r"], dbg[l]["pk"], dbg[l]["scores"], dbg[l]["h"]),
     }
-    kus = time_ops({name: [(lambda f=f, l=l: f(l)) for l in range(n_layers)] for name, f in per_layer.items()},
+    launches = {name: step_layers.get(name, list(range(n_layers))) for name in per_layer}
+    kus = time_ops({name: [(lambda f=f, l=l: f(l)) for l in launches[name]] for name, f in per_layer.items()},
                    reps=3)
+    step_us = {name: kus[name] * len(launches[name]) for name in kus}
 
     dense = cfg.qkv_rows * cfg.hidden // 2 * 9 // 8 + cfg.hidden * cfg.heads * 128 // 2 * 9 // 8 \
         + cfg.experts * cfg.hidden // 2 * 9 // 8
@@ -343,7 +352,8 @@ def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int 
                      "frac": alg_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                      "split": {"experts": sum(U) * per_expert, "kv": n_layers * kv, "dense": n_layers * dense}},
         "op_us": kus,
-        "op_us_sum_per_step": n_layers * sum(kus.values()),
+        "op_us_per_step": step_us,
+        "op_us_sum_per_step": sum(step_us.values()),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": (achieved / HBM_PEAK_GBS) if achieved else None, "traffic": traffic,
                      "alg_bytes_per_launch": alg_op.get(dom), "launch_us": kus[dom]},
@@ -492,7 +502,7 @@ def main() -> int:
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
             "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to MLX 4-bit g64)",
             "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"]}
-    for key in ("step_hbm", "op_us", "op_us_sum_per_step", "kernels_us"):
+    for key in ("step_hbm", "op_us", "op_us_per_step", "op_us_sum_per_step", "kernels_us"):
         if key in res:
             line[key] = res[key]
     print(json.dumps(line), flush=True)

@@ -162,6 +162,14 @@ int jit_moe_down_packed(const uint16_t *h, int I, const int32_t *expert_cnt,
 int jit_moe_combine(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int B, int k,
                     int D, const uint16_t *resid, uint16_t *y, void *stream);
 
+/* jit_moe_combine followed by jit_rmsnorm of its output y with weight w (the
+ * next decoder layer's input norm, Q36/model/model.py:65-80) in one launch: y as
+ * jit_moe_combine writes it and xn = rmsnorm(y) * w, bit for bit the two calls.
+ * Contract: that of both calls (D % 8 == 0, D <= 2048). */
+int jit_moe_combine_rmsnorm(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int B, int k,
+                            int D, const uint16_t *resid, uint16_t *y, const uint16_t *w, float eps,
+                            uint16_t *xn, void *stream);
+
 /* ----------------------------------------------------- decoder block glue --
  * RMSNorm of rows x [rows, D] (mx.fast.rms_norm as the decoder layer applies it,
  * Q36/model/model.py:65-80; Q36/model/attention.py:59-60): sum(x^2) in fp32,
@@ -188,10 +196,11 @@ int jit_qk_norm_rope_append(const uint16_t *qkv, int B, int H, int Hkv, const ui
 /* --------------------------------------------------------- paged KV pool --
  * Pool layout (the build's design; the reference keeps one contiguous
  * [1, Hkv, cap, Dh] buffer per request, Q36/kvcache/kv_cache.py:27-85):
- * pool [num_pages, 2, Hkv, 16 * 128] bf16 per layer; part 0 of a page holds K
- * chunk-major ([d / 32][slot][d % 32]: an MFMA fragment's 16 slots x 32 dims
- * are 1 KB contiguous), part 1 holds V dim-major ([d][slot]).  Token t of
- * sequence b is at page page_table[b * max_pages + t / 16], slot t % 16.
+ * pool [num_pages, Hkv, 2, 16 * 128] bf16 per layer; for each kv head, part 0
+ * of a page holds K chunk-major ([d / 32][slot][d % 32]: an MFMA fragment's 16
+ * slots x 32 dims are 1 KB contiguous) and part 1 holds V dim-major
+ * ([d][slot]), so one kv head's K and V are one contiguous 8 KiB block.  Token
+ * t of sequence b is at page page_table[b * max_pages + t / 16], slot t % 16.
  *
  * KV append: write k, v [B, Hkv, 128] of row b at position pos[b]
  * (KVSlot.append, Q36/kvcache/kv_cache.py:76-85).  Contract: Dh == 128. */

@@ -36,6 +36,7 @@ _SIGNATURES = {
     "jit_moe_down": [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _P, _P],
     "jit_moe_down_packed": [_P, _I, _P, _P, _I, _P, _I, _I, _P, _P],
     "jit_moe_combine": [_P, _P, _P, _I, _I, _I, _P, _P, _P],
+    "jit_moe_combine_rmsnorm": [_P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P],
     "jit_rmsnorm": [_P, _P, _I, _I, _P, _F, _P, _P, _P],
     "jit_qk_norm_rope_append": [_P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _I, _P, _P, _P],
     "jit_kv_append_paged": [_P, _P, _I, _I, _P, _P, _I, _P, _P],

@@ -1,10 +1,11 @@
 // Paged KV pool append and split-K paged GQA decode attention for gfx950.
 //
-// Pool page (one layer): [2][Hkv][16 * 128] bf16.  The K part of a (page, kv
-// head) is chunk-major -- [4 d-chunks][16 slots][32 dims], so the 16 slots x 32
-// dims one MFMA A fragment covers are 1 KB contiguous -- and the V part is
-// dim-major -- [128 dims][16 slots], so a B fragment's 16 dims x 4 slots per lane
-// group are 512 B contiguous.  Both are 4 KiB per (page, kv head).
+// Pool page (one layer): [Hkv][2][16 * 128] bf16 -- per kv head its K part, then
+// its V part, so what one wave reads of a page (its kv head) is 8 KiB contiguous.
+// The K part is chunk-major -- [4 d-chunks][16 slots][32 dims], so the 16 slots x
+// 32 dims one MFMA A fragment covers are 1 KB contiguous -- and the V part is
+// dim-major -- [128 dims][16 slots], so a fragment's 16 dims x 4 slots per lane
+// group are 512 B contiguous.
 //
 // Attention work item: one workgroup per 256-key chunk of one sequence, one wave per
 // kv head; a wave streams the chunk's keys two 16-key pages (32 keys) per step:
@@ -27,7 +28,7 @@ namespace {
 
 constexpr int kD = JIT_HEAD_DIM;      // 128
 constexpr int kPage = JIT_PAGE_TOKENS;  // 16
-constexpr int kPageHead = kPage * kD;   // bf16 elements of one (page, part, kv head)
+constexpr int kPageHead = kPage * kD;   // bf16 elements of one (page, kv head, part)
 constexpr int kChunk = 256;             // keys per work item (one wave per kv head)
 
 __device__ __forceinline__ int k_off(int slot, int d) { return k_page_offset(slot, d); }
@@ -55,8 +56,9 @@ __global__ void kv_append_kernel(const uint16_t *__restrict__ k, const uint16_t 
   for (int t = threadIdx.x; t < Hkv * kD; t += blockDim.x) {
     const int h = t / kD, d = t % kD;
     const long long src = ((long long)b * Hkv + h) * kD + d;
-    pool[((long long)page * 2 * Hkv + h) * kPageHead + k_off(slot, d)] = k[src];
-    pool[(((long long)page * 2 + 1) * Hkv + h) * kPageHead + d * kPage + slot] = v[src];
+    uint16_t *hp = pool + ((long long)page * Hkv + h) * 2 * kPageHead;
+    hp[k_off(slot, d)] = k[src];
+    hp[kPageHead + d * kPage + slot] = v[src];
   }
 }
 
@@ -94,13 +96,18 @@ __device__ __forceinline__ float sum_xor32(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// The K part of kv head kvh in page pg (its V part follows).
+__device__ __forceinline__ const uint16_t *head_part(const uint16_t *pool, int pg, int Hkv, int kvh) {
+  return pool + ((long long)pg * Hkv + kvh) * 2 * kPageHead;
+}
+
 // K fragments of two pages: the A operand of S^T = K . Q^T (lane: slot lr, dims
 // 8*lg..8*lg+7 of each 32-dim chunk).
-__device__ __forceinline__ void load_k2(Frag8 (&k)[2][4], const uint16_t *pool, long long part_stride, int kvh,
-                                        int pg0, int pg1, int lr, int lg) {
+__device__ __forceinline__ void load_k2(Frag8 (&k)[2][4], const uint16_t *pool, int Hkv, int kvh, int pg0, int pg1,
+                                        int lr, int lg) {
 #pragma unroll
   for (int t = 0; t < 2; t++) {
-    const uint16_t *kp = pool + (long long)(t ? pg1 : pg0) * part_stride + (long long)kvh * kPageHead;
+    const uint16_t *kp = head_part(pool, t ? pg1 : pg0, Hkv, kvh);
 #pragma unroll
     for (int cc = 0; cc < 4; cc++) k[t][cc].q = *(const uint4 *)(kp + cc * (kPage * 32) + lr * 32 + 8 * lg);
   }
@@ -108,11 +115,11 @@ __device__ __forceinline__ void load_k2(Frag8 (&k)[2][4], const uint16_t *pool, 
 
 // V fragments of two pages: the A operand of O^T = V^T . P^T (lane: dim 16*cc + lr,
 // slots 4*lg..4*lg+3 of each page).
-__device__ __forceinline__ void load_v2(uint2 (&v)[2][8], const uint16_t *pool, long long part_stride, int kvh,
-                                        int Hkv, int pg0, int pg1, int lr, int lg) {
+__device__ __forceinline__ void load_v2(uint2 (&v)[2][8], const uint16_t *pool, int Hkv, int kvh, int pg0, int pg1,
+                                        int lr, int lg) {
 #pragma unroll
   for (int t = 0; t < 2; t++) {
-    const uint16_t *vp = pool + (long long)(t ? pg1 : pg0) * part_stride + (long long)(Hkv + kvh) * kPageHead;
+    const uint16_t *vp = head_part(pool, t ? pg1 : pg0, Hkv, kvh) + kPageHead;
 #pragma unroll
     for (int cc = 0; cc < 8; cc++) v[t][cc] = *(const uint2 *)(vp + (16 * cc + lr) * kPage + 4 * lg);
   }
@@ -138,7 +145,6 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
   const int wk1 = min(wk0 + kChunk, L);
   const int npg = (wk1 - wk0 + kPage - 1) / kPage;  // >= 1: every chunk holds a key
   const int nst = (npg + 1) >> 1;                     // 32-key steps
-  const long long part_stride = (long long)2 * a.Hkv * kPageHead;  // bf16 per page
   // the chunk's page ids, one per lane (at most kChunk / 16 = 16)
   const int my_page = l < npg ? a.page_table[(long long)b * a.max_pages + (wk0 >> 4) + l] : 0;
   const int last = npg - 1;
@@ -166,9 +172,9 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
   Frag8 kf[2][4];
   uint2 vv[2][8];
   // K before V, as in the loop, so a step's K wait leaves its V loads in flight
-  load_k2(kf, a.pool, part_stride, kvh, page(0), page(1), lr, lg);
+  load_k2(kf, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
   asm volatile("" ::: "memory");
-  load_v2(vv, a.pool, part_stride, kvh, a.Hkv, page(0), page(1), lr, lg);
+  load_v2(vv, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
   for (int st = 0; st < nst; st++) {
     const int k0 = wk0 + 32 * st;
     f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -178,7 +184,7 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
       s1 = mfma16x16x32(kf[1][cc], qf[cc], s1);
     }
     // K registers are free: the next step's K is in flight during softmax and P.V
-    load_k2(kf, a.pool, part_stride, kvh, page(2 * st + 2), page(2 * st + 3), lr, lg);
+    load_k2(kf, a.pool, a.Hkv, kvh, page(2 * st + 2), page(2 * st + 3), lr, lg);
     float p0[4], p1[4], tmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -234,7 +240,7 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
       vf.u[3] = vv[1][cc].y;
       o[cc] = mfma16x16x32(vf, pf, o[cc]);
     }
-    load_v2(vv, a.pool, part_stride, kvh, a.Hkv, page(2 * st + 2), page(2 * st + 3), lr, lg);
+    load_v2(vv, a.pool, a.Hkv, kvh, page(2 * st + 2), page(2 * st + 3), lr, lg);
     // keep these loads in this step: sunk into the next step they would only be
     // issued once that step's K has arrived
     asm volatile("" ::: "memory");

@@ -1,6 +1,7 @@
 // The decoder block's small fused kernels for gfx950: RMSNorm (with the residual
-// add fused in front) and the per-head q/k RMSNorm + RoPE + paged KV append that
-// sits between the qkv projection and decode attention.
+// add fused in front), the MoE combine (optionally followed by the next layer's
+// input RMSNorm), and the per-head q/k RMSNorm + RoPE + paged KV append that sits
+// between the qkv projection and decode attention.
 //
 // Arithmetic follows the reference's MLX ops (Q36/model/attention.py:42-68,
 // 99-119; Q36/model/model.py:65-80): RMSNorm accumulates sum(x^2) in fp32 and
@@ -79,6 +80,108 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
   }
 }
 
+// Weighted combine of one row's 8 consecutive outputs n..n+7 (slot order, each
+// product and each partial sum rounded to bf16; a dropped pair, inv < 0,
+// contributes nothing), plus the residual when given.  Every slot's loads are
+// issued before any is used.
+__device__ __forceinline__ void combine8(const uint16_t *__restrict__ r, const int32_t *__restrict__ inv,
+                                         const uint16_t *__restrict__ scores, int k, int D,
+                                         const uint16_t *__restrict__ resid, long long bt, int n, float (&acc)[8]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+  for (int j0 = 0; j0 < k; j0 += 8) {
+    uint4 rv[8];
+    float sc[8];
+    bool use[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const int j = min(j0 + jj, k - 1);
+      const int p = inv[bt * k + j];
+      use[jj] = j0 + jj < k && p >= 0;
+      sc[jj] = bf2f(scores[bt * k + j]);
+      rv[jj] = *(const uint4 *)(r + (long long)(p < 0 ? 0 : p) * D + n);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      if (!use[jj]) continue;
+      const uint32_t wds[4] = {rv[jj].x, rv[jj].y, rv[jj].z, rv[jj].w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float rr = (i & 1) ? bf2f_hi(wds[i >> 1]) : bf2f(wds[i >> 1] & 0xffffu);
+        const float pr = bf2f(f2bf(rr * sc[jj]));
+        acc[i] = bf2f(f2bf(acc[i] + pr));
+      }
+    }
+  }
+  if (resid) {
+    const uint4 rv = *(const uint4 *)(resid + bt * D + n);
+    const uint32_t wds[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float rr = (i & 1) ? bf2f_hi(wds[i >> 1]) : bf2f(wds[i >> 1] & 0xffffu);
+      acc[i] = bf2f(f2bf(rr + acc[i]));
+    }
+  }
+}
+
+__device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
+  uint4 o;
+  o.x = f2bf(v[0]) | (f2bf(v[1]) << 16);
+  o.y = f2bf(v[2]) | (f2bf(v[3]) << 16);
+  o.z = f2bf(v[4]) | (f2bf(v[5]) << 16);
+  o.w = f2bf(v[6]) | (f2bf(v[7]) << 16);
+  return o;
+}
+
+// Weighted combine: one workgroup per token row, 8 outputs per thread.
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict__ r,
+                                                      const int32_t *__restrict__ inv,
+                                                      const uint16_t *__restrict__ scores, int k, int D,
+                                                      const uint16_t *__restrict__ resid,
+                                                      uint16_t *__restrict__ y) {
+  const long long bt = blockIdx.x;
+  for (int n = threadIdx.x * 8; n < D; n += blockDim.x * 8) {
+    float acc[8];
+    combine8(r, inv, scores, k, D, resid, bt, n, acc);
+    *(uint4 *)(y + bt * D + n) = pack8(acc);
+  }
+}
+
+// The combine of a layer's last step followed by the next layer's input RMSNorm,
+// in the thread layout and summation order of rmsnorm_kernel (so xn is bit for bit
+// rmsnorm(y)): y = combine (+ resid) is written, and xn = rmsnorm(y) * w.
+__global__ __launch_bounds__(256) void combine_rmsnorm_kernel(
+    const uint16_t *__restrict__ r, const int32_t *__restrict__ inv, const uint16_t *__restrict__ scores, int k,
+    int D, const uint16_t *__restrict__ resid, uint16_t *__restrict__ y, const uint16_t *__restrict__ w, float eps,
+    uint16_t *__restrict__ xn) {
+  __shared__ float red[4];
+  const long long bt = blockIdx.x;
+  const int n = threadIdx.x * 8;
+  const bool on = n < D;
+  float v[8];
+  float ss = 0.0f;
+  if (on) {
+    combine8(r, inv, scores, k, D, resid, bt, n, v);
+    *(uint4 *)(y + bt * D + n) = pack8(v);
+#pragma unroll
+    for (int i = 0; i < 8; i++) ss = fmaf(v[i], v[i], ss);
+  }
+  const float tot = block_sum_256(ss, red);
+  const float rs = rsqrtf(tot / (float)D + eps);
+  if (on) {
+    const uint4 wq = *(const uint4 *)(w + n);
+    const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float wi = (i & 1) ? bf2f_hi(ww[i >> 1]) : bf2f(ww[i >> 1] & 0xffffu);
+      o[i] = bf2f(f2bf(wi * bf2f(f2bf(v[i] * rs))));
+    }
+    *(uint4 *)(xn + bt * D + n) = pack8(o);
+  }
+}
+
 // One wave per (token, head) of the fused qkv row [q: H*128 | k: Hkv*128 | v: Hkv*128].
 // Lane l owns dims l and l + 64 -- exactly one RoPE pair -- so the per-head
 // RMSNorm is a wave butterfly and the rotation needs no exchange.  q heads go to
@@ -98,11 +201,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
   const int p = pos[b];
   const int page = page_table[(long long)b * max_pages + p / kPage];
   const int slot = p % kPage;
-  const long long part = (long long)Hkv * kPage * kD;  // bf16 elements of one (page, K or V)
+  // this row's page for kv head h: K part, then V part (kPage * kD bf16 each)
+  auto head_part = [&](int h) { return pool + ((long long)page * Hkv + h) * 2 * (kPage * kD); };
   float x1 = bf2f(src[l]), x2 = bf2f(src[l + 64]);
   if (head >= H + Hkv) {  // v: copy into the dim-major V part
     const int h = head - H - Hkv;
-    uint16_t *vp = pool + ((long long)page * 2 + 1) * part + (long long)h * kPage * kD;
+    uint16_t *vp = head_part(h) + kPage * kD;
     vp[l * kPage + slot] = src[l];
     vp[(l + 64) * kPage + slot] = src[l + 64];
     return;
@@ -124,7 +228,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
     qo[l + 64] = (uint16_t)o2;
   } else {
     const int h = head - H;
-    uint16_t *kp = pool + (long long)page * 2 * part + (long long)h * kPage * kD;
+    uint16_t *kp = head_part(h);
     kp[k_page_offset(slot, l)] = (uint16_t)o1;
     kp[k_page_offset(slot, l + 64)] = (uint16_t)o2;
   }
@@ -157,3 +261,27 @@ extern "C" int jit_qk_norm_rope_append(const uint16_t *qkv, int B, int H, int Hk
                                                                     pos, page_table, max_pages, pool, q_out);
   return jit::check_launch("jit_qk_norm_rope_append");
 }
+
+extern "C" int jit_moe_combine(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int B, int k, int D,
+                               const uint16_t *resid, uint16_t *y, void *stream) {
+  if (B < 0 || k <= 0 || D <= 0) return jit::fail(JIT_EINVAL, "moe_combine: bad dims B=%d k=%d D=%d", B, k, D);
+  if (D % 8 != 0) return jit::fail(JIT_EUNSUPPORTED, "moe_combine covers D %% 8 == 0, got %d", D);
+  if (B == 0) return JIT_OK;
+  if (!r || !inv || !scores || !y) return jit::fail(JIT_EINVAL, "moe_combine: null pointer");
+  combine_kernel<<<B, 256, 0, (hipStream_t)stream>>>(r, inv, scores, k, D, resid, y);
+  return jit::check_launch("jit_moe_combine");
+}
+
+extern "C" int jit_moe_combine_rmsnorm(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int B, int k,
+                                       int D, const uint16_t *resid, uint16_t *y, const uint16_t *w, float eps,
+                                       uint16_t *xn, void *stream) {
+  if (B < 0 || k <= 0 || D <= 0)
+    return jit::fail(JIT_EINVAL, "moe_combine_rmsnorm: bad dims B=%d k=%d D=%d", B, k, D);
+  if (D % 8 != 0 || D > 2048)
+    return jit::fail(JIT_EUNSUPPORTED, "moe_combine_rmsnorm covers D %% 8 == 0 and D <= 2048, got %d", D);
+  if (B == 0) return JIT_OK;
+  if (!r || !inv || !scores || !y || !w || !xn) return jit::fail(JIT_EINVAL, "moe_combine_rmsnorm: null pointer");
+  combine_rmsnorm_kernel<<<B, 256, 0, (hipStream_t)stream>>>(r, inv, scores, k, D, resid, y, w, eps, xn);
+  return jit::check_launch("jit_moe_combine_rmsnorm");
+}
+

@@ -314,63 +314,6 @@ __global__ __launch_bounds__(64) void q4_prepack_kernel(const uint32_t *__restri
   }
 }
 
-// Weighted combine: one workgroup per token row, 8 outputs per thread; each
-// product and each partial sum is rounded to bf16, slots in ascending order.
-__global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict__ r,
-                                                      const int32_t *__restrict__ inv,
-                                                      const uint16_t *__restrict__ scores, int k,
-                                                      int D, const uint16_t *__restrict__ resid,
-                                                      uint16_t *__restrict__ y) {
-#pragma clang fp contract(off)
-  const int bt = blockIdx.x;
-  for (int n = threadIdx.x * 8; n < D; n += blockDim.x * 8) {
-    float acc[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = 0.0f;
-    // slots in groups of 8, every load of a group issued before any is used (a
-    // dropped pair, inv < 0, reads row 0 and contributes nothing)
-    for (int j0 = 0; j0 < k; j0 += 8) {
-      uint4 rv[8];
-      float sc[8];
-      bool use[8];
-#pragma unroll
-      for (int jj = 0; jj < 8; jj++) {
-        const int j = min(j0 + jj, k - 1);
-        const int p = inv[bt * k + j];
-        use[jj] = j0 + jj < k && p >= 0;
-        sc[jj] = bf2f(scores[bt * k + j]);
-        rv[jj] = *(const uint4 *)(r + (long long)(p < 0 ? 0 : p) * D + n);
-      }
-#pragma unroll
-      for (int jj = 0; jj < 8; jj++) {
-        if (!use[jj]) continue;
-        const uint32_t wds[4] = {rv[jj].x, rv[jj].y, rv[jj].z, rv[jj].w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const float rr = (i & 1) ? bf2f_hi(wds[i >> 1]) : bf2f(wds[i >> 1] & 0xffffu);
-          const float pr = bf2f(f2bf(rr * sc[jj]));
-          acc[i] = bf2f(f2bf(acc[i] + pr));
-        }
-      }
-    }
-    if (resid) {
-      const uint4 rv = *(const uint4 *)(resid + (long long)bt * D + n);
-      const uint32_t wds[4] = {rv.x, rv.y, rv.z, rv.w};
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float rr = (i & 1) ? bf2f_hi(wds[i >> 1]) : bf2f(wds[i >> 1] & 0xffffu);
-        acc[i] = bf2f(f2bf(rr + acc[i]));
-      }
-    }
-    uint4 o;
-    o.x = f2bf(acc[0]) | (f2bf(acc[1]) << 16);
-    o.y = f2bf(acc[2]) | (f2bf(acc[3]) << 16);
-    o.z = f2bf(acc[4]) | (f2bf(acc[5]) << 16);
-    o.w = f2bf(acc[6]) | (f2bf(acc[7]) << 16);
-    *(uint4 *)(y + (long long)bt * D + n) = o;
-  }
-}
-
 }  // namespace
 
 extern "C" int64_t jit_q4_packed_bytes(int E, int N, int K) {
@@ -484,14 +427,4 @@ extern "C" int jit_moe_down_packed(const uint16_t *h, int I, const int32_t *expe
   QmmArgs a{h, nullptr, expert_cnt, expert_off, (const uint32_t *)packed, nullptr, nullptr, r, I, D, 0,
             jit_q4_packed_bytes(1, D, I), 0, D};
   return launch_qmm<4, 4, false, true>(a, E, (hipStream_t)stream, "jit_moe_down_packed");
-}
-
-extern "C" int jit_moe_combine(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int B,
-                               int k, int D, const uint16_t *resid, uint16_t *y, void *stream) {
-  if (B < 0 || k <= 0 || D <= 0) return jit::fail(JIT_EINVAL, "moe_combine: bad dims B=%d k=%d D=%d", B, k, D);
-  if (D % 8 != 0) return jit::fail(JIT_EUNSUPPORTED, "moe_combine covers D %% 8 == 0, got %d", D);
-  if (B == 0) return JIT_OK;
-  if (!r || !inv || !scores || !y) return jit::fail(JIT_EINVAL, "moe_combine: null pointer");
-  combine_kernel<<<B, 256, 0, (hipStream_t)stream>>>(r, inv, scores, k, D, resid, y);
-  return jit::check_launch("jit_moe_combine");
 }

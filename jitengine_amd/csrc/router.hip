@@ -49,12 +49,26 @@ __device__ __forceinline__ uint32_t key_bf16(uint32_t key) {
   return (o & 0x8000u) ? (o & 0x7fffu) : (~o & 0xffffu);
 }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) {
-    const uint32_t y = (uint32_t)__shfl_xor((int)v, o, 64);
-    v = y > v ? y : v;
+// Wave maximum with no LDS round trip: DPP quad permutes (lane ^ 1, lane ^ 2), row
+// half-mirror and row mirror (every lane of a 16-lane row then holds the row's
+// maximum), then the permlane swaps across rows.  A maximum needs no fixed pairing,
+// so the mirrors serve where an xor butterfly would.
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v, int ctrl) {
+  uint32_t y;
+  switch (ctrl) {  // the DPP control is an immediate
+    case 0: y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false); break;   // [1,0,3,2]
+    case 1: y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false); break;   // [2,3,0,1]
+    case 2: y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false); break;  // half mirror
+    default: y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false); break; // mirror
   }
+  return y > v ? y : v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = dpp_max_u32(v, 0);
+  v = dpp_max_u32(v, 1);
+  v = dpp_max_u32(v, 2);
+  v = dpp_max_u32(v, 3);
   auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
   v = r[0] > r[1] ? r[0] : r[1];
   r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
@@ -69,19 +83,13 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // slots rank-(N-k) in ascending (value, index) order.  The wave finds them as k
 // rounds of a maximum over (value, index) keys, round t filling slot k-1-t -- the
 // same slots the ranks give, with no pairwise comparison.
+// One row on one wave: softmax (unless FROM_GATES) and the top-k slots, written to
+// inds / scores.  `skey` is the wave's LDS scratch of k entries.
 template <int NPL, bool FROM_GATES>
-__global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t *__restrict__ src, int rows,
-                                                          int N, int k, int norm,
-                                                          uint32_t *__restrict__ inds,
-                                                          uint16_t *__restrict__ scores,
-                                                          uint16_t *__restrict__ gates_out) {
-  __shared__ uint32_t skey[kRowsPerBlock][kMaxN];
-  const int w = threadIdx.x >> 6, l = lane_id();
-  const int row = blockIdx.x * kRowsPerBlock + w;
-  if (row >= rows) return;  // the whole wave: row is uniform
-  const uint16_t *lg = src + (size_t)row * N;
+__device__ __forceinline__ void topk_row(const uint16_t *__restrict__ lg, int row, int N, int k, int norm,
+                                         uint32_t *__restrict__ inds, uint16_t *__restrict__ scores,
+                                         uint16_t *__restrict__ gates_out, uint32_t *skey, int l) {
   uint32_t key[NPL];
-
   if (FROM_GATES) {
 #pragma unroll
     for (int j = 0; j < NPL; j++) {
@@ -128,22 +136,35 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t *__rest
     m = wave_max_u32(m);
 #pragma unroll
     for (int j = 0; j < NPL; j++) key[j] = key[j] == m ? 0u : key[j];
-    if (l == 0) skey[w][k - 1 - t] = m;
+    if (l == 0) skey[k - 1 - t] = m;
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float tot = 0.0f;
   if (scores != nullptr)
-    for (int j = 0; j < k; j++) tot = bf2f(f2bf(tot + bf2f(key_bf16(skey[w][j]))));
+    for (int j = 0; j < k; j++) tot = bf2f(f2bf(tot + bf2f(key_bf16(skey[j]))));
   for (int j = l; j < k; j += 64) {
-    const uint32_t m = skey[w][j];
+    const uint32_t m = skey[j];
     inds[(size_t)row * k + j] = m & 0xffffu;
     if (scores != nullptr) {
       const float sc = bf2f(key_bf16(m));
       scores[(size_t)row * k + j] = (uint16_t)(norm ? f2bf(sc / tot) : f2bf(sc));
     }
   }
+}
+
+template <int NPL, bool FROM_GATES>
+__global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t *__restrict__ src, int rows,
+                                                          int N, int k, int norm,
+                                                          uint32_t *__restrict__ inds,
+                                                          uint16_t *__restrict__ scores,
+                                                          uint16_t *__restrict__ gates_out) {
+  __shared__ uint32_t skey[kRowsPerBlock][kMaxN];
+  const int w = threadIdx.x >> 6, l = lane_id();
+  const int row = blockIdx.x * kRowsPerBlock + w;
+  if (row >= rows) return;  // the whole wave: row is uniform
+  topk_row<NPL, FROM_GATES>(src + (size_t)row * N, row, N, k, norm, inds, scores, gates_out, skey[w], l);
 }
 
 template <bool FROM_GATES>
@@ -184,11 +205,14 @@ __device__ __forceinline__ int wave_incl_scan(int x, int l) {
   return x;
 }
 
-__global__ __launch_bounds__(kPackThreads) void moe_pack_kernel(
-    const uint32_t *__restrict__ inds, int P, int k, int E, int32_t *__restrict__ order,
-    int32_t *__restrict__ pair_row, int32_t *__restrict__ inv, int32_t *__restrict__ expert_cnt,
-    int32_t *__restrict__ expert_off, int32_t *__restrict__ seg_expert,
-    int32_t *__restrict__ seg_start, int32_t *__restrict__ seg_cnt, int32_t *__restrict__ meta) {
+// The packing, run by one workgroup of kPackThreads threads; ind(p) is flat pair p's
+// expert id.
+template <typename IndFn>
+__device__ __forceinline__ void pack_body(IndFn ind, int P, int k, int E, int32_t *__restrict__ order,
+                                          int32_t *__restrict__ pair_row, int32_t *__restrict__ inv,
+                                          int32_t *__restrict__ expert_cnt, int32_t *__restrict__ expert_off,
+                                          int32_t *__restrict__ seg_expert, int32_t *__restrict__ seg_start,
+                                          int32_t *__restrict__ seg_cnt, int32_t *__restrict__ meta) {
   __shared__ int cnt[kPackThreads];
   __shared__ int nxt[kPackThreads];
   __shared__ unsigned short wcnt[kPackWaves][kPackThreads];
@@ -199,7 +223,7 @@ __global__ __launch_bounds__(kPackThreads) void moe_pack_kernel(
   if (t == 0) bad = 0;
   __syncthreads();
   for (int p = t; p < P; p += kPackThreads) {
-    const uint32_t e = inds[p];
+    const uint32_t e = ind(p);
     if (e < (uint32_t)E)
       atomicAdd(&cnt[e], 1);
     else
@@ -249,7 +273,7 @@ __global__ __launch_bounds__(kPackThreads) void moe_pack_kernel(
   const int nbits = 32 - __clz(E);  // enough bits for ids 0..E (E = "no expert")
   for (int base = 0; base < P; base += kPackThreads) {
     const int p = base + t;
-    uint32_t e = p < P ? inds[p] : (uint32_t)E;
+    uint32_t e = p < P ? ind(p) : (uint32_t)E;
     if (e > (uint32_t)E) e = (uint32_t)E;
     unsigned long long m = ~0ull;
     for (int bt = 0; bt < nbits; bt++) {
@@ -280,6 +304,16 @@ __global__ __launch_bounds__(kPackThreads) void moe_pack_kernel(
     }
     __syncthreads();
   }
+}
+
+
+__global__ __launch_bounds__(kPackThreads) void moe_pack_kernel(
+    const uint32_t *__restrict__ inds, int P, int k, int E, int32_t *__restrict__ order,
+    int32_t *__restrict__ pair_row, int32_t *__restrict__ inv, int32_t *__restrict__ expert_cnt,
+    int32_t *__restrict__ expert_off, int32_t *__restrict__ seg_expert,
+    int32_t *__restrict__ seg_start, int32_t *__restrict__ seg_cnt, int32_t *__restrict__ meta) {
+  pack_body([&](int p) { return inds[p]; }, P, k, E, order, pair_row, inv, expert_cnt, expert_off, seg_expert,
+            seg_start, seg_cnt, meta);
 }
 
 }  // namespace

@@ -2,9 +2,9 @@
 
 The reference keeps one contiguous growable [1, Hkv, cap, Dh] buffer per request and layer
 (KVSlot, Q36/kvcache/kv_cache.py:27-85).  The build replaces it with a pool of 16-token pages per
-layer, [num_pages, 2, Hkv, 16 * 128] bf16: part 0 of a page holds K chunk-major ([d / 32][slot]
-[d % 32]), part 1 holds V dim-major ([d][slot]) -- the operand layouts the attention kernel reads
-with contiguous loads.  A sequence owns a list of pages, the
+layer, [num_pages, Hkv, 2, 16 * 128] bf16: for each kv head, part 0 of a page holds K
+chunk-major ([d / 32][slot][d % 32]) and part 1 holds V dim-major ([d][slot]) -- the operand
+layouts the attention kernel reads, with one kv head's K and V one contiguous 8 KiB block.  A sequence owns a list of pages, the
 same page ids in every layer; token t sits in page pages[t // 16], slot t % 16.  The pool is
 zero-initialised, so every slot of an allocated page always holds finite values.
 """
@@ -38,7 +38,7 @@ class KVPool:
         self.pages: dict = {}
         self.lengths: dict = {}
         self.pools = (
-            [torch.zeros((num_pages, 2, n_kv_heads, PAGE * HEAD_DIM), dtype=torch.bfloat16, device=self.device)
+            [torch.zeros((num_pages, n_kv_heads, 2, PAGE * HEAD_DIM), dtype=torch.bfloat16, device=self.device)
              for _ in range(n_layers)]
             if allocate else []
         )

@@ -112,10 +112,18 @@ class DecoderLayer:
     def step(self, x: torch.Tensor, pool: torch.Tensor, st: StepState, debug: dict | None = None) -> torch.Tensor:
         """x [B, D] -> the layer's output rows (Q36/model/model.py:65-80 order: attention
         sub-block, residual, MoE sub-block, residual); `debug` receives every intermediate."""
+        return self.run(x, pool, st, debug=debug)[0]
+
+    def run(self, x: torch.Tensor, pool: torch.Tensor, st: StepState, xn: torch.Tensor | None = None,
+            next_norm: torch.Tensor | None = None, debug: dict | None = None):
+        """(y, xn_next): the layer on rows x whose input norm xn = rmsnorm(x) may come from the
+        previous layer; with next_norm (the next layer's input-norm weight) the closing combine
+        also returns that layer's normed input in the same launch, else xn_next is None."""
         cfg = self.cfg
         B = x.shape[0]
         moe = self.moe
-        xn = ops.rmsnorm(x, self.input_norm, cfg.eps)
+        if xn is None:
+            xn = ops.rmsnorm(x, self.input_norm, cfg.eps)
         qkv = ops.qmm(xn, self.qkv)
         q = ops.qk_norm_rope_append(qkv, cfg.heads, cfg.kv_heads, self.q_norm, self.k_norm, cfg.eps,
                                     self.inv_freq, st.pos, st.page_table, pool)
@@ -127,11 +135,14 @@ class DecoderLayer:
         pk = ops.moe_pack(inds, moe.num_experts)
         hh = ops.expert_gate_up(hn, moe.gate_up, pk)
         r = ops.expert_down(hh, moe.down, pk)
-        y = ops.moe_combine(r, pk, scores, h)
+        if next_norm is None:
+            y, xn_next = ops.moe_combine(r, pk, scores, h), None
+        else:
+            y, xn_next = ops.moe_combine_rmsnorm(r, pk, scores, h, next_norm, cfg.eps)
         if debug is not None:
             debug.update(x=x, xn=xn, qkv=qkv, q=q, attn=attn, o=o, h=h, hn=hn, logits=logits, inds=inds,
                          scores=scores, pk=pk, hh=hh, r=r, y=y)
-        return y
+        return y, xn_next
 
 
 class Model:
@@ -146,6 +157,8 @@ class Model:
 
     def decode_step(self, x: torch.Tensor, pools: list, st: StepState) -> torch.Tensor:
         """x [B, D] bf16 hidden rows -> the last layer's output rows; pools[l] is layer l's KV pool."""
-        for layer, pool in zip(self.layers, pools):
-            x = layer.step(x, pool, st)
+        xn = None
+        for i, (layer, pool) in enumerate(zip(self.layers, pools)):
+            nxt = self.layers[i + 1].input_norm if i + 1 < len(self.layers) else None
+            x, xn = layer.run(x, pool, st, xn=xn, next_norm=nxt)
         return x

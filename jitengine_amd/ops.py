@@ -261,6 +261,32 @@ def moe_combine(r: torch.Tensor, pk: Packing, scores: torch.Tensor, resid: torch
     return y
 
 
+def moe_combine_rmsnorm(r: torch.Tensor, pk: Packing, scores: torch.Tensor, resid: torch.Tensor | None,
+                        w: torch.Tensor, eps: float):
+    """(y, xn): y = moe_combine(r, pk, scores, resid) and xn = rmsnorm(y, w, eps) in one launch
+    (jit_moe_combine_rmsnorm; bit for bit the two calls) -- a layer's output and the next layer's
+    normed input."""
+    _need(r, torch.bfloat16, "r")
+    _need(scores, torch.bfloat16, "scores")
+    _need(w, torch.bfloat16, "w")
+    B, k = scores.shape
+    D = r.shape[-1]
+    if resid is not None:
+        _need(resid, torch.bfloat16, "resid")
+        if resid.shape != (B, D):
+            raise ValueError("resid must be [B, D]")
+    if w.numel() != D:
+        raise ValueError(f"norm weight of {w.numel()} for rows of {D}")
+    y = torch.empty((B, D), dtype=torch.bfloat16, device=r.device)
+    xn = torch.empty_like(y)
+    _lib.check(
+        _lib.lib().jit_moe_combine_rmsnorm(_p(r), _p(pk.inv), _p(scores), B, k, D, _p(resid), _p(y), _p(w),
+                                           float(eps), _p(xn), _stream()),
+        "moe_combine_rmsnorm",
+    )
+    return y, xn
+
+
 # ----------------------------------------------------------------------------- decoder block glue
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, resid: torch.Tensor | None = None,
             return_sum: bool = False):
@@ -296,7 +322,7 @@ def qk_norm_rope_append(qkv: torch.Tensor, H: int, Hkv: int, q_norm: torch.Tenso
     _need(page_table, torch.int32, "page_table")
     _need(inv_freq, torch.float32, "inv_freq")
     B = qkv.shape[0]
-    if qkv.shape[1] != (H + 2 * Hkv) * HEAD_DIM or pool.shape[2] != Hkv or inv_freq.numel() != HEAD_DIM // 2:
+    if qkv.shape[1] != (H + 2 * Hkv) * HEAD_DIM or _pool_heads(pool) != Hkv or inv_freq.numel() != HEAD_DIM // 2:
         raise ValueError("qkv / pool / inv_freq do not match the head geometry")
     q = torch.empty((B, H, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
     _lib.check(
@@ -310,6 +336,13 @@ def qk_norm_rope_append(qkv: torch.Tensor, H: int, Hkv: int, q_norm: torch.Tenso
 
 
 # ----------------------------------------------------------------------------- paged KV
+def _pool_heads(pool: torch.Tensor) -> int:
+    """kv heads of a layer's pool [num_pages, Hkv, 2 (K, V), 16 * 128] (ValueError otherwise)."""
+    if pool.dim() != 4 or pool.shape[2] != 2 or pool.shape[3] != PAGE * HEAD_DIM or not pool.is_contiguous():
+        raise ValueError(f"a KV pool is a contiguous [pages, Hkv, 2, {PAGE * HEAD_DIM}] tensor, got {tuple(pool.shape)}")
+    return int(pool.shape[1])
+
+
 def kv_append_paged(pool: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor,
                     page_table: torch.Tensor) -> None:
     """Write k, v [B, Hkv, 128] at positions pos [B] (KVSlot.append, Q36/kvcache/kv_cache.py:76-85)."""
@@ -319,8 +352,8 @@ def kv_append_paged(pool: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: t
     _need(pos, torch.int32, "pos")
     _need(page_table, torch.int32, "page_table")
     B, Hkv, Dh = k.shape
-    if Dh != HEAD_DIM or v.shape != k.shape or pool.shape[2] != Hkv or pool.shape[3] != PAGE * HEAD_DIM:
-        raise ValueError("kv_append_paged: k/v [B, Hkv, 128] must match the pool [pages, 2, Hkv, 2048]")
+    if Dh != HEAD_DIM or v.shape != k.shape or _pool_heads(pool) != Hkv:
+        raise ValueError("kv_append_paged: k/v [B, Hkv, 128] must match the pool [pages, Hkv, 2, 2048]")
     _lib.check(
         _lib.lib().jit_kv_append_paged(
             _p(k), _p(v), B, Hkv, _p(pos), _p(page_table), page_table.shape[1], _p(pool), _stream()
@@ -377,7 +410,7 @@ def paged_decode_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torc
     _need(pool, torch.bfloat16, "pool")
     _need(page_table, torch.int32, "page_table")
     B, H, Dh = q.shape
-    Hkv = pool.shape[2]
+    Hkv = _pool_heads(pool)
     if Dh != HEAD_DIM:
         raise _lib.UnsupportedShape(f"paged_decode_attention covers head_dim 128, got {Dh}")
     if plan.lens.shape[0] != B or page_table.shape[0] != B:
@@ -385,8 +418,8 @@ def paged_decode_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torc
     if B and int((plan.lens_host.max() + PAGE - 1) // PAGE) > page_table.shape[1]:
         raise ValueError(f"page_table has {page_table.shape[1]} columns, the longest sequence needs "
                          f"{int((plan.lens_host.max() + PAGE - 1) // PAGE)}")
-    if H % Hkv or pool.shape[3] != PAGE * HEAD_DIM:
-        raise ValueError(f"{H} query heads over a pool of {Hkv} kv heads / page width {pool.shape[3]}")
+    if H % Hkv:
+        raise ValueError(f"{H} query heads over a pool of {Hkv} kv heads")
     need = attn_workspace_bytes(plan.total, H)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)

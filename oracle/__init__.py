@@ -320,7 +320,7 @@ PAGE = 16
 
 
 def kv_append_paged(pool, k, v, pos, page_table) -> None:
-    """In place: pool [num_pages, 2, Hkv, 16*Dh] bf16; k, v [B, Hkv, Dh]; pos [B]."""
+    """In place: pool [num_pages, Hkv, 2, 16*Dh] bf16; k, v [B, Hkv, Dh]; pos [B]."""
     assert pool.flags["C_CONTIGUOUS"] and pool.dtype == np.uint16
     k, v, pos, pt = _u16(k), _u16(v), _i32(pos), _i32(page_table)
     B, Hkv, Dh = k.shape
@@ -345,7 +345,7 @@ def paged_decode_attn(q, pool, page_table, lens, scale: float) -> np.ndarray:
     """q [B, H, Dh] bf16 -> out [B, H, Dh] bf16 (float64 softmax attention over lens[b] tokens)."""
     q, pool, pt, ln = _u16(q), _u16(pool), _i32(page_table), _i32(lens)
     B, H, Dh = q.shape
-    Hkv = pool.shape[2]
+    Hkv = pool.shape[1]
     out = np.empty_like(q)
     _check(
         lib().jo_paged_decode_attn(

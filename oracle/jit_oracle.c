@@ -441,18 +441,19 @@ int jo_moe_combine(const uint16_t *r, const int32_t *inv, const uint16_t *scores
 /* ----------------------------------------------------- a6/a7 paged KV
  * Paged pool layout (the build's design; the reference keeps one contiguous
  * [1, Hkv, cap, Dh] buffer per request, Q36/kvcache/kv_cache.py:27-85):
- * pool [num_pages, 2, Hkv, 16 * Dh] bf16; part 0 of a page is K chunk-major
- * ([d / 32][slot][d % 32]), part 1 is V dim-major ([d][slot]).  Token t of
- * sequence b lives in page page_table[b * max_pages + t / 16], slot t % 16. */
+ * pool [num_pages, Hkv, 2, 16 * Dh] bf16; for each kv head part 0 of a page is
+ * K chunk-major ([d / 32][slot][d % 32]), part 1 is V dim-major ([d][slot]).
+ * Token t of sequence b lives in page page_table[b * max_pages + t / 16], slot
+ * t % 16. */
 #define JO_PAGE 16
 
 static inline size_t k_index(int page, int Hkv, int Dh, int h, int slot, int d) {
   /* chunk-major K block: [Dh / 32 chunks][16 slots][32 dims] */
-  return (((size_t)page * 2 + 0) * Hkv + h) * (size_t)(JO_PAGE * Dh) + (size_t)(d / 32) * (JO_PAGE * 32) +
+  return (((size_t)page * Hkv + h) * 2 + 0) * (size_t)(JO_PAGE * Dh) + (size_t)(d / 32) * (JO_PAGE * 32) +
          (size_t)slot * 32 + (d % 32);
 }
 static inline size_t v_index(int page, int Hkv, int Dh, int h, int slot, int d) {
-  return (((size_t)page * 2 + 1) * Hkv + h) * (size_t)(JO_PAGE * Dh) + (size_t)d * JO_PAGE + slot;
+  return (((size_t)page * Hkv + h) * 2 + 1) * (size_t)(JO_PAGE * Dh) + (size_t)d * JO_PAGE + slot;
 }
 
 /* KVSlot.append restated for pages (Q36/kvcache/kv_cache.py:76-85): the k, v

@@ -46,7 +46,7 @@ def test_qk_norm_rope_append_parity(pos):
     table = rng.integers(0, num_pages, (B, npg)).astype(np.int32)  # only the written page matters
     for b, p in enumerate(pos):
         table[b, p // 16] = b  # distinct pages for the written slots
-    pool = normal_bf16((num_pages, 2, Hkv, 2048), seed=9)
+    pool = normal_bf16((num_pages, Hkv, 2, 2048), seed=9)
     pt = bf16_tensor(pool, DEV)
     q = ops.qk_norm_rope_append(bf16_tensor(qkv, DEV), H, Hkv, bf16_tensor(qn, DEV), bf16_tensor(kn, DEV), 1e-6,
                                 torch.from_numpy(inv).to(DEV), _i32(pos), _i32(table), pt)
@@ -55,9 +55,9 @@ def test_qk_norm_rope_append_parity(pos):
     st = assert_close_bf16(u16(q), wq, what="q")
     assert st["bit_equal"] > 0.95, st
     got_pool = u16(pt)
-    assert np.array_equal(got_pool[:, 1], want_pool[:, 1])  # V parts: copied verbatim, nothing else touched
-    kg = got_pool[:, 0].reshape(num_pages, Hkv, 4, 16, 32).copy()  # K chunk-major [d/32][slot][d%32]
-    kw = want_pool[:, 0].reshape(num_pages, Hkv, 4, 16, 32).copy()
+    assert np.array_equal(got_pool[:, :, 1], want_pool[:, :, 1])  # V parts: copied verbatim, nothing else touched
+    kg = got_pool[:, :, 0].reshape(num_pages, Hkv, 4, 16, 32).copy()  # K chunk-major [d/32][slot][d%32]
+    kw = want_pool[:, :, 0].reshape(num_pages, Hkv, 4, 16, 32).copy()
     for b, p in enumerate(pos):
         assert_close_bf16(kg[b, :, :, p % 16], kw[b, :, :, p % 16], what="k")
         kg[b, :, :, p % 16] = kw[b, :, :, p % 16]
@@ -87,7 +87,7 @@ def _ctx(lens, cfg, seed):
     for i, n in enumerate(npg):
         table[i, :n] = perm[at:at + n]
         at += n
-    pools = [normal_bf16((num_pages, 2, cfg.kv_heads, 2048), seed=seed + 10 + l) for l in range(cfg.layers)]
+    pools = [normal_bf16((num_pages, cfg.kv_heads, 2, 2048), seed=seed + 10 + l) for l in range(cfg.layers)]
     return table, pools
 
 
@@ -120,6 +120,44 @@ def test_decoder_layer_parity():
     # combine, residual): up to 4 ulps where that exceeds the absolute 2e-2 (|y| in [2, 4) has
     # an ulp of 1.6e-2)
     assert_close_bf16(u16(y), ref["y"], what="layer output", ulps=4.0)
+
+
+@pytest.mark.parametrize("B,resid", [(1, True), (32, True), (33, False)])
+def test_combine_rmsnorm_equals_combine_then_rmsnorm(B, resid):
+    """The fused layer-closing launch gives bit for bit moe_combine and then the next layer's
+    input RMSNorm of its output."""
+    k, D, P = 8, 2048, B * 8
+    rng = np.random.default_rng(B)
+    r = bf16_tensor(normal_bf16((P, D), seed=B + 1, scale=0.5), DEV)
+    inds = np.stack([rng.permutation(128)[:k] for _ in range(B)]).astype(np.int32)
+    pk = ops.moe_pack(_i32(inds), 128)
+    scores = bf16_tensor(normal_bf16((B, k), seed=B + 2, scale=0.2), DEV)
+    h = bf16_tensor(normal_bf16((B, D), seed=B + 3), DEV) if resid else None
+    w = bf16_tensor(oracle.f32_to_bf16((1 + 0.02 * rng.standard_normal(D)).astype(np.float32)), DEV)
+    y, xn = ops.moe_combine_rmsnorm(r, pk, scores, h, w, 1e-6)
+    y2 = ops.moe_combine(r, pk, scores, h)
+    assert torch.equal(y, y2)
+    assert torch.equal(xn, ops.rmsnorm(y2, w, 1e-6))
+
+
+def test_model_decode_step_equals_layer_chain():
+    """Model.decode_step (each layer's combine also norms the next layer's input) gives bit for
+    bit the chain of stand-alone layer steps."""
+    cfg = MoEConfig(experts=32, layers=3)
+    lens = [70, 1500, 9]
+    model = Model(cfg, [random_layer_weights(cfg, seed=40 + l, device=DEV) for l in range(cfg.layers)])
+    table, pools = _ctx(lens, cfg, seed=41)
+    x = bf16_tensor(normal_bf16((len(lens), 2048), seed=42), DEV)
+    st = model.make_state(np.array(lens), _i32(table))
+    pa = [bf16_tensor(p, DEV) for p in pools]
+    pb = [bf16_tensor(p, DEV) for p in pools]
+    fused = model.decode_step(x, pa, st)
+    y = x
+    for layer, pool in zip(model.layers, pb):
+        y = layer.step(y, pool, st)
+    assert torch.equal(fused, y)
+    for p, q in zip(pa, pb):
+        assert torch.equal(p, q)  # the same KV appended
 
 
 def test_model_decode_step_rows_are_independent():

@@ -17,7 +17,8 @@ from jitengine_amd import ops
 from jitengine_amd.moe import MoEBlock
 from jitengine_amd.quant import QLinear
 from tests.helpers import (
-    assert_close_bf16, bf16_tensor, bf16_to_f32, make_stack, normal_bf16, router_logits, stack_np, tie_gates, u16,
+    assert_close_bf16, bf16_tensor, bf16_to_f32, f32_to_bf16, make_stack, normal_bf16, router_logits, stack_np, tie_gates,
+    u16,
 )
 
 pytestmark = pytest.mark.gpu
@@ -272,7 +273,7 @@ def _pool(lens, seed, Hkv=4, H=32, extra=5):
     for i, n in enumerate(npg):
         table[i, :n] = perm[at:at + n]
         at += n
-    pool = normal_bf16((total, 2, Hkv, 16 * 128), seed=seed + 1)
+    pool = normal_bf16((total, Hkv, 2, 16 * 128), seed=seed + 1)
     q = normal_bf16((len(lens), H, 128), seed=seed + 2)
     return q, pool, table
 

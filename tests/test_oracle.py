@@ -236,7 +236,7 @@ def _pool_case(lens, Hkv=4, H=32, seed=0, extra_pages=3):
     for i, n in enumerate(pages_per):
         table[i, :n] = perm[at:at + n]
         at += n
-    pool = normal_bf16((num_pages, 2, Hkv, 16 * 128), seed=seed + 1)
+    pool = normal_bf16((num_pages, Hkv, 2, 16 * 128), seed=seed + 1)
     q = normal_bf16((len(lens), H, 128), seed=seed + 2)
     return q, pool, table
 
@@ -253,8 +253,8 @@ def test_kv_append_gather_round_trip():
         kc, vc = oracle.kv_gather(pool, table[b], lens[b], 4, 128)
         assert np.array_equal(kc[:, pos[b]], k[b]) and np.array_equal(vc[:, pos[b]], v[b])
         pg, sl = table[b, pos[b] // 16], pos[b] % 16
-        assert np.array_equal(pool[pg, 0].reshape(4, 4, 16, 32)[:, :, sl].reshape(4, 128), k[b])  # K chunk-major
-        assert np.array_equal(pool[pg, 1].reshape(4, 128, 16)[:, :, sl], v[b])  # V dim-major
+        assert np.array_equal(pool[pg, :, 0].reshape(4, 4, 16, 32)[:, :, sl].reshape(4, 128), k[b])  # K chunk-major
+        assert np.array_equal(pool[pg, :, 1].reshape(4, 128, 16)[:, :, sl], v[b])  # V dim-major
 
 
 def test_attention_matches_torch_sdpa_float64():
@@ -353,7 +353,7 @@ def _rope_case(pos, seed=80, H=2, Hkv=1):
     inv = (1e6 ** (-np.arange(0, 128, 2) / 128)).astype(np.float32)
     pages = max(p // 16 for p in pos) + 1
     table = np.tile(np.arange(pages, dtype=np.int32), (len(pos), 1))
-    pool = np.zeros((pages, 2, Hkv, 2048), np.uint16)
+    pool = np.zeros((pages, Hkv, 2, 2048), np.uint16)
     q = oracle.qk_norm_rope_append(qkv, H, Hkv, ones, ones, 1e-6, inv, np.array(pos, np.int32), pool, table)
     return qkv, q, pool, inv
 
