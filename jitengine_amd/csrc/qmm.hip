@@ -111,6 +111,17 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   const int G = a.K >> 6, KW = a.K >> 3;
   const int g0 = wave * GPW;
 
+  // x rows of the first pass's tokens, requested before the weights: vector loads
+  // complete in order, so a row index loaded after the weights would hold the
+  // activation loads back until every weight load had landed
+  auto x_row = [&](int tok) {
+    const int pos = off + (tok < cnt ? tok : 0);
+    return a.row_index ? a.row_index[pos] : pos;
+  };
+  int xrow0[TT];
+#pragma unroll
+  for (int tt = 0; tt < TT; tt++) xrow0[tt] = x_row(16 * tt + lr);
+
   // ---- the wave's whole weight slice: GPW groups x NBW row blocks
   uint2 wv[GPW][NBW];
   uint32_t sv[NBW][(GPW + 1) / 2], bv[NBW][(GPW + 1) / 2];  // bf16 pairs (groups 2j, 2j+1)
@@ -160,16 +171,16 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
 
   // TT token tiles of 16 per pass: their activations are loaded together, their
   // partial sums meet in LDS once (one barrier round and one epilogue per pass)
-  for (int t0 = 0; t0 < cnt; t0 += 16 * TT) {
+  // (the first pass is peeled off so that its x rows are the ones requested up front,
+  // with no merge of load paths in front of its activation loads)
+  auto pass = [&](const int t0, const int (&xrows)[TT]) {
     // activation fragments (natural k order, as the unpacked weights); lanes past the
     // last token load a valid row (no branch around the loads): they only feed output
     // rows of tokens that are never stored
     Frag8 xa[TT][GPW][2];
 #pragma unroll
     for (int tt = 0; tt < TT; tt++) {
-      const int tok = t0 + 16 * tt + lr;
-      const int pos = off + (tok < cnt ? tok : 0);
-      const int xrow = a.row_index ? a.row_index[pos] : pos;
+      const int xrow = xrows[tt];
       const uint16_t *xr = a.x + (long long)xrow * a.K + 64 * g0 + 16 * lg;
 #pragma unroll
       for (int g = 0; g < GPW; g++) {
@@ -236,6 +247,13 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
       }
     }
     __syncthreads();
+  };
+  pass(0, xrow0);
+  for (int t0 = 16 * TT; t0 < cnt; t0 += 16 * TT) {
+    int xr[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) xr[tt] = x_row(t0 + 16 * tt + lr);
+    pass(t0, xr);
   }
 }
 
