@@ -7,7 +7,7 @@
 // dim-major -- [128 dims][16 slots], so a fragment's 16 dims x 4 slots per lane
 // group are 512 B contiguous.
 //
-// Attention work item: one workgroup per 256-key chunk of one sequence, one wave per
+// Attention work item: one workgroup per 384-key chunk of one sequence, one wave per
 // kv head; a wave streams the chunk's keys two 16-key pages (32 keys) per step:
 //   S^T[16 keys x 16 q heads] = K_page . Q^T      (4 MFMA 16x16x32 per page)
 //   online softmax in the exp2 domain (fp32 running max / sum per q head)
@@ -29,7 +29,7 @@ namespace {
 constexpr int kD = JIT_HEAD_DIM;      // 128
 constexpr int kPage = JIT_PAGE_TOKENS;  // 16
 constexpr int kPageHead = kPage * kD;   // bf16 elements of one (page, kv head, part)
-constexpr int kChunk = 256;             // keys per work item (one wave per kv head)
+constexpr int kChunk = 384;             // keys per work item (12 two-page steps per wave)
 
 __device__ __forceinline__ int k_off(int slot, int d) { return k_page_offset(slot, d); }
 
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
   const int wk1 = min(wk0 + kChunk, L);
   const int npg = (wk1 - wk0 + kPage - 1) / kPage;  // >= 1: every chunk holds a key
   const int nst = (npg + 1) >> 1;                     // 32-key steps
-  // the chunk's page ids, one per lane (at most kChunk / 16 = 16)
+  // the chunk's page ids, one per lane (at most kChunk / 16 = 24)
   const int my_page = l < npg ? a.page_table[(long long)b * a.max_pages + (wk0 >> 4) + l] : 0;
   const int last = npg - 1;
   // page id i of the chunk (past the last page: the last page again, whose keys are

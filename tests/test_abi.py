@@ -63,7 +63,7 @@ def test_attn_plan_is_a_function_of_each_length():
                               seq.ctypes.data_as(ctypes.c_void_p), seq.size)
     ck = [lib.jit_attn_chunk_tokens(int(L)) for L in lens]
     n = [-(-int(L) // c) for L, c in zip(lens, ck)]
-    assert ck == [256] * 7
+    assert ck == [384] * 7
     assert total == sum(n)
     assert list(cs) == list(np.concatenate([[0], np.cumsum(n)]))
     for b in range(lens.size):

@@ -291,7 +291,8 @@ def test_kv_append_bit_exact():
     assert np.array_equal(u16(pt), want)
 
 
-LENS = [1, 7, 16, 17, 31, 32, 33, 255, 256, 257, 300, 1023, 1024, 1500, 4095, 4096, 6000, 9000, 16384, 16385, 20000]
+LENS = [1, 7, 16, 17, 31, 32, 33, 255, 256, 257, 300, 383, 384, 385, 769, 1023, 1024, 1500, 4095, 4096, 6000, 9000,
+        16384, 16385, 20000]
 
 
 def _attn(q, pool, table, lens, scale=128 ** -0.5):
