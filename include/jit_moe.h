@@ -103,13 +103,15 @@ int jit_qmm(const uint16_t *x, int T, int K, const uint32_t *w, const uint16_t *
 /* Packed tile layout of a quantized stack (the build's MI355X layout; no
  * counterpart in the reference, whose loader keeps the MLX layout,
  * Q36/linear.py:101-128).  The same bytes as the MLX layout, reordered once at
- * load time: per (expert, block of 16 rows, pair of groups) one 1152-byte tile,
- * 64 lanes x 16 B of nibble words in the order the MFMA B operand consumes them
- * (lane 16*j + r: words 2j, 2j+1 of the pair's first group and 2j, 2j+1 of its
- * second group, row r), then 16 rows x (scale pair, bias pair) bf16.  A wave
- * reads a tile with one fully coalesced 1 KB load (the MLX layout in MFMA
- * fragment order is read in 32-byte pieces per row, which caps HBM reads well
- * below the streaming rate).
+ * load time: per (expert, block of 16 rows) GP = K / 128 nibble tiles of 1 KB,
+ * one per pair of groups -- 64 lanes x 16 B of nibble words in the order the
+ * MFMA B operand consumes them (lane 16*j + r: words 2j, 2j+1 of the pair's
+ * first group and 2j, 2j+1 of its second group, row r; each word's nibbles
+ * reordered to q0 q2 q4 q6 q1 q3 q5 q7) -- followed by GP scale tiles of 128 B,
+ * 16 rows x (scale pair, bias pair) bf16.  A wave reads a nibble tile with one
+ * fully coalesced 1 KB load and the scales of 4 consecutive pairs with one 512 B
+ * load (the MLX layout in MFMA fragment order is read in 32-byte pieces per row,
+ * which caps HBM reads well below the streaming rate).
  * jit_q4_packed_bytes: bytes of the packed stack [E, N, K] (-1 if N % 16 or
  * K % 128 != 0).  jit_q4_prepack: w, scales, biases (MLX layout) -> packed. */
 int64_t jit_q4_packed_bytes(int E, int N, int K);

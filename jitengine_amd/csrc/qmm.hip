@@ -41,12 +41,15 @@ struct QmmArgs {
   int rows_w;                      // weight rows per expert (2N with SWIGLU)
 };
 
-// Packed tile layout (jit_q4_prepack): per (expert, 16-row block, pair of groups) one
-// 1152-byte tile -- 64 lanes x 16 B of nibble words in MFMA fragment order (lane
-// 16*lg + lr holds words 2lg, 2lg+1 of the pair's first group and 2lg, 2lg+1 of the
-// second, row lr), then 16 rows x (scale pair, bias pair) bf16.  A wave reads a tile
-// with one fully coalesced 1 KB load plus one 128-byte load.
-constexpr int kTileBytes = 1152;
+// Packed layout (jit_q4_prepack): per (expert, 16-row block) a block of GP = K / 128
+// group pairs -- first GP nibble tiles of 1 KB, 64 lanes x 16 B in MFMA fragment order
+// (lane 16*lg + lr holds words 2lg, 2lg+1 of the pair's first group and 2lg, 2lg+1 of
+// the second, row lr), then GP scale tiles of 128 B, 16 rows x (scale pair, bias
+// pair) bf16.  A wave reads a nibble tile with one fully coalesced 1 KB load, and the
+// scales of up to 4 consecutive pairs with one 512 B load (lane 16*p + lr: pair p, row
+// lr) whose pieces it then passes to the lanes of row lr.
+constexpr int kNibbleBytes = 1024, kScaleBytes = 128;
+constexpr int kTileBytes = kNibbleBytes + kScaleBytes;  // per (16-row block, group pair)
 
 // Nibble order inside a packed-layout word: the MLX word holds q0..q7 at bits 4i;
 // the packed word holds q0, q2, q4, q6 at nibble positions 0-3 and q1, q3, q5, q7 at
@@ -132,17 +135,23 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     const int rowo = n0 + 16 * ob < a.N ? n0 + 16 * ob : n0;
     const int rowb = (SWIGLU && rb >= NB ? a.N : 0) + rowo;  // first row of the block
     if (PACKED) {
+      static_assert(GPW / 2 <= 4, "one scale load covers at most 4 group pairs");
       const int GP = a.K >> 7;
-      const uint8_t *tb = (const uint8_t *)a.w + (long long)e * a.w_estride +
-                          ((long long)(rowb >> 4) * GP + (g0 >> 1)) * kTileBytes;
+      const uint8_t *blk = (const uint8_t *)a.w + (long long)e * a.w_estride + (long long)(rowb >> 4) * GP * kTileBytes;
+      const uint8_t *nb = blk + (g0 >> 1) * kNibbleBytes;
+      // lane group lg fetches pair min(lg, GPW/2 - 1) (lanes past the slice re-read its last pair)
+      const uint2 sbl = *(const uint2 *)(blk + (long long)GP * kNibbleBytes +
+                                         ((g0 >> 1) + min(lg, GPW / 2 - 1)) * kScaleBytes + 8 * lr);
 #pragma unroll
       for (int j = 0; j < GPW / 2; j++) {
-        const uint4 q = *(const uint4 *)(tb + j * kTileBytes + 16 * l);
-        const uint2 sb2 = *(const uint2 *)(tb + j * kTileBytes + 1024 + 8 * lr);
+        const uint4 q = *(const uint4 *)(nb + j * kNibbleBytes + 16 * l);
         wv[2 * j][rb] = make_uint2(q.x, q.y);
         wv[2 * j + 1][rb] = make_uint2(q.z, q.w);
-        sv[rb][j] = sb2.x;
-        bv[rb][j] = sb2.y;
+      }
+#pragma unroll
+      for (int j = 0; j < GPW / 2; j++) {
+        sv[rb][j] = (uint32_t)__shfl((int)sbl.x, 16 * j + lr, 64);
+        bv[rb][j] = (uint32_t)__shfl((int)sbl.y, 16 * j + lr, 64);
       }
     } else {
       const long long row = (long long)rowb + lr;
@@ -305,7 +314,8 @@ int launch_dense(const QmmArgs &a, hipStream_t st) {
   }
 }
 
-// One-time repack of an MLX-layout stack into the tile layout above: one wave per tile.
+// One-time repack of an MLX-layout stack into the packed layout above: one wave per
+// (16-row block, group pair).
 __global__ __launch_bounds__(64) void q4_prepack_kernel(const uint32_t *__restrict__ w,
                                                         const uint16_t *__restrict__ s,
                                                         const uint16_t *__restrict__ b, int N, int K,
@@ -323,12 +333,12 @@ __global__ __launch_bounds__(64) void q4_prepack_kernel(const uint32_t *__restri
   q.y = nibbles_natural(wr[1]);
   q.z = nibbles_natural(wr[8]);
   q.w = nibbles_natural(wr[9]);
-  uint8_t *t = out + tile * kTileBytes;
-  *(uint4 *)(t + 16 * l) = q;
+  uint8_t *blk = out + (tile / GP) * GP * kTileBytes;  // the (expert, row block)'s block
+  *(uint4 *)(blk + gp * kNibbleBytes + 16 * l) = q;
   if (lg == 0) {
     const uint16_t *sr = s + row * G + 2 * gp, *br = b + row * G + 2 * gp;
-    *(uint2 *)(t + 1024 + 8 * lr) = make_uint2((uint32_t)sr[0] | ((uint32_t)sr[1] << 16),
-                                               (uint32_t)br[0] | ((uint32_t)br[1] << 16));
+    *(uint2 *)(blk + (long long)GP * kNibbleBytes + gp * kScaleBytes + 8 * lr) =
+        make_uint2((uint32_t)sr[0] | ((uint32_t)sr[1] << 16), (uint32_t)br[0] | ((uint32_t)br[1] << 16));
   }
 }
 

@@ -632,11 +632,13 @@ int jo_qk_norm_rope_append(const uint16_t *qkv, int B, int H, int Hkv, const uin
 
 /* ------------------------------------------------- packed tile layout
  * The build's MI355X layout of a quantized stack [E, N, K] (no counterpart in
- * the reference): per (expert, block of 16 rows, pair of groups) a 1152-byte
- * tile; bytes 0..1023 hold, for lane l = 16 j + r (j = l / 16, r = l % 16),
- * words 2j, 2j+1 of group 2gp and words 2j, 2j+1 of group 2gp+1 of row 16 rb + r
- * (word w of group g = word 8g + w of the row); bytes 1024..1151 hold, for row
- * r, (scale[2gp], scale[2gp+1], bias[2gp], bias[2gp+1]) bf16. */
+ * the reference): per (expert, block of 16 rows) a block of GP = K / 128 group
+ * pairs, GP * 1152 bytes: first GP nibble tiles of 1024 bytes -- tile gp holds,
+ * for lane l = 16 j + r (j = l / 16, r = l % 16), words 2j, 2j+1 of group 2gp
+ * and words 2j, 2j+1 of group 2gp+1 of row 16 rb + r (word w of group g = word
+ * 8g + w of the row), each with its nibbles reordered as below -- then GP scale
+ * tiles of 128 bytes: tile gp holds, for row r, (scale[2gp], scale[2gp+1],
+ * bias[2gp], bias[2gp+1]) bf16. */
 /* Nibble order of a packed-layout word: q0, q2, q4, q6 at nibble positions 0-3 and
  * q1, q3, q5, q7 at 4-7 (the MLX word holds q_i at position i). */
 static uint32_t nibbles_natural(uint32_t w) {
@@ -656,7 +658,8 @@ int jo_q4_prepack(const uint32_t *w, const uint16_t *s, const uint16_t *b, int E
   for (int e = 0; e < E; e++)
     for (int rb = 0; rb < NRB; rb++)
       for (int gp = 0; gp < GP; gp++) {
-        uint8_t *t = out + (((size_t)e * NRB + rb) * GP + gp) * 1152;
+        uint8_t *blk = out + ((size_t)e * NRB + rb) * GP * 1152; /* GP nibble tiles, then GP scale tiles */
+        uint8_t *t = blk + (size_t)gp * 1024;
         for (int l = 0; l < 64; l++) {
           const int j = l / 16, r = l % 16;
           const uint32_t *wr = w + ((size_t)e * N + rb * 16 + r) * KW;
@@ -670,7 +673,7 @@ int jo_q4_prepack(const uint32_t *w, const uint16_t *s, const uint16_t *b, int E
           const size_t row = (size_t)e * N + rb * 16 + r;
           const uint16_t v[4] = {s[row * G + 2 * gp], s[row * G + 2 * gp + 1], b[row * G + 2 * gp],
                                  b[row * G + 2 * gp + 1]};
-          memcpy(t + 1024 + 8 * r, v, 8);
+          memcpy(blk + (size_t)GP * 1024 + (size_t)gp * 128 + 8 * r, v, 8);
         }
       }
   return JO_OK;

@@ -298,33 +298,36 @@ def _nibbles(words: np.ndarray) -> np.ndarray:
 def test_prepack_is_a_permutation_of_words_and_scales():
     """The packed layout holds every MLX word once, with its nibbles reordered so that the
     unpack (shifts by 0, 4, 8, 12 of the 16-bit halves) yields q0..q7 in natural order, and
-    every scale and bias once."""
+    every scale and bias once: per (expert, 16-row block) GP nibble tiles of 1 KB, then GP
+    scale tiles of 128 B."""
     E, N, K = 2, 32, 256
+    GP = K // 128
     rng = np.random.default_rng(11)
     w = rng.integers(0, 2**32, (E, N, K // 8), dtype=np.uint64).astype(np.uint32)
     s = np.arange(E * N * K // 64, dtype=np.uint16).reshape(E, N, K // 64)
     b = (s + 40000).astype(np.uint16)
     out = oracle.q4_prepack(w, s, b)
-    assert out.size == E * (N // 16) * (K // 128) * 1152
-    tiles = out.reshape(-1, 1152)
-    words = tiles[:, :1024].copy().view(np.uint32).ravel()
+    assert out.size == E * (N // 16) * GP * 1152
+    blocks = out.reshape(-1, GP * 1152)
+    words = blocks[:, :GP * 1024].copy().view(np.uint32).ravel()
     # the unpack order: output pair s (s = 0..3) takes bits 4s (low half) and 16 + 4s (high half)
     pk = _nibbles(words)
     unpacked = np.stack([pk[:, 0], pk[:, 4], pk[:, 1], pk[:, 5], pk[:, 2], pk[:, 6], pk[:, 3], pk[:, 7]], -1)
     back = (unpacked.astype(np.uint32) << (4 * np.arange(8, dtype=np.uint32))).sum(-1).astype(np.uint32)
     assert np.array_equal(np.sort(back), np.sort(w.ravel()))  # each word placed exactly once
-    sb = tiles[:, 1024:].copy().view(np.uint16).reshape(-1, 16, 4)
+    sb = blocks[:, GP * 1024:].copy().view(np.uint16).reshape(-1, 16, 4)
     assert np.array_equal(np.sort(sb[..., :2].ravel()), s.ravel())
     assert np.array_equal(np.sort(sb[..., 2:].ravel()), b.ravel())
-    # tile (e=1, rb=1, gp=1), lane 16*2 + 5: row 21, words 2*2, 2*2+1 of groups 2 and 3; the
-    # unpacked halves of each are q0..q7 of the MLX word in order
-    t = tiles[(1 * 2 + 1) * 2 + 1]
-    lane = t[16 * (16 * 2 + 5):16 * (16 * 2 + 6)].copy().view(np.uint32)
+    # block (e=1, rb=1), pair gp=1, lane 16*2 + 5: row 21, words 2*2, 2*2+1 of groups 2 and 3;
+    # the unpacked halves of each are q0..q7 of the MLX word in order
+    blk = blocks[1 * 2 + 1]
+    lane = blk[1024 * 1 + 16 * (16 * 2 + 5):1024 * 1 + 16 * (16 * 2 + 6)].copy().view(np.uint32)
     want = [w[1, 21, 8 * 2 + 4], w[1, 21, 8 * 2 + 5], w[1, 21, 8 * 3 + 4], w[1, 21, 8 * 3 + 5]]
     for got_w, want_w in zip(lane, want):
         halves = [(int(got_w) >> (4 * i)) & 0xF for i in (0, 4, 1, 5, 2, 6, 3, 7)]
         assert halves == [(int(want_w) >> (4 * i)) & 0xF for i in range(8)]
-    assert list(t[1024 + 8 * 5:1024 + 8 * 6].view(np.uint16)) == [s[1, 21, 2], s[1, 21, 3], b[1, 21, 2], b[1, 21, 3]]
+    sc = blk[GP * 1024 + 128 * 1 + 8 * 5:GP * 1024 + 128 * 1 + 8 * 6].copy().view(np.uint16)
+    assert list(sc) == [s[1, 21, 2], s[1, 21, 3], b[1, 21, 2], b[1, 21, 3]]
 
 
 # ----------------------------------------------------------------------------- decoder block glue
