@@ -23,7 +23,7 @@
 // tiles of 16, so an expert's weights leave HBM once however many tokens it has.
 // The waves' partial sums meet in LDS and are added in wave order (a fixed
 // order: results do not depend on the batch).
-#include "common.hpp"
+#include "qtile.hpp"
 
 namespace {
 
@@ -41,46 +41,12 @@ struct QmmArgs {
   int rows_w;                      // weight rows per expert (2N with SWIGLU)
 };
 
-// Packed layout (jit_q4_prepack): per (expert, 16-row block) a block of GP = K / 128
-// group pairs -- first GP nibble tiles of 1 KB, 64 lanes x 16 B in MFMA fragment order
-// (lane 16*lg + lr holds words 2lg, 2lg+1 of the pair's first group and 2lg, 2lg+1 of
-// the second, row lr), then GP scale tiles of 128 B, 16 rows x (scale pair, bias
-// pair) bf16.  A wave reads a nibble tile with one fully coalesced 1 KB load, and the
-// scales of up to 4 consecutive pairs with one 512 B load (lane 16*p + lr: pair p, row
-// lr) whose pieces it then passes to the lanes of row lr.
-constexpr int kNibbleBytes = 1024, kScaleBytes = 128;
-constexpr int kTileBytes = kNibbleBytes + kScaleBytes;  // per (16-row block, group pair)
-
-// Nibble order inside a packed-layout word: the MLX word holds q0..q7 at bits 4i;
-// the packed word holds q0, q2, q4, q6 at nibble positions 0-3 and q1, q3, q5, q7 at
-// 4-7, so that unpacking yields the k values in natural order and the activations
-// need no shuffle.  jit_q4_prepack applies this once; the MLX-layout kernels apply it
-// in registers, so both feed the matrix cores the same operands.
-__device__ __forceinline__ uint32_t nibbles_natural(uint32_t w) {
-  uint32_t e = w & 0x0F0F0F0Fu, o = (w >> 4) & 0x0F0F0F0Fu;
-  e = (e | (e >> 4)) & 0x00FF00FFu;
-  o = (o | (o >> 4)) & 0x00FF00FFu;
-  e = (e | (e >> 8)) & 0x0000FFFFu;
-  o = (o | (o >> 8)) & 0x0000FFFFu;
-  return e | (o << 16);
-}
-
-// bf16 fragment of the 8 nibbles of a packed-order word: (q0, ..., q7) + 128, each
-// output one shift and one v_and_or_b32 (m = 0x000F000F and c = 0x43004300 are
-// passed in registers: the instruction takes no literal operands).
-__device__ __forceinline__ Frag8 unpack_nibbles(uint32_t w, uint32_t m, uint32_t c) {
-  Frag8 f;
-  f.u[0] = (w & m) | c;
-  f.u[1] = ((w >> 4) & m) | c;
-  f.u[2] = ((w >> 8) & m) | c;
-  f.u[3] = ((w >> 12) & m) | c;
-  return f;
-}
-
-// The unpack masks as register values the compiler cannot fold back into literals.
-#define UNPACK_CONSTANTS(m, c)            \
-  uint32_t m = 0x000F000Fu, c = 0x43004300u; \
-  asm volatile("" : "+v"(m), "+v"(c))
+using qtile::kNibbleBytes;
+using qtile::kScaleBytes;
+using qtile::kTileBytes;
+using qtile::nibbles_natural;
+using qtile::unpack_nibbles;
+#define UNPACK_CONSTANTS(m, c) QTILE_UNPACK_CONSTANTS(m, c)
 
 // SwiGLU with the reference's bf16 rounding points: g, u rounded; sigmoid(g)
 // rounded; bf16(g * sigmoid) * u rounded.

@@ -1,0 +1,109 @@
+// The build's packed 4-bit tile layout and the per-wave MFMA step over it, shared by
+// the quantized projection kernels.
+//
+// Packed layout (jit_q4_prepack): per (expert, 16-row block) a block of GP = K / 128
+// group pairs -- first GP nibble tiles of 1 KB, 64 lanes x 16 B in MFMA fragment order
+// (lane 16*lg + lr holds words 2lg, 2lg+1 of the pair's first group and 2lg, 2lg+1 of
+// the second, row lr), then GP scale tiles of 128 B, 16 rows x (scale pair, bias
+// pair) bf16.  A wave reads a nibble tile with one fully coalesced 1 KB load, and the
+// scales of up to 4 consecutive pairs with one 512 B load (lane 16*p + lr: pair p, row
+// lr) whose pieces it then passes to the lanes of row lr.
+//
+// MFMA tile: v_mfma_f32_16x16x32_bf16 computes C[16 tokens x 16 weight rows], tokens
+// on the M side (A operand = activations), weight rows on the N side (B operand =
+// nibbles).  Every MFMA sees k values of a single quant group, so the group's scale
+// and bias apply to the MFMA result:
+//   sum_k x_k (s q_k + b) = s * sum_k x_k (q_k + 128) + (b - 128 s) * sum_k x_k,
+// with q + 128 formed as a bf16 by one AND-OR and sum_k x_k from an MFMA against ones.
+#pragma once
+
+#include "common.hpp"
+
+namespace qtile {
+
+constexpr int kNibbleBytes = 1024, kScaleBytes = 128;
+constexpr int kTileBytes = kNibbleBytes + kScaleBytes;  // per (16-row block, group pair)
+
+// Nibble order inside a packed-layout word: the MLX word holds q0..q7 at bits 4i;
+// the packed word holds q0, q2, q4, q6 at nibble positions 0-3 and q1, q3, q5, q7 at
+// 4-7, so that unpacking yields the k values in natural order and the activations
+// need no shuffle.  jit_q4_prepack applies this once; the MLX-layout kernels apply it
+// in registers, so both feed the matrix cores the same operands.
+__device__ __forceinline__ uint32_t nibbles_natural(uint32_t w) {
+  uint32_t e = w & 0x0F0F0F0Fu, o = (w >> 4) & 0x0F0F0F0Fu;
+  e = (e | (e >> 4)) & 0x00FF00FFu;
+  o = (o | (o >> 4)) & 0x00FF00FFu;
+  e = (e | (e >> 8)) & 0x0000FFFFu;
+  o = (o | (o >> 8)) & 0x0000FFFFu;
+  return e | (o << 16);
+}
+
+// bf16 fragment of the 8 nibbles of a packed-order word: (q0, ..., q7) + 128, each
+// output one shift and one v_and_or_b32 (m = 0x000F000F and c = 0x43004300 are
+// passed in registers: the instruction takes no literal operands).
+__device__ __forceinline__ Frag8 unpack_nibbles(uint32_t w, uint32_t m, uint32_t c) {
+  Frag8 f;
+  f.u[0] = (w & m) | c;
+  f.u[1] = ((w >> 4) & m) | c;
+  f.u[2] = ((w >> 8) & m) | c;
+  f.u[3] = ((w >> 12) & m) | c;
+  return f;
+}
+
+// The unpack masks as register values the compiler cannot fold back into literals.
+#define QTILE_UNPACK_CONSTANTS(m, c)         \
+  uint32_t m = 0x000F000Fu, c = 0x43004300u; \
+  asm volatile("" : "+v"(m), "+v"(c))
+
+// Loads of one wave's slice of a packed 16-row block: GPW consecutive groups from
+// group g0 (GPW even, at most 8).  wv[g] are the nibble words the lane feeds into
+// group g's two MFMAs; sv[j] / bv[j] the (scale, bias) bf16 pairs of groups 2j, 2j+1
+// of the lane's row.
+template <int GPW>
+__device__ __forceinline__ void load_packed_slice(const uint8_t *blk, int K, int g0, int l, uint2 (&wv)[GPW],
+                                                  uint32_t (&sv)[GPW / 2], uint32_t (&bv)[GPW / 2]) {
+  static_assert(GPW % 2 == 0 && GPW / 2 <= 4, "packed tiles hold pairs of groups; one scale load covers 4");
+  const int GP = K >> 7, lr = l & 15, lg = l >> 4;
+  const uint8_t *nb = blk + (g0 >> 1) * kNibbleBytes;
+  // lane group lg fetches pair min(lg, GPW/2 - 1) (lanes past the slice re-read its last pair)
+  const uint2 sbl = *(const uint2 *)(blk + (long long)GP * kNibbleBytes +
+                                     ((g0 >> 1) + min(lg, GPW / 2 - 1)) * kScaleBytes + 8 * lr);
+#pragma unroll
+  for (int j = 0; j < GPW / 2; j++) {
+    const uint4 q = *(const uint4 *)(nb + j * kNibbleBytes + 16 * l);
+    wv[2 * j] = make_uint2(q.x, q.y);
+    wv[2 * j + 1] = make_uint2(q.z, q.w);
+  }
+#pragma unroll
+  for (int j = 0; j < GPW / 2; j++) {
+    sv[j] = (uint32_t)__shfl((int)sbl.x, 16 * j + lr, 64);
+    bv[j] = (uint32_t)__shfl((int)sbl.y, 16 * j + lr, 64);
+  }
+}
+
+// One quant group of one 16-row block against one token tile: acc (lane l: tokens
+// 4 * (l / 16) + i, row l % 16) += s * C + (b - 128 s) * X, where C = x . (q + 128)
+// over the group's 64 k (two MFMAs) and X = sum of the tile's x over the group (from
+// the caller, one MFMA pair against ones per tile and group).
+__device__ __forceinline__ void group_step(const Frag8 (&xa)[2], const f32x4 &X, uint32_t w0, uint32_t w1,
+                                           uint32_t spair, uint32_t bpair, int odd, uint32_t um, uint32_t uc,
+                                           f32x4 &acc) {
+  const Frag8 B0 = unpack_nibbles(w0, um, uc), B1 = unpack_nibbles(w1, um, uc);
+  const float sc = odd ? bf2f_hi(spair) : bf2f(spair & 0xffffu);
+  const float bi = odd ? bf2f_hi(bpair) : bf2f(bpair & 0xffffu);
+  const float bq = fmaf(-128.0f, sc, bi);
+  f32x4 C = mfma16x16x32(xa[0], B0, f32x4{0.f, 0.f, 0.f, 0.f});
+  C = mfma16x16x32(xa[1], B1, C);
+#pragma unroll
+  for (int i = 0; i < 4; i++) acc[i] = fmaf(bq, X[i], fmaf(sc, C[i], acc[i]));
+}
+
+__device__ __forceinline__ f32x4 group_xsum(const Frag8 (&xa)[2]) {
+  Frag8 ones;
+#pragma unroll
+  for (int i = 0; i < 4; i++) ones.u[i] = 0x3F803F80u;
+  f32x4 X = mfma16x16x32(xa[0], ones, f32x4{0.f, 0.f, 0.f, 0.f});
+  return mfma16x16x32(xa[1], ones, X);
+}
+
+}  // namespace qtile

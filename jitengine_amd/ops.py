@@ -96,9 +96,7 @@ def moe_pack(inds: torch.Tensor, n_experts: int) -> Packing:
     k = inds.shape[-1]
     P = inds.numel()
     E = int(n_experts)
-    buf = torch.empty(3 * P + 5 * E + 4, dtype=torch.int32, device=inds.device)
-    parts = torch.split(buf, [P, P, P, E, E, E, E, E, 4])
-    pk = Packing(*parts, P=P, k=k, E=E)
+    pk = _packing_buffers(P, k, E, inds.device)
     _lib.check(
         _lib.lib().jit_moe_pack(
             _p(inds), P, k, E, _p(pk.order), _p(pk.pair_row), _p(pk.inv), _p(pk.expert_cnt),
@@ -108,6 +106,12 @@ def moe_pack(inds: torch.Tensor, n_experts: int) -> Packing:
         "moe_pack",
     )
     return pk
+
+
+def _packing_buffers(P: int, k: int, E: int, device) -> Packing:
+    buf = torch.empty(3 * P + 5 * E + 4, dtype=torch.int32, device=device)
+    parts = torch.split(buf, [P, P, P, E, E, E, E, E, 4])
+    return Packing(*parts, P=P, k=k, E=E)
 
 
 # ----------------------------------------------------------------------------- packed layout

@@ -174,3 +174,33 @@ def test_model_decode_step_rows_are_independent():
         stb = model.make_state(np.array(lens[b:b + 1]), _i32(table[b:b + 1]))
         solo = u16(model.decode_step(bf16_tensor(x[b:b + 1], DEV), [bf16_tensor(p, DEV) for p in pools], stb))
         assert np.array_equal(solo[0], batched[b]), b
+
+
+def test_layer_packed_equals_mlx_layout_layer():
+    """A decoder layer on packed weights and the same layer on MLX-layout weights give the same
+    intermediates and output and append the same KV bits."""
+    cfg = MoEConfig(experts=64, layers=1)
+    lens = [5, 700, 64, 4000, 1]
+    rng = np.random.default_rng(5)
+    npg = [-(-(L + 1) // 16) for L in lens]
+    num_pages = sum(npg) + 2
+    perm = rng.permutation(num_pages)
+    table = np.zeros((len(lens), max(npg)), np.int32)
+    at = 0
+    for i, n in enumerate(npg):
+        table[i, :n] = perm[at:at + n]
+        at += n
+    w = random_layer_weights(cfg, seed=77, device=DEV)
+    fused, plain = DecoderLayer(cfg, w, prepack=True), DecoderLayer(cfg, w, prepack=False)
+    pool = bf16_tensor(normal_bf16((num_pages, cfg.kv_heads, 2, 2048), seed=78), DEV)
+    pa, pb = pool.clone(), pool.clone()
+    st = make_step_state(cfg, np.array(lens), torch.from_numpy(table).to(DEV))
+    x = bf16_tensor(normal_bf16((len(lens), 2048), seed=79), DEV)
+    da, db = {}, {}
+    ya = fused.step(x, pa, st, debug=da)
+    yb = plain.step(x, pb, st, debug=db)
+    torch.cuda.synchronize()
+    for name in ("hn", "logits", "inds", "scores", "hh", "r"):
+        assert torch.equal(da[name], db[name]), name
+    assert torch.equal(ya, yb)
+    assert torch.equal(pa, pb)
