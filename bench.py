@@ -6,6 +6,7 @@ config 2 (the default; BASELINE.json configs[2], the workload the metric is quot
 continuous-batch decode of 32 sequences over the paged KV pool through 48 layers of the 4-bit
 Qwen3-MoE-style block; a step decodes one token per sequence (value = tokens/s).  The step is
 captured once as a HIP graph and replayed (--no-graph times eager launches).
+config 3 (the expert half of BASELINE.json configs[3]): 2,108 rows on the segment GEMM (MFMA roofline).
 config 1: one standalone quantized-MoE call -- 64 tokens, top-8 of 128
 experts drawn from softmax of N(0,1) logits, gate/up [768 x 2048] and down [2048 x 768] per expert
 (4-bit g64, N(0, 0.02) weights); a step = packing + gate||up/SwiGLU + down + combine.
@@ -181,6 +182,103 @@ def bench_config1(steps: int, warmup: int, dev: str) -> dict:
         "cpu_baseline": {"value": cpu_tps, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
                          "sample": f"oracle expert chain (pack, gate_up, down, combine; float64 dots) on {nb} of "
                                    f"the {B} tokens, median of 5 after a warm-up"},
+        "_y": y,
+    }
+
+
+def bench_config3(steps: int, warmup: int, dev: str) -> dict:
+    """The expert half of BASELINE configs[3], the mixed chunked-prefill + decode step: 4 prefill
+    chunks of 512 tokens plus 60 decode rows = 2,108 rows routed top-8 over 128 experts (router
+    logits N(0,1)), ~132 pairs per expert, on the segment GEMM (row a9: MFMA tiles over long expert
+    segments).  A step = packing + gate||up/SwiGLU + down + combine; the roofline is the MFMA one
+    (bf16 dense peak), flops = 2 * P * (2I * D + D * I)."""
+    import oracle
+    from jitengine_amd import ops
+
+    B, E, D, I, k = 4 * 512 + 60, 128, 2048, 768, 8
+    seed = seed_for(3)
+    rng = np.random.default_rng(seed)
+    gu_mlx = gen_stack((E, 2 * I, D), seed + 1, dev)
+    dn_mlx = gen_stack((E, D, I), seed + 2, dev)
+    gu, dn = ops.prepack(gu_mlx), ops.prepack(dn_mlx)
+    logits = oracle.f32_to_bf16(rng.standard_normal((B, E)).astype(np.float32))
+    x_np = oracle.f32_to_bf16(rng.standard_normal((B, D)).astype(np.float32))
+    to_dev = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(dev)  # noqa: E731
+    x = to_dev(x_np)
+    inds, scores = ops.router_topk(to_dev(logits), k, True)
+    torch.cuda.synchronize()
+
+    def step():
+        pk = ops.moe_pack(inds, E)
+        h = ops.expert_gate_up(x, gu, pk, seg=True)
+        r = ops.expert_down(h, dn, pk, seg=True)
+        return ops.moe_combine(r, pk, scores)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        y = step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    pk = ops.moe_pack(inds, E)
+    h = ops.expert_gate_up(x, gu, pk, seg=True)
+    r = ops.expert_down(h, dn, pk, seg=True)
+    kus = time_ops({"moe_pack": [lambda: ops.moe_pack(inds, E)],
+                    "gate_up_swiglu_seg": [lambda: ops.expert_gate_up(x, gu, pk, seg=True)],
+                    "down_seg": [lambda: ops.expert_down(h, dn, pk, seg=True)],
+                    "combine": [lambda: ops.moe_combine(r, pk, scores)]}, reps=max(steps, 5))
+    P = B * k
+    fl_gu, fl_dn = 2.0 * P * 2 * I * D, 2.0 * P * D * I
+    dom = "gate_up_swiglu_seg"
+    achieved = fl_gu / (kus[dom] * 1e-6) / 1e12
+    U = int(np.unique(inds.cpu().numpy()).size)
+
+    # CPU baseline: the oracle's segment-GEMM arithmetic (bf16 weights, float64 sums) on 16 rows
+    nb = 16
+    ind_np = inds.cpu().numpy().view(np.uint32)[:nb]
+    sc_np = scores[:nb].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    def host(q):
+        return (q.weight.cpu().numpy().view(np.uint32), q.scales.view(torch.int16).cpu().numpy().view(np.uint16),
+                q.biases.view(torch.int16).cpu().numpy().view(np.uint16))
+
+    gu_h, dn_h = host(gu_mlx), host(dn_mlx)
+    oracle.set_num_threads(cpu_threads())
+
+    def cpu_chain():
+        opk = oracle.moe_pack(ind_np, E)
+        hh = oracle.moe_gate_up(x_np[:nb], ind_np, opk, *gu_h, bf16w=True)
+        rr = oracle.moe_down(hh, ind_np, opk, *dn_h, bf16w=True)
+        return oracle.moe_combine(rr, opk["inv"], sc_np)
+
+    cpu_chain()
+    times = []
+    for _ in range(5):
+        c0 = time.perf_counter()
+        cpu_chain()
+        times.append(time.perf_counter() - c0)
+    cpu_tps = nb / float(np.median(times))
+    return {
+        "metric": "decode tok/s (bs=1, ragged bs=32) + achieved HBM GB/s as % of MI355X peak",
+        "value": B / (ms * 1e-3),
+        "unit": "tokens/s",
+        "ms_per_step": ms,
+        "dtype": "bf16 activations and dequantized bf16 weights (4-bit g64 source), fp32 accumulate",
+        "config": {"workload": "config3 expert half: 2,108 rows (4 x 512 prefill + 60 decode) x top-8 of 128 experts "
+                               "on the segment GEMM, gate/up 768x2048, down 2048x768, 4-bit g64",
+                   "rows": B, "pairs": P, "experts": E, "distinct_experts": U,
+                   "max_pairs_per_expert": int(pk.meta[1])},
+        "step_tflops": (fl_gu + fl_dn) / (ms * 1e-3) / 1e12,
+        "kernels_us": kus,
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": achieved / 2500.0, "flops_per_launch": fl_gu, "traffic": None},
+        "cpu_baseline": {"value": cpu_tps, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
+                         "sample": f"oracle segment-GEMM expert chain (bf16 weights, float64 sums) on {nb} of the "
+                                   f"{B} rows, median of 5 after a warm-up"},
         "_y": y,
     }
 
@@ -388,6 +486,8 @@ OP_KERNELS = {  # the kernels one op launches (rocprofv3 kernel names contain th
     "paged_attention": ["paged_attn_kernel", "attn_merge_kernel"],
     "gate_up_swiglu": ["qmm_kernel<1, 8, true, true"],
     "down": ["qmm_kernel<4, 4, false, true"],
+    "gate_up_swiglu_seg": ["seg_kernel<true>"],
+    "down_seg": ["seg_kernel<false>"],
 }
 
 
@@ -413,12 +513,13 @@ def rocprof_summary(args) -> int:
 
     d_dir = args.rocprof_summary
     stats = {r["Name"]: r for r in csv.DictReader(open(os.path.join(d_dir, "kt", "kt_kernel_stats.csv")))}
-    print(f"# rocprofv3 summary of bench.py's default workload (config 2), op {args.op}")
+    cfg = "" if args.config == 2 else f" --config {args.config}"
+    print(f"# rocprofv3 summary of bench.py's config-{args.config} workload, op {args.op}")
     print("# made on one MI355X from the repository root by:")
-    print("#   rocprofv3 --kernel-trace --stats -f csv -d prof/kt -o kt -- python3 bench.py --steps 10 --warmup 2")
+    print(f"#   rocprofv3 --kernel-trace --stats -f csv -d prof/kt -o kt -- python3 bench.py{cfg} --steps 10 --warmup 2")
     if args.op == "step":
-        print("#   python3 bench.py --rocprof-summary prof --op step")
-        print("# this library's kernels over the whole run (48 layers x (warm-up + timed steps + per-op replays));")
+        print(f"#   python3 bench.py --rocprof-summary prof --op step{cfg}")
+        print("# this library's kernels over the whole run (warm-up + timed steps + per-op replays);")
         print("# launches, average / min / max duration in us, share of this library's kernel time")
         ours = [r for r in stats.values() if "(anonymous namespace)::" in r["Name"] and "at::" not in r["Name"]
                 and "prepack" not in r["Name"]]
@@ -429,12 +530,12 @@ def rocprof_summary(args) -> int:
             print(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:9.2f} "
                   f"{float(r['MaxNs']) / 1e3:9.2f} {100 * float(r['TotalDurationNs']) / tot:6.1f}%  {name}")
         return 0
-    for c in ("FETCH_SIZE -f csv -d prof/fetch -o fetch -- python3 bench.py --steps 1 --warmup 1 --no-graph",
-              "WRITE_SIZE -f csv -d prof/write -o write -- python3 bench.py --steps 1 --warmup 1 --no-graph",
+    for c in (f"FETCH_SIZE -f csv -d prof/fetch -o fetch -- python3 bench.py{cfg} --steps 1 --warmup 1 --no-graph",
+              f"WRITE_SIZE -f csv -d prof/write -o write -- python3 bench.py{cfg} --steps 1 --warmup 1 --no-graph",
               "FETCH_SIZE -f csv -d prof/cfetch -o cfetch -- python3 bench.py --copy-calibration",
               "WRITE_SIZE -f csv -d prof/cwrite -o cwrite -- python3 bench.py --copy-calibration"):
         print(f"#   rocprofv3 --pmc {c}")
-    print(f"#   python3 bench.py --rocprof-summary prof --op {args.op}")
+    print(f"#   python3 bench.py --rocprof-summary prof --op {args.op}{cfg}")
     fetch = per_kernel(os.path.join(d_dir, "fetch", "fetch_counter_collection.csv"))
     write = per_kernel(os.path.join(d_dir, "write", "write_counter_collection.csv"))
     cfetch = per_kernel(os.path.join(d_dir, "cfetch", "cfetch_counter_collection.csv"))
@@ -493,6 +594,8 @@ def main() -> int:
         res = bench_config1(args.steps, args.warmup, dev)
     elif args.config == 2:
         res = bench_config2(args.steps, args.warmup, dev, graph=not args.no_graph, n_layers=args.layers)
+    elif args.config == 3:
+        res = bench_config3(args.steps, args.warmup, dev)
     else:
         print(f"config {args.config} is not wired into bench.py", file=sys.stderr)
         return 2
@@ -502,7 +605,7 @@ def main() -> int:
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
             "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to MLX 4-bit g64)",
             "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"]}
-    for key in ("step_hbm", "op_us", "op_us_per_step", "op_us_sum_per_step", "kernels_us"):
+    for key in ("step_hbm", "step_tflops", "op_us", "op_us_per_step", "op_us_sum_per_step", "kernels_us"):
         if key in res:
             line[key] = res[key]
     print(json.dumps(line), flush=True)

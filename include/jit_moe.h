@@ -156,6 +156,23 @@ int jit_moe_down_packed(const uint16_t *h, int I, const int32_t *expert_cnt,
                         const int32_t *expert_off, int E, const void *packed, int D, int P,
                         uint16_t *r, void *stream);
 
+/* Expert GEMMs for long expert segments (chunked prefill: at least 4 pairs per
+ * expert on average, the reference's switch in Q36/model/moe.py:161-175): the
+ * sorted-segment gather_qmm of Q36/kernels/gather_qmm_prefill.py:1-257
+ * (seg_gather_qmm), on matrix-core tiles.  Its arithmetic is that of the
+ * reference's tile GEMM (MLX's quantized block loader): every weight is
+ * dequantized to bf16, w = bf16(fma(s, q, b)), and bf16 products accumulate in
+ * fp32; rows are independent.  Packed stacks only (jit_q4_prepack).
+ * Segments, pair_row and the sorted output order are those of
+ * jit_moe_gate_up_swiglu / jit_moe_down.
+ * gate||up + SwiGLU: x [B, K] -> h [P, I]; contract K % 128 == 0, I % 128 == 0.
+ * down: h [P, I] -> r [P, D]; contract I % 128 == 0, D % 256 == 0. */
+int jit_moe_gate_up_swiglu_seg(const uint16_t *x, int K, const int32_t *pair_row,
+                               const int32_t *expert_cnt, const int32_t *expert_off, int E,
+                               const void *packed, int I, int P, uint16_t *h, void *stream);
+int jit_moe_down_seg(const uint16_t *h, int I, const int32_t *expert_cnt, const int32_t *expert_off,
+                     int E, const void *packed, int D, int P, uint16_t *r, void *stream);
+
 /* Weighted combine in slot order: y[b] = sum_j bf16(r[inv[b*k+j]] * score[b, j])
  * with each product rounded to bf16 and a sequential bf16 sum over j = 0..k-1
  * (Q36/kernels/expert_solo.py:1-6,155-163,307-315; stock

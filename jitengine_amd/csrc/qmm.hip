@@ -48,15 +48,7 @@ using qtile::nibbles_natural;
 using qtile::unpack_nibbles;
 #define UNPACK_CONSTANTS(m, c) QTILE_UNPACK_CONSTANTS(m, c)
 
-// SwiGLU with the reference's bf16 rounding points: g, u rounded; sigmoid(g)
-// rounded; bf16(g * sigmoid) * u rounded.
-__device__ __forceinline__ uint32_t swiglu_bf16(float gacc, float uacc) {
-  const float g = bf2f(f2bf(gacc)), u = bf2f(f2bf(uacc));
-  const float y = 1.0f / (1.0f + __expf(fabsf(g)));
-  const float sg = bf2f(f2bf(g < 0.0f ? y : 1.0f - y));
-  const float sl = bf2f(f2bf(g * sg));
-  return f2bf(sl * u);
-}
+using qtile::swiglu_bf16;
 
 template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1>
 __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {

@@ -106,4 +106,14 @@ __device__ __forceinline__ f32x4 group_xsum(const Frag8 (&xa)[2]) {
   return mfma16x16x32(xa[1], ones, X);
 }
 
+// SwiGLU with the reference's bf16 rounding points: g, u rounded; sigmoid(g)
+// rounded; bf16(g * sigmoid) * u rounded.
+__device__ __forceinline__ uint32_t swiglu_bf16(float gacc, float uacc) {
+  const float g = bf2f(f2bf(gacc)), u = bf2f(f2bf(uacc));
+  const float y = 1.0f / (1.0f + __expf(fabsf(g)));
+  const float sg = bf2f(f2bf(g < 0.0f ? y : 1.0f - y));
+  const float sl = bf2f(f2bf(g * sg));
+  return f2bf(sl * u);
+}
+
 }  // namespace qtile

@@ -41,17 +41,24 @@ class MoEBlock:
         logits = ops.qmm(x, self.router)
         return ops.router_topk(logits, self.top_k, self.norm_topk)
 
+    def use_seg(self, P: int, prefill: bool) -> bool:
+        """Whether a prefill batch of P pairs takes the segment GEMM: at least 4 pairs per expert
+        on average (the reference's switch, Q36/model/moe.py:161-175) on packed stacks.  Decode
+        steps always take the decode kernels, as the reference's decode path does."""
+        return prefill and isinstance(self.gate_up, ops.PackedQ4) and P >= 16 and P // self.num_experts >= 4
+
     def experts(self, x: torch.Tensor, inds: torch.Tensor, scores: torch.Tensor,
-                resid: torch.Tensor | None = None) -> torch.Tensor:
+                resid: torch.Tensor | None = None, prefill: bool = False) -> torch.Tensor:
         """Every selected expert applied and combined: y [B, D] (+ resid)."""
         pk = ops.moe_pack(inds, self.num_experts)
-        h = ops.expert_gate_up(x, self.gate_up, pk)
-        r = ops.expert_down(h, self.down, pk)
+        seg = self.use_seg(pk.P, prefill)
+        h = ops.expert_gate_up(x, self.gate_up, pk, seg=seg)
+        r = ops.expert_down(h, self.down, pk, seg=seg)
         return ops.moe_combine(r, pk, scores, resid)
 
-    def __call__(self, x: torch.Tensor, resid: torch.Tensor | None = None) -> torch.Tensor:
+    def __call__(self, x: torch.Tensor, resid: torch.Tensor | None = None, prefill: bool = False) -> torch.Tensor:
         inds, scores = self.route(x)
-        return self.experts(x, inds, scores, resid)
+        return self.experts(x, inds, scores, resid, prefill)
 
     def with_residual(self, x: torch.Tensor, resid: torch.Tensor) -> torch.Tensor:
         """resid + moe(x)."""

@@ -200,9 +200,16 @@ def _experts_of(lin) -> int:
     return lin.weight.shape[0]
 
 
-def expert_gate_up(x: torch.Tensor, gate_up, pk: Packing) -> torch.Tensor:
+def _need_packed(lin, what: str) -> None:
+    if not isinstance(lin, PackedQ4):
+        raise ValueError(f"{what}: the segment GEMM takes packed stacks (ops.prepack)")
+
+
+def expert_gate_up(x: torch.Tensor, gate_up, pk: Packing, seg: bool = False) -> torch.Tensor:
     """x [B, K] bf16, fused stack [E, 2I, K] -> h [P, I] bf16 in sorted pair order: the grouped
-    gate||up + SwiGLU (expert_gate_up_exact(_rows), Q36/kernels/expert_solo.py:213-232,380-401)."""
+    gate||up + SwiGLU (expert_gate_up_exact(_rows), Q36/kernels/expert_solo.py:213-232,380-401).
+    seg=True runs the segment GEMM of long expert segments instead (seg_gather_qmm,
+    Q36/kernels/gather_qmm_prefill.py:226-257; bf16 weights, jit_moe_gate_up_swiglu_seg)."""
     _need(x, torch.bfloat16, "x")
     E = _experts_of(gate_up)
     if x.shape[-1] != gate_up.in_dims or E != pk.E:
@@ -210,7 +217,13 @@ def expert_gate_up(x: torch.Tensor, gate_up, pk: Packing) -> torch.Tensor:
     I = gate_up.out_dims // 2
     h = torch.empty((pk.P, I), dtype=torch.bfloat16, device=x.device)
     L = _lib.lib()
-    if isinstance(gate_up, PackedQ4):
+    if seg:
+        _need_packed(gate_up, "expert_gate_up")
+        rc = L.jit_moe_gate_up_swiglu_seg(
+            _p(x), x.shape[-1], _p(pk.pair_row), _p(pk.expert_cnt), _p(pk.expert_off), E, _p(gate_up.data),
+            I, pk.P, _p(h), _stream(),
+        )
+    elif isinstance(gate_up, PackedQ4):
         rc = L.jit_moe_gate_up_swiglu_packed(
             _p(x), x.shape[-1], _p(pk.pair_row), _p(pk.expert_cnt), _p(pk.expert_off), E, _p(gate_up.data),
             I, pk.P, _p(h), _stream(),
@@ -224,8 +237,9 @@ def expert_gate_up(x: torch.Tensor, gate_up, pk: Packing) -> torch.Tensor:
     return h
 
 
-def expert_down(h: torch.Tensor, down, pk: Packing) -> torch.Tensor:
-    """h [P, I] bf16, stack [E, D, I] -> r [P, D] bf16 (the down gather, Q36/model/moe.py:193)."""
+def expert_down(h: torch.Tensor, down, pk: Packing, seg: bool = False) -> torch.Tensor:
+    """h [P, I] bf16, stack [E, D, I] -> r [P, D] bf16 (the down gather, Q36/model/moe.py:193);
+    seg=True: the segment GEMM (jit_moe_down_seg), as in expert_gate_up."""
     _need(h, torch.bfloat16, "h")
     E = _experts_of(down)
     D = down.out_dims
@@ -233,7 +247,12 @@ def expert_down(h: torch.Tensor, down, pk: Packing) -> torch.Tensor:
         raise ValueError("h / stack / packing disagree on I, E or P")
     r = torch.empty((pk.P, D), dtype=torch.bfloat16, device=h.device)
     L = _lib.lib()
-    if isinstance(down, PackedQ4):
+    if seg:
+        _need_packed(down, "expert_down")
+        rc = L.jit_moe_down_seg(
+            _p(h), h.shape[-1], _p(pk.expert_cnt), _p(pk.expert_off), E, _p(down.data), D, pk.P, _p(r), _stream(),
+        )
+    elif isinstance(down, PackedQ4):
         rc = L.jit_moe_down_packed(
             _p(h), h.shape[-1], _p(pk.expert_cnt), _p(pk.expert_off), E, _p(down.data), D, pk.P, _p(r), _stream(),
         )

@@ -172,11 +172,12 @@ def moe_pack(inds, n_experts: int) -> dict:
 
 
 # ----------------------------------------------------------------------------- quantized maths
-def dequant4(w, s, b) -> np.ndarray:
+def dequant4(w, s, b, bf16w: bool = False) -> np.ndarray:
+    """[N, K] float64 weights s * q + b; with bf16w the segment GEMM's bf16(fma(s, q, b))."""
     w, s, b = _u32(w), _u16(s), _u16(b)
     N, K = w.shape[0], w.shape[1] * 8
     out = np.empty((N, K), np.float64)
-    _check(lib().jo_dequant4(_p(w), _p(s), _p(b), N, K, _p(out)), "dequant4")
+    _check(lib().jo_dequant4(_p(w), _p(s), _p(b), N, K, int(bf16w), _p(out)), "dequant4")
     return out
 
 
@@ -212,8 +213,9 @@ def qmv_mlx_f32(x, w, s, b) -> np.ndarray:
 
 
 # ----------------------------------------------------------------------------- experts
-def moe_gate_up(x, inds, pack: dict, w, s, b) -> np.ndarray:
-    """h [P, I] bf16 in sorted pair order; w [E, 2I, D/8], s/b [E, 2I, D/64]."""
+def moe_gate_up(x, inds, pack: dict, w, s, b, bf16w: bool = False) -> np.ndarray:
+    """h [P, I] bf16 in sorted pair order; w [E, 2I, D/8], s/b [E, 2I, D/64]; bf16w: the segment
+    GEMM's bf16 weights."""
     x, ind, w, s, b = _u16(x), _u32(inds), _u32(w), _u16(s), _u16(b)
     B, D = x.shape
     E, two_i = w.shape[0], w.shape[1]
@@ -222,21 +224,21 @@ def moe_gate_up(x, inds, pack: dict, w, s, b) -> np.ndarray:
     _check(
         lib().jo_moe_gate_up(
             _p(x), B, D, _p(ind), P, _p(pack["order"]), _p(pack["pair_row"]), _p(w), _p(s), _p(b),
-            E, two_i // 2, _p(h),
+            E, two_i // 2, int(bf16w), _p(h),
         ),
         "moe_gate_up",
     )
     return h
 
 
-def moe_down(h, inds, pack: dict, w, s, b) -> np.ndarray:
-    """r [P, D] bf16 in sorted pair order; w [E, D, I/8], s/b [E, D, I/64]."""
+def moe_down(h, inds, pack: dict, w, s, b, bf16w: bool = False) -> np.ndarray:
+    """r [P, D] bf16 in sorted pair order; w [E, D, I/8], s/b [E, D, I/64]; bf16w as in moe_gate_up."""
     h, ind, w, s, b = _u16(h), _u32(inds), _u32(w), _u16(s), _u16(b)
     P, I = h.shape
     E, D = w.shape[0], w.shape[1]
     r = np.empty((P, D), np.uint16)
     _check(
-        lib().jo_moe_down(_p(h), P, I, _p(ind), _p(pack["order"]), _p(w), _p(s), _p(b), E, D, _p(r)),
+        lib().jo_moe_down(_p(h), P, I, _p(ind), _p(pack["order"]), _p(w), _p(s), _p(b), E, D, int(bf16w), _p(r)),
         "moe_down",
     )
     return r

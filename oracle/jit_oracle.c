@@ -237,11 +237,27 @@ static void dequant_row(const uint32_t *w, const uint16_t *s, const uint16_t *b,
   }
 }
 
-int jo_dequant4(const uint32_t *w, const uint16_t *s, const uint16_t *b, int N, int K, double *out) {
+/* The segment GEMM's weights (a9, Q36/kernels/gather_qmm_prefill.py:1-257, whose
+ * MLX quantized block loader dequantizes into the activation type before the
+ * tile MMA): w = bf16(s * q + b), formed as one fp32 fused multiply-add rounded
+ * to bf16.  bf16w selects these weights over the exact ones of dequant_row. */
+static void dequant_row_w(const uint32_t *w, const uint16_t *s, const uint16_t *b, int K, int bf16w,
+                          double *out) {
+  if (!bf16w) {
+    dequant_row(w, s, b, K, out);
+    return;
+  }
+  for (int j = 0; j < K; j++) {
+    const uint32_t q = (w[j >> 3] >> (4 * (j & 7))) & 0xfu;
+    out[j] = (double)bf2f(f2bf(fmaf(bf2f(s[j >> 6]), (float)q, bf2f(b[j >> 6]))));
+  }
+}
+
+int jo_dequant4(const uint32_t *w, const uint16_t *s, const uint16_t *b, int N, int K, int bf16w, double *out) {
   if (N < 0 || K <= 0 || (K % 64) != 0) return JO_EINVAL;
   for (int n = 0; n < N; n++)
-    dequant_row(w + (size_t)n * (K / 8), s + (size_t)n * (K / 64), b + (size_t)n * (K / 64), K,
-                out + (size_t)n * K);
+    dequant_row_w(w + (size_t)n * (K / 8), s + (size_t)n * (K / 64), b + (size_t)n * (K / 64), K, bf16w,
+                  out + (size_t)n * K);
   return JO_OK;
 }
 
@@ -345,10 +361,11 @@ static inline uint16_t swiglu_bf16(uint16_t gt, uint16_t ut) {
 uint16_t jo_swiglu_bf16(uint16_t g, uint16_t u) { return swiglu_bf16(g, u); }
 
 /* h[p, :] for every sorted pair p; x [B, D] bf16; stacks [E, 2I, D/8] u32 and
- * [E, 2I, D/64] bf16; pair_row/order from jo_moe_pack; inds the flat expert ids. */
+ * [E, 2I, D/64] bf16; pair_row/order from jo_moe_pack; inds the flat expert ids;
+ * bf16w: the segment GEMM's bf16 weights (dequant_row_w). */
 int jo_moe_gate_up(const uint16_t *x, int B, int D, const uint32_t *inds, int P, const int32_t *order,
                    const int32_t *pair_row, const uint32_t *w, const uint16_t *s, const uint16_t *b,
-                   int E, int I, uint16_t *h) {
+                   int E, int I, int bf16w, uint16_t *h) {
   if (B < 0 || P < 0 || D <= 0 || (D % 64) != 0 || I <= 0) return JO_EINVAL;
   const size_t ws = (size_t)2 * I * (D / 8), gs = (size_t)2 * I * (D / 64);
 #pragma omp parallel
@@ -362,10 +379,10 @@ int jo_moe_gate_up(const uint16_t *x, int B, int D, const uint32_t *inds, int P,
         const int e = (int)inds[order[p]];
         if (e < 0 || e >= E) continue;
         if (e != last_e) {
-          dequant_row(w + e * ws + (size_t)n * (D / 8), s + e * gs + (size_t)n * (D / 64),
-                      b + e * gs + (size_t)n * (D / 64), D, gr);
-          dequant_row(w + e * ws + (size_t)(I + n) * (D / 8), s + e * gs + (size_t)(I + n) * (D / 64),
-                      b + e * gs + (size_t)(I + n) * (D / 64), D, ur);
+          dequant_row_w(w + e * ws + (size_t)n * (D / 8), s + e * gs + (size_t)n * (D / 64),
+                        b + e * gs + (size_t)n * (D / 64), D, bf16w, gr);
+          dequant_row_w(w + e * ws + (size_t)(I + n) * (D / 8), s + e * gs + (size_t)(I + n) * (D / 64),
+                        b + e * gs + (size_t)(I + n) * (D / 64), D, bf16w, ur);
           last_e = e;
         }
         const uint16_t *xr = x + (size_t)pair_row[p] * D;
@@ -386,9 +403,9 @@ int jo_moe_gate_up(const uint16_t *x, int B, int D, const uint32_t *inds, int P,
 
 /* ---------------------------------------------------- a5 down + combine
  * r[p, :] = bf16(h[p] . dequant(Wd_e)^T) for every sorted pair (the down
- * gather's bf16 output, Q36/model/moe.py:193). */
+ * gather's bf16 output, Q36/model/moe.py:193); bf16w as in jo_moe_gate_up. */
 int jo_moe_down(const uint16_t *h, int P, int I, const uint32_t *inds, const int32_t *order,
-                const uint32_t *w, const uint16_t *s, const uint16_t *b, int E, int D, uint16_t *r) {
+                const uint32_t *w, const uint16_t *s, const uint16_t *b, int E, int D, int bf16w, uint16_t *r) {
   if (P < 0 || I <= 0 || (I % 64) != 0 || D <= 0) return JO_EINVAL;
   const size_t ws = (size_t)D * (I / 8), gs = (size_t)D * (I / 64);
 #pragma omp parallel
@@ -401,8 +418,8 @@ int jo_moe_down(const uint16_t *h, int P, int I, const uint32_t *inds, const int
         const int e = (int)inds[order[p]];
         if (e < 0 || e >= E) continue;
         if (e != last_e) {
-          dequant_row(w + e * ws + (size_t)n * (I / 8), s + e * gs + (size_t)n * (I / 64),
-                      b + e * gs + (size_t)n * (I / 64), I, row);
+          dequant_row_w(w + e * ws + (size_t)n * (I / 8), s + e * gs + (size_t)n * (I / 64),
+                        b + e * gs + (size_t)n * (I / 64), I, bf16w, row);
           last_e = e;
         }
         const uint16_t *hr = h + (size_t)p * I;

@@ -148,6 +148,30 @@ def test_dequant_matches_independent_unpack():
     assert np.array_equal(oracle.dequant4(w, s, b), want)
 
 
+def _bf16_weights_numpy(w, s, b):
+    """The segment GEMM's weights computed independently: s * q + b is exact in float64 (bf16 s, b
+    and q <= 15), its float32 rounding is the fused multiply-add's result, then RNE to bf16."""
+    N = w.shape[0]
+    nib = ((w.view(np.uint8)[..., None] >> np.array([0, 4], np.uint8)) & 0xF).reshape(N, -1).astype(np.float64)
+    exact = nib * np.repeat(bf16_to_f32(s), 64, -1) + np.repeat(bf16_to_f32(b), 64, -1)
+    return bf16_to_f32(f32_to_bf16(exact.astype(np.float32))).astype(np.float64), exact
+
+
+def test_bf16_weights_match_independent_rounding():
+    q = make_stack((48, 512), seed=13)
+    w, s, b = stack_np(q)
+    want, exact = _bf16_weights_numpy(w, s, b)
+    got = oracle.dequant4(w, s, b, bf16w=True)
+    assert np.array_equal(got, want)
+    assert np.any(got != exact)  # the rounding is real at these scales
+    assert np.all(np.abs(got - exact) <= 2.0**-8 * np.abs(exact))  # within half a bf16 ulp
+    # known answer: 2q - 1 is a bf16 value, so rounding changes nothing
+    w1 = np.full((1, 8), 0x76543210, np.uint32)
+    one = oracle.dequant4(w1, f32_to_bf16(np.array([[2.0]], np.float32)), f32_to_bf16(np.array([[-1.0]], np.float32)),
+                          bf16w=True)
+    assert np.array_equal(one[0], np.tile(2.0 * np.arange(8) - 1.0, 8))
+
+
 def test_qmm_matches_torch_float64_matmul():
     q = make_stack((96, 512), seed=4)
     w, s, b = stack_np(q)
@@ -389,3 +413,27 @@ def test_qk_append_writes_k_and_v_at_the_position():
     assert np.array_equal(vc[0, 40], qkv[1, 3 * 128:])  # v copied verbatim
     assert np.array_equal(vc[0, 3], qkv[0, 3 * 128:])
     assert not np.array_equal(kc[0, 40], qkv[1, 2 * 128:3 * 128])  # k normed + rotated
+
+
+def test_segment_gemm_weights_in_gate_up_and_down():
+    """bf16w gate||up and down equal float64 products over independently rounded weights, rounded
+    to bf16 (and SwiGLU for gate||up) -- and differ from the exact-weight results only slightly."""
+    x, inds, scores, gu, dn = _moe_case(seed=20)
+    pk = oracle.moe_pack(inds, 16)
+    h = oracle.moe_gate_up(x, inds, pk, *gu, bf16w=True)
+    h_exact = oracle.moe_gate_up(x, inds, pk, *gu)
+    r = oracle.moe_down(h, inds, pk, *dn, bf16w=True)
+    I = h.shape[1]
+    flat = inds.reshape(-1)
+    xf = bf16_to_f32(x).astype(np.float64)
+    for p in range(0, pk["order"].size, 13):
+        e, row = int(flat[pk["order"][p]]), int(pk["pair_row"][p])
+        wgu, _ = _bf16_weights_numpy(gu[0][e], gu[1][e], gu[2][e])
+        acc = wgu @ xf[row]
+        g, u = f32_to_bf16(acc[:I].astype(np.float32)), f32_to_bf16(acc[I:].astype(np.float32))
+        assert np.array_equal(h[p], np.array([oracle.swiglu_bf16(a, c) for a, c in zip(g, u)], np.uint16)), p
+        wd, _ = _bf16_weights_numpy(dn[0][e], dn[1][e], dn[2][e])
+        assert np.array_equal(r[p], f32_to_bf16((wd @ bf16_to_f32(h[p]).astype(np.float64)).astype(np.float32))), p
+    assert not np.array_equal(h, h_exact)
+    d = np.abs(bf16_to_f32(h).astype(np.float64) - bf16_to_f32(h_exact))
+    assert d.max() <= 2e-2
