@@ -7,8 +7,9 @@
 // dim-major -- [128 dims][16 slots], so a fragment's 16 dims x 4 slots per lane
 // group are 512 B contiguous.
 //
-// Attention work item: one workgroup per 384-key chunk of one sequence, one wave per
-// kv head; a wave streams the chunk's keys two 16-key pages (32 keys) per step:
+// Attention work item: one workgroup per 1536-key chunk of one sequence and 2 kv heads,
+// 4 waves per kv head, each wave streaming a quarter of the chunk (384 keys) two 16-key
+// pages (32 keys) per step; the 4 waves' states meet in LDS:
 //   S^T[16 keys x 16 q heads] = K_page . Q^T      (4 MFMA 16x16x32 per page)
 //   online softmax in the exp2 domain (fp32 running max / sum per q head)
 //   O^T[128 d x 16 q heads] += V^T . P^T           (8 MFMA 16x16x32, all 32 keys)
@@ -29,7 +30,17 @@ namespace {
 constexpr int kD = JIT_HEAD_DIM;      // 128
 constexpr int kPage = JIT_PAGE_TOKENS;  // 16
 constexpr int kPageHead = kPage * kD;   // bf16 elements of one (page, kv head, part)
-constexpr int kChunk = 384;             // keys per work item (12 two-page steps per wave)
+#ifndef JIT_ATTN_CHUNK
+#define JIT_ATTN_CHUNK 1536
+#endif
+// keys per work item: fewer, longer chunks write fewer partials for the merge, and the
+// waves that split a chunk keep the parallelism of short ones (config 2 on MI355X:
+// kernel + merge 73.4 us with 384-key chunks of one wave per kv head, 68.3 us here)
+constexpr int kChunk = JIT_ATTN_CHUNK;
+#ifndef JIT_ATTN_SPLITS
+#define JIT_ATTN_SPLITS 4
+#endif
+constexpr int kAttnSplits = JIT_ATTN_SPLITS;  // waves per kv head and chunk
 
 __device__ __forceinline__ int k_off(int slot, int d) { return k_page_offset(slot, d); }
 
@@ -130,22 +141,34 @@ __device__ __forceinline__ uint32_t mask_pair(uint32_t w, int k, int L) {
   return (k < L ? (w & 0xffffu) : 0u) | (k + 1 < L ? (w & 0xffff0000u) : 0u);
 }
 
+// WS waves share a kv head's chunk: wave s streams keys [s * kChunk / WS, (s + 1) * kChunk / WS)
+// of it, and the workgroup merges the WS (max, sum, o) states in LDS in wave order, so a
+// chunk's result depends only on its keys.  More waves with shorter key runs each keep more
+// loads in flight than one wave per kv head walking the whole chunk.
+constexpr int kStateFloats = 32 + 2;  // o[8][4], max, sum per lane
+
+template <int WS>
 __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
+  static_assert(kChunk % (32 * WS) == 0, "a wave's key run is whole 32-key steps");
+  constexpr int kRun = kChunk / WS;
+  extern __shared__ float xstate[];  // [WS - 1][hb][kStateFloats][64]
   const int gc = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
-  const int kvh = blockIdx.y * (blockDim.x >> 6) + wave;
-  if (kvh >= a.Hkv) return;
+  const int hb = (blockDim.x >> 6) / WS;  // kv heads per workgroup
+  const int kvl = wave % hb, split = wave / hb;
+  const int kvh = blockIdx.y * hb + kvl;
+  const bool live = kvh < a.Hkv;  // (dead waves still meet the barrier of the merge)
   const int b = a.chunk_seq[gc];
   const int L = a.lens[b];
   const int c = gc - a.chunk_start[b];
   const int nchunks = (L + kChunk - 1) / kChunk;
   const int lr = l & 15, lg = l >> 4;
   const int G = a.G;
-  const int wk0 = c * kChunk;
-  const int wk1 = min(wk0 + kChunk, L);
-  const int npg = (wk1 - wk0 + kPage - 1) / kPage;  // >= 1: every chunk holds a key
-  const int nst = (npg + 1) >> 1;                     // 32-key steps
-  // the chunk's page ids, one per lane (at most kChunk / 16 = 24)
+  const int wk0 = c * kChunk + split * kRun;
+  const int wk1 = min(c * kChunk + (split + 1) * kRun, L);
+  const int npg = wk1 > wk0 ? (wk1 - wk0 + kPage - 1) / kPage : 0;  // split 0 always holds a key
+  const int nst = live ? (npg + 1) >> 1 : 0;                          // 32-key steps
+  // the run's page ids, one per lane (at most kRun / 16 <= 24)
   const int my_page = l < npg ? a.page_table[(long long)b * a.max_pages + (wk0 >> 4) + l] : 0;
   const int last = npg - 1;
   // page id i of the chunk (past the last page: the last page again, whose keys are
@@ -172,9 +195,11 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
   Frag8 kf[2][4];
   uint2 vv[2][8];
   // K before V, as in the loop, so a step's K wait leaves its V loads in flight
-  load_k2(kf, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
-  asm volatile("" ::: "memory");
-  load_v2(vv, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
+  if (nst > 0) {
+    load_k2(kf, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
+    asm volatile("" ::: "memory");
+    load_v2(vv, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
+  }
   for (int st = 0; st < nst; st++) {
     const int k0 = wk0 + 32 * st;
     f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -244,6 +269,34 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
     // keep these loads in this step: sunk into the next step they would only be
     // issued once that step's K has arrived
     asm volatile("" ::: "memory");
+  }
+  if (WS > 1) {  // the splits' states meet: split 0 of each kv head adds splits 1.. in order
+    if (split > 0) {
+      float *st = xstate + (((split - 1) * hb + kvl) * kStateFloats) * 64 + l;
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) st[(4 * cc + i) * 64] = o[cc][i];
+      st[32 * 64] = m_run;
+      st[33 * 64] = l_run;
+    }
+    __syncthreads();
+    if (split > 0 || !live) return;
+#pragma unroll
+    for (int sp = 1; sp < WS; sp++) {
+      const float *st = xstate + (((sp - 1) * hb + kvl) * kStateFloats) * 64 + l;
+      const float m2 = st[32 * 64], l2 = st[33 * 64];
+      const float M = fmaxf(m_run, m2);  // split 0 holds a key: M is finite
+      const float f0 = exp2f(m_run - M), f1 = exp2f(m2 - M);
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[cc][i] = o[cc][i] * f0 + st[(4 * cc + i) * 64] * f1;
+      l_run = l_run * f0 + l2 * f1;
+      m_run = M;
+    }
+  } else if (!live) {
+    return;
   }
   // per-head sum over the four lane groups
   const float l_tot = sum_xor32(sum_xor16(l_run));
@@ -393,8 +446,10 @@ extern "C" int jit_paged_decode_attn(const uint16_t *q, const uint16_t *pool,
   AttnArgs a{q, pool, page_table, lens, chunk_start, chunk_seq, part_o, part_ml, out,
              max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f};
   hipStream_t st = (hipStream_t)stream;
-  const int hb = Hkv < 8 ? Hkv : 8;  // kv heads (waves) per workgroup
-  paged_attn_kernel<<<dim3(total_chunks, (Hkv + hb - 1) / hb), 64 * hb, 0, st>>>(a);
+  constexpr int WS = kAttnSplits;
+  const int hb = Hkv < 8 / WS ? Hkv : 8 / WS;  // kv heads per workgroup (WS waves each, <= 8 waves)
+  const size_t lds = (size_t)(WS - 1) * hb * kStateFloats * 64 * sizeof(float);
+  paged_attn_kernel<WS><<<dim3(total_chunks, (Hkv + hb - 1) / hb), 64 * hb * WS, lds, st>>>(a);
   int rc = jit::check_launch("jit_paged_decode_attn");
   if (rc) return rc;
   attn_merge_kernel<<<dim3(B, H), 512, 0, st>>>(lens, chunk_start, part_o, part_ml, H, out);

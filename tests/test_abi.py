@@ -56,14 +56,14 @@ def test_contract_breaks_return_einval_before_launch():
 
 def test_attn_plan_is_a_function_of_each_length():
     lib = _lib.lib()
-    lens = np.array([1, 255, 256, 257, 16384, 16385, 262144], np.int32)
+    lens = np.array([1, 255, 256, 1535, 1536, 1537, 16385, 262144], np.int32)
     cs = np.zeros(lens.size + 1, np.int32)
     seq = np.zeros(2000, np.int32)
     total = lib.jit_attn_plan(lens.ctypes.data_as(ctypes.c_void_p), lens.size, cs.ctypes.data_as(ctypes.c_void_p),
                               seq.ctypes.data_as(ctypes.c_void_p), seq.size)
     ck = [lib.jit_attn_chunk_tokens(int(L)) for L in lens]
     n = [-(-int(L) // c) for L, c in zip(lens, ck)]
-    assert ck == [384] * 7
+    assert ck == [1536] * 8
     assert total == sum(n)
     assert list(cs) == list(np.concatenate([[0], np.cumsum(n)]))
     for b in range(lens.size):

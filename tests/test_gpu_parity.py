@@ -291,8 +291,8 @@ def test_kv_append_bit_exact():
     assert np.array_equal(u16(pt), want)
 
 
-LENS = [1, 7, 16, 17, 31, 32, 33, 255, 256, 257, 300, 383, 384, 385, 769, 1023, 1024, 1500, 4095, 4096, 6000, 9000,
-        16384, 16385, 20000]
+LENS = [1, 7, 16, 17, 31, 32, 33, 255, 256, 257, 300, 383, 384, 385, 769, 1023, 1024, 1152, 1500, 1535, 1536, 1537,
+        3072, 3073, 4095, 4096, 6000, 9000, 16384, 16385, 20000]
 
 
 def _attn(q, pool, table, lens, scale=128 ** -0.5):
@@ -307,6 +307,16 @@ def test_paged_attention_parity():
     want = oracle.paged_decode_attn(q, pool, table, LENS, 128 ** -0.5)
     for b, L in enumerate(LENS):
         assert_close_bf16(got[b], want[b], max_abs=2e-2, min_cos=0.9995, what=f"attention L={L}")
+
+
+def test_paged_attention_long_context():
+    """BASELINE config 4's shape: one sequence of 262,144 keys in permuted 16-token pages
+    (171 chunks split over 4 waves per kv head, merged in chunk order)."""
+    L = 262144
+    q, pool, table = _pool([L], seed=23)
+    got = _attn(q, pool, table, [L])
+    want = oracle.paged_decode_attn(q, pool, table, [L], 128 ** -0.5)
+    assert_close_bf16(got, want, max_abs=2e-2, min_cos=0.9995, what="attention L=262144")
 
 
 def test_paged_attention_one_key_is_its_value():
