@@ -71,6 +71,10 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   const int n0 = blockIdx.x * (16 * NB);
   const int G = a.K >> 6, KW = a.K >> 3;
   const int g0 = wave * GPW;
+  // token passes of 16 * TT tokens; with gridDim.z > 1 the passes are dealt to z
+  // workgroups of the same rows (a dense decode batch split over more workgroups)
+  const int tfirst = 16 * TT * blockIdx.z, tstride = 16 * TT * gridDim.z;
+  if (tfirst >= cnt) return;  // uniform over the workgroup
 
   // x rows of the first pass's tokens, requested before the weights: vector loads
   // complete in order, so a row index loaded after the weights would hold the
@@ -81,7 +85,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   };
   int xrow0[TT];
 #pragma unroll
-  for (int tt = 0; tt < TT; tt++) xrow0[tt] = x_row(16 * tt + lr);
+  for (int tt = 0; tt < TT; tt++) xrow0[tt] = x_row(tfirst + 16 * tt + lr);
 
   // ---- the wave's whole weight slice: GPW groups x NBW row blocks
   uint2 wv[GPW][NBW];
@@ -215,8 +219,8 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     }
     __syncthreads();
   };
-  pass(0, xrow0);
-  for (int t0 = 16 * TT; t0 < cnt; t0 += 16 * TT) {
+  pass(tfirst, xrow0);
+  for (int t0 = tfirst + tstride; t0 < cnt; t0 += tstride) {
     int xr[TT];
 #pragma unroll
     for (int tt = 0; tt < TT; tt++) xr[tt] = x_row(t0 + 16 * tt + lr);
@@ -225,13 +229,13 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
 }
 
 template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1>
-int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what) {
+int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what, int zsplit = 1) {
   constexpr int NBW = SWIGLU ? 2 * NB : NB;
   const int G = a.K / 64;
   const int ksplit = G / GPW;
   if (ksplit * GPW != G || ksplit < 1 || ksplit > 8)
     return jit::fail(JIT_EUNSUPPORTED, "%s: K=%d does not split into %d-group wave slices", what, a.K, GPW);
-  const dim3 grid((a.N + 16 * NB - 1) / (16 * NB), E), block(64 * ksplit);
+  const dim3 grid((a.N + 16 * NB - 1) / (16 * NB), E, zsplit), block(64 * ksplit);
   const size_t lds = (size_t)ksplit * TT * NBW * 4 * 64 * sizeof(float);
   qmm_kernel<NB, GPW, SWIGLU, PACKED, TT><<<grid, block, lds, st>>>(a);
   return jit::check_launch(what);
@@ -251,13 +255,24 @@ int dense_gpw(int K) {
 // short K-slice per wave (the activations each workgroup pulls through L2 then
 // serve twice the rows).  The shape never changes a result: each output sums the
 // same groups in the same order.
+#ifndef JIT_DENSE_ZMAX
+#define JIT_DENSE_ZMAX 4
+#endif
+#ifndef JIT_DENSE_WIDE_N
+#define JIT_DENSE_WIDE_N 4096
+#endif
 template <bool PACKED, int GPW>
 int launch_dense_gpw(const QmmArgs &a, hipStream_t st, const char *what) {
-  const bool two_tiles = a.T > 16, wide = GPW <= 4 && a.N >= 4096;
-  if (wide) return two_tiles ? launch_qmm<2, GPW, false, PACKED, 2>(a, 1, st, what)
-                             : launch_qmm<2, GPW, false, PACKED, 1>(a, 1, st, what);
-  return two_tiles ? launch_qmm<1, GPW, false, PACKED, 2>(a, 1, st, what)
-                   : launch_qmm<1, GPW, false, PACKED, 1>(a, 1, st, what);
+  // a decode batch's 16-token tiles go to separate workgroups (up to JIT_DENSE_ZMAX), so a
+  // matrix of few row blocks still fills the chip and each workgroup pulls one tile's
+  // activations; longer batches take two tiles per pass
+  const int tiles = (a.T + 15) / 16;
+  const bool wide = GPW <= 4 && a.N >= JIT_DENSE_WIDE_N;
+  if (tiles <= JIT_DENSE_ZMAX)
+    return wide ? launch_qmm<2, GPW, false, PACKED, 1>(a, 1, st, what, tiles)
+                : launch_qmm<1, GPW, false, PACKED, 1>(a, 1, st, what, tiles);
+  return wide ? launch_qmm<2, GPW, false, PACKED, 2>(a, 1, st, what)
+              : launch_qmm<1, GPW, false, PACKED, 2>(a, 1, st, what);
 }
 
 template <bool PACKED>
