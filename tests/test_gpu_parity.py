@@ -319,6 +319,20 @@ def test_paged_attention_long_context():
     assert_close_bf16(got, want, max_abs=2e-2, min_cos=0.9995, what="attention L=262144")
 
 
+def test_paged_attention_merge_paths_are_per_sequence():
+    """A sequence's result does not depend on whether another sequence of the batch is long
+    enough (> 32 chunks) to need the merge kernel: the merge path follows each sequence's own
+    length."""
+    lens = [5000, 60000, 300]  # 60,000 keys = 40 chunks of 1,536
+    q, pool, table = _pool(lens, seed=43)
+    batched = _attn(q, pool, table, lens)
+    for b in (0, 2):
+        solo = _attn(q[b:b + 1], pool, table[b:b + 1], lens[b:b + 1])
+        assert np.array_equal(solo[0], batched[b]), b
+    want = oracle.paged_decode_attn(q, pool, table, lens, 128 ** -0.5)
+    assert_close_bf16(batched, want, what="mixed merge paths")
+
+
 def test_paged_attention_one_key_is_its_value():
     q, pool, table = _pool([1, 1], seed=31)
     got = _attn(q, pool, table, [1, 1])
