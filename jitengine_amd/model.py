@@ -133,8 +133,7 @@ class DecoderLayer:
         logits = ops.qmm(hn, moe.router)
         inds, scores = ops.router_topk(logits, moe.top_k, moe.norm_topk)
         pk = ops.moe_pack(inds, moe.num_experts)
-        hh = ops.expert_gate_up(hn, moe.gate_up, pk)
-        r = ops.expert_down(hh, moe.down, pk)
+        hh, r = moe.expert_mlp(hn, pk)
         if next_norm is None:
             y, xn_next = ops.moe_combine(r, pk, scores, h), None
         else:

@@ -43,18 +43,23 @@ class MoEBlock:
 
     def use_seg(self, P: int, prefill: bool) -> bool:
         """Whether a prefill batch of P pairs takes the segment GEMM: at least 4 pairs per expert
-        on average (the reference's switch, Q36/model/moe.py:161-175) on packed stacks.  Decode
+        on average (the reference's switch, Q36/model/moe.py:161-175) on prepacked stacks.  Decode
         steps always take the decode kernels, as the reference's decode path does."""
-        return prefill and isinstance(self.gate_up, ops.PackedQ4) and P >= 16 and P // self.num_experts >= 4
+        packed = isinstance(self.gate_up, ops.PackedQ4) and isinstance(self.down, ops.PackedQ4)
+        return prefill and packed and P >= 16 and P // self.num_experts >= 4
 
     def experts(self, x: torch.Tensor, inds: torch.Tensor, scores: torch.Tensor,
                 resid: torch.Tensor | None = None, prefill: bool = False) -> torch.Tensor:
         """Every selected expert applied and combined: y [B, D] (+ resid)."""
         pk = ops.moe_pack(inds, self.num_experts)
+        _, r = self.expert_mlp(x, pk, prefill)
+        return ops.moe_combine(r, pk, scores, resid)
+
+    def expert_mlp(self, x: torch.Tensor, pk: ops.Packing, prefill: bool = False):
+        """(h [P, I], r [P, D]) in sorted pair order: gate||up + SwiGLU and down over packed pairs."""
         seg = self.use_seg(pk.P, prefill)
         h = ops.expert_gate_up(x, self.gate_up, pk, seg=seg)
-        r = ops.expert_down(h, self.down, pk, seg=seg)
-        return ops.moe_combine(r, pk, scores, resid)
+        return h, ops.expert_down(h, self.down, pk, seg=seg)
 
     def __call__(self, x: torch.Tensor, resid: torch.Tensor | None = None, prefill: bool = False) -> torch.Tensor:
         inds, scores = self.route(x)
