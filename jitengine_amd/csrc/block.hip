@@ -38,6 +38,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
   float ss = 0.0f;
   const int n = threadIdx.x * 8;
   const bool on = n < D;
+  // the norm weights are requested with the row (a load after the barrier would add a
+  // memory round trip to the kernel's critical path)
+  const uint4 wq = on ? *(const uint4 *)(w + n) : make_uint4(0u, 0u, 0u, 0u);
   if (on) {
     const uint4 a = *(const uint4 *)(x + row * D + n);
     const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
@@ -63,7 +66,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
   const float tot = block_sum_256(ss, red);
   const float r = rsqrtf(tot / (float)D + eps);
   if (on) {
-    const uint4 wq = *(const uint4 *)(w + n);
     const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
     float o[8];
 #pragma unroll
@@ -90,6 +92,7 @@ __device__ __forceinline__ void combine8(const uint16_t *__restrict__ r, const i
 #pragma clang fp contract(off)
 #pragma unroll
   for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+  const uint4 res = resid ? *(const uint4 *)(resid + bt * D + n) : make_uint4(0u, 0u, 0u, 0u);
   for (int j0 = 0; j0 < k; j0 += 8) {
     uint4 rv[8];
     float sc[8];
@@ -115,8 +118,7 @@ __device__ __forceinline__ void combine8(const uint16_t *__restrict__ r, const i
     }
   }
   if (resid) {
-    const uint4 rv = *(const uint4 *)(resid + bt * D + n);
-    const uint32_t wds[4] = {rv.x, rv.y, rv.z, rv.w};
+    const uint32_t wds[4] = {res.x, res.y, res.z, res.w};
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const float rr = (i & 1) ? bf2f_hi(wds[i >> 1]) : bf2f(wds[i >> 1] & 0xffffu);
@@ -159,6 +161,7 @@ __global__ __launch_bounds__(256) void combine_rmsnorm_kernel(
   const long long bt = blockIdx.x;
   const int n = threadIdx.x * 8;
   const bool on = n < D;
+  const uint4 wq = on ? *(const uint4 *)(w + n) : make_uint4(0u, 0u, 0u, 0u);  // requested up front
   float v[8];
   float ss = 0.0f;
   if (on) {
@@ -170,7 +173,6 @@ __global__ __launch_bounds__(256) void combine_rmsnorm_kernel(
   const float tot = block_sum_256(ss, red);
   const float rs = rsqrtf(tot / (float)D + eps);
   if (on) {
-    const uint4 wq = *(const uint4 *)(w + n);
     const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
     float o[8];
 #pragma unroll
