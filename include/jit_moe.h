@@ -260,6 +260,24 @@ int jit_paged_decode_attn(const uint16_t *q, const uint16_t *pool, const int32_t
                           const int32_t *chunk_seq, int B, int H, int Hkv, float scale,
                           int total_chunks, void *workspace, uint16_t *out, void *stream);
 
+/* Causal attention of prefill chunks over the paged pool: the other half of a
+ * chunked-prefill step (mx.fast.scaled_dot_product_attention with mask = "causal"
+ * over the slot's keys, Q36/model/attention.py:70-74, after the chunk's KV append).
+ * Chunk c owns q rows chunk_row[c] .. + chunk_len[c] - 1 of q [T, H, 128] (normed,
+ * rotated); its token t sits at position chunk_ctx[c] + t of sequence chunk_seq[c]
+ * and attends keys 0 .. chunk_ctx[c] + t (the pool must hold them: the chunk's own
+ * keys appended).  Work items: nblk (chunk, first token) pairs blk_chunk, blk_q0 of
+ * jit_prefill_block_tokens(H, Hkv) tokens each, covering every chunk (any order;
+ * longest first balances best).  out [T, H, 128] bf16; fp32 online softmax.
+ * Contract: H % Hkv == 0 (JIT_EINVAL), H / Hkv divides 16, max_pages <= 4096
+ * (JIT_EUNSUPPORTED). */
+int jit_prefill_block_tokens(int H, int Hkv);
+int jit_paged_prefill_attn(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,
+                           int max_pages, const int32_t *chunk_seq, const int32_t *chunk_ctx,
+                           const int32_t *chunk_len, const int32_t *chunk_row, int C,
+                           const int32_t *blk_chunk, const int32_t *blk_q0, int nblk, int H, int Hkv,
+                           float scale, uint16_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -391,7 +391,228 @@ __global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restri
   *(uint2 *)(out + ((long long)b * H + h) * kD + 4 * t) = w;
 }
 
+// ---------------------------------------------------------------- prefill (causal chunks)
+// Causal attention of prefill chunks over the paged pool: query token t of a chunk (at
+// position ctx + t of its sequence) attends keys 0 .. ctx + t, whose K/V the chunk's
+// append already wrote (mx.fast.scaled_dot_product_attention with mask = "causal" over the
+// slot's keys, Q36/model/attention.py:70-74).  A workgroup owns kPfWaves * kPfTiles 16-row
+// q tiles of one kv head -- a tile's rows are 16 / G tokens x the G q heads that share the
+// kv head -- and streams the keys up to its last token in 32-key steps through LDS, so each
+// K/V byte it reads serves all its tokens; per step and tile the arithmetic is the decode
+// kernel's (S^T = K . Q^T, online softmax in the exp2 domain, O^T += V^T . P^T), with keys
+// past a row's position masked.  A token's result depends only on its q row and its keys:
+// the steps and their order are the same wherever the token's tile sits.
+constexpr int kPfWaves = 4, kPfTiles = 2;
+constexpr int kPfMaxPages = 4096;  // page ids of a workgroup's keys, held in LDS
+
+struct PrefillArgs {
+  const uint16_t *q;          // [T, H, 128] bf16 (normed, rotated)
+  const uint16_t *pool;
+  const int32_t *page_table;  // [S, max_pages]
+  const int32_t *blk_chunk;   // [nblk] chunk of each workgroup
+  const int32_t *blk_q0;      // [nblk] first token (within the chunk) of each workgroup
+  const int32_t *chunk_seq, *chunk_ctx, *chunk_len, *chunk_row;  // [C]
+  uint16_t *out;              // [T, H, 128] bf16
+  int max_pages, H, Hkv, G;
+  float qk_scale;             // scale * log2(e)
+};
+
+__global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t kvs[4 * kPageHead];  // K0, V0, K1, V1 of a step
+  __shared__ int pgs[kPfMaxPages];
+  const int ch = a.blk_chunk[blockIdx.x], q0 = a.blk_q0[blockIdx.x];
+  const int kvh = blockIdx.y;
+  const int seq = a.chunk_seq[ch], ctx = a.chunk_ctx[ch], len = a.chunk_len[ch], row0 = a.chunk_row[ch];
+  const int G = a.G, TR = 16 / G, tpw = kPfTiles * TR;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = lane_id();
+  const int lr = l & 15, lg = l >> 4;
+  const int tlast = min(q0 + kPfWaves * tpw, len) - 1;  // the workgroup's last token
+  const int kend = ctx + tlast + 1;                     // its keys: [0, kend)
+  const int nst = (kend + 31) >> 5, npages = (kend + 15) >> 4;
+  for (int i = tid; i < npages; i += 64 * kPfWaves) pgs[i] = a.page_table[(long long)seq * a.max_pages + i];
+
+  // the lane's q row in tile j: token t (clamped into the chunk), head kvh * G + lr % G
+  int tok[kPfTiles];
+  bool store[kPfTiles];
+  Frag8 qf[kPfTiles][4];
+  float m_run[kPfTiles], l_run[kPfTiles];
+  f32x4 o[kPfTiles][8];
+#pragma unroll
+  for (int j = 0; j < kPfTiles; j++) {
+    const int t = q0 + wave * tpw + j * TR + lr / G;
+    store[j] = t < len;
+    tok[j] = min(t, len - 1);
+    const uint16_t *qp = a.q + ((long long)(row0 + tok[j]) * a.H + kvh * G + lr % G) * kD + 8 * lg;
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) qf[j][cc].q = *(const uint4 *)(qp + 32 * cc);
+    m_run[j] = -INFINITY;
+    l_run[j] = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) o[j][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // the last position among each tile's rows (uniform over the wave)
+  int tile_last[kPfTiles];
+#pragma unroll
+  for (int j = 0; j < kPfTiles; j++) tile_last[j] = ctx + min(q0 + wave * tpw + j * TR + TR - 1, len - 1);
+  __syncthreads();
+
+  // staging of step st: thread tid moves 16 B piece tid of each of the four 4 KB parts
+  // (u = 0..3: K of page 2st, V of page 2st, K of page 2st + 1, V of page 2st + 1; a page
+  // past the keys repeats the last one, whose slots are masked)
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 arrays land in scratch)
+  u32x4 stg[4];
+#define PF_FETCH(st)                                                                                   \
+  _Pragma("unroll") for (int u = 0; u < 4; u++) {                                                      \
+    const int pg = pgs[min(2 * (st) + (u >> 1), npages - 1)];                                          \
+    stg[u] = *(const u32x4 *)(head_part(a.pool, pg, a.Hkv, kvh) + (u & 1) * kPageHead + 8 * tid);      \
+  }
+  PF_FETCH(0);
+  for (int st = 0; st < nst; st++) {
+    __syncthreads();  // the previous step's LDS reads are done
+#pragma unroll
+    for (int u = 0; u < 4; u++) *(u32x4 *)(kvs + u * kPageHead + 8 * tid) = stg[u];
+    __syncthreads();
+    if (st + 1 < nst) {  // in flight during this step's math
+      PF_FETCH(st + 1);
+    }
+    const int k0 = 32 * st;
+    // phase 1: scores and softmax of every tile from the K fragments
+    uint32_t pw[kPfTiles][4];  // P^T fragments (bf16 pairs)
+    float alpha[kPfTiles];
+    {
+      Frag8 kf[2][4];
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++)
+          kf[t][cc].q = *(const uint4 *)(kvs + 2 * t * kPageHead + cc * (kPage * 32) + lr * 32 + 8 * lg);
+#pragma unroll
+      for (int j = 0; j < kPfTiles; j++) {
+        alpha[j] = 1.0f;
+        pw[j][0] = pw[j][1] = pw[j][2] = pw[j][3] = 0u;
+        if (k0 > tile_last[j]) continue;  // every key of the step is past the tile's rows
+        f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) {
+          s0 = mfma16x16x32(kf[0][cc], qf[j][cc], s0);
+          s1 = mfma16x16x32(kf[1][cc], qf[j][cc], s1);
+        }
+        const int pos = ctx + tok[j];
+        float p0[4], p1[4], tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int key = k0 + 4 * lg + i;
+          p0[i] = key <= pos ? s0[i] * a.qk_scale : -INFINITY;
+          p1[i] = key + 16 <= pos ? s1[i] * a.qk_scale : -INFINITY;
+          tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
+        }
+        tmax = max_xor32(max_xor16(tmax));
+        const float m_new = fmaxf(m_run[j], tmax);  // finite: key 0 is in every row's first step
+        alpha[j] = exp2f(m_run[j] - m_new);
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          p0[i] = exp2f(p0[i] - m_new);
+          p1[i] = exp2f(p1[i] - m_new);
+          psum += p0[i] + p1[i];
+        }
+        l_run[j] = l_run[j] * alpha[j] + psum;
+        m_run[j] = m_new;
+        pw[j][0] = pack_bf16x2(p0[0], p0[1]);
+        pw[j][1] = pack_bf16x2(p0[2], p0[3]);
+        pw[j][2] = pack_bf16x2(p1[0], p1[1]);
+        pw[j][3] = pack_bf16x2(p1[2], p1[3]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the V fragments are read after the K fragments are dead
+    // phase 2: O^T += V^T . P^T for every tile from the V fragments
+    uint2 vv[2][8];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++)
+        vv[t][cc] = *(const uint2 *)(kvs + (2 * t + 1) * kPageHead + (16 * cc + lr) * kPage + 4 * lg);
+    if (k0 + 32 > kend) {  // slots past the keys may hold stale bits: their V is made 0
+      const int kb = k0 + 4 * lg;
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++) {
+        vv[0][cc].x = mask_pair(vv[0][cc].x, kb, kend);
+        vv[0][cc].y = mask_pair(vv[0][cc].y, kb + 2, kend);
+        vv[1][cc].x = mask_pair(vv[1][cc].x, kb + 16, kend);
+        vv[1][cc].y = mask_pair(vv[1][cc].y, kb + 18, kend);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kPfTiles; j++) {
+      if (k0 > tile_last[j]) continue;
+      if (__any(alpha[j] != 1.0f)) {
+#pragma unroll
+        for (int cc = 0; cc < 8; cc++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) o[j][cc][i] *= alpha[j];
+      }
+      Frag8 pf;
+#pragma unroll
+      for (int i = 0; i < 4; i++) pf.u[i] = pw[j][i];
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++) {
+        Frag8 vf;
+        vf.u[0] = vv[0][cc].x;
+        vf.u[1] = vv[0][cc].y;
+        vf.u[2] = vv[1][cc].x;
+        vf.u[3] = vv[1][cc].y;
+        o[j][cc] = mfma16x16x32(vf, pf, o[j][cc]);
+      }
+    }
+  }
+#undef PF_FETCH
+#pragma unroll
+  for (int j = 0; j < kPfTiles; j++) {
+    const float l_tot = sum_xor32(sum_xor16(l_run[j]));
+    if (!store[j]) continue;
+    const float inv = 1.0f / l_tot;
+    uint16_t *op = a.out + ((long long)(row0 + tok[j]) * a.H + kvh * G + lr % G) * kD + 4 * lg;
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) {
+      uint2 w;
+      w.x = pack_bf16x2(o[j][cc][0] * inv, o[j][cc][1] * inv);
+      w.y = pack_bf16x2(o[j][cc][2] * inv, o[j][cc][3] * inv);
+      *(uint2 *)(op + 16 * cc) = w;
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int jit_prefill_block_tokens(int H, int Hkv) {
+  if (H <= 0 || Hkv <= 0 || H % Hkv != 0 || 16 % (H / Hkv) != 0) return -1;
+  return kPfWaves * kPfTiles * 16 / (H / Hkv);
+}
+
+extern "C" int jit_paged_prefill_attn(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,
+                                      int max_pages, const int32_t *chunk_seq, const int32_t *chunk_ctx,
+                                      const int32_t *chunk_len, const int32_t *chunk_row, int C,
+                                      const int32_t *blk_chunk, const int32_t *blk_q0, int nblk, int H, int Hkv,
+                                      float scale, uint16_t *out, void *stream) {
+  if (C < 0 || nblk < 0 || H <= 0 || Hkv <= 0 || max_pages <= 0)
+    return jit::fail(JIT_EINVAL, "paged_prefill_attn: bad dims C=%d nblk=%d H=%d Hkv=%d", C, nblk, H, Hkv);
+  if (H % Hkv != 0) return jit::fail(JIT_EINVAL, "%d query heads do not share %d KV heads evenly", H, Hkv);
+  if (16 % (H / Hkv) != 0)
+    return jit::fail(JIT_EUNSUPPORTED, "paged_prefill_attn covers H / Hkv in {1, 2, 4, 8, 16}, got %d", H / Hkv);
+  if (max_pages > kPfMaxPages)
+    return jit::fail(JIT_EUNSUPPORTED, "paged_prefill_attn covers max_pages <= %d (keys <= %d), got %d",
+                     kPfMaxPages, kPfMaxPages * kPage, max_pages);
+  if (C == 0 || nblk == 0) return JIT_OK;
+  if (!q || !pool || !page_table || !chunk_seq || !chunk_ctx || !chunk_len || !chunk_row || !blk_chunk ||
+      !blk_q0 || !out)
+    return jit::fail(JIT_EINVAL, "paged_prefill_attn: null pointer");
+  const PrefillArgs a{q, pool, page_table, blk_chunk, blk_q0, chunk_seq, chunk_ctx, chunk_len, chunk_row, out,
+                      max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f};
+  prefill_attn_kernel<<<dim3(nblk, Hkv), 64 * kPfWaves, 0, (hipStream_t)stream>>>(a);
+  return jit::check_launch("jit_paged_prefill_attn");
+}
+
+
 
 extern "C" int jit_kv_append_paged(const uint16_t *k, const uint16_t *v, int B, int Hkv,
                                    const int32_t *pos, const int32_t *page_table, int max_pages,

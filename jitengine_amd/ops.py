@@ -425,6 +425,65 @@ def attn_workspace_bytes(total_chunks: int, H: int) -> int:
     return int(_lib.lib().jit_attn_workspace_bytes(int(total_chunks), int(H)))
 
 
+@dataclass
+class PrefillPlan:
+    """Chunks (seq, ctx, length) of a prefill step in q-row order and their work items for
+    jit_paged_prefill_attn (device int32 tables, built once on the host)."""
+
+    chunks: list
+    tables: torch.Tensor  # [4, C] chunk_seq, chunk_ctx, chunk_len, chunk_row
+    blocks: torch.Tensor  # [2, nblk] blk_chunk, blk_q0
+    rows: int
+
+
+def prefill_plan(chunks, H: int, Hkv: int, device) -> PrefillPlan:
+    """Plan of causal prefill attention over chunks [(seq, ctx, length), ...]: every chunk cut
+    into work items of jit_prefill_block_tokens tokens, the items with the most keys first."""
+    bt = int(_lib.lib().jit_prefill_block_tokens(H, Hkv))
+    if bt <= 0:
+        raise _lib.UnsupportedShape(f"prefill attention covers H / Hkv in (1, 2, 4, 8, 16), got {H}/{Hkv}")
+    rows, tab, items = 0, [], []
+    for c, (seq, ctx, length) in enumerate(chunks):
+        if seq < 0 or ctx < 0 or length < 1:
+            raise ValueError(f"chunk {c}: seq {seq}, ctx {ctx}, length {length}")
+        tab.append((seq, ctx, length, rows))
+        rows += length
+        items += [(ctx + min(q0 + bt, length), c, q0) for q0 in range(0, length, bt)]
+    items.sort(key=lambda it: -it[0])
+    tables = torch.tensor(np.array(tab, np.int32).T.copy() if tab else np.zeros((4, 0), np.int32), device=device)
+    blocks = torch.tensor(np.array([(c, q0) for _, c, q0 in items], np.int32).T.copy() if items
+                          else np.zeros((2, 0), np.int32), device=device)
+    return PrefillPlan(list(chunks), tables.contiguous(), blocks.contiguous(), rows)
+
+
+def paged_prefill_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor, plan: PrefillPlan,
+                            scale: float) -> torch.Tensor:
+    """q [T, H, 128] bf16 (the plan's chunk rows) -> out [T, H, 128]: causal attention of each chunk
+    token over its sequence's keys up to its own position (jit_paged_prefill_attn)."""
+    _need(q, torch.bfloat16, "q")
+    _need(pool, torch.bfloat16, "pool")
+    _need(page_table, torch.int32, "page_table")
+    T, H, Dh = q.shape
+    Hkv = _pool_heads(pool)
+    if Dh != HEAD_DIM:
+        raise _lib.UnsupportedShape(f"paged_prefill_attention covers head_dim 128, got {Dh}")
+    if T != plan.rows:
+        raise ValueError(f"q has {T} rows, the plan's chunks {plan.rows}")
+    for seq, ctx, length in plan.chunks:
+        if seq >= page_table.shape[0] or (ctx + length + PAGE - 1) // PAGE > page_table.shape[1]:
+            raise ValueError(f"chunk ({seq}, {ctx}, {length}) is outside page_table {tuple(page_table.shape)}")
+    out = torch.empty_like(q)
+    tb, bl = plan.tables, plan.blocks
+    _lib.check(
+        _lib.lib().jit_paged_prefill_attn(
+            _p(q), _p(pool), _p(page_table), page_table.shape[1], _p(tb[0]), _p(tb[1]), _p(tb[2]), _p(tb[3]),
+            tb.shape[1], _p(bl[0]), _p(bl[1]), bl.shape[1], H, Hkv, float(scale), _p(out), _stream(),
+        ),
+        "paged_prefill_attn",
+    )
+    return out
+
+
 def paged_decode_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor,
                            plan: AttnPlan, scale: float, workspace: torch.Tensor | None = None):
     """q [B, H, 128] bf16 -> out [B, H, 128] bf16 over each sequence's first lens[b] keys of the

@@ -343,6 +343,23 @@ def kv_gather(pool, page_row, n: int, Hkv: int, Dh: int):
     return kc, vc
 
 
+def paged_prefill_attn(q, pool, page_table, chunks, scale: float) -> np.ndarray:
+    """Causal attention of prefill chunks: q [T, H, Dh] bf16 holds the chunks' rows in order; chunk
+    (seq, ctx, length) owns the next `length` rows, and its token t (position ctx + t of sequence
+    seq) attends keys 0 .. ctx + t of page_table[seq] -- decode attention of that token over
+    ctx + t + 1 keys (the causal mask of mx.fast.scaled_dot_product_attention, aligned to the last
+    key), so this is paged_decode_attn row by row."""
+    pt = _i32(page_table)
+    lens, rows = [], []
+    for seq, ctx, length in chunks:
+        for t in range(length):
+            lens.append(ctx + t + 1)
+            rows.append(pt[seq])
+    if not lens:
+        return np.empty_like(_u16(q))
+    return paged_decode_attn(q, pool, np.stack(rows), np.array(lens, np.int32), scale)
+
+
 def paged_decode_attn(q, pool, page_table, lens, scale: float) -> np.ndarray:
     """q [B, H, Dh] bf16 -> out [B, H, Dh] bf16 (float64 softmax attention over lens[b] tokens)."""
     q, pool, pt, ln = _u16(q), _u16(pool), _i32(page_table), _i32(lens)

@@ -45,6 +45,13 @@ def test_contract_breaks_return_einval_before_launch():
     assert lib.jit_moe_down(None, 768 + 64, None, None, 8, None, None, None, 2048, 16, None, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_paged_decode_attn(None, None, None, 4, None, None, None, 2, 30, 4, 0.1, 4, None, None, None) == _lib.JIT_EINVAL
     assert lib.jit_paged_decode_attn(None, None, None, 4, None, None, None, 2, 64, 2, 0.1, 4, None, None, None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_prefill_block_tokens(32, 4) == 16 and lib.jit_prefill_block_tokens(24, 8) == -1
+    assert lib.jit_paged_prefill_attn(*([None] * 3), 16, *([None] * 4), 1, None, None, 1, 32, 3, 0.1, None,
+                                      None) == _lib.JIT_EINVAL
+    assert lib.jit_paged_prefill_attn(*([None] * 3), 16, *([None] * 4), 1, None, None, 1, 24, 8, 0.1, None,
+                                      None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_paged_prefill_attn(*([None] * 3), 5000, *([None] * 4), 1, None, None, 1, 32, 4, 0.1, None,
+                                      None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_moe_combine_rmsnorm(None, None, None, 2, 8, 4096, None, None, None, 1e-6, None, None) == _lib.JIT_EUNSUPPORTED
     # empty work is a no-op, not an error
     assert lib.jit_router_topk(None, 0, 128, 8, 1, None, None, None, None) == _lib.JIT_OK

@@ -1,0 +1,117 @@
+"""Causal attention of prefill chunks over the paged pool vs the CPU oracle (MI355X only).
+
+The oracle states the causal mask as what it is: chunk token t at position ctx + t attends the
+first ctx + t + 1 keys of its sequence, i.e. the float64 decode attention of that token over
+ctx + t + 1 keys (oracle.paged_prefill_attn).  The bar is the north-star float tolerance; the
+invariants below are bit-exact."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from jitengine_amd import ops
+from tests.helpers import assert_close_bf16, bf16_tensor, normal_bf16, u16
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SCALE = 128 ** -0.5
+
+
+def _pool(seq_keys, seed, Hkv=4, extra=7):
+    """A pool holding each sequence's keys in permuted pages; table [S, max_pages]."""
+    rng = np.random.default_rng(seed)
+    npg = [-(-n // 16) for n in seq_keys]
+    total = sum(npg) + extra
+    perm = rng.permutation(total)
+    table = np.zeros((len(seq_keys), max(npg)), np.int32)
+    at = 0
+    for i, n in enumerate(npg):
+        table[i, :n] = perm[at:at + n]
+        at += n
+    pool = normal_bf16((total, Hkv, 2, 16 * 128), seed=seed + 1)
+    return pool, table
+
+
+def _run(q, pool, table, chunks, H=32, Hkv=4):
+    plan = ops.prefill_plan(chunks, H, Hkv, DEV)
+    out = ops.paged_prefill_attention(bf16_tensor(q, DEV), bf16_tensor(pool, DEV),
+                                      torch.from_numpy(table).to(DEV), plan, SCALE)
+    return u16(out)
+
+
+@pytest.mark.parametrize("H,Hkv", [(32, 4), (16, 1), (8, 8)])
+def test_prefill_attention_parity(H, Hkv):
+    # chunks: from position 0, a context ending mid-page, one token, a long context, a chunk
+    # whose keys end exactly on a 32-key step
+    chunks = [(0, 0, 37), (1, 100, 64), (2, 1500, 1), (3, 4093, 70), (4, 16, 16)]
+    keys = [ctx + n for _, ctx, n in chunks]
+    pool, table = _pool(keys, seed=H + Hkv, Hkv=Hkv)
+    T = sum(n for *_, n in chunks)
+    q = normal_bf16((T, H, 128), seed=5)
+    got = _run(q, pool, table, chunks, H, Hkv)
+    want = oracle.paged_prefill_attn(q, pool, table, chunks, SCALE)
+    assert_close_bf16(got, want, what=f"prefill H={H} Hkv={Hkv}")
+
+
+def test_prefill_token_result_is_independent_of_the_chunking():
+    """A token's bits depend only on its q row and its keys: the same 90 positions prefilled as
+    one chunk, as two chunks, or decoded row by row through prefill chunks of one token agree."""
+    pool, table = _pool([300], seed=11)
+    q = normal_bf16((90, 32, 128), seed=12)
+    whole = _run(q, pool, table, [(0, 210, 90)])
+    split = _run(q, pool, table, [(0, 210, 41), (0, 251, 49)])
+    assert np.array_equal(whole, split)
+    single = _run(q[57:58], pool, table, [(0, 267, 1)])
+    assert np.array_equal(single[0], whole[57])
+
+
+def test_prefill_one_token_matches_decode_attention():
+    """A one-token chunk at position p is decode attention over p + 1 keys (both within the
+    tolerance of the same oracle row, and close to each other)."""
+    pool, table = _pool([2000], seed=21)
+    q = normal_bf16((1, 32, 128), seed=22)
+    pre = _run(q, pool, table, [(0, 1799, 1)])
+    plan = ops.attn_plan([1800], DEV)
+    dec = u16(ops.paged_decode_attention(bf16_tensor(q, DEV), bf16_tensor(pool, DEV),
+                                         torch.from_numpy(table).to(DEV), plan, SCALE))
+    want = oracle.paged_decode_attn(q, pool, table, [1800], SCALE)
+    assert_close_bf16(pre, want, what="prefill one token")
+    assert_close_bf16(pre, dec, what="prefill vs decode")
+
+
+def test_prefill_page_permutation_and_stale_slots():
+    """Moving the pages leaves the bits unchanged, and NaN bits in slots past the last key (a
+    page's unwritten tail) do not reach the output."""
+    chunks = [(0, 5, 23), (1, 700, 9)]
+    pool, table = _pool([28, 709], seed=31)
+    q = normal_bf16((32, 32, 128), seed=32)
+    base = _run(q, pool, table, chunks)
+    poisoned = pool.copy()
+    for seq, n in ((0, 28), (1, 709)):  # slots n % 16 .. 15 of the last page (K chunk-major, V dim-major)
+        pg = table[seq, (n - 1) // 16]
+        k = poisoned[pg, :, 0].reshape(4, 4, 16, 32)
+        k[:, :, n % 16:, :] = 0x7FC0
+        v = poisoned[pg, :, 1].reshape(4, 128, 16)
+        v[:, :, n % 16:] = 0x7FC0
+    assert np.array_equal(_run(q, poisoned, table, chunks), base)
+    perm = np.random.default_rng(33).permutation(pool.shape[0])
+    pool2 = np.empty_like(pool)
+    pool2[perm] = pool
+    assert np.array_equal(_run(q, pool2, perm[table].astype(np.int32), chunks), base)
+
+
+def test_prefill_config3_chunks():
+    """BASELINE config 3's prefill half: 4 chunks of 512 tokens after contexts up to 8,192."""
+    rng = np.random.default_rng(0x4A450030)
+    ctx = rng.integers(0, 8193, 4)
+    chunks = [(i, int(c), 512) for i, c in enumerate(ctx)]
+    pool, table = _pool([int(c) + 512 for c in ctx], seed=41)
+    q = normal_bf16((2048, 32, 128), seed=42)
+    got = _run(q, pool, table, chunks)
+    sel = np.r_[0:40, 500:560, 1024:1030, 2000:2048]  # rows across every chunk (the oracle is O(T.L))
+    lens = np.array([int(ctx[r // 512]) + r % 512 + 1 for r in sel], np.int32)
+    want = oracle.paged_decode_attn(q[sel], pool, table[sel // 512], lens, SCALE)
+    assert_close_bf16(got[sel], want, what="config 3 prefill")
