@@ -6,7 +6,9 @@ config 2 (the default; BASELINE.json configs[2], the workload the metric is quot
 continuous-batch decode of 32 sequences over the paged KV pool through 48 layers of the 4-bit
 Qwen3-MoE-style block; a step decodes one token per sequence (value = tokens/s).  The step is
 captured once as a HIP graph and replayed (--no-graph times eager launches).
-config 3 (the expert half of BASELINE.json configs[3]): 2,108 rows on the segment GEMM (MFMA roofline).
+config 3: one mixed chunked-prefill + decode step of one block -- 4 x 512
+prefill tokens (causal attention over their contexts) + 60 decode rows, the MoE on the segment GEMM
+(value = rows/s; MFMA roofline of the dominant kernel).
 config 1: one standalone quantized-MoE call -- 64 tokens, top-8 of 128
 experts drawn from softmax of N(0,1) logits, gate/up [768 x 2048] and down [2048 x 768] per expert
 (4-bit g64, N(0, 0.02) weights); a step = packing + gate||up/SwiGLU + down + combine.
@@ -187,98 +189,159 @@ def bench_config1(steps: int, warmup: int, dev: str) -> dict:
 
 
 def bench_config3(steps: int, warmup: int, dev: str) -> dict:
-    """The expert half of BASELINE configs[3], the mixed chunked-prefill + decode step: 4 prefill
-    chunks of 512 tokens plus 60 decode rows = 2,108 rows routed top-8 over 128 experts (router
-    logits N(0,1)), ~132 pairs per expert, on the segment GEMM (row a9: MFMA tiles over long expert
-    segments).  A step = packing + gate||up/SwiGLU + down + combine; the roofline is the MFMA one
-    (bf16 dense peak), flops = 2 * P * (2I * D + D * I)."""
+    """one mixed chunked-prefill + decode step of one decoder block -- 4
+    prefill chunks of 512 tokens after prior contexts U{0..8192} plus 60 decode sequences with
+    lengths log-uniform in [256, 16384], 2,108 rows in all (DecoderLayer.mixed: qkv, norms and
+    RoPE with the KV append of every row, causal prefill attention and split-K decode attention,
+    o_proj, router, top-k, packing, the segment GEMM experts (~132 pairs per expert), combine).
+    value = rows / step time; the roofline is the MFMA one of the dominant kernel."""
     import oracle
     from jitengine_amd import ops
+    from jitengine_amd.model import DecoderLayer, MoEConfig, make_mixed_state, random_layer_weights, rope_inv_freq
 
-    B, E, D, I, k = 4 * 512 + 60, 128, 2048, 768, 8
+    cfg = MoEConfig(layers=1)
     seed = seed_for(3)
     rng = np.random.default_rng(seed)
-    gu_mlx = gen_stack((E, 2 * I, D), seed + 1, dev)
-    dn_mlx = gen_stack((E, D, I), seed + 2, dev)
-    gu, dn = ops.prepack(gu_mlx), ops.prepack(dn_mlx)
-    logits = oracle.f32_to_bf16(rng.standard_normal((B, E)).astype(np.float32))
-    x_np = oracle.f32_to_bf16(rng.standard_normal((B, D)).astype(np.float32))
-    to_dev = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(dev)  # noqa: E731
-    x = to_dev(x_np)
-    inds, scores = ops.router_topk(to_dev(logits), k, True)
+    ctx = rng.integers(0, 8193, 4)
+    dec_len = np.round(np.exp(rng.uniform(np.log(256), np.log(16384), 60))).astype(np.int32)
+    chunks = [(i, int(c), 512) for i, c in enumerate(ctx)]
+    keys = [int(c) + 512 for c in ctx] + [int(L) + 1 for L in dec_len]  # decode row b writes position L_b
+    npg = [-(-n // 16) for n in keys]
+    perm = rng.permutation(sum(npg))
+    table = np.zeros((len(keys), max(npg)), np.int32)
+    at = 0
+    for i, n in enumerate(npg):
+        table[i, :n] = perm[at:at + n]
+        at += n
+    w = random_layer_weights(cfg, seed * 100, dev)
+    layer = DecoderLayer(cfg, w)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed + 7)
+    pool = torch.randn((sum(npg), cfg.kv_heads, 2, 16 * 128), generator=gen, device=dev, dtype=torch.bfloat16)
+    ms = make_mixed_state(cfg, chunks, table[:4], dec_len, table[4:], dev)
+    T = ms.P + len(dec_len)
+    x = torch.randn((T, cfg.hidden), generator=gen, device=dev, dtype=torch.bfloat16)
+    dbg = {}
+    layer.mixed(x, pool, ms, debug=dbg)
     torch.cuda.synchronize()
 
     def step():
-        pk = ops.moe_pack(inds, E)
-        h = ops.expert_gate_up(x, gu, pk, seg=True)
-        r = ops.expert_down(h, dn, pk, seg=True)
-        return ops.moe_combine(r, pk, scores)
+        return layer.mixed(x, pool, ms)
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = step()
+    g.replay()
+    torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for _ in range(steps):
-        y = step()
+        g.replay()
     t1.record()
     torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / steps
-    pk = ops.moe_pack(inds, E)
-    h = ops.expert_gate_up(x, gu, pk, seg=True)
-    r = ops.expert_down(h, dn, pk, seg=True)
-    kus = time_ops({"moe_pack": [lambda: ops.moe_pack(inds, E)],
-                    "gate_up_swiglu_seg": [lambda: ops.expert_gate_up(x, gu, pk, seg=True)],
-                    "down_seg": [lambda: ops.expert_down(h, dn, pk, seg=True)],
-                    "combine": [lambda: ops.moe_combine(r, pk, scores)]}, reps=max(steps, 5))
-    P = B * k
-    fl_gu, fl_dn = 2.0 * P * 2 * I * D, 2.0 * P * D * I
-    dom = "gate_up_swiglu_seg"
-    achieved = fl_gu / (kus[dom] * 1e-6) / 1e12
-    U = int(np.unique(inds.cpu().numpy()).size)
+    ms_step = t0.elapsed_time(t1) / steps
+    del g
 
-    # CPU baseline: the oracle's segment-GEMM arithmetic (bf16 weights, float64 sums) on 16 rows
+    # per-op device time on the step's own intermediates
+    scale = cfg.head_dim ** -0.5
+    moe, pk = layer.moe, dbg["pk"]
+    q = dbg["q"]
+    kus = time_ops({
+        "rmsnorm": [lambda: ops.rmsnorm(x, layer.input_norm, cfg.eps)],
+        "qkv_proj": [lambda: ops.qmm(dbg["xn"], layer.qkv)],
+        "qk_norm_rope_append": [lambda: ops.qk_norm_rope_append(
+            dbg["qkv"], cfg.heads, cfg.kv_heads, layer.q_norm, layer.k_norm, cfg.eps, layer.inv_freq, ms.pos_rows,
+            ms.table_rows, pool)],
+        "prefill_attention": [lambda: ops.paged_prefill_attention(q[:ms.P], pool, ms.seq_table, ms.prefill, scale)],
+        "decode_attention": [lambda: ops.paged_decode_attention(q[ms.P:], pool, ms.dec_table, ms.decode, scale,
+                                                                ms.workspace)],
+        "o_proj": [lambda: ops.qmm(dbg["attn"].view(T, -1), layer.o)],
+        "add_rmsnorm": [lambda: ops.rmsnorm(dbg["o"], layer.post_norm, cfg.eps, resid=x, return_sum=True)],
+        "router_proj": [lambda: ops.qmm(dbg["hn"], moe.router)],
+        "router_topk": [lambda: ops.router_topk(dbg["logits"], cfg.top_k, cfg.norm_topk)],
+        "moe_pack": [lambda: ops.moe_pack(dbg["inds"], cfg.experts)],
+        "gate_up_swiglu_seg": [lambda: ops.expert_gate_up(dbg["hn"], moe.gate_up, pk, seg=True)],
+        "down_seg": [lambda: ops.expert_down(dbg["hh"], moe.down, pk, seg=True)],
+        "combine": [lambda: ops.moe_combine(dbg["r"], pk, dbg["scores"], dbg["h"])],
+    }, reps=max(steps, 5))
+    D, I, E, H = cfg.hidden, cfg.inter, cfg.experts, cfg.heads
+    P = T * cfg.top_k
+    flops = {
+        "gate_up_swiglu_seg": 2.0 * P * 2 * I * D,
+        "down_seg": 2.0 * P * D * I,
+        "prefill_attention": float(sum(4.0 * H * 128 * (c + t + 1) for _, c, n in chunks for t in range(n))),
+        "qkv_proj": 2.0 * T * cfg.qkv_rows * D,
+        "o_proj": 2.0 * T * D * H * 128,
+    }
+    dom = max((k for k in kus if k in flops), key=kus.get)
+    achieved = flops[dom] / (kus[dom] * 1e-6) / 1e12
+    step_flops = sum(flops.values()) + 2.0 * T * E * D + float(sum(4.0 * H * 128 * (L + 1) for L in dec_len))
+
+    # CPU baseline: the oracle's block on a self-contained row sample -- the first 16 tokens of
+    # chunk 0 (their keys: chunk 0's context and themselves) and 16 decode rows
+    u16 = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)  # noqa: E731
+
+    def host_q(lin):
+        return (lin.weight.cpu().numpy().view(np.uint32), u16(lin.scales), u16(lin.biases))
+
+    lw = {k: (host_q(v) if k in ("qkv", "o", "router", "gate_up", "down") else u16(v)) for k, v in w.items()}
     nb = 16
-    ind_np = inds.cpu().numpy().view(np.uint32)[:nb]
-    sc_np = scores[:nb].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-
-    def host(q):
-        return (q.weight.cpu().numpy().view(np.uint32), q.scales.view(torch.int16).cpu().numpy().view(np.uint16),
-                q.biases.view(torch.int16).cpu().numpy().view(np.uint16))
-
-    gu_h, dn_h = host(gu_mlx), host(dn_mlx)
+    sel = np.r_[0:nb, ms.P:ms.P + nb]
+    xs = u16(x)[sel]
+    pos_s = np.concatenate([np.arange(ctx[0], ctx[0] + nb), dec_len[:nb]]).astype(np.int32)
+    rows_s = np.concatenate([np.repeat(table[:1], nb, 0), table[4:4 + nb]]).astype(np.int32)
+    pool_h = u16(pool)
+    inv_freq = rope_inv_freq(cfg.rope_theta, 128)
     oracle.set_num_threads(cpu_threads())
 
-    def cpu_chain():
-        opk = oracle.moe_pack(ind_np, E)
-        hh = oracle.moe_gate_up(x_np[:nb], ind_np, opk, *gu_h, bf16w=True)
-        rr = oracle.moe_down(hh, ind_np, opk, *dn_h, bf16w=True)
-        return oracle.moe_combine(rr, opk["inv"], sc_np)
+    def cpu_sample():
+        ph = pool_h.copy()
+        xn, _ = oracle.rmsnorm(xs, lw["input_norm"], cfg.eps)
+        _, qkv = oracle.qmm(xn, *lw["qkv"])
+        qh = oracle.qk_norm_rope_append(qkv, H, cfg.kv_heads, lw["q_norm"], lw["k_norm"], cfg.eps, inv_freq, pos_s,
+                                        ph, rows_s)
+        a_pre = oracle.paged_prefill_attn(qh[:nb], ph, table[:1], [(0, int(ctx[0]), nb)], scale)
+        a_dec = oracle.paged_decode_attn(qh[nb:], ph, table[4:4 + nb], dec_len[:nb] + 1, scale)
+        _, o = oracle.qmm(np.concatenate([a_pre, a_dec]).reshape(2 * nb, -1), *lw["o"])
+        hn, h = oracle.rmsnorm(o, lw["post_norm"], cfg.eps, resid=xs)
+        _, logits = oracle.qmm(hn, *lw["router"])
+        wi, ws, _ = oracle.router_topk(logits, cfg.top_k, True)
+        opk = oracle.moe_pack(wi, E)
+        hh = oracle.moe_gate_up(hn, wi, opk, *lw["gate_up"], bf16w=True)
+        rr = oracle.moe_down(hh, wi, opk, *lw["down"], bf16w=True)
+        return oracle.moe_combine(rr, opk["inv"], ws)
 
-    cpu_chain()
+    cpu_sample()
     times = []
     for _ in range(5):
         c0 = time.perf_counter()
-        cpu_chain()
+        cpu_sample()
         times.append(time.perf_counter() - c0)
-    cpu_tps = nb / float(np.median(times))
+    cpu_tps = 2 * nb / float(np.median(times))
+    U = int(torch.unique(dbg["inds"]).numel())
     return {
         "metric": "decode tok/s (bs=1, ragged bs=32) + achieved HBM GB/s as % of MI355X peak",
-        "value": B / (ms * 1e-3),
+        "value": T / (ms_step * 1e-3),
         "unit": "tokens/s",
-        "ms_per_step": ms,
-        "dtype": "bf16 activations and dequantized bf16 weights (4-bit g64 source), fp32 accumulate",
-        "config": {"workload": "config3 expert half: 2,108 rows (4 x 512 prefill + 60 decode) x top-8 of 128 experts "
-                               "on the segment GEMM, gate/up 768x2048, down 2048x768, 4-bit g64",
-                   "rows": B, "pairs": P, "experts": E, "distinct_experts": U,
-                   "max_pairs_per_expert": int(pk.meta[1])},
-        "step_tflops": (fl_gu + fl_dn) / (ms * 1e-3) / 1e12,
-        "kernels_us": kus,
+        "ms_per_step": ms_step,
+        "dtype": "bf16 activations, 4-bit g64 weights (bf16-dequantized on the segment GEMM), fp32 accumulate",
+        "config": {"workload": "config3: one mixed chunked-prefill + decode step of one block -- 4 x 512 prefill "
+                               "tokens after contexts U{0..8192} + 60 decode rows (lengths log-uniform [256, 16384])",
+                   "rows": T, "prefill_ctx": [int(c) for c in ctx], "decode_kv_tokens": int(dec_len.sum()) + 60,
+                   "pairs": P, "experts": E, "distinct_experts": U, "max_pairs_per_expert": int(pk.meta[1]),
+                   "hip_graph": True},
+        "step_tflops": step_flops / (ms_step * 1e-3) / 1e12,
+        "op_us": kus,
+        "op_us_sum_per_step": sum(kus.values()),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": achieved / 2500.0, "flops_per_launch": fl_gu, "traffic": None},
+                     "frac": achieved / 2500.0, "flops_per_launch": flops[dom], "traffic": None},
         "cpu_baseline": {"value": cpu_tps, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
-                         "sample": f"oracle segment-GEMM expert chain (bf16 weights, float64 sums) on {nb} of the "
-                                   f"{B} rows, median of 5 after a warm-up"},
+                         "sample": f"the oracle's block (dense, norms, RoPE + append, causal prefill and decode "
+                                   f"attention, router, segment-GEMM experts) on {2 * nb} of the {T} rows: the first "
+                                   f"{nb} tokens of chunk 0 and {nb} decode rows, median of 5 after a warm-up"},
         "_y": y,
     }
 
@@ -488,6 +551,7 @@ OP_KERNELS = {  # the kernels one op launches (rocprofv3 kernel names contain th
     "down": ["qmm_kernel<4, 4, false, true"],
     "gate_up_swiglu_seg": ["seg_kernel<true>"],
     "down_seg": ["seg_kernel<false>"],
+    "prefill_attention": ["prefill_attn_kernel"],
 }
 
 

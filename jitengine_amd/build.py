@@ -4,8 +4,9 @@ Every HIP translation unit is built with the packed-FP32 feature disabled (hipcc
 v_pk_{add,mul,fma}_f32 from ordinary float code otherwise).  router.hip is built with
 -ffp-contract=off: its softmax must reproduce the CPU restatement bit for bit.  qmm.hip is
 built with MFMA results in ordinary VGPRs (-amdgpu-mfma-vgpr-form) instead of accumulation
-registers, which removes a register copy per MFMA result from its inner loops; qmm_seg.hip is not
-(its accumulators live in accumulation registers).
+registers, which removes a register copy per MFMA result from its inner loops, and so is
+attention.hip (the prefill kernel's scores feed the softmax directly; the decode kernels compile to
+the same code either way); qmm_seg.hip is not (its accumulators live in accumulation registers).
 """
 
 from __future__ import annotations
@@ -29,7 +30,7 @@ SOURCES = {
     "router.hip": ["-ffp-contract=off"],
     "qmm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "qmm_seg.hip": [],
-    "attention.hip": [],
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "block.hip": [],
 }
 

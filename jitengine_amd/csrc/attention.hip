@@ -402,7 +402,8 @@ __global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restri
 // kernel's (S^T = K . Q^T, online softmax in the exp2 domain, O^T += V^T . P^T), with keys
 // past a row's position masked.  A token's result depends only on its q row and its keys:
 // the steps and their order are the same wherever the token's tile sits.
-constexpr int kPfWaves = 4, kPfTiles = 2;
+constexpr int kPfWaves = 8, kPfTiles = 2;
+constexpr int kPfPieces = 4 * kPageHead / 8 / (64 * kPfWaves);  // 16 B pieces of a step per thread
 constexpr int kPfMaxPages = 4096;  // page ids of a workgroup's keys, held in LDS
 
 struct PrefillArgs {
@@ -456,113 +457,121 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   for (int j = 0; j < kPfTiles; j++) tile_last[j] = ctx + min(q0 + wave * tpw + j * TR + TR - 1, len - 1);
   __syncthreads();
 
-  // staging of step st: thread tid moves 16 B piece tid of each of the four 4 KB parts
-  // (u = 0..3: K of page 2st, V of page 2st, K of page 2st + 1, V of page 2st + 1; a page
-  // past the keys repeats the last one, whose slots are masked)
+  // staging of step st: the step's four 4 KB parts (K of page 2st, V of page 2st, K of page
+  // 2st + 1, V of page 2st + 1; a page past the keys repeats the last one, whose slots are
+  // masked) in 16 B pieces, piece tid + u * threads for thread tid
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 arrays land in scratch)
-  u32x4 stg[4];
+  u32x4 stg[kPfPieces];
 #define PF_FETCH(st)                                                                                   \
-  _Pragma("unroll") for (int u = 0; u < 4; u++) {                                                      \
-    const int pg = pgs[min(2 * (st) + (u >> 1), npages - 1)];                                          \
-    stg[u] = *(const u32x4 *)(head_part(a.pool, pg, a.Hkv, kvh) + (u & 1) * kPageHead + 8 * tid);      \
+  _Pragma("unroll") for (int u = 0; u < kPfPieces; u++) {                                              \
+    const int pc = tid + u * 64 * kPfWaves, part = pc >> 8;                                            \
+    const int pg = pgs[min(2 * (st) + (part >> 1), npages - 1)];                                       \
+    stg[u] = *(const u32x4 *)(head_part(a.pool, pg, a.Hkv, kvh) + (part & 1) * kPageHead + 8 * (pc & 255)); \
   }
   PF_FETCH(0);
   for (int st = 0; st < nst; st++) {
     __syncthreads();  // the previous step's LDS reads are done
 #pragma unroll
-    for (int u = 0; u < 4; u++) *(u32x4 *)(kvs + u * kPageHead + 8 * tid) = stg[u];
+    for (int u = 0; u < kPfPieces; u++) *(u32x4 *)(kvs + 8 * (tid + u * 64 * kPfWaves)) = stg[u];
     __syncthreads();
     if (st + 1 < nst) {  // in flight during this step's math
       PF_FETCH(st + 1);
     }
     const int k0 = 32 * st;
-    // phase 1: scores and softmax of every tile from the K fragments
-    uint32_t pw[kPfTiles][4];  // P^T fragments (bf16 pairs)
-    float alpha[kPfTiles];
-    {
-      Frag8 kf[2][4];
+    // phase 1: scores of every tile, one page of K fragments at a time
+    f32x4 sc[kPfTiles][2];
 #pragma unroll
-      for (int t = 0; t < 2; t++)
+    for (int t = 0; t < 2; t++) {
+      Frag8 kf[4];
 #pragma unroll
-        for (int cc = 0; cc < 4; cc++)
-          kf[t][cc].q = *(const uint4 *)(kvs + 2 * t * kPageHead + cc * (kPage * 32) + lr * 32 + 8 * lg);
+      for (int cc = 0; cc < 4; cc++)
+        kf[cc].q = *(const uint4 *)(kvs + 2 * t * kPageHead + cc * (kPage * 32) + lr * 32 + 8 * lg);
 #pragma unroll
       for (int j = 0; j < kPfTiles; j++) {
-        alpha[j] = 1.0f;
-        pw[j][0] = pw[j][1] = pw[j][2] = pw[j][3] = 0u;
+        sc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (k0 > tile_last[j]) continue;  // every key of the step is past the tile's rows
-        f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int cc = 0; cc < 4; cc++) {
-          s0 = mfma16x16x32(kf[0][cc], qf[j][cc], s0);
-          s1 = mfma16x16x32(kf[1][cc], qf[j][cc], s1);
-        }
-        const int pos = ctx + tok[j];
-        float p0[4], p1[4], tmax = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int key = k0 + 4 * lg + i;
-          p0[i] = key <= pos ? s0[i] * a.qk_scale : -INFINITY;
-          p1[i] = key + 16 <= pos ? s1[i] * a.qk_scale : -INFINITY;
-          tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
-        }
-        tmax = max_xor32(max_xor16(tmax));
-        const float m_new = fmaxf(m_run[j], tmax);  // finite: key 0 is in every row's first step
-        alpha[j] = exp2f(m_run[j] - m_new);
-        float psum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          p0[i] = exp2f(p0[i] - m_new);
-          p1[i] = exp2f(p1[i] - m_new);
-          psum += p0[i] + p1[i];
-        }
-        l_run[j] = l_run[j] * alpha[j] + psum;
-        m_run[j] = m_new;
-        pw[j][0] = pack_bf16x2(p0[0], p0[1]);
-        pw[j][1] = pack_bf16x2(p0[2], p0[3]);
-        pw[j][2] = pack_bf16x2(p1[0], p1[1]);
-        pw[j][3] = pack_bf16x2(p1[2], p1[3]);
+        for (int cc = 0; cc < 4; cc++) sc[j][t] = mfma16x16x32(kf[cc], qf[j][cc], sc[j][t]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);  // the V fragments are read after the K fragments are dead
-    // phase 2: O^T += V^T . P^T for every tile from the V fragments
-    uint2 vv[2][8];
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-#pragma unroll
-      for (int cc = 0; cc < 8; cc++)
-        vv[t][cc] = *(const uint2 *)(kvs + (2 * t + 1) * kPageHead + (16 * cc + lr) * kPage + 4 * lg);
-    if (k0 + 32 > kend) {  // slots past the keys may hold stale bits: their V is made 0
-      const int kb = k0 + 4 * lg;
-#pragma unroll
-      for (int cc = 0; cc < 8; cc++) {
-        vv[0][cc].x = mask_pair(vv[0][cc].x, kb, kend);
-        vv[0][cc].y = mask_pair(vv[0][cc].y, kb + 2, kend);
-        vv[1][cc].x = mask_pair(vv[1][cc].x, kb + 16, kend);
-        vv[1][cc].y = mask_pair(vv[1][cc].y, kb + 18, kend);
-      }
-    }
+    // online softmax of every tile
+    uint32_t pw[kPfTiles][4];  // P^T fragments (bf16 pairs)
+    float alpha[kPfTiles];
 #pragma unroll
     for (int j = 0; j < kPfTiles; j++) {
+      alpha[j] = 1.0f;
+      pw[j][0] = pw[j][1] = pw[j][2] = pw[j][3] = 0u;
       if (k0 > tile_last[j]) continue;
+      const int pos = ctx + tok[j];
+      float p0[4], p1[4], tmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int key = k0 + 4 * lg + i;
+        p0[i] = key <= pos ? sc[j][0][i] * a.qk_scale : -INFINITY;
+        p1[i] = key + 16 <= pos ? sc[j][1][i] * a.qk_scale : -INFINITY;
+        tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
+      }
+      tmax = max_xor32(max_xor16(tmax));
+      const float m_new = fmaxf(m_run[j], tmax);  // finite: key 0 is in every row's first step
+      alpha[j] = exp2f(m_run[j] - m_new);
+      float psum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        p0[i] = exp2f(p0[i] - m_new);
+        p1[i] = exp2f(p1[i] - m_new);
+        psum += p0[i] + p1[i];
+      }
+      l_run[j] = l_run[j] * alpha[j] + psum;
+      m_run[j] = m_new;
+      pw[j][0] = pack_bf16x2(p0[0], p0[1]);
+      pw[j][1] = pack_bf16x2(p0[2], p0[3]);
+      pw[j][2] = pack_bf16x2(p1[0], p1[1]);
+      pw[j][3] = pack_bf16x2(p1[2], p1[3]);
       if (__any(alpha[j] != 1.0f)) {
 #pragma unroll
         for (int cc = 0; cc < 8; cc++)
 #pragma unroll
           for (int i = 0; i < 4; i++) o[j][cc][i] *= alpha[j];
       }
-      Frag8 pf;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // phase 2: O^T += V^T . P^T for every tile, half the V fragments (64 dims) at a time
 #pragma unroll
-      for (int i = 0; i < 4; i++) pf.u[i] = pw[j][i];
+    for (int hv = 0; hv < 2; hv++) {
+      uint2 vv[2][4];
 #pragma unroll
-      for (int cc = 0; cc < 8; cc++) {
-        Frag8 vf;
-        vf.u[0] = vv[0][cc].x;
-        vf.u[1] = vv[0][cc].y;
-        vf.u[2] = vv[1][cc].x;
-        vf.u[3] = vv[1][cc].y;
-        o[j][cc] = mfma16x16x32(vf, pf, o[j][cc]);
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int c4 = 0; c4 < 4; c4++)
+          vv[t][c4] = *(const uint2 *)(kvs + (2 * t + 1) * kPageHead + (16 * (4 * hv + c4) + lr) * kPage + 4 * lg);
+      if (k0 + 32 > kend) {  // slots past the keys may hold stale bits: their V is made 0
+        const int kb = k0 + 4 * lg;
+#pragma unroll
+        for (int c4 = 0; c4 < 4; c4++) {
+          vv[0][c4].x = mask_pair(vv[0][c4].x, kb, kend);
+          vv[0][c4].y = mask_pair(vv[0][c4].y, kb + 2, kend);
+          vv[1][c4].x = mask_pair(vv[1][c4].x, kb + 16, kend);
+          vv[1][c4].y = mask_pair(vv[1][c4].y, kb + 18, kend);
+        }
       }
+#pragma unroll
+      for (int j = 0; j < kPfTiles; j++) {
+        if (k0 > tile_last[j]) continue;
+        Frag8 pf;
+#pragma unroll
+        for (int i = 0; i < 4; i++) pf.u[i] = pw[j][i];
+#pragma unroll
+        for (int c4 = 0; c4 < 4; c4++) {
+          Frag8 vf;
+          vf.u[0] = vv[0][c4].x;
+          vf.u[1] = vv[0][c4].y;
+          vf.u[2] = vv[1][c4].x;
+          vf.u[3] = vv[1][c4].y;
+          o[j][4 * hv + c4] = mfma16x16x32(vf, pf, o[j][4 * hv + c4]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 #undef PF_FETCH

@@ -266,13 +266,15 @@ int launch_dense_gpw(const QmmArgs &a, hipStream_t st, const char *what) {
   // a decode batch's 16-token tiles go to separate workgroups (up to JIT_DENSE_ZMAX), so a
   // matrix of few row blocks still fills the chip and each workgroup pulls one tile's
   // activations; longer batches take two tiles per pass
+  // (a prefill-sized batch spreads its 32-token passes over workgroups too: one pass each)
   const int tiles = (a.T + 15) / 16;
   const bool wide = GPW <= 4 && a.N >= JIT_DENSE_WIDE_N;
   if (tiles <= JIT_DENSE_ZMAX)
     return wide ? launch_qmm<2, GPW, false, PACKED, 1>(a, 1, st, what, tiles)
                 : launch_qmm<1, GPW, false, PACKED, 1>(a, 1, st, what, tiles);
-  return wide ? launch_qmm<2, GPW, false, PACKED, 2>(a, 1, st, what)
-              : launch_qmm<1, GPW, false, PACKED, 2>(a, 1, st, what);
+  const int passes = (tiles + 1) / 2;
+  return wide ? launch_qmm<2, GPW, false, PACKED, 2>(a, 1, st, what, passes)
+              : launch_qmm<1, GPW, false, PACKED, 2>(a, 1, st, what, passes);
 }
 
 template <bool PACKED>

@@ -94,6 +94,44 @@ def make_step_state(cfg: MoEConfig, pos_host, page_table: torch.Tensor) -> StepS
     return StepState(torch.from_numpy(pos_host).to(dev), page_table, plan, ws)
 
 
+@dataclass
+class MixedState:
+    """Per-step inputs of a mixed chunked-prefill + decode step.  Rows: the prefill chunks' tokens
+    in chunk order, then one row per decode sequence.  Every row writes its K/V at pos_rows[r]
+    through its own page-table row; the prefill rows attend causally over their sequence's keys,
+    the decode rows over pos + 1 keys."""
+
+    P: int                       # prefill rows (the first P rows)
+    pos_rows: torch.Tensor       # int32 [T]
+    table_rows: torch.Tensor     # int32 [T, max_pages]: row r's sequence's pages
+    seq_table: torch.Tensor      # int32 [S, max_pages]: the prefill sequences' pages
+    prefill: ops.PrefillPlan     # chunks (seq index into seq_table, ctx, length)
+    dec_table: torch.Tensor      # int32 [D, max_pages]: the decode sequences' pages
+    decode: ops.AttnPlan         # decode lens = pos + 1
+    workspace: torch.Tensor
+
+
+def make_mixed_state(cfg: MoEConfig, chunks, seq_table_host, dec_pos_host, dec_table_host, device) -> MixedState:
+    """chunks [(seq, ctx, length)] over the rows of seq_table_host [S, max_pages]; decode sequence d
+    writes position dec_pos_host[d] through dec_table_host[d] (both tables of equal width)."""
+    seq_table_host = np.asarray(seq_table_host, np.int32)
+    dec_table_host = np.asarray(dec_table_host, np.int32)
+    dec_pos = np.asarray(dec_pos_host, np.int32)
+    pos, rows = [], []
+    for seq, ctx, length in chunks:
+        pos += range(ctx, ctx + length)
+        rows += [seq_table_host[seq]] * length
+    P = len(pos)
+    pos_rows = np.concatenate([np.asarray(pos, np.int32), dec_pos]).astype(np.int32)
+    table_rows = np.concatenate([np.stack(rows) if rows else np.zeros((0, dec_table_host.shape[1]), np.int32),
+                                 dec_table_host]).astype(np.int32)
+    dplan = ops.attn_plan(dec_pos + 1, device)
+    ws = torch.empty(max(ops.attn_workspace_bytes(dplan.total, cfg.heads), 4), dtype=torch.uint8, device=device)
+    return MixedState(P, torch.from_numpy(pos_rows).to(device), torch.from_numpy(table_rows).to(device),
+                      torch.from_numpy(seq_table_host).to(device), ops.prefill_plan(chunks, cfg.heads, cfg.kv_heads, device),
+                      torch.from_numpy(dec_table_host).to(device), dplan, ws)
+
+
 class DecoderLayer:
     """One decoder layer over B ragged decode rows; weights stay resident (packed layout)."""
 
@@ -142,6 +180,38 @@ class DecoderLayer:
             debug.update(x=x, xn=xn, qkv=qkv, q=q, attn=attn, o=o, h=h, hn=hn, logits=logits, inds=inds,
                          scores=scores, pk=pk, hh=hh, r=r, y=y)
         return y, xn_next
+
+
+    def mixed(self, x: torch.Tensor, pool: torch.Tensor, ms: MixedState, debug: dict | None = None) -> torch.Tensor:
+        """One mixed chunked-prefill + decode step of the layer over rows x [T, D]: the decode
+        step's block with the prefill rows' attention causal over their chunks
+        (Q36/model/attention.py:70-74) and the MoE on the segment GEMM when the batch is long
+        (Q36/model/moe.py:161-190)."""
+        cfg = self.cfg
+        T = x.shape[0]
+        xn = ops.rmsnorm(x, self.input_norm, cfg.eps)
+        qkv = ops.qmm(xn, self.qkv)
+        q = ops.qk_norm_rope_append(qkv, cfg.heads, cfg.kv_heads, self.q_norm, self.k_norm, cfg.eps,
+                                    self.inv_freq, ms.pos_rows, ms.table_rows, pool)
+        scale = cfg.head_dim ** -0.5
+        parts = []
+        if ms.P:
+            parts.append(ops.paged_prefill_attention(q[:ms.P], pool, ms.seq_table, ms.prefill, scale))
+        if T > ms.P:
+            parts.append(ops.paged_decode_attention(q[ms.P:], pool, ms.dec_table, ms.decode, scale, ms.workspace))
+        attn = torch.cat(parts) if len(parts) > 1 else parts[0]
+        o = ops.qmm(attn.view(T, -1), self.o)
+        hn, h = ops.rmsnorm(o, self.post_norm, cfg.eps, resid=x, return_sum=True)
+        moe = self.moe
+        logits = ops.qmm(hn, moe.router)
+        inds, scores = ops.router_topk(logits, moe.top_k, moe.norm_topk)
+        pk = ops.moe_pack(inds, moe.num_experts)
+        hh, r = moe.expert_mlp(hn, pk, prefill=True)
+        y = ops.moe_combine(r, pk, scores, h)
+        if debug is not None:
+            debug.update(x=x, xn=xn, qkv=qkv, q=q, attn=attn, o=o, h=h, hn=hn, logits=logits, inds=inds,
+                         scores=scores, pk=pk, hh=hh, r=r, y=y)
+        return y
 
 
 class Model:

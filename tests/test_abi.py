@@ -45,7 +45,7 @@ def test_contract_breaks_return_einval_before_launch():
     assert lib.jit_moe_down(None, 768 + 64, None, None, 8, None, None, None, 2048, 16, None, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_paged_decode_attn(None, None, None, 4, None, None, None, 2, 30, 4, 0.1, 4, None, None, None) == _lib.JIT_EINVAL
     assert lib.jit_paged_decode_attn(None, None, None, 4, None, None, None, 2, 64, 2, 0.1, 4, None, None, None) == _lib.JIT_EUNSUPPORTED
-    assert lib.jit_prefill_block_tokens(32, 4) == 16 and lib.jit_prefill_block_tokens(24, 8) == -1
+    assert lib.jit_prefill_block_tokens(32, 4) == 32 and lib.jit_prefill_block_tokens(24, 8) == -1
     assert lib.jit_paged_prefill_attn(*([None] * 3), 16, *([None] * 4), 1, None, None, 1, 32, 3, 0.1, None,
                                       None) == _lib.JIT_EINVAL
     assert lib.jit_paged_prefill_attn(*([None] * 3), 16, *([None] * 4), 1, None, None, 1, 24, 8, 0.1, None,

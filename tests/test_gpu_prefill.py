@@ -13,7 +13,7 @@ import torch
 
 import oracle
 from jitengine_amd import ops
-from tests.helpers import assert_close_bf16, bf16_tensor, normal_bf16, u16
+from tests.helpers import assert_close_bf16, bf16_tensor, bf16_to_f32, normal_bf16, u16
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -115,3 +115,43 @@ def test_prefill_config3_chunks():
     lens = np.array([int(ctx[r // 512]) + r % 512 + 1 for r in sel], np.int32)
     want = oracle.paged_decode_attn(q[sel], pool, table[sel // 512], lens, SCALE)
     assert_close_bf16(got[sel], want, what="config 3 prefill")
+
+
+def test_mixed_prefill_decode_layer_stages():
+    """One mixed chunked-prefill + decode step of a decoder layer (config 3's shape, small): the
+    attention rows against the oracle on the step's own q and pool, and the MoE half (segment GEMM)
+    against the oracle's expert chain on the step's own normed rows."""
+    from jitengine_amd.model import DecoderLayer, MoEConfig, make_mixed_state, random_layer_weights
+
+    cfg = MoEConfig(experts=32, layers=1)
+    chunks = [(0, 30, 40), (1, 0, 21), (2, 511, 64)]
+    dec_pos = [100, 7, 3000]
+    seq_keys = [ctx + n for _, ctx, n in chunks] + [p + 1 for p in dec_pos]
+    pool, table = _pool(seq_keys, seed=51)
+    w = random_layer_weights(cfg, seed=52, device=DEV)
+    layer = DecoderLayer(cfg, w)
+    ms = make_mixed_state(cfg, chunks, table[:3], dec_pos, table[3:], DEV)
+    T = ms.P + len(dec_pos)
+    x = bf16_tensor(normal_bf16((T, cfg.hidden), seed=53), DEV)
+    pt = bf16_tensor(pool, DEV)
+    dbg = {}
+    y = layer.mixed(x, pt, ms, debug=dbg)
+    torch.cuda.synchronize()
+    assert layer.moe.use_seg(T * cfg.top_k, prefill=True)
+    q, attn, pool_after = u16(dbg["q"]), u16(dbg["attn"]), u16(pt)
+    want_pre = oracle.paged_prefill_attn(q[:ms.P], pool_after, table[:3], chunks, SCALE)
+    assert_close_bf16(attn[:ms.P], want_pre, what="mixed step prefill rows")
+    want_dec = oracle.paged_decode_attn(q[ms.P:], pool_after, table[3:], np.array(dec_pos) + 1, SCALE)
+    assert_close_bf16(attn[ms.P:], want_dec, what="mixed step decode rows")
+
+    def host_q(lin):
+        return (lin.weight.cpu().numpy().view(np.uint32), u16(lin.scales), u16(lin.biases))
+
+    hn = u16(dbg["hn"])
+    wi = dbg["inds"].cpu().numpy().view(np.uint32)
+    pk = oracle.moe_pack(wi, cfg.experts)
+    h = oracle.moe_gate_up(hn, wi, pk, *host_q(w["gate_up"]), bf16w=True)
+    r = oracle.moe_down(h, wi, pk, *host_q(w["down"]), bf16w=True)
+    moe = oracle.moe_combine(r, pk["inv"], u16(dbg["scores"]))
+    want_y = oracle.f32_to_bf16(bf16_to_f32(u16(dbg["h"])) + bf16_to_f32(moe))
+    assert_close_bf16(u16(y), want_y, what="mixed step output")
