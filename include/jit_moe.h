@@ -173,6 +173,14 @@ int jit_moe_gate_up_swiglu_seg(const uint16_t *x, int K, const int32_t *pair_row
 int jit_moe_down_seg(const uint16_t *h, int I, const int32_t *expert_cnt, const int32_t *expert_off,
                      int E, const void *packed, int D, int P, uint16_t *r, void *stream);
 
+/* A prefill-sized dense projection y[T, N] = x[T, K] . W[N, K]^T on the segment GEMM's
+ * tiles, with its arithmetic: bf16-dequantized weights, fp32 accumulate -- that of
+ * MLX's affine_qmm_t for long inputs, which the reference's dense prefill kernel keeps
+ * (Q36/kernels/qmm_prefill.py:1-6,86-90; called from QLinear.__call__,
+ * Q36/linear.py:219-231).  W packed (jit_q4_prepack); the token chunks are spread over
+ * workgroups.  Contract: K % 128 == 0, N % 256 == 0. */
+int jit_qmm_seg(const uint16_t *x, int T, int K, const void *packed, int N, uint16_t *y, void *stream);
+
 /* Weighted combine in slot order: y[b] = sum_j bf16(r[inv[b*k+j]] * score[b, j])
  * with each product rounded to bf16 and a sequential bf16 sum over j = 0..k-1
  * (Q36/kernels/expert_solo.py:1-6,155-163,307-315; stock

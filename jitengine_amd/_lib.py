@@ -37,6 +37,7 @@ _SIGNATURES = {
     "jit_moe_down_packed": [_P, _I, _P, _P, _I, _P, _I, _I, _P, _P],
     "jit_moe_gate_up_swiglu_seg": [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P, _P],
     "jit_moe_down_seg": [_P, _I, _P, _P, _I, _P, _I, _I, _P, _P],
+    "jit_qmm_seg": [_P, _I, _I, _P, _I, _P, _P],
     "jit_moe_combine": [_P, _P, _P, _I, _I, _I, _P, _P, _P],
     "jit_moe_combine_rmsnorm": [_P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P],
     "jit_rmsnorm": [_P, _P, _I, _I, _P, _F, _P, _P, _P],

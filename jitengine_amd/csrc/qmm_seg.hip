@@ -32,11 +32,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 is 
 struct SegArgs {
   const uint16_t *x;          // activations [rows, K] bf16
   const int32_t *row_index;   // x row of each sorted position (null: the position itself)
-  const int32_t *cnt, *off;   // pairs per expert, first sorted position per expert
+  const int32_t *cnt, *off;   // pairs per expert, first sorted position per expert (null: a
+                              // dense matrix, E = 1, rows 0 .. T - 1)
   const uint8_t *w;           // packed stack [E, rows_w, K]
   uint16_t *out;              // [P, N] bf16 in sorted order
   long long w_estride;        // packed bytes per expert
   int K, N;                   // N: output columns (I for gate||up, D for down)
+  int T;                      // rows of a dense matrix (cnt null)
 };
 
 // 8 packed-order nibbles of a word -> 8 bf16 weights bf16(s * q + b) in natural k order.
@@ -68,7 +70,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ __attribute__((aligned(16))) uint16_t xs[kSegTokens * kXStride];
   __shared__ int xrow[kSegTokens];
   const int e = blockIdx.y;
-  const int cnt = a.cnt[e], off = a.off[e];
+  const int cnt = a.cnt ? a.cnt[e] : a.T, off = a.cnt ? a.off[e] : 0;
   if (cnt <= 0) return;  // uniform over the workgroup
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
   const int lr = l & 15, lg = l >> 4;
@@ -86,7 +88,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   const uint8_t *wexp = a.w + (long long)e * a.w_estride;
 
-  for (int c0 = 0; c0 < cnt; c0 += kSegTokens) {
+  // (the token chunks are dealt to the workgroups of gridDim.z: one z for an expert segment,
+  // several for a dense batch)
+  for (int c0 = blockIdx.z * kSegTokens; c0 < cnt; c0 += gridDim.z * kSegTokens) {
     const int nt = min(kSegTokens, cnt - c0);
     const int ntiles = (nt + 15) >> 4;
     __syncthreads();  // the previous chunk's LDS reads are done
@@ -205,7 +209,7 @@ extern "C" int jit_moe_gate_up_swiglu_seg(const uint16_t *x, int K, const int32_
   if (P == 0) return JIT_OK;
   if (!x || !pair_row || !expert_cnt || !expert_off || !packed || !h)
     return jit::fail(JIT_EINVAL, "moe_gate_up_seg: null pointer");
-  SegArgs a{x, pair_row, expert_cnt, expert_off, (const uint8_t *)packed, h, jit_q4_packed_bytes(1, 2 * I, K), K, I};
+  SegArgs a{x, pair_row, expert_cnt, expert_off, (const uint8_t *)packed, h, jit_q4_packed_bytes(1, 2 * I, K), K, I, 0};
   seg_kernel<true><<<dim3(I / 128, E), 256, 0, (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_moe_gate_up_swiglu_seg");
 }
@@ -219,7 +223,20 @@ extern "C" int jit_moe_down_seg(const uint16_t *h, int I, const int32_t *expert_
                      I, D);
   if (P == 0) return JIT_OK;
   if (!h || !expert_cnt || !expert_off || !packed || !r) return jit::fail(JIT_EINVAL, "moe_down_seg: null pointer");
-  SegArgs a{h, nullptr, expert_cnt, expert_off, (const uint8_t *)packed, r, jit_q4_packed_bytes(1, D, I), I, D};
+  SegArgs a{h, nullptr, expert_cnt, expert_off, (const uint8_t *)packed, r, jit_q4_packed_bytes(1, D, I), I, D, 0};
   seg_kernel<false><<<dim3(D / kSegRows, E), 256, 0, (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_moe_down_seg");
+}
+
+extern "C" int jit_qmm_seg(const uint16_t *x, int T, int K, const void *packed, int N, uint16_t *y, void *stream) {
+  if (T < 0 || K <= 0 || N <= 0) return jit::fail(JIT_EINVAL, "qmm_seg: bad dims T=%d K=%d N=%d", T, K, N);
+  if (K % 128 != 0 || N % kSegRows != 0)
+    return jit::fail(JIT_EUNSUPPORTED, "qmm_seg covers K %% 128 == 0 and N %% %d == 0, got K=%d N=%d", kSegRows, K,
+                     N);
+  if (T == 0) return JIT_OK;
+  if (!x || !packed || !y) return jit::fail(JIT_EINVAL, "qmm_seg: null pointer");
+  SegArgs a{x, nullptr, nullptr, nullptr, (const uint8_t *)packed, y, 0, K, N, T};
+  const int chunks = (T + kSegTokens - 1) / kSegTokens;
+  seg_kernel<false><<<dim3(N / kSegRows, 1, chunks), 256, 0, (hipStream_t)stream>>>(a);
+  return jit::check_launch("jit_qmm_seg");
 }

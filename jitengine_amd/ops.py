@@ -164,9 +164,15 @@ def prepack(lin: QLinear) -> PackedQ4:
 
 
 # ----------------------------------------------------------------------------- projections
-def qmm(x: torch.Tensor, lin) -> torch.Tensor:
+QMM_SEG_MIN_ROWS = 192  # the reference's switch to its prefill tile GEMM (Q36/kernels/qmm_prefill.py:75)
+
+
+def qmm(x: torch.Tensor, lin, seg: bool | None = None) -> torch.Tensor:
     """x [T, K] bf16 -> [T, N] bf16 against a 4-bit matrix [N, K] (QLinear in the MLX layout or
-    PackedQ4): QLinear.__call__ / .rows (Q36/linear.py:219-313)."""
+    PackedQ4): QLinear.__call__ / .rows (Q36/linear.py:219-313).  A packed matrix and a batch of
+    at least QMM_SEG_MIN_ROWS rows take the prefill tile GEMM (jit_qmm_seg: bf16-dequantized
+    weights, as the reference's dense prefill kernel) where its shape allows; seg forces the
+    choice."""
     _need(x, torch.bfloat16, "x")
     T, K = x.shape
     if K != lin.in_dims:
@@ -175,8 +181,15 @@ def qmm(x: torch.Tensor, lin) -> torch.Tensor:
     if isinstance(lin, PackedQ4):
         if lin.stacked:
             raise ValueError("qmm takes one [N, K] matrix")
-        _lib.check(_lib.lib().jit_qmm_packed(_p(x), T, K, _p(lin.data), lin.N, _p(y), _stream()), "qmm_packed")
+        if seg is None:
+            seg = T >= QMM_SEG_MIN_ROWS and lin.N % 256 == 0 and K % 128 == 0
+        if seg:
+            _lib.check(_lib.lib().jit_qmm_seg(_p(x), T, K, _p(lin.data), lin.N, _p(y), _stream()), "qmm_seg")
+        else:
+            _lib.check(_lib.lib().jit_qmm_packed(_p(x), T, K, _p(lin.data), lin.N, _p(y), _stream()), "qmm_packed")
         return y
+    if seg:
+        raise ValueError("the prefill tile GEMM reads a packed matrix")
     if lin.weight.dim() != 2:
         raise ValueError("qmm takes one [N, K] matrix")
     lin.validate()

@@ -251,6 +251,24 @@ def test_qmm_packed_equals_direct(T, N, K):
     assert torch.equal(ops.qmm(x, ops.prepack(q)), ops.qmm(x, q))
 
 
+@pytest.mark.parametrize("T,N,K", [(192, 256, 2048), (300, 5120, 2048), (2108, 2048, 4096), (161, 512, 768)])
+def test_qmm_prefill_tile_gemm(T, N, K):
+    """A long batch on the prefill tile GEMM (jit_qmm_seg): the reference's prefill arithmetic,
+    bf16-dequantized weights with fp32 sums, restated by the oracle's bf16-weight mode (a dense
+    matrix is a one-expert stack whose pairs are the rows in order); 161 rows: a partial token
+    chunk."""
+    q = make_stack((N, K), seed=T + K)
+    x = normal_bf16((T, K), seed=T)
+    y = ops.qmm(bf16_tensor(x, DEV), ops.prepack(_dev(q)), seg=True)
+    inds = np.zeros((T, 1), np.uint32)
+    w, s_, b = stack_np(q)
+    want = oracle.moe_down(x, inds, oracle.moe_pack(inds, 1), w[None], s_[None], b[None], bf16w=True)
+    st = assert_close_bf16(u16(y), want, what=f"qmm_seg T={T} N={N} K={K}")
+    assert st["bit_equal"] > 0.9, st
+    if T >= ops.QMM_SEG_MIN_ROWS:  # the automatic switch takes it too
+        assert torch.equal(ops.qmm(bf16_tensor(x, DEV), ops.prepack(_dev(q))), y)
+
+
 @pytest.mark.parametrize("B,E", [(64, 128), (300, 8), (1, 16)])
 def test_expert_paths_packed_equal_direct(B, E):
     gu, dn, x, inds, scores = _moe_inputs(B, E, 2048, 768, seed=60 + B)
