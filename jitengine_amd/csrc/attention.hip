@@ -403,7 +403,8 @@ __global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restri
 // past a row's position masked.  A token's result depends only on its q row and its keys:
 // the steps and their order are the same wherever the token's tile sits.
 constexpr int kPfWaves = 8, kPfTiles = 2;
-constexpr int kPfPieces = 4 * kPageHead / 8 / (64 * kPfWaves);  // 16 B pieces of a step per thread
+constexpr int kPfStages = 4;                                  // LDS ring depth (steps)
+constexpr int kPfChunks = 4 * kPageHead * 2 / 1024 / kPfWaves;  // 1 KB chunks of a step per wave
 constexpr int kPfMaxPages = 4096;  // page ids of a workgroup's keys, held in LDS
 
 struct PrefillArgs {
@@ -419,7 +420,9 @@ struct PrefillArgs {
 };
 
 __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t kvs[4 * kPageHead];  // K0, V0, K1, V1 of a step
+  // a ring of kPfStages steps, each K0, V0, K1, V1 of its two pages (4 KB each), filled by
+  // direct global->LDS loads kPfStages - 1 steps ahead of the step being computed
+  __shared__ __attribute__((aligned(16))) uint16_t kvs[kPfStages][4 * kPageHead];
   __shared__ int pgs[kPfMaxPages];
   const int ch = a.blk_chunk[blockIdx.x], q0 = a.blk_q0[blockIdx.x];
   const int kvh = blockIdx.y;
@@ -457,35 +460,67 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   for (int j = 0; j < kPfTiles; j++) tile_last[j] = ctx + min(q0 + wave * tpw + j * TR + TR - 1, len - 1);
   __syncthreads();
 
-  // staging of step st: the step's four 4 KB parts (K of page 2st, V of page 2st, K of page
-  // 2st + 1, V of page 2st + 1; a page past the keys repeats the last one, whose slots are
-  // masked) in 16 B pieces, piece tid + u * threads for thread tid
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 arrays land in scratch)
-  u32x4 stg[kPfPieces];
-#define PF_FETCH(st)                                                                                   \
-  _Pragma("unroll") for (int u = 0; u < kPfPieces; u++) {                                              \
-    const int pc = tid + u * 64 * kPfWaves, part = pc >> 8;                                            \
+  // staging of step st into stage st % kPfStages: chunk c = kPfChunks * wave + u (1 KB, one
+  // load instruction of the wave) of the step's four parts -- K of page 2st, V of page 2st, K of
+  // page 2st + 1, V of page 2st + 1 (a page past the keys repeats the last one: its slots are
+  // masked, and the steps past the end are loaded and never read, so every wave always has
+  // (kPfStages - 1) * kPfChunks loads issued after a step's own)
+  // The loads are issued from inline assembly: the compiler then keeps no track of them (its
+  // own waits would otherwise include them before every LDS read, as it cannot tell the
+  // stages apart), and the explicit waits below order them; its waits for other loads only
+  // grow more conservative.
+  const uint32_t kvs_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)&kvs[0][0];
+#define PF_STAGE(st)                                                                                   \
+  _Pragma("unroll") for (int u = 0; u < kPfChunks; u++) {                                              \
+    const int c = kPfChunks * wave + u, part = c >> 2;                                                 \
     const int pg = pgs[min(2 * (st) + (part >> 1), npages - 1)];                                       \
-    stg[u] = *(const u32x4 *)(head_part(a.pool, pg, a.Hkv, kvh) + (part & 1) * kPageHead + 8 * (pc & 255)); \
+    const uint16_t *src = head_part(a.pool, pg, a.Hkv, kvh) + (part & 1) * kPageHead + (c & 3) * 512 + 8 * l; \
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(kvs_lds + 2 * (((st) % kPfStages) * 4 * kPageHead + 512 * c)); \
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0"); \
   }
-  PF_FETCH(0);
-  for (int st = 0; st < nst; st++) {
-    __syncthreads();  // the previous step's LDS reads are done
+  // the q fragments have landed before the first staged load is issued: the compiler's waits
+  // for them would otherwise sit inside the loop, where they would also wait for the staging
 #pragma unroll
-    for (int u = 0; u < kPfPieces; u++) *(u32x4 *)(kvs + 8 * (tid + u * 64 * kPfWaves)) = stg[u];
-    __syncthreads();
-    if (st + 1 < nst) {  // in flight during this step's math
-      PF_FETCH(st + 1);
-    }
+  for (int j = 0; j < kPfTiles; j++)
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++)
+      asm volatile("" ::"v"(qf[j][cc].u[0]), "v"(qf[j][cc].u[1]), "v"(qf[j][cc].u[2]), "v"(qf[j][cc].u[3]));
+#pragma unroll
+  for (int st = 0; st < kPfStages - 1; st++) {
+    PF_STAGE(st);
+  }
+  // the wait that leaves the loads of the next kPfStages - 2 steps in flight, and no lgkm or
+  // export wait (vmcnt is split over bits 3:0 and 15:14)
+  constexpr int kPfVm = (kPfStages - 2) * kPfChunks;
+  constexpr int kPfWait = (kPfVm & 15) | ((kPfVm >> 4) << 14) | (7 << 4) | (15 << 8);
+  for (int st = 0; st < nst; st++) {
+    // this wave's loads of step st have landed and its reads of step st - 1 are done; after
+    // the barrier so are every wave's, and stage (st - 1) % kPfStages may be refilled
+    // (the empty asm statements keep the compiler from moving LDS accesses across the barrier,
+    // which is issued bare: a __syncthreads fence would wait for every load in flight)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kPfWait);
+    __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    PF_STAGE(st + kPfStages - 1);
+    const uint16_t *kvsc = kvs[st % kPfStages];
     const int k0 = 32 * st;
-    // phase 1: scores of every tile, one page of K fragments at a time
+    // Key order: the P.V MFMA's k index 8 lg + j (lane group lg) is key 8 lg + j of the step
+    // (page lg / 2, slot 8 (lg % 2) + j), so a lane's V operand is 8 consecutive slots of one
+    // page -- 16 contiguous bytes of the page's dim-major V part.  Score tile t therefore holds
+    // in its row 4 lg + i key 8 lg + 4 t + i: its A operand row r (lane lr = r) reads the K
+    // row of key 8 (r / 4) + 4 t + r % 4, and each lane's 8 scores are then exactly its
+    // P^T operand (tile 0: j < 4, tile 1: j >= 4).
+    // phase 1: scores of every tile, one score tile of K fragments at a time
     f32x4 sc[kPfTiles][2];
 #pragma unroll
     for (int t = 0; t < 2; t++) {
       Frag8 kf[4];
+      const int kr = 8 * (lr >> 2) + 4 * t + (lr & 3);  // the key of this lane's A row
 #pragma unroll
       for (int cc = 0; cc < 4; cc++)
-        kf[cc].q = *(const uint4 *)(kvs + 2 * t * kPageHead + cc * (kPage * 32) + lr * 32 + 8 * lg);
+        kf[cc].q = *(const uint4 *)(kvsc + 2 * (kr >> 4) * kPageHead + cc * (kPage * 32) + (kr & 15) * 32 + 8 * lg);
 #pragma unroll
       for (int j = 0; j < kPfTiles; j++) {
         sc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -507,9 +542,9 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
       float p0[4], p1[4], tmax = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int key = k0 + 4 * lg + i;
+        const int key = k0 + 8 * lg + i;  // (tile 1: + 4)
         p0[i] = key <= pos ? sc[j][0][i] * a.qk_scale : -INFINITY;
-        p1[i] = key + 16 <= pos ? sc[j][1][i] * a.qk_scale : -INFINITY;
+        p1[i] = key + 4 <= pos ? sc[j][1][i] * a.qk_scale : -INFINITY;
         tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
       }
       tmax = max_xor32(max_xor16(tmax));
@@ -536,24 +571,21 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // phase 2: O^T += V^T . P^T for every tile, half the V fragments (64 dims) at a time
+    // phase 2: O^T += V^T . P^T for every tile, half the V fragments (64 dims) at a time; the
+    // lane's 8 keys are slots 8 (lg % 2) .. + 7 of page lg / 2
 #pragma unroll
     for (int hv = 0; hv < 2; hv++) {
-      uint2 vv[2][4];
+      Frag8 vf[4];
 #pragma unroll
-      for (int t = 0; t < 2; t++)
+      for (int c4 = 0; c4 < 4; c4++)
+        vf[c4].q = *(const uint4 *)(kvsc + (2 * (lg >> 1) + 1) * kPageHead + (16 * (4 * hv + c4) + lr) * kPage +
+                                    8 * (lg & 1));
+      if (k0 + 32 > kend) {  // slots past the keys may hold stale bits: their V is made 0
+        const int kb = k0 + 8 * lg;
 #pragma unroll
         for (int c4 = 0; c4 < 4; c4++)
-          vv[t][c4] = *(const uint2 *)(kvs + (2 * t + 1) * kPageHead + (16 * (4 * hv + c4) + lr) * kPage + 4 * lg);
-      if (k0 + 32 > kend) {  // slots past the keys may hold stale bits: their V is made 0
-        const int kb = k0 + 4 * lg;
 #pragma unroll
-        for (int c4 = 0; c4 < 4; c4++) {
-          vv[0][c4].x = mask_pair(vv[0][c4].x, kb, kend);
-          vv[0][c4].y = mask_pair(vv[0][c4].y, kb + 2, kend);
-          vv[1][c4].x = mask_pair(vv[1][c4].x, kb + 16, kend);
-          vv[1][c4].y = mask_pair(vv[1][c4].y, kb + 18, kend);
-        }
+          for (int w2 = 0; w2 < 4; w2++) vf[c4].u[w2] = mask_pair(vf[c4].u[w2], kb + 2 * w2, kend);
       }
 #pragma unroll
       for (int j = 0; j < kPfTiles; j++) {
@@ -562,19 +594,13 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
 #pragma unroll
         for (int i = 0; i < 4; i++) pf.u[i] = pw[j][i];
 #pragma unroll
-        for (int c4 = 0; c4 < 4; c4++) {
-          Frag8 vf;
-          vf.u[0] = vv[0][c4].x;
-          vf.u[1] = vv[0][c4].y;
-          vf.u[2] = vv[1][c4].x;
-          vf.u[3] = vv[1][c4].y;
-          o[j][4 * hv + c4] = mfma16x16x32(vf, pf, o[j][4 * hv + c4]);
-        }
+        for (int c4 = 0; c4 < 4; c4++) o[j][4 * hv + c4] = mfma16x16x32(vf[c4], pf, o[j][4 * hv + c4]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-#undef PF_FETCH
+#undef PF_STAGE
+  __builtin_amdgcn_s_waitcnt(0);  // no load may still write the LDS when the workgroup ends
 #pragma unroll
   for (int j = 0; j < kPfTiles; j++) {
     const float l_tot = sum_xor32(sum_xor16(l_run[j]));
