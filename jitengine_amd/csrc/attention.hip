@@ -454,10 +454,13 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
 #pragma unroll
     for (int cc = 0; cc < 8; cc++) o[j][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  // the last position among each tile's rows (uniform over the wave)
-  int tile_last[kPfTiles];
+  // the first and last positions among each tile's rows (uniform over the wave)
+  int tile_first[kPfTiles], tile_last[kPfTiles];
 #pragma unroll
-  for (int j = 0; j < kPfTiles; j++) tile_last[j] = ctx + min(q0 + wave * tpw + j * TR + TR - 1, len - 1);
+  for (int j = 0; j < kPfTiles; j++) {
+    tile_first[j] = ctx + min(q0 + wave * tpw + j * TR, len - 1);
+    tile_last[j] = ctx + min(q0 + wave * tpw + j * TR + TR - 1, len - 1);
+  }
   __syncthreads();
 
   // staging of step st into stage st % kPfStages: chunk c = kPfChunks * wave + u (1 KB, one
@@ -538,31 +541,43 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
       alpha[j] = 1.0f;
       pw[j][0] = pw[j][1] = pw[j][2] = pw[j][3] = 0u;
       if (k0 > tile_last[j]) continue;
-      const int pos = ctx + tok[j];
-      float p0[4], p1[4], tmax = -INFINITY;
+      // keys past a row's position are masked on the steps that reach into the tile's rows;
+      // the scale is applied inside the exponent (max of the raw scores times the positive
+      // scale is the max of the scaled ones)
+      float p0[4], p1[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int key = k0 + 8 * lg + i;  // (tile 1: + 4)
-        p0[i] = key <= pos ? sc[j][0][i] * a.qk_scale : -INFINITY;
-        p1[i] = key + 4 <= pos ? sc[j][1][i] * a.qk_scale : -INFINITY;
-        tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
+        p0[i] = sc[j][0][i];
+        p1[i] = sc[j][1][i];
       }
-      tmax = max_xor32(max_xor16(tmax));
+      if (k0 + 31 > tile_first[j]) {
+        const int pos = ctx + tok[j];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int key = k0 + 8 * lg + i;  // (tile 1: + 4)
+          p0[i] = key <= pos ? p0[i] : -INFINITY;
+          p1[i] = key + 4 <= pos ? p1[i] : -INFINITY;
+        }
+      }
+      float tmax = fmaxf(p0[0], p1[0]);
+#pragma unroll
+      for (int i = 1; i < 4; i++) tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
+      tmax = max_xor32(max_xor16(tmax)) * a.qk_scale;
       const float m_new = fmaxf(m_run[j], tmax);  // finite: key 0 is in every row's first step
-      alpha[j] = exp2f(m_run[j] - m_new);
+      alpha[j] = __builtin_amdgcn_exp2f(m_run[j] - m_new);
       float psum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        p0[i] = exp2f(p0[i] - m_new);
-        p1[i] = exp2f(p1[i] - m_new);
+        p0[i] = __builtin_amdgcn_exp2f(fmaf(p0[i], a.qk_scale, -m_new));
+        p1[i] = __builtin_amdgcn_exp2f(fmaf(p1[i], a.qk_scale, -m_new));
         psum += p0[i] + p1[i];
       }
       l_run[j] = l_run[j] * alpha[j] + psum;
       m_run[j] = m_new;
-      pw[j][0] = pack_bf16x2(p0[0], p0[1]);
-      pw[j][1] = pack_bf16x2(p0[2], p0[3]);
-      pw[j][2] = pack_bf16x2(p1[0], p1[1]);
-      pw[j][3] = pack_bf16x2(p1[2], p1[3]);
+      pw[j][0] = pack_bf16x2_rne(p0[0], p0[1]);
+      pw[j][1] = pack_bf16x2_rne(p0[2], p0[3]);
+      pw[j][2] = pack_bf16x2_rne(p1[0], p1[1]);
+      pw[j][3] = pack_bf16x2_rne(p1[2], p1[3]);
       if (__any(alpha[j] != 1.0f)) {
 #pragma unroll
         for (int cc = 0; cc < 8; cc++)

@@ -36,6 +36,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f2bf(lo) | (f2bf(hi) << 16);
 }
 
+// The same rounding in one instruction (v_cvt_pk_bf16_f32, round-to-nearest-even), for finite
+// values: NaN payloads may differ from f2bf's.
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // ------------------------------------------------------------------ wave
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 
