@@ -337,7 +337,8 @@ def bench_config3(steps: int, warmup: int, dev: str) -> dict:
         "op_us": kus,
         "op_us_sum_per_step": sum(kus.values()),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": achieved / 2500.0, "flops_per_launch": flops[dom], "traffic": None},
+                     "frac": achieved / 2500.0, "flops_per_launch": flops[dom],
+                     "traffic": profile_traffic(f"{dom}_config3")},
         "cpu_baseline": {"value": cpu_tps, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
                          "sample": f"the oracle's block (dense, norms, RoPE + append, causal prefill and decode "
                                    f"attention, router, segment-GEMM experts) on {2 * nb} of the {T} rows: the first "
@@ -549,8 +550,9 @@ OP_KERNELS = {  # the kernels one op launches (rocprofv3 kernel names contain th
     "paged_attention": ["paged_attn_kernel", "attn_merge_kernel"],
     "gate_up_swiglu": ["qmm_kernel<1, 8, true, true"],
     "down": ["qmm_kernel<4, 4, false, true"],
-    "gate_up_swiglu_seg": ["seg_kernel<true>"],
-    "down_seg": ["seg_kernel<false>"],
+    "gate_up_swiglu_seg": ["seg_kernel<true, false>"],
+    "down_seg": ["seg_kernel<false, false>"],
+    "qkv_proj_seg": ["seg_kernel<false, true>"],
     "prefill_attention": ["prefill_attn_kernel"],
 }
 
@@ -594,8 +596,9 @@ def rocprof_summary(args) -> int:
             print(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:9.2f} "
                   f"{float(r['MaxNs']) / 1e3:9.2f} {100 * float(r['TotalDurationNs']) / tot:6.1f}%  {name}")
         return 0
-    for c in (f"FETCH_SIZE -f csv -d prof/fetch -o fetch -- python3 bench.py{cfg} --steps 1 --warmup 1 --no-graph",
-              f"WRITE_SIZE -f csv -d prof/write -o write -- python3 bench.py{cfg} --steps 1 --warmup 1 --no-graph",
+    ng = " --no-graph" if args.config == 2 else ""  # (config 3 always replays a graph)
+    for c in (f"FETCH_SIZE -f csv -d prof/fetch -o fetch -- python3 bench.py{cfg} --steps 1 --warmup 1{ng}",
+              f"WRITE_SIZE -f csv -d prof/write -o write -- python3 bench.py{cfg} --steps 1 --warmup 1{ng}",
               "FETCH_SIZE -f csv -d prof/cfetch -o cfetch -- python3 bench.py --copy-calibration",
               "WRITE_SIZE -f csv -d prof/cwrite -o cwrite -- python3 bench.py --copy-calibration"):
         print(f"#   rocprofv3 --pmc {c}")

@@ -525,22 +525,18 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
       for (int cc = 0; cc < 4; cc++)
         kf[cc].q = *(const uint4 *)(kvsc + 2 * (kr >> 4) * kPageHead + cc * (kPage * 32) + (kr & 15) * 32 + 8 * lg);
 #pragma unroll
-      for (int j = 0; j < kPfTiles; j++) {
-        sc[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (k0 > tile_last[j]) continue;  // every key of the step is past the tile's rows
+      for (int j = 0; j < kPfTiles; j++) {  // (a tile past the step's keys discards its scores)
+        sc[j][t] = mfma16x16x32(kf[0], qf[j][0], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-        for (int cc = 0; cc < 4; cc++) sc[j][t] = mfma16x16x32(kf[cc], qf[j][cc], sc[j][t]);
+        for (int cc = 1; cc < 4; cc++) sc[j][t] = mfma16x16x32(kf[cc], qf[j][cc], sc[j][t]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     // online softmax of every tile
-    uint32_t pw[kPfTiles][4];  // P^T fragments (bf16 pairs)
-    float alpha[kPfTiles];
+    uint32_t pw[kPfTiles][4];  // P^T fragments (bf16 pairs; set for the tiles the step reaches)
 #pragma unroll
     for (int j = 0; j < kPfTiles; j++) {
-      alpha[j] = 1.0f;
-      pw[j][0] = pw[j][1] = pw[j][2] = pw[j][3] = 0u;
-      if (k0 > tile_last[j]) continue;
+      if (k0 > tile_last[j]) continue;  // every key of the step is past the tile's rows
       // keys past a row's position are masked on the steps that reach into the tile's rows;
       // the scale is applied inside the exponent (max of the raw scores times the positive
       // scale is the max of the scaled ones)
@@ -564,7 +560,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
       for (int i = 1; i < 4; i++) tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
       tmax = max_xor32(max_xor16(tmax)) * a.qk_scale;
       const float m_new = fmaxf(m_run[j], tmax);  // finite: key 0 is in every row's first step
-      alpha[j] = __builtin_amdgcn_exp2f(m_run[j] - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
       float psum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -572,17 +568,17 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
         p1[i] = __builtin_amdgcn_exp2f(fmaf(p1[i], a.qk_scale, -m_new));
         psum += p0[i] + p1[i];
       }
-      l_run[j] = l_run[j] * alpha[j] + psum;
+      l_run[j] = l_run[j] * alpha + psum;
       m_run[j] = m_new;
       pw[j][0] = pack_bf16x2_rne(p0[0], p0[1]);
       pw[j][1] = pack_bf16x2_rne(p0[2], p0[3]);
       pw[j][2] = pack_bf16x2_rne(p1[0], p1[1]);
       pw[j][3] = pack_bf16x2_rne(p1[2], p1[3]);
-      if (__any(alpha[j] != 1.0f)) {
+      if (__any(alpha != 1.0f)) {
 #pragma unroll
         for (int cc = 0; cc < 8; cc++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) o[j][cc][i] *= alpha[j];
+          for (int i = 0; i < 4; i++) o[j][cc][i] *= alpha;
       }
     }
     __builtin_amdgcn_sched_barrier(0);

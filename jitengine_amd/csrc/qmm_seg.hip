@@ -65,12 +65,13 @@ __device__ __forceinline__ Frag8 dequant_word(uint32_t w, float s, float b) {
   return f;
 }
 
-template <bool SWIGLU>
+// DENSE: one dense matrix (E = 1, cnt null), its token chunks spread over gridDim.z
+template <bool SWIGLU, bool DENSE = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void seg_kernel(const SegArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[kSegTokens * kXStride];
   __shared__ int xrow[kSegTokens];
   const int e = blockIdx.y;
-  const int cnt = a.cnt ? a.cnt[e] : a.T, off = a.cnt ? a.off[e] : 0;
+  const int cnt = DENSE ? a.T : a.cnt[e], off = DENSE ? 0 : a.off[e];
   if (cnt <= 0) return;  // uniform over the workgroup
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
   const int lr = l & 15, lg = l >> 4;
@@ -237,6 +238,6 @@ extern "C" int jit_qmm_seg(const uint16_t *x, int T, int K, const void *packed, 
   if (!x || !packed || !y) return jit::fail(JIT_EINVAL, "qmm_seg: null pointer");
   SegArgs a{x, nullptr, nullptr, nullptr, (const uint8_t *)packed, y, 0, K, N, T};
   const int chunks = (T + kSegTokens - 1) / kSegTokens;
-  seg_kernel<false><<<dim3(N / kSegRows, 1, chunks), 256, 0, (hipStream_t)stream>>>(a);
+  seg_kernel<false, true><<<dim3(N / kSegRows, 1, chunks), 256, 0, (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_qmm_seg");
 }
