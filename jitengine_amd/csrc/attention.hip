@@ -210,22 +210,33 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
     }
     // K registers are free: the next step's K is in flight during softmax and P.V
     load_k2(kf, a.pool, a.Hkv, kvh, page(2 * st + 2), page(2 * st + 3), lr, lg);
-    float p0[4], p1[4], tmax = -INFINITY;
+    // keys past the run are masked on its last step only; the scale is applied inside the
+    // exponent's fma (the max of the raw scores times the positive scale is the scaled max)
+    float p0[4], p1[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int key = k0 + 4 * lg + i;
-      p0[i] = key < wk1 ? s0[i] * a.qk_scale : -INFINITY;
-      p1[i] = key + 16 < wk1 ? s1[i] * a.qk_scale : -INFINITY;
-      tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
+      p0[i] = s0[i];
+      p1[i] = s1[i];
     }
-    tmax = max_xor32(max_xor16(tmax));
+    if (k0 + 32 > wk1) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int key = k0 + 4 * lg + i;
+        p0[i] = key < wk1 ? p0[i] : -INFINITY;
+        p1[i] = key + 16 < wk1 ? p1[i] : -INFINITY;
+      }
+    }
+    float tmax = fmaxf(p0[0], p1[0]);
+#pragma unroll
+    for (int i = 1; i < 4; i++) tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
+    tmax = max_xor32(max_xor16(tmax)) * a.qk_scale;
     const float m_new = fmaxf(m_run, tmax);
-    const float alpha = exp2f(m_run - m_new);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     float psum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      p0[i] = exp2f(p0[i] - m_new);
-      p1[i] = exp2f(p1[i] - m_new);
+      p0[i] = __builtin_amdgcn_exp2f(fmaf(p0[i], a.qk_scale, -m_new));
+      p1[i] = __builtin_amdgcn_exp2f(fmaf(p1[i], a.qk_scale, -m_new));
       psum += p0[i] + p1[i];
     }
     l_run = l_run * alpha + psum;
@@ -233,10 +244,10 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
     // P^T fragment (B operand): head lr, k slots 8*lg + j = key 4*lg + j of the first
     // page (j < 4) and of the second (j >= 4) -- the lane's own probabilities
     Frag8 pf;
-    pf.u[0] = pack_bf16x2(p0[0], p0[1]);
-    pf.u[1] = pack_bf16x2(p0[2], p0[3]);
-    pf.u[2] = pack_bf16x2(p1[0], p1[1]);
-    pf.u[3] = pack_bf16x2(p1[2], p1[3]);
+    pf.u[0] = pack_bf16x2_rne(p0[0], p0[1]);
+    pf.u[1] = pack_bf16x2_rne(p0[2], p0[3]);
+    pf.u[2] = pack_bf16x2_rne(p1[0], p1[1]);
+    pf.u[3] = pack_bf16x2_rne(p1[2], p1[3]);
     if (lr >= G) pf.q = make_uint4(0, 0, 0, 0);
     // the tail page may hold stale slots past L: their p is 0, make their V 0 too
     if (k0 + 32 > L) {
