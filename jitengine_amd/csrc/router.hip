@@ -186,15 +186,14 @@ int launch_router(const uint16_t *src, int rows, int N, int k, int norm, uint32_
 }
 
 // --------------------------------------------------------------- packing
-// One workgroup of 1024 threads.  (1) per-expert counts in LDS; (2) exclusive
+// One workgroup (128, 256 or 1024 threads).  (1) per-expert counts in LDS; (2) exclusive
 // scans give each expert's first sorted position and the ascending list of
-// non-empty experts; (3) pairs are placed in tiles of 1024 in flat order: within
+// non-empty experts; (3) pairs are placed in tiles of the workgroup's size in flat order: within
 // a wave, lanes holding the same expert id find each other with ballots over
 // the id's bits, so a pair's position is its expert's running offset plus the
 // pairs of that expert in earlier waves of the tile plus its rank among its own
 // wave's lanes -- a stable counting sort.
-constexpr int kPackThreads = 1024;
-constexpr int kPackWaves = kPackThreads / 64;
+constexpr int kPackThreads = 1024;  // the largest workgroup (and expert count) of the packing
 
 __device__ __forceinline__ int wave_incl_scan(int x, int l) {
 #pragma unroll
@@ -205,24 +204,24 @@ __device__ __forceinline__ int wave_incl_scan(int x, int l) {
   return x;
 }
 
-// The packing, run by one workgroup of kPackThreads threads; ind(p) is flat pair p's
+// The packing, run by one workgroup of TH threads (TH >= E); ind(p) is flat pair p's
 // expert id.
-template <typename IndFn>
+template <int TH, typename IndFn>
 __device__ __forceinline__ void pack_body(IndFn ind, int P, int k, int E, int32_t *__restrict__ order,
                                           int32_t *__restrict__ pair_row, int32_t *__restrict__ inv,
                                           int32_t *__restrict__ expert_cnt, int32_t *__restrict__ expert_off,
                                           int32_t *__restrict__ seg_expert, int32_t *__restrict__ seg_start,
                                           int32_t *__restrict__ seg_cnt, int32_t *__restrict__ meta) {
-  __shared__ int cnt[kPackThreads];
-  __shared__ int nxt[kPackThreads];
-  __shared__ unsigned short wcnt[kPackWaves][kPackThreads];
-  __shared__ int wsum[kPackWaves], wflag[kPackWaves], wmax[kPackWaves];
+  __shared__ int cnt[TH];
+  __shared__ int nxt[TH];
+  __shared__ unsigned short wcnt[(TH / 64)][TH];
+  __shared__ int wsum[(TH / 64)], wflag[(TH / 64)], wmax[(TH / 64)];
   __shared__ int bad;
   const int t = threadIdx.x, w = t >> 6, l = t & 63;
   cnt[t] = 0;
   if (t == 0) bad = 0;
   __syncthreads();
-  for (int p = t; p < P; p += kPackThreads) {
+  for (int p = t; p < P; p += TH) {
     const uint32_t e = ind(p);
     if (e < (uint32_t)E)
       atomicAdd(&cnt[e], 1);
@@ -244,7 +243,7 @@ __device__ __forceinline__ void pack_body(IndFn ind, int P, int k, int E, int32_
   }
   __syncthreads();
   int cbase = 0, fbase = 0, tot_f = 0, tot_m = 0;
-  for (int ww = 0; ww < kPackWaves; ww++) {
+  for (int ww = 0; ww < (TH / 64); ww++) {
     if (ww < w) {
       cbase += wsum[ww];
       fbase += wflag[ww];
@@ -271,7 +270,7 @@ __device__ __forceinline__ void pack_body(IndFn ind, int P, int k, int E, int32_
     meta[3] = 0;
   }
   const int nbits = 32 - __clz(E);  // enough bits for ids 0..E (E = "no expert")
-  for (int base = 0; base < P; base += kPackThreads) {
+  for (int base = 0; base < P; base += TH) {
     const int p = base + t;
     uint32_t e = p < P ? ind(p) : (uint32_t)E;
     if (e > (uint32_t)E) e = (uint32_t)E;
@@ -283,7 +282,7 @@ __device__ __forceinline__ void pack_body(IndFn ind, int P, int k, int E, int32_
     }
     const int rank = __popcll(m & ((1ull << l) - 1ull));
     const int total = __popcll(m);
-    for (int idx = t; idx < kPackWaves * E; idx += kPackThreads) wcnt[idx / E][idx % E] = 0;
+    for (int idx = t; idx < (TH / 64) * E; idx += TH) wcnt[idx / E][idx % E] = 0;
     __syncthreads();
     if (e < (uint32_t)E && rank == total - 1) wcnt[w][e] = (unsigned short)total;
     __syncthreads();
@@ -299,7 +298,7 @@ __device__ __forceinline__ void pack_body(IndFn ind, int P, int k, int E, int32_
     __syncthreads();
     if (t < E) {
       int s = 0;
-      for (int ww = 0; ww < kPackWaves; ww++) s += wcnt[ww][t];
+      for (int ww = 0; ww < (TH / 64); ww++) s += wcnt[ww][t];
       nxt[t] += s;
     }
     __syncthreads();
@@ -307,12 +306,13 @@ __device__ __forceinline__ void pack_body(IndFn ind, int P, int k, int E, int32_
 }
 
 
-__global__ __launch_bounds__(kPackThreads) void moe_pack_kernel(
+template <int TH>
+__global__ __launch_bounds__(TH) void moe_pack_kernel(
     const uint32_t *__restrict__ inds, int P, int k, int E, int32_t *__restrict__ order,
     int32_t *__restrict__ pair_row, int32_t *__restrict__ inv, int32_t *__restrict__ expert_cnt,
     int32_t *__restrict__ expert_off, int32_t *__restrict__ seg_expert,
     int32_t *__restrict__ seg_start, int32_t *__restrict__ seg_cnt, int32_t *__restrict__ meta) {
-  pack_body([&](int p) { return inds[p]; }, P, k, E, order, pair_row, inv, expert_cnt, expert_off, seg_expert,
+  pack_body<TH>([&](int p) { return inds[p]; }, P, k, E, order, pair_row, inv, expert_cnt, expert_off, seg_expert,
             seg_start, seg_cnt, meta);
 }
 
@@ -351,8 +351,17 @@ extern "C" int jit_moe_pack(const uint32_t *inds, int P, int k, int E, int32_t *
   if (!expert_cnt || !expert_off || !seg_expert || !seg_start || !seg_cnt || !meta)
     return jit::fail(JIT_EINVAL, "moe_pack: null pointer");
   if (P > 0 && (!inds || !order || !pair_row || !inv)) return jit::fail(JIT_EINVAL, "moe_pack: null pointer");
-  moe_pack_kernel<<<1, kPackThreads, 0, (hipStream_t)stream>>>(inds, P, k, E, order, pair_row, inv,
-                                                              expert_cnt, expert_off, seg_expert,
-                                                              seg_start, seg_cnt, meta);
+  // a decode batch's few pairs take the smallest workgroup that owns every expert (fewer waves
+  // at each of the placement's barriers); long batches take 1024 threads a tile
+  const hipStream_t st = (hipStream_t)stream;
+#define JIT_PACK(TH) moe_pack_kernel<TH><<<1, TH, 0, st>>>(inds, P, k, E, order, pair_row, inv, expert_cnt, \
+                                                           expert_off, seg_expert, seg_start, seg_cnt, meta)
+  if (P <= 2048 && E <= 128)
+    JIT_PACK(128);
+  else if (P <= 2048 && E <= 256)
+    JIT_PACK(256);
+  else
+    JIT_PACK(1024);
+#undef JIT_PACK
   return jit::check_launch("jit_moe_pack");
 }
