@@ -414,8 +414,9 @@ __global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restri
 // past a row's position masked.  A token's result depends only on its q row and its keys:
 // the steps and their order are the same wherever the token's tile sits.
 constexpr int kPfWaves = 8, kPfTiles = 2;
-constexpr int kPfStages = 4;                                  // LDS ring depth (steps)
-constexpr int kPfChunks = 4 * kPageHead * 2 / 1024 / kPfWaves;  // 1 KB chunks of a step per wave
+constexpr int kPfHalves = 2;                                           // 32-key halves of a step
+constexpr int kPfStages = 4;                                           // LDS ring depth (steps)
+constexpr int kPfChunks = kPfHalves * 4 * kPageHead * 2 / 1024 / kPfWaves;  // 1 KB chunks of a step per wave
 constexpr int kPfMaxPages = 4096;  // page ids of a workgroup's keys, held in LDS
 
 struct PrefillArgs {
@@ -431,9 +432,10 @@ struct PrefillArgs {
 };
 
 __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const PrefillArgs a) {
-  // a ring of kPfStages steps, each K0, V0, K1, V1 of its two pages (4 KB each), filled by
-  // direct global->LDS loads kPfStages - 1 steps ahead of the step being computed
-  __shared__ __attribute__((aligned(16))) uint16_t kvs[kPfStages][4 * kPageHead];
+  // a ring of kPfStages steps of 64 keys, each two halves of K0, V0, K1, V1 of their two pages
+  // (4 KB each), filled by direct global->LDS loads kPfStages - 1 steps ahead of the step
+  // being computed
+  __shared__ __attribute__((aligned(16))) uint16_t kvs[kPfStages][kPfHalves * 4 * kPageHead];
   __shared__ int pgs[kPfMaxPages];
   const int ch = a.blk_chunk[blockIdx.x], q0 = a.blk_q0[blockIdx.x];
   const int kvh = blockIdx.y;
@@ -443,7 +445,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   const int lr = l & 15, lg = l >> 4;
   const int tlast = min(q0 + kPfWaves * tpw, len) - 1;  // the workgroup's last token
   const int kend = ctx + tlast + 1;                     // its keys: [0, kend)
-  const int nst = (kend + 31) >> 5, npages = (kend + 15) >> 4;
+  const int nst = (kend + 32 * kPfHalves - 1) / (32 * kPfHalves), npages = (kend + 15) >> 4;
   for (int i = tid; i < npages; i += 64 * kPfWaves) pgs[i] = a.page_table[(long long)seq * a.max_pages + i];
 
   // the lane's q row in tile j: token t (clamped into the chunk), head kvh * G + lr % G
@@ -486,10 +488,11 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   const uint32_t kvs_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)&kvs[0][0];
 #define PF_STAGE(st)                                                                                   \
   _Pragma("unroll") for (int u = 0; u < kPfChunks; u++) {                                              \
-    const int c = kPfChunks * wave + u, part = c >> 2;                                                 \
-    const int pg = pgs[min(2 * (st) + (part >> 1), npages - 1)];                                       \
+    const int c = kPfChunks * wave + u, part = c >> 2;  /* part: K or V (part & 1) of page part / 2 */ \
+    const int pg = pgs[min(2 * kPfHalves * (st) + (part >> 1), npages - 1)];                          \
     const uint16_t *src = head_part(a.pool, pg, a.Hkv, kvh) + (part & 1) * kPageHead + (c & 3) * 512 + 8 * l; \
-    const uint32_t dst = __builtin_amdgcn_readfirstlane(kvs_lds + 2 * (((st) % kPfStages) * 4 * kPageHead + 512 * c)); \
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(                                               \
+        kvs_lds + 2 * (((st) % kPfStages) * kPfHalves * 4 * kPageHead + 512 * c));                     \
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0"); \
   }
   // the q fragments have landed before the first staged load is issued: the compiler's waits
@@ -518,73 +521,91 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     PF_STAGE(st + kPfStages - 1);
-    const uint16_t *kvsc = kvs[st % kPfStages];
-    const int k0 = 32 * st;
-    // Key order: the P.V MFMA's k index 8 lg + j (lane group lg) is key 8 lg + j of the step
-    // (page lg / 2, slot 8 (lg % 2) + j), so a lane's V operand is 8 consecutive slots of one
-    // page -- 16 contiguous bytes of the page's dim-major V part.  Score tile t therefore holds
-    // in its row 4 lg + i key 8 lg + 4 t + i: its A operand row r (lane lr = r) reads the K
-    // row of key 8 (r / 4) + 4 t + r % 4, and each lane's 8 scores are then exactly its
-    // P^T operand (tile 0: j < 4, tile 1: j >= 4).
-    // phase 1: scores of every tile, one score tile of K fragments at a time
-    f32x4 sc[kPfTiles][2];
+    const uint16_t *kvst = kvs[st % kPfStages];
+    const int k0 = 32 * kPfHalves * st;
+    // Key order within each 32-key half h (keys k0 + 32 h ..): the P.V MFMA's k index 8 lg + j
+    // (lane group lg) is key 8 lg + j of the half (page lg / 2, slot 8 (lg % 2) + j), so a
+    // lane's V operand is 8 consecutive slots of one page -- 16 contiguous bytes of the page's
+    // dim-major V part.  Score tile t therefore holds in its row 4 lg + i key 8 lg + 4 t + i:
+    // its A operand row r (lane lr = r) reads the K row of key 8 (r / 4) + 4 t + r % 4, and
+    // each lane's 8 scores of a half are then exactly its P^T operand (tile 0: j < 4, tile 1:
+    // j >= 4).
+    // phase 1: scores of every tile and half, one score tile of K fragments at a time
+    f32x4 sc[kPfTiles][kPfHalves][2];
 #pragma unroll
-    for (int t = 0; t < 2; t++) {
-      Frag8 kf[4];
-      const int kr = 8 * (lr >> 2) + 4 * t + (lr & 3);  // the key of this lane's A row
+    for (int h = 0; h < kPfHalves; h++)
 #pragma unroll
-      for (int cc = 0; cc < 4; cc++)
-        kf[cc].q = *(const uint4 *)(kvsc + 2 * (kr >> 4) * kPageHead + cc * (kPage * 32) + (kr & 15) * 32 + 8 * lg);
+      for (int t = 0; t < 2; t++) {
+        Frag8 kf[4];
+        const int kr = 8 * (lr >> 2) + 4 * t + (lr & 3);  // the key of this lane's A row
+        const uint16_t *kvsc = kvst + h * 4 * kPageHead;
 #pragma unroll
-      for (int j = 0; j < kPfTiles; j++) {  // (a tile past the step's keys discards its scores)
-        sc[j][t] = mfma16x16x32(kf[0], qf[j][0], f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int cc = 0; cc < 4; cc++)
+          kf[cc].q = *(const uint4 *)(kvsc + 2 * (kr >> 4) * kPageHead + cc * (kPage * 32) + (kr & 15) * 32 + 8 * lg);
 #pragma unroll
-        for (int cc = 1; cc < 4; cc++) sc[j][t] = mfma16x16x32(kf[cc], qf[j][cc], sc[j][t]);
+        for (int j = 0; j < kPfTiles; j++) {  // (a tile past the step's keys discards its scores)
+          sc[j][h][t] = mfma16x16x32(kf[0], qf[j][0], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int cc = 1; cc < 4; cc++) sc[j][h][t] = mfma16x16x32(kf[cc], qf[j][cc], sc[j][h][t]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // online softmax of every tile
-    uint32_t pw[kPfTiles][4];  // P^T fragments (bf16 pairs; set for the tiles the step reaches)
+    // online softmax of every tile over the step's 64 keys
+    uint32_t pw[kPfTiles][kPfHalves][4];  // P^T fragments (bf16 pairs; set for the tiles the step reaches)
 #pragma unroll
     for (int j = 0; j < kPfTiles; j++) {
       if (k0 > tile_last[j]) continue;  // every key of the step is past the tile's rows
       // keys past a row's position are masked on the steps that reach into the tile's rows;
       // the scale is applied inside the exponent (max of the raw scores times the positive
       // scale is the max of the scaled ones)
-      float p0[4], p1[4];
+      float p[kPfHalves][2][4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        p0[i] = sc[j][0][i];
-        p1[i] = sc[j][1][i];
-      }
-      if (k0 + 31 > tile_first[j]) {
+      for (int h = 0; h < kPfHalves; h++)
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) p[h][t][i] = sc[j][h][t][i];
+      if (k0 + 32 * kPfHalves - 1 > tile_first[j]) {
         const int pos = ctx + tok[j];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int key = k0 + 8 * lg + i;  // (tile 1: + 4)
-          p0[i] = key <= pos ? p0[i] : -INFINITY;
-          p1[i] = key + 4 <= pos ? p1[i] : -INFINITY;
-        }
-      }
-      float tmax = fmaxf(p0[0], p1[0]);
+        for (int h = 0; h < kPfHalves; h++)
 #pragma unroll
-      for (int i = 1; i < 4; i++) tmax = fmaxf(tmax, fmaxf(p0[i], p1[i]));
+          for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const int key = k0 + 32 * h + 8 * lg + 4 * t + i;
+              p[h][t][i] = key <= pos ? p[h][t][i] : -INFINITY;
+            }
+      }
+      float tmax = p[0][0][0];
+#pragma unroll
+      for (int h = 0; h < kPfHalves; h++)
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) tmax = fmaxf(tmax, p[h][t][i]);
       tmax = max_xor32(max_xor16(tmax)) * a.qk_scale;
       const float m_new = fmaxf(m_run[j], tmax);  // finite: key 0 is in every row's first step
       const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
       float psum = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        p0[i] = __builtin_amdgcn_exp2f(fmaf(p0[i], a.qk_scale, -m_new));
-        p1[i] = __builtin_amdgcn_exp2f(fmaf(p1[i], a.qk_scale, -m_new));
-        psum += p0[i] + p1[i];
-      }
+      for (int h = 0; h < kPfHalves; h++)
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            p[h][t][i] = __builtin_amdgcn_exp2f(fmaf(p[h][t][i], a.qk_scale, -m_new));
+            psum += p[h][t][i];
+          }
       l_run[j] = l_run[j] * alpha + psum;
       m_run[j] = m_new;
-      pw[j][0] = pack_bf16x2_rne(p0[0], p0[1]);
-      pw[j][1] = pack_bf16x2_rne(p0[2], p0[3]);
-      pw[j][2] = pack_bf16x2_rne(p1[0], p1[1]);
-      pw[j][3] = pack_bf16x2_rne(p1[2], p1[3]);
+#pragma unroll
+      for (int h = 0; h < kPfHalves; h++) {
+        pw[j][h][0] = pack_bf16x2_rne(p[h][0][0], p[h][0][1]);
+        pw[j][h][1] = pack_bf16x2_rne(p[h][0][2], p[h][0][3]);
+        pw[j][h][2] = pack_bf16x2_rne(p[h][1][0], p[h][1][1]);
+        pw[j][h][3] = pack_bf16x2_rne(p[h][1][2], p[h][1][3]);
+      }
       if (__any(alpha != 1.0f)) {
 #pragma unroll
         for (int cc = 0; cc < 8; cc++)
@@ -593,32 +614,37 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // phase 2: O^T += V^T . P^T for every tile, half the V fragments (64 dims) at a time; the
-    // lane's 8 keys are slots 8 (lg % 2) .. + 7 of page lg / 2
+    // phase 2: O^T += V^T . P^T for every tile and half, a quarter of the V fragments (32
+    // dims of a half) at a time; the lane's 8 keys are slots 8 (lg % 2) .. + 7 of page lg / 2
 #pragma unroll
-    for (int hv = 0; hv < 2; hv++) {
-      Frag8 vf[4];
+    for (int h = 0; h < kPfHalves; h++) {
+      const uint16_t *kvsc = kvst + h * 4 * kPageHead;
+      const int kh = k0 + 32 * h;
 #pragma unroll
-      for (int c4 = 0; c4 < 4; c4++)
-        vf[c4].q = *(const uint4 *)(kvsc + (2 * (lg >> 1) + 1) * kPageHead + (16 * (4 * hv + c4) + lr) * kPage +
-                                    8 * (lg & 1));
-      if (k0 + 32 > kend) {  // slots past the keys may hold stale bits: their V is made 0
-        const int kb = k0 + 8 * lg;
+      for (int hv = 0; hv < 2; hv++) {
+        Frag8 vf[4];
 #pragma unroll
         for (int c4 = 0; c4 < 4; c4++)
+          vf[c4].q = *(const uint4 *)(kvsc + (2 * (lg >> 1) + 1) * kPageHead + (16 * (4 * hv + c4) + lr) * kPage +
+                                      8 * (lg & 1));
+        if (kh + 32 > kend) {  // slots past the keys may hold stale bits: their V is made 0
+          const int kb = kh + 8 * lg;
 #pragma unroll
-          for (int w2 = 0; w2 < 4; w2++) vf[c4].u[w2] = mask_pair(vf[c4].u[w2], kb + 2 * w2, kend);
+          for (int c4 = 0; c4 < 4; c4++)
+#pragma unroll
+            for (int w2 = 0; w2 < 4; w2++) vf[c4].u[w2] = mask_pair(vf[c4].u[w2], kb + 2 * w2, kend);
+        }
+#pragma unroll
+        for (int j = 0; j < kPfTiles; j++) {
+          if (k0 > tile_last[j]) continue;
+          Frag8 pf;
+#pragma unroll
+          for (int i = 0; i < 4; i++) pf.u[i] = pw[j][h][i];
+#pragma unroll
+          for (int c4 = 0; c4 < 4; c4++) o[j][4 * hv + c4] = mfma16x16x32(vf[c4], pf, o[j][4 * hv + c4]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int j = 0; j < kPfTiles; j++) {
-        if (k0 > tile_last[j]) continue;
-        Frag8 pf;
-#pragma unroll
-        for (int i = 0; i < 4; i++) pf.u[i] = pw[j][i];
-#pragma unroll
-        for (int c4 = 0; c4 < 4; c4++) o[j][4 * hv + c4] = mfma16x16x32(vf[c4], pf, o[j][4 * hv + c4]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
     }
   }
 #undef PF_STAGE
