@@ -408,14 +408,15 @@ __global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restri
 // append already wrote (mx.fast.scaled_dot_product_attention with mask = "causal" over the
 // slot's keys, Q36/model/attention.py:70-74).  A workgroup owns kPfWaves * kPfTiles 16-row
 // q tiles of one kv head -- a tile's rows are 16 / G tokens x the G q heads that share the
-// kv head -- and streams the keys up to its last token in 32-key steps through LDS, so each
+// kv head -- and streams the keys up to its last token in steps of kPfHalves x 32 keys through
+// LDS (one barrier and one softmax update a step), so each
 // K/V byte it reads serves all its tokens; per step and tile the arithmetic is the decode
 // kernel's (S^T = K . Q^T, online softmax in the exp2 domain, O^T += V^T . P^T), with keys
 // past a row's position masked.  A token's result depends only on its q row and its keys:
 // the steps and their order are the same wherever the token's tile sits.
 constexpr int kPfWaves = 8, kPfTiles = 2;
-constexpr int kPfHalves = 2;                                           // 32-key halves of a step
-constexpr int kPfStages = 4;                                           // LDS ring depth (steps)
+constexpr int kPfHalves = 4;                                           // 32-key halves of a step
+constexpr int kPfStages = 2;                                           // LDS ring depth (steps)
 constexpr int kPfChunks = kPfHalves * 4 * kPageHead * 2 / 1024 / kPfWaves;  // 1 KB chunks of a step per wave
 constexpr int kPfMaxPages = 4096;  // page ids of a workgroup's keys, held in LDS
 
@@ -432,7 +433,7 @@ struct PrefillArgs {
 };
 
 __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const PrefillArgs a) {
-  // a ring of kPfStages steps of 64 keys, each two halves of K0, V0, K1, V1 of their two pages
+  // a ring of kPfStages steps of kPfHalves x 32 keys, each half K0, V0, K1, V1 of its two pages
   // (4 KB each), filled by direct global->LDS loads kPfStages - 1 steps ahead of the step
   // being computed
   __shared__ __attribute__((aligned(16))) uint16_t kvs[kPfStages][kPfHalves * 4 * kPageHead];
@@ -550,7 +551,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-    // online softmax of every tile over the step's 64 keys
+    // online softmax of every tile over the step's keys
     uint32_t pw[kPfTiles][kPfHalves][4];  // P^T fragments (bf16 pairs; set for the tiles the step reaches)
 #pragma unroll
     for (int j = 0; j < kPfTiles; j++) {
