@@ -1,11 +1,15 @@
 """Benchmark of the ragged MoE decode step on one MI355X (prints ONE JSON line).
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--layers 48] [--no-graph]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--layers 48] [--no-graph] [--no-bs1]
 
 config 2 (the default; BASELINE.json configs[2], the workload the metric is quoted on): ragged
 continuous-batch decode of 32 sequences over the paged KV pool through 48 layers of the 4-bit
 Qwen3-MoE-style block; a step decodes one token per sequence (value = tokens/s).  The step is
-captured once as a HIP graph and replayed (--no-graph times eager launches).
+captured once as a HIP graph and replayed (--no-graph times eager launches).  The metric's bs=1
+half -- config 4 on the same model -- is measured after it and reported in the line's "bs1" object
+(--no-bs1 leaves it out).
+config 4: single-sequence decode at 262,144 KV tokens through the 48
+layers (value = tokens/s).
 config 3: one mixed chunked-prefill + decode step of one block -- 4 x 512
 prefill tokens (causal attention over their contexts) + 60 decode rows, the MoE on the segment GEMM
 (value = rows/s; MFMA roofline of the dominant kernel).
@@ -347,21 +351,47 @@ def bench_config3(steps: int, warmup: int, dev: str) -> dict:
     }
 
 
-def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int = 48) -> dict:
-    """ragged continuous-batch decode over the paged KV pool -- 32 sequences
-    with lengths log-uniform in [128, 32768], 16-token pages in a random permutation, the full
-    Qwen3-MoE-style 4-bit decoder block for 48 layers with independent seeded weights.  A step
-    decodes one token per sequence through all layers (each row writes position L_b and attends
-    to L_b + 1 keys)."""
+CONFIG4_KEYS = 262144  # one sequence decoding at 262,144 KV tokens
+
+
+def decode_model(cfg, seed: int, dev: str):
+    """The 48-layer model of a decode config: layer l's weights seeded with seed * 100 + l.  Also
+    returns layer 0's weights (the CPU baseline's layer)."""
+    from jitengine_amd.model import DecoderLayer, Model, random_layer_weights
+
+    layers, w0 = [], None
+    for l in range(cfg.layers):
+        w = random_layer_weights(cfg, seed * 100 + l, dev)
+        layers.append(DecoderLayer(cfg, w))
+        if l == 0:
+            w0 = w
+        del w
+    model = Model.__new__(Model)
+    model.cfg, model.layers = cfg, layers
+    return model, w0
+
+
+def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_layers: int = 48,
+                 model=None, cpu: bool = True) -> dict:
+    """A decode step of the 4-bit Qwen3-MoE-style model over the paged KV pool (16-token pages in a
+    random permutation of the pool), one token per sequence through every layer (each row writes
+    position L_b and attends to L_b + 1 keys).
+    config 2: 32 sequences with lengths log-uniform in [128, 32768], 48 layers
+    with independent seeded weights.
+    config 4: one sequence at 262,144 KV tokens (the step's own token is the
+    262,144th key), 48 layers; `model` may pass in config 2's weights, which are as random as its own."""
     import oracle
     from jitengine_amd import ops
-    from jitengine_amd.model import DecoderLayer, MoEConfig, Model, make_step_state, random_layer_weights, rope_inv_freq
+    from jitengine_amd.model import MoEConfig, make_step_state, rope_inv_freq
 
-    cfg = MoEConfig(layers=n_layers)
-    seed = seed_for(2)
+    seed = seed_for(config)
     rng = np.random.default_rng(seed)
-    B = 32
-    lens = np.round(np.exp(rng.uniform(np.log(128), np.log(32768), B))).astype(np.int32)
+    if config == 2:
+        B = 32
+        lens = np.round(np.exp(rng.uniform(np.log(128), np.log(32768), B))).astype(np.int32)
+    else:
+        B = 1
+        lens = np.array([CONFIG4_KEYS - 1], np.int32)
     npg = (lens + 1 + 15) // 16
     num_pages = int(npg.sum())
     perm = rng.permutation(num_pages)
@@ -370,15 +400,11 @@ def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int 
     for b in range(B):
         table[b, :npg[b]] = perm[at:at + npg[b]]
         at += npg[b]
-    layers, w0 = [], None
-    for l in range(n_layers):
-        w = random_layer_weights(cfg, seed * 100 + l, dev)
-        layers.append(DecoderLayer(cfg, w))
-        if l == 0:
-            w0 = w
-        del w
-    model = Model.__new__(Model)
-    model.cfg, model.layers = cfg, layers
+    w0 = None
+    if model is None:
+        model, w0 = decode_model(MoEConfig(layers=n_layers), seed, dev)
+    cfg = model.cfg
+    n_layers = cfg.layers
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed + 7)
     pools = [torch.randn((num_pages, cfg.kv_heads, 2, 16 * 128), generator=gen, device=dev, dtype=torch.bfloat16)
@@ -473,10 +499,42 @@ def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int 
               "down": float(np.mean(U)) * 884736}
     dom = max(kus, key=kus.get)
     achieved = alg_op[dom] / (kus[dom] * 1e-6) / 1e9 if dom in alg_op else None
-    traffic = profile_traffic(f"{dom}_config2")
 
-    # CPU baseline: the oracle's decoder layer (layer 0's weights and pool) on all 32 rows, median
-    # of 5 after a warm-up, scaled to the 48 layers of a step
+    traffic = profile_traffic(f"{dom}_config{config}")
+    if config == 2:
+        workload = (f"config2: ragged 32-sequence decode, {n_layers} layers of the Qwen3-MoE-style 4-bit block, "
+                    "paged bf16 KV (16-token pages, permuted), lens log-uniform [128, 32768]")
+    else:
+        workload = (f"config4: single-sequence decode at {CONFIG4_KEYS} KV tokens, {n_layers} layers of the "
+                    "Qwen3-MoE-style 4-bit block, paged bf16 KV (16-token pages, permuted), split-K attention")
+    res = {
+        "metric": "decode tok/s (bs=1, ragged bs=32) + achieved HBM GB/s as % of MI355X peak",
+        "value": B / (ms * 1e-3),
+        "unit": "tokens/s",
+        "ms_per_step": ms,
+        "dtype": "bf16",
+        "config": {"workload": workload,
+                   "weights": "MLX 4-bit affine g64 (bf16 scale/bias), dequantized in registers; fp32 accumulate",
+                   "sequences": B, "layers": n_layers, "kv_tokens": int(lens.sum()), "lens_min": int(lens.min()),
+                   "lens_max": int(lens.max()), "distinct_experts_mean": float(np.mean(U)),
+                   "hip_graph": bool(graph), "ms_per_step_eager": ms_eager},
+        "step_hbm": {"alg_bytes": alg_step, "GB_s": alg_step / (ms * 1e-3) / 1e9,
+                     "frac": alg_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "split": {"experts": sum(U) * per_expert, "kv": n_layers * kv, "dense": n_layers * dense}},
+        "op_us": kus,
+        "op_us_per_step": step_us,
+        "op_us_sum_per_step": sum(step_us.values()),
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": (achieved / HBM_PEAK_GBS) if achieved else None, "traffic": traffic,
+                     "alg_bytes_per_launch": alg_op.get(dom), "launch_us": kus[dom]},
+        "_y": y,
+        "_model": model,
+    }
+    if not cpu or w0 is None:
+        return res
+
+    # CPU baseline: the oracle's decoder layer (layer 0's weights and pool) on all rows, median of
+    # 5 after a warm-up, scaled to the 48 layers of a step
     def host_q(lin):
         return (lin.weight.cpu().numpy().view(np.uint32), lin.scales.view(torch.int16).cpu().numpy().view(np.uint16),
                 lin.biases.view(torch.int16).cpu().numpy().view(np.uint16))
@@ -498,33 +556,11 @@ def bench_config2(steps: int, warmup: int, dev: str, graph: bool, n_layers: int 
             times.append(time.perf_counter() - c0)
     cpu_tps = B / (float(np.median(times)) * n_layers)
 
-    return {
-        "metric": "decode tok/s (bs=1, ragged bs=32) + achieved HBM GB/s as % of MI355X peak",
-        "value": B / (ms * 1e-3),
-        "unit": "tokens/s",
-        "ms_per_step": ms,
-        "dtype": "bf16",
-        "config": {"workload": f"config2: ragged 32-sequence decode, {n_layers} layers of the Qwen3-MoE-style 4-bit "
-                               "block, paged bf16 KV (16-token pages, permuted), lens log-uniform [128, 32768]",
-                   "weights": "MLX 4-bit affine g64 (bf16 scale/bias), dequantized in registers; fp32 accumulate",
-                   "sequences": B, "layers": n_layers, "kv_tokens": int(lens.sum()), "lens_min": int(lens.min()),
-                   "lens_max": int(lens.max()), "distinct_experts_mean": float(np.mean(U)),
-                   "hip_graph": bool(graph), "ms_per_step_eager": ms_eager},
-        "step_hbm": {"alg_bytes": alg_step, "GB_s": alg_step / (ms * 1e-3) / 1e9,
-                     "frac": alg_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                     "split": {"experts": sum(U) * per_expert, "kv": n_layers * kv, "dense": n_layers * dense}},
-        "op_us": kus,
-        "op_us_per_step": step_us,
-        "op_us_sum_per_step": sum(step_us.values()),
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": (achieved / HBM_PEAK_GBS) if achieved else None, "traffic": traffic,
-                     "alg_bytes_per_launch": alg_op.get(dom), "launch_us": kus[dom]},
-        "cpu_baseline": {"value": cpu_tps, "unit": "tokens/s", "cores": cpu_threads(), "kind": "port",
-                         "sample": f"oracle decoder layer (C, float64 dots, OpenMP) on all {B} rows with layer 0's "
-                                   f"weights and KV ({int(lens.sum())} keys), median of 5 after a warm-up, "
-                                   f"x {n_layers} layers"},
-        "_y": y,
-    }
+    res["cpu_baseline"] = {
+        "value": cpu_tps, "unit": "tokens/s", "cores": cpu_threads(), "kind": "port",
+        "sample": f"oracle decoder layer (C, float64 dots, OpenMP) on all {B} rows with layer 0's weights and KV "
+                  f"({int(lens.sum())} keys), median of 5 after a warm-up, x {n_layers} layers"}
+    return res
 
 
 def copy_calibration(dev: str) -> int:
@@ -579,7 +615,7 @@ def rocprof_summary(args) -> int:
 
     d_dir = args.rocprof_summary
     stats = {r["Name"]: r for r in csv.DictReader(open(os.path.join(d_dir, "kt", "kt_kernel_stats.csv")))}
-    cfg = "" if args.config == 2 else f" --config {args.config}"
+    cfg = " --no-bs1" if args.config == 2 else f" --config {args.config}"
     print(f"# rocprofv3 summary of bench.py's config-{args.config} workload, op {args.op}")
     print("# made on one MI355X from the repository root by:")
     print(f"#   rocprofv3 --kernel-trace --stats -f csv -d prof/kt -o kt -- python3 bench.py{cfg} --steps 10 --warmup 2")
@@ -596,7 +632,7 @@ def rocprof_summary(args) -> int:
             print(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:9.2f} "
                   f"{float(r['MaxNs']) / 1e3:9.2f} {100 * float(r['TotalDurationNs']) / tot:6.1f}%  {name}")
         return 0
-    ng = " --no-graph" if args.config == 2 else ""  # (config 3 always replays a graph)
+    ng = " --no-graph" if args.config in (2, 4) else ""  # (config 3 always replays a graph)
     for c in (f"FETCH_SIZE -f csv -d prof/fetch -o fetch -- python3 bench.py{cfg} --steps 1 --warmup 1{ng}",
               f"WRITE_SIZE -f csv -d prof/write -o write -- python3 bench.py{cfg} --steps 1 --warmup 1{ng}",
               "FETCH_SIZE -f csv -d prof/cfetch -o cfetch -- python3 bench.py --copy-calibration",
@@ -642,6 +678,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph replay")
+    ap.add_argument("--no-bs1", action="store_true",
+                    help="config 2 only: skip the bs=1 (config 4) measurement reported beside it")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--rocprof-summary", metavar="DIR",
                     help="summarise rocprofv3 CSV output under DIR (kt/, fetch/, write/, cfetch/, cwrite/)")
@@ -659,20 +697,33 @@ def main() -> int:
         return copy_calibration(dev)
     if args.config == 1:
         res = bench_config1(args.steps, args.warmup, dev)
-    elif args.config == 2:
-        res = bench_config2(args.steps, args.warmup, dev, graph=not args.no_graph, n_layers=args.layers)
+    elif args.config in (2, 4):
+        res = bench_decode(args.config, args.steps, args.warmup, dev, graph=not args.no_graph,
+                           n_layers=args.layers)
+        if args.config == 2 and not args.no_bs1:
+            # the metric's bs=1 half: config 4 on the same model, reported beside config 2
+            model = res.pop("_model")
+            torch.cuda.empty_cache()
+            r4 = bench_decode(4, args.steps, args.warmup, dev, graph=not args.no_graph, model=model, cpu=False)
+            res["bs1"] = {"workload": r4["config"]["workload"] + " (config 2's weights)",
+                          "value": r4["value"], "unit": "tokens/s", "ms_per_step": r4["ms_per_step"],
+                          "step_hbm": r4["step_hbm"], "op_us_per_step": r4["op_us_per_step"],
+                          "attention": {k: r4["roofline"][k] for k in ("achieved", "alg_bytes_per_launch",
+                                                                        "launch_us")} | {"unit": "GB/s"}}
+            del r4, model
     elif args.config == 3:
         res = bench_config3(args.steps, args.warmup, dev)
     else:
         print(f"config {args.config} is not wired into bench.py", file=sys.stderr)
         return 2
     res.pop("_y", None)
+    res.pop("_model", None)
     line = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
             "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to MLX 4-bit g64)",
             "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"]}
-    for key in ("step_hbm", "step_tflops", "op_us", "op_us_per_step", "op_us_sum_per_step", "kernels_us"):
+    for key in ("step_hbm", "step_tflops", "op_us", "op_us_per_step", "op_us_sum_per_step", "kernels_us", "bs1"):
         if key in res:
             line[key] = res[key]
     print(json.dumps(line), flush=True)

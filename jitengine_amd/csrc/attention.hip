@@ -7,8 +7,9 @@
 // dim-major -- [128 dims][16 slots], so a fragment's 16 dims x 4 slots per lane
 // group are 512 B contiguous.
 //
-// Attention work item: one workgroup per 1536-key chunk of one sequence and 2 kv heads,
-// 4 waves per kv head, each wave streaming a quarter of the chunk (384 keys) two 16-key
+// Attention work item: one workgroup per chunk (1536 keys; longer for sequences past
+// 196,608 keys) of one sequence and 2 kv heads, 4 waves per kv head, each wave streaming
+// a quarter of the chunk (384 keys) two 16-key
 // pages (32 keys) per step; the 4 waves' states meet in LDS:
 //   S^T[16 keys x 16 q heads] = K_page . Q^T      (4 MFMA 16x16x32 per page)
 //   online softmax in the exp2 domain (fp32 running max / sum per q head)
@@ -41,17 +42,29 @@ constexpr int kChunk = JIT_ATTN_CHUNK;
 #define JIT_ATTN_SPLITS 4
 #endif
 constexpr int kAttnSplits = JIT_ATTN_SPLITS;  // waves per kv head and chunk
+// A sequence longer than kLongChunks chunks of kChunk keys is cut into about kLongChunks
+// chunks instead (two workgroups each: one per CU of MI355X's 256), so that a lone long
+// sequence still fills the chip in one even wave of workgroups (262,144 keys: 128 chunks of
+// 2048, 100 us a layer against 116 us for 171 chunks of 1536).  A wave's run stays at most
+// 64 pages (one page id per lane), hence the cap.
+constexpr int kLongChunks = 128;
+constexpr int kChunkMax = 64 * kPage * kAttnSplits;
+static_assert(kChunk % (32 * kAttnSplits) == 0 && kChunk <= kChunkMax, "a wave's run is whole 32-key steps");
+
+__host__ __device__ __forceinline__ int chunk_tokens(int len) {
+  if (len <= kChunk * kLongChunks) return kChunk;
+  constexpr int kStep = 32 * kAttnSplits;
+  const int c = ((len + kLongChunks - 1) / kLongChunks + kStep - 1) / kStep * kStep;
+  return c < kChunkMax ? c : kChunkMax;
+}
 
 __device__ __forceinline__ int k_off(int slot, int d) { return k_page_offset(slot, d); }
 
 }  // namespace
 
 // Chunk length rule: a pure function of the sequence's own length (so results do
-// not depend on the batch); one size serves every length.
-extern "C" int jit_attn_chunk_tokens(int len) {
-  (void)len;
-  return kChunk;
-}
+// not depend on the batch).
+extern "C" int jit_attn_chunk_tokens(int len) { return chunk_tokens(len); }
 
 namespace {
 
@@ -141,7 +154,7 @@ __device__ __forceinline__ uint32_t mask_pair(uint32_t w, int k, int L) {
   return (k < L ? (w & 0xffffu) : 0u) | (k + 1 < L ? (w & 0xffff0000u) : 0u);
 }
 
-// WS waves share a kv head's chunk: wave s streams keys [s * kChunk / WS, (s + 1) * kChunk / WS)
+// WS waves share a kv head's chunk of ck keys: wave s streams keys [s * ck / WS, (s + 1) * ck / WS)
 // of it, and the workgroup merges the WS (max, sum, o) states in LDS in wave order, so a
 // chunk's result depends only on its keys.  More waves with shorter key runs each keep more
 // loads in flight than one wave per kv head walking the whole chunk.
@@ -149,8 +162,7 @@ constexpr int kStateFloats = 32 + 2;  // o[8][4], max, sum per lane
 
 template <int WS>
 __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
-  static_assert(kChunk % (32 * WS) == 0, "a wave's key run is whole 32-key steps");
-  constexpr int kRun = kChunk / WS;
+  static_assert(WS == kAttnSplits, "the chunk rule rounds to whole 32-key steps of each of WS waves");
   extern __shared__ float xstate[];  // [WS - 1][hb][kStateFloats][64]
   const int gc = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
@@ -161,14 +173,15 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
   const int b = a.chunk_seq[gc];
   const int L = a.lens[b];
   const int c = gc - a.chunk_start[b];
-  const int nchunks = (L + kChunk - 1) / kChunk;
+  const int ck = chunk_tokens(L), kRun = ck / WS;
+  const int nchunks = (L + ck - 1) / ck;
   const int lr = l & 15, lg = l >> 4;
   const int G = a.G;
-  const int wk0 = c * kChunk + split * kRun;
-  const int wk1 = min(c * kChunk + (split + 1) * kRun, L);
+  const int wk0 = c * ck + split * kRun;
+  const int wk1 = min(c * ck + (split + 1) * kRun, L);
   const int npg = wk1 > wk0 ? (wk1 - wk0 + kPage - 1) / kPage : 0;  // split 0 always holds a key
   const int nst = live ? (npg + 1) >> 1 : 0;                          // 32-key steps
-  // the run's page ids, one per lane (at most kRun / 16 <= 24)
+  // the run's page ids, one per lane (at most kRun / 16 <= 64)
   const int my_page = l < npg ? a.page_table[(long long)b * a.max_pages + (wk0 >> 4) + l] : 0;
   const int last = npg - 1;
   // page id i of the chunk (past the last page: the last page again, whose keys are
@@ -350,7 +363,8 @@ __global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restri
                                                          uint16_t *__restrict__ out) {
   const int b = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
   const int L = lens[b];
-  const int n = (L + kChunk - 1) / kChunk;
+  const int ck = chunk_tokens(L);
+  const int n = (L + ck - 1) / ck;
   if (n <= 1) return;
   const long long c0 = chunk_start[b];
   __shared__ float s_max[512 / 64];

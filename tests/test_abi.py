@@ -64,14 +64,17 @@ def test_contract_breaks_return_einval_before_launch():
 
 def test_attn_plan_is_a_function_of_each_length():
     lib = _lib.lib()
-    lens = np.array([1, 255, 256, 1535, 1536, 1537, 16385, 262144], np.int32)
+    lens = np.array([1, 255, 256, 1535, 1536, 1537, 16385, 196608, 196609, 200003, 262144, 1 << 20], np.int32)
     cs = np.zeros(lens.size + 1, np.int32)
     seq = np.zeros(2000, np.int32)
     total = lib.jit_attn_plan(lens.ctypes.data_as(ctypes.c_void_p), lens.size, cs.ctypes.data_as(ctypes.c_void_p),
                               seq.ctypes.data_as(ctypes.c_void_p), seq.size)
     ck = [lib.jit_attn_chunk_tokens(int(L)) for L in lens]
     n = [-(-int(L) // c) for L, c in zip(lens, ck)]
-    assert ck == [1536] * 8
+    # 1536-key chunks up to 128 of them; a longer sequence gets about 128 chunks, whole 128-key
+    # steps (32 keys for each of 4 waves), at most 4096 keys (a wave's run of at most 64 pages)
+    assert ck == [1536] * 8 + [1664, 1664, 2048, 4096]
+    assert n[7:] == [128, 119, 121, 128, 256]
     assert total == sum(n)
     assert list(cs) == list(np.concatenate([[0], np.cumsum(n)]))
     for b in range(lens.size):

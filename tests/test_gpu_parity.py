@@ -327,10 +327,11 @@ def test_paged_attention_parity():
         assert_close_bf16(got[b], want[b], max_abs=2e-2, min_cos=0.9995, what=f"attention L={L}")
 
 
-def test_paged_attention_long_context():
+@pytest.mark.parametrize("L", [262144, 200003])
+def test_paged_attention_long_context(L):
     """BASELINE config 4's shape: one sequence of 262,144 keys in permuted 16-token pages
-    (171 chunks split over 4 waves per kv head, merged in chunk order)."""
-    L = 262144
+    (128 chunks of 2048 keys split over 4 waves per kv head, merged in chunk order); and a
+    length just past the 1536-key rule (121 chunks of 1664, the last one partial)."""
     q, pool, table = _pool([L], seed=23)
     got = _attn(q, pool, table, [L])
     want = oracle.paged_decode_attn(q, pool, table, [L], 128 ** -0.5)
