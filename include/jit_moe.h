@@ -286,6 +286,31 @@ int jit_paged_prefill_attn(const uint16_t *q, const uint16_t *pool, const int32_
                            const int32_t *blk_chunk, const int32_t *blk_q0, int nblk, int H, int Hkv,
                            float scale, uint16_t *out, void *stream);
 
+/* ------------------------------------------------------------------ step ends and KV pages */
+
+/* Embedding lookup of MLX 4-bit affine rows: out[b] = dequantize(weight[ids[b]]) [B, D] bf16,
+ * weight [V, D/8] u32 (nibble i of word j = column 8j + i), scales/biases [V, D/64] bf16, each
+ * value bf16(bf16(scale * q) + bias) -- mx.dequantize in bf16 arithmetic
+ * (QEmbedding.lookup, Q36/linear.py:680-690).  An id outside [0, V) gives a zero row (callers
+ * validate token ids on the host).  Contract: D % 64 == 0 (JIT_EUNSUPPORTED). */
+int jit_embed_q4(const int32_t *ids, int B, const uint32_t *weight, const uint16_t *scales,
+                 const uint16_t *biases, int V, int D, uint16_t *out, void *stream);
+
+/* Greedy choice: out[b] = the first index of the largest of logits[b, 0..V) (bf16).  The
+ * reference takes mx.argmax of the log-probabilities (Sampler.__call__ with temperature 0,
+ * Q36/sampler.py:371-374); log-softmax is monotone per row, so the index is the same.  NaN
+ * never wins against a number; a row of NaNs gives 0. */
+int jit_argmax_rows(const uint16_t *logits, int B, int V, int32_t *out, void *stream);
+
+/* Copy page src[i] to page dst[i] (i < n; device arrays) inside one layer's pool
+ * [num_pages, Hkv, 2, 16 * 128] bf16: the copy-on-write of a shared page before a sequence
+ * writes into it.  It replaces the reference's snapshot copies of a stored prefix
+ * (RequestState.snapshot / restore, Q36/kvcache/state.py:58-149; KVSlot.load,
+ * Q36/kvcache/kv_cache.py:38-58): full pages of a prefix are shared, only its partial last
+ * page is copied.  A page id outside [0, num_pages) copies nothing. */
+int jit_kv_copy_pages(uint16_t *pool, int num_pages, int Hkv, const int32_t *src, const int32_t *dst, int n,
+                      void *stream);
+
 #ifdef __cplusplus
 }
 #endif

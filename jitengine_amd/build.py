@@ -32,6 +32,7 @@ SOURCES = {
     "qmm_seg.hip": [],
     "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "block.hip": [],
+    "head.hip": [],
 }
 
 _COMMON = [

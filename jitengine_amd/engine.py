@@ -1,0 +1,210 @@
+"""Continuous-batching generation over the paged KV pool (greedy draws).
+
+Mirrors the reference's scheduler loop (Q36/scheduler/scheduler.py, admission.py, prefill.py,
+decode.py, retire.py) on this build's pieces:
+  * admission (AdmissionMixin._admit, Q36/scheduler/admission.py:19-51): strict FIFO; a request is
+    charged its whole generation (prompt + max_tokens positions, :82-88) in KV pages up front, and
+    the first request that does not fit stops admission until pages come back;
+  * a prefix already in the prefix store is restored instead of recomputed -- here by sharing its
+    pages (PrefixStore), where the reference copies a snapshot (Q36/kvcache/state.py:121-149);
+  * every step runs the decoding rows (one token each) together with prompt chunks of the
+    requests still in prefill (at most prefill_chunk tokens each, max_step_tokens in all), as the
+    reference's mixed chunked-prefill step does; a step with no prompt chunk is the batched decode
+    step (Model.decode_step);
+  * a request retires on an end-of-sequence token or after max_tokens tokens
+    (Q36/scheduler/retire.py); its prompt's pages then go to the prefix store and the rest of its
+    reservation back to the pool.
+Tokens are drawn greedily on the GPU (jit_argmax_rows).
+"""
+
+from __future__ import annotations
+
+import itertools
+from collections import deque
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from .kvpool import KVPool, PoolExhausted, PrefixStore, pages_for
+from .ops import PAGE
+from .model import CausalLM, make_mixed_state, make_step_state
+
+
+@dataclass
+class Request:
+    rid: int
+    prompt: list
+    max_tokens: int
+    eos: frozenset
+    tokens: list = field(default_factory=list)  # generated so far
+    done_prompt: int = 0   # prompt positions whose KV is written (restored ones included)
+    cached: int = 0        # prompt positions restored from the prefix store
+    state: str = "queued"  # queued -> prefill -> decode -> done
+    finish_reason: str | None = None
+    reserved: int = 0      # pages charged at admission and not yet allocated
+
+    @property
+    def length(self) -> int:
+        """KV positions written so far."""
+        return self.done_prompt + max(0, len(self.tokens) - 1)
+
+
+class Engine:
+    """Requests in, greedy tokens out, many sequences per step over one KV pool."""
+
+    def __init__(self, lm: CausalLM, num_pages: int, prefill_chunk: int = 512, max_step_tokens: int = 2048,
+                 prefix_store: bool = True, page_seed: int | None = None, device=None, allocate: bool = True):
+        if prefill_chunk <= 0 or max_step_tokens <= 0:
+            raise ValueError("prefill_chunk and max_step_tokens must be positive")
+        self.lm = lm
+        cfg = lm.cfg
+        dev = device if device is not None else lm.final_norm.device
+        self.device = torch.device(dev)
+        self.pool = KVPool(len(lm.layers), num_pages, cfg.kv_heads, self.device, seed=page_seed, allocate=allocate)
+        self.store = PrefixStore(self.pool) if prefix_store else None
+        self.prefill_chunk = int(prefill_chunk)
+        self.max_step_tokens = int(max_step_tokens)
+        self.queue: deque = deque()
+        self.rows: list = []       # admitted requests, in admission order
+        self.outstanding = 0       # pages charged to admitted requests, not yet allocated
+        self.deferred = 0          # admission attempts stopped by the pool
+        self.steps = 0
+        self._ids = itertools.count()
+
+    # ------------------------------------------------------------------ requests
+    def submit(self, prompt, max_tokens: int, eos=None) -> Request:
+        prompt = [int(t) for t in prompt]
+        if not prompt:
+            raise ValueError("empty prompt")
+        if max_tokens < 1:
+            raise ValueError("max_tokens must be >= 1")
+        if min(prompt) < 0 or max(prompt) >= self.lm.vocab:
+            raise ValueError(f"prompt token ids must lie in [0, {self.lm.vocab})")
+        need = pages_for(len(prompt) + max_tokens)
+        if need > self.pool.num_pages:
+            raise PoolExhausted(f"a generation of {len(prompt) + max_tokens} positions needs {need} pages, "
+                                f"the pool has {self.pool.num_pages}")
+        eos = frozenset(self.lm.eos_ids if eos is None else eos)
+        r = Request(next(self._ids), prompt, int(max_tokens), eos)
+        self.queue.append(r)
+        return r
+
+    @property
+    def busy(self) -> bool:
+        return bool(self.queue or self.rows)
+
+    def _admit(self) -> None:
+        while self.queue:
+            r = self.queue[0]
+            total = pages_for(len(r.prompt) + r.max_tokens)
+            n, pages = self.store.lookup(r.prompt) if self.store is not None else (0, [])
+            need = total - n // PAGE  # a shared partial page is copied before it is written
+            if self.pool.free_pages - self.outstanding < need and self.store is not None:
+                self.store.make_room(need + self.outstanding)
+                n, pages = self.store.lookup(r.prompt)  # (the entry may have been evicted)
+                need = total - n // PAGE
+            if self.pool.free_pages - self.outstanding < need:
+                self.deferred += 1
+                break  # strict FIFO
+            self.queue.popleft()
+            self.pool.open(r.rid, pages[: pages_for(n)], n)
+            r.done_prompt = r.cached = n
+            r.reserved = need
+            self.outstanding += need
+            r.state = "prefill"
+            self.rows.append(r)
+
+    def _write(self, r: Request, start: int, n: int) -> None:
+        before = self.pool.free_pages
+        self.pool.prepare_write(r.rid, start, n)
+        used = before - self.pool.free_pages
+        r.reserved -= used
+        self.outstanding -= used
+
+    def _retire(self, r: Request, reason: str) -> None:
+        r.state, r.finish_reason = "done", reason
+        if self.store is not None:
+            self.store.insert(r.prompt, self.pool.pages[r.rid])
+        self.pool.release(r.rid)
+        self.outstanding -= r.reserved
+        r.reserved = 0
+        self.rows.remove(r)
+
+    # ---------------------------------------------------------------------- step
+    def step(self) -> list:
+        """One scheduling round; returns the (request, token) pairs it drew."""
+        self._admit()
+        decode = [r for r in self.rows if r.state == "decode"]
+        budget = self.max_step_tokens - len(decode)
+        chunks = []
+        for r in self.rows:
+            if r.state == "prefill" and budget > 0:
+                n = min(self.prefill_chunk, len(r.prompt) - r.done_prompt, budget)
+                chunks.append((r, r.done_prompt, n))
+                budget -= n
+        if not decode and not chunks:
+            return []
+        for r, ctx, n in chunks:
+            self._write(r, ctx, n)
+        for r in decode:
+            self._write(r, r.length, 1)
+        lm, cfg, dev = self.lm, self.lm.cfg, self.device
+        dec_pos = np.array([r.length for r in decode], np.int32)
+        dec_ids = [r.tokens[-1] for r in decode]
+        if not chunks:
+            table = self.pool.page_table([r.rid for r in decode])
+            st = make_step_state(cfg, dec_pos, table)
+            x = lm.embed_tokens(torch.tensor(dec_ids, dtype=torch.int32, device=dev))
+            toks = lm.greedy(lm.model.decode_step(x, self.pool.pools, st))
+            drawn = list(zip(decode, toks.tolist()))
+        else:
+            ids = list(itertools.chain.from_iterable(r.prompt[c:c + n] for r, c, n in chunks)) + dec_ids
+            seqs = [r.rid for r, _, _ in chunks]
+            w = max(1, max(len(self.pool.pages[s]) for s in seqs + [r.rid for r in decode]))
+            seq_table = self.pool.page_table_host(seqs, w)
+            dec_table = self.pool.page_table_host([r.rid for r in decode], w)
+            ms = make_mixed_state(cfg, [(i, c, n) for i, (_, c, n) in enumerate(chunks)], seq_table, dec_pos,
+                                  dec_table, dev)
+            x = lm.embed_tokens(torch.tensor(ids, dtype=torch.int32, device=dev))
+            for layer, pool in zip(lm.layers, self.pool.pools):
+                x = layer.mixed(x, pool, ms)
+            want, rows = [], []
+            end = 0
+            for r, c, n in chunks:
+                end += n
+                if c + n == len(r.prompt):
+                    want.append(end - 1)
+                    rows.append(r)
+            want += [ms.P + j for j in range(len(decode))]
+            rows += decode
+            drawn = []
+            if want:
+                sel = x[torch.tensor(want, dtype=torch.long, device=dev)].contiguous()
+                drawn = list(zip(rows, lm.greedy(sel).tolist()))
+            for r, c, n in chunks:
+                r.done_prompt = c + n
+        self.steps += 1
+        for r, t in drawn:
+            r.tokens.append(int(t))
+            r.state = "decode"
+        for r in list(self.rows):
+            if r.state == "decode" and r.tokens:
+                self.pool.lengths[r.rid] = r.length
+                if r.tokens[-1] in r.eos:
+                    self._retire(r, "stop")
+                elif len(r.tokens) >= r.max_tokens:
+                    self._retire(r, "length")
+            elif r.state == "prefill":
+                self.pool.lengths[r.rid] = r.done_prompt
+        return drawn
+
+    def run(self, max_steps: int | None = None) -> None:
+        """Step until every submitted request is done (or max_steps rounds)."""
+        n = 0
+        while self.busy and (max_steps is None or n < max_steps):
+            if not self.step() and not self.rows:
+                if self.queue:
+                    raise PoolExhausted("the queue head cannot be admitted into an idle pool")
+                break
+            n += 1

@@ -231,3 +231,53 @@ class Model:
             nxt = self.layers[i + 1].input_norm if i + 1 < len(self.layers) else None
             x, xn = layer.run(x, pool, st, xn=xn, next_norm=nxt)
         return x
+
+
+class CausalLM:
+    """The whole model around the decoder stack: 4-bit embedding table, final RMSNorm, 4-bit lm_head
+    and the greedy draw (Q36/model/model.py:248-270 `forward`: embed.lookup -> layers -> norm ->
+    lm_head; Q36/sampler.py:371-374 with temperature 0).  A tied head reads the embedding table."""
+
+    def __init__(self, model: Model, embed: QLinear, final_norm: torch.Tensor, lm_head: QLinear, vocab: int,
+                 eos_ids=(), prepack: bool = True):
+        embed.validate()
+        if embed.weight.dim() != 2 or embed.out_dims != vocab or embed.in_dims != model.cfg.hidden:
+            raise ValueError(f"embedding table must be [{vocab}, {model.cfg.hidden}]")
+        if lm_head.out_dims != vocab or lm_head.in_dims != model.cfg.hidden:
+            raise ValueError(f"lm_head must be [{vocab}, {model.cfg.hidden}]")
+        self.model, self.cfg = model, model.cfg
+        self.embed = embed
+        self.final_norm = final_norm.contiguous()
+        self.lm_head = ops.prepack(lm_head) if prepack else lm_head
+        self.vocab = int(vocab)
+        self.eos_ids = tuple(int(e) for e in eos_ids)
+
+    @property
+    def layers(self) -> list:
+        return self.model.layers
+
+    def embed_tokens(self, ids: torch.Tensor) -> torch.Tensor:
+        """ids int32 [B] -> hidden rows [B, D] bf16."""
+        return ops.embed_q4(ids, self.embed)
+
+    def logits(self, h: torch.Tensor) -> torch.Tensor:
+        """Last-layer rows [B, D] -> logits [B, V] bf16."""
+        return ops.qmm(ops.rmsnorm(h, self.final_norm, self.cfg.eps), self.lm_head)
+
+    def greedy(self, h: torch.Tensor) -> torch.Tensor:
+        """Last-layer rows -> the greedy token of each row, int32 [B]."""
+        return ops.argmax_rows(self.logits(h))
+
+
+def random_causal_lm(cfg: MoEConfig, vocab: int, seed: int, device, std: float = 0.02,
+                     prepack: bool = True) -> CausalLM:
+    """A seeded synthetic model of the geometry: random_layer_weights per layer, an N(0, std)
+    embedding table and lm_head quantized to 4-bit, a final norm 1 + N(0, std)."""
+    layers = [random_layer_weights(cfg, seed * 100 + l, device, std) for l in range(cfg.layers)]
+    model = Model(cfg, layers, prepack)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(int(seed) * 7 + 3)
+    final_norm = (1.0 + std * torch.randn(cfg.hidden, generator=gen, device=device)).to(torch.bfloat16)
+    embed = random_quantized((vocab, cfg.hidden), seed * 10 + 8, std, device)
+    head = random_quantized((vocab, cfg.hidden), seed * 10 + 9, std, device)
+    return CausalLM(model, embed, final_norm, head, vocab, (), prepack)

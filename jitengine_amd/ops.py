@@ -527,3 +527,41 @@ def paged_decode_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torc
         "paged_decode_attn",
     )
     return out
+
+
+# ----------------------------------------------------------------------------- step ends, KV pages
+def embed_q4(ids: torch.Tensor, table: QLinear) -> torch.Tensor:
+    """Embedding rows [B, D] bf16 of token ids [B] int32 from an MLX 4-bit table [V, D]
+    (QEmbedding.lookup, Q36/linear.py:680-690: mx.dequantize of the gathered rows)."""
+    _need(ids, torch.int32, "ids")
+    for t, n in ((table.weight, "weight"), (table.scales, "scales"), (table.biases, "biases")):
+        if not t.is_cuda:
+            raise ValueError(f"embedding {n} must be a device tensor")
+    if ids.dim() != 1 or table.weight.dim() != 2:
+        raise ValueError("embed_q4 takes ids [B] and a [V, D] table")
+    V, D = table.weight.shape[0], table.weight.shape[1] * 8
+    out = torch.empty((ids.shape[0], D), dtype=torch.bfloat16, device=ids.device)
+    _lib.check(_lib.lib().jit_embed_q4(_p(ids), ids.shape[0], _p(table.weight), _p(table.scales), _p(table.biases),
+                                       V, D, _p(out), _stream()), "embed_q4")
+    return out
+
+
+def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
+    """int32 [B]: the first index of each row's largest logit (the greedy draw of
+    Q36/sampler.py:371-374)."""
+    _need(logits, torch.bfloat16, "logits")
+    B, V = logits.shape
+    out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    _lib.check(_lib.lib().jit_argmax_rows(_p(logits), B, V, _p(out), _stream()), "argmax_rows")
+    return out
+
+
+def kv_copy_pages(pool: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) -> None:
+    """Copy pages src[i] -> dst[i] (int32 device tensors) inside one layer's pool."""
+    _need(pool, torch.bfloat16, "pool")
+    _need(src, torch.int32, "src")
+    _need(dst, torch.int32, "dst")
+    if src.shape != dst.shape or src.dim() != 1:
+        raise ValueError("src and dst must be equal-length 1-D page lists")
+    _lib.check(_lib.lib().jit_kv_copy_pages(_p(pool), pool.shape[0], _pool_heads(pool), _p(src), _p(dst),
+                                            src.shape[0], _stream()), "kv_copy_pages")

@@ -20,6 +20,8 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
   q4_prepack              a byte permutation (multiset of bytes preserved, every word placed once);
                           on the GPU, GEMMs on packed and MLX layouts agree bit for bit
   paged_decode_attn       vs torch scaled_dot_product_attention in float64 on gathered KV
+  embed_q4                vs torch's own bf16 multiply and add (a library routine), q = 0 rows = bias
+  argmax_rows             vs numpy argmax (first index of the maximum) on NaN-free rows
 """
 
 from __future__ import annotations
@@ -372,4 +374,36 @@ def paged_decode_attn(q, pool, page_table, lens, scale: float) -> np.ndarray:
         ),
         "paged_decode_attn",
     )
+    return out
+
+
+def embed_q4(ids, w, s, b) -> np.ndarray:
+    """bf16 rows [B, D] of an MLX 4-bit table: mx.dequantize of the gathered rows
+    (Q36/linear.py:680-690) in bf16 arithmetic, bf16(bf16(scale * q) + bias) per value; an id
+    outside [0, V) gives a zero row."""
+    ids = np.asarray(ids, np.int64)
+    w, s, b = _u32(w), _u16(s), _u16(b)
+    V, D = w.shape[0], w.shape[1] * 8
+    out = np.zeros((ids.size, D), np.uint16)
+    ok = (ids >= 0) & (ids < V)
+    if ok.any():
+        rows = ids[ok]
+        q = ((w[rows][:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15).reshape(rows.size, D)
+        sc = np.repeat(bf16_to_f32(s[rows]), 64, axis=1)
+        bi = np.repeat(bf16_to_f32(b[rows]), 64, axis=1)
+        sq = bf16_to_f32(f32_to_bf16((sc * q.astype(np.float32)).astype(np.float32)))
+        out[ok] = f32_to_bf16((sq + bi).astype(np.float32))
+    return out
+
+
+def argmax_rows(logits) -> np.ndarray:
+    """int32 [B]: the first index of each row's largest bf16 logit (the greedy draw,
+    Q36/sampler.py:371-374); NaN entries never win, a row of NaNs gives 0."""
+    x = bf16_to_f32(_u16(logits)).astype(np.float64)
+    out = np.zeros(x.shape[0], np.int32)
+    for r in range(x.shape[0]):
+        ok = ~np.isnan(x[r])
+        if ok.any():
+            m = x[r][ok].max()
+            out[r] = int(np.flatnonzero(ok & (x[r] == m))[0])
     return out

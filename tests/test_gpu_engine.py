@@ -1,0 +1,176 @@
+"""The step's ends (embedding, lm_head + greedy draw), KV page copies, the continuous-batching
+engine and the checkpoint loader on MI355X.
+
+Kernel parity: embedding and argmax bit-exact against the oracle, page copies bit-exact, logits
+within the north-star tolerance.  Engine: generation is a function of each request alone --
+bit-identical tokens whether a request runs alone or batched with staggered others, whether its
+prompt's KV is computed or restored from the prefix store (shared pages, one copied), and when a
+small pool defers admission.  The engine tests keep every step under 64 rows, where every op takes
+its row-independent decode kernels (larger batches switch to the segment GEMMs, as the reference
+switches to its prefill kernels)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from jitengine_amd import checkpoint, ops
+from jitengine_amd.engine import Engine
+from jitengine_amd.model import CausalLM, DecoderLayer, Model, MoEConfig, random_causal_lm
+from jitengine_amd.quant import QLinear, random_quantized
+from tests.ckpt_util import config_dict, write_checkpoint
+from tests.helpers import assert_close_bf16, bf16_tensor, normal_bf16, u16
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+CFG = MoEConfig(layers=2, experts=32)
+VOCAB = 2048
+
+
+@pytest.fixture(scope="module")
+def lm():
+    return random_causal_lm(CFG, VOCAB, seed=11, device=DEV)
+
+
+def _np(lin: QLinear):
+    return (lin.weight.cpu().numpy().view(np.uint32), u16(lin.scales), u16(lin.biases))
+
+
+def test_embed_q4_matches_oracle():
+    tab = random_quantized((1000, 2048), 3, std=0.05, device=DEV)
+    ids = np.array([0, 999, 17, 512, 1000, -1, 17], np.int32)
+    got = u16(ops.embed_q4(torch.from_numpy(ids).to(DEV), tab))
+    want = oracle.embed_q4(ids, *_np(tab))
+    assert np.array_equal(got, want)
+    assert not got[4].any() and not got[5].any() and np.array_equal(got[2], got[6])
+
+
+@pytest.mark.parametrize("V", [151936, 1001])
+def test_argmax_rows_matches_oracle(V):
+    x = normal_bf16((6, V), seed=V)
+    x[1, [5, 77, V - 1]] = 0x4300  # 128.0 three times: the first index wins
+    x[2, 10:20] = 0x7FC0           # NaNs never win
+    x[2, 30] = 0x4400
+    x[3, :] = 0xFF80               # all -inf: index 0
+    x[4, :] = 0x7FC0               # all NaN: index 0
+    got = ops.argmax_rows(bf16_tensor(x, DEV)).cpu().numpy()
+    want = oracle.argmax_rows(x)
+    assert np.array_equal(got, want)
+    assert got[1] == 5 and got[2] == 30 and got[3] == 0 and got[4] == 0
+    ok = np.argmax(oracle.bf16_to_f32(x[[0, 5]]), axis=1)
+    assert np.array_equal(got[[0, 5]], ok)
+
+
+def test_kv_copy_pages_exact():
+    pool = normal_bf16((12, 4, 2, 16 * 128), seed=9)
+    pt = bf16_tensor(pool, DEV)
+    src, dst = np.array([3, 7, 0], np.int32), np.array([5, 1, 11], np.int32)
+    ops.kv_copy_pages(pt, torch.from_numpy(src).to(DEV), torch.from_numpy(dst).to(DEV))
+    want = pool.copy()
+    want[dst] = pool[src]
+    assert np.array_equal(u16(pt), want)
+
+
+def test_lm_logits_and_greedy(lm):
+    h = normal_bf16((5, CFG.hidden), seed=4)
+    logits = u16(lm.logits(bf16_tensor(h, DEV)))
+    hn, _ = oracle.rmsnorm(h, u16(lm.final_norm), CFG.eps)
+    _, want = oracle.qmm(hn, *_np(random_quantized((VOCAB, CFG.hidden), 11 * 10 + 9, device=DEV)))
+    assert_close_bf16(logits, want, what="logits")
+    assert np.array_equal(lm.greedy(bf16_tensor(h, DEV)).cpu().numpy(), oracle.argmax_rows(logits))
+
+
+def _prompts(seed, lens):
+    rng = np.random.default_rng(seed)
+    return [rng.integers(0, VOCAB, n).tolist() for n in lens]
+
+
+def _solo(lm, prompt, max_tokens, **kw):
+    e = Engine(lm, 64, prefill_chunk=16, max_step_tokens=48, **kw)
+    r = e.submit(prompt, max_tokens, eos=())
+    e.run()
+    return r.tokens
+
+
+def test_engine_batched_equals_solo(lm):
+    prompts = _prompts(1, [5, 17, 33, 40, 9])
+    e = Engine(lm, 128, prefill_chunk=16, max_step_tokens=48, page_seed=7)
+    reqs = [e.submit(p, 6, eos=()) for p in prompts[:2]]
+    e.step()
+    e.step()
+    reqs += [e.submit(p, 6, eos=()) for p in prompts[2:]]
+    e.run()
+    assert e.pool.free_pages + sum(len(v) for v in e.store.entries.values()) == 128
+    for r, p in zip(reqs, prompts):
+        assert r.finish_reason == "length" and len(r.tokens) == 6
+        assert r.tokens == _solo(lm, p, 6, prefix_store=False), r.rid
+
+
+def test_engine_prefix_sharing_is_exact(lm):
+    base, = _prompts(2, [40])
+    ext = _prompts(3, [10, 7])
+    e = Engine(lm, 128, prefill_chunk=16, max_step_tokens=48)
+    a = e.submit(base, 4, eos=())
+    e.run()
+    stored = list(e.store.entries[tuple(base)])
+    before = [u16(p[stored]) for p in e.pool.pools]
+    b = e.submit(base + ext[0], 5, eos=())
+    c = e.submit(base + ext[1], 5, eos=())
+    e.run()
+    assert b.cached == 40 and c.cached == 40 and e.pool.copies >= 2
+    assert all(np.array_equal(u16(p[stored]), x) for p, x in zip(e.pool.pools, before))  # never written
+    assert a.tokens == _solo(lm, base, 4, prefix_store=False)
+    assert b.tokens == _solo(lm, base + ext[0], 5, prefix_store=False)
+    assert c.tokens == _solo(lm, base + ext[1], 5, prefix_store=False)
+
+
+def test_engine_small_pool_defers_and_stops_on_eos(lm):
+    prompts = _prompts(4, [30, 20])
+    e = Engine(lm, 5, prefill_chunk=16, max_step_tokens=48, prefix_store=False)
+    r0 = e.submit(prompts[0], 8, eos=())   # 3 pages
+    r1 = e.submit(prompts[1], 30, eos=())  # 4 pages: waits for r0
+    e.run()
+    assert e.deferred > 0 and e.pool.free_pages == 5
+    assert r0.tokens == _solo(lm, prompts[0], 8, prefix_store=False)
+    assert r1.tokens == _solo(lm, prompts[1], 30, prefix_store=False)
+    stop = r1.tokens[3]
+    e2 = Engine(lm, 16, prefill_chunk=16, max_step_tokens=48)
+    r = e2.submit(prompts[1], 30, eos=(stop,))
+    e2.run()
+    first = r1.tokens.index(stop)
+    assert r.finish_reason == "stop" and r.tokens == r1.tokens[:first + 1]
+
+
+def test_checkpoint_model_generates_on_gpu(tmp_path):
+    cfg = config_dict(D=2048, H=32, Hkv=4, E=32, k=8, I=768, V=512, L=2)
+    src = write_checkpoint(str(tmp_path), cfg, device=DEV)
+    lm = checkpoint.load(str(tmp_path), DEV)
+    mcfg = lm.cfg
+    # the same model assembled by hand from the written tensors
+    def q(n):
+        return QLinear(src[n + ".weight"], src[n + ".scales"], src[n + ".biases"])
+
+    def cat(ns, dim):
+        return QLinear(*(torch.cat([src[n + "." + part] for n in ns], dim).contiguous()
+                         for part in ("weight", "scales", "biases")))
+    layers = []
+    for i in range(2):
+        p = f"model.layers.{i}."
+        layers.append({"input_norm": src[p + "input_layernorm.weight"],
+                       "qkv": cat([p + f"self_attn.{m}_proj" for m in "qkv"], 0),
+                       "q_norm": src[p + "self_attn.q_norm.weight"], "k_norm": src[p + "self_attn.k_norm.weight"],
+                       "o": q(p + "self_attn.o_proj"), "post_norm": src[p + "post_attention_layernorm.weight"],
+                       "router": q(p + "mlp.gate"),
+                       "gate_up": cat([p + f"mlp.switch_mlp.{m}_proj" for m in ("gate", "up")], 1),
+                       "down": q(p + "mlp.switch_mlp.down_proj")})
+    ref = CausalLM(Model(mcfg, layers), q("model.embed_tokens"), src["model.norm.weight"], q("lm_head"), 512)
+    prompts = [[1, 2, 3, 4, 5, 6, 7], [100, 200, 300]]
+    out = []
+    for m in (lm, ref):
+        e = Engine(m, 32, prefill_chunk=16, max_step_tokens=48)
+        rs = [e.submit(p, 5, eos=()) for p in prompts]
+        e.run()
+        out.append([r.tokens for r in rs])
+    assert out[0] == out[1]
