@@ -437,3 +437,35 @@ def test_segment_gemm_weights_in_gate_up_and_down():
     assert not np.array_equal(h, h_exact)
     d = np.abs(bf16_to_f32(h).astype(np.float64) - bf16_to_f32(h_exact))
     assert d.max() <= 2e-2
+
+
+def test_embed_q4_pinned_by_torch_bf16_ops():
+    """mx.dequantize in bf16 arithmetic: bf16(bf16(s * q) + b), against torch's own bf16 multiply
+    and add (a library routine); q = 0 gives the bias exactly; an out-of-range id a zero row."""
+    rng = np.random.default_rng(8)
+    V, D = 40, 256
+    w = rng.integers(0, 2**32, (V, D // 8), dtype=np.uint64).astype(np.uint32)
+    w[5] = 0
+    s = oracle.f32_to_bf16(rng.normal(0, 0.01, (V, D // 64)).astype(np.float32))
+    b = oracle.f32_to_bf16(rng.normal(0, 0.05, (V, D // 64)).astype(np.float32))
+    ids = np.array([3, 0, 39, 5, 40, -2])
+    got = oracle.embed_q4(ids, w, s, b)
+    q = ((torch.from_numpy(w.astype(np.int64))[:, :, None] >> (4 * torch.arange(8))) & 15).reshape(V, D)
+    st = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16).repeat_interleave(64, 1)
+    bt = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).repeat_interleave(64, 1)
+    ref = (st * q.to(torch.bfloat16) + bt).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got[:4], ref[[3, 0, 39, 5]])
+    assert np.array_equal(got[3], np.repeat(b[5], 64))
+    assert not got[4].any() and not got[5].any()
+
+
+def test_argmax_rows_pinned_by_numpy():
+    x = oracle.f32_to_bf16(np.random.default_rng(2).normal(0, 3, (7, 1001)).astype(np.float32))
+    x[1, [4, 9]] = x[1].view(np.int16).max()  # positive bf16 patterns order like their values
+    got = oracle.argmax_rows(x)
+    assert np.array_equal(got, np.argmax(oracle.bf16_to_f32(x), axis=1))
+    y = x.copy()
+    y[0, :3] = 0x7FC0                     # NaN never wins
+    y[2, :] = 0x7FC0                      # all NaN: 0
+    assert oracle.argmax_rows(y)[0] == np.argmax(oracle.bf16_to_f32(x[0, 3:])) + 3
+    assert oracle.argmax_rows(y)[2] == 0
