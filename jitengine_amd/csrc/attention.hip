@@ -351,9 +351,9 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
 // q head).  The partials were written by workgroups on other XCDs, so every read
 // here misses this XCD's L2; the chunks are spread over 16 chunk lanes (thread =
 // chunk lane x 32 dim quads) so that many of those reads are in flight at once
-// instead of one per chunk in a serial chain.  Lane j sums chunks j, j + 16, ...
-// and the 16 lane sums are added in lane order: a fixed order that depends only on
-// the sequence's chunk count.
+// instead of one per chunk in a serial chain.  Lane j merges chunks j, j + 16, ...
+// online (running max, one pass over the partials), and the 16 lane states are
+// merged in lane order: a fixed order that depends only on the sequence's chunk count.
 constexpr int kMergeLanes = 16;
 
 __global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restrict__ lens,
@@ -367,47 +367,46 @@ __global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restri
   const int n = (L + ck - 1) / ck;
   if (n <= 1) return;
   const long long c0 = chunk_start[b];
-  __shared__ float s_max[512 / 64];
   __shared__ float4 s_o[kMergeLanes][32];
-  __shared__ float s_l[kMergeLanes];
-  // the largest chunk max (max is exact, so any order)
-  float M = -INFINITY;
-  for (int c = t; c < n; c += 512) M = fmaxf(M, part_ml[((c0 + c) * H + h) * 2]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor_f(M, off));
-  if ((t & 63) == 0) s_max[t >> 6] = M;
-  __syncthreads();
-#pragma unroll
-  for (int w = 0; w < 512 / 64; w++) M = fmaxf(M, s_max[w]);
+  __shared__ float s_m[kMergeLanes], s_l[kMergeLanes];
   const int cl = t >> 5, dq = t & 31;
   float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-  float Ls = 0.0f;
-#pragma unroll 4
+  float m_run = -INFINITY, Ls = 0.0f;  // every chunk holds a key: its max is finite
+#pragma unroll 2
   for (int c = cl; c < n; c += kMergeLanes) {
     const long long r = (c0 + c) * H + h;
     const float2 ml = *(const float2 *)(part_ml + r * 2);
     const float4 o = *(const float4 *)(part_o + r * kD + 4 * dq);
-    const float f = exp2f(ml.x - M);
-    Ls += ml.y * f;
-    O.x += o.x * f;
-    O.y += o.y * f;
-    O.z += o.z * f;
-    O.w += o.w * f;
+    const float mn = fmaxf(m_run, ml.x);
+    const float fa = exp2f(m_run - mn), fb = exp2f(ml.x - mn);
+    Ls = Ls * fa + ml.y * fb;
+    O.x = O.x * fa + o.x * fb;
+    O.y = O.y * fa + o.y * fb;
+    O.z = O.z * fa + o.z * fb;
+    O.w = O.w * fa + o.w * fb;
+    m_run = mn;
   }
   s_o[cl][dq] = O;
-  if (dq == 0) s_l[cl] = Ls;
+  if (dq == 0) {
+    s_m[cl] = m_run;
+    s_l[cl] = Ls;
+  }
   __syncthreads();
   if (t >= 32) return;
-  float4 acc = s_o[0][t];
-  float lsum = s_l[0];
+  float M = s_m[0];
 #pragma unroll
-  for (int j = 1; j < kMergeLanes; j++) {
+  for (int j = 1; j < kMergeLanes; j++) M = fmaxf(M, s_m[j]);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float lsum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kMergeLanes; j++) {  // lanes without a chunk hold m = -inf: weight 0
+    const float f = exp2f(s_m[j] - M);
     const float4 v = s_o[j][t];
-    acc.x += v.x;
-    acc.y += v.y;
-    acc.z += v.z;
-    acc.w += v.w;
-    lsum += s_l[j];
+    acc.x += v.x * f;
+    acc.y += v.y * f;
+    acc.z += v.z * f;
+    acc.w += v.w * f;
+    lsum += s_l[j] * f;
   }
   const float inv = 1.0f / lsum;
   uint2 w;
