@@ -363,6 +363,19 @@ extern "C" int jit_qmm_packed(const uint16_t *x, int T, int K, const void *packe
   return launch_dense<true>(a, (hipStream_t)stream);
 }
 
+// Expert GEMV shapes (groups of 64 per wave; row blocks of 16 per workgroup), chosen by timing
+// sweeps on MI355X over the config-2 routing.
+#ifndef JIT_GU_GPW
+#define JIT_GU_GPW 8
+#endif
+#ifndef JIT_DN_NB
+#define JIT_DN_NB 4
+#endif
+#ifndef JIT_DN_GPW
+#define JIT_DN_GPW 4
+#endif
+constexpr int kGuGpw = JIT_GU_GPW, kDnNb = JIT_DN_NB, kDnGpw = JIT_DN_GPW;
+
 static int gate_up_check(const uint16_t *x, int K, const int32_t *pair_row, const int32_t *cnt,
                          const int32_t *off, int E, int I, int P, uint16_t *h) {
   if (K <= 0 || I <= 0 || E <= 0 || P < 0)
@@ -384,7 +397,7 @@ extern "C" int jit_moe_gate_up_swiglu(const uint16_t *x, int K, const int32_t *p
   if (!w || !scales || !biases) return jit::fail(JIT_EINVAL, "moe_gate_up: null pointer");
   QmmArgs a{x, pair_row, expert_cnt, expert_off, w, scales, biases, h, K, I, 0,
             (long long)2 * I * (K / 8), (long long)2 * I * (K / 64), 2 * I};
-  return launch_qmm<1, 8, true, false>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu");
+  return launch_qmm<1, kGuGpw, true, false>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu");
 }
 
 extern "C" int jit_moe_gate_up_swiglu_packed(const uint16_t *x, int K, const int32_t *pair_row,
@@ -395,7 +408,7 @@ extern "C" int jit_moe_gate_up_swiglu_packed(const uint16_t *x, int K, const int
   if (!packed) return jit::fail(JIT_EINVAL, "moe_gate_up_packed: null pointer");
   QmmArgs a{x, pair_row, expert_cnt, expert_off, (const uint32_t *)packed, nullptr, nullptr, h, K, I, 0,
             jit_q4_packed_bytes(1, 2 * I, K), 0, 2 * I};
-  return launch_qmm<1, 8, true, true>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu_packed");
+  return launch_qmm<1, kGuGpw, true, true>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu_packed");
 }
 
 static int down_check(const uint16_t *h, int I, const int32_t *cnt, const int32_t *off, int E, int D, int P,
@@ -418,7 +431,7 @@ extern "C" int jit_moe_down(const uint16_t *h, int I, const int32_t *expert_cnt,
   if (!w || !scales || !biases) return jit::fail(JIT_EINVAL, "moe_down: null pointer");
   QmmArgs a{h, nullptr, expert_cnt, expert_off, w, scales, biases, r, I, D, 0,
             (long long)D * (I / 8), (long long)D * (I / 64), D};
-  return launch_qmm<4, 4, false, false>(a, E, (hipStream_t)stream, "jit_moe_down");
+  return launch_qmm<kDnNb, kDnGpw, false, false>(a, E, (hipStream_t)stream, "jit_moe_down");
 }
 
 extern "C" int jit_moe_down_packed(const uint16_t *h, int I, const int32_t *expert_cnt,
@@ -429,5 +442,5 @@ extern "C" int jit_moe_down_packed(const uint16_t *h, int I, const int32_t *expe
   if (!packed) return jit::fail(JIT_EINVAL, "moe_down_packed: null pointer");
   QmmArgs a{h, nullptr, expert_cnt, expert_off, (const uint32_t *)packed, nullptr, nullptr, r, I, D, 0,
             jit_q4_packed_bytes(1, D, I), 0, D};
-  return launch_qmm<4, 4, false, true>(a, E, (hipStream_t)stream, "jit_moe_down_packed");
+  return launch_qmm<kDnNb, kDnGpw, false, true>(a, E, (hipStream_t)stream, "jit_moe_down_packed");
 }
