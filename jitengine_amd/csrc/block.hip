@@ -11,6 +11,16 @@
 
 namespace {
 
+// Eight floats to eight bf16 (round-to-nearest-even), packed.
+__device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
+  uint4 o;
+  o.x = pack_bf16x2_rne(v[0], v[1]);
+  o.y = pack_bf16x2_rne(v[2], v[3]);
+  o.z = pack_bf16x2_rne(v[4], v[5]);
+  o.w = pack_bf16x2_rne(v[6], v[7]);
+  return o;
+}
+
 constexpr int kD = JIT_HEAD_DIM;
 constexpr int kPage = JIT_PAGE_TOKENS;
 
@@ -50,15 +60,12 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
       const uint4 r = *(const uint4 *)(resid + row * D + n);
       const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = bf2f(f2bf(v[i] + ((i & 1) ? bf2f_hi(rw[i >> 1]) : bf2f(rw[i >> 1] & 0xffffu))));
-      if (h_out) {
-        uint4 o;
-        o.x = f2bf(v[0]) | (f2bf(v[1]) << 16);
-        o.y = f2bf(v[2]) | (f2bf(v[3]) << 16);
-        o.z = f2bf(v[4]) | (f2bf(v[5]) << 16);
-        o.w = f2bf(v[6]) | (f2bf(v[7]) << 16);
-        *(uint4 *)(h_out + row * D + n) = o;
+      for (int i = 0; i < 8; i += 2) {
+        v[i] += bf2f(rw[i >> 1] & 0xffffu);
+        v[i + 1] += bf2f_hi(rw[i >> 1]);
+        round_bf2(v[i], v[i + 1]);
       }
+      if (h_out) *(uint4 *)(h_out + row * D + n) = pack8(v);
     }
 #pragma unroll
     for (int i = 0; i < 8; i++) ss = fmaf(v[i], v[i], ss);
@@ -69,16 +76,13 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
     const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
     float o[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float wi = (i & 1) ? bf2f_hi(ww[i >> 1]) : bf2f(ww[i >> 1] & 0xffffu);
-      o[i] = bf2f(f2bf(wi * bf2f(f2bf(v[i] * r))));
+    for (int i = 0; i < 8; i += 2) {
+      float n0 = v[i] * r, n1 = v[i + 1] * r;
+      round_bf2(n0, n1);
+      o[i] = bf2f(ww[i >> 1] & 0xffffu) * n0;
+      o[i + 1] = bf2f_hi(ww[i >> 1]) * n1;
     }
-    uint4 out;
-    out.x = f2bf(o[0]) | (f2bf(o[1]) << 16);
-    out.y = f2bf(o[2]) | (f2bf(o[3]) << 16);
-    out.z = f2bf(o[4]) | (f2bf(o[5]) << 16);
-    out.w = f2bf(o[6]) | (f2bf(o[7]) << 16);
-    *(uint4 *)(y + row * D + n) = out;
+    *(uint4 *)(y + row * D + n) = pack8(o);
   }
 }
 
@@ -110,31 +114,28 @@ __device__ __forceinline__ void combine8(const uint16_t *__restrict__ r, const i
       if (!use[jj]) continue;
       const uint32_t wds[4] = {rv[jj].x, rv[jj].y, rv[jj].z, rv[jj].w};
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float rr = (i & 1) ? bf2f_hi(wds[i >> 1]) : bf2f(wds[i >> 1] & 0xffffu);
-        const float pr = bf2f(f2bf(rr * sc[jj]));
-        acc[i] = bf2f(f2bf(acc[i] + pr));
+      for (int i = 0; i < 8; i += 2) {
+        float p0 = bf2f(wds[i >> 1] & 0xffffu) * sc[jj], p1 = bf2f_hi(wds[i >> 1]) * sc[jj];
+        round_bf2(p0, p1);
+        float a0 = acc[i] + p0, a1 = acc[i + 1] + p1;
+        round_bf2(a0, a1);
+        acc[i] = a0;
+        acc[i + 1] = a1;
       }
     }
   }
   if (resid) {
     const uint32_t wds[4] = {res.x, res.y, res.z, res.w};
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float rr = (i & 1) ? bf2f_hi(wds[i >> 1]) : bf2f(wds[i >> 1] & 0xffffu);
-      acc[i] = bf2f(f2bf(rr + acc[i]));
+    for (int i = 0; i < 8; i += 2) {
+      float a0 = bf2f(wds[i >> 1] & 0xffffu) + acc[i], a1 = bf2f_hi(wds[i >> 1]) + acc[i + 1];
+      round_bf2(a0, a1);
+      acc[i] = a0;
+      acc[i + 1] = a1;
     }
   }
 }
 
-__device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
-  uint4 o;
-  o.x = f2bf(v[0]) | (f2bf(v[1]) << 16);
-  o.y = f2bf(v[2]) | (f2bf(v[3]) << 16);
-  o.z = f2bf(v[4]) | (f2bf(v[5]) << 16);
-  o.w = f2bf(v[6]) | (f2bf(v[7]) << 16);
-  return o;
-}
 
 // Weighted combine: one workgroup per token row, 8 outputs per thread.
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict__ r,
@@ -176,9 +177,11 @@ __global__ __launch_bounds__(256) void combine_rmsnorm_kernel(
     const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
     float o[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float wi = (i & 1) ? bf2f_hi(ww[i >> 1]) : bf2f(ww[i >> 1] & 0xffffu);
-      o[i] = bf2f(f2bf(wi * bf2f(f2bf(v[i] * rs))));
+    for (int i = 0; i < 8; i += 2) {
+      float n0 = v[i] * rs, n1 = v[i + 1] * rs;
+      round_bf2(n0, n1);
+      o[i] = bf2f(ww[i >> 1] & 0xffffu) * n0;
+      o[i + 1] = bf2f_hi(ww[i >> 1]) * n1;
     }
     *(uint4 *)(xn + bt * D + n) = pack8(o);
   }

@@ -44,6 +44,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Round two floats to bf16 (the hardware rounding above) and widen them back: the bf16 values
+// as floats, in three instructions for the pair.
+__device__ __forceinline__ void round_bf2(float &a, float &b) {
+  const uint32_t p = pack_bf16x2_rne(a, b);
+  a = __uint_as_float(p << 16);
+  b = __uint_as_float(p & 0xffff0000u);
+}
+
 // ------------------------------------------------------------------ wave
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 
