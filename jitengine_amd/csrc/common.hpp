@@ -24,12 +24,13 @@ union Frag8 {  // 8 bf16 = one MFMA 16x16x32 operand fragment of one lane
 __device__ __forceinline__ float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
 __device__ __forceinline__ float bf2f_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// fp32 -> bf16 round-to-nearest-even (NaN kept quiet), the rounding of MLX's bf16 type.
+// fp32 -> bf16 round-to-nearest-even (NaN kept quiet: its top 16 bits with the quiet bit set),
+// the rounding of MLX's bf16 type.  Numbers take the hardware conversion (v_cvt_pk_bf16_f32,
+// the same rounding); only the NaN payload is formed by hand.
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t h = __builtin_bit_cast(unsigned short, (__bf16)f);
+  return (u & 0x7fffffffu) > 0x7f800000u ? (((u >> 16) | 0x40u) & 0xffffu) : h;
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
