@@ -13,7 +13,12 @@ decode.py, retire.py) on this build's pieces:
     step (Model.decode_step);
   * a request retires on an end-of-sequence token or after max_tokens tokens
     (Q36/scheduler/retire.py); its prompt's pages then go to the prefix store and the rest of its
-    reservation back to the pool.
+    reservation back to the pool;
+  * decode pipelining (DecodingMixin._pump, Q36/scheduler/decode.py:21-114): while only decoding
+    rows are left, the next step is issued -- fed by this step's tokens on the device, its
+    positions known on the host -- before this step's tokens are read, so the host's bookkeeping
+    overlaps the GPU's step; a row that stops on an end-of-sequence token costs one discarded step,
+    as in the reference.
 Tokens are drawn greedily on the GPU (jit_argmax_rows).
 """
 
@@ -54,7 +59,8 @@ class Engine:
     """Requests in, greedy tokens out, many sequences per step over one KV pool."""
 
     def __init__(self, lm: CausalLM, num_pages: int, prefill_chunk: int = 512, max_step_tokens: int = 2048,
-                 prefix_store: bool = True, page_seed: int | None = None, device=None, allocate: bool = True):
+                 prefix_store: bool = True, page_seed: int | None = None, device=None, allocate: bool = True,
+                 pipeline: bool = True):
         if prefill_chunk <= 0 or max_step_tokens <= 0:
             raise ValueError("prefill_chunk and max_step_tokens must be positive")
         self.lm = lm
@@ -70,6 +76,9 @@ class Engine:
         self.outstanding = 0       # pages charged to admitted requests, not yet allocated
         self.deferred = 0          # admission attempts stopped by the pool
         self.steps = 0
+        self.pipeline = bool(pipeline)
+        self.pipelined = 0          # steps issued before the previous step's tokens were read
+        self._inflight = None       # (rows, device tokens) of a decode step not yet read
         self._ids = itertools.count()
 
     # ------------------------------------------------------------------ requests
@@ -92,7 +101,7 @@ class Engine:
 
     @property
     def busy(self) -> bool:
-        return bool(self.queue or self.rows)
+        return bool(self.queue or self.rows or self._inflight)
 
     def _admit(self) -> None:
         while self.queue:
@@ -132,8 +141,54 @@ class Engine:
         self.rows.remove(r)
 
     # ---------------------------------------------------------------------- step
+    def _issue_decode(self, rows: list, ids, pos: np.ndarray) -> torch.Tensor:
+        """Launch one batched decode step over `rows` (ids: host list or int32 device tensor); returns
+        the drawn tokens, int32 [B] on the device (not read)."""
+        lm = self.lm
+        st = make_step_state(lm.cfg, pos, self.pool.page_table([r.rid for r in rows]))
+        ids_t = ids if torch.is_tensor(ids) else torch.tensor(ids, dtype=torch.int32, device=self.device)
+        return lm.greedy(lm.model.decode_step(lm.embed_tokens(ids_t), self.pool.pools, st))
+
+    def _can_pipeline(self, rows: list, ahead: int) -> bool:
+        """Whether a decode step over `rows` may be issued with `ahead` steps' tokens still unread:
+        no request waits to join, every row is decoding and needs that many more tokens."""
+        return (self.pipeline and not self.queue and len(rows) == len(self.rows)
+                and all(r.state == "decode" and len(r.tokens) + ahead < r.max_tokens for r in rows))
+
+    def _pump(self) -> list:
+        """Consume the step in flight, having issued the next one first when the rows allow."""
+        rows, toks = self._inflight
+        self._inflight = None
+        if self._can_pipeline(rows, 1):
+            pos = np.array([r.length + 1 for r in rows], np.int32)
+            for r in rows:
+                self._write(r, r.length + 1, 1)
+            self._inflight = (rows, self._issue_decode(rows, toks, pos))
+            self.steps += 1
+            self.pipelined += 1
+        drawn = [(r, t) for r, t in zip(rows, toks.tolist()) if r.state != "done"]
+        self._consume(drawn)
+        return drawn
+
+    def _consume(self, drawn: list) -> None:
+        for r, t in drawn:
+            r.tokens.append(int(t))
+            r.state = "decode"
+        for r in list(self.rows):
+            if r.state == "decode" and r.tokens:
+                self.pool.lengths[r.rid] = r.length
+                if r.tokens[-1] in r.eos:
+                    self._retire(r, "stop")
+                elif len(r.tokens) >= r.max_tokens:
+                    self._retire(r, "length")
+            elif r.state == "prefill":
+                self.pool.lengths[r.rid] = r.done_prompt
+
     def step(self) -> list:
-        """One scheduling round; returns the (request, token) pairs it drew."""
+        """One scheduling round; returns the (request, token) pairs it drew (with pipelining, the
+        tokens of the step issued one round earlier)."""
+        if self._inflight is not None:
+            return self._pump()
         self._admit()
         decode = [r for r in self.rows if r.state == "decode"]
         budget = self.max_step_tokens - len(decode)
@@ -153,10 +208,11 @@ class Engine:
         dec_pos = np.array([r.length for r in decode], np.int32)
         dec_ids = [r.tokens[-1] for r in decode]
         if not chunks:
-            table = self.pool.page_table([r.rid for r in decode])
-            st = make_step_state(cfg, dec_pos, table)
-            x = lm.embed_tokens(torch.tensor(dec_ids, dtype=torch.int32, device=dev))
-            toks = lm.greedy(lm.model.decode_step(x, self.pool.pools, st))
+            toks = self._issue_decode(decode, dec_ids, dec_pos)
+            self.steps += 1
+            if self._can_pipeline(decode, 0):
+                self._inflight = (decode, toks)
+                return []  # read at the next round, after the following step is issued
             drawn = list(zip(decode, toks.tolist()))
         else:
             ids = list(itertools.chain.from_iterable(r.prompt[c:c + n] for r, c, n in chunks)) + dec_ids
@@ -184,26 +240,15 @@ class Engine:
                 drawn = list(zip(rows, lm.greedy(sel).tolist()))
             for r, c, n in chunks:
                 r.done_prompt = c + n
-        self.steps += 1
-        for r, t in drawn:
-            r.tokens.append(int(t))
-            r.state = "decode"
-        for r in list(self.rows):
-            if r.state == "decode" and r.tokens:
-                self.pool.lengths[r.rid] = r.length
-                if r.tokens[-1] in r.eos:
-                    self._retire(r, "stop")
-                elif len(r.tokens) >= r.max_tokens:
-                    self._retire(r, "length")
-            elif r.state == "prefill":
-                self.pool.lengths[r.rid] = r.done_prompt
+            self.steps += 1
+        self._consume(drawn)
         return drawn
 
     def run(self, max_steps: int | None = None) -> None:
         """Step until every submitted request is done (or max_steps rounds)."""
         n = 0
         while self.busy and (max_steps is None or n < max_steps):
-            if not self.step() and not self.rows:
+            if not self.step() and not self.rows and self._inflight is None:
                 if self.queue:
                     raise PoolExhausted("the queue head cannot be admitted into an idle pool")
                 break

@@ -88,7 +88,7 @@ def _prompts(seed, lens):
 
 
 def _solo(lm, prompt, max_tokens, **kw):
-    e = Engine(lm, 64, prefill_chunk=16, max_step_tokens=48, **kw)
+    e = Engine(lm, 64, prefill_chunk=16, max_step_tokens=48, pipeline=False, **kw)
     r = e.submit(prompt, max_tokens, eos=())
     e.run()
     return r.tokens
@@ -174,3 +174,26 @@ def test_checkpoint_model_generates_on_gpu(tmp_path):
         e.run()
         out.append([r.tokens for r in rs])
     assert out[0] == out[1]
+
+
+def test_engine_decode_pipelining_is_exact(lm):
+    """Issuing step n + 1 before reading step n (fed by its tokens on the device) draws the same
+    tokens; an end-of-sequence token seen one step late only costs a discarded step."""
+    prompts = _prompts(6, [12, 25, 7])
+    out = {}
+    for pipe in (False, True):
+        e = Engine(lm, 64, prefill_chunk=16, max_step_tokens=48, pipeline=pipe)
+        reqs = [e.submit(p, 9, eos=()) for p in prompts]
+        e.run()
+        out[pipe] = [r.tokens for r in reqs]
+        if pipe:
+            assert e.pipelined > 0
+        assert e.pool.free_pages + sum(len(v) for v in e.store.entries.values()) == 64
+    assert out[True] == out[False]
+    stop = out[False][1][4]
+    e = Engine(lm, 64, prefill_chunk=16, max_step_tokens=48, pipeline=True)
+    reqs = [e.submit(p, 9, eos=(stop,)) for p in prompts]
+    e.run()
+    for r, full in zip(reqs, out[False]):
+        want = full[:full.index(stop) + 1] if stop in full else full
+        assert r.tokens == want and r.finish_reason == ("stop" if stop in full else "length")
