@@ -477,12 +477,16 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
         "router_proj": lambda l: ops.qmm(dbg[l]["hn"], L_[l].moe.router),
         "router_topk": lambda l: ops.router_topk(dbg[l]["logits"], cfg.top_k, cfg.norm_topk),
         "moe_pack": lambda l: ops.moe_pack(dbg[l]["inds"], cfg.experts),
+        "route_pack": lambda l: ops.route_pack(dbg[l]["logits"], cfg.top_k, cfg.norm_topk),
         "gate_up_swiglu": lambda l: ops.expert_gate_up(dbg[l]["hn"], L_[l].moe.gate_up, dbg[l]["pk"]),
         "down": lambda l: ops.expert_down(dbg[l]["hh"], L_[l].moe.down, dbg[l]["pk"]),
         "combine_rmsnorm": lambda l: ops.moe_combine_rmsnorm(dbg[l]["r"], dbg[l]["pk"], dbg[l]["scores"],
                                                              dbg[l]["h"], L_[l + 1].input_norm, cfg.eps),
         "combine": lambda l: ops.moe_combine(dbg[l]["r"], dbg[l]["pk"], dbg[l]["scores"], dbg[l]["h"]),
     }
+    # a step of at most ROUTE_PACK_MAX_ROWS rows routes and packs in one launch, a larger one in two
+    for name in (("router_topk", "moe_pack") if B <= ops.ROUTE_PACK_MAX_ROWS else ("route_pack",)):
+        del per_layer[name]
     launches = {name: step_layers.get(name, list(range(n_layers))) for name in per_layer}
     kus = time_ops({name: [(lambda f=f, l=l: f(l)) for l in launches[name]] for name, f in per_layer.items()},
                    reps=3)

@@ -90,6 +90,15 @@ int jit_moe_pack(const uint32_t *inds, int P, int k, int E, int32_t *order, int3
                  int32_t *inv, int32_t *expert_cnt, int32_t *expert_off, int32_t *seg_expert,
                  int32_t *seg_start, int32_t *seg_cnt, int32_t *meta, void *stream);
 
+/* The router top-k of at most 4 rows followed by their packing, in one launch: the same
+ * outputs, bit for bit, as jit_router_topk (inds [rows, k], scores) then jit_moe_pack over
+ * P = rows * k pairs of E = N experts (their two contracts, plus rows <= 4 and N <= 128:
+ * JIT_EUNSUPPORTED otherwise).  For the decode step of one sequence (the reference's solo path,
+ * Q36/model/moe.py:304-315 then :151-159), where the second launch costs as much as the work. */
+int jit_route_pack(const uint16_t *logits, int rows, int N, int k, int norm, uint32_t *inds, uint16_t *scores,
+                   int32_t *order, int32_t *pair_row, int32_t *inv, int32_t *expert_cnt, int32_t *expert_off,
+                   int32_t *seg_expert, int32_t *seg_start, int32_t *seg_cnt, int32_t *meta, void *stream);
+
 /* ------------------------------------------------ quantized projections --
  * Dense 4-bit projection y[T, N] = x[T, K] . dequant(W[N, K])^T, fp32
  * accumulation, bf16 out: QLinear.__call__ / .rows (Q36/linear.py:219-313,

@@ -27,6 +27,7 @@ _SIGNATURES = {
     "jit_router_topk": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "jit_topk": [_P, _I, _I, _I, _P, _P],
     "jit_moe_pack": [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "jit_route_pack": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "jit_q4_packed_bytes": [_I, _I, _I],
     "jit_q4_prepack": [_P, _P, _P, _I, _I, _I, _P, _P],
     "jit_qmm": [_P, _I, _I, _P, _P, _P, _I, _P, _P],

@@ -316,7 +316,52 @@ __global__ __launch_bounds__(TH) void moe_pack_kernel(
             seg_start, seg_cnt, meta);
 }
 
+// Top-k of a few rows and their packing in one launch (a decode step of at most
+// kRoutePackRows rows, e.g. one sequence): the same topk_row and pack_body as the two
+// kernels above, so the same bits, one launch fewer.  Two waves take the rows in turn;
+// the packing reads the indices they wrote after the workgroup barrier.
+constexpr int kRoutePackRows = 4;
+
+template <int NPL>
+__global__ __launch_bounds__(128) void route_pack_kernel(
+    const uint16_t *__restrict__ logits, int rows, int N, int k, int norm, uint32_t *__restrict__ inds,
+    uint16_t *__restrict__ scores, int32_t *__restrict__ order, int32_t *__restrict__ pair_row,
+    int32_t *__restrict__ inv, int32_t *__restrict__ expert_cnt, int32_t *__restrict__ expert_off,
+    int32_t *__restrict__ seg_expert, int32_t *__restrict__ seg_start, int32_t *__restrict__ seg_cnt,
+    int32_t *__restrict__ meta) {
+  __shared__ uint32_t skey[2][kMaxN];
+  const int w = threadIdx.x >> 6, l = lane_id();
+  for (int row = w; row < rows; row += 2)
+    topk_row<NPL, false>(logits + (size_t)row * N, row, N, k, norm, inds, scores, nullptr, skey[w], l);
+  __syncthreads();
+  pack_body<128>([&](int p) { return inds[p]; }, rows * k, k, N, order, pair_row, inv, expert_cnt, expert_off,
+                 seg_expert, seg_start, seg_cnt, meta);
+}
+
 }  // namespace
+
+extern "C" int jit_route_pack(const uint16_t *logits, int rows, int N, int k, int norm, uint32_t *inds,
+                              uint16_t *scores, int32_t *order, int32_t *pair_row, int32_t *inv,
+                              int32_t *expert_cnt, int32_t *expert_off, int32_t *seg_expert, int32_t *seg_start,
+                              int32_t *seg_cnt, int32_t *meta, void *stream) {
+  if (rows < 0 || N <= 0 || !(0 < k && k <= N))
+    return jit::fail(JIT_EINVAL, "route_pack takes rows >= 0 and 0 < k <= N, got rows=%d N=%d k=%d", rows, N, k);
+  if (rows > kRoutePackRows || N % 32 != 0 || N > 128)
+    return jit::fail(JIT_EUNSUPPORTED, "route_pack covers rows <= %d and N %% 32 == 0, N <= 128, got rows=%d N=%d",
+                     kRoutePackRows, rows, N);
+  if (!expert_cnt || !expert_off || !seg_expert || !seg_start || !seg_cnt || !meta)
+    return jit::fail(JIT_EINVAL, "route_pack: null pointer");
+  if (rows > 0 && (!logits || !inds || !scores || !order || !pair_row || !inv))
+    return jit::fail(JIT_EINVAL, "route_pack: null pointer");
+  const hipStream_t st = (hipStream_t)stream;
+  if (N <= 64)
+    route_pack_kernel<1><<<1, 128, 0, st>>>(logits, rows, N, k, norm, inds, scores, order, pair_row, inv, expert_cnt,
+                                           expert_off, seg_expert, seg_start, seg_cnt, meta);
+  else
+    route_pack_kernel<2><<<1, 128, 0, st>>>(logits, rows, N, k, norm, inds, scores, order, pair_row, inv, expert_cnt,
+                                           expert_off, seg_expert, seg_start, seg_cnt, meta);
+  return jit::check_launch("jit_route_pack");
+}
 
 extern "C" int jit_router_topk(const uint16_t *logits, int rows, int N, int k, int norm,
                                uint32_t *inds, uint16_t *scores, uint16_t *gates_out,

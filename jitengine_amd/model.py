@@ -169,8 +169,11 @@ class DecoderLayer:
         o = ops.qmm(attn.view(B, -1), self.o)
         hn, h = ops.rmsnorm(o, self.post_norm, cfg.eps, resid=x, return_sum=True)
         logits = ops.qmm(hn, moe.router)
-        inds, scores = ops.router_topk(logits, moe.top_k, moe.norm_topk)
-        pk = ops.moe_pack(inds, moe.num_experts)
+        if B <= ops.ROUTE_PACK_MAX_ROWS and moe.num_experts <= 128:  # one launch for a small step
+            inds, scores, pk = ops.route_pack(logits, moe.top_k, moe.norm_topk)
+        else:
+            inds, scores = ops.router_topk(logits, moe.top_k, moe.norm_topk)
+            pk = ops.moe_pack(inds, moe.num_experts)
         hh, r = moe.expert_mlp(hn, pk)
         if next_norm is None:
             y, xn_next = ops.moe_combine(r, pk, scores, h), None

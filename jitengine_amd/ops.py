@@ -108,6 +108,28 @@ def moe_pack(inds: torch.Tensor, n_experts: int) -> Packing:
     return pk
 
 
+ROUTE_PACK_MAX_ROWS = 4
+
+
+def route_pack(logits: torch.Tensor, k: int, norm: bool):
+    """router_topk then moe_pack of at most ROUTE_PACK_MAX_ROWS rows in one launch (jit_route_pack):
+    (inds, scores, Packing), bit for bit the two-launch result; the expert count is N."""
+    _need(logits, torch.bfloat16, "logits")
+    rows, n = logits.shape
+    inds = torch.empty((rows, k), dtype=torch.int32, device=logits.device)
+    scores = torch.empty((rows, k), dtype=torch.bfloat16, device=logits.device)
+    pk = _packing_buffers(rows * k, k, n, logits.device)
+    _lib.check(
+        _lib.lib().jit_route_pack(
+            _p(logits), rows, n, int(k), int(bool(norm)), _p(inds), _p(scores), _p(pk.order), _p(pk.pair_row),
+            _p(pk.inv), _p(pk.expert_cnt), _p(pk.expert_off), _p(pk.seg_expert), _p(pk.seg_start),
+            _p(pk.seg_cnt), _p(pk.meta), _stream(),
+        ),
+        "route_pack",
+    )
+    return inds, scores, pk
+
+
 def _packing_buffers(P: int, k: int, E: int, device) -> Packing:
     buf = torch.empty(3 * P + 5 * E + 4, dtype=torch.int32, device=device)
     parts = torch.split(buf, [P, P, P, E, E, E, E, E, 4])

@@ -41,6 +41,9 @@ def test_contract_breaks_return_einval_before_launch():
     assert lib.jit_topk(None, 1, 8, 9, None, None) == _lib.JIT_EINVAL
     assert lib.jit_moe_pack(None, 10, 8, 128, *([None] * 9), None) == _lib.JIT_EINVAL  # P % k
     assert lib.jit_moe_pack(None, 16, 8, 2000, *([None] * 9), None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_route_pack(None, 1, 128, 0, 1, *([None] * 11), None) == _lib.JIT_EINVAL
+    assert lib.jit_route_pack(None, 5, 128, 8, 1, *([None] * 11), None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_route_pack(None, 1, 256, 8, 1, *([None] * 11), None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_qmm(None, 4, 100, None, None, None, 64, None, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_moe_down(None, 768 + 64, None, None, 8, None, None, None, 2048, 16, None, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_paged_decode_attn(None, None, None, 4, None, None, None, 2, 30, 4, 0.1, 4, None, None, None) == _lib.JIT_EINVAL

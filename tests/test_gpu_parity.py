@@ -65,6 +65,23 @@ def test_topk_from_gates_bit_exact(N, k):
 
 
 # ----------------------------------------------------------------------------- packing
+@pytest.mark.parametrize("rows,N", [(1, 128), (2, 128), (3, 64), (4, 128), (4, 32), (1, 96)])
+def test_route_pack_equals_two_launches(rows, N):
+    """The one-launch top-k + packing of a small step gives the two launches' bits."""
+    for t in range(6):
+        lg = bf16_tensor(router_logits(t % 4, rows, N, seed=700 + 10 * rows + t), DEV)
+        for norm in (True, False):
+            i2, s2 = ops.router_topk(lg, 8, norm)
+            p2 = ops.moe_pack(i2, N)
+            i1, s1, p1 = ops.route_pack(lg, 8, norm)
+            assert torch.equal(i1, i2) and torch.equal(s1.view(torch.int16), s2.view(torch.int16)), (t, norm)
+            U = int(p2.meta[0])
+            for name in ("order", "pair_row", "inv", "expert_cnt", "expert_off", "meta"):
+                assert torch.equal(getattr(p1, name), getattr(p2, name)), (name, t)
+            for name in ("seg_expert", "seg_start", "seg_cnt"):
+                assert torch.equal(getattr(p1, name)[:U], getattr(p2, name)[:U]), (name, t)
+
+
 @pytest.mark.parametrize("B,k,E", [(64, 8, 128), (32, 8, 128), (1, 8, 128), (2108, 8, 128), (300, 5, 7), (3, 8, 1024)])
 def test_pack_bit_exact(B, k, E):
     rng = np.random.default_rng(B + E)
