@@ -42,6 +42,10 @@ constexpr int kChunk = JIT_ATTN_CHUNK;
 #define JIT_ATTN_SPLITS 4
 #endif
 constexpr int kAttnSplits = JIT_ATTN_SPLITS;  // waves per kv head and chunk
+#ifndef JIT_ATTN_HB
+#define JIT_ATTN_HB (8 / JIT_ATTN_SPLITS)
+#endif
+constexpr int kAttnHeadsPerBlock = JIT_ATTN_HB;  // kv heads per workgroup
 // A sequence longer than kLongChunks chunks of kChunk keys is cut into about kLongChunks
 // chunks instead (two workgroups each: one per CU of MI355X's 256), so that a lone long
 // sequence still fills the chip in one even wave of workgroups (262,144 keys: 128 chunks of
@@ -765,7 +769,7 @@ extern "C" int jit_paged_decode_attn(const uint16_t *q, const uint16_t *pool,
              max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f};
   hipStream_t st = (hipStream_t)stream;
   constexpr int WS = kAttnSplits;
-  const int hb = Hkv < 8 / WS ? Hkv : 8 / WS;  // kv heads per workgroup (WS waves each, <= 8 waves)
+  const int hb = Hkv < kAttnHeadsPerBlock ? Hkv : kAttnHeadsPerBlock;  // kv heads per workgroup (WS waves each)
   const size_t lds = (size_t)(WS - 1) * hb * kStateFloats * 64 * sizeof(float);
   paged_attn_kernel<WS><<<dim3(total_chunks, (Hkv + hb - 1) / hb), 64 * hb * WS, lds, st>>>(a);
   int rc = jit::check_launch("jit_paged_decode_attn");
