@@ -176,7 +176,8 @@ def bench_config1(steps: int, warmup: int, dev: str) -> dict:
         "value": B / (ms * 1e-3),
         "unit": "tokens/s",
         "ms_per_step": ms,
-        "dtype": "bf16 activations, 4-bit g64 weights, fp32 accumulate",
+        "dtype": "bf16",
+        "arithmetic": "bf16 activations, 4-bit g64 weights, fp32 accumulate",
         "config": {"workload": "config1: standalone quantized MoE call, 64 tokens x top-8 of 128 experts, "
                                "gate/up 768x2048, down 2048x768, 4-bit g64",
                    "tokens": B, "experts": E, "top_k": k, "distinct_experts": U},
@@ -331,7 +332,8 @@ def bench_config3(steps: int, warmup: int, dev: str) -> dict:
         "value": T / (ms_step * 1e-3),
         "unit": "tokens/s",
         "ms_per_step": ms_step,
-        "dtype": "bf16 activations, 4-bit g64 weights (bf16-dequantized on the segment GEMM), fp32 accumulate",
+        "dtype": "bf16",
+        "arithmetic": "bf16 activations, 4-bit g64 weights (bf16-dequantized on the segment GEMM), fp32 accumulate",
         "config": {"workload": "config3: one mixed chunked-prefill + decode step of one block -- 4 x 512 prefill "
                                "tokens after contexts U{0..8192} + 60 decode rows (lengths log-uniform [256, 16384])",
                    "rows": T, "prefill_ctx": [int(c) for c in ctx], "decode_kv_tokens": int(dec_len.sum()) + 60,
@@ -727,7 +729,8 @@ def main() -> int:
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
             "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to MLX 4-bit g64)",
             "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"]}
-    for key in ("step_hbm", "step_tflops", "op_us", "op_us_per_step", "op_us_sum_per_step", "kernels_us", "bs1"):
+    for key in ("arithmetic", "step_hbm", "step_tflops", "op_us", "op_us_per_step", "op_us_sum_per_step", "kernels_us",
+                "bs1"):
         if key in res:
             line[key] = res[key]
     print(json.dumps(line), flush=True)
