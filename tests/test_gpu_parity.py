@@ -396,3 +396,21 @@ def test_paged_attention_gqa_shapes():
         got = _attn(q, pool, table, [70, 3000])
         want = oracle.paged_decode_attn(q, pool, table, [70, 3000], 128 ** -0.5)
         assert_close_bf16(got, want, what=f"H={H} Hkv={Hkv}")
+
+
+def test_empty_batches():
+    """Zero rows through every op of the step: empty outputs, no launch, no error."""
+    from jitengine_amd.quant import random_quantized
+
+    lg = torch.empty((0, 128), dtype=torch.bfloat16, device=DEV)
+    inds, scores = ops.router_topk(lg, 8, True)
+    assert inds.shape == (0, 8) and scores.shape == (0, 8)
+    pk = ops.moe_pack(inds, 128)
+    assert pk.P == 0 and int(pk.expert_cnt.sum()) == 0 and int(pk.meta[0]) == 0
+    i1, s1, p1 = ops.route_pack(lg, 8, True)
+    assert i1.shape == (0, 8) and int(p1.expert_cnt.sum()) == 0
+    lin = ops.prepack(random_quantized((256, 2048), 5, device=DEV))
+    assert ops.qmm(torch.empty((0, 2048), dtype=torch.bfloat16, device=DEV), lin).shape == (0, 256)
+    assert ops.argmax_rows(torch.empty((0, 1000), dtype=torch.bfloat16, device=DEV)).shape == (0,)
+    assert ops.embed_q4(torch.empty(0, dtype=torch.int32, device=DEV),
+                        random_quantized((16, 128), 6, device=DEV)).shape == (0, 128)
