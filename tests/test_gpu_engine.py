@@ -197,3 +197,24 @@ def test_engine_decode_pipelining_is_exact(lm):
     for r, full in zip(reqs, out[False]):
         want = full[:full.index(stop) + 1] if stop in full else full
         assert r.tokens == want and r.finish_reason == ("stop" if stop in full else "length")
+
+
+def test_engine_page_aligned_edges(lm):
+    """Page-aligned prompts and prefixes: a 32-token prompt retires after one token; a request
+    restoring its 32-token prefix shares both pages and copies none; a 16-token prefix behind a
+    17-token prompt restores one page."""
+    p32, tail, p16 = _prompts(8, [32, 5, 16])
+    e = Engine(lm, 32, prefill_chunk=16, max_step_tokens=48)
+    a = e.submit(p32, 1, eos=())
+    e.run()
+    assert a.finish_reason == "length" and len(a.tokens) == 1
+    assert a.tokens == _solo(lm, p32, 1, prefix_store=False)
+    b = e.submit(p32 + tail, 3, eos=())
+    e.run()
+    assert b.cached == 32 and e.pool.copies == 0
+    assert b.tokens == _solo(lm, p32 + tail, 3, prefix_store=False)
+    c = e.submit(p16, 2, eos=())
+    e.run()
+    d = e.submit(p16 + [7], 4, eos=())
+    e.run()
+    assert d.cached == 16 and d.tokens == _solo(lm, p16 + [7], 4, prefix_store=False)
