@@ -676,6 +676,46 @@ def rocprof_summary(args) -> int:
     return 0
 
 
+def rocprof_mfma(args) -> int:
+    """Per-kernel MFMA evidence from one rocprofv3 --pmc pass (SQ_VALU_MFMA_BUSY_CYCLES,
+    SQ_INSTS_VALU_MFMA_MOPS_BF16, SQ_BUSY_CU_CYCLES, GRBM_GUI_ACTIVE): the MFMA pipes' busy share of the
+    kernel's active cycles over all 1,024 SIMDs (GRBM_GUI_ACTIVE adds up the 8 XCDs' active cycles, so
+    the kernel's own cycles are an eighth of it), and the bf16 MFMA FLOPs actually issued (one MOP is
+    512 FLOPs; padding rows and tokens included) per launch."""
+    import csv
+    import collections
+
+    d_dir = args.rocprof_mfma
+    vals = collections.defaultdict(lambda: collections.defaultdict(list))
+    for r in csv.DictReader(open(os.path.join(d_dir, "mfma", "mfma_counter_collection.csv"))):
+        vals[r["Kernel_Name"]][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    cfg = " --no-bs1" if args.config == 2 else f" --config {args.config}"
+    ng = " --no-graph" if args.config in (2, 4) else ""
+    print(f"# rocprofv3 MFMA counters of bench.py's config-{args.config} workload")
+    print("# made on one MI355X from the repository root by:")
+    print("#   rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE "
+          f"-f csv -d prof/mfma -o mfma -- python3 bench.py{cfg} --steps 1 --warmup 1{ng}")
+    print(f"#   python3 bench.py --rocprof-mfma prof{cfg}")
+    print("# per kernel (mean over dispatches): MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs"
+          " x 1024 SIMDs);")
+    print("# issued = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 FLOPs per launch")
+    print(f"{'dispatches':>10} {'MFMA busy':>10} {'issued GFLOP':>13}  kernel")
+    rows = []
+    for name, c in vals.items():
+        if "(anonymous namespace)::" not in name or "at::" in name:
+            continue
+        busy = float(np.mean(c.get("SQ_VALU_MFMA_BUSY_CYCLES", [0.0])))
+        act = float(np.mean(c.get("GRBM_GUI_ACTIVE", [1.0])))
+        mops = float(np.mean(c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", [0.0])))
+        n = len(c.get("GRBM_GUI_ACTIVE", []))
+        rows.append((busy / (act / 8.0 * 1024.0) if act else 0.0, mops * 512 / 1e9, n,
+                     name.replace("(anonymous namespace)::", "").split("(")[0]))
+    for frac, gf, n, name in sorted(rows, key=lambda r: -r[1]):
+        if gf > 0:
+            print(f"{n:10d} {100 * frac:9.1f}% {gf:13.2f}  {name}")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -690,9 +730,12 @@ def main() -> int:
     ap.add_argument("--rocprof-summary", metavar="DIR",
                     help="summarise rocprofv3 CSV output under DIR (kt/, fetch/, write/, cfetch/, cwrite/)")
     ap.add_argument("--op", default="paged_attention", choices=sorted(OP_KERNELS) + ["step"])
+    ap.add_argument("--rocprof-mfma", metavar="DIR", help="summarise an MFMA counter pass under DIR/mfma/")
     args = ap.parse_args()
     if args.rocprof_summary:
         return rocprof_summary(args)
+    if args.rocprof_mfma:
+        return rocprof_mfma(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
