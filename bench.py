@@ -677,11 +677,13 @@ def rocprof_summary(args) -> int:
 
 
 def rocprof_mfma(args) -> int:
-    """Per-kernel MFMA evidence from one rocprofv3 --pmc pass (SQ_VALU_MFMA_BUSY_CYCLES,
-    SQ_INSTS_VALU_MFMA_MOPS_BF16, SQ_BUSY_CU_CYCLES, GRBM_GUI_ACTIVE): the MFMA pipes' busy share of the
+    """Per-kernel MFMA and LDS evidence from one rocprofv3 --pmc pass (SQ_VALU_MFMA_BUSY_CYCLES,
+    SQ_INSTS_VALU_MFMA_MOPS_BF16, SQ_BUSY_CU_CYCLES, SQ_LDS_BANK_CONFLICT, SQ_LDS_IDX_ACTIVE,
+    GRBM_GUI_ACTIVE): the MFMA pipes' busy share of the
     kernel's active cycles over all 1,024 SIMDs (GRBM_GUI_ACTIVE adds up the 8 XCDs' active cycles, so
     the kernel's own cycles are an eighth of it), and the bf16 MFMA FLOPs actually issued (one MOP is
-    512 FLOPs; padding rows and tokens included) per launch."""
+    512 FLOPs; padding rows and tokens included) per launch, and the LDS bank-conflict cycles per LDS
+    active cycle."""
     import csv
     import collections
 
@@ -693,13 +695,14 @@ def rocprof_mfma(args) -> int:
     ng = " --no-graph" if args.config in (2, 4) else ""
     print(f"# rocprofv3 MFMA counters of bench.py's config-{args.config} workload")
     print("# made on one MI355X from the repository root by:")
-    print("#   rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE "
-          f"-f csv -d prof/mfma -o mfma -- python3 bench.py{cfg} --steps 1 --warmup 1{ng}")
+    print("#   rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_BUSY_CU_CYCLES SQ_LDS_BANK_CONFLICT "
+          f"SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE -f csv -d prof/mfma -o mfma -- python3 bench.py{cfg} --steps 1 --warmup 1{ng}")
     print(f"#   python3 bench.py --rocprof-mfma prof{cfg}")
     print("# per kernel (mean over dispatches): MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs"
           " x 1024 SIMDs);")
-    print("# issued = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 FLOPs per launch")
-    print(f"{'dispatches':>10} {'MFMA busy':>10} {'issued GFLOP':>13}  kernel")
+    print("# issued = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 FLOPs per launch;"
+          " LDS conflict = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE")
+    print(f"{'dispatches':>10} {'MFMA busy':>10} {'issued GFLOP':>13} {'LDS conflict':>13}  kernel")
     rows = []
     for name, c in vals.items():
         if "(anonymous namespace)::" not in name or "at::" in name:
@@ -708,11 +711,14 @@ def rocprof_mfma(args) -> int:
         act = float(np.mean(c.get("GRBM_GUI_ACTIVE", [1.0])))
         mops = float(np.mean(c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", [0.0])))
         n = len(c.get("GRBM_GUI_ACTIVE", []))
+        lds = float(np.mean(c.get("SQ_LDS_IDX_ACTIVE", [0.0])))
+        conf = float(np.mean(c.get("SQ_LDS_BANK_CONFLICT", [0.0])))
         rows.append((busy / (act / 8.0 * 1024.0) if act else 0.0, mops * 512 / 1e9, n,
-                     name.replace("(anonymous namespace)::", "").split("(")[0]))
-    for frac, gf, n, name in sorted(rows, key=lambda r: -r[1]):
-        if gf > 0:
-            print(f"{n:10d} {100 * frac:9.1f}% {gf:13.2f}  {name}")
+                     name.replace("(anonymous namespace)::", "").split("(")[0], conf / lds if lds else None))
+    for frac, gf, n, name, cr in sorted(rows, key=lambda r: -r[1]):
+        if gf > 0 or cr is not None:
+            crs = f"{100 * cr:12.1f}%" if cr is not None else f"{'-':>13}"
+            print(f"{n:10d} {100 * frac:9.1f}% {gf:13.2f} {crs}  {name}")
     return 0
 
 
