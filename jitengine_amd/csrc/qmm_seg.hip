@@ -25,7 +25,10 @@ constexpr int kSegRB = 4;                 // row blocks per wave
 constexpr int kSegRows = 16 * kSegRB * kSegWaves;  // weight rows per workgroup
 constexpr int kSegTT = 10;                // token tiles per chunk (160 tokens)
 constexpr int kSegTokens = 16 * kSegTT;
-constexpr int kXStride = 128 + 8;         // LDS row stride of the staged activations (bf16)
+#ifndef JIT_SEG_XPAD
+#define JIT_SEG_XPAD 8
+#endif
+constexpr int kXStride = 128 + JIT_SEG_XPAD;  // LDS row stride of the staged activations (bf16)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 is a union-based struct)
 
