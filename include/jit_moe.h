@@ -19,7 +19,8 @@
  *    reference would take its stock MLX fallback); JIT_ELAUNCH reports a HIP
  *    launch failure.  jit_last_error() describes the last failure on the
  *    calling thread.
- *  - No entry point allocates device memory: workspaces are arguments.
+ *  - No entry point allocates device memory: workspaces are arguments (or, for
+ *    jit_paged_decode_attn_noalloc, a fixed array inside the library).
  *  - Calls are asynchronous on `stream`; device-side contents (expert ids,
  *    page ids) are trusted, as the reference's kernels trust theirs
  *    ("entry points validate nothing; callers gate them", FN/kernels/README.md:4).
@@ -276,6 +277,23 @@ int jit_paged_decode_attn(const uint16_t *q, const uint16_t *pool, const int32_t
                           int max_pages, const int32_t *lens, const int32_t *chunk_start,
                           const int32_t *chunk_seq, int B, int H, int Hkv, float scale,
                           int total_chunks, void *workspace, uint16_t *out, void *stream);
+
+/* jit_paged_decode_attn without a workspace argument: the same kernels and the same bits,
+ * with the fp32 split-K partials in a file-scope device array of JIT_ATTN_SCRATCH_BYTES
+ * (16 MiB) that each GPU holds from the library's first call on it until the process ends.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * calls no allocating routine.  Limit: jit_attn_workspace_bytes(total_chunks, H) <=
+ * JIT_ATTN_SCRATCH_BYTES (about 1,000 chunks at H = 32), else JIT_EUNSUPPORTED before any
+ * launch.  The scratch address is taken for the device current at the call (the stream must
+ * belong to it).  All calls on one GPU share its array: calls that overlap in time on one GPU
+ * (other streams, other threads) race on it; calls in one stream are ordered and safe.
+ * Nothing in the array needs clearing: each call writes every partial it reads. */
+#define JIT_ATTN_SCRATCH_BYTES (16 << 20)
+int jit_paged_decode_attn_noalloc(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,
+                                  int max_pages, const int32_t *lens, const int32_t *chunk_start,
+                                  const int32_t *chunk_seq, int B, int H, int Hkv, float scale,
+                                  int total_chunks, uint16_t *out, void *stream);
 
 /* Causal attention of prefill chunks over the paged pool: the other half of a
  * chunked-prefill step (mx.fast.scaled_dot_product_attention with mask = "causal"

@@ -15,6 +15,7 @@ JIT_OK = 0
 JIT_EINVAL = -1
 JIT_EUNSUPPORTED = -2
 JIT_ELAUNCH = -3
+JIT_ATTN_SCRATCH_BYTES = 16 << 20  # jit_paged_decode_attn_noalloc's partials limit
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -48,6 +49,7 @@ _SIGNATURES = {
     "jit_attn_plan": [_P, _I, _P, _P, _I],
     "jit_attn_workspace_bytes": [_I, _I],
     "jit_paged_decode_attn": [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P, _P],
+    "jit_paged_decode_attn_noalloc": [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P],
     "jit_prefill_block_tokens": [_I, _I],
     "jit_paged_prefill_attn": [_P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _F, _P, _P],
     "jit_embed_q4": [_P, _I, _P, _P, _P, _I, _I, _P, _P],

@@ -26,6 +26,8 @@
 // attn_merge_kernel combines in chunk order.
 #include "common.hpp"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kD = JIT_HEAD_DIM;      // 128
@@ -751,29 +753,105 @@ extern "C" int64_t jit_attn_workspace_bytes(int total_chunks, int H) {
   return (int64_t)total_chunks * H * (kD + 2) * (int64_t)sizeof(float);
 }
 
+namespace {
+
+// The two launches of a decode-attention call: the split-K chunks, then the chunk-order merge.
+// `workspace` holds the fp32 partials of multi-chunk sequences (every partial the merge reads
+// is written by the first launch of the same call, so nothing in it has to start at zero).
+int decode_attn_launch(const uint16_t *q, const uint16_t *pool, const int32_t *page_table, int max_pages,
+                       const int32_t *lens, const int32_t *chunk_start, const int32_t *chunk_seq, int B, int H,
+                       int Hkv, float scale, int total_chunks, void *workspace, uint16_t *out, hipStream_t st,
+                       const char *what) {
+  float *part_o = (float *)workspace;
+  float *part_ml = part_o + (long long)total_chunks * H * kD;
+  AttnArgs a{q, pool, page_table, lens, chunk_start, chunk_seq, part_o, part_ml, out,
+             max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f};
+  constexpr int WS = kAttnSplits;
+  const int hb = Hkv < kAttnHeadsPerBlock ? Hkv : kAttnHeadsPerBlock;  // kv heads per workgroup (WS waves each)
+  const size_t lds = (size_t)(WS - 1) * hb * kStateFloats * 64 * sizeof(float);
+  paged_attn_kernel<WS><<<dim3(total_chunks, (Hkv + hb - 1) / hb), 64 * hb * WS, lds, st>>>(a);
+  int rc = jit::check_launch(what);
+  if (rc) return rc;
+  attn_merge_kernel<<<dim3(B, H), 512, 0, st>>>(lens, chunk_start, part_o, part_ml, H, out);
+  return jit::check_launch(what);
+}
+
+// Scalar contract shared by both decode-attention entry points (host only, before any launch).
+int decode_attn_contract(int B, int H, int Hkv, int max_pages, int total_chunks, const char *what) {
+  if (B < 0 || H <= 0 || Hkv <= 0 || max_pages <= 0 || total_chunks < 0)
+    return jit::fail(JIT_EINVAL, "%s: bad dims B=%d H=%d Hkv=%d", what, B, H, Hkv);
+  if (H % Hkv != 0) return jit::fail(JIT_EINVAL, "%d query heads do not share %d KV heads evenly", H, Hkv);
+  if (H / Hkv > 16) return jit::fail(JIT_EUNSUPPORTED, "%s covers H / Hkv <= 16, got %d", what, H / Hkv);
+  return JIT_OK;
+}
+
+// ------------------------------------------------------------ allocation-free variant
+// The split-K partials of jit_paged_decode_attn_noalloc live in this file-scope device array
+// instead of a caller's workspace: every device the library runs on holds its own copy until
+// the process ends.  On the host, `scratch` names a host-side stand-in, not device memory, so
+// it is never passed to a kernel, a copy or a fill: host code uses only the per-device address
+// hipGetSymbolAddress returns (g_scratch_dev), taken once per device with that device current.
+static __device__ __align__(256) unsigned char scratch[JIT_ATTN_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_dev[kMaxDevices];
+
+// The current device's address of `scratch` (looked up on the first call on that device).
+int scratch_of_current_device(void **ptr, const char *what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return jit::fail(JIT_ELAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return jit::fail(JIT_EUNSUPPORTED, "%s: device %d is past the %d devices the scratch table covers", what, dev,
+                     kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return jit::fail(JIT_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                       hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *ptr = g_scratch_dev[dev];
+  return JIT_OK;
+}
+
+}  // namespace
+
 extern "C" int jit_paged_decode_attn(const uint16_t *q, const uint16_t *pool,
                                      const int32_t *page_table, int max_pages, const int32_t *lens,
                                      const int32_t *chunk_start, const int32_t *chunk_seq, int B,
                                      int H, int Hkv, float scale, int total_chunks, void *workspace,
                                      uint16_t *out, void *stream) {
-  if (B < 0 || H <= 0 || Hkv <= 0 || max_pages <= 0 || total_chunks < 0)
-    return jit::fail(JIT_EINVAL, "paged_decode_attn: bad dims B=%d H=%d Hkv=%d", B, H, Hkv);
-  if (H % Hkv != 0) return jit::fail(JIT_EINVAL, "%d query heads do not share %d KV heads evenly", H, Hkv);
-  if (H / Hkv > 16) return jit::fail(JIT_EUNSUPPORTED, "paged_decode_attn covers H / Hkv <= 16, got %d", H / Hkv);
+  int rc = decode_attn_contract(B, H, Hkv, max_pages, total_chunks, "paged_decode_attn");
+  if (rc) return rc;
   if (B == 0 || total_chunks == 0) return JIT_OK;
   if (!q || !pool || !page_table || !lens || !chunk_start || !chunk_seq || !workspace || !out)
     return jit::fail(JIT_EINVAL, "paged_decode_attn: null pointer");
-  float *part_o = (float *)workspace;
-  float *part_ml = part_o + (long long)total_chunks * H * kD;
-  AttnArgs a{q, pool, page_table, lens, chunk_start, chunk_seq, part_o, part_ml, out,
-             max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f};
-  hipStream_t st = (hipStream_t)stream;
-  constexpr int WS = kAttnSplits;
-  const int hb = Hkv < kAttnHeadsPerBlock ? Hkv : kAttnHeadsPerBlock;  // kv heads per workgroup (WS waves each)
-  const size_t lds = (size_t)(WS - 1) * hb * kStateFloats * 64 * sizeof(float);
-  paged_attn_kernel<WS><<<dim3(total_chunks, (Hkv + hb - 1) / hb), 64 * hb * WS, lds, st>>>(a);
-  int rc = jit::check_launch("jit_paged_decode_attn");
+  return decode_attn_launch(q, pool, page_table, max_pages, lens, chunk_start, chunk_seq, B, H, Hkv, scale,
+                            total_chunks, workspace, out, (hipStream_t)stream, "jit_paged_decode_attn");
+}
+
+extern "C" int jit_paged_decode_attn_noalloc(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,
+                                             int max_pages, const int32_t *lens, const int32_t *chunk_start,
+                                             const int32_t *chunk_seq, int B, int H, int Hkv, float scale,
+                                             int total_chunks, uint16_t *out, void *stream) {
+  int rc = decode_attn_contract(B, H, Hkv, max_pages, total_chunks, "paged_decode_attn_noalloc");
   if (rc) return rc;
-  attn_merge_kernel<<<dim3(B, H), 512, 0, st>>>(lens, chunk_start, part_o, part_ml, H, out);
-  return jit::check_launch("jit_paged_decode_attn merge");
+  const int64_t need = jit_attn_workspace_bytes(total_chunks, H);
+  if (need > (int64_t)JIT_ATTN_SCRATCH_BYTES)
+    return jit::fail(JIT_EUNSUPPORTED,
+                     "paged_decode_attn_noalloc: %d chunks x %d heads need %lld bytes of partials, past the "
+                     "%d-byte scratch (use jit_paged_decode_attn with a workspace)",
+                     total_chunks, H, (long long)need, (int)JIT_ATTN_SCRATCH_BYTES);
+  if (B == 0 || total_chunks == 0) return JIT_OK;
+  if (!q || !pool || !page_table || !lens || !chunk_start || !chunk_seq || !out)
+    return jit::fail(JIT_EINVAL, "paged_decode_attn_noalloc: null pointer");
+  void *ws = nullptr;
+  rc = scratch_of_current_device(&ws, "paged_decode_attn_noalloc");
+  if (rc) return rc;
+  return decode_attn_launch(q, pool, page_table, max_pages, lens, chunk_start, chunk_seq, B, H, Hkv, scale,
+                            total_chunks, ws, out, (hipStream_t)stream, "jit_paged_decode_attn_noalloc");
 }

@@ -551,6 +551,36 @@ def paged_decode_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torc
     return out
 
 
+def paged_decode_attention_noalloc(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor,
+                                   plan: AttnPlan, scale: float, out: torch.Tensor):
+    """paged_decode_attention into a caller-given `out` [B, H, 128] bf16, with the split-K partials in
+    the library's fixed device scratch (jit_paged_decode_attn_noalloc): nothing is allocated, for
+    callers that cannot allocate.  Calls overlapping in time on one GPU race on that scratch."""
+    _need(q, torch.bfloat16, "q")
+    _need(pool, torch.bfloat16, "pool")
+    _need(page_table, torch.int32, "page_table")
+    _need(out, torch.bfloat16, "out")
+    B, H, Dh = q.shape
+    Hkv = _pool_heads(pool)
+    if Dh != HEAD_DIM:
+        raise _lib.UnsupportedShape(f"paged_decode_attention covers head_dim 128, got {Dh}")
+    if out.shape != q.shape:
+        raise ValueError(f"out {tuple(out.shape)} must match q {tuple(q.shape)}")
+    if plan.lens.shape[0] != B or page_table.shape[0] != B:
+        raise ValueError("q, page_table and plan disagree on the number of sequences")
+    if B and int((plan.lens_host.max() + PAGE - 1) // PAGE) > page_table.shape[1]:
+        raise ValueError(f"page_table has {page_table.shape[1]} columns, the longest sequence needs "
+                         f"{int((plan.lens_host.max() + PAGE - 1) // PAGE)}")
+    _lib.check(
+        _lib.lib().jit_paged_decode_attn_noalloc(
+            _p(q), _p(pool), _p(page_table), page_table.shape[1], _p(plan.lens), _p(plan.chunk_start),
+            _p(plan.chunk_seq), B, H, Hkv, float(scale), plan.total, _p(out), _stream(),
+        ),
+        "paged_decode_attn_noalloc",
+    )
+    return out
+
+
 # ----------------------------------------------------------------------------- step ends, KV pages
 def embed_q4(ids: torch.Tensor, table: QLinear) -> torch.Tensor:
     """Embedding rows [B, D] bf16 of token ids [B] int32 from an MLX 4-bit table [V, D]
