@@ -152,6 +152,14 @@ int jit_moe_gate_up_swiglu_packed(const uint16_t *x, int K, const int32_t *pair_
                                   const int32_t *expert_cnt, const int32_t *expert_off, int E,
                                   const void *packed, int I, int P, uint16_t *h, void *stream);
 
+/* Elementwise SwiGLU of bf16 gate and up values: h[i] = bf16(bf16(g[i] * SigmoidX(g[i])) * u[i]),
+ * SigmoidX's steps each rounded to bf16 (e = bf16(exp|g|), d = bf16(1 + e), y = bf16(1 / d),
+ * g < 0 ? y : bf16(1 - y)) -- exactly the epilogue of jit_moe_gate_up_swiglu* on given operands.
+ * Replaces the stock swiglu (Q36/kernels/elementwise.py:14-15, nn.silu(gate) * x in bf16, used by
+ * Q36/model/moe.py:189-197).  g, u, h: n bf16 values, 16-byte aligned.  NaN inputs give NaN
+ * outputs (payload bits unspecified). */
+int jit_swiglu(const uint16_t *g, const uint16_t *u, int64_t n, uint16_t *h, void *stream);
+
 /* Grouped down projection over packed pairs: r[p] = bf16(h[p] . dequant(Wd_e)^T)
  * for every sorted pair p of expert e (the down gather of Q36/model/moe.py:193;
  * the per-expert GEMV inside expert_down_exact(_par),

@@ -13,7 +13,8 @@
 // pages (32 keys) per step; the 4 waves' states meet in LDS:
 //   S^T[16 keys x 16 q heads] = K_page . Q^T      (4 MFMA 16x16x32 per page)
 //   online softmax in the exp2 domain (fp32 running max / sum per q head)
-//   O^T[128 d x 16 q heads] += V^T . P^T           (8 MFMA 16x16x32, all 32 keys)
+//   O^T[128 d x 16 q heads] += V^T . P^T           (16 MFMA 16x16x32, all 32 keys: P as a
+//                                                   bf16 high part plus a bf16 residual)
 // Every lane owns one q head (lane % 16) in the scores, the softmax state and the
 // output tile alike, so the rescale needs no lane exchange; the cross-lane max and
 // sum use the gfx950 permlane swaps.  Each K/V byte is read once for all
@@ -260,14 +261,20 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    // P^T fragment (B operand): head lr, k slots 8*lg + j = key 4*lg + j of the first
-    // page (j < 4) and of the second (j >= 4) -- the lane's own probabilities
-    Frag8 pf;
-    pf.u[0] = pack_bf16x2_rne(p0[0], p0[1]);
-    pf.u[1] = pack_bf16x2_rne(p0[2], p0[3]);
-    pf.u[2] = pack_bf16x2_rne(p1[0], p1[1]);
-    pf.u[3] = pack_bf16x2_rne(p1[2], p1[3]);
-    if (lr >= G) pf.q = make_uint4(0, 0, 0, 0);
+    // P^T fragments (B operand): head lr, k slots 8*lg + j = key 4*lg + j of the first
+    // page (j < 4) and of the second (j >= 4) -- the lane's own probabilities, as bf16
+    // high parts (pf) and bf16 residuals (pl): O^T += V^T . pf^T + V^T . pl^T keeps P at
+    // 16 significant bits, as the reference's fp32 P.V does (one bf16 P rounds each
+    // probability by up to 2^-9 and moves ~40% of the bf16 outputs by an ulp)
+    Frag8 pf, pl;
+    split_bf16x2(p0[0], p0[1], pf.u[0], pl.u[0]);
+    split_bf16x2(p0[2], p0[3], pf.u[1], pl.u[1]);
+    split_bf16x2(p1[0], p1[1], pf.u[2], pl.u[2]);
+    split_bf16x2(p1[2], p1[3], pf.u[3], pl.u[3]);
+    if (lr >= G) {
+      pf.q = make_uint4(0, 0, 0, 0);
+      pl.q = make_uint4(0, 0, 0, 0);
+    }
     // the tail page may hold stale slots past L: their p is 0, make their V 0 too
     if (k0 + 32 > L) {
       const int kb = k0 + 4 * lg;
@@ -286,15 +293,17 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) o[cc][i] *= alpha;
     }
+    Frag8 vf[8];
 #pragma unroll
     for (int cc = 0; cc < 8; cc++) {
-      Frag8 vf;
-      vf.u[0] = vv[0][cc].x;
-      vf.u[1] = vv[0][cc].y;
-      vf.u[2] = vv[1][cc].x;
-      vf.u[3] = vv[1][cc].y;
-      o[cc] = mfma16x16x32(vf, pf, o[cc]);
+      vf[cc].u[0] = vv[0][cc].x;
+      vf[cc].u[1] = vv[0][cc].y;
+      vf[cc].u[2] = vv[1][cc].x;
+      vf[cc].u[3] = vv[1][cc].y;
+      o[cc] = mfma16x16x32(vf[cc], pf, o[cc]);
     }
+#pragma unroll
+    for (int cc = 0; cc < 8; cc++) o[cc] = mfma16x16x32(vf[cc], pl, o[cc]);
     load_v2(vv, a.pool, a.Hkv, kvh, page(2 * st + 2), page(2 * st + 3), lr, lg);
     // keep these loads in this step: sunk into the next step they would only be
     // issued once that step's K has arrived
@@ -420,6 +429,10 @@ __global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restri
   w.y = pack_bf16x2(acc.z * inv, acc.w * inv);
   *(uint2 *)(out + ((long long)b * H + h) * kD + 4 * t) = w;
 }
+
+#ifndef JIT_PF_PSPLIT
+#define JIT_PF_PSPLIT 1  // prefill P.V with P as bf16 high part + bf16 residual (two MFMAs)
+#endif
 
 // ---------------------------------------------------------------- prefill (causal chunks)
 // Causal attention of prefill chunks over the paged pool: query token t of a chunk (at
@@ -570,21 +583,19 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-    // online softmax of every tile over the step's keys
-    uint32_t pw[kPfTiles][kPfHalves][4];  // P^T fragments (bf16 pairs; set for the tiles the step reaches)
+    // online softmax of every tile over the step's keys: the masked scores' running max first
+    // (the o rescale happens before the step's first P.V MFMA), then, half by half, the
+    // probabilities, their sum and the P.V products, so that only one half's P fragments are live
+    float m_step[kPfTiles], alpha[kPfTiles], psum[kPfTiles];
 #pragma unroll
     for (int j = 0; j < kPfTiles; j++) {
+      psum[j] = 0.0f;
+      alpha[j] = 1.0f;
+      m_step[j] = m_run[j];
       if (k0 > tile_last[j]) continue;  // every key of the step is past the tile's rows
       // keys past a row's position are masked on the steps that reach into the tile's rows;
       // the scale is applied inside the exponent (max of the raw scores times the positive
       // scale is the max of the scaled ones)
-      float p[kPfHalves][2][4];
-#pragma unroll
-      for (int h = 0; h < kPfHalves; h++)
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) p[h][t][i] = sc[j][h][t][i];
       if (k0 + 32 * kPfHalves - 1 > tile_first[j]) {
         const int pos = ctx + tok[j];
 #pragma unroll
@@ -594,50 +605,58 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
 #pragma unroll
             for (int i = 0; i < 4; i++) {
               const int key = k0 + 32 * h + 8 * lg + 4 * t + i;
-              p[h][t][i] = key <= pos ? p[h][t][i] : -INFINITY;
+              sc[j][h][t][i] = key <= pos ? sc[j][h][t][i] : -INFINITY;
             }
       }
-      float tmax = p[0][0][0];
+      float tmax = sc[j][0][0][0];
 #pragma unroll
       for (int h = 0; h < kPfHalves; h++)
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) tmax = fmaxf(tmax, p[h][t][i]);
+          for (int i = 0; i < 4; i++) tmax = fmaxf(tmax, sc[j][h][t][i]);
       tmax = max_xor32(max_xor16(tmax)) * a.qk_scale;
-      const float m_new = fmaxf(m_run[j], tmax);  // finite: key 0 is in every row's first step
-      const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
-      float psum = 0.0f;
+      m_step[j] = fmaxf(m_run[j], tmax);  // finite: key 0 is in every row's first step
+      alpha[j] = __builtin_amdgcn_exp2f(m_run[j] - m_step[j]);
+      if (__any(alpha[j] != 1.0f)) {
 #pragma unroll
-      for (int h = 0; h < kPfHalves; h++)
+        for (int cc = 0; cc < 8; cc++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) o[j][cc][i] *= alpha[j];
+      }
+    }
+    // O^T += V^T . P^T for every tile and half, a quarter of the V fragments (32 dims of a half)
+    // at a time; the lane's 8 keys are slots 8 (lg % 2) .. + 7 of page lg / 2
+#pragma unroll
+    for (int h = 0; h < kPfHalves; h++) {
+      // the half's P^T fragments: bf16 high parts (pw) and, with JIT_PF_PSPLIT, bf16 residuals (pl)
+      uint32_t pw[kPfTiles][4];
+#if JIT_PF_PSPLIT
+      uint32_t pl[kPfTiles][4];
+#endif
+#pragma unroll
+      for (int j = 0; j < kPfTiles; j++) {
+        if (k0 > tile_last[j]) continue;
+        float p[2][4];
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            p[h][t][i] = __builtin_amdgcn_exp2f(fmaf(p[h][t][i], a.qk_scale, -m_new));
-            psum += p[h][t][i];
+            p[t][i] = __builtin_amdgcn_exp2f(fmaf(sc[j][h][t][i], a.qk_scale, -m_step[j]));
+            psum[j] += p[t][i];
           }
-      l_run[j] = l_run[j] * alpha + psum;
-      m_run[j] = m_new;
-#pragma unroll
-      for (int h = 0; h < kPfHalves; h++) {
-        pw[j][h][0] = pack_bf16x2_rne(p[h][0][0], p[h][0][1]);
-        pw[j][h][1] = pack_bf16x2_rne(p[h][0][2], p[h][0][3]);
-        pw[j][h][2] = pack_bf16x2_rne(p[h][1][0], p[h][1][1]);
-        pw[j][h][3] = pack_bf16x2_rne(p[h][1][2], p[h][1][3]);
+#if JIT_PF_PSPLIT
+        split_bf16x2(p[0][0], p[0][1], pw[j][0], pl[j][0]);
+        split_bf16x2(p[0][2], p[0][3], pw[j][1], pl[j][1]);
+        split_bf16x2(p[1][0], p[1][1], pw[j][2], pl[j][2]);
+        split_bf16x2(p[1][2], p[1][3], pw[j][3], pl[j][3]);
+#else
+        pw[j][0] = pack_bf16x2_rne(p[0][0], p[0][1]);
+        pw[j][1] = pack_bf16x2_rne(p[0][2], p[0][3]);
+        pw[j][2] = pack_bf16x2_rne(p[1][0], p[1][1]);
+        pw[j][3] = pack_bf16x2_rne(p[1][2], p[1][3]);
+#endif
       }
-      if (__any(alpha != 1.0f)) {
-#pragma unroll
-        for (int cc = 0; cc < 8; cc++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) o[j][cc][i] *= alpha;
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // phase 2: O^T += V^T . P^T for every tile and half, a quarter of the V fragments (32
-    // dims of a half) at a time; the lane's 8 keys are slots 8 (lg % 2) .. + 7 of page lg / 2
-#pragma unroll
-    for (int h = 0; h < kPfHalves; h++) {
       const uint16_t *kvsc = kvst + h * 4 * kPageHead;
       const int kh = k0 + 32 * h;
 #pragma unroll
@@ -659,12 +678,24 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
           if (k0 > tile_last[j]) continue;
           Frag8 pf;
 #pragma unroll
-          for (int i = 0; i < 4; i++) pf.u[i] = pw[j][h][i];
+          for (int i = 0; i < 4; i++) pf.u[i] = pw[j][i];
 #pragma unroll
           for (int c4 = 0; c4 < 4; c4++) o[j][4 * hv + c4] = mfma16x16x32(vf[c4], pf, o[j][4 * hv + c4]);
+#if JIT_PF_PSPLIT
+#pragma unroll
+          for (int i = 0; i < 4; i++) pf.u[i] = pl[j][i];
+#pragma unroll
+          for (int c4 = 0; c4 < 4; c4++) o[j][4 * hv + c4] = mfma16x16x32(vf[c4], pf, o[j][4 * hv + c4]);
+#endif
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+    }
+#pragma unroll
+    for (int j = 0; j < kPfTiles; j++) {
+      if (k0 > tile_last[j]) continue;
+      l_run[j] = l_run[j] * alpha[j] + psum[j];
+      m_run[j] = m_step[j];
     }
   }
 #undef PF_STAGE

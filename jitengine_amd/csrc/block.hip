@@ -8,6 +8,7 @@
 // returns bf16(w * bf16(x * rsqrt(mean + eps))); RoPE (traditional = False)
 // rotates the pairs (x[i], x[i + D/2]) by pos * inv_freq[i] in fp32.
 #include "common.hpp"
+#include "qtile.hpp"
 
 namespace {
 
@@ -239,7 +240,38 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
   }
 }
 
+// Elementwise SwiGLU on bf16 g, u: the expert GEMM epilogue's chain (qtile::swiglu_bf16) on given
+// operands, 8 values per thread.
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *__restrict__ g, const uint16_t *__restrict__ u,
+                                                     long long n, uint16_t *__restrict__ h) {
+  const long long i0 = ((long long)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i0 >= n) return;
+  if (i0 + 8 <= n) {
+    const uint4 gv = *(const uint4 *)(g + i0), uv = *(const uint4 *)(u + i0);
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t hw[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      hw[j] = qtile::swiglu_bf16(bf2f(gw[j] & 0xffffu), bf2f(uw[j] & 0xffffu)) |
+              (qtile::swiglu_bf16(bf2f_hi(gw[j]), bf2f_hi(uw[j])) << 16);
+    *(uint4 *)(h + i0) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  } else {
+    for (long long i = i0; i < n; i++) h[i] = (uint16_t)qtile::swiglu_bf16(bf2f(g[i]), bf2f(u[i]));
+  }
+}
+
 }  // namespace
+
+extern "C" int jit_swiglu(const uint16_t *g, const uint16_t *u, int64_t n, uint16_t *h, void *stream) {
+  if (n < 0) return jit::fail(JIT_EINVAL, "swiglu: bad length %lld", (long long)n);
+  if (n == 0) return JIT_OK;
+  if (!g || !u || !h) return jit::fail(JIT_EINVAL, "swiglu: null pointer");
+  if (((uintptr_t)g | (uintptr_t)u | (uintptr_t)h) & 15)
+    return jit::fail(JIT_EINVAL, "swiglu: g, u and h must be 16-byte aligned");
+  const long long blocks = (n + 256 * 8 - 1) / (256 * 8);
+  swiglu_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(g, u, (long long)n, h);
+  return jit::check_launch("jit_swiglu");
+}
 
 extern "C" int jit_rmsnorm(const uint16_t *x, const uint16_t *resid, int rows, int D, const uint16_t *w,
                            float eps, uint16_t *h_out, uint16_t *y, void *stream) {

@@ -53,6 +53,15 @@ __device__ __forceinline__ void round_bf2(float &a, float &b) {
   b = __uint_as_float(p & 0xffff0000u);
 }
 
+// Split two floats into bf16 high parts and bf16 residuals: hi = bf16(a), lo = bf16(a - hi) (the
+// subtraction is exact).  hi + lo carries a to 16 significant bits (relative error <= 2^-17), so a
+// P.V product issued as two bf16 MFMAs, V.hi + V.lo, keeps the probabilities at nearly fp32
+// precision where one bf16 P would round each of them by up to 2^-9.
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t &hi, uint32_t &lo) {
+  hi = pack_bf16x2_rne(a, b);
+  lo = pack_bf16x2_rne(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+}
+
 // ------------------------------------------------------------------ wave
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 

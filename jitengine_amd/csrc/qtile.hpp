@@ -106,13 +106,55 @@ __device__ __forceinline__ f32x4 group_xsum(const Frag8 (&xa)[2]) {
   return mfma16x16x32(xa[1], ones, X);
 }
 
-// SwiGLU with the reference's bf16 rounding points: g, u rounded; sigmoid(g)
-// rounded; bf16(g * sigmoid) * u rounded.
+// e^x for 0 <= x: Cody-Waite reduction x = n ln2 + r with fdlibm's two-part ln2, degree-7
+// Taylor polynomial of e^r in Horner form with fused multiply-adds, scaled by 2^(n-1) and then 2
+// (n = 128 stays finite); x > 89 or NaN gives x * inf.  The CPU restatement (jo_exp_pos) runs
+// the identical operation sequence, so the sigmoid below rounds the same fp32 value to bf16.
+__device__ __forceinline__ float exp_pos(float x) {
+#pragma clang fp contract(off)
+  if (!(x <= 89.0f)) return x * __builtin_inff();
+  const float t = x * 1.44269504088896341f;
+  const float n = __builtin_rintf(t);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.42860682030941723e-6f, r);
+  float p = 1.98412698412698413e-4f;
+  p = __builtin_fmaf(p, r, 1.38888888888888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666666666666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666666666666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int e = (int)n;
+  const float sc = __uint_as_float((uint32_t)(e - 1 + 127) << 23);
+  return (p * sc) * 2.0f;
+}
+
+// bf16 round trip of a float (round to nearest even, v_cvt_pk_bf16_f32): exact for every
+// number; NaN payloads are not kept (the final outputs below still go through f2bf).
+__device__ __forceinline__ float rne_bf16(float x) { return static_cast<float>(static_cast<__bf16>(x)); }
+
+// SigmoidX on a bf16 value g (MLX's Sigmoid on bf16, Q36/kernels/expert_solo.py:56-62): every
+// step is an fp32 operation on bf16 operands rounded to bf16 -- e = bf16(exp|g|),
+// d = bf16(1 + e), y = bf16(1 / d), g < 0 ? y : bf16(1 - y) -- the bits of the CPU restatement
+// (which divides correctly rounded).  1 / d: the reciprocal of any bf16 value lies at least 192
+// fp32 ulps from every bf16 rounding tie, so the 1-ulp hardware reciprocal rounds to the same bf16;
+// from d = 2^126 on (|g| > 87.3) the reciprocal is subnormal and is formed as rcp(d / 4) / 4.
+__device__ __forceinline__ float sigmoid_bf16(float g) {
+#pragma clang fp contract(off)
+  const float e = rne_bf16(exp_pos(fabsf(g)));
+  const float d = rne_bf16(1.0f + e);
+  const float sc = d < 0x1p126f ? 1.0f : 0.25f;
+  const float y = rne_bf16(__builtin_amdgcn_rcpf(d * sc) * sc);
+  return g < 0.0f ? y : rne_bf16(1.0f - y);
+}
+
+// SwiGLU with the reference's bf16 rounding points (Q36/kernels/expert_solo.py:106-115): g, u
+// rounded; sigmoid(g) by the bf16 steps above; sl = bf16(g * sigmoid); h = bf16(sl * u).
 __device__ __forceinline__ uint32_t swiglu_bf16(float gacc, float uacc) {
-  const float g = bf2f(f2bf(gacc)), u = bf2f(f2bf(uacc));
-  const float y = 1.0f / (1.0f + __expf(fabsf(g)));
-  const float sg = bf2f(f2bf(g < 0.0f ? y : 1.0f - y));
-  const float sl = bf2f(f2bf(g * sg));
+#pragma clang fp contract(off)
+  const float g = rne_bf16(gacc), u = rne_bf16(uacc);
+  const float sl = rne_bf16(g * sigmoid_bf16(g));
   return f2bf(sl * u);
 }
 

@@ -272,6 +272,18 @@ def expert_gate_up(x: torch.Tensor, gate_up, pk: Packing, seg: bool = False) -> 
     return h
 
 
+def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    """Elementwise SwiGLU of bf16 g, u (the stock swiglu, Q36/kernels/elementwise.py:14-15:
+    nn.silu(gate) * up with every step rounded to bf16), via jit_swiglu."""
+    _need(g, torch.bfloat16, "g")
+    _need(u, torch.bfloat16, "u")
+    if g.shape != u.shape:
+        raise ValueError(f"g {tuple(g.shape)} and u {tuple(u.shape)} differ")
+    h = torch.empty_like(g)
+    _lib.check(_lib.lib().jit_swiglu(_p(g), _p(u), g.numel(), _p(h), _stream()), "swiglu")
+    return h
+
+
 def expert_down(h: torch.Tensor, down, pk: Packing, seg: bool = False) -> torch.Tensor:
     """h [P, I] bf16, stack [E, D, I] -> r [P, D] bf16 (the down gather, Q36/model/moe.py:193);
     seg=True: the segment GEMM (jit_moe_down_seg), as in expert_gate_up."""

@@ -13,6 +13,9 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
   dequant4                known-answer words + an independent numpy unpack
   qmm                     vs torch float64 matmul of independently dequantized weights
   qmv_mlx_f32             vs float64 within fp32 accumulation bounds (it is only an error yardstick)
+  exp_pos                 vs math.exp within 2 ulp over [0, 88.7] (closed form)
+  sigmoid_bf16            exhaustively over every bf16 g vs an independent numpy restatement of the
+                          SigmoidX bf16 steps (float64 exp); they differ only within 2^-16 of a tie
   swiglu_bf16             vs float64 silu(g) * u within bf16 rounding bounds
   moe_gate_up / moe_down  vs qmm + swiglu composed in numpy (different code path, same maths)
   moe_combine             vs torch bf16 ops in slot order (a library routine)
@@ -20,6 +23,8 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
   q4_prepack              a byte permutation (multiset of bytes preserved, every word placed once);
                           on the GPU, GEMMs on packed and MLX layouts agree bit for bit
   paged_decode_attn       vs torch scaled_dot_product_attention in float64 on gathered KV
+  sdpa_mlx_f32            vs float64 within fp32 bounds; n = 1 gives v[0]; one-pass/two-pass routing
+                          and the bf16 partials of the two-pass form (it is only an error yardstick)
   embed_q4                vs torch's own bf16 multiply and add (a library routine), q = 0 rows = bias
   argmax_rows             vs numpy argmax (first index of the maximum) on NaN-free rows
 """
@@ -55,7 +60,10 @@ def lib():
         _LIB.jo_f2bf.argtypes = [ctypes.c_float]
         _LIB.jo_swiglu_bf16.restype = ctypes.c_uint16
         _LIB.jo_swiglu_bf16.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
-        _LIB.jo_paged_decode_attn.argtypes = [_P, _P, _P, _I, _P, _I, _I, _I, _I, ctypes.c_float, _P]
+        _LIB.jo_paged_decode_attn.argtypes = [_P, _P, _P, _I, _P, _I, _I, _I, _I, ctypes.c_float, _P, _P]
+        _LIB.jo_sdpa_mlx_f32.argtypes = [_P, _P, _P, _I, _P, _I, _I, _I, _I, ctypes.c_float, _P, _P]
+        _LIB.jo_exp_pos.restype = ctypes.c_float
+        _LIB.jo_exp_pos.argtypes = [ctypes.c_float]
         _LIB.jo_num_threads.restype = _I
     return _LIB
 
@@ -85,10 +93,13 @@ def _u32(a) -> np.ndarray:
 # ----------------------------------------------------------------------------- bf16 helpers
 def f32_to_bf16(x) -> np.ndarray:
     """Round float32 values to bf16 bit patterns (nearest-even), as the oracle and kernels do."""
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    nan = (u & 0x7FFFFFFF) > 0x7F800000
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = (u & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    with np.errstate(over="ignore"):  # only NaN patterns wrap, and those are replaced below
+        r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    if nan.any():
+        r = np.where(nan, ((u >> np.uint32(16)) | np.uint32(0x40)).astype(np.uint16), r)
+    return r
 
 
 def bf16_to_f32(h) -> np.ndarray:
@@ -105,6 +116,18 @@ def set_num_threads(n: int) -> None:
 
 def exp_neg(x: float) -> float:
     return float(lib().jo_exp_neg(float(x)))
+
+
+def exp_pos(x: float) -> float:
+    return float(lib().jo_exp_pos(float(x)))
+
+
+def sigmoid_bf16(g) -> np.ndarray:
+    """SigmoidX on bf16 g (any shape), each step rounded to bf16 (Q36/kernels/expert_solo.py:56-62)."""
+    g = _u16(g)
+    out = np.empty_like(g)
+    _check(lib().jo_sigmoid_bf16_n(_p(g), int(g.size), _p(out)), "sigmoid_bf16")
+    return out
 
 
 def swiglu_bf16(g: int, u: int) -> int:
@@ -345,12 +368,12 @@ def kv_gather(pool, page_row, n: int, Hkv: int, Dh: int):
     return kc, vc
 
 
-def paged_prefill_attn(q, pool, page_table, chunks, scale: float) -> np.ndarray:
+def paged_prefill_attn(q, pool, page_table, chunks, scale: float, exact: bool = False):
     """Causal attention of prefill chunks: q [T, H, Dh] bf16 holds the chunks' rows in order; chunk
     (seq, ctx, length) owns the next `length` rows, and its token t (position ctx + t of sequence
     seq) attends keys 0 .. ctx + t of page_table[seq] -- decode attention of that token over
     ctx + t + 1 keys (the causal mask of mx.fast.scaled_dot_product_attention, aligned to the last
-    key), so this is paged_decode_attn row by row."""
+    key), so this is paged_decode_attn row by row.  exact=True also returns the float64 values."""
     pt = _i32(page_table)
     lens, rows = [], []
     for seq, ctx, length in chunks:
@@ -358,23 +381,44 @@ def paged_prefill_attn(q, pool, page_table, chunks, scale: float) -> np.ndarray:
             lens.append(ctx + t + 1)
             rows.append(pt[seq])
     if not lens:
-        return np.empty_like(_u16(q))
-    return paged_decode_attn(q, pool, np.stack(rows), np.array(lens, np.int32), scale)
+        e = np.empty_like(_u16(q))
+        return (e, e.astype(np.float64)) if exact else e
+    return paged_decode_attn(q, pool, np.stack(rows), np.array(lens, np.int32), scale, exact=exact)
 
 
-def paged_decode_attn(q, pool, page_table, lens, scale: float) -> np.ndarray:
-    """q [B, H, Dh] bf16 -> out [B, H, Dh] bf16 (float64 softmax attention over lens[b] tokens)."""
+def paged_decode_attn(q, pool, page_table, lens, scale: float, exact: bool = False):
+    """q [B, H, Dh] bf16 -> out [B, H, Dh] bf16 (float64 softmax attention over lens[b] tokens);
+    with exact=True also the float64 values before the bf16 rounding: (out, out64)."""
     q, pool, pt, ln = _u16(q), _u16(pool), _i32(page_table), _i32(lens)
     B, H, Dh = q.shape
     Hkv = pool.shape[1]
     out = np.empty_like(q)
+    out64 = np.empty(q.shape, np.float64) if exact else None
     _check(
         lib().jo_paged_decode_attn(
-            _p(q), _p(pool), _p(pt), pt.shape[1], _p(ln), B, H, Hkv, Dh, float(scale), _p(out)
+            _p(q), _p(pool), _p(pt), pt.shape[1], _p(ln), B, H, Hkv, Dh, float(scale), _p(out),
+            None if out64 is None else _p(out64),
         ),
         "paged_decode_attn",
     )
-    return out
+    return (out, out64) if exact else out
+
+
+def sdpa_mlx_f32(q, pool, page_table, lens, scale: float):
+    """The reference's stock decode attention in MLX's fp32 arithmetic (one-pass sdpa_vector, or the
+    two-pass kernels with bf16 partials, routed as on the reference's M4 Pro): (out bf16, out fp32)."""
+    q, pool, pt, ln = _u16(q), _u16(pool), _i32(page_table), _i32(lens)
+    B, H, Dh = q.shape
+    Hkv = pool.shape[1]
+    out = np.empty_like(q)
+    f32 = np.empty(q.shape, np.float32)
+    _check(
+        lib().jo_sdpa_mlx_f32(
+            _p(q), _p(pool), _p(pt), pt.shape[1], _p(ln), B, H, Hkv, Dh, float(scale), _p(out), _p(f32)
+        ),
+        "sdpa_mlx_f32",
+    )
+    return out, f32
 
 
 def embed_q4(ids, w, s, b) -> np.ndarray:

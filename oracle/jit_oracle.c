@@ -344,20 +344,63 @@ int jo_qmv_mlx_f32(const uint16_t *x, int T, const uint32_t *w, const uint16_t *
 }
 
 /* ------------------------------------------------ a4 gate||up + SwiGLU
- * One pair p (sorted position) against expert e's fused gate||up stack
- * [2I, D]: g, u = x . dequant(W)^T, rounded to bf16; then, as the exact kernel
- * does in bf16 (Q36/kernels/expert_solo.py:56-62,106-115):
- *   sg = sigmoid(g) (MLX SigmoidX: y = 1/(1+e^|g|), g<0 ? y : 1-y), rounded;
- *   sl = bf16(g * sg); h = bf16(sl * u).
- * The sigmoid is evaluated in float64 from the bf16 g and rounded once. */
+ * e^x for 0 <= x (the sigmoid's exp(|g|)): the method of jo_exp_neg (Cody-Waite
+ * reduction with fdlibm's two-part ln2, degree-7 Taylor polynomial in Horner form
+ * with fused multiply-adds), scaled by 2^(n-1) then 2 so that n = 128 (x up to
+ * 88.72) stays finite; x > 89 (or NaN) gives x * inf.  The GPU's SwiGLU epilogue
+ * (qtile.hpp) executes the identical operation sequence, so both round the same
+ * fp32 value to bf16. */
+float jo_exp_pos(float x) {
+  if (!(x <= 89.0f)) return x * INFINITY;
+  const float t = x * 1.44269504088896341f;
+  const float n = rintf(t);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, 1.42860682030941723e-6f, r);
+  float p = 1.98412698412698413e-4f;
+  p = fmaf(p, r, 1.38888888888888889e-3f);
+  p = fmaf(p, r, 8.33333333333333333e-3f);
+  p = fmaf(p, r, 4.16666666666666667e-2f);
+  p = fmaf(p, r, 1.66666666666666667e-1f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int e = (int)n;
+  const uint32_t bits = (uint32_t)(e - 1 + 127) << 23;
+  float sc;
+  memcpy(&sc, &bits, 4);
+  return (p * sc) * 2.0f;
+}
+
+/* One pair p (sorted position) against expert e's fused gate||up stack
+ * [2I, D]: g, u = x . dequant(W)^T, rounded to bf16; then the exact kernel's
+ * bf16 chain (Q36/kernels/expert_solo.py:106-115): sg = SigmoidX(g), sl =
+ * bf16(g * sg), h = bf16(sl * u).  SigmoidX (MLX's Sigmoid on bf16,
+ * Q36/kernels/expert_solo.py:56-62: y = 1 / (1 + exp(|g|)), g < 0 ? y : 1 - y)
+ * evaluates each step in fp32 from bf16 operands and rounds it to bf16, as MLX's
+ * bf16 type does for bf16-with-integer arithmetic and its bf16 exp overload:
+ *   e = bf16(exp(|g|)); d = bf16(1 + e); y = bf16(1 / d); sg = g < 0 ? y : bf16(1 - y).
+ * exp is jo_exp_pos (Metal's exp bits are not reproducible here; the bf16
+ * rounding of e hides its last fp32 bits except within 2^-16 of a tie) and the
+ * division is the correctly rounded one. */
+static inline uint16_t sigmoid_bf16(uint16_t gt) {
+  const float ag = fabsf(bf2f(gt));
+  const float e = bf2f(f2bf(jo_exp_pos(ag)));
+  const float d = bf2f(f2bf(1.0f + e));
+  const float y = bf2f(f2bf(1.0f / d));
+  return bf2f(gt) < 0.0f ? f2bf(y) : f2bf(1.0f - y);
+}
+
 static inline uint16_t swiglu_bf16(uint16_t gt, uint16_t ut) {
-  const double g = (double)bf2f(gt);
-  const double y = 1.0 / (1.0 + exp(fabs(g)));
-  const uint16_t sg = f2bf((float)(g < 0 ? y : 1.0 - y));
+  const uint16_t sg = sigmoid_bf16(gt);
   const uint16_t sl = f2bf(bf2f(gt) * bf2f(sg));
   return f2bf(bf2f(sl) * bf2f(ut));
 }
 
+int jo_sigmoid_bf16_n(const uint16_t *g, int n, uint16_t *out) {
+  if (n < 0) return JO_EINVAL;
+  for (int i = 0; i < n; i++) out[i] = sigmoid_bf16(g[i]);
+  return JO_OK;
+}
 uint16_t jo_swiglu_bf16(uint16_t g, uint16_t u) { return swiglu_bf16(g, u); }
 
 /* h[p, :] for every sorted pair p; x [B, D] bf16; stacks [E, 2I, D/8] u32 and
@@ -512,10 +555,11 @@ int jo_kv_gather(const uint16_t *pool, int Hkv, int Dh, const int32_t *page_row,
  * the first lens[b] tokens: softmax(scale * q . K^T) . V, the result of
  * sdpa_decode / mx.fast.scaled_dot_product_attention with mask=None
  * (Q36/kernels/sdpa_decode.py:16-74,448-476; Q36/model/attention.py:70-74),
- * evaluated in float64 and rounded to bf16 once.  q [B, H, Dh], out [B, H, Dh]. */
+ * evaluated in float64 and rounded to bf16 once.  q [B, H, Dh], out [B, H, Dh];
+ * out64 (may be NULL) receives the float64 values before that rounding. */
 int jo_paged_decode_attn(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,
                          int max_pages, const int32_t *lens, int B, int H, int Hkv, int Dh, float scale,
-                         uint16_t *out) {
+                         uint16_t *out, double *out64) {
   if (B < 0 || H <= 0 || Hkv <= 0 || (H % Hkv) != 0 || Dh <= 0) return JO_EINVAL;
   for (int b = 0; b < B; b++)
     if (lens[b] < 1 || (lens[b] + JO_PAGE - 1) / JO_PAGE > max_pages) return JO_EINVAL;
@@ -549,8 +593,155 @@ int jo_paged_decode_attn(const uint16_t *q, const uint16_t *pool, const int32_t 
       }
       uint16_t *o = out + ((size_t)b * H + h) * Dh;
       for (int d = 0; d < Dh; d++) o[d] = f2bf((float)(acc[d] / den));
+      if (out64)
+        for (int d = 0; d < Dh; d++) out64[((size_t)b * H + h) * Dh + d] = acc[d] / den;
       free(sc);
       free(acc);
+    }
+  }
+  return JO_OK;
+}
+
+/* MLX's decode attention in its own fp32 arithmetic, the reference's "stock"
+ * numerics for one query over n keys (the error yardstick of the attention
+ * parity tests, as jo_qmv_mlx_f32 is for the projections).  Restated from the
+ * reference's transcriptions of MLX's kernels:
+ *  - one pass, sdpa_vector (Q36/kernels/sdpa_decode.py:16-74): q pre-scaled in
+ *    fp32; 32 simdgroups, simdgroup s taking keys s, s + 32, ...; per key the 32
+ *    lanes' 4-element partial dots are simd-summed; online softmax with
+ *    max = -FLT_MAX initially, factor = exp(max - new_max), o = o * factor +
+ *    exp_score * v; then the 32 simdgroups' (max, sum, o) merge by simd_max /
+ *    simd_sum of o * factor, o / sum, cast to bf16;
+ *  - two passes, sdpa_vector_2pass_1/_2 (:217-315): `blocks` strided key sets,
+ *    each pass-1 block runs the same online softmax and stores its unnormalised o
+ *    AS BF16 with fp32 (sum, max); pass 2 takes the max over blocks, sums
+ *    exp(m_b - max) * s_b, adds exp(m_b - max) * o_b over blocks j = lane + 32 i
+ *    per lane, simd-sums the 32 lanes and divides.
+ * Routing (:318-350) is that of the reference's M4 Pro ('s' architecture):
+ * two passes when n >= 1024 (or n >= 4096 with GQA), blocks = 64, or for n >
+ * 1024 with more than 4 q heads per kv head 128 / 256 / 512 / 1024 up to 8192 /
+ * 32768 / 65536 / beyond keys.  Unpinned here: Metal's fast::exp (exp2f(x *
+ * log2 e) in fp32 stands in) and simd_sum's order (an xor butterfly).
+ * out_f32 [B, H, Dh] receives the fp32 values before the final bf16 cast. */
+static float simd_sum32(float *v) {
+  float t[32];
+  memcpy(t, v, sizeof t);
+  for (int o = 16; o >= 1; o >>= 1) {
+    float nx[32];
+    for (int l = 0; l < 32; l++) nx[l] = t[l] + t[l ^ o];
+    memcpy(t, nx, sizeof t);
+  }
+  return t[0];
+}
+
+static inline float mlx_exp(float x) { return exp2f(x * 1.44269504088896341f); }
+
+static int mlx_blocks(int n, int gqa) {
+  int blocks = 64;
+  if (n > 1024 && gqa > 4) blocks = n <= 8192 ? 128 : n <= 32768 ? 256 : n <= 65536 ? 512 : 1024;
+  return blocks;
+}
+
+/* one online-softmax run over keys first, first + stride, ... < n of one (q head, kv head):
+ * returns (max, sum) and o[Dh] (fp32), the per-simdgroup loop of both kernels */
+static void mlx_run(const float *qs, const uint16_t *pool, const int32_t *prow, int Hkv, int Dh, int kvh, int first,
+                    int stride, int n, float *m_out, float *s_out, float *o) {
+  const int per = Dh / 32;
+  float max_score = -3.40282347e38f, sum = 0.0f;
+  for (int d = 0; d < Dh; d++) o[d] = 0.0f;
+  for (int t = first; t < n; t += stride) {
+    const int page = prow[t / JO_PAGE], slot = t % JO_PAGE;
+    float lane[32];
+    for (int l = 0; l < 32; l++) {
+      float sc = 0.0f;
+      for (int j = 0; j < per; j++)
+        sc += qs[l * per + j] * bf2f(pool[k_index(page, Hkv, Dh, kvh, slot, l * per + j)]);
+      lane[l] = sc;
+    }
+    const float score = simd_sum32(lane);
+    const float new_max = fmaxf(max_score, score);
+    const float factor = mlx_exp(max_score - new_max);
+    const float es = mlx_exp(score - new_max);
+    max_score = new_max;
+    sum = sum * factor + es;
+    for (int d = 0; d < Dh; d++) o[d] = o[d] * factor + es * bf2f(pool[v_index(page, Hkv, Dh, kvh, slot, d)]);
+  }
+  *m_out = max_score;
+  *s_out = sum;
+}
+
+int jo_sdpa_mlx_f32(const uint16_t *q, const uint16_t *pool, const int32_t *page_table, int max_pages,
+                    const int32_t *lens, int B, int H, int Hkv, int Dh, float scale, uint16_t *out,
+                    float *out_f32) {
+  if (B < 0 || H <= 0 || Hkv <= 0 || (H % Hkv) != 0 || Dh <= 0 || (Dh % 32) != 0) return JO_EINVAL;
+  for (int b = 0; b < B; b++)
+    if (lens[b] < 1 || (lens[b] + JO_PAGE - 1) / JO_PAGE > max_pages) return JO_EINVAL;
+  const int G = H / Hkv;
+#pragma omp parallel for schedule(dynamic, 1) collapse(2)
+  for (int b = 0; b < B; b++) {
+    for (int h = 0; h < H; h++) {
+      const int n = lens[b], kvh = h / G;
+      const int32_t *prow = page_table + (size_t)b * max_pages;
+      const uint16_t *qh = q + ((size_t)b * H + h) * Dh;
+      float *qs = (float *)malloc(sizeof(float) * (size_t)Dh);
+      float *res = (float *)malloc(sizeof(float) * (size_t)Dh);
+      for (int d = 0; d < Dh; d++) qs[d] = scale * bf2f(qh[d]);
+      const int two_pass = n >= 1024 || (Hkv < H && n >= 4096);
+      const int nb = two_pass ? mlx_blocks(n, G) : 32;
+      float *ms = (float *)malloc(sizeof(float) * (size_t)nb);
+      float *ss = (float *)malloc(sizeof(float) * (size_t)nb);
+      float *os = (float *)malloc(sizeof(float) * (size_t)nb * Dh);
+      for (int blk = 0; blk < nb; blk++) {
+        mlx_run(qs, pool, prow, Hkv, Dh, kvh, blk, nb, n, &ms[blk], &ss[blk], os + (size_t)blk * Dh);
+        if (two_pass)  /* pass 1 stores o as bf16 */
+          for (int d = 0; d < Dh; d++) os[(size_t)blk * Dh + d] = bf2f(f2bf(os[(size_t)blk * Dh + d]));
+      }
+      if (!two_pass) {  /* sdpa_vector's merge of its 32 simdgroups */
+        float new_max = ms[0];
+        for (int j = 1; j < 32; j++) new_max = fmaxf(new_max, ms[j]);
+        float v[32];
+        for (int j = 0; j < 32; j++) v[j] = ss[j] * mlx_exp(ms[j] - new_max);
+        const float total = simd_sum32(v);
+        for (int d = 0; d < Dh; d++) {
+          for (int j = 0; j < 32; j++) v[j] = os[(size_t)j * Dh + d] * mlx_exp(ms[j] - new_max);
+          const float od = simd_sum32(v);
+          res[d] = total == 0.0f ? od : od / total;
+        }
+      } else {  /* sdpa_vector_2pass_2: lane l holds blocks l, l + 32, ... */
+        float mx = -3.40282347e38f;
+        float lanev[32];
+        for (int l = 0; l < 32; l++) {
+          float m = -3.40282347e38f;
+          for (int i = 0; i < nb / 32; i++) m = fmaxf(m, ms[l + 32 * i]);
+          lanev[l] = m;
+        }
+        for (int l = 0; l < 32; l++) mx = fmaxf(mx, lanev[l]);
+        for (int l = 0; l < 32; l++) {
+          float acc = 0.0f;
+          for (int i = 0; i < nb / 32; i++) acc += mlx_exp(ms[l + 32 * i] - mx) * ss[l + 32 * i];
+          lanev[l] = acc;
+        }
+        const float total = simd_sum32(lanev);
+        for (int d = 0; d < Dh; d++) {
+          for (int l = 0; l < 32; l++) {
+            float acc = 0.0f;
+            for (int i = 0; i < nb / 32; i++)
+              acc += mlx_exp(ms[l + 32 * i] - mx) * os[(size_t)(l + 32 * i) * Dh + d];
+            lanev[l] = acc;
+          }
+          const float od = simd_sum32(lanev);
+          res[d] = total == 0.0f ? od : od / total;
+        }
+      }
+      for (int d = 0; d < Dh; d++) {
+        out[((size_t)b * H + h) * Dh + d] = f2bf(res[d]);
+        if (out_f32) out_f32[((size_t)b * H + h) * Dh + d] = res[d];
+      }
+      free(qs);
+      free(res);
+      free(ms);
+      free(ss);
+      free(os);
     }
   }
   return JO_OK;

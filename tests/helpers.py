@@ -20,8 +20,18 @@ def bf16_tensor(a: np.ndarray, device="cpu") -> torch.Tensor:
 
 
 def normal_bf16(shape, seed: int, scale: float = 1.0) -> np.ndarray:
+    """N(0, scale^2) values rounded to bf16 (drawn in float32: pools of 10^8 values stay quick)."""
     rng = np.random.default_rng(seed)
-    return f32_to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+    out = np.empty(shape, np.uint16)
+    flat = out.reshape(-1)
+    buf = np.empty(min(flat.size, 1 << 21), np.float32)  # drawn in chunks: large pools touch little fresh memory
+    for i in range(0, flat.size, buf.size):
+        b = buf[:min(buf.size, flat.size - i)]
+        rng.standard_normal(out=b, dtype=np.float32)
+        if scale != 1.0:
+            b *= np.float32(scale)
+        flat[i:i + b.size] = f32_to_bf16(b)
+    return out
 
 
 def stack_np(q: QLinear):
@@ -88,3 +98,52 @@ def assert_close_bf16(got_u16: np.ndarray, want_u16: np.ndarray, max_abs: float 
     assert worst <= 1.0, f"{what}: error {err:.3g} exceeds max({max_abs}, {ulps} ulp) (worst ratio {worst:.2f})"
     assert cos >= min_cos, f"{what}: cosine {cos:.6f} < {min_cos}"
     return {"max_abs": err, "cos": cos, "bit_equal": exact}
+
+
+def assert_attention_parity(got_u16: np.ndarray, exact: np.ndarray, stock_u16: np.ndarray | None = None,
+                            what: str = "", min_equal: float = 0.98, rel: float = 2.0**-14) -> dict:
+    """The attention bar, on outputs [S, ..., Dh] (S = sequences or token rows, each checked alone):
+
+    1. the reference's own criterion (FN/kernels/selfcheck.py:313-331), when `stock_u16` (the
+       reference's fp32 arithmetic, oracle.sdpa_mlx_f32) is given: per sequence,
+       max|got - exact| <= 8 max|stock - exact| + 4 * 2^-24 * max|exact|;
+    2. every element within one bf16 ulp of the exact (float64) value plus `rel` of its row's
+       largest |exact| (an fp32-accurate kernel's error is ~2^-18 of the row; one bf16-rounded P
+       alone moves elements by ~2^-9 of the row);
+    3. per sequence, at least `min_equal` of the elements equal the correctly rounded result
+       bf16(exact) bit for bit.
+    2 and 3 scale with each row's own magnitude, so they fail when a page is dropped or read from
+    the wrong place at any context length (tests/test_attention_bar.py plants those mistakes in the
+    oracle and checks that this bar rejects them)."""
+    g = bf16_to_f32(got_u16).astype(np.float64)
+    e = np.asarray(exact, np.float64)
+    assert g.shape == e.shape, (g.shape, e.shape)
+    assert np.all(np.isfinite(g)), f"{what}: non-finite outputs"
+    S = g.shape[0]
+    gs, es = g.reshape(S, -1, g.shape[-1]), e.reshape(S, -1, e.shape[-1])
+    cr = f32_to_bf16(es.astype(np.float32))
+    rowmax = np.abs(es).max(-1, keepdims=True)
+    bound = bf16_ulp(es) + rel * rowmax
+    ratio = np.abs(gs - es) / bound
+    worst = float(ratio.max()) if g.size else 0.0
+    if worst > 1.0:
+        s, r, d = np.unravel_index(int(ratio.argmax()), ratio.shape)
+        raise AssertionError(f"{what}: sequence {s} row {r} dim {d}: {gs[s, r, d]:.6g} against exact "
+                             f"{es[s, r, d]:.6g} (bound {bound[s, r, d]:.3g}, worst ratio {worst:.2f})")
+    eq = np.mean(f32_to_bf16(gs.astype(np.float32)) == cr, axis=(1, 2)) if g.size else np.ones(S)
+    low = int(eq.argmin()) if S else 0
+    assert S == 0 or eq.min() >= min_equal, (
+        f"{what}: sequence {low}: {eq[low]:.4f} of the outputs equal the correctly rounded result "
+        f"(floor {min_equal})")
+    out = {"worst_ratio": worst, "min_equal": float(eq.min()) if S else 1.0, "mean_equal": float(eq.mean()) if S else 1.0}
+    if stock_u16 is not None:
+        st = bf16_to_f32(stock_u16).astype(np.float64).reshape(gs.shape)
+        e_got = np.abs(gs - es).reshape(S, -1).max(1)
+        e_stock = np.abs(st - es).reshape(S, -1).max(1)
+        scale = np.abs(es).reshape(S, -1).max(1)
+        lim = 8 * e_stock + 4 * 2.0**-24 * scale
+        bad = np.flatnonzero(e_got > lim)
+        assert bad.size == 0, (f"{what}: sequence {bad[0]}: error {e_got[bad[0]]:.3g} exceeds 8x the reference "
+                               f"arithmetic's {e_stock[bad[0]]:.3g}")
+        out["err_vs_stock"] = float((e_got / np.maximum(e_stock, 1e-300)).max())
+    return out

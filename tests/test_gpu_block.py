@@ -91,6 +91,66 @@ def _ctx(lens, cfg, seed):
     return table, pools
 
 
+def _layer_vs_oracle(cfg, lens, table, pool, x, w, what, max_flips):
+    """One layer step on the GPU against oracle.decoder_layer on the same inputs, stage by stage
+    (the MoE half under the GPU's routing, which is bit-exact given the logits); rows whose float64
+    routing differs are counted.  The layer output composes ~6 bf16 rounding stages (attention,
+    o_proj, residual, experts, combine, residual): up to 4 ulps where that exceeds the absolute 2e-2."""
+    layer = DecoderLayer(cfg, w)
+    pool_t = bf16_tensor(pool, DEV)
+    st = make_step_state(cfg, np.array(lens), _i32(table))
+    dbg = {}
+    y = layer.step(bf16_tensor(x, DEV), pool_t, st, debug=dbg)
+    ref_pool = pool.copy()
+    ocfg = {"heads": cfg.heads, "kv_heads": cfg.kv_heads, "experts": cfg.experts, "top_k": cfg.top_k,
+            "eps": cfg.eps, "inv_freq": rope_inv_freq(cfg.rope_theta, 128)}
+    gi = dbg["inds"].cpu().numpy().view(np.uint32)
+    gs = u16(dbg["scores"])
+    ref = oracle.decoder_layer(x, _layer_numpy(w), ref_pool, table, np.array(lens, np.int32), ocfg, routing=(gi, gs))
+    for name in ("xn", "qkv", "q", "attn", "o", "h", "hn"):
+        assert_close_bf16(u16(dbg[name]).reshape(ref[name].shape), ref[name], what=f"{what}: {name}")
+    own = oracle.router_topk(ref["logits"], cfg.top_k, True)[0]
+    flips = int(np.sum(np.any(np.sort(own, -1) != np.sort(gi, -1), -1)))
+    assert flips <= max_flips, f"{what}: {flips} rows routed differently from the float64 logits"
+    assert_close_bf16(u16(y), ref["y"], what=f"{what}: layer output", ulps=4.0)
+    return dbg, ref
+
+
+def test_decoder_layer_config0():
+    """BASELINE configs[0] on the GPU: one Qwen3-MoE-style block (128 experts, top-8) at batch 1,
+    decoding at position 4,096 over a 4,096-token context in pages 0..255 in order (the new key
+    goes to page 256), against the oracle's block."""
+    cfg = MoEConfig(layers=1)
+    L = 4096
+    table = np.arange(L // 16 + 1, dtype=np.int32)[None]
+    pool = normal_bf16((L // 16 + 1, cfg.kv_heads, 2, 2048), seed=0x4A450000 + 1)
+    x = normal_bf16((1, cfg.hidden), seed=0x4A450000 + 2)
+    w = random_layer_weights(cfg, seed=0x4A450000 % 100000, device=DEV)
+    dbg, ref = _layer_vs_oracle(cfg, [L], table, pool, x, w, "config 0", max_flips=1)
+    assert int(torch.unique(dbg["inds"]).numel()) == 8
+
+
+def test_decoder_layer_config2_rows():
+    """BASELINE configs[2]'s step on one layer at full geometry: the bench's 32 ragged rows (lengths
+    log-uniform in [128, 32768], pages a random permutation) through a 128-expert block -- the
+    decode expert GEMVs in their real regime (~2 rows per distinct expert) -- against the oracle."""
+    cfg = MoEConfig(layers=1)
+    rng = np.random.default_rng(0x4A450000 + 16 * 2)
+    lens = np.round(np.exp(rng.uniform(np.log(128), np.log(32768), 32))).astype(np.int32)
+    npg = (lens + 1 + 15) // 16
+    perm = rng.permutation(int(npg.sum()))
+    table = np.zeros((32, int(npg.max())), np.int32)
+    at = 0
+    for b in range(32):
+        table[b, :npg[b]] = perm[at:at + npg[b]]
+        at += npg[b]
+    pool = normal_bf16((int(npg.sum()), cfg.kv_heads, 2, 2048), seed=0x4A450000 + 33)
+    x = normal_bf16((32, cfg.hidden), seed=0x4A450000 + 34)
+    w = random_layer_weights(cfg, seed=0x4A450000 % 100000 + 2, device=DEV)
+    dbg, ref = _layer_vs_oracle(cfg, list(lens), table, pool, x, w, "config 2 rows", max_flips=3)
+    assert int(torch.unique(dbg["inds"]).numel()) > 90  # the regime: most experts hit by 1-3 rows
+
+
 def test_decoder_layer_parity():
     """One layer, 12 ragged rows: every stage checked against the oracle's layer; the MoE half
     is compared under the GPU's routing (routing is bit-exact given the router logits, and the

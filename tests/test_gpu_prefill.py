@@ -3,7 +3,10 @@
 The oracle states the causal mask as what it is: chunk token t at position ctx + t attends the
 first ctx + t + 1 keys of its sequence, i.e. the float64 decode attention of that token over
 ctx + t + 1 keys (oracle.paged_prefill_attn).  The bar is the north-star float tolerance; the
-invariants below are bit-exact."""
+invariants below are bit-exact.  The float bar is tests.helpers.assert_attention_parity without its
+stock criterion (MLX's full-attention kernel is not restated): every element within one bf16 ulp +
+2^-14 of its row of the float64 result and >= 98% of each row's outputs correctly rounded, which a
+dropped or misplaced page fails (tests/test_attention_bar.py); plus the north star's tolerance."""
 
 from __future__ import annotations
 
@@ -13,7 +16,7 @@ import torch
 
 import oracle
 from jitengine_amd import ops
-from tests.helpers import assert_close_bf16, bf16_tensor, bf16_to_f32, normal_bf16, u16
+from tests.helpers import assert_attention_parity, assert_close_bf16, bf16_tensor, bf16_to_f32, normal_bf16, u16
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -52,7 +55,8 @@ def test_prefill_attention_parity(H, Hkv):
     T = sum(n for *_, n in chunks)
     q = normal_bf16((T, H, 128), seed=5)
     got = _run(q, pool, table, chunks, H, Hkv)
-    want = oracle.paged_prefill_attn(q, pool, table, chunks, SCALE)
+    want, exact = oracle.paged_prefill_attn(q, pool, table, chunks, SCALE, exact=True)
+    assert_attention_parity(got, exact, what=f"prefill H={H} Hkv={Hkv}")
     assert_close_bf16(got, want, what=f"prefill H={H} Hkv={Hkv}")
 
 
@@ -77,9 +81,11 @@ def test_prefill_one_token_matches_decode_attention():
     plan = ops.attn_plan([1800], DEV)
     dec = u16(ops.paged_decode_attention(bf16_tensor(q, DEV), bf16_tensor(pool, DEV),
                                          torch.from_numpy(table).to(DEV), plan, SCALE))
-    want = oracle.paged_decode_attn(q, pool, table, [1800], SCALE)
+    want, exact = oracle.paged_decode_attn(q, pool, table, [1800], SCALE, exact=True)
+    assert_attention_parity(pre, exact, what="prefill one token")
+    assert_attention_parity(dec, exact, what="decode one token")
     assert_close_bf16(pre, want, what="prefill one token")
-    assert_close_bf16(pre, dec, what="prefill vs decode")
+    assert np.mean(pre == dec) >= 0.98
 
 
 def test_prefill_page_permutation_and_stale_slots():
@@ -113,7 +119,8 @@ def test_prefill_config3_chunks():
     got = _run(q, pool, table, chunks)
     sel = np.r_[0:40, 500:560, 1024:1030, 2000:2048]  # rows across every chunk (the oracle is O(T.L))
     lens = np.array([int(ctx[r // 512]) + r % 512 + 1 for r in sel], np.int32)
-    want = oracle.paged_decode_attn(q[sel], pool, table[sel // 512], lens, SCALE)
+    want, exact = oracle.paged_decode_attn(q[sel], pool, table[sel // 512], lens, SCALE, exact=True)
+    assert_attention_parity(got[sel], exact, what="config 3 prefill")
     assert_close_bf16(got[sel], want, what="config 3 prefill")
 
 
@@ -139,9 +146,12 @@ def test_mixed_prefill_decode_layer_stages():
     torch.cuda.synchronize()
     assert layer.moe.use_seg(T * cfg.top_k, prefill=True)
     q, attn, pool_after = u16(dbg["q"]), u16(dbg["attn"]), u16(pt)
-    want_pre = oracle.paged_prefill_attn(q[:ms.P], pool_after, table[:3], chunks, SCALE)
+    want_pre, ex_pre = oracle.paged_prefill_attn(q[:ms.P], pool_after, table[:3], chunks, SCALE, exact=True)
+    assert_attention_parity(attn[:ms.P], ex_pre, what="mixed step prefill rows")
     assert_close_bf16(attn[:ms.P], want_pre, what="mixed step prefill rows")
-    want_dec = oracle.paged_decode_attn(q[ms.P:], pool_after, table[3:], np.array(dec_pos) + 1, SCALE)
+    want_dec, ex_dec = oracle.paged_decode_attn(q[ms.P:], pool_after, table[3:], np.array(dec_pos) + 1, SCALE,
+                                                exact=True)
+    assert_attention_parity(attn[ms.P:], ex_dec, what="mixed step decode rows")
     assert_close_bf16(attn[ms.P:], want_dec, what="mixed step decode rows")
 
     def host_q(lin):

@@ -40,6 +40,54 @@ def test_exp_neg_close_to_exp():
     assert oracle.exp_neg(-64.0) == 0.0 and oracle.exp_neg(-1e9) == 0.0
 
 
+def test_exp_pos_close_to_exp():
+    xs = np.concatenate([np.linspace(0.0, 88.72, 40001), np.geomspace(1e-8, 88.0, 4000)]).astype(np.float32)
+    worst = max(abs(oracle.exp_pos(float(x)) - math.exp(float(x))) / math.exp(float(x)) for x in xs)
+    assert worst < 4 * 2.0**-24, worst  # within 2 ulp of e^x
+    assert oracle.exp_pos(0.0) == 1.0
+    assert math.isinf(oracle.exp_pos(89.5)) and math.isinf(oracle.exp_pos(1e30))
+    assert math.isnan(oracle.exp_pos(float("nan")))
+
+
+def test_sigmoid_steps_exhaustive():
+    """SigmoidX's bf16 steps (Q36/kernels/expert_solo.py:56-62) over every finite bf16 g, against an
+    independent numpy restatement with float64 exp: e = bf16(exp|g|), d = bf16(1 + e),
+    y = bf16(1 / d), g < 0 ? y : bf16(1 - y).  (The oracle's own exp and numpy's differ in the last
+    fp32 bits; rounded to bf16 they give the same e on every input here.)  The steps matter: a
+    single rounding of the float64 sigmoid differs on over a thousand inputs."""
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    gf = bf16_to_f32(g)
+    g, gf = g[np.isfinite(gf)], gf[np.isfinite(gf)]
+    got = oracle.sigmoid_bf16(g)
+    a = np.abs(gf).astype(np.float64)
+    with np.errstate(over="ignore", divide="ignore"):
+        e = f32_to_bf16(np.exp(a).astype(np.float32))
+        d = f32_to_bf16(np.float32(1) + bf16_to_f32(e))
+        y = f32_to_bf16(np.float32(1) / bf16_to_f32(d))
+    want = np.where(gf < 0, y, f32_to_bf16(np.float32(1) - bf16_to_f32(y)))
+    assert np.array_equal(got, want)
+    with np.errstate(over="ignore"):
+        yy = 1.0 / (1.0 + np.exp(a))
+    single = f32_to_bf16(np.where(gf < 0, yy, 1.0 - yy).astype(np.float32))
+    assert np.sum(single != got) > 1000
+    # known answers: sigma(0) = 0.5, sigma(+-inf-like) saturates
+    h = f32_to_bf16(np.array([0.0, 100.0, -100.0, 1.0], np.float32))
+    assert list(bf16_to_f32(oracle.sigmoid_bf16(h))[:3]) == [0.5, 1.0, 0.0]
+
+
+def test_bf16_reciprocals_are_far_from_bf16_ties():
+    """Why the GPU's SigmoidX may take the 1-ulp hardware reciprocal of d = bf16(1 + e): for every
+    bf16 significand m, 1 / (m / 128) lies at least 192 fp32 ulps from the nearest bf16 rounding tie,
+    so any reciprocal within a few ulps rounds to the bf16 of the correctly rounded division."""
+    from fractions import Fraction
+
+    worst = min(
+        abs(Fraction(128, m) * 1024 - (2 * round((Fraction(128, m) * 1024 - 1) / 2) + 1)) * 2**14
+        for m in range(129, 256)
+    )
+    assert worst > 192, float(worst)
+
+
 # ----------------------------------------------------------------------------- router
 @pytest.mark.parametrize("N", [32, 128, 256, 1024])
 def test_softmax_within_one_ulp_of_float64(N):
@@ -311,6 +359,37 @@ def test_attention_page_permutation_invariance():
     pool2[perm] = pool
     b = oracle.paged_decode_attn(q, pool2, perm[table].astype(np.int32), lens, 0.088)
     assert np.array_equal(a, b)
+
+
+def test_attention_float64_output_rounds_to_the_bf16_output():
+    lens = [3, 900]
+    q, pool, table = _pool_case(lens, seed=12)
+    out, out64 = oracle.paged_decode_attn(q, pool, table, lens, 0.088, exact=True)
+    assert np.array_equal(f32_to_bf16(out64.astype(np.float32)), out)
+
+
+def test_sdpa_mlx_f32_pins():
+    """The reference's stock arithmetic (an error yardstick only): fp32-accurate in the one-pass
+    form (n < 1024), bf16 partials visible in the two-pass form (n >= 1024 on the M4 Pro), one key
+    gives its value, pages may move and rows may be batched without changing a bit."""
+    lens = [1, 300, 1023, 1024, 5000, 40000]
+    q, pool, table = _pool_case(lens, seed=13)
+    st, f32 = oracle.sdpa_mlx_f32(q, pool, table, lens, 128 ** -0.5)
+    assert np.array_equal(f32_to_bf16(f32), st)
+    _, ex = oracle.paged_decode_attn(q, pool, table, lens, 128 ** -0.5, exact=True)
+    rel = np.abs(f32 - ex).max(-1) / np.abs(ex).max(-1)  # [B, H]
+    assert rel[:3].max() < 2.0**-19, rel[:3].max()       # one pass: fp32 error
+    assert rel[3:].max() < 2.0**-8, rel[3:].max()        # two passes: bf16 partials...
+    assert rel[3:].max(-1).min() > 2.0**-16              # ...visibly above fp32 error in every row
+    kc, vc = oracle.kv_gather(pool, table[0], 1, 4, 128)
+    assert np.array_equal(st[0].reshape(4, 8, 128), np.repeat(vc[:, :1], 8, 1))
+    perm = np.random.default_rng(14).permutation(pool.shape[0])
+    pool2 = np.empty_like(pool)
+    pool2[perm] = pool
+    st2, _ = oracle.sdpa_mlx_f32(q, pool2, perm[table].astype(np.int32), lens, 128 ** -0.5)
+    assert np.array_equal(st2, st)
+    solo, _ = oracle.sdpa_mlx_f32(q[4:5], pool, table[4:5], lens[4:5], 128 ** -0.5)
+    assert np.array_equal(solo[0], st[4])
 
 
 # ----------------------------------------------------------------------------- packed layout
