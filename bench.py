@@ -588,6 +588,88 @@ def copy_calibration(dev: str) -> int:
     return 0
 
 
+def probe(dev: str, parts=("read", "launch", "barrier")) -> int:
+    """The yardsticks the kernels are rated against, measured on this GPU (csrc/probe.hip):
+    the HBM streaming-read ceiling (4 GiB read whole, grid-stride or one contiguous run per
+    workgroup, plain or nontemporal loads; and 196 MB reads, one launch each, rotating through 48
+    distinct windows as the expert kernels' layers do), the device time of an empty launch inside
+    a HIP graph, and the cost of a grid-wide barrier inside one cooperative launch."""
+    import ctypes
+
+    from jitengine_amd import build as hip_build
+
+    lib = ctypes.CDLL(hip_build.PROBE_LIB)
+    P, I, LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
+    lib.probe_read.argtypes = [P, LL, I, I, P, P]
+    lib.probe_empty.argtypes = [P]
+    lib.probe_barrier.argtypes = [I, I, I, P, P, I, P, P]
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(reps):
+            fn()
+        e.record(stream)
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps  # ms
+
+    out = {"read": {}, "launch": {}, "barrier": {}}
+    if "read" in parts:
+        big = 4 << 30
+        buf = torch.empty(big // 4, dtype=torch.int32, device=dev).random_()
+        sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+        names = {0: "grid_stride", 1: "grid_stride_nt", 2: "contiguous_runs", 3: "contiguous_runs_nt"}
+        for mode in range(4):
+            for blocks in (1024, 4096, 16384):
+                ms = timed(lambda: lib.probe_read(ctypes.c_void_p(buf.data_ptr()), big, mode, blocks,
+                                                  ctypes.c_void_p(sink.data_ptr()), sp), 5)
+                out["read"][f"{names[mode]}_{blocks}wg_4GiB"] = round(big / (ms * 1e-3) / 1e9, 1)
+        win = 196 * 1000 * 1000 // 16 * 16
+        n_win = min(48, big // win)
+        for mode in (2, 3):
+            def rot(mode=mode):
+                for w in range(n_win):
+                    lib.probe_read(ctypes.c_void_p(buf.data_ptr() + w * win), win, mode, 5376,
+                                   ctypes.c_void_p(sink.data_ptr()), sp)
+            ms = timed(rot, 3)
+            out["read"][f"{names[mode]}_5376wg_196MB_per_launch"] = round(n_win * win / (ms * 1e-3) / 1e9, 1)
+        del buf
+        torch.cuda.empty_cache()
+
+    if "launch" in parts:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(48):
+                lib.probe_empty(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        ms = timed(g.replay, 20)
+        out["launch"]["empty_in_graph_us"] = round(ms * 1e3 / 48, 3)
+        del g
+
+    if "barrier" in parts:
+        cnt = torch.zeros(1, dtype=torch.int32, device=dev)
+        status = torch.zeros(2, dtype=torch.int32, device=dev)
+        max_blocks = int(lib.probe_barrier_max_blocks())
+        for blocks in sorted({256, min(512, max_blocks)}):
+            data = torch.zeros(blocks * 1024, dtype=torch.int32, device=dev)
+            for words in (0, 1024):
+                res = {}
+                for phases in (0, 64):
+                    def run(phases=phases, words=words, blocks=blocks, data=data):
+                        cnt.zero_()
+                        lib.probe_barrier(blocks, phases, words, ctypes.c_void_p(cnt.data_ptr()),
+                                          ctypes.c_void_p(data.data_ptr()), 1 << 22,
+                                          ctypes.c_void_p(status.data_ptr()), sp)
+                    res[phases] = timed(run, 10)
+                out["barrier"][f"{blocks}wg_{words * 4}B_per_wg_us"] = round((res[64] - res[0]) * 1e3 / 64, 3)
+        out["barrier"]["timeouts"] = int(status[0])
+    print(json.dumps({"probe": out}), flush=True)
+    return 0
+
+
 OP_KERNELS = {  # the kernels one op launches (rocprofv3 kernel names contain these)
     "paged_attention": ["paged_attn_kernel", "attn_merge_kernel"],
     "gate_up_swiglu": ["qmm_kernel<1, 8, true, true"],
@@ -733,6 +815,10 @@ def main() -> int:
     ap.add_argument("--no-bs1", action="store_true",
                     help="config 2 only: skip the bs=1 (config 4) measurement reported beside it")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--probe", action="store_true",
+                    help="measure the streaming-read ceiling, the empty-launch floor and the grid-barrier cost")
+    ap.add_argument("--probe-parts", default="read,launch,barrier",
+                    help="which probe measurements to run (the barrier's cooperative launch ends rocprofv3 badly)")
     ap.add_argument("--rocprof-summary", metavar="DIR",
                     help="summarise rocprofv3 CSV output under DIR (kt/, fetch/, write/, cfetch/, cwrite/)")
     ap.add_argument("--op", default="paged_attention", choices=sorted(OP_KERNELS) + ["step"])
@@ -750,6 +836,8 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.copy_calibration:
         return copy_calibration(dev)
+    if args.probe:
+        return probe(dev, set(args.probe_parts.split(",")))
     if args.config == 1:
         res = bench_config1(args.steps, args.warmup, dev)
     elif args.config in (2, 4):

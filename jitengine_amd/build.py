@@ -23,6 +23,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(OUT_DIR, "libjit_moe.so")
+PROBE_LIB = os.path.join(OUT_DIR, "libjit_probe.so")  # bench.py's measurement kernels (csrc/probe.hip)
 ARCH = "gfx950"
 
 SOURCES = {
@@ -76,7 +77,20 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     for o in objs:
         os.remove(o)
+    _build_probe(verbose)
     return LIB
+
+
+def _build_probe(verbose: bool) -> None:
+    """The benchmark's measurement kernels, a library of their own (never loaded by the package)."""
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [hipcc(), "-x", "hip", *_COMMON, "-shared", os.path.join(CSRC, "probe.hip"), "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on probe.hip:\n{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
 
 
 if __name__ == "__main__":

@@ -140,7 +140,7 @@ __device__ __forceinline__ void load_k2(Frag8 (&k)[2][4], const uint16_t *pool, 
   for (int t = 0; t < 2; t++) {
     const uint16_t *kp = head_part(pool, t ? pg1 : pg0, Hkv, kvh);
 #pragma unroll
-    for (int cc = 0; cc < 4; cc++) k[t][cc].q = *(const uint4 *)(kp + cc * (kPage * 32) + lr * 32 + 8 * lg);
+    for (int cc = 0; cc < 4; cc++) k[t][cc].q = ld_stream16(kp + cc * (kPage * 32) + lr * 32 + 8 * lg);
   }
 }
 
@@ -152,7 +152,7 @@ __device__ __forceinline__ void load_v2(uint2 (&v)[2][8], const uint16_t *pool, 
   for (int t = 0; t < 2; t++) {
     const uint16_t *vp = head_part(pool, t ? pg1 : pg0, Hkv, kvh) + kPageHead;
 #pragma unroll
-    for (int cc = 0; cc < 8; cc++) v[t][cc] = *(const uint2 *)(vp + (16 * cc + lr) * kPage + 4 * lg);
+    for (int cc = 0; cc < 8; cc++) v[t][cc] = ld_stream8(vp + (16 * cc + lr) * kPage + 4 * lg);
   }
 }
 

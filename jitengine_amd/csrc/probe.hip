@@ -1,0 +1,133 @@
+// Measurement kernels of the benchmark (not part of the hot path's C-ABI): the HBM
+// streaming-read ceiling the hot-path kernels are rated against, the device cost of an empty
+// launch inside a HIP graph, and the cost of a grid-wide barrier between the phases of one
+// persistent launch (the alternative to a launch per phase).  Built into their own library,
+// libjit_probe.so, which only bench.py loads.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int MODE>
+__device__ __forceinline__ u32x4 load16(const u32x4 *p) {
+  return (MODE & 1) ? __builtin_nontemporal_load(p) : *p;
+}
+
+// Streaming read of n16 16-byte words.  mode bit 0: nontemporal loads; bit 1: each workgroup
+// reads one contiguous run of the buffer (the access shape of the expert and attention kernels)
+// instead of grid-stride passes over the whole buffer.  Four loads per thread are in flight per
+// iteration; the XOR of everything read goes to sink[blockIdx.x] so no load is dead.
+template <int MODE>
+__global__ __launch_bounds__(256) void probe_read_kernel(const u32x4 *__restrict__ p, long long n16,
+                                                          uint32_t *__restrict__ sink) {
+  uint32_t acc = 0;
+  long long begin, end, stride;
+  if (MODE & 2) {
+    const long long per = (n16 + gridDim.x - 1) / gridDim.x;
+    begin = (long long)blockIdx.x * per + threadIdx.x;
+    end = min(n16, (long long)(blockIdx.x + 1) * per);
+    stride = 256;
+  } else {
+    begin = (long long)blockIdx.x * 256 + threadIdx.x;
+    end = n16;
+    stride = (long long)gridDim.x * 256;
+  }
+  long long i = begin;
+  for (; i + 3 * stride < end; i += 4 * stride) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = load16<MODE>(p + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (; i < end; i += stride) {
+    const u32x4 v = load16<MODE>(p + i);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  for (int o = 32; o >= 1; o >>= 1) acc ^= __shfl_xor(acc, o, 64);
+  __shared__ uint32_t red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
+__global__ void probe_empty_kernel() {}
+
+// `phases` grid-wide barriers in one launch.  Every workgroup must be resident at once (the
+// host launches it cooperatively).  Per phase each workgroup writes `words` 32-bit words of its
+// own slot of `data` and, after the barrier, reads its neighbour's slot (so the release/acquire
+// moves real data between XCDs).  Thread 0 arrives on `counter` (device-scope atomic add after
+// a release fence) and waits, sleeping between polls, until every workgroup of the phase has
+// arrived; a wait longer than spin_limit polls gives up, counts itself in status[0] and leaves
+// the kernel, so every wave ends whatever happens.
+__global__ __launch_bounds__(256) void probe_barrier_kernel(int phases, int words, uint32_t *counter,
+                                                            uint32_t *data, int spin_limit, int *status) {
+  const int nb = gridDim.x, b = blockIdx.x, t = threadIdx.x;
+  __shared__ int give_up;
+  uint32_t acc = 0;
+  for (int ph = 0; ph < phases; ph++) {
+    for (int w = t; w < words; w += 256) data[(long long)b * words + w] = (uint32_t)(ph * 131 + b + w);
+    __syncthreads();
+    if (t == 0) {
+      __atomic_thread_fence(__ATOMIC_RELEASE);
+      __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t target = (uint32_t)(ph + 1) * (uint32_t)nb;
+      int spins = 0;
+      while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > spin_limit) break;
+      }
+      __atomic_thread_fence(__ATOMIC_ACQUIRE);
+      give_up = spins > spin_limit;
+    }
+    __syncthreads();
+    if (give_up) {
+      if (t == 0) atomicAdd(status, 1);
+      return;
+    }
+    const int nbr = (b + 1) % nb;
+    for (int w = t; w < words; w += 256) acc ^= data[(long long)nbr * words + w];
+  }
+  if (acc == 0x9e3779b9u) status[1] = 1;  // keeps the reads alive
+}
+
+}  // namespace
+
+extern "C" int probe_read(const void *p, long long bytes, int mode, int blocks, uint32_t *sink, void *stream) {
+  if (!p || !sink || bytes < 16 || blocks <= 0 || mode < 0 || mode > 3) return -1;
+  const long long n16 = bytes / 16;
+  hipStream_t st = (hipStream_t)stream;
+  switch (mode) {
+    case 0: probe_read_kernel<0><<<blocks, 256, 0, st>>>((const u32x4 *)p, n16, sink); break;
+    case 1: probe_read_kernel<1><<<blocks, 256, 0, st>>>((const u32x4 *)p, n16, sink); break;
+    case 2: probe_read_kernel<2><<<blocks, 256, 0, st>>>((const u32x4 *)p, n16, sink); break;
+    default: probe_read_kernel<3><<<blocks, 256, 0, st>>>((const u32x4 *)p, n16, sink); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int probe_empty(void *stream) {
+  probe_empty_kernel<<<1, 64, 0, (hipStream_t)stream>>>();
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+// The largest grid of probe_barrier_kernel that is resident at once (cooperative launch limit).
+extern "C" int probe_barrier_max_blocks(void) {
+  int dev = 0, per_cu = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -3;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, probe_barrier_kernel, 256, 0) != hipSuccess) return -3;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -3;
+  return per_cu * cus;
+}
+
+extern "C" int probe_barrier(int blocks, int phases, int words, uint32_t *counter, uint32_t *data, int spin_limit,
+                             int *status, void *stream) {
+  const int cap = probe_barrier_max_blocks();
+  if (blocks <= 0 || blocks > cap || phases < 0 || words < 0 || !counter || !data || !status) return -1;
+  void *args[] = {&phases, &words, &counter, &data, &spin_limit, &status};
+  const hipError_t e = hipLaunchCooperativeKernel((const void *)probe_barrier_kernel, dim3(blocks), dim3(256), args,
+                                                  0, (hipStream_t)stream);
+  return e == hipSuccess ? 0 : -3;
+}

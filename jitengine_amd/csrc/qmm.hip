@@ -102,11 +102,11 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
       const uint8_t *blk = (const uint8_t *)a.w + (long long)e * a.w_estride + (long long)(rowb >> 4) * GP * kTileBytes;
       const uint8_t *nb = blk + (g0 >> 1) * kNibbleBytes;
       // lane group lg fetches pair min(lg, GPW/2 - 1) (lanes past the slice re-read its last pair)
-      const uint2 sbl = *(const uint2 *)(blk + (long long)GP * kNibbleBytes +
-                                         ((g0 >> 1) + min(lg, GPW / 2 - 1)) * kScaleBytes + 8 * lr);
+      const uint2 sbl = ld_stream8(blk + (long long)GP * kNibbleBytes +
+                                   ((g0 >> 1) + min(lg, GPW / 2 - 1)) * kScaleBytes + 8 * lr);
 #pragma unroll
       for (int j = 0; j < GPW / 2; j++) {
-        const uint4 q = *(const uint4 *)(nb + j * kNibbleBytes + 16 * l);
+        const uint4 q = ld_stream16(nb + j * kNibbleBytes + 16 * l);
         wv[2 * j][rb] = make_uint2(q.x, q.y);
         wv[2 * j + 1][rb] = make_uint2(q.z, q.w);
       }
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
       const uint16_t *bp = a.b + e * a.g_estride + row * G + g0;
 #pragma unroll
       for (int g = 0; g < GPW; g++) {
-        const uint2 wm = *(const uint2 *)(wp + 8 * g);
+        const uint2 wm = ld_stream8(wp + 8 * g);
         wv[g][rb] = make_uint2(nibbles_natural(wm.x), nibbles_natural(wm.y));
       }
 #pragma unroll
