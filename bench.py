@@ -602,6 +602,7 @@ def probe(dev: str, parts=("read", "launch", "barrier")) -> int:
     P, I, LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
     lib.probe_read.argtypes = [P, LL, I, I, P, P]
     lib.probe_empty.argtypes = [P]
+    lib.probe_paged.argtypes = [P, P, I, I, I, P, P]
     lib.probe_barrier.argtypes = [I, I, I, P, P, I, P, P]
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
@@ -637,7 +638,15 @@ def probe(dev: str, parts=("read", "launch", "barrier")) -> int:
                                    ctypes.c_void_p(sink.data_ptr()), sp)
             ms = timed(rot, 3)
             out["read"][f"{names[mode]}_5376wg_196MB_per_launch"] = round(n_win * win / (ms * 1e-3) / 1e9, 1)
-        del buf
+        # the attention access shape: 8 KB blocks at random pages, 2048 waves of 64-block runs
+        nblk = big // 8192
+        waves, run = 2048, 64
+        perm = torch.randperm(nblk, device=dev)[:waves * run].to(torch.int32).contiguous()
+        for mode, name in ((0, "paged_8KB_blocks_16B_loads"), (1, "paged_8KB_blocks_attention_loads")):
+            ms = timed(lambda: lib.probe_paged(ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(perm.data_ptr()),
+                                               waves, run, mode, ctypes.c_void_p(sink.data_ptr()), sp), 5)
+            out["read"][f"{name}_2048waves"] = round(waves * run * 8192 / (ms * 1e-3) / 1e9, 1)
+        del buf, perm
         torch.cuda.empty_cache()
 
     if "launch" in parts:

@@ -53,6 +53,45 @@ __global__ __launch_bounds__(256) void probe_read_kernel(const u32x4 *__restrict
   if (threadIdx.x == 0) sink[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
 
+// The decode-attention access shape without its arithmetic: wave w of the grid reads `run` 8 KB
+// blocks (a kv head's K and V of one 16-token page), the blocks at pages[w * run ..] of a
+// random permutation, two blocks per step with all their 16-byte nontemporal loads issued
+// together (MODE 0), or 1 KB of each K part and 512 B pieces of each V part as the kernel's
+// fragments do (MODE 1: 8-byte loads for V).
+template <int MODE>
+__global__ __launch_bounds__(256) void probe_paged_kernel(const u32x4 *__restrict__ p, const int *__restrict__ pages,
+                                                           int run, uint32_t *__restrict__ sink) {
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  uint32_t acc = 0;
+  for (int i = 0; i < run; i += 2) {
+    const u32x4 *b0 = p + (long long)pages[w * run + i] * 512;
+    const u32x4 *b1 = p + (long long)pages[w * run + min(i + 1, run - 1)] * 512;
+    u32x4 v[16];
+    if (MODE == 0) {
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = load16<1>(b0 + 64 * u + l);
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[8 + u] = load16<1>(b1 + 64 * u + l);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; u++) v[u] = load16<1>(b0 + 64 * u + l);
+#pragma unroll
+      for (int u = 0; u < 4; u++) v[4 + u] = load16<1>(b1 + 64 * u + l);
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const u32x2 a = __builtin_nontemporal_load((const u32x2 *)(b0 + 256) + 64 * u + l);
+        const u32x2 c = __builtin_nontemporal_load((const u32x2 *)(b1 + 256) + 64 * u + l);
+        v[8 + u] = u32x4{a.x, a.y, c.x, c.y};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 16; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (int o = 32; o >= 1; o >>= 1) acc ^= __shfl_xor(acc, o, 64);
+  if (l == 0) sink[w] = acc;
+}
+
 __global__ void probe_empty_kernel() {}
 
 // `phases` grid-wide barriers in one launch.  Every workgroup must be resident at once (the
@@ -105,6 +144,17 @@ extern "C" int probe_read(const void *p, long long bytes, int mode, int blocks, 
     case 2: probe_read_kernel<2><<<blocks, 256, 0, st>>>((const u32x4 *)p, n16, sink); break;
     default: probe_read_kernel<3><<<blocks, 256, 0, st>>>((const u32x4 *)p, n16, sink); break;
   }
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int probe_paged(const void *p, const int *pages, int waves, int run, int mode, uint32_t *sink,
+                           void *stream) {
+  if (!p || !pages || !sink || waves <= 0 || waves % 4 || run <= 0 || mode < 0 || mode > 1) return -1;
+  hipStream_t st = (hipStream_t)stream;
+  if (mode == 0)
+    probe_paged_kernel<0><<<waves / 4, 256, 0, st>>>((const u32x4 *)p, pages, run, sink);
+  else
+    probe_paged_kernel<1><<<waves / 4, 256, 0, st>>>((const u32x4 *)p, pages, run, sink);
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
