@@ -813,6 +813,57 @@ def rocprof_mfma(args) -> int:
     return 0
 
 
+SQ_PASSES = {  # two rocprofv3 --pmc passes (at most 8 SQ counters each)
+    "sqa": ["SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_ANY",
+            "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_VMEM"],
+    "sqb": ["SQ_INST_LEVEL_VMEM", "SQ_INSTS_VMEM_RD", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU", "SQ_INSTS_MFMA",
+            "SQ_ACTIVE_INST_LDS", "SQ_WAIT_INST_LDS", "SQ_CYCLES"],
+}
+
+
+def rocprof_sq(args) -> int:
+    """Per-kernel issue and memory-wait evidence from the two SQ counter passes of SQ_PASSES: where
+    a wave's life goes (waiting on a counter or barrier, ready but not issued, issuing; all as shares
+    of SQ_WAVE_CYCLES), the instructions per wave (VALU, MFMA, vector-memory reads) and the mean
+    vector-memory latency (SQ_INST_LEVEL_VMEM / SQ_INSTS_VMEM_RD, in SQ cycles)."""
+    import csv
+    import collections
+
+    d_dir = args.rocprof_sq
+    vals = collections.defaultdict(lambda: collections.defaultdict(list))
+    for pas in SQ_PASSES:
+        for r in csv.DictReader(open(os.path.join(d_dir, pas, f"{pas}_counter_collection.csv"))):
+            vals[r["Kernel_Name"]][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    cfg = " --no-bs1" if args.config == 2 else f" --config {args.config}"
+    print(f"# rocprofv3 SQ counters of bench.py's config-{args.config} workload")
+    print("# made on one MI355X from the repository root by:")
+    for pas, cs in SQ_PASSES.items():
+        print(f"#   rocprofv3 --pmc {' '.join(cs)} -f csv -d prof/{pas} -o {pas} -- python3 bench.py{cfg} --steps 1 "
+              "--warmup 1 --no-graph")
+    print(f"#   python3 bench.py --rocprof-sq prof{cfg}")
+    print("# shares of SQ_WAVE_CYCLES: wait = SQ_WAIT_ANY (a counter or barrier), ready = SQ_WAIT_INST_ANY (an "
+          "instruction ready, not issued), issue = SQ_ACTIVE_INST_ANY;")
+    print("# per wave: VALU = SQ_INSTS_VALU / SQ_WAVES, MFMA = SQ_INSTS_MFMA / SQ_WAVES, VMEM rd = SQ_INSTS_VMEM_RD / "
+          "SQ_WAVES; vmem latency = SQ_INST_LEVEL_VMEM / SQ_INSTS_VMEM_RD (SQ cycles)")
+    print(f"{'waves':>8} {'wait':>6} {'ready':>6} {'issue':>6} {'VALU/w':>7} {'MFMA/w':>7} {'VMEMrd/w':>8} "
+          f"{'vmem lat':>8}  kernel")
+    for name, c in sorted(vals.items(), key=lambda kv: -float(np.mean(kv[1].get("SQ_WAVE_CYCLES", [0.0])))):
+        if "(anonymous namespace)::" not in name or "at::" in name:
+            continue
+        m = {k: float(np.mean(v)) for k, v in c.items()}
+        wc = m.get("SQ_WAVE_CYCLES", 0.0)
+        w = m.get("SQ_WAVES", 0.0)
+        if not wc or not w:
+            continue
+        rd = m.get("SQ_INSTS_VMEM_RD", 0.0)
+        lat = m.get("SQ_INST_LEVEL_VMEM", 0.0) / rd if rd else 0.0
+        print(f"{w:8.0f} {100 * m.get('SQ_WAIT_ANY', 0) / wc:5.1f}% {100 * m.get('SQ_WAIT_INST_ANY', 0) / wc:5.1f}% "
+              f"{100 * m.get('SQ_ACTIVE_INST_ANY', 0) / wc:5.1f}% {m.get('SQ_INSTS_VALU', 0) / w:7.0f} "
+              f"{m.get('SQ_INSTS_MFMA', 0) / w:7.1f} {rd / w:8.1f} {lat:8.0f}  "
+              f"{name.replace('(anonymous namespace)::', '').split('(')[0]}")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -832,11 +883,14 @@ def main() -> int:
                     help="summarise rocprofv3 CSV output under DIR (kt/, fetch/, write/, cfetch/, cwrite/)")
     ap.add_argument("--op", default="paged_attention", choices=sorted(OP_KERNELS) + ["step"])
     ap.add_argument("--rocprof-mfma", metavar="DIR", help="summarise an MFMA counter pass under DIR/mfma/")
+    ap.add_argument("--rocprof-sq", metavar="DIR", help="summarise the SQ counter passes under DIR/sqa/, DIR/sqb/")
     args = ap.parse_args()
     if args.rocprof_summary:
         return rocprof_summary(args)
     if args.rocprof_mfma:
         return rocprof_mfma(args)
+    if args.rocprof_sq:
+        return rocprof_sq(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
