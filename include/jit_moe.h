@@ -312,8 +312,8 @@ int jit_paged_decode_attn_noalloc(const uint16_t *q, const uint16_t *pool, const
  * keys appended).  Work items: nblk (chunk, first token) pairs blk_chunk, blk_q0 of
  * jit_prefill_block_tokens(H, Hkv) tokens each, covering every chunk (any order;
  * longest first balances best).  out [T, H, 128] bf16; fp32 online softmax.
- * Contract: H % Hkv == 0 (JIT_EINVAL), H / Hkv divides 16, max_pages <= 4096
- * (JIT_EUNSUPPORTED). */
+ * Contract: H % Hkv == 0 (JIT_EINVAL), H / Hkv divides 16 (JIT_EUNSUPPORTED).  Any context
+ * length: the first 4,096 page ids of a work item are staged in LDS, later ones read from the table. */
 int jit_prefill_block_tokens(int H, int Hkv);
 int jit_paged_prefill_attn(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,
                            int max_pages, const int32_t *chunk_seq, const int32_t *chunk_ctx,

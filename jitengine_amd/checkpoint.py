@@ -97,11 +97,34 @@ def read_config(model_path: str) -> CheckpointConfig:
         raise CheckpointError("linear-attention layers are not served (every layer must be full attention)")
     if int(t.get("shared_expert_intermediate_size", 0) or 0):
         raise CheckpointError("shared experts are not served")
+    # RoPE as the reference reads it (Q36/model/config.py:91-95): rope_parameters first, then the
+    # top-level keys; the kernels rotate the whole head with plain frequencies only
+    rp = t.get("rope_parameters") or {}
+    if not isinstance(rp, dict):
+        raise CheckpointError("rope_parameters is not an object")
+    theta = float(rp.get("rope_theta", t.get("rope_theta", 1e6)))
+    prf = float(rp.get("partial_rotary_factor", t.get("partial_rotary_factor", 1.0)))
+    if prf != 1.0:
+        raise CheckpointError(f"partial_rotary_factor {prf}: the kernels rotate the whole head (1.0)")
+    scaling = t.get("rope_scaling") or rp.get("rope_scaling")
+    rtype = rp.get("rope_type", rp.get("type", "default"))
+    if scaling or rtype not in ("default", None):
+        raise CheckpointError(f"RoPE scaling ({scaling or rtype}) is not served: plain RoPE frequencies only")
     cfg = MoEConfig(hidden=D, heads=H, kv_heads=Hkv, head_dim=hd, experts=int(need("num_experts")),
                     top_k=int(need("num_experts_per_tok")), inter=int(need("moe_intermediate_size")),
-                    rope_theta=float(t.get("rope_theta", 1e6)), eps=float(t.get("rms_norm_eps", 1e-6)),
+                    rope_theta=theta, eps=float(t.get("rms_norm_eps", 1e-6)),
                     layers=L, norm_topk=bool(t.get("norm_topk_prob", True)))
+    # stop tokens: config.json's, replaced by generation_config.json's when that file names them
+    # (the reference's order, Q36/model/config.py:98-103)
     eos = raw.get("eos_token_id", t.get("eos_token_id", ()))
+    gen_path = os.path.join(model_path, "generation_config.json")
+    if os.path.exists(gen_path):
+        try:
+            with open(gen_path) as f:
+                g = json.load(f)
+        except ValueError as exc:
+            raise CheckpointError(f"{gen_path} is not valid JSON: {exc}") from None
+        eos = g.get("eos_token_id", eos)
     eos = tuple(int(e) for e in (eos if isinstance(eos, (list, tuple)) else [eos]) if e is not None)
     return CheckpointConfig(cfg, int(need("vocab_size")),
                             bool(raw.get("tie_word_embeddings", t.get("tie_word_embeddings", False))), eos)

@@ -450,7 +450,7 @@ constexpr int kPfWaves = 8, kPfTiles = 2;
 constexpr int kPfHalves = 4;                                           // 32-key halves of a step
 constexpr int kPfStages = 2;                                           // LDS ring depth (steps)
 constexpr int kPfChunks = kPfHalves * 4 * kPageHead * 2 / 1024 / kPfWaves;  // 1 KB chunks of a step per wave
-constexpr int kPfMaxPages = 4096;  // page ids of a workgroup's keys, held in LDS
+constexpr int kPfMaxPages = 4096;  // page ids held in LDS (the first 64 Ki keys; later ones read from the table)
 
 struct PrefillArgs {
   const uint16_t *q;          // [T, H, 128] bf16 (normed, rotated)
@@ -479,7 +479,11 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   const int tlast = min(q0 + kPfWaves * tpw, len) - 1;  // the workgroup's last token
   const int kend = ctx + tlast + 1;                     // its keys: [0, kend)
   const int nst = (kend + 32 * kPfHalves - 1) / (32 * kPfHalves), npages = (kend + 15) >> 4;
-  for (int i = tid; i < npages; i += 64 * kPfWaves) pgs[i] = a.page_table[(long long)seq * a.max_pages + i];
+  const int32_t *prow = a.page_table + (long long)seq * a.max_pages;
+  for (int i = tid; i < min(npages, kPfMaxPages); i += 64 * kPfWaves) pgs[i] = prow[i];
+  // page id i of the workgroup's keys: from LDS for the first kPfMaxPages pages, past them (a context
+  // beyond 64 Ki keys) from the table itself
+  auto page_id = [&](int i) { return i < kPfMaxPages ? pgs[i] : prow[i]; };
 
   // the lane's q row in tile j: token t (clamped into the chunk), head kvh * G + lr % G
   int tok[kPfTiles];
@@ -522,7 +526,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
 #define PF_STAGE(st)                                                                                   \
   _Pragma("unroll") for (int u = 0; u < kPfChunks; u++) {                                              \
     const int c = kPfChunks * wave + u, part = c >> 2;  /* part: K or V (part & 1) of page part / 2 */ \
-    const int pg = pgs[min(2 * kPfHalves * (st) + (part >> 1), npages - 1)];                          \
+    const int pg = page_id(min(2 * kPfHalves * (st) + (part >> 1), npages - 1));                      \
     const uint16_t *src = head_part(a.pool, pg, a.Hkv, kvh) + (part & 1) * kPageHead + (c & 3) * 512 + 8 * l; \
     const uint32_t dst = __builtin_amdgcn_readfirstlane(                                               \
         kvs_lds + 2 * (((st) % kPfStages) * kPfHalves * 4 * kPageHead + 512 * c));                     \
@@ -733,9 +737,6 @@ extern "C" int jit_paged_prefill_attn(const uint16_t *q, const uint16_t *pool, c
   if (H % Hkv != 0) return jit::fail(JIT_EINVAL, "%d query heads do not share %d KV heads evenly", H, Hkv);
   if (16 % (H / Hkv) != 0)
     return jit::fail(JIT_EUNSUPPORTED, "paged_prefill_attn covers H / Hkv in {1, 2, 4, 8, 16}, got %d", H / Hkv);
-  if (max_pages > kPfMaxPages)
-    return jit::fail(JIT_EUNSUPPORTED, "paged_prefill_attn covers max_pages <= %d (keys <= %d), got %d",
-                     kPfMaxPages, kPfMaxPages * kPage, max_pages);
   if (C == 0 || nblk == 0) return JIT_OK;
   if (!q || !pool || !page_table || !chunk_seq || !chunk_ctx || !chunk_len || !chunk_row || !blk_chunk ||
       !blk_q0 || !out)

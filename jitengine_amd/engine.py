@@ -7,10 +7,13 @@ decode.py, retire.py) on this build's pieces:
     the first request that does not fit stops admission until pages come back;
   * a prefix already in the prefix store is restored instead of recomputed -- here by sharing its
     pages (PrefixStore), where the reference copies a snapshot (Q36/kvcache/state.py:121-149);
-  * every step runs the decoding rows (one token each) together with prompt chunks of the
-    requests still in prefill (at most prefill_chunk tokens each, max_step_tokens in all), as the
-    reference's mixed chunked-prefill step does; a step with no prompt chunk is the batched decode
-    step (Model.decode_step);
+  * every step runs the decoding rows (one token each) as one batched decode step
+    (Model.decode_step, on the decode kernels whatever the batch size) and prompt chunks of the
+    requests still in prefill, each chunk a forward of its own (max_step_tokens rows in all);
+  * a generation depends on its request alone, as in the reference (Q36/scheduler/prefill.py:1-6):
+    prompt chunks end at absolute multiples of prefill_chunk and a stored prefix is restored only
+    at such a multiple, so a prompt position is always computed in a chunk of the same rows, with
+    the same kernels (a chunk of 192 or more rows takes the segment GEMMs), cold, warm or batched;
   * a request retires on an end-of-sequence token or after max_tokens tokens
     (Q36/scheduler/retire.py); its prompt's pages then go to the prefix store and the rest of its
     reservation back to the pool;
@@ -63,6 +66,8 @@ class Engine:
                  pipeline: bool = True):
         if prefill_chunk <= 0 or max_step_tokens <= 0:
             raise ValueError("prefill_chunk and max_step_tokens must be positive")
+        if prefill_chunk > max_step_tokens:
+            raise ValueError(f"a prompt chunk ({prefill_chunk} rows) must fit a step ({max_step_tokens} rows)")
         self.lm = lm
         cfg = lm.cfg
         dev = device if device is not None else lm.final_norm.device
@@ -78,7 +83,7 @@ class Engine:
         self.steps = 0
         self.pipeline = bool(pipeline)
         self.pipelined = 0          # steps issued before the previous step's tokens were read
-        self._inflight = None       # (rows, device tokens) of a decode step not yet read
+        self._inflight = None       # (rows, device tokens, pinned host copy, its event) of an unread step
         self._ids = itertools.count()
 
     # ------------------------------------------------------------------ requests
@@ -107,11 +112,11 @@ class Engine:
         while self.queue:
             r = self.queue[0]
             total = pages_for(len(r.prompt) + r.max_tokens)
-            n, pages = self.store.lookup(r.prompt) if self.store is not None else (0, [])
+            n, pages = self._lookup(r.prompt)
             need = total - n // PAGE  # a shared partial page is copied before it is written
             if self.pool.free_pages - self.outstanding < need and self.store is not None:
                 self.store.make_room(need + self.outstanding)
-                n, pages = self.store.lookup(r.prompt)  # (the entry may have been evicted)
+                n, pages = self._lookup(r.prompt)  # (the entry may have been evicted)
                 need = total - n // PAGE
             if self.pool.free_pages - self.outstanding < need:
                 self.deferred += 1
@@ -123,6 +128,15 @@ class Engine:
             self.outstanding += need
             r.state = "prefill"
             self.rows.append(r)
+
+    def _lookup(self, prompt) -> tuple:
+        """The longest stored prefix of the prompt, cut back to a multiple of prefill_chunk (the chunk
+        grid), so the rest of the prompt is computed in the same chunks as a cold run's."""
+        if self.store is None:
+            return 0, []
+        n, pages = self.store.lookup(prompt)
+        n = n // self.prefill_chunk * self.prefill_chunk
+        return n, pages[: pages_for(n)]
 
     def _write(self, r: Request, start: int, n: int) -> None:
         before = self.pool.free_pages
@@ -155,18 +169,29 @@ class Engine:
         return (self.pipeline and not self.queue and len(rows) == len(self.rows)
                 and all(r.state == "decode" and len(r.tokens) + ahead < r.max_tokens for r in rows))
 
+    def _in_flight(self, rows: list, toks: torch.Tensor) -> tuple:
+        """A decode step left unread: its tokens' copy into pinned host memory is queued right behind
+        it (before any later step), so reading them waits for this step alone, not for the step
+        issued after it."""
+        host = torch.empty(toks.shape, dtype=toks.dtype, pin_memory=True)
+        host.copy_(toks, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        return rows, toks, host, ev
+
     def _pump(self) -> list:
         """Consume the step in flight, having issued the next one first when the rows allow."""
-        rows, toks = self._inflight
+        rows, toks, host, ev = self._inflight
         self._inflight = None
         if self._can_pipeline(rows, 1):
             pos = np.array([r.length + 1 for r in rows], np.int32)
             for r in rows:
                 self._write(r, r.length + 1, 1)
-            self._inflight = (rows, self._issue_decode(rows, toks, pos))
+            self._inflight = self._in_flight(rows, self._issue_decode(rows, toks, pos))
             self.steps += 1
             self.pipelined += 1
-        drawn = [(r, t) for r, t in zip(rows, toks.tolist()) if r.state != "done"]
+        ev.synchronize()  # this step's tokens have landed; the next step may still be running
+        drawn = [(r, t) for r, t in zip(rows, host.tolist()) if r.state != "done"]
         self._consume(drawn)
         return drawn
 
@@ -194,55 +219,52 @@ class Engine:
         budget = self.max_step_tokens - len(decode)
         chunks = []
         for r in self.rows:
-            if r.state == "prefill" and budget > 0:
-                n = min(self.prefill_chunk, len(r.prompt) - r.done_prompt, budget)
-                chunks.append((r, r.done_prompt, n))
-                budget -= n
+            if r.state != "prefill":
+                continue
+            # the chunk up to the next multiple of prefill_chunk (or the prompt's end); a chunk that
+            # does not fit the step's budget waits (strict FIFO), it is never cut short
+            n = min(self.prefill_chunk - r.done_prompt % self.prefill_chunk, len(r.prompt) - r.done_prompt)
+            if n > budget:
+                break
+            chunks.append((r, r.done_prompt, n))
+            budget -= n
         if not decode and not chunks:
             return []
         for r, ctx, n in chunks:
             self._write(r, ctx, n)
         for r in decode:
             self._write(r, r.length, 1)
-        lm, cfg, dev = self.lm, self.lm.cfg, self.device
-        dec_pos = np.array([r.length for r in decode], np.int32)
-        dec_ids = [r.tokens[-1] for r in decode]
-        if not chunks:
-            toks = self._issue_decode(decode, dec_ids, dec_pos)
-            self.steps += 1
-            if self._can_pipeline(decode, 0):
-                self._inflight = (decode, toks)
+        drawn = []
+        if decode:
+            dec_pos = np.array([r.length for r in decode], np.int32)
+            toks = self._issue_decode(decode, [r.tokens[-1] for r in decode], dec_pos)
+            if not chunks and self._can_pipeline(decode, 0):
+                self.steps += 1
+                self._inflight = self._in_flight(decode, toks)
                 return []  # read at the next round, after the following step is issued
-            drawn = list(zip(decode, toks.tolist()))
-        else:
-            ids = list(itertools.chain.from_iterable(r.prompt[c:c + n] for r, c, n in chunks)) + dec_ids
-            seqs = [r.rid for r, _, _ in chunks]
-            w = max(1, max(len(self.pool.pages[s]) for s in seqs + [r.rid for r in decode]))
-            seq_table = self.pool.page_table_host(seqs, w)
-            dec_table = self.pool.page_table_host([r.rid for r in decode], w)
-            ms = make_mixed_state(cfg, [(i, c, n) for i, (_, c, n) in enumerate(chunks)], seq_table, dec_pos,
-                                  dec_table, dev)
-            x = lm.embed_tokens(torch.tensor(ids, dtype=torch.int32, device=dev))
-            for layer, pool in zip(lm.layers, self.pool.pools):
-                x = layer.mixed(x, pool, ms)
-            want, rows = [], []
-            end = 0
-            for r, c, n in chunks:
-                end += n
-                if c + n == len(r.prompt):
-                    want.append(end - 1)
-                    rows.append(r)
-            want += [ms.P + j for j in range(len(decode))]
-            rows += decode
-            drawn = []
-            if want:
-                sel = x[torch.tensor(want, dtype=torch.long, device=dev)].contiguous()
-                drawn = list(zip(rows, lm.greedy(sel).tolist()))
-            for r, c, n in chunks:
-                r.done_prompt = c + n
-            self.steps += 1
+            drawn += list(zip(decode, toks.tolist()))
+        for r, c, n in chunks:
+            tok = self._prefill_chunk(r, c, n)
+            r.done_prompt = c + n
+            if tok is not None:
+                drawn.append((r, tok))
+        self.steps += 1
         self._consume(drawn)
         return drawn
+
+    def _prefill_chunk(self, r: Request, c: int, n: int):
+        """Prompt positions c .. c + n - 1 of request r as a forward of their own (the chunked-prefill
+        layer step over one chunk); returns the drawn token when the chunk ends the prompt."""
+        lm, dev = self.lm, self.device
+        seq_table = self.pool.page_table_host([r.rid])
+        ms = make_mixed_state(lm.cfg, [(0, c, n)], seq_table, np.zeros(0, np.int32),
+                              np.zeros((0, seq_table.shape[1]), np.int32), dev)
+        x = lm.embed_tokens(torch.tensor(r.prompt[c:c + n], dtype=torch.int32, device=dev))
+        for layer, pool in zip(lm.layers, self.pool.pools):
+            x = layer.mixed(x, pool, ms)
+        if c + n < len(r.prompt):
+            return None
+        return int(lm.greedy(x[n - 1:n].contiguous()).item())
 
     def run(self, max_steps: int | None = None) -> None:
         """Step until every submitted request is done (or max_steps rounds)."""

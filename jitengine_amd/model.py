@@ -162,13 +162,15 @@ class DecoderLayer:
         moe = self.moe
         if xn is None:
             xn = ops.rmsnorm(x, self.input_norm, cfg.eps)
-        qkv = ops.qmm(xn, self.qkv)
+        # decode rows take the decode kernels at any batch size (seg=False): a row's bits never
+        # depend on how many other rows the step carries
+        qkv = ops.qmm(xn, self.qkv, seg=False)
         q = ops.qk_norm_rope_append(qkv, cfg.heads, cfg.kv_heads, self.q_norm, self.k_norm, cfg.eps,
                                     self.inv_freq, st.pos, st.page_table, pool)
         attn = ops.paged_decode_attention(q, pool, st.page_table, st.plan, cfg.head_dim ** -0.5, st.workspace)
-        o = ops.qmm(attn.view(B, -1), self.o)
+        o = ops.qmm(attn.view(B, -1), self.o, seg=False)
         hn, h = ops.rmsnorm(o, self.post_norm, cfg.eps, resid=x, return_sum=True)
-        logits = ops.qmm(hn, moe.router)
+        logits = ops.qmm(hn, moe.router, seg=False)
         if B <= ops.ROUTE_PACK_MAX_ROWS and moe.num_experts <= 128:  # one launch for a small step
             inds, scores, pk = ops.route_pack(logits, moe.top_k, moe.norm_topk)
         else:
@@ -264,8 +266,9 @@ class CausalLM:
         return ops.embed_q4(ids, self.embed)
 
     def logits(self, h: torch.Tensor) -> torch.Tensor:
-        """Last-layer rows [B, D] -> logits [B, V] bf16."""
-        return ops.qmm(ops.rmsnorm(h, self.final_norm, self.cfg.eps), self.lm_head)
+        """Last-layer rows [B, D] -> logits [B, V] bf16 (the decode kernel at any row count, so a row's
+        logits do not depend on the batch)."""
+        return ops.qmm(ops.rmsnorm(h, self.final_norm, self.cfg.eps), self.lm_head, seg=False)
 
     def greedy(self, h: torch.Tensor) -> torch.Tensor:
         """Last-layer rows -> the greedy token of each row, int32 [B]."""

@@ -53,8 +53,6 @@ def test_contract_breaks_return_einval_before_launch():
                                       None) == _lib.JIT_EINVAL
     assert lib.jit_paged_prefill_attn(*([None] * 3), 16, *([None] * 4), 1, None, None, 1, 24, 8, 0.1, None,
                                       None) == _lib.JIT_EUNSUPPORTED
-    assert lib.jit_paged_prefill_attn(*([None] * 3), 5000, *([None] * 4), 1, None, None, 1, 32, 4, 0.1, None,
-                                      None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_qmm_seg(None, 4, 2048, None, 128, None, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_moe_combine_rmsnorm(None, None, None, 2, 8, 4096, None, None, None, 1e-6, None, None) == _lib.JIT_EUNSUPPORTED
     # empty work is a no-op, not an error

@@ -59,6 +59,10 @@ def test_tied_head_and_layer_limit(tmp_path):
     ({"mlp_only_layers": [1]}, "dense MLP"),
     ({"layer_types": ["linear_attention", "full_attention"]}, "linear-attention"),
     ({"shared_expert_intermediate_size": 512}, "shared experts"),
+    ({"partial_rotary_factor": 0.25}, "partial_rotary_factor"),
+    ({"rope_parameters": {"rope_theta": 1e6, "partial_rotary_factor": 0.5}}, "partial_rotary_factor"),
+    ({"rope_scaling": {"type": "yarn", "factor": 4.0}}, "RoPE scaling"),
+    ({"rope_parameters": {"rope_theta": 1e6, "rope_type": "yarn"}}, "RoPE scaling"),
 ])
 def test_config_rejections(tmp_path, change, what):
     cfg = config_dict()
@@ -106,3 +110,19 @@ def test_shape_mismatch(tmp_path):
     json.dump(cfg, open(tmp_path / "config.json", "w"))
     with pytest.raises(CheckpointError, match="switch_mlp.gate_proj"):
         checkpoint.load(str(tmp_path), "cpu", prepack=False)
+
+
+def test_config_rope_parameters_and_generation_eos(tmp_path):
+    """rope_parameters.rope_theta wins over a top-level rope_theta, and generation_config.json's stop
+    tokens replace config.json's (Q36/model/config.py:91-103)."""
+    cfg = config_dict()
+    cfg["rope_theta"] = 5e5
+    cfg["rope_parameters"] = {"rope_theta": 1e7, "rope_type": "default", "partial_rotary_factor": 1.0}
+    cfg["eos_token_id"] = 7
+    with open(os.path.join(tmp_path, "config.json"), "w") as f:
+        json.dump(cfg, f)
+    cc = checkpoint.read_config(str(tmp_path))
+    assert cc.model.rope_theta == 1e7 and cc.eos_ids == (7,)
+    with open(os.path.join(tmp_path, "generation_config.json"), "w") as f:
+        json.dump({"eos_token_id": [3, 9]}, f)
+    assert checkpoint.read_config(str(tmp_path)).eos_ids == (3, 9)

@@ -7,7 +7,10 @@ bit-identical tokens whether a request runs alone or batched with staggered othe
 prompt's KV is computed or restored from the prefix store (shared pages, one copied), and when a
 small pool defers admission.  The engine tests keep every step under 64 rows, where every op takes
 its row-independent decode kernels (larger batches switch to the segment GEMMs, as the reference
-switches to its prefill kernels)."""
+switches to its prefill kernels): the engine keeps a generation independent of the batch by
+computing prompt chunks on an absolute grid, each in a forward of its own, and decode rows on the
+decode kernels at any batch size (test_engine_long_prompts_cold_warm_batched covers chunks of 512
+rows, which take the segment GEMMs)."""
 
 from __future__ import annotations
 
@@ -109,9 +112,12 @@ def test_engine_batched_equals_solo(lm):
 
 
 def test_engine_prefix_sharing_is_exact(lm):
+    """A 40-token prefix restores at the chunk grid (24 tokens with 24-token chunks): one page shared
+    whole, the half-used second one copied before the request writes into it, the stored pages never
+    written; every generation equals the cold solo run."""
     base, = _prompts(2, [40])
     ext = _prompts(3, [10, 7])
-    e = Engine(lm, 128, prefill_chunk=16, max_step_tokens=48)
+    e = Engine(lm, 128, prefill_chunk=24, max_step_tokens=48)
     a = e.submit(base, 4, eos=())
     e.run()
     stored = list(e.store.entries[tuple(base)])
@@ -119,7 +125,7 @@ def test_engine_prefix_sharing_is_exact(lm):
     b = e.submit(base + ext[0], 5, eos=())
     c = e.submit(base + ext[1], 5, eos=())
     e.run()
-    assert b.cached == 40 and c.cached == 40 and e.pool.copies >= 2
+    assert b.cached == 24 and c.cached == 24 and e.pool.copies >= 2
     assert all(np.array_equal(u16(p[stored]), x) for p, x in zip(e.pool.pools, before))  # never written
     assert a.tokens == _solo(lm, base, 4, prefix_store=False)
     assert b.tokens == _solo(lm, base + ext[0], 5, prefix_store=False)
@@ -218,3 +224,83 @@ def test_engine_page_aligned_edges(lm):
     d = e.submit(p16 + [7], 4, eos=())
     e.run()
     assert d.cached == 16 and d.tokens == _solo(lm, p16 + [7], 4, prefix_store=False)
+
+
+def test_engine_long_prompts_cold_warm_batched(lm):
+    """Prompts over 192 tokens at the default prefill_chunk (512): their chunks take the segment
+    GEMMs (the reference's prefill kernels), yet every generation is bit-identical cold (solo, no
+    prefix store), warm (a stored 600-token prefix restores at the 512-token grid) and batched with
+    another long prompt and decoding rows."""
+    base, = _prompts(9, [600])
+    tails = _prompts(10, [120, 30])
+    A, B, X = base + tails[0], base + tails[1], base
+
+    def solo(p, n):
+        e = Engine(lm, 256, pipeline=False, prefix_store=False)
+        r = e.submit(p, n, eos=())
+        e.run()
+        return r.tokens
+
+    cold_a, cold_b = solo(A, 4), solo(B, 4)
+    e = Engine(lm, 256)
+    x = e.submit(X, 2, eos=())
+    e.run()
+    a = e.submit(A, 4, eos=())
+    b = e.submit(B, 4, eos=())
+    e.run()
+    assert a.cached == 512 and b.cached == 512
+    assert a.tokens == cold_a and b.tokens == cold_b
+    e2 = Engine(lm, 256, prefix_store=False)
+    rs = [e2.submit(p, n, eos=()) for p, n in ((A, 4), (B, 4), (X, 2))]
+    short = e2.submit(_prompts(11, [9])[0], 6, eos=())
+    e2.run()
+    assert rs[0].tokens == cold_a and rs[1].tokens == cold_b and rs[2].tokens == x.tokens
+    assert short.tokens == solo(_prompts(11, [9])[0], 6)
+
+
+def test_decode_rows_independent_of_a_large_batch():
+    """A decode step of 200 rows (past the 192-row switch of the dense projections) keeps every row's
+    bits equal to the row decoded alone: the decode step never takes the segment GEMMs."""
+    cfg = MoEConfig(layers=1, experts=32)
+    from jitengine_amd.model import random_layer_weights
+
+    model = Model(cfg, [random_layer_weights(cfg, seed=61, device=DEV)])
+    B = 200
+    rng = np.random.default_rng(62)
+    lens = rng.integers(1, 60, B)
+    npg = (lens + 1 + 15) // 16
+    perm = rng.permutation(int(npg.sum()))
+    table = np.zeros((B, int(npg.max())), np.int32)
+    at = 0
+    for b in range(B):
+        table[b, :npg[b]] = perm[at:at + npg[b]]
+        at += npg[b]
+    pool = normal_bf16((int(npg.sum()), cfg.kv_heads, 2, 2048), seed=63)
+    x = normal_bf16((B, 2048), seed=64)
+    st = model.make_state(lens, torch.from_numpy(table).to(DEV))
+    batched = u16(model.decode_step(bf16_tensor(x, DEV), [bf16_tensor(pool, DEV)], st))
+    for b in (0, 77, 199):
+        stb = model.make_state(lens[b:b + 1], torch.from_numpy(table[b:b + 1]).to(DEV))
+        solo = u16(model.decode_step(bf16_tensor(x[b:b + 1], DEV), [bf16_tensor(pool, DEV)], stb))
+        assert np.array_equal(solo[0], batched[b]), b
+
+
+def test_engine_pipelining_overlaps_the_host(lm):
+    """With pipelining the host reads step n's tokens (a pinned copy queued right behind step n) while
+    step n + 1 runs: a decode-only run is no slower than the synchronous loop (timings printed)."""
+    import time
+
+    prompts = _prompts(12, [20, 9, 33, 14])
+    t = {}
+    for pipe in (False, True, False, True):
+        e = Engine(lm, 128, prefill_chunk=16, max_step_tokens=48, pipeline=pipe, prefix_store=False)
+        rs = [e.submit(p, 40, eos=()) for p in prompts]
+        while any(r.state in ("queued", "prefill") for r in rs):
+            e.step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e.run()
+        torch.cuda.synchronize()
+        t[pipe] = time.perf_counter() - t0
+    print(f"decode-only run: synchronous {1e3 * t[False]:.1f} ms, pipelined {1e3 * t[True]:.1f} ms", flush=True)
+    assert t[True] <= 1.1 * t[False]

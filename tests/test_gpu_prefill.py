@@ -165,3 +165,36 @@ def test_mixed_prefill_decode_layer_stages():
     moe = oracle.moe_combine(r, pk["inv"], u16(dbg["scores"]))
     want_y = oracle.f32_to_bf16(bf16_to_f32(u16(dbg["h"])) + bf16_to_f32(moe))
     assert_close_bf16(u16(y), want_y, what="mixed step output")
+
+
+def test_prefill_and_mixed_step_past_4096_pages():
+    """Contexts beyond 65,536 keys (4,096 pages, the page ids a prefill work item stages in LDS): a
+    prefill chunk after 70,000 tokens reads its later page ids from the table, and a mixed step carries
+    a decode row of 70,001 keys beside a short chunk; both against the oracle."""
+    from jitengine_amd.model import DecoderLayer, MoEConfig, make_mixed_state, random_layer_weights
+
+    pool, table = _pool([70040], seed=71)
+    q = normal_bf16((40, 32, 128), seed=72)
+    got = _run(q, pool, table, [(0, 70000, 40)])
+    sel = np.array([0, 13, 39])
+    want, exact = oracle.paged_decode_attn(q[sel], pool, table[[0, 0, 0]], 70000 + sel + 1, SCALE, exact=True)
+    assert_attention_parity(got[sel], exact, what="prefill past 4096 pages")
+    assert_close_bf16(got[sel], want, what="prefill past 4096 pages")
+
+    cfg = MoEConfig(experts=32, layers=1)
+    chunks = [(0, 100, 30)]
+    dec_pos = [70000]
+    pool, table = _pool([130, 70001], seed=73)
+    w = random_layer_weights(cfg, seed=74, device=DEV)
+    layer = DecoderLayer(cfg, w)
+    ms = make_mixed_state(cfg, chunks, table[:1], dec_pos, table[1:], DEV)
+    x = bf16_tensor(normal_bf16((31, cfg.hidden), seed=75), DEV)
+    pt = bf16_tensor(pool, DEV)
+    dbg = {}
+    layer.mixed(x, pt, ms, debug=dbg)
+    torch.cuda.synchronize()
+    qh, attn, pool_after = u16(dbg["q"]), u16(dbg["attn"]), u16(pt)
+    _, ex_pre = oracle.paged_prefill_attn(qh[:30], pool_after, table[:1], chunks, SCALE, exact=True)
+    assert_attention_parity(attn[:30], ex_pre, what="mixed prefill rows")
+    _, ex_dec = oracle.paged_decode_attn(qh[30:], pool_after, table[1:], np.array(dec_pos) + 1, SCALE, exact=True)
+    assert_attention_parity(attn[30:], ex_dec, what="mixed decode row of 70,001 keys")

@@ -78,11 +78,11 @@ def test_prefix_store_lookup_insert_evict():
     assert not s.entries and p.free_pages == 32
 
 
-def _engine(num_pages, store=True):
+def _engine(num_pages, store=True, prefill_chunk=8):
     cfg = SimpleNamespace(kv_heads=4, heads=32)
     lm = SimpleNamespace(cfg=cfg, layers=[None, None], vocab=100, eos_ids=(99,),
                          final_norm=torch.zeros(1))
-    return Engine(lm, num_pages, prefix_store=store, allocate=False)
+    return Engine(lm, num_pages, prefill_chunk=prefill_chunk, prefix_store=store, allocate=False)
 
 
 def test_admission_is_fifo_and_charges_the_whole_generation():
@@ -123,3 +123,21 @@ def test_admission_restores_a_stored_prefix():
     assert e.pool.copies == 1 and b.reserved == 0
     assert e.pool.pages[b.rid][:2] == e.store.entries[tuple(range(40))][:2]
     assert e.pool.pages[b.rid][2] != e.store.entries[tuple(range(40))][2]
+
+
+def test_restore_is_cut_back_to_the_chunk_grid():
+    """A stored prefix restores only up to a multiple of prefill_chunk (the reference's absolute chunk
+    grid, Q36/scheduler/prefill.py:1-6), so the rest of the prompt is computed in the chunks of a cold
+    run; a chunk never crosses a grid line and a chunk larger than a step is refused."""
+    e = _engine(20, prefill_chunk=16)
+    a = e.submit(list(range(40)), 8)
+    e._admit()
+    e._write(a, 0, 40)
+    a.done_prompt = 40
+    e._retire(a, "length")
+    b = e.submit(list(range(40)) + [7, 8, 9], 5)
+    e._admit()
+    assert b.cached == 32 and b.done_prompt == 32 and len(e.pool.pages[b.rid]) == 2
+    with pytest.raises(ValueError):
+        Engine(SimpleNamespace(cfg=SimpleNamespace(kv_heads=4, heads=32), layers=[None], vocab=10, eos_ids=(),
+                               final_norm=torch.zeros(1)), 4, prefill_chunk=64, max_step_tokens=32, allocate=False)
