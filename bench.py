@@ -354,6 +354,7 @@ def bench_config3(steps: int, warmup: int, dev: str) -> dict:
 
 
 CONFIG4_KEYS = 262144  # one sequence decoding at 262,144 KV tokens
+CONFIG0_KEYS = 4096    # one block, batch 1, 4,096 context tokens in one page run
 
 
 def decode_model(cfg, seed: int, dev: str):
@@ -391,12 +392,17 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
     if config == 2:
         B = 32
         lens = np.round(np.exp(rng.uniform(np.log(128), np.log(32768), B))).astype(np.int32)
+    elif config == 0:
+        B = 1
+        lens = np.array([CONFIG0_KEYS], np.int32)
+        n_layers = 1
     else:
         B = 1
         lens = np.array([CONFIG4_KEYS - 1], np.int32)
     npg = (lens + 1 + 15) // 16
     num_pages = int(npg.sum())
-    perm = rng.permutation(num_pages)
+    # config 0's context is one contiguous page run (pages 0.. in order); the others are permuted
+    perm = np.arange(num_pages) if config == 0 else rng.permutation(num_pages)
     table = np.zeros((B, int(npg.max())), np.int32)
     at = 0
     for b in range(B):
@@ -490,6 +496,8 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
     for name in (("router_topk", "moe_pack") if B <= ops.ROUTE_PACK_MAX_ROWS else ("route_pack",)):
         del per_layer[name]
     launches = {name: step_layers.get(name, list(range(n_layers))) for name in per_layer}
+    launches = {name: ls for name, ls in launches.items() if ls}  # (a one-layer step has no combine_rmsnorm)
+    per_layer = {name: f for name, f in per_layer.items() if name in launches}
     kus = time_ops({name: [(lambda f=f, l=l: f(l)) for l in launches[name]] for name, f in per_layer.items()},
                    reps=3)
     step_us = {name: kus[name] * len(launches[name]) for name in kus}
@@ -502,7 +510,8 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
     # the dominant op by device time, and its algorithmic bytes per launch (the same for every layer
     # for attention; the mean over layers for the experts)
     alg_op = {"paged_attention": kv, "gate_up_swiglu": float(np.mean(U)) * 1769472,
-              "down": float(np.mean(U)) * 884736}
+              "down": float(np.mean(U)) * 884736, "qkv_proj": cfg.qkv_rows * cfg.hidden // 2 * 9 // 8,
+              "o_proj": cfg.hidden * cfg.heads * 128 // 2 * 9 // 8, "router_proj": cfg.experts * cfg.hidden // 2 * 9 // 8}
     dom = max(kus, key=kus.get)
     achieved = alg_op[dom] / (kus[dom] * 1e-6) / 1e9 if dom in alg_op else None
 
@@ -510,6 +519,9 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
     if config == 2:
         workload = (f"config2: ragged 32-sequence decode, {n_layers} layers of the Qwen3-MoE-style 4-bit block, "
                     "paged bf16 KV (16-token pages, permuted), lens log-uniform [128, 32768]")
+    elif config == 0:
+        workload = ("config0: one Qwen3-MoE-style 4-bit block, batch-1 decode at position 4096 over a 4,096-token "
+                    "bf16 context in one contiguous page run (pages 0..256 in order)")
     else:
         workload = (f"config4: single-sequence decode at {CONFIG4_KEYS} KV tokens, {n_layers} layers of the "
                     "Qwen3-MoE-style 4-bit block, paged bf16 KV (16-token pages, permuted), split-K attention")
@@ -557,15 +569,16 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
     for i in range(6):
         ph = pool_h.copy()
         c0 = time.perf_counter()
-        oracle.decoder_layer(xs, lw, ph, table, lens, ocfg)
+        oracle.decoder_layer_mlx_f32(xs, lw, ph, table, lens, ocfg)
         if i:
             times.append(time.perf_counter() - c0)
     cpu_tps = B / (float(np.median(times)) * n_layers)
 
     res["cpu_baseline"] = {
-        "value": cpu_tps, "unit": "tokens/s", "cores": cpu_threads(), "kind": "port",
-        "sample": f"oracle decoder layer (C, float64 dots, OpenMP) on all {B} rows with layer 0's weights and KV "
-                  f"({int(lens.sum())} keys), median of 5 after a warm-up, x {n_layers} layers"}
+        "value": cpu_tps, "unit": "tokens/s", "cores": cpu_threads(), "kind": "port", "label": "restatement",
+        "sample": f"the reference's MLX op chain restated in its own fp32 arithmetic (oracle.decoder_layer_mlx_f32: "
+                  f"qmv per-lane order, sdpa_vector / two-pass attention, C + OpenMP) on all {B} rows with layer 0's "
+                  f"weights and KV ({int(lens.sum())} keys), median of 5 after a warm-up, x {n_layers} layers"}
     return res
 
 
@@ -903,7 +916,7 @@ def main() -> int:
         return probe(dev, set(args.probe_parts.split(",")))
     if args.config == 1:
         res = bench_config1(args.steps, args.warmup, dev)
-    elif args.config in (2, 4):
+    elif args.config in (0, 2, 4):
         res = bench_decode(args.config, args.steps, args.warmup, dev, graph=not args.no_graph,
                            n_layers=args.layers)
         if args.config == 2 and not args.no_bs1:

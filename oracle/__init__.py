@@ -342,6 +342,41 @@ def decoder_layer(x, layer: dict, pool, page_table, pos, cfg: dict, routing=None
             "inds": inds, "scores": scores, "y": y}
 
 
+def decoder_layer_mlx_f32(x, layer: dict, pool, page_table, pos, cfg: dict) -> np.ndarray:
+    """decoder_layer in the reference's own fp32 arithmetic (the MLX CPU op chain this build's CPU
+    baseline times): the projections in MLX qmv's per-lane fp32 order (qmv_mlx_f32) rounded to
+    bf16, attention as MLX's sdpa_vector / two-pass kernels (sdpa_mlx_f32), every expert pair's
+    gate/up/down by qmv_mlx_f32 with the SigmoidX bf16 chain, and the slot-order bf16 combine.
+    Returns the layer output y [B, D] bf16; `pool` is updated in place (the KV append)."""
+    H, Hkv, E, k, eps = cfg["heads"], cfg["kv_heads"], cfg["experts"], cfg["top_k"], cfg["eps"]
+    B = x.shape[0]
+    xn, _ = rmsnorm(x, layer["input_norm"], eps)
+    qkv = f32_to_bf16(qmv_mlx_f32(xn, *layer["qkv"]))
+    q = qk_norm_rope_append(qkv, H, Hkv, layer["q_norm"], layer["k_norm"], eps, cfg["inv_freq"], pos, pool, page_table)
+    attn, _ = sdpa_mlx_f32(q, pool, page_table, np.asarray(pos, np.int64) + 1, 128 ** -0.5)
+    o = f32_to_bf16(qmv_mlx_f32(attn.reshape(B, -1), *layer["o"]))
+    hn, h = rmsnorm(o, layer["post_norm"], eps, resid=x)
+    logits = f32_to_bf16(qmv_mlx_f32(hn, *layer["router"]))
+    inds, scores, _ = router_topk(logits, k, True)
+    gw, gs, gb = layer["gate_up"]
+    dw, ds, db = layer["down"]
+    I = gw.shape[1] // 2
+    r = np.zeros((B, k, hn.shape[1]), np.uint16)
+    for e in np.unique(inds):
+        rows, slots = np.nonzero(inds == e)
+        gu = f32_to_bf16(qmv_mlx_f32(hn[rows], gw[e], gs[e], gb[e]))
+        g, u = gu[:, :I], gu[:, I:]
+        with np.errstate(over="ignore", invalid="ignore"):
+            sl = f32_to_bf16(bf16_to_f32(g) * bf16_to_f32(sigmoid_bf16(g)))
+            hh = f32_to_bf16(bf16_to_f32(sl) * bf16_to_f32(u))
+        r[rows, slots] = f32_to_bf16(qmv_mlx_f32(hh, dw[e], ds[e], db[e]))
+    acc = np.zeros(hn.shape, np.float32)
+    for j in range(k):
+        p = bf16_to_f32(f32_to_bf16(bf16_to_f32(r[:, j]) * bf16_to_f32(scores[:, j:j + 1])))
+        acc = bf16_to_f32(f32_to_bf16(acc + p))
+    return f32_to_bf16(bf16_to_f32(h) + acc)
+
+
 # ----------------------------------------------------------------------------- paged KV
 PAGE = 16
 

@@ -298,7 +298,10 @@ int jo_qmm(const uint16_t *x, int T, const uint32_t *w, const uint16_t *s, const
  * (FN/kernels/selfcheck.py:313-331). */
 int jo_qmv_mlx_f32(const uint16_t *x, int T, const uint32_t *w, const uint16_t *s,
                    const uint16_t *b, int N, int K, float *out) {
-  if (T < 0 || N < 0 || K <= 0 || (K % 512) != 0) return JO_EINVAL;
+  /* K % 512 is qmv_fast's case; a K with a partial last block (K % 64 == 0, e.g. the
+   * 768-wide down projection) leaves the lanes past K out of that block (MLX's plain qmv
+   * tail; its lane bits there are not pinned) */
+  if (T < 0 || N < 0 || K <= 0 || (K % 64) != 0) return JO_EINVAL;
 #pragma omp parallel for schedule(static)
   for (int n = 0; n < N; n++) {
     const uint8_t *wb = (const uint8_t *)(w + (size_t)n * (K / 8));
@@ -310,6 +313,7 @@ int jo_qmv_mlx_f32(const uint16_t *x, int T, const uint32_t *w, const uint16_t *
         float res = 0.0f;
         for (int kb = 0; kb < K; kb += 512) {
           const int k0 = kb + 16 * l;
+          if (k0 >= K) continue;
           float xt[16], sum = 0.0f;
           for (int i = 0; i < 16; i += 4) {
             const float a0 = bf2f(xr[k0 + i]), a1 = bf2f(xr[k0 + i + 1]);

@@ -548,3 +548,37 @@ def test_argmax_rows_pinned_by_numpy():
     y[2, :] = 0x7FC0                      # all NaN: 0
     assert oracle.argmax_rows(y)[0] == np.argmax(oracle.bf16_to_f32(x[0, 3:])) + 3
     assert oracle.argmax_rows(y)[2] == 0
+
+
+def test_mlx_f32_layer_close_to_float64_layer():
+    """decoder_layer_mlx_f32 (the reference's fp32 arithmetic, the CPU baseline's chain) agrees with
+    the float64 decoder_layer within the composition tolerance, and its 768-wide down projection (a
+    partial 512-block of qmv lanes) is fp32-accurate."""
+    from jitengine_amd.model import MoEConfig, random_layer_weights, rope_inv_freq
+
+    cfg = MoEConfig(layers=1, experts=16)
+    w = random_layer_weights(cfg, 9, "cpu")
+    qn = ("qkv", "o", "router", "gate_up", "down")
+    lw = {k: (stack_np(v) if k in qn else v.view(torch.int16).numpy().view(np.uint16)) for k, v in w.items()}
+    lens = [5, 300, 2000]
+    npg = [-(-(L + 1) // 16) for L in lens]
+    perm = np.random.default_rng(3).permutation(sum(npg))
+    table = np.zeros((3, max(npg)), np.int32)
+    at = 0
+    for i, n in enumerate(npg):
+        table[i, :n] = perm[at:at + n]
+        at += n
+    pool = normal_bf16((sum(npg), 4, 2, 2048), seed=4)
+    x = normal_bf16((3, 2048), seed=5)
+    ocfg = {"heads": 32, "kv_heads": 4, "experts": 16, "top_k": 8, "eps": 1e-6, "inv_freq": rope_inv_freq(1e6, 128)}
+    pos = np.array(lens, np.int32)
+    y = oracle.decoder_layer_mlx_f32(x, lw, pool.copy(), table, pos, ocfg)
+    ref = oracle.decoder_layer(x, lw, pool.copy(), table, pos, ocfg)["y"]
+    a, b = bf16_to_f32(y).astype(np.float64), bf16_to_f32(ref).astype(np.float64)
+    assert a.ravel() @ b.ravel() / (np.linalg.norm(a) * np.linalg.norm(b)) > 0.9999
+    assert np.abs(a - b).max() <= 4 * np.maximum(np.abs(b), 1) .max() * 2.0**-8
+    dw, ds, db = lw["down"]
+    hx = normal_bf16((4, 768), seed=6)
+    f, _ = oracle.qmm(hx, dw[0], ds[0], db[0])
+    m = oracle.qmv_mlx_f32(hx, dw[0], ds[0], db[0]).astype(np.float64)
+    assert np.abs(m - f).max() <= 2.0**-16 * np.abs(f).max()
