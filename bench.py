@@ -742,7 +742,7 @@ def rocprof_summary(args) -> int:
             print(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:9.2f} "
                   f"{float(r['MaxNs']) / 1e3:9.2f} {100 * float(r['TotalDurationNs']) / tot:6.1f}%  {name}")
         return 0
-    ng = " --no-graph" if args.config in (2, 4) else ""  # (config 3 always replays a graph)
+    ng = " --no-graph" if args.config in (0, 2, 4) else ""  # (config 3 always replays a graph)
     for c in (f"FETCH_SIZE -f csv -d prof/fetch -o fetch -- python3 bench.py{cfg} --steps 1 --warmup 1{ng}",
               f"WRITE_SIZE -f csv -d prof/write -o write -- python3 bench.py{cfg} --steps 1 --warmup 1{ng}",
               "FETCH_SIZE -f csv -d prof/cfetch -o cfetch -- python3 bench.py --copy-calibration",
@@ -796,7 +796,7 @@ def rocprof_mfma(args) -> int:
     for r in csv.DictReader(open(os.path.join(d_dir, "mfma", "mfma_counter_collection.csv"))):
         vals[r["Kernel_Name"]][r["Counter_Name"]].append(float(r["Counter_Value"]))
     cfg = " --no-bs1" if args.config == 2 else f" --config {args.config}"
-    ng = " --no-graph" if args.config in (2, 4) else ""
+    ng = " --no-graph" if args.config in (0, 2, 4) else ""
     print(f"# rocprofv3 MFMA counters of bench.py's config-{args.config} workload")
     print("# made on one MI355X from the repository root by:")
     print("#   rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_BUSY_CU_CYCLES SQ_LDS_BANK_CONFLICT "

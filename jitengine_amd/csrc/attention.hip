@@ -450,7 +450,9 @@ constexpr int kPfWaves = 8, kPfTiles = 2;
 constexpr int kPfHalves = 4;                                           // 32-key halves of a step
 constexpr int kPfStages = 2;                                           // LDS ring depth (steps)
 constexpr int kPfChunks = kPfHalves * 4 * kPageHead * 2 / 1024 / kPfWaves;  // 1 KB chunks of a step per wave
-constexpr int kPfMaxPages = 4096;  // page ids held in LDS (the first 64 Ki keys; later ones read from the table)
+// each wave stages the K and V of one page per step (4 parts of 4 KB in 1 KB chunks)
+static_assert(kPfChunks == 8 && kPfWaves == 2 * kPfHalves, "one page per wave per step");
+static_assert(kPfStages == 2, "the page-id prefetch below runs one step ahead of the staging");
 
 struct PrefillArgs {
   const uint16_t *q;          // [T, H, 128] bf16 (normed, rotated)
@@ -469,7 +471,6 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   // (4 KB each), filled by direct global->LDS loads kPfStages - 1 steps ahead of the step
   // being computed
   __shared__ __attribute__((aligned(16))) uint16_t kvs[kPfStages][kPfHalves * 4 * kPageHead];
-  __shared__ int pgs[kPfMaxPages];
   const int ch = a.blk_chunk[blockIdx.x], q0 = a.blk_q0[blockIdx.x];
   const int kvh = blockIdx.y;
   const int seq = a.chunk_seq[ch], ctx = a.chunk_ctx[ch], len = a.chunk_len[ch], row0 = a.chunk_row[ch];
@@ -480,10 +481,12 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   const int kend = ctx + tlast + 1;                     // its keys: [0, kend)
   const int nst = (kend + 32 * kPfHalves - 1) / (32 * kPfHalves), npages = (kend + 15) >> 4;
   const int32_t *prow = a.page_table + (long long)seq * a.max_pages;
-  for (int i = tid; i < min(npages, kPfMaxPages); i += 64 * kPfWaves) pgs[i] = prow[i];
-  // page id i of the workgroup's keys: from LDS for the first kPfMaxPages pages, past them (a context
-  // beyond 64 Ki keys) from the table itself
-  auto page_id = [&](int i) { return i < kPfMaxPages ? pgs[i] : prow[i]; };
+  // wave w stages on step st page 2 kPfHalves st + w of the workgroup's keys (a page past the keys
+  // repeats the last one); lane i reads the page of wave i % kPfWaves, so that the ids stay in a
+  // vector register until the step that stages them reads its lane
+  auto pages_of_step = [&](int st) {
+    return prow[min(2 * kPfHalves * st + (l & (kPfWaves - 1)), npages - 1)];
+  };
 
   // the lane's q row in tile j: token t (clamped into the chunk), head kvh * G + lr % G
   int tok[kPfTiles];
@@ -523,14 +526,16 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   // stages apart), and the explicit waits below order them; its waits for other loads only
   // grow more conservative.
   const uint32_t kvs_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)&kvs[0][0];
-#define PF_STAGE(st)                                                                                   \
+#define PF_STAGE(st, pv)                                                                               \
+  {                                                                                                    \
+  const int pg = __builtin_amdgcn_readlane(pv, wave);                                                  \
   _Pragma("unroll") for (int u = 0; u < kPfChunks; u++) {                                              \
-    const int c = kPfChunks * wave + u, part = c >> 2;  /* part: K or V (part & 1) of page part / 2 */ \
-    const int pg = page_id(min(2 * kPfHalves * (st) + (part >> 1), npages - 1));                      \
+    const int c = kPfChunks * wave + u, part = c >> 2;  /* part: K or V (part & 1) of page pg */       \
     const uint16_t *src = head_part(a.pool, pg, a.Hkv, kvh) + (part & 1) * kPageHead + (c & 3) * 512 + 8 * l; \
     const uint32_t dst = __builtin_amdgcn_readfirstlane(                                               \
         kvs_lds + 2 * (((st) % kPfStages) * kPfHalves * 4 * kPageHead + 512 * c));                     \
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0"); \
+  }                                                                                                    \
   }
   // the q fragments have landed before the first staged load is issued: the compiler's waits
   // for them would otherwise sit inside the loop, where they would also wait for the staging
@@ -539,10 +544,10 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
 #pragma unroll
     for (int cc = 0; cc < 4; cc++)
       asm volatile("" ::"v"(qf[j][cc].u[0]), "v"(qf[j][cc].u[1]), "v"(qf[j][cc].u[2]), "v"(qf[j][cc].u[3]));
-#pragma unroll
-  for (int st = 0; st < kPfStages - 1; st++) {
-    PF_STAGE(st);
-  }
+  PF_STAGE(0, pages_of_step(0));
+  // the pages of the next step to stage, read one step ahead so that their latency hides behind a
+  // step's arithmetic (the wait for them is the loop's own wait for the staging)
+  int pv_next = pages_of_step(1);
   // the wait that leaves the loads of the next kPfStages - 2 steps in flight, and no lgkm or
   // export wait (vmcnt is split over bits 3:0 and 15:14)
   constexpr int kPfVm = (kPfStages - 2) * kPfChunks;
@@ -557,7 +562,8 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
     __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    PF_STAGE(st + kPfStages - 1);
+    PF_STAGE(st + 1, pv_next);
+    pv_next = pages_of_step(st + 2);
     const uint16_t *kvst = kvs[st % kPfStages];
     const int k0 = 32 * kPfHalves * st;
     // Key order within each 32-key half h (keys k0 + 32 h ..): the P.V MFMA's k index 8 lg + j
