@@ -331,11 +331,49 @@ int jit_paged_prefill_attn(const uint16_t *q, const uint16_t *pool, const int32_
 int jit_embed_q4(const int32_t *ids, int B, const uint32_t *weight, const uint16_t *scales,
                  const uint16_t *biases, int V, int D, uint16_t *out, void *stream);
 
-/* Greedy choice: out[b] = the first index of the largest of logits[b, 0..V) (bf16).  The
- * reference takes mx.argmax of the log-probabilities (Sampler.__call__ with temperature 0,
- * Q36/sampler.py:371-374); log-softmax is monotone per row, so the index is the same.  NaN
- * never wins against a number; a row of NaNs gives 0. */
+/* Token sampling over rows of bf16 logits [B, V] (Q36/sampler.py), one workgroup per row.
+ * Shared definitions:
+ *   lse  = bf16(m0 + ln(S 2^-42)), m0 the row's largest logit and S = sum floor(e^(x - m0) 2^42);
+ *   lp   = bf16(x - lse) (logprobs_from_logits, Q36/sampler.py:295-297).
+ * The sums are exact integers, so results do not depend on the order of the additions; the
+ * reference's fp32 reductions (MLX's logsumexp, cumsum and sum orders) are not restated.
+ * Contract: 1 <= V <= 2^20 (JIT_EUNSUPPORTED beyond); finite or -inf logits with at least one
+ * finite value per row (other rows give unspecified tokens, never a fault). */
+
+/* lp [B, V] bf16 = the rows' log-probabilities as defined above. */
+int jit_logprobs_rows(const uint16_t *logits, int B, int V, uint16_t *lp, void *stream);
+
+/* Greedy choice: out[b] = the first index of the largest lp of row b (Sampler.__call__ with
+ * temperature 0: mx.argmax of the log-probabilities, Q36/sampler.py:371-374).  The bf16
+ * rounding of x - lse can tie logits that differ, so this is not always the argmax of the
+ * logits themselves. */
 int jit_argmax_rows(const uint16_t *logits, int B, int V, int32_t *out, void *stream);
+
+/* One draw per row under shared settings (the rows of a Sampler.rows_key group,
+ * Q36/sampler.py:479-483): temperature <= 0 is the greedy choice above; otherwise, with
+ * inv_t = bf16(fp32(1 / temperature)) and thr = bf16(fp32(1 - top_p)):
+ *   order   ascending (lp, index), -0 tying +0 (the stable argsort, :458-459);
+ *   top_p   in (0, 1): position r survives iff bf16(sum_{r' <= r} floor(bf16(e^lp) 2^42) 2^-42)
+ *           > thr (apply_top_p, :300-312; _sample_exact_full, :460-462); outside (0, 1) all survive;
+ *   top_k   in [1, V): of the survivors, the k largest by (value desc, index asc) (apply_top_k,
+ *           :315-318; _sample_exact_full's cut, :463-469); 0 or >= V: all survivors;
+ *   weights x = bf16(lp inv_t) of the kept, m = max x, W = floor(e^(x - m) 2^42), 0 elsewhere;
+ *   draw    C_i = sum_{j < i} W_j, U = floor(u' 2^32 sum(W) 2^-32) with u' = u[b] clamped to
+ *           [0, 1 - 2^-24]; tokens[b] = the last i with C_i <= U (the categorical draw as
+ *           searchsorted(cdf, u * sum(w), "right") - 1, :470-476).
+ * Where no position survives top_p (bf16 mass below 1 - top_p: top_p under about 0.03) the
+ * greedy token is drawn; the reference's chains disagree among themselves there.
+ * u: [B] fp32 uniforms on the device (jit_threefry_uniform); unused when greedy.
+ * Contract breaks (JIT_EINVAL): NaN settings, top_k < 0, null uniforms when sampling;
+ * 1 / temperature that rounds to 0 or infinity in bf16 is JIT_EUNSUPPORTED. */
+int jit_sample_rows(const uint16_t *logits, int B, int V, double temperature, double top_p, int top_k,
+                    const float *u, int32_t *tokens, void *stream);
+
+/* u[b] = min(fp32(y0) / 2^32, 1 - 2^-24), (y0, y1) = Threefry-2x32-20(keys[b] = (k0, k1),
+ * counter (0, 0)) (Salmon et al., SC'11): the uniform mx.random.uniform(shape=(1,), key) draws
+ * for a step key (Sampler.uniform, Q36/sampler.py:367-369; the fused tail's replay,
+ * :160-177).  keys: [B, 2] uint32 on the device. */
+int jit_threefry_uniform(const uint32_t *keys, int B, float *u, void *stream);
 
 /* Copy page src[i] to page dst[i] (i < n; device arrays) inside one layer's pool
  * [num_pages, Hkv, 2, 16 * 128] bf16: the copy-on-write of a shared page before a sequence

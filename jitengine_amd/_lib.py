@@ -54,7 +54,10 @@ _SIGNATURES = {
     "jit_prefill_block_tokens": [_I, _I],
     "jit_paged_prefill_attn": [_P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _F, _P, _P],
     "jit_embed_q4": [_P, _I, _P, _P, _P, _I, _I, _P, _P],
+    "jit_logprobs_rows": [_P, _I, _I, _P, _P],
     "jit_argmax_rows": [_P, _I, _I, _P, _P],
+    "jit_sample_rows": [_P, _I, _I, ctypes.c_double, ctypes.c_double, _I, _P, _P, _P],
+    "jit_threefry_uniform": [_P, _I, _P, _P],
     "jit_kv_copy_pages": [_P, _I, _I, _P, _P, _I, _P],
 }
 _RESTYPES = {"jit_last_error": ctypes.c_char_p, "jit_attn_workspace_bytes": ctypes.c_int64,

@@ -34,6 +34,7 @@ SOURCES = {
     "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "block.hip": [],
     "head.hip": [],
+    "sampler.hip": ["-ffp-contract=off"],
 }
 
 _COMMON = [

@@ -1,9 +1,6 @@
 // The ends of the decode step and the KV pages' copy-on-write:
 //   * embedding lookup of MLX 4-bit affine rows (QEmbedding.lookup = mx.dequantize of the
 //     gathered rows, Q36/linear.py:680-690),
-//   * greedy token choice, the first index of each row's largest logit (mx.argmax of the
-//     log-probabilities, Q36/sampler.py:371-374; log-softmax is monotone, so the logits give
-//     the same index),
 //   * whole-page copies inside a layer's KV pool (the copy a sequence makes of a shared page
 //     before writing into it).
 #include "common.hpp"
@@ -39,68 +36,6 @@ __global__ __launch_bounds__(256) void embed_q4_kernel(const int32_t *__restrict
   }
 }
 
-// (value, index) order of the argmax: larger value first, then the lower index.  NaN never
-// wins against a number.
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-  return v > bv || (v == bv && i < bi) || (bv != bv && v == v);
-}
-
-// One 1024-thread workgroup per row: strided scan (8 logits a load when V % 8 == 0), then a
-// wave butterfly and one LDS step over the 16 waves.
-__global__ __launch_bounds__(1024) void argmax_rows_kernel(const uint16_t *__restrict__ logits, int V,
-                                                           int32_t *__restrict__ out) {
-  __shared__ float sv[16];
-  __shared__ int si[16];
-  const int b = blockIdx.x, t = threadIdx.x;
-  const uint16_t *row = logits + (long long)b * V;
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  if ((V & 7) == 0) {
-    for (int j = t; j < V / 8; j += 1024) {
-      const uint4 u = *(const uint4 *)(row + 8 * j);
-      const uint32_t ww[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float v = (i & 1) ? bf2f_hi(ww[i >> 1]) : bf2f(ww[i >> 1] & 0xffffu);
-        if (better(v, 8 * j + i, bv, bi)) {
-          bv = v;
-          bi = 8 * j + i;
-        }
-      }
-    }
-  } else {
-    for (int j = t; j < V; j += 1024) {
-      const float v = bf2f(row[j]);
-      if (better(v, j, bv, bi)) {
-        bv = v;
-        bi = j;
-      }
-    }
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = shfl_xor_f(bv, off);
-    const int oi = __shfl_xor(bi, off, 64);
-    if (better(ov, oi, bv, bi)) {
-      bv = ov;
-      bi = oi;
-    }
-  }
-  if ((t & 63) == 0) {
-    sv[t >> 6] = bv;
-    si[t >> 6] = bi;
-  }
-  __syncthreads();
-  if (t == 0) {
-    for (int w = 1; w < 16; w++)
-      if (better(sv[w], si[w], bv, bi)) {
-        bv = sv[w];
-        bi = si[w];
-      }
-    out[b] = bi < V ? bi : 0;  // (a row of NaNs only: index 0)
-  }
-}
-
 // Workgroup i copies page src[i] to page dst[i] of one layer's pool; page_words = 16-byte words
 // of a page (all kv heads' K and V).  A page id outside [0, num_pages) copies nothing.
 __global__ __launch_bounds__(256) void kv_copy_pages_kernel(uint4 *__restrict__ pool, const int32_t *__restrict__ src,
@@ -122,14 +57,6 @@ extern "C" int jit_embed_q4(const int32_t *ids, int B, const uint32_t *weight, c
   if (!ids || !weight || !scales || !biases || !out) return jit::fail(JIT_EINVAL, "embed_q4: null pointer");
   embed_q4_kernel<<<B, 256, 0, (hipStream_t)stream>>>(ids, weight, scales, biases, V, D, out);
   return jit::check_launch("jit_embed_q4");
-}
-
-extern "C" int jit_argmax_rows(const uint16_t *logits, int B, int V, int32_t *out, void *stream) {
-  if (B < 0 || V <= 0) return jit::fail(JIT_EINVAL, "argmax_rows: bad dims B=%d V=%d", B, V);
-  if (B == 0) return JIT_OK;
-  if (!logits || !out) return jit::fail(JIT_EINVAL, "argmax_rows: null pointer");
-  argmax_rows_kernel<<<B, 1024, 0, (hipStream_t)stream>>>(logits, V, out);
-  return jit::check_launch("jit_argmax_rows");
 }
 
 extern "C" int jit_kv_copy_pages(uint16_t *pool, int num_pages, int Hkv, const int32_t *src, const int32_t *dst,

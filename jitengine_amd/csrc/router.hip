@@ -8,30 +8,11 @@
 #pragma clang fp contract(off)
 
 #include "common.hpp"
+#include "fmath.hpp"
 
 namespace {
 
-// e^x for x <= 0: Cody-Waite reduction x = n ln2 + r with fdlibm's two-part ln2,
-// degree-7 Taylor polynomial of e^r in Horner form (|r| <= ln2/2), scaling by 2^n
-// through the exponent field; x <= -64 gives 0 so no subnormal is ever formed.
-__device__ __forceinline__ float exp_neg(float x) {
-  if (!(x > -64.0f)) return 0.0f;
-  const float t = x * 1.44269504088896341f;
-  const float n = __builtin_rintf(t);
-  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
-  r = __builtin_fmaf(-n, 1.42860682030941723e-6f, r);
-  float p = 1.98412698412698413e-4f;
-  p = __builtin_fmaf(p, r, 1.38888888888888889e-3f);
-  p = __builtin_fmaf(p, r, 8.33333333333333333e-3f);
-  p = __builtin_fmaf(p, r, 4.16666666666666667e-2f);
-  p = __builtin_fmaf(p, r, 1.66666666666666667e-1f);
-  p = __builtin_fmaf(p, r, 0.5f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  const int e = (int)n;
-  const float sc = __uint_as_float((uint32_t)(e + 127) << 23);
-  return p * sc;
-}
+using fmath::exp_neg;
 
 constexpr int kRowsPerBlock = 4;  // one wave64 per token row
 constexpr int kMaxN = 1024;

@@ -1,0 +1,494 @@
+// Token sampling over rows of bf16 logits for gfx950: log-probabilities, the greedy draw, and
+// temperature / top-p / top-k draws in mlx_lm's order (Q36/sampler.py:320-383), one 1024-thread
+// workgroup per row.
+//
+// Definitions (shared with the CPU restatement, oracle/jit_oracle.c):
+//   lse  = bf16(m0 + ln s), m0 = the row's largest logit, s = S 2^-42 rounded to fp32, where
+//          S = sum_i floor(e^(x_i - m0) 2^42) (an integer, so the order of the additions is free)
+//   lp_i = bf16(x_i - lse)                                   (logprobs_from_logits, :295-297)
+//   greedy: the first index of the largest lp                (mx.argmax, :373-374)
+//   sort order: ascending (lp, index), -0 tying +0           (the stable argsort, :458-459)
+//   top-p: cum_r = sum over sorted positions <= r of floor(bf16(e^lp) 2^42), survivor iff
+//          bf16(cum_r 2^-42) > bf16(1 - top_p)                (:460-462; apply_top_p :300-312)
+//   top-k: of the survivors, the k largest by (value desc, index asc)   (:463-469)
+//   x_i  = bf16(lp_i * bf16(1 / T)) over the kept, m = max x, W_i = floor(e^(x_i - m) 2^42)
+//   draw: C_i = sum_{j < i} W_j in vocabulary order, U = floor(u sum(W)), token = the last i
+//         with C_i <= U                                         (:470-476)
+// Every sum is an exact integer sum, so the histogram selection below reaches the bits of the
+// restatement's sort-based chain.  Where no token survives top-p (bf16 mass below 1 - top_p,
+// only for top_p under about 0.03) the greedy token is drawn.
+//
+// Selection without a sort: the bf16 log-probabilities are <= 0, so their magnitudes index a
+// 32,768-bin count histogram in LDS (128 KB); the cut points of top-p and top-k are found by
+// scans over the bins (the mass of a bin is its count times the bin value's weight).  Only the
+// tie group at the top-k / top-p cut needs the vocabulary order: its members' ranks come from a
+// counting pass.
+#include <cstring>
+
+#include "common.hpp"
+#include "fmath.hpp"
+
+namespace {
+
+using namespace fmath;
+
+constexpr int kThreads = 1024, kWaves = 16;
+constexpr int kStep = 512;        // values a wave covers per step: 64 lanes x 8
+constexpr int kKeys = 32768;      // histogram bins: the magnitudes of values <= 0
+constexpr int kBinsPerThread = kKeys / kThreads;
+constexpr int kMaxV = 1 << 20;    // 2^42-scaled sums of at most 2^20 terms stay below 2^62
+
+enum Mode { kLogprobs = 0, kGreedy = 1, kSample = 2 };
+
+struct SampleArgs {
+  const uint16_t *logits;
+  int V;
+  float inv_t, thr;  // bf16 values; thr > 0 turns top-p on
+  int k;             // 0: no top-k
+  const float *u;
+  int32_t *tok;
+  uint16_t *lp;
+};
+
+// ascending-order key of a log-probability (a bf16 value <= 0): 0x7fff - magnitude, so that
+// +0 and -0 tie at the top and -inf sits at 0x7f
+__device__ __forceinline__ int key_of(float lp) { return 0x7fff - (int)((__float_as_uint(lp) >> 16) & 0x7fffu); }
+__device__ __forceinline__ float value_of(int key) { return __uint_as_float((0x8000u | (uint32_t)(0x7fff - key)) << 16); }
+
+__device__ __forceinline__ float bf16r(float x) { return bf2f(f2bf(x)); }
+
+// ---- workgroup reductions and scans (every thread of the workgroup calls them) ----
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// inclusive prefix over the wave's lanes
+template <typename T>
+__device__ __forceinline__ T wave_incl(T v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const T n = __shfl_up(v, o, 64);
+    if (l >= o) v += n;
+  }
+  return v;
+}
+
+struct Shared {
+  float f[kWaves];
+  uint64_t q[kWaves];
+  uint64_t qx[kWaves];
+  int cut[8];
+};
+
+__device__ __forceinline__ float wg_max(float v, Shared &sh) {
+  v = wave_max(v);
+  __syncthreads();
+  if (lane_id() == 0) sh.f[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float m = sh.f[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; w++) m = fmaxf(m, sh.f[w]);
+  return m;
+}
+
+__device__ __forceinline__ uint64_t wg_sum(uint64_t v, Shared &sh) {
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane_id() == 0) sh.q[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint64_t s = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; w++) s += sh.q[w];
+  return s;
+}
+
+// exclusive prefix over the workgroup's threads in thread order (rev: in reverse thread order)
+template <bool kRev>
+__device__ __forceinline__ uint64_t wg_excl(uint64_t v, Shared &sh) {
+  const int t = kRev ? kThreads - 1 - (int)threadIdx.x : (int)threadIdx.x;
+  // kRev: lanes and waves are walked from the top, so the wave scan runs over the mirrored lane
+  // (a shuffle of lane 63 - l) and the wave totals are combined from the last wave down
+  uint64_t x = kRev ? __shfl(v, 63 - lane_id(), 64) : v;
+  const uint64_t inc = wave_incl(x);
+  __syncthreads();
+  if (lane_id() == 63) sh.qx[t >> 6] = inc;
+  __syncthreads();
+  uint64_t base = 0;
+  for (int w = 0; w < (t >> 6); w++) base += sh.qx[w];
+  const uint64_t ex = base + inc - x;
+  return kRev ? __shfl(ex, 63 - lane_id(), 64) : ex;
+}
+
+// ---- the row, a wave's contiguous range of it at a time ----
+// wave w covers [w R, min(V, (w + 1) R)), R a multiple of 8; step s of the wave covers 512
+// values, lane l the 8 consecutive ones from s + 8 l (kVec: one 16-byte load)
+struct Range {
+  int lo, hi;
+};
+
+__device__ __forceinline__ Range wave_range(int V) {
+  const int R = ((V + kWaves * 8 - 1) / (kWaves * 8)) * 8;
+  const int w = threadIdx.x >> 6;
+  return Range{min(V, w * R), min(V, (w + 1) * R)};
+}
+
+template <bool kVec>
+__device__ __forceinline__ int load8(const uint16_t *row, int i0, int hi, float v[8]) {
+  if (kVec) {
+    if (i0 >= hi) return 0;
+    const uint4 q = *(const uint4 *)(row + i0);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = (j & 1) ? bf2f_hi(w[j >> 1]) : bf2f(w[j >> 1] & 0xffffu);
+    return 8;
+  }
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    v[j] = (i0 + j < hi) ? bf2f(row[i0 + j]) : -INFINITY;
+    n += (i0 + j < hi);
+  }
+  return n;
+}
+
+template <bool kVec, typename F>
+__device__ __forceinline__ void for_each(const uint16_t *row, int V, F &&f) {
+  const Range r = wave_range(V);
+  for (int s = r.lo; s < r.hi; s += kStep) {
+    const int i0 = s + 8 * lane_id();
+    float v[8];
+    const int n = load8<kVec>(row, i0, r.hi, v);
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      if (j < n) f(i0 + j, v[j]);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void threefry_uniform_kernel(const uint32_t *__restrict__ keys, int B,
+                                                                    float *__restrict__ u) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  // Threefry-2x32 with 20 rounds (Salmon et al., SC'11; Random123): counter (0, 0) under the
+  // row's key; the draw's uniform is the first output word / 2^32, clamped below 1
+  const uint32_t k0 = keys[2 * b], k1 = keys[2 * b + 1];
+  const uint32_t ks[3] = {k0, k1, k0 ^ k1 ^ 0x1BD11BDAu};
+  const int rot[8] = {13, 15, 26, 6, 17, 29, 16, 24};
+  uint32_t x0 = ks[0], x1 = ks[1];
+#pragma unroll
+  for (int i = 0; i < 5; i++) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int r = rot[(i & 1) * 4 + q];
+      x0 += x1;
+      x1 = (x1 << r) | (x1 >> (32 - r));
+      x1 ^= x0;
+    }
+    x0 += ks[(i + 1) % 3];
+    x1 += ks[(i + 2) % 3] + (uint32_t)(i + 1);
+  }
+  u[b] = fminf((float)x0 / 4294967296.0f, 0x1.fffffep-1f);
+}
+
+template <int kMode, bool kVec>
+__global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs a) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x, t = threadIdx.x, l = lane_id();
+  const int V = a.V;
+  const uint16_t *row = a.logits + (long long)b * V;
+
+  // log-sum-exp: the largest logit, then the exact integer sum of the 2^42-scaled exponentials
+  float m0 = -INFINITY;
+  for_each<kVec>(row, V, [&](int, float x) { m0 = fmaxf(m0, x); });
+  m0 = wg_max(m0, sh);
+  uint64_t S = 0;
+  for_each<kVec>(row, V, [&](int, float x) { S += fix42(exp_neg(x - m0)); });
+  S = wg_sum(S, sh);
+  const float lse = bf16r(m0 + log_ge1(fix42_to_f32(S)));
+  const float lpmax = bf16r(m0 - lse);
+
+  if constexpr (kMode == kLogprobs) {
+    uint16_t *out = a.lp + (long long)b * V;
+    for_each<kVec>(row, V, [&](int i, float x) { out[i] = (uint16_t)f2bf(x - lse); });
+    return;
+  }
+
+  // the first index of the largest log-probability (lp is monotone in x: the indices with
+  // lp == lpmax are the x whose difference rounds to it)
+  auto first_max = [&]() {
+    uint64_t best = (uint64_t)V;
+    for_each<kVec>(row, V, [&](int i, float x) {
+      if (bf16r(x - lse) == lpmax && (uint64_t)i < best) best = (uint64_t)i;
+    });
+    // workgroup minimum through the sum slots (min of non-negative values)
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint64_t n = __shfl_xor(best, o, 64);
+      best = n < best ? n : best;
+    }
+    __syncthreads();
+    if (l == 0) sh.q[t >> 6] = best;
+    __syncthreads();
+    uint64_t m = sh.q[0];
+    for (int w = 1; w < kWaves; w++) m = sh.q[w] < m ? sh.q[w] : m;
+    return m < (uint64_t)V ? (int)m : 0;  // (a row without a number: 0)
+  };
+
+  if constexpr (kMode == kGreedy) {
+    const int i = first_max();
+    if (t == 0) a.tok[b] = i;
+    return;
+  }
+
+  if constexpr (kMode == kSample) {
+    __shared__ uint32_t hist[kKeys];
+    for (int j = t; j < kKeys; j += kThreads) hist[j] = 0u;
+    __syncthreads();
+    for_each<kVec>(row, V, [&](int, float x) { atomicAdd(&hist[key_of(bf16r(x - lse))], 1u); });
+    __syncthreads();
+
+    // thread t owns the bins [32 t, 32 t + 32)
+    const int k0 = t * kBinsPerThread;
+    auto mass_of = [&](int key) { return fix42(bf16r(exp_neg(value_of(key)))); };
+
+    // top-p: the boundary bin key_p and the number j0 of its (lowest-index) members cut
+    const bool topp = a.thr > 0.0f;
+    if (t == 0) {
+      sh.cut[0] = topp ? -1 : 0;  // key_p (no top-p: every bin survives, from key 0)
+      sh.cut[1] = 0;              // j0
+    }
+    if (topp) {
+      uint64_t mass = 0;
+      for (int j = 0; j < kBinsPerThread; j++) {
+        const uint32_t c = hist[k0 + j];
+        if (c) mass += (uint64_t)c * mass_of(k0 + j);
+      }
+      uint64_t cb = wg_excl<false>(mass, sh);  // (its barriers order the writes above)
+      for (int j = 0; j < kBinsPerThread; j++) {
+        const uint32_t c = hist[k0 + j];
+        if (!c) continue;
+        const uint64_t F = mass_of(k0 + j), ce = cb + (uint64_t)c * F;
+        if (fix42_to_bf16(cb) <= a.thr && fix42_to_bf16(ce) > a.thr) {
+          // the smallest j0 whose member (rank j0, cum cb + (j0 + 1) F) survives
+          uint32_t lo = 0, hi = c - 1;
+          while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (fix42_to_bf16(cb + (uint64_t)(mid + 1) * F) > a.thr) hi = mid;
+            else lo = mid + 1;
+          }
+          sh.cut[0] = k0 + j;
+          sh.cut[1] = (int)lo;
+        }
+        cb = ce;
+      }
+    }
+    __syncthreads();
+    const int key_p = sh.cut[0], j0 = sh.cut[1];
+    if (key_p < 0) {  // nothing survives top-p: the greedy token
+      const int i = first_max();
+      if (t == 0) a.tok[b] = i;
+      return;
+    }
+    auto surv = [&](int key, uint32_t c) -> uint32_t {
+      return key > key_p ? c : (key == key_p ? c - (uint32_t)j0 : 0u);
+    };
+
+    // the kept set: keys above key_t, and the members of key_t's group of rank [r_lo, r_hi)
+    uint64_t nt = 0;
+    for (int j = 0; j < kBinsPerThread; j++) nt += surv(k0 + j, hist[k0 + j]);
+    const uint64_t n_surv = wg_sum(nt, sh);
+    if (t == 0) {
+      sh.cut[2] = key_p;                    // key_t
+      sh.cut[3] = j0;                       // r_lo
+      sh.cut[4] = (int)hist[key_p];         // r_hi
+    }
+    if (a.k > 0 && n_surv > (uint64_t)a.k) {
+      uint64_t above = wg_excl<true>(nt, sh);  // survivors in the bins of the threads above
+      for (int j = kBinsPerThread - 1; j >= 0; j--) {
+        const uint32_t s = surv(k0 + j, hist[k0 + j]);
+        if (above < (uint64_t)a.k && (uint64_t)a.k <= above + s) {
+          const int lo = (k0 + j == key_p) ? j0 : 0;
+          sh.cut[2] = k0 + j;
+          sh.cut[3] = lo;
+          sh.cut[4] = lo + (a.k - (int)above);
+        }
+        above += s;
+      }
+    }
+    __syncthreads();
+    const int key_t = sh.cut[2], r_lo = sh.cut[3], r_hi = sh.cut[4];
+    const bool partial = r_lo > 0 || r_hi < (int)hist[key_t];
+    const float m = bf16r(lpmax * a.inv_t);
+
+    // ranks of key_t's members: the members in the waves below
+    uint32_t tie_base = 0;
+    if (partial) {
+      uint64_t n = 0;
+      for_each<kVec>(row, V, [&](int, float x) { n += key_of(bf16r(x - lse)) == key_t; });
+      n = wave_sum(n);
+      __syncthreads();
+      if (l == 0) sh.q[t >> 6] = n;
+      __syncthreads();
+      for (int w = 0; w < (t >> 6); w++) tie_base += (uint32_t)sh.q[w];
+    }
+
+    // one pass over the wave's range in vocabulary order: each value's weight, with the rank
+    // of key_t's members running along; `f(i, W)` sees every value, `g(step_total)` each step
+    auto weights = [&](auto &&f) {
+      const Range r = wave_range(V);
+      uint32_t carry = tie_base;
+      for (int s = r.lo; s < r.hi; s += kStep) {
+        const int i0 = s + 8 * l;
+        float v[8];
+        const int n = load8<kVec>(row, i0, r.hi, v);
+        int key[8];
+        uint32_t ties = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          key[j] = j < n ? key_of(bf16r(v[j] - lse)) : -1;
+          ties += key[j] == key_t;
+        }
+        const uint32_t tincl = partial ? wave_incl(ties) : 0u;
+        uint32_t rank = carry + tincl - ties;
+        uint64_t W[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          bool kept = key[j] > key_t;
+          if (key[j] == key_t) {
+            kept = !partial || ((int)rank >= r_lo && (int)rank < r_hi);
+            rank++;
+          }
+          W[j] = kept ? fix42(exp_neg(bf16r(bf16r(v[j] - lse) * a.inv_t) - m)) : 0ull;
+        }
+        if (partial) carry += __shfl(tincl, 63, 64);
+        f(i0, W);
+      }
+    };
+
+    uint64_t tw = 0;
+    weights([&](int, const uint64_t *W) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) tw += W[j];
+    });
+    tw = wave_sum(tw);
+    __syncthreads();
+    if (l == 0) sh.q[t >> 6] = tw;
+    __syncthreads();
+    uint64_t base = 0, total = 0;
+    for (int w = 0; w < kWaves; w++) {
+      if (w < (t >> 6)) base += sh.q[w];
+      total += sh.q[w];
+    }
+    float u = a.u[b];
+    u = fminf(fmaxf(u, 0.0f), 0x1.fffffep-1f);  // (NaN -> 0)
+    const uint64_t U = mul_u32_u64_hi((uint64_t)(u * 4294967296.0f), total);
+
+    // the number of i with C_i <= U, wave by wave: a wave whose values all lie at or below U
+    // counts its range, one above U none, and the one wave that holds U walks its range
+    const Range r = wave_range(V);
+    uint64_t cnt = 0;
+    if (base + tw <= U) {
+      cnt = l == 0 ? (uint64_t)(r.hi - r.lo) : 0ull;
+    } else if (base <= U) {
+      uint64_t run = base;
+      weights([&](int i0, const uint64_t *W) {
+        uint64_t lt = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) lt += W[j];
+        const uint64_t incl = wave_incl(lt);
+        uint64_t c = run + incl - lt;  // C of the lane's first value
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          if (i0 + j < r.hi && c <= U) cnt++;
+          c += W[j];
+        }
+        run += __shfl(incl, 63, 64);
+      });
+    }
+    const uint64_t count = wg_sum(cnt, sh);
+    if (t == 0) a.tok[b] = (int32_t)(count - 1);
+  }
+}
+
+int check_rows(const char *what, const void *logits, int B, int V, const void *out) {
+  if (B < 0 || V <= 0) return jit::fail(JIT_EINVAL, "%s: bad dims B=%d V=%d", what, B, V);
+  if (V > kMaxV) return jit::fail(JIT_EUNSUPPORTED, "%s covers V <= %d, got %d", what, kMaxV, V);
+  if (B > 0 && (!logits || !out)) return jit::fail(JIT_EINVAL, "%s: null pointer", what);
+  return JIT_OK;
+}
+
+template <int kMode>
+int launch(const SampleArgs &a, int B, void *stream) {
+  if ((a.V & 7) == 0 && ((uintptr_t)a.logits & 15) == 0)
+    sample_rows_kernel<kMode, true><<<B, kThreads, 0, (hipStream_t)stream>>>(a);
+  else
+    sample_rows_kernel<kMode, false><<<B, kThreads, 0, (hipStream_t)stream>>>(a);
+  return jit::check_launch("jit_sample_rows");
+}
+
+// bf16 round trip of a float on the host (round to nearest even)
+float host_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return f;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  float r;
+  memcpy(&r, &u, 4);
+  return r;
+}
+
+}  // namespace
+
+extern "C" int jit_logprobs_rows(const uint16_t *logits, int B, int V, uint16_t *lp, void *stream) {
+  if (int rc = check_rows("logprobs_rows", logits, B, V, lp)) return rc;
+  if (B == 0) return JIT_OK;
+  SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, nullptr, lp};
+  return launch<kLogprobs>(a, B, stream);
+}
+
+extern "C" int jit_argmax_rows(const uint16_t *logits, int B, int V, int32_t *out, void *stream) {
+  if (int rc = check_rows("argmax_rows", logits, B, V, out)) return rc;
+  if (B == 0) return JIT_OK;
+  SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, out, nullptr};
+  return launch<kGreedy>(a, B, stream);
+}
+
+extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temperature, double top_p, int top_k,
+                               const float *u, int32_t *tokens, void *stream) {
+  if (int rc = check_rows("sample_rows", logits, B, V, tokens)) return rc;
+  if (!(temperature == temperature) || !(top_p == top_p) || top_k < 0)
+    return jit::fail(JIT_EINVAL, "sample_rows: bad settings T=%g top_p=%g top_k=%d", temperature, top_p, top_k);
+  if (B == 0) return JIT_OK;
+  if (temperature <= 0.0) {
+    SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, tokens, nullptr};
+    return launch<kGreedy>(a, B, stream);
+  }
+  if (!u) return jit::fail(JIT_EINVAL, "sample_rows: null uniforms");
+  // the settings as the reference's scalars reach its bf16 arrays: a Python float, then fp32,
+  // then bf16 (Q36/sampler.py:381, 462, 470)
+  const float inv_t = host_bf16((float)(1.0 / temperature));
+  const float thr = (top_p > 0.0 && top_p < 1.0) ? host_bf16((float)(1.0 - top_p)) : 0.0f;
+  if (!(inv_t > 0.0f) || !(inv_t < INFINITY))
+    return jit::fail(JIT_EUNSUPPORTED, "sample_rows: 1 / T = %g is not a finite positive bf16", 1.0 / temperature);
+  const int k = top_k >= V ? 0 : top_k;
+  SampleArgs a{logits, V, inv_t, thr, k, u, tokens, nullptr};
+  return launch<kSample>(a, B, stream);
+}
+
+extern "C" int jit_threefry_uniform(const uint32_t *keys, int B, float *u, void *stream) {
+  if (B < 0) return jit::fail(JIT_EINVAL, "threefry_uniform: B=%d", B);
+  if (B == 0) return JIT_OK;
+  if (!keys || !u) return jit::fail(JIT_EINVAL, "threefry_uniform: null pointer");
+  threefry_uniform_kernel<<<(B + 255) / 256, 256, 0, (hipStream_t)stream>>>(keys, B, u);
+  return jit::check_launch("jit_threefry_uniform");
+}

@@ -610,13 +610,54 @@ def embed_q4(ids: torch.Tensor, table: QLinear) -> torch.Tensor:
     return out
 
 
+def logprobs_rows(logits: torch.Tensor) -> torch.Tensor:
+    """bf16 [B, V]: lp = bf16(x - lse) per row with lse = bf16(m0 + ln(S 2^-42)), S the exact
+    integer sum of floor(e^(x - m0) 2^42) (logprobs_from_logits, Q36/sampler.py:295-297)."""
+    _need(logits, torch.bfloat16, "logits")
+    B, V = logits.shape
+    out = torch.empty_like(logits)
+    _lib.check(_lib.lib().jit_logprobs_rows(_p(logits), B, V, _p(out), _stream()), "logprobs_rows")
+    return out
+
+
 def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
-    """int32 [B]: the first index of each row's largest logit (the greedy draw of
+    """int32 [B]: the first index of each row's largest log-probability (the greedy draw,
     Q36/sampler.py:371-374)."""
     _need(logits, torch.bfloat16, "logits")
     B, V = logits.shape
     out = torch.empty(B, dtype=torch.int32, device=logits.device)
     _lib.check(_lib.lib().jit_argmax_rows(_p(logits), B, V, _p(out), _stream()), "argmax_rows")
+    return out
+
+
+def sample_rows(logits: torch.Tensor, temperature: float, top_p: float, top_k: int,
+                u: torch.Tensor | None) -> torch.Tensor:
+    """int32 [B]: one draw per row of bf16 logits [B, V] under shared settings, given fp32
+    uniforms u [B] (Sampler._sample_exact_full / sample_rows, Q36/sampler.py:451-476, 486-543;
+    the definitions are jit_sample_rows'); temperature <= 0 is the greedy draw."""
+    _need(logits, torch.bfloat16, "logits")
+    B, V = logits.shape
+    if temperature > 0:
+        if u is None:
+            raise ValueError("sample_rows needs uniforms when temperature > 0")
+        _need(u, torch.float32, "u")
+        if u.shape != (B,):
+            raise ValueError(f"u must be [{B}], got {tuple(u.shape)}")
+    out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    _lib.check(_lib.lib().jit_sample_rows(_p(logits), B, V, float(temperature), float(top_p), int(top_k),
+                                          _p(u) if u is not None else None, _p(out), _stream()), "sample_rows")
+    return out
+
+
+def threefry_uniform(keys: torch.Tensor) -> torch.Tensor:
+    """fp32 [B]: the uniform of each uint32 key pair (keys [B, 2] as int32 bits): the first word
+    of Threefry-2x32-20 at counter (0, 0), / 2^32, clamped below 1 (Sampler.uniform,
+    Q36/sampler.py:367-369)."""
+    _need(keys, torch.int32, "keys")
+    if keys.dim() != 2 or keys.shape[1] != 2:
+        raise ValueError("keys must be [B, 2]")
+    out = torch.empty(keys.shape[0], dtype=torch.float32, device=keys.device)
+    _lib.check(_lib.lib().jit_threefry_uniform(_p(keys), keys.shape[0], _p(out), _stream()), "threefry_uniform")
     return out
 
 

@@ -65,6 +65,15 @@ def lib():
         _LIB.jo_exp_pos.restype = ctypes.c_float
         _LIB.jo_exp_pos.argtypes = [ctypes.c_float]
         _LIB.jo_num_threads.restype = _I
+        _LIB.jo_log_ge1.restype = ctypes.c_float
+        _LIB.jo_log_ge1.argtypes = [ctypes.c_float]
+        _LIB.jo_fix42_to_bf16.restype = ctypes.c_float
+        _LIB.jo_fix42_to_bf16.argtypes = [ctypes.c_uint64]
+        _LIB.jo_sample_rows.argtypes = [_P, _I, _I, ctypes.c_double, ctypes.c_double, _I, _P, _P, _P]
+        _LIB.jo_threefry2x32.argtypes = [_P, _P, _P]
+        _LIB.jo_threefry2x32.restype = None
+        _LIB.jo_threefry_uniform.argtypes = [_P, _I, _P]
+        _LIB.jo_threefry_uniform.restype = None
     return _LIB
 
 
@@ -475,14 +484,58 @@ def embed_q4(ids, w, s, b) -> np.ndarray:
     return out
 
 
+def log_ge1(s: float) -> float:
+    """ln s for s >= 1 (the build's own fp32 sequence, shared with the GPU)."""
+    return float(lib().jo_log_ge1(ctypes.c_float(s)))
+
+
+def fix42_to_bf16(c: int) -> float:
+    """c 2^-42 rounded once (nearest even) to bf16."""
+    return float(lib().jo_fix42_to_bf16(ctypes.c_uint64(c)))
+
+
+def logprobs_rows(logits) -> np.ndarray:
+    """bf16 [B, V]: lp = bf16(x - lse), lse = bf16(m0 + ln(S 2^-42)), S = sum floor(e^(x - m0)
+    2^42) (logprobs_from_logits, Q36/sampler.py:295-297)."""
+    x = np.ascontiguousarray(_u16(logits))
+    B, V = x.shape
+    out = np.empty_like(x)
+    _check(lib().jo_logprobs_rows(_p(x), B, V, _p(out)), "logprobs_rows")
+    return out
+
+
+def sample_rows(logits, temperature: float, top_p: float, top_k: int, u=None, weights: bool = False):
+    """int32 [B]: Sampler._sample_exact_full's draw per row (Q36/sampler.py:451-476) given fp32
+    uniforms u [B]; temperature <= 0 is the greedy draw (the first index of the largest lp).
+    weights=True also returns the rows' integer weights W [B, V] (uint64, 2^42-scaled)."""
+    x = np.ascontiguousarray(_u16(logits))
+    B, V = x.shape
+    uu = np.zeros(B, np.float32) if u is None else np.ascontiguousarray(np.asarray(u, np.float32))
+    out = np.zeros(B, np.int32)
+    w = np.zeros((B, V), np.uint64) if weights else None
+    _check(lib().jo_sample_rows(_p(x), B, V, float(temperature), float(top_p), int(top_k), _p(uu), _p(out),
+                                _p(w) if weights else None), "sample_rows")
+    return (out, w) if weights else out
+
+
 def argmax_rows(logits) -> np.ndarray:
-    """int32 [B]: the first index of each row's largest bf16 logit (the greedy draw,
-    Q36/sampler.py:371-374); NaN entries never win, a row of NaNs gives 0."""
-    x = bf16_to_f32(_u16(logits)).astype(np.float64)
-    out = np.zeros(x.shape[0], np.int32)
-    for r in range(x.shape[0]):
-        ok = ~np.isnan(x[r])
-        if ok.any():
-            m = x[r][ok].max()
-            out[r] = int(np.flatnonzero(ok & (x[r] == m))[0])
+    """int32 [B]: the greedy draw, the first index of each row's largest log-probability
+    (Sampler.__call__ with temperature 0, Q36/sampler.py:371-374)."""
+    return sample_rows(logits, 0.0, 1.0, 0)
+
+
+def threefry2x32(key, ctr) -> tuple:
+    """Threefry-2x32-20 of one counter pair under one key pair (uint32 values)."""
+    k = np.asarray(key, np.uint32)
+    c = np.asarray(ctr, np.uint32)
+    out = np.zeros(2, np.uint32)
+    lib().jo_threefry2x32(_p(k), _p(c), _p(out))
+    return int(out[0]), int(out[1])
+
+
+def threefry_uniform(keys) -> np.ndarray:
+    """fp32 [B]: min(fp32(threefry(key, (0, 0))[0]) / 2^32, 1 - 2^-24) per key pair [B, 2]."""
+    k = np.ascontiguousarray(np.asarray(keys, np.uint32).reshape(-1, 2))
+    out = np.zeros(k.shape[0], np.float32)
+    lib().jo_threefry_uniform(_p(k), k.shape[0], _p(out))
     return out

@@ -890,3 +890,224 @@ int jo_q4_prepack(const uint32_t *w, const uint16_t *s, const uint16_t *b, int E
       }
   return JO_OK;
 }
+
+/* ---------------------------------------------------------- f.4 sampler
+ * Token sampling in mlx_lm's order (Q36/sampler.py): logprobs_from_logits
+ * (:295-297), the greedy draw (Sampler.__call__, :371-374) and
+ * _sample_exact_full (:451-476), which is bit for bit the stock chain
+ * (apply_top_p :300-312, apply_top_k :315-318, categorical), restated with
+ * the reference's own steps: one stable ascending argsort, the top-p mask on
+ * the cumulative mass, the top-k cut v = sv[n-k] / above / first /
+ * cut = first + (k - above), x = bf16(sv * bf16(1/T)), w = exp(x - max),
+ * exclusive cumulative weights in vocabulary order and count(cdf <= u sum) - 1.
+ * The fp32 reductions whose association MLX fixes inside its kernels
+ * (logsumexp's sum, the cumsums, sum(w)) are exact integer sums of 2^42-scaled
+ * terms here (the GPU path adds in another order and must reach the same
+ * bits); exp is jo_exp_neg and ln is jo_log_ge1 (Metal's bits are not
+ * reproducible here).  Where no position survives top_p the greedy token is
+ * drawn (the reference's windowed and full chains disagree there).
+ */
+
+/* ln s for 1 <= s: s = 2^k f, f in [sqrt(1/2), sqrt(2)], ln f = 2 atanh(z),
+ * z = (f - 1) / (f + 1), by the odd series through z^11 (Horner on z^2), then
+ * k ln2 + ln f with one fused multiply-add. */
+float jo_log_ge1(float s) {
+  uint32_t u;
+  memcpy(&u, &s, 4);
+  int k = (int)((u >> 23) & 0xffu) - 127;
+  const uint32_t fu = (u & 0x007fffffu) | 0x3f800000u;
+  float f;
+  memcpy(&f, &fu, 4);
+  if (f > 1.41421356f) {
+    f = f * 0.5f;
+    k += 1;
+  }
+  const float z = (f - 1.0f) / (f + 1.0f);
+  const float z2 = z * z;
+  float p = 9.09090909090909091e-2f;
+  p = fmaf(p, z2, 1.11111111111111111e-1f);
+  p = fmaf(p, z2, 1.42857142857142857e-1f);
+  p = fmaf(p, z2, 2.0e-1f);
+  p = fmaf(p, z2, 3.33333333333333333e-1f);
+  p = fmaf(p, z2, 1.0f);
+  const float lf = (z + z) * p;
+  return fmaf((float)k, 0.693147182464599609375f, lf);
+}
+
+static inline uint64_t fix42(float w) { return (uint64_t)(w * 0x1p42f); }
+
+/* c rounded to nearest even at `bits` significant bits, times 2^scale_exp */
+static float u64_round(uint64_t c, int bits, int scale_exp) {
+  if (c == 0) return 0.0f;
+  const int e = 63 - __builtin_clzll(c);
+  int sh = e - (bits - 1);
+  uint64_t m = c;
+  if (sh > 0) {
+    const uint64_t rem = c & ((1ull << sh) - 1), half = 1ull << (sh - 1);
+    m = c >> sh;
+    if (rem > half || (rem == half && (m & 1))) m++;
+  } else {
+    sh = 0;
+  }
+  return ldexpf((float)m, sh + scale_exp);
+}
+
+float jo_fix42_to_bf16(uint64_t c) { return u64_round(c, 8, -42); }
+
+/* lse of one row: bf16(m0 + ln(S 2^-42 rounded to fp32)), S = sum floor(e^(x - m0) 2^42) */
+static float row_lse(const uint16_t *x, int V) {
+  float m0 = -INFINITY;
+  for (int i = 0; i < V; i++) m0 = fmaxf(m0, bf2f(x[i]));
+  uint64_t S = 0;
+  for (int i = 0; i < V; i++) S += fix42(jo_exp_neg(bf2f(x[i]) - m0));
+  return bf2f(f2bf(m0 + jo_log_ge1(u64_round(S, 24, -42))));
+}
+
+int jo_logprobs_rows(const uint16_t *x, int B, int V, uint16_t *lp) {
+  if (B < 0 || V <= 0) return JO_EINVAL;
+  for (int b = 0; b < B; b++) {
+    const uint16_t *r = x + (size_t)b * V;
+    const float lse = row_lse(r, V);
+    for (int i = 0; i < V; i++) lp[(size_t)b * V + i] = f2bf(bf2f(r[i]) - lse);
+  }
+  return JO_OK;
+}
+
+typedef struct {
+  float v;
+  int i;
+} jo_vi;
+
+static int cmp_vi(const void *a, const void *b) {
+  const jo_vi *p = (const jo_vi *)a, *q = (const jo_vi *)b;
+  if (p->v < q->v) return -1;
+  if (p->v > q->v) return 1;
+  return (p->i > q->i) - (p->i < q->i);
+}
+
+/* the first index of the largest value; NaN never wins, a row without a number gives 0 */
+static int first_max(const float *lp, int V) {
+  int best = -1;
+  for (int i = 0; i < V; i++)
+    if (lp[i] == lp[i] && (best < 0 || lp[i] > lp[best])) best = i;
+  return best < 0 ? 0 : best;
+}
+
+/* temperature <= 0: greedy.  u: [B] uniforms (clamped to [0, 1 - 2^-24]).
+ * w_out (optional, [B, V]): each row's integer weights W in vocabulary order
+ * (all 0 for a greedy or degenerate row). */
+int jo_sample_rows(const uint16_t *x, int B, int V, double temperature, double top_p, int top_k,
+                   const float *u, int32_t *tok, uint64_t *w_out) {
+  if (B < 0 || V <= 0 || top_k < 0) return JO_EINVAL;
+  const int greedy = !(temperature > 0.0);
+  const float inv_t = greedy ? 0.0f : bf2f(f2bf((float)(1.0 / temperature)));
+  const int topp = top_p > 0.0 && top_p < 1.0;
+  const float thr = topp ? bf2f(f2bf((float)(1.0 - top_p))) : 0.0f;
+  const int k = top_k >= V ? 0 : top_k;
+  float *lp = (float *)malloc(sizeof(float) * V), *sv = (float *)malloc(sizeof(float) * V);
+  jo_vi *s = (jo_vi *)malloc(sizeof(jo_vi) * V);
+  uint64_t *W = (uint64_t *)malloc(sizeof(uint64_t) * V);
+  if (!lp || !sv || !s || !W) {
+    free(lp); free(sv); free(s); free(W);
+    return JO_ENOMEM;
+  }
+  for (int b = 0; b < B; b++) {
+    const uint16_t *r = x + (size_t)b * V;
+    const float lse = row_lse(r, V);
+    for (int i = 0; i < V; i++) lp[i] = bf2f(f2bf(bf2f(r[i]) - lse));
+    if (w_out) memset(w_out + (size_t)b * V, 0, sizeof(uint64_t) * V);
+    if (greedy) {
+      tok[b] = first_max(lp, V);
+      continue;
+    }
+    /* idx = argsort(lp) (stable, ascending), sv = lp[idx] */
+    for (int i = 0; i < V; i++) {
+      s[i].v = lp[i];
+      s[i].i = i;
+    }
+    qsort(s, V, sizeof(jo_vi), cmp_vi);
+    for (int p = 0; p < V; p++) sv[p] = s[p].v;
+    /* top-p: cum = cumsum(exp(sv)) over bf16 exponentials; sv = where(cum > thr, sv, -inf) */
+    if (topp) {
+      uint64_t cum = 0;
+      for (int p = 0; p < V; p++) {
+        cum += fix42(bf2f(f2bf(jo_exp_neg(sv[p]))));
+        if (!(u64_round(cum, 8, -42) > thr)) sv[p] = -INFINITY;
+      }
+    }
+    if (!(sv[V - 1] > -INFINITY)) {  /* nothing survived top-p */
+      tok[b] = first_max(lp, V);
+      continue;
+    }
+    /* top-k: v = sv[n-k]; keep sv > v, or sv == v at positions < first + (k - above) */
+    if (k > 0) {
+      const float v = sv[V - k];
+      int above = 0, first = 0;
+      for (int p = 0; p < V; p++) {
+        above += sv[p] > v;
+        first += sv[p] < v;
+      }
+      const int cut = first + (k - above);
+      for (int p = 0; p < V; p++)
+        if (!(sv[p] > v || (sv[p] == v && p < cut))) sv[p] = -INFINITY;
+    }
+    /* x = put_along_axis(zeros, idx, sv) * inv_t in bf16, then fp32; w = exp(x - max x) */
+    float m = -INFINITY;
+    for (int p = 0; p < V; p++) {
+      sv[p] = bf2f(f2bf(sv[p] * inv_t));
+      m = fmaxf(m, sv[p]);
+    }
+    for (int p = 0; p < V; p++) W[s[p].i] = fix42(jo_exp_neg(sv[p] - m));
+    /* cdf = exclusive cumsum in vocabulary order; token = count(cdf <= u * sum) - 1 */
+    uint64_t T = 0;
+    for (int i = 0; i < V; i++) T += W[i];
+    if (w_out) memcpy(w_out + (size_t)b * V, W, sizeof(uint64_t) * V);
+    float uu = u[b];
+    uu = fminf(fmaxf(uu, 0.0f), 0x1.fffffep-1f);
+    const uint64_t A = (uint64_t)(uu * 4294967296.0f);
+    const uint64_t U = A * (T >> 32) + ((A * (T & 0xffffffffull)) >> 32);
+    uint64_t C = 0;
+    int count = 0;
+    for (int i = 0; i < V; i++) {
+      count += C <= U;
+      C += W[i];
+    }
+    tok[b] = count - 1;
+  }
+  free(lp); free(sv); free(s); free(W);
+  return JO_OK;
+}
+
+/* Threefry-2x32 with 20 rounds (Salmon, Moraes, Dror, Shaw, "Parallel random
+ * numbers: as easy as 1, 2, 3", SC'11; the Random123 library): rotation
+ * constants 13 15 26 6 17 29 16 24, key-schedule parity 0x1BD11BDA, a key
+ * injection after every 4 rounds.  MLX's random bits use it (the reference's
+ * replay, Q36/sampler.py:160-177). */
+void jo_threefry2x32(const uint32_t *key, const uint32_t *ctr, uint32_t *out) {
+  static const int rot[8] = {13, 15, 26, 6, 17, 29, 16, 24};
+  const uint32_t ks[3] = {key[0], key[1], key[0] ^ key[1] ^ 0x1BD11BDAu};
+  uint32_t x0 = ctr[0] + ks[0], x1 = ctr[1] + ks[1];
+  for (int i = 0; i < 5; i++) {
+    for (int q = 0; q < 4; q++) {
+      const int r = rot[(i & 1) * 4 + q];
+      x0 += x1;
+      x1 = (x1 << r) | (x1 >> (32 - r));
+      x1 ^= x0;
+    }
+    x0 += ks[(i + 1) % 3];
+    x1 += ks[(i + 2) % 3] + (uint32_t)(i + 1);
+  }
+  out[0] = x0;
+  out[1] = x1;
+}
+
+/* u[b] = min(fp32(y0) / 2^32, 1 - 2^-24), y = threefry(keys[b], (0, 0)):
+ * mx.random.uniform(shape=(1,), key) (Sampler.uniform, Q36/sampler.py:367-369). */
+void jo_threefry_uniform(const uint32_t *keys, int B, float *u) {
+  const uint32_t zero[2] = {0u, 0u};
+  for (int b = 0; b < B; b++) {
+    uint32_t y[2];
+    jo_threefry2x32(keys + 2 * b, zero, y);
+    u[b] = fminf((float)y[0] / 4294967296.0f, 0x1.fffffep-1f);
+  }
+}

@@ -147,3 +147,30 @@ def assert_attention_parity(got_u16: np.ndarray, exact: np.ndarray, stock_u16: n
                                f"arithmetic's {e_stock[bad[0]]:.3g}")
         out["err_vs_stock"] = float((e_got / np.maximum(e_stock, 1e-300)).max())
     return out
+
+
+def sampler_logits(kind: int, B: int, V: int, seed: int, scale: float = 1.0) -> np.ndarray:
+    """bf16 [B, V] logit rows of the reference's sampler checks (Q36/sampler.py:546-604 and
+    Q36T/metal/test_sampler.py): 0 normal * 3, 1 integers in [-3, 3) (heavy ties), 2 all equal,
+    3 sparse spikes of 4, 4 three confident tokens (+30), 5 normal * 0.3, 6 normal * scale rounded
+    to halves (ties), 7 normal * scale with a tenth of the entries at -inf."""
+    rng = np.random.default_rng(seed)
+    n = rng.standard_normal((B, V)).astype(np.float32)
+    if kind == 0:
+        x = n * 3
+    elif kind == 1:
+        x = rng.integers(-3, 3, (B, V)).astype(np.float32)
+    elif kind == 2:
+        x = np.zeros((B, V), np.float32)
+    elif kind == 3:
+        x = (rng.random((B, V)) < 0.001).astype(np.float32) * 4
+    elif kind == 4:
+        x = n + 30 * (np.arange(V) < 3)[None, :]
+    elif kind == 5:
+        x = n * 0.3
+    elif kind == 6:
+        x = np.round(n * scale * 2) / 2
+    else:
+        x = n * scale
+        x[rng.random((B, V)) < 0.1] = -np.inf
+    return f32_to_bf16(x.astype(np.float32))
