@@ -1,4 +1,4 @@
-"""Continuous-batching generation over the paged KV pool (greedy draws).
+"""Continuous-batching generation over the paged KV pool.
 
 Mirrors the reference's scheduler loop (Q36/scheduler/scheduler.py, admission.py, prefill.py,
 decode.py, retire.py) on this build's pieces:
@@ -22,7 +22,10 @@ decode.py, retire.py) on this build's pieces:
     positions known on the host -- before this step's tokens are read, so the host's bookkeeping
     overlaps the GPU's step; a row that stops on an end-of-sequence token costs one discarded step,
     as in the reference.
-Tokens are drawn greedily on the GPU (jit_argmax_rows).
+Tokens are drawn on the GPU by each request's Sampler (DecodingMixin._draw, Q36/scheduler/decode.py:116-
+176): greedy (jit_argmax_rows) or temperature / top-p / top-k under the request's own key stream
+(jit_sample_rows), the rows of equal settings in one launch, each drawing token n with its step-n
+key, so a request's tokens do not depend on the batch.
 """
 
 from __future__ import annotations
@@ -37,6 +40,7 @@ import torch
 from .kvpool import KVPool, PoolExhausted, PrefixStore, pages_for
 from .ops import PAGE
 from .model import CausalLM, make_mixed_state, make_step_state
+from .sampler import Sampler, sample_rows
 
 
 @dataclass
@@ -51,6 +55,7 @@ class Request:
     state: str = "queued"  # queued -> prefill -> decode -> done
     finish_reason: str | None = None
     reserved: int = 0      # pages charged at admission and not yet allocated
+    sampler: Sampler | None = None  # (None: greedy)
 
     @property
     def length(self) -> int:
@@ -59,7 +64,7 @@ class Request:
 
 
 class Engine:
-    """Requests in, greedy tokens out, many sequences per step over one KV pool."""
+    """Requests in, tokens out, many sequences per step over one KV pool."""
 
     def __init__(self, lm: CausalLM, num_pages: int, prefill_chunk: int = 512, max_step_tokens: int = 2048,
                  prefix_store: bool = True, page_seed: int | None = None, device=None, allocate: bool = True,
@@ -87,7 +92,10 @@ class Engine:
         self._ids = itertools.count()
 
     # ------------------------------------------------------------------ requests
-    def submit(self, prompt, max_tokens: int, eos=None) -> Request:
+    def submit(self, prompt, max_tokens: int, eos=None, temperature: float = 0.0, top_p: float | None = None,
+               top_k: int | None = None, seed: int | None = None) -> Request:
+        """Queue a request; temperature > 0 samples with top_p / top_k under `seed`'s key stream
+        (Sampler, Q36/scheduler/admission.py:104-113), else its tokens are greedy."""
         prompt = [int(t) for t in prompt]
         if not prompt:
             raise ValueError("empty prompt")
@@ -100,7 +108,8 @@ class Engine:
             raise PoolExhausted(f"a generation of {len(prompt) + max_tokens} positions needs {need} pages, "
                                 f"the pool has {self.pool.num_pages}")
         eos = frozenset(self.lm.eos_ids if eos is None else eos)
-        r = Request(next(self._ids), prompt, int(max_tokens), eos)
+        r = Request(next(self._ids), prompt, int(max_tokens), eos,
+                    sampler=Sampler(temperature, top_p, top_k, seed, int(max_tokens), self.lm.vocab))
         self.queue.append(r)
         return r
 
@@ -155,13 +164,35 @@ class Engine:
         self.rows.remove(r)
 
     # ---------------------------------------------------------------------- step
-    def _issue_decode(self, rows: list, ids, pos: np.ndarray) -> torch.Tensor:
-        """Launch one batched decode step over `rows` (ids: host list or int32 device tensor); returns
-        the drawn tokens, int32 [B] on the device (not read)."""
+    def _draw(self, rows: list, h: torch.Tensor, steps: list) -> torch.Tensor:
+        """The token of each row from its last-layer row h[i], int32 [B] on the device: the rows of
+        equal sampler settings drawn in one launch, row i with its step-steps[i] key
+        (DecodingMixin._draw / _draw_groups, Q36/scheduler/decode.py:116-176)."""
+        samplers = [r.sampler for r in rows]
+        keys = [s.rows_key() for s in samplers]
+        if all(k is None for k in keys):
+            return self.lm.greedy(h)
+        logits = self.lm.logits(h)
+        out = torch.empty(len(rows), dtype=torch.int32, device=logits.device)
+        groups: dict = {}
+        for i, k in enumerate(keys):
+            groups.setdefault(k, []).append(i)
+        for members in groups.values():
+            idx = torch.tensor(members, dtype=torch.int64, device=logits.device)
+            sel = logits if len(members) == len(rows) else logits.index_select(0, idx).contiguous()
+            tok = sample_rows(sel, [samplers[i] for i in members], [steps[i] for i in members])
+            out.index_copy_(0, idx, tok)
+        return out
+
+    def _issue_decode(self, rows: list, ids, pos: np.ndarray, ahead: int = 0) -> torch.Tensor:
+        """Launch one batched decode step over `rows` (ids: host list or int32 device tensor), whose
+        tokens are each row's token len(tokens) + ahead; returns them, int32 [B] on the device (not
+        read)."""
         lm = self.lm
         st = make_step_state(lm.cfg, pos, self.pool.page_table([r.rid for r in rows]))
         ids_t = ids if torch.is_tensor(ids) else torch.tensor(ids, dtype=torch.int32, device=self.device)
-        return lm.greedy(lm.model.decode_step(lm.embed_tokens(ids_t), self.pool.pools, st))
+        h = lm.model.decode_step(lm.embed_tokens(ids_t), self.pool.pools, st)
+        return self._draw(rows, h, [len(r.tokens) + ahead for r in rows])
 
     def _can_pipeline(self, rows: list, ahead: int) -> bool:
         """Whether a decode step over `rows` may be issued with `ahead` steps' tokens still unread:
@@ -187,7 +218,7 @@ class Engine:
             pos = np.array([r.length + 1 for r in rows], np.int32)
             for r in rows:
                 self._write(r, r.length + 1, 1)
-            self._inflight = self._in_flight(rows, self._issue_decode(rows, toks, pos))
+            self._inflight = self._in_flight(rows, self._issue_decode(rows, toks, pos, ahead=1))
             self.steps += 1
             self.pipelined += 1
         ev.synchronize()  # this step's tokens have landed; the next step may still be running
@@ -264,7 +295,7 @@ class Engine:
             x = layer.mixed(x, pool, ms)
         if c + n < len(r.prompt):
             return None
-        return int(lm.greedy(x[n - 1:n].contiguous()).item())
+        return int(self._draw([r], x[n - 1:n].contiguous(), [len(r.tokens)]).item())
 
     def run(self, max_steps: int | None = None) -> None:
         """Step until every submitted request is done (or max_steps rounds)."""

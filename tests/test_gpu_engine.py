@@ -90,9 +90,14 @@ def _prompts(seed, lens):
     return [rng.integers(0, VOCAB, n).tolist() for n in lens]
 
 
+_SAMPLING = ("temperature", "top_p", "top_k", "seed")
+
+
 def _solo(lm, prompt, max_tokens, **kw):
-    e = Engine(lm, 64, prefill_chunk=16, max_step_tokens=48, pipeline=False, **kw)
-    r = e.submit(prompt, max_tokens, eos=())
+    smp = {k: kw.pop(k) for k in _SAMPLING if k in kw}
+    kw.setdefault("pipeline", False)
+    e = Engine(lm, 64, prefill_chunk=16, max_step_tokens=48, **kw)
+    r = e.submit(prompt, max_tokens, eos=(), **smp)
     e.run()
     return r.tokens
 
@@ -109,6 +114,45 @@ def test_engine_batched_equals_solo(lm):
     for r, p in zip(reqs, prompts):
         assert r.finish_reason == "length" and len(r.tokens) == 6
         assert r.tokens == _solo(lm, p, 6, prefix_store=False), r.rid
+
+
+def test_engine_sampled_requests_are_batch_independent(lm):
+    """Sampled requests (temperature / top-p / top-k, seeded) generate the same tokens alone and
+    batched with greedy and differently-set requests, pipelined or not; the same seed repeats its
+    tokens and another seed differs; each token equals the oracle's draw given its step key's
+    uniform (the draw of a whole generation, checked on the first token of every request)."""
+    from jitengine_amd.sampler import Sampler
+    prompts = _prompts(9, [12, 20, 7, 30])
+    settings = [dict(temperature=0.8, top_p=0.9, top_k=40, seed=5), dict(), dict(temperature=1.2, top_p=1.0,
+                top_k=0, seed=6), dict(temperature=0.8, top_p=0.9, top_k=40, seed=11)]
+    e = Engine(lm, 128, prefill_chunk=16, max_step_tokens=48, page_seed=3)
+    reqs = [e.submit(p, 7, eos=(), **kw) for p, kw in zip(prompts, settings)]
+    e.run()
+    for r, p, kw in zip(reqs, prompts, settings):
+        assert len(r.tokens) == 7
+        assert r.tokens == _solo(lm, p, 7, prefix_store=False, **kw), r.rid
+        assert r.tokens == _solo(lm, p, 7, prefix_store=False, pipeline=True, **kw), r.rid
+    other = _solo(lm, prompts[0], 7, prefix_store=False, temperature=0.8, top_p=0.9, top_k=40, seed=99)
+    assert other != reqs[0].tokens
+    # every draw of a solo run: the oracle's draw from the row's logits and its step key
+    class Recording(Engine):
+        def _draw(self, rows, h, steps):
+            tok = super()._draw(rows, h, steps)
+            self.seen.append((u16(self.lm.logits(h)), list(steps), tok.cpu().numpy()))
+            return tok
+
+    for p, kw in zip(prompts, settings):
+        if not kw:
+            continue
+        e = Recording(lm, 64, prefill_chunk=16, max_step_tokens=48, pipeline=False)
+        e.seen = []
+        e.submit(p, 7, eos=(), **kw)
+        e.run()
+        smp = Sampler(kw["temperature"], kw["top_p"], kw["top_k"], kw["seed"], 7, lm.vocab)
+        assert [st[0] for _, st, _ in e.seen] == list(range(7))
+        for logits, st, tok in e.seen:
+            u = oracle.threefry_uniform(smp.key(st[0])[None, :])
+            assert oracle.sample_rows(logits, kw["temperature"], kw["top_p"], kw["top_k"], u)[0] == tok[0]
 
 
 def test_engine_prefix_sharing_is_exact(lm):
