@@ -582,6 +582,31 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
     return res
 
 
+def bench_sampler(dev: str) -> int:
+    """The sampler's kernels (csrc/sampler.hip) on the reference's vocabulary (248,320) for 1 and
+    32 rows of N(0, 3) logits: log-probabilities, the greedy draw, and draws under the settings of
+    the reference's sampler checks (Q36/sampler.py:575).  One workgroup per row reads its row
+    about six times from L2 (max, log-sum-exp, histogram, weights, the draw's walk); the
+    algorithmic bytes are the row's 2 V once."""
+    from jitengine_amd import ops
+
+    V = 248320
+    out = {"vocab": V, "us": {}, "row_GB_s": {}}
+    for B in (1, 32):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1000 + B)
+        x = (torch.randn((B, V), generator=gen, device=dev) * 3).to(torch.bfloat16)
+        u = torch.rand(B, generator=gen, device=dev)
+        launches = {"logprobs": [lambda: ops.logprobs_rows(x)], "greedy": [lambda: ops.argmax_rows(x)]}
+        for T, p, k in ((0.7, 0.95, 40), (1.0, 0.9, 20), (1.0, 0.95, 0), (1.0, 1.0, 0)):
+            launches[f"T{T}_p{p}_k{k}"] = [lambda T=T, p=p, k=k: ops.sample_rows(x, T, p, k, u)]
+        us = time_ops(launches, reps=20)
+        out["us"][f"B{B}"] = {k: round(v, 2) for k, v in us.items()}
+        out["row_GB_s"][f"B{B}"] = {k: round(B * V * 2 / (v * 1e-6) / 1e9, 1) for k, v in us.items()}
+    print(json.dumps({"sampler": out}), flush=True)
+    return 0
+
+
 def copy_calibration(dev: str) -> int:
     """A plain device copy of 256 MiB (torch's copy kernel), run 5 times: the known-size transfer
     the FETCH_SIZE / WRITE_SIZE counters are scaled by."""
@@ -888,6 +913,7 @@ def main() -> int:
     ap.add_argument("--no-bs1", action="store_true",
                     help="config 2 only: skip the bs=1 (config 4) measurement reported beside it")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--sampler", action="store_true", help="time the sampler's kernels (vocabulary 248,320)")
     ap.add_argument("--probe", action="store_true",
                     help="measure the streaming-read ceiling, the empty-launch floor and the grid-barrier cost")
     ap.add_argument("--probe-parts", default="read,launch,barrier",
@@ -914,6 +940,8 @@ def main() -> int:
         return copy_calibration(dev)
     if args.probe:
         return probe(dev, set(args.probe_parts.split(",")))
+    if args.sampler:
+        return bench_sampler(dev)
     if args.config == 1:
         res = bench_config1(args.steps, args.warmup, dev)
     elif args.config in (0, 2, 4):

@@ -337,7 +337,7 @@ int jit_embed_q4(const int32_t *ids, int B, const uint32_t *weight, const uint16
  *   lp   = bf16(x - lse) (logprobs_from_logits, Q36/sampler.py:295-297).
  * The sums are exact integers, so results do not depend on the order of the additions; the
  * reference's fp32 reductions (MLX's logsumexp, cumsum and sum orders) are not restated.
- * Contract: 1 <= V <= 2^20 (JIT_EUNSUPPORTED beyond); finite or -inf logits with at least one
+ * Contract: 1 <= V <= 2^19 (JIT_EUNSUPPORTED beyond); finite or -inf logits with at least one
  * finite value per row (other rows give unspecified tokens, never a fault). */
 
 /* lp [B, V] bf16 = the rows' log-probabilities as defined above. */

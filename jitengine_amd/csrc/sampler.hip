@@ -36,7 +36,8 @@ constexpr int kThreads = 1024, kWaves = 16;
 constexpr int kStep = 512;        // values a wave covers per step: 64 lanes x 8
 constexpr int kKeys = 32768;      // histogram bins: the magnitudes of values <= 0
 constexpr int kBinsPerThread = kKeys / kThreads;
-constexpr int kMaxV = 1 << 20;    // 2^42-scaled sums of at most 2^20 terms stay below 2^62
+constexpr int kMaxV = 1 << 19;    // (2^42-scaled sums of at most 2^20 terms stay below 2^62)
+constexpr int kMaxSteps = (kMaxV / (kWaves * 8) * 8 + kStep - 1) / kStep;  // steps of a wave's range
 
 enum Mode { kLogprobs = 0, kGreedy = 1, kSample = 2 };
 
@@ -142,36 +143,58 @@ __device__ __forceinline__ Range wave_range(int V) {
   return Range{min(V, w * R), min(V, (w + 1) * R)};
 }
 
+// the lane's 8 values of a step from i0 (kVec: one 16-byte load; else element loads, -inf past hi)
+struct Raw8 {
+  uint32_t w[4];
+};
+
 template <bool kVec>
-__device__ __forceinline__ int load8(const uint16_t *row, int i0, int hi, float v[8]) {
+__device__ __forceinline__ Raw8 load8(const uint16_t *row, int i0, int hi) {
+  Raw8 r;
   if (kVec) {
-    if (i0 >= hi) return 0;
-    const uint4 q = *(const uint4 *)(row + i0);
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    const uint4 q = i0 < hi ? *(const uint4 *)(row + i0) : make_uint4(0u, 0u, 0u, 0u);
+    r.w[0] = q.x, r.w[1] = q.y, r.w[2] = q.z, r.w[3] = q.w;
+  } else {
 #pragma unroll
-    for (int j = 0; j < 8; j++) v[j] = (j & 1) ? bf2f_hi(w[j >> 1]) : bf2f(w[j >> 1] & 0xffffu);
-    return 8;
+    for (int j = 0; j < 4; j++) {
+      const uint32_t lo = i0 + 2 * j < hi ? row[i0 + 2 * j] : 0xff80u;
+      const uint32_t hi16 = i0 + 2 * j + 1 < hi ? row[i0 + 2 * j + 1] : 0xff80u;
+      r.w[j] = lo | (hi16 << 16);
+    }
   }
-  int n = 0;
+  return r;
+}
+
+__device__ __forceinline__ float val(const Raw8 &r, int j) {
+  return (j & 1) ? bf2f_hi(r.w[j >> 1]) : bf2f(r.w[j >> 1] & 0xffffu);
+}
+
+constexpr int kAhead = 8;  // steps whose loads a wave issues before it uses the first
+
+// f(i0, raw, n) for every step of the wave's range in order (n = the lane's values in range);
+// the loads of kAhead steps are in flight together.  The step condition is uniform over the
+// wave, so f may use cross-lane operations.
+template <bool kVec, typename F>
+__device__ __forceinline__ void for_steps(const uint16_t *row, int V, F &&f) {
+  const Range r = wave_range(V);
+  const int l8 = 8 * lane_id();
+  for (int s = r.lo; s < r.hi; s += kStep * kAhead) {
+    Raw8 q[kAhead];
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    v[j] = (i0 + j < hi) ? bf2f(row[i0 + j]) : -INFINITY;
-    n += (i0 + j < hi);
+    for (int u = 0; u < kAhead; u++) q[u] = load8<kVec>(row, s + u * kStep + l8, r.hi);
+#pragma unroll
+    for (int u = 0; u < kAhead; u++)
+      if (s + u * kStep < r.hi) f(s + u * kStep + l8, q[u], max(0, min(8, r.hi - (s + u * kStep + l8))));
   }
-  return n;
 }
 
 template <bool kVec, typename F>
 __device__ __forceinline__ void for_each(const uint16_t *row, int V, F &&f) {
-  const Range r = wave_range(V);
-  for (int s = r.lo; s < r.hi; s += kStep) {
-    const int i0 = s + 8 * lane_id();
-    float v[8];
-    const int n = load8<kVec>(row, i0, r.hi, v);
+  for_steps<kVec>(row, V, [&](int i0, const Raw8 &q, int n) {
 #pragma unroll
     for (int j = 0; j < 8; j++)
-      if (j < n) f(i0 + j, v[j]);
-  }
+      if (j < n) f(i0 + j, val(q, j));
+  });
 }
 
 __global__ __launch_bounds__(kThreads) void threefry_uniform_kernel(const uint32_t *__restrict__ keys, int B,
@@ -218,7 +241,20 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
 
   if constexpr (kMode == kLogprobs) {
     uint16_t *out = a.lp + (long long)b * V;
-    for_each<kVec>(row, V, [&](int i, float x) { out[i] = (uint16_t)f2bf(x - lse); });
+    for_steps<kVec>(row, V, [&](int i0, const Raw8 &q, int n) {
+      uint32_t h[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) h[j] = f2bf(val(q, j) - lse);
+      if (kVec) {
+        if (n == 8)
+          *(uint4 *)(out + i0) = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                            h[6] | (h[7] << 16));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+          if (j < n) out[i0 + j] = (uint16_t)h[j];
+      }
+    });
     return;
   }
 
@@ -341,78 +377,91 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
       for (int w = 0; w < (t >> 6); w++) tie_base += (uint32_t)sh.q[w];
     }
 
-    // one pass over the wave's range in vocabulary order: each value's weight, with the rank
-    // of key_t's members running along; `f(i, W)` sees every value, `g(step_total)` each step
-    auto weights = [&](auto &&f) {
-      const Range r = wave_range(V);
-      uint32_t carry = tie_base;
-      for (int s = r.lo; s < r.hi; s += kStep) {
-        const int i0 = s + 8 * l;
-        float v[8];
-        const int n = load8<kVec>(row, i0, r.hi, v);
-        int key[8];
-        uint32_t ties = 0;
+    // the weights of one step of the wave's range: W[j] of the lane's values; the rank of key_t's
+    // members runs on from `carry` (the members in earlier waves and in the wave's earlier steps);
+    // returns the step's members
+    auto step_weights = [&](const Raw8 &q, int n, uint32_t carry, uint64_t W[8]) -> uint32_t {
+      int key[8];
+      uint32_t ties = 0;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          key[j] = j < n ? key_of(bf16r(v[j] - lse)) : -1;
-          ties += key[j] == key_t;
-        }
-        const uint32_t tincl = partial ? wave_incl(ties) : 0u;
-        uint32_t rank = carry + tincl - ties;
-        uint64_t W[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          bool kept = key[j] > key_t;
-          if (key[j] == key_t) {
-            kept = !partial || ((int)rank >= r_lo && (int)rank < r_hi);
-            rank++;
-          }
-          W[j] = kept ? fix42(exp_neg(bf16r(bf16r(v[j] - lse) * a.inv_t) - m)) : 0ull;
-        }
-        if (partial) carry += __shfl(tincl, 63, 64);
-        f(i0, W);
+      for (int j = 0; j < 8; j++) {
+        key[j] = j < n ? key_of(bf16r(val(q, j) - lse)) : -1;
+        ties += key[j] == key_t;
       }
+      const uint32_t tincl = partial ? wave_incl(ties) : 0u;
+      uint32_t rank = carry + tincl - ties;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        bool kept = key[j] > key_t;
+        if (key[j] == key_t) {
+          kept = !partial || ((int)rank >= r_lo && (int)rank < r_hi);
+          rank++;
+        }
+        W[j] = kept ? fix42(exp_neg(bf16r(bf16r(val(q, j) - lse) * a.inv_t) - m)) : 0ull;
+      }
+      return partial ? __shfl(tincl, 63, 64) : 0u;
     };
 
+    // each step's total weight and starting rank, recorded for the draw below
+    __shared__ uint64_t step_tot[kWaves][kMaxSteps];
+    __shared__ uint32_t step_carry[kWaves][kMaxSteps];
+    const int w = t >> 6;
     uint64_t tw = 0;
-    weights([&](int, const uint64_t *W) {
+    uint32_t carry = tie_base;
+    int js = 0;
+    for_steps<kVec>(row, V, [&](int, const Raw8 &q, int n) {
+      uint64_t W[8];
+      const uint32_t c0 = carry;
+      carry += step_weights(q, n, c0, W);
+      uint64_t lt = 0;
 #pragma unroll
-      for (int j = 0; j < 8; j++) tw += W[j];
+      for (int j = 0; j < 8; j++) lt += W[j];
+      const uint64_t st = wave_sum(lt);
+      if (l == 0) {
+        step_tot[w][js] = st;
+        step_carry[w][js] = c0;
+      }
+      tw += st;
+      js++;
     });
-    tw = wave_sum(tw);
     __syncthreads();
-    if (l == 0) sh.q[t >> 6] = tw;
+    if (l == 0) sh.q[w] = tw;
     __syncthreads();
     uint64_t base = 0, total = 0;
-    for (int w = 0; w < kWaves; w++) {
-      if (w < (t >> 6)) base += sh.q[w];
-      total += sh.q[w];
+    for (int v = 0; v < kWaves; v++) {
+      if (v < w) base += sh.q[v];
+      total += sh.q[v];
     }
     float u = a.u[b];
     u = fminf(fmaxf(u, 0.0f), 0x1.fffffep-1f);  // (NaN -> 0)
     const uint64_t U = mul_u32_u64_hi((uint64_t)(u * 4294967296.0f), total);
 
     // the number of i with C_i <= U, wave by wave: a wave whose values all lie at or below U
-    // counts its range, one above U none, and the one wave that holds U walks its range
+    // counts its range, one above U none; in the one wave that holds U, the steps before the
+    // step that holds it count whole, and that step is reloaded and walked
     const Range r = wave_range(V);
     uint64_t cnt = 0;
     if (base + tw <= U) {
       cnt = l == 0 ? (uint64_t)(r.hi - r.lo) : 0ull;
     } else if (base <= U) {
       uint64_t run = base;
-      weights([&](int i0, const uint64_t *W) {
-        uint64_t lt = 0;
+      int j = 0;
+      while (run + step_tot[w][j] <= U) run += step_tot[w][j++];
+      const int i0 = r.lo + j * kStep + 8 * l;
+      const Raw8 q = load8<kVec>(row, i0, r.hi);
+      const int n = max(0, min(8, r.hi - i0));
+      uint64_t W[8];
+      step_weights(q, n, step_carry[w][j], W);
+      uint64_t lt = 0;
 #pragma unroll
-        for (int j = 0; j < 8; j++) lt += W[j];
-        const uint64_t incl = wave_incl(lt);
-        uint64_t c = run + incl - lt;  // C of the lane's first value
+      for (int jj = 0; jj < 8; jj++) lt += W[jj];
+      uint64_t c = run + wave_incl(lt) - lt;  // C of the lane's first value
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          if (i0 + j < r.hi && c <= U) cnt++;
-          c += W[j];
-        }
-        run += __shfl(incl, 63, 64);
-      });
+      for (int jj = 0; jj < 8; jj++) {
+        if (jj < n && c <= U) cnt++;
+        c += W[jj];
+      }
+      if (l == 0) cnt += (uint64_t)j * kStep;
     }
     const uint64_t count = wg_sum(cnt, sh);
     if (t == 0) a.tok[b] = (int32_t)(count - 1);

@@ -56,7 +56,7 @@ def test_contract_breaks_return_einval_before_launch():
     assert lib.jit_qmm_seg(None, 4, 2048, None, 128, None, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_moe_combine_rmsnorm(None, None, None, 2, 8, 4096, None, None, None, 1e-6, None, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_sample_rows(None, 2, 0, 1.0, 0.9, 5, None, None, None) == _lib.JIT_EINVAL
-    assert lib.jit_sample_rows(None, 2, (1 << 20) + 1, 1.0, 0.9, 5, None, None, None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_sample_rows(None, 2, (1 << 19) + 1, 1.0, 0.9, 5, None, None, None) == _lib.JIT_EUNSUPPORTED
     dummy = ctypes.c_void_p(16)  # (never dereferenced: every call below returns before a launch)
     assert lib.jit_sample_rows(dummy, 2, 64, 1.0, 0.9, -1, dummy, dummy, None) == _lib.JIT_EINVAL
     assert lib.jit_sample_rows(dummy, 2, 64, float("nan"), 0.9, 5, dummy, dummy, None) == _lib.JIT_EINVAL

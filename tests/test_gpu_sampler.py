@@ -119,7 +119,7 @@ def test_sampler_contract():
         ops.sample_rows(x, 1.0, 0.9, 5, None)
     with pytest.raises(ValueError):
         ops.sample_rows(x, float("nan"), 0.9, 5, u)
-    big = torch.zeros((1, (1 << 20) + 8), dtype=torch.bfloat16, device=DEV)
+    big = torch.zeros((1, (1 << 19) + 8), dtype=torch.bfloat16, device=DEV)
     from jitengine_amd._lib import UnsupportedShape
     with pytest.raises(UnsupportedShape):
         ops.sample_rows(big, 1.0, 0.9, 5, u[:1])
