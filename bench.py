@@ -639,6 +639,7 @@ def probe(dev: str, parts=("read", "launch", "barrier")) -> int:
     lib = ctypes.CDLL(hip_build.PROBE_LIB)
     P, I, LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
     lib.probe_read.argtypes = [P, LL, I, I, P, P]
+    lib.probe_lds_ring.argtypes = [P, LL, I, I, P, P]
     lib.probe_empty.argtypes = [P]
     lib.probe_paged.argtypes = [P, P, I, I, I, P, P]
     lib.probe_barrier.argtypes = [I, I, I, P, P, I, P, P]
@@ -656,7 +657,23 @@ def probe(dev: str, parts=("read", "launch", "barrier")) -> int:
         torch.cuda.synchronize()
         return s.elapsed_time(e) / reps  # ms
 
-    out = {"read": {}, "launch": {}, "barrier": {}}
+    out = {"read": {}, "launch": {}, "barrier": {}, "lds_ring": {}}
+    if "lds" in parts:
+        # streaming through an LDS ring by direct loads, one persistent workgroup per CU, over 48
+        # rotating 196 MB windows (the expert weights' volume)
+        win, n_win = 196 << 20, 8
+        buf = torch.empty(win * n_win // 4, dtype=torch.int32, device=dev).random_()
+        sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        shapes = {0: "4x9KB_4stages", 1: "3x9KB_5stages", 2: "8x4KB_4stages", 3: "4x4KB_8stages", 4: "4x2KB_16stages"}
+        for shape, name in shapes.items():
+            def rot(shape=shape):
+                for w in range(n_win):
+                    lib.probe_lds_ring(ctypes.c_void_p(buf.data_ptr() + w * win), win, shape, cus,
+                                       ctypes.c_void_p(sink.data_ptr()), sp)
+            ms = timed(rot, 5)
+            out["lds_ring"][f"{name}_{cus}wg"] = round(n_win * win / (ms * 1e-3) / 1e9, 1)
+        del buf
     if "read" in parts:
         big = 4 << 30
         buf = torch.empty(big // 4, dtype=torch.int32, device=dev).random_()

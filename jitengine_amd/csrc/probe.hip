@@ -132,6 +132,45 @@ __global__ __launch_bounds__(256) void probe_barrier_kernel(int phases, int word
   if (acc == 0x9e3779b9u) status[1] = 1;  // keeps the reads alive
 }
 
+// Streaming through an LDS ring by direct global->LDS loads, the shape of a persistent streaming
+// kernel without its arithmetic: each workgroup reads one contiguous run of the buffer in stages
+// of NL KB x L waves (each wave NL loads of 1 KB per stage), S stages of LDS, the loads of S - 2
+// stages left in flight at each stage's wait, one workgroup barrier per stage.
+template <int L, int S, int NL>
+__global__ __launch_bounds__(64 * L) void probe_lds_ring_kernel(const uint8_t *__restrict__ p, long long bytes,
+                                                              uint32_t *__restrict__ sink) {
+  extern __shared__ uint8_t ring[];
+  constexpr int kStage = L * NL * 1024;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const long long per = bytes / gridDim.x / kStage * kStage;  // whole stages of each run
+  const uint8_t *run = p + (long long)blockIdx.x * per;
+  const int n = (int)(per / kStage);
+  const uint32_t base = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring);
+  auto stage = [&](int st, int slot) {
+    st = st < n ? st : n - 1;
+#pragma unroll
+    for (int c = 0; c < NL; c++) {
+      const uint8_t *src = run + (long long)st * kStage + (w * NL + c) * 1024 + 16 * l;
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(base + slot * kStage + (w * NL + c) * 1024);
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(dst) : "memory", "m0");
+    }
+  };
+  for (int st = 0; st < S - 1; st++) stage(st, st);
+  uint32_t acc = 0;
+  for (int st = 0; st < n; st++) {
+    constexpr int kVm = (S - 2) * NL;
+    __builtin_amdgcn_s_waitcnt((kVm & 15) | ((kVm >> 4) << 14) | (7 << 4) | (15 << 8));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    stage(st + S - 1, (st + S - 1) % S);
+    acc ^= ((const uint32_t *)(ring + (st % S) * kStage))[threadIdx.x];
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;  // keeps the reads alive
+}
+
 }  // namespace
 
 extern "C" int probe_read(const void *p, long long bytes, int mode, int blocks, uint32_t *sink, void *stream) {
@@ -180,4 +219,28 @@ extern "C" int probe_barrier(int blocks, int phases, int words, uint32_t *counte
   const hipError_t e = hipLaunchCooperativeKernel((const void *)probe_barrier_kernel, dim3(blocks), dim3(256), args,
                                                   0, (hipStream_t)stream);
   return e == hipSuccess ? 0 : -3;
+}
+
+// shape: 0 = 4 waves x 9 KB, 4 stages (144 KB); 1 = 3 x 9 KB, 5 stages (135 KB); 2 = 8 x 4 KB,
+// 4 stages (128 KB); 3 = 4 x 4 KB, 8 stages (128 KB); 4 = 4 x 2 KB, 16 stages (128 KB)
+extern "C" int probe_lds_ring(const void *p, long long bytes, int shape, int blocks, uint32_t *sink, void *stream) {
+  if (!p || !sink || blocks <= 0 || shape < 0 || shape > 4) return -1;
+  hipStream_t st = (hipStream_t)stream;
+#define PROBE_RING(L, S, NL)                                                                                 \
+  {                                                                                                          \
+    const size_t lds = (size_t)S * L * NL * 1024;                                                            \
+    (void)hipFuncSetAttribute((const void *)&probe_lds_ring_kernel<L, S, NL>,                                \
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                         \
+    probe_lds_ring_kernel<L, S, NL><<<blocks, 64 * L, lds, st>>>((const uint8_t *)p, bytes, sink);            \
+    break;                                                                                                   \
+  }
+  switch (shape) {
+    case 0: PROBE_RING(4, 4, 9)
+    case 1: PROBE_RING(3, 5, 9)
+    case 2: PROBE_RING(8, 4, 4)
+    case 3: PROBE_RING(4, 8, 4)
+    default: PROBE_RING(4, 16, 2)
+  }
+#undef PROBE_RING
+  return hipGetLastError() == hipSuccess ? 0 : -3;
 }
