@@ -42,7 +42,24 @@ struct SegArgs {
   long long w_estride;        // packed bytes per expert
   int K, N;                   // N: output columns (I for gate||up, D for down)
   int T;                      // rows of a dense matrix (cnt null)
+  int nx, groups;             // column blocks per group; groups = experts (or a dense matrix's token chunks)
 };
+
+// Workgroup -> (group, column block), XCD-aware.  MI355X deals the workgroups of a launch to its
+// 8 XCDs round-robin (workgroup i to XCD i % 8), and each XCD has its own L2.  All column blocks
+// of one group (an expert's segment, or one token chunk of a dense matrix) read the same
+// activation rows, so they are given consecutive slots of one XCD: group g goes to XCD g % 8,
+// and its nx blocks follow each other there, resident together, so the rows leave HBM (or the
+// last-level cache) once per group instead of once per column block.  The grid is padded to
+// 8 * ceil(groups / 8) groups; the padding's workgroups exit at once.
+__device__ __forceinline__ bool seg_block(const SegArgs &a, int &g, int &cb) {
+  const int L = blockIdx.x, xcd = L & 7, slot = L >> 3;
+  g = xcd + 8 * (slot / a.nx);
+  cb = slot % a.nx;
+  return g < a.groups;
+}
+
+inline dim3 seg_grid(int nx, int groups) { return dim3(nx * 8 * ((groups + 7) / 8)); }
 
 // 8 packed-order nibbles of a word -> 8 bf16 weights bf16(s * q + b) in natural k order.
 // The masked words pass through an empty asm so that each byte converts with one
@@ -68,12 +85,14 @@ __device__ __forceinline__ Frag8 dequant_word(uint32_t w, float s, float b) {
   return f;
 }
 
-// DENSE: one dense matrix (E = 1, cnt null), its token chunks spread over gridDim.z
+// DENSE: one dense matrix (E = 1, cnt null), one token chunk per group
 template <bool SWIGLU, bool DENSE = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void seg_kernel(const SegArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[kSegTokens * kXStride];
   __shared__ int xrow[kSegTokens];
-  const int e = blockIdx.y;
+  int grp, cb;
+  if (!seg_block(a, grp, cb)) return;  // grid padding (uniform over the workgroup)
+  const int e = DENSE ? 0 : grp;
   const int cnt = DENSE ? a.T : a.cnt[e], off = DENSE ? 0 : a.off[e];
   if (cnt <= 0) return;  // uniform over the workgroup
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
@@ -86,15 +105,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
   for (int r = 0; r < kSegRB; r++) {
     if (SWIGLU)  // gate blocks 8 cb + 2 wave + r (r < 2), and the up blocks of the same columns
-      rbk[r] = (r >= 2 ? a.N / 16 : 0) + blockIdx.x * 8 + 2 * wave + (r & 1);
+      rbk[r] = (r >= 2 ? a.N / 16 : 0) + cb * 8 + 2 * wave + (r & 1);
     else
-      rbk[r] = blockIdx.x * 16 + 4 * wave + r;
+      rbk[r] = cb * 16 + 4 * wave + r;
   }
   const uint8_t *wexp = a.w + (long long)e * a.w_estride;
 
-  // (the token chunks are dealt to the workgroups of gridDim.z: one z for an expert segment,
-  // several for a dense batch)
-  for (int c0 = blockIdx.z * kSegTokens; c0 < cnt; c0 += gridDim.z * kSegTokens) {
+  // token chunks: every chunk of an expert segment in turn; one chunk (the group) of a dense batch
+  const int cend = DENSE ? min(cnt, (grp + 1) * kSegTokens) : cnt;
+  for (int c0 = DENSE ? grp * kSegTokens : 0; c0 < cend; c0 += kSegTokens) {
     const int nt = min(kSegTokens, cnt - c0);
     const int ntiles = (nt + 15) >> 4;
     __syncthreads();  // the previous chunk's LDS reads are done
@@ -213,8 +232,9 @@ extern "C" int jit_moe_gate_up_swiglu_seg(const uint16_t *x, int K, const int32_
   if (P == 0) return JIT_OK;
   if (!x || !pair_row || !expert_cnt || !expert_off || !packed || !h)
     return jit::fail(JIT_EINVAL, "moe_gate_up_seg: null pointer");
-  SegArgs a{x, pair_row, expert_cnt, expert_off, (const uint8_t *)packed, h, jit_q4_packed_bytes(1, 2 * I, K), K, I, 0};
-  seg_kernel<true><<<dim3(I / 128, E), 256, 0, (hipStream_t)stream>>>(a);
+  SegArgs a{x, pair_row, expert_cnt, expert_off, (const uint8_t *)packed, h, jit_q4_packed_bytes(1, 2 * I, K), K, I, 0,
+            I / 128, E};
+  seg_kernel<true><<<seg_grid(a.nx, E), 256, 0, (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_moe_gate_up_swiglu_seg");
 }
 
@@ -227,8 +247,9 @@ extern "C" int jit_moe_down_seg(const uint16_t *h, int I, const int32_t *expert_
                      I, D);
   if (P == 0) return JIT_OK;
   if (!h || !expert_cnt || !expert_off || !packed || !r) return jit::fail(JIT_EINVAL, "moe_down_seg: null pointer");
-  SegArgs a{h, nullptr, expert_cnt, expert_off, (const uint8_t *)packed, r, jit_q4_packed_bytes(1, D, I), I, D, 0};
-  seg_kernel<false><<<dim3(D / kSegRows, E), 256, 0, (hipStream_t)stream>>>(a);
+  SegArgs a{h, nullptr, expert_cnt, expert_off, (const uint8_t *)packed, r, jit_q4_packed_bytes(1, D, I), I, D, 0,
+            D / kSegRows, E};
+  seg_kernel<false><<<seg_grid(a.nx, E), 256, 0, (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_moe_down_seg");
 }
 
@@ -239,8 +260,8 @@ extern "C" int jit_qmm_seg(const uint16_t *x, int T, int K, const void *packed, 
                      N);
   if (T == 0) return JIT_OK;
   if (!x || !packed || !y) return jit::fail(JIT_EINVAL, "qmm_seg: null pointer");
-  SegArgs a{x, nullptr, nullptr, nullptr, (const uint8_t *)packed, y, 0, K, N, T};
   const int chunks = (T + kSegTokens - 1) / kSegTokens;
-  seg_kernel<false, true><<<dim3(N / kSegRows, 1, chunks), 256, 0, (hipStream_t)stream>>>(a);
+  SegArgs a{x, nullptr, nullptr, nullptr, (const uint8_t *)packed, y, 0, K, N, T, N / kSegRows, chunks};
+  seg_kernel<false, true><<<seg_grid(a.nx, chunks), 256, 0, (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_qmm_seg");
 }
