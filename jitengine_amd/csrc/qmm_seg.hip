@@ -25,10 +25,13 @@ constexpr int kSegRB = 4;                 // row blocks per wave
 constexpr int kSegRows = 16 * kSegRB * kSegWaves;  // weight rows per workgroup
 constexpr int kSegTT = 10;                // token tiles per chunk (160 tokens)
 constexpr int kSegTokens = 16 * kSegTT;
-#ifndef JIT_SEG_XPAD
-#define JIT_SEG_XPAD 8
+#ifndef JIT_SEG_AHEAD
+#define JIT_SEG_AHEAD 1
 #endif
-constexpr int kXStride = 128 + JIT_SEG_XPAD;  // LDS row stride of the staged activations (bf16)
+constexpr int kSegAhead = JIT_SEG_AHEAD;  // token tiles whose fragment reads run ahead of the MFMAs
+#ifndef JIT_SEG_IGLP
+#define JIT_SEG_IGLP 0
+#endif
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 is a union-based struct)
 
@@ -63,7 +66,8 @@ inline dim3 seg_grid(int nx, int groups) { return dim3(nx * 8 * ((groups + 7) / 
 
 // 8 packed-order nibbles of a word -> 8 bf16 weights bf16(s * q + b) in natural k order.
 // The masked words pass through an empty asm so that each byte converts with one
-// v_cvt_f32_ubyteN (the compiler would otherwise extract every nibble separately).
+// v_cvt_f32_ubyteN (the compiler would otherwise extract every nibble separately), and the
+// weights are rounded in pairs (one v_cvt_pk_bf16_f32 each; s q + b is finite).
 __device__ __forceinline__ Frag8 dequant_word(uint32_t w, float s, float b) {
   uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
   asm volatile("" : "+v"(lo), "+v"(hi));
@@ -74,22 +78,67 @@ __device__ __forceinline__ Frag8 dequant_word(uint32_t w, float s, float b) {
   const float q2 = (float)(hi & 0xffu), q6 = (float)((hi >> 8) & 0xffu);
   const float q3 = (float)((hi >> 16) & 0xffu), q7 = (float)(hi >> 24);
   Frag8 f;
-  f.v[0] = (__bf16)fmaf(s, q0, b);
-  f.v[1] = (__bf16)fmaf(s, q1, b);
-  f.v[2] = (__bf16)fmaf(s, q2, b);
-  f.v[3] = (__bf16)fmaf(s, q3, b);
-  f.v[4] = (__bf16)fmaf(s, q4, b);
-  f.v[5] = (__bf16)fmaf(s, q5, b);
-  f.v[6] = (__bf16)fmaf(s, q6, b);
-  f.v[7] = (__bf16)fmaf(s, q7, b);
+  f.u[0] = pack_bf16x2_rne(fmaf(s, q0, b), fmaf(s, q1, b));
+  f.u[1] = pack_bf16x2_rne(fmaf(s, q2, b), fmaf(s, q3, b));
+  f.u[2] = pack_bf16x2_rne(fmaf(s, q4, b), fmaf(s, q5, b));
+  f.u[3] = pack_bf16x2_rne(fmaf(s, q6, b), fmaf(s, q7, b));
   return f;
 }
 
-// DENSE: one dense matrix (E = 1, cnt null), one token chunk per group
+// LDS of a workgroup:
+//   two activation stages: one K step's activations, kSegTokens rows of 128 k (256 B, no
+//     padding).  Row r's 16 B piece c sits in slot c ^ (r % 16), so the 16 rows one fragment
+//     read touches (same piece, rows 16 t .. 16 t + 15) fall in 16 different slots: the reads
+//     are free of bank conflicts without the padding the direct global->LDS loads (1 KB = 4
+//     whole rows per wave instruction) could not insert;
+//   three weight stages: per wave its 4 row blocks' nibble tiles of one K step (4 x 1 KB) and
+//     their scale tiles (4 x 128 B, then a copy of them: the instruction writes 1 KB);
+//   the chunk's activation row indices.
+constexpr int kSegStageBytes = kSegTokens * 256;
+constexpr int kSegWWave = 5 * 1024;
+constexpr int kSegWStageBytes = kSegWaves * kSegWWave;
+constexpr int kSegWOff = 2 * kSegStageBytes;
+constexpr int kSegRowOff = kSegWOff + 3 * kSegWStageBytes;
+constexpr int kSegLdsBytes = kSegRowOff + kSegTokens * (int)sizeof(int);
+static_assert(kSegLdsBytes <= 160 * 1024, "gfx950 gives a workgroup at most 160 KB of LDS");
+
+// s_waitcnt vmcnt(N), nothing else.  Direct loads are counted by hand: the compiler does not see
+// the ones issued by inline assembly.
+template <int N>
+__device__ __forceinline__ void seg_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// A workgroup barrier that waits for nothing else: every wave has already waited for its own
+// direct loads (__syncthreads()'s fence would also wait for the loads still in flight).
+__device__ __forceinline__ void seg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void seg_load_lds(const void *src, uint32_t dst) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "memory", "m0");
+}
+
+// DENSE: one dense matrix (E = 1, cnt null), one token chunk per group.
+//
+// Pipeline over the K steps p (one group pair each).  Per wave and step, 15 direct loads:
+// 10 of activations (the wave's 4 rows of each token tile) and 5 of its packed weights.
+//   top of step p: wait for step p's activations (requested at the top of step p - 1), one
+//     barrier; request step p + 1's activations into the other stage and step p + 2's weights;
+//   group 0's token tiles against B fragments dequantized during step p - 1, with the
+//     dequantization of this step's group 1 between their MFMAs;
+//   wait for step p + 1's weights (the wave's own: no barrier), then group 1's token tiles
+//     with the dequantization of step p + 1's group 0 between their MFMAs.
+// Each tile's activation fragments are read kSegAhead tiles ahead of its MFMAs.  Weights are
+// requested one and a half steps before they are dequantized, activations (mostly L2 hits:
+// an expert's column blocks run on one XCD) a step before they are read.
 template <bool SWIGLU, bool DENSE = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void seg_kernel(const SegArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[kSegTokens * kXStride];
-  __shared__ int xrow[kSegTokens];
+  extern __shared__ __attribute__((aligned(16))) uint8_t seg_lds[];
+  int *xrow = (int *)(seg_lds + kSegRowOff);
   int grp, cb;
   if (!seg_block(a, grp, cb)) return;  // grid padding (uniform over the workgroup)
   const int e = DENSE ? 0 : grp;
@@ -99,6 +148,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int lr = l & 15, lg = l >> 4;
   const int tid = threadIdx.x;
   const int GP = a.K >> 7;  // K steps (group pairs)
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)seg_lds);
 
   // the wave's 4 row blocks (index of the first row / 16 inside the expert's stack)
   int rbk[kSegRB];
@@ -110,93 +161,144 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       rbk[r] = cb * 16 + 4 * wave + r;
   }
   const uint8_t *wexp = a.w + (long long)e * a.w_estride;
+  const long long tile_row = (long long)GP * qtile::kTileBytes;  // bytes of one row block's tiles
+  // weight staging: nibble instruction r moves row block r's tile (lane l: its 16 B piece); the
+  // scale instruction's lane l moves piece l % 8 of row block (l / 8) % 4's scale tile
+  const uint8_t *wnib = wexp + 16 * l;
+  const int srb = (l >> 3) & 3;
+  const int rb_s = srb == 0 ? rbk[0] : srb == 1 ? rbk[1] : srb == 2 ? rbk[2] : rbk[3];
+  const uint8_t *wscl = wexp + rb_s * tile_row + (long long)GP * qtile::kNibbleBytes + 16 * (l & 7);
+  const uint32_t wlds = lds0 + kSegWOff + wave * kSegWWave;  // + stage * kSegWStageBytes
+  const uint8_t *wmine = seg_lds + kSegWOff + wave * kSegWWave;
+  auto load_w = [&](int p) {
+    const uint32_t st = wlds + (p % 3) * kSegWStageBytes;
+#pragma unroll
+    for (int r = 0; r < kSegRB; r++)
+      seg_load_lds(wnib + rbk[r] * tile_row + p * qtile::kNibbleBytes, __builtin_amdgcn_readfirstlane(st + r * 1024));
+    seg_load_lds(wscl + p * qtile::kScaleBytes, __builtin_amdgcn_readfirstlane(st + 4096));
+  };
+  // B fragment h of group g, row block r, from the staged step p: bf16(s q + b) of the lane's
+  // word h of the group (the nibble tile's 16 B piece holds group 0's two words, then group 1's)
+  auto dequant_word_at = [&](int p, int g, int r, int h, Frag8 (&bw)[kSegRB][2]) {
+    const uint8_t *st = wmine + (p % 3) * kSegWStageBytes;
+    const uint32_t q = *(const uint32_t *)(st + r * 1024 + 16 * l + 8 * g + 4 * h);
+    const uint2 sb = *(const uint2 *)(st + 4096 + r * 128 + 8 * lr);
+    const float sc = g ? bf2f_hi(sb.x) : bf2f(sb.x & 0xffffu);
+    const float bi = g ? bf2f_hi(sb.y) : bf2f(sb.y & 0xffffu);
+    bw[r][h] = dequant_word(q, sc, bi);
+  };
+  auto dequant_rb = [&](int p, int g, int r, Frag8 (&bw)[kSegRB][2]) {
+    dequant_word_at(p, g, r, 0, bw);
+    dequant_word_at(p, g, r, 1, bw);
+  };
+  // activation staging: the wave's instruction j moves rows 16 j + 4 wave .. + 3 (1 KB); lane l
+  // fetches the piece its slot l % 16 holds in row 16 j + srow
+  const int srow = 4 * wave + (l >> 4);
+  const int spiece = (l & 15) ^ srow;
+  // fragment reads: lane (lr, lg) reads pieces 8 g + 2 lg and + 1 of row 16 t + lr
+  const int frow = lr * 256;
 
-  // token chunks: every chunk of an expert segment in turn; one chunk (the group) of a dense batch
   const int cend = DENSE ? min(cnt, (grp + 1) * kSegTokens) : cnt;
   for (int c0 = DENSE ? grp * kSegTokens : 0; c0 < cend; c0 += kSegTokens) {
     const int nt = min(kSegTokens, cnt - c0);
     const int ntiles = (nt + 15) >> 4;
-    __syncthreads();  // the previous chunk's LDS reads are done
+    __syncthreads();  // the previous chunk's reads of the stages and of xrow are done
     for (int j = tid; j < kSegTokens; j += 256) {
       const int pos = off + c0 + min(j, nt - 1);  // rows past the segment re-read its last row
       xrow[j] = a.row_index ? a.row_index[pos] : pos;
     }
     __syncthreads();
-
-    // staging of one K step's activations: thread t moves 16 B piece (t % 16) of rows
-    // t / 16 + 16 i; packed weights of one K step: per row block the pair's nibble tile
-    // (16 B per lane) and its scale tile (scale pair, bias pair of row lr)
-    u32x4 xv[kSegTT];
-    uint4 wq[kSegRB];
-    uint2 wsb[kSegRB];
-    uint32_t xsrc[kSegTT];  // element offsets of this thread's pieces (x holds < 2^32 elements)
+    uint32_t xsrc[kSegTT];  // element offsets of this lane's pieces (x holds < 2^32 elements)
 #pragma unroll
-    for (int i = 0; i < kSegTT; i++) xsrc[i] = (uint32_t)xrow[(tid >> 4) + 16 * i] * (uint32_t)a.K + 8 * (tid & 15);
-#define SEG_LOAD_STEP(p)                                                                                   \
-  {                                                                                                        \
-    _Pragma("unroll") for (int i = 0; i < kSegTT; i++) if ((tid >> 4) + 16 * i < 16 * ntiles) xv[i] =      \
-        *(const u32x4 *)(a.x + xsrc[i] + 128 * (p));                                                       \
-    _Pragma("unroll") for (int r = 0; r < kSegRB; r++) {                                                   \
-      const uint8_t *blk = wexp + (long long)rbk[r] * GP * qtile::kTileBytes;                              \
-      wq[r] = *(const uint4 *)(blk + (p) * qtile::kNibbleBytes + 16 * l);                                  \
-      wsb[r] = *(const uint2 *)(blk + (long long)GP * qtile::kNibbleBytes + (p) * qtile::kScaleBytes + 8 * lr); \
-    }                                                                                                      \
-  }
+    for (int j = 0; j < kSegTT; j++) xsrc[j] = (uint32_t)xrow[16 * j + srow] * (uint32_t)a.K + 8 * spiece;
+    auto load_x = [&](int p) {
+      const uint32_t st = lds0 + (p & 1) * kSegStageBytes + 4 * wave * 256;
+#pragma unroll
+      for (int j = 0; j < kSegTT; j++)
+        seg_load_lds(a.x + xsrc[j] + 128 * p, __builtin_amdgcn_readfirstlane(st + 16 * j * 256));
+    };
 
     f32x4 acc[kSegTT][kSegRB];
 #pragma unroll
     for (int t = 0; t < kSegTT; t++)
 #pragma unroll
       for (int r = 0; r < kSegRB; r++) acc[t][r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    Frag8 bw0[kSegRB][2], bw1[kSegRB][2];
 
-    SEG_LOAD_STEP(0);
-    for (int p = 0; p < GP; p++) {
-      __syncthreads();  // every wave is done reading the previous step's activations
+    // all kSegTT token tiles of group g of step p against bw, with no branch (tiles past the
+    // chunk compute on rows that are never stored: a branch per tile would keep the
+    // dequantization from being scheduled between the MFMAs); side(t) is the dequantization of
+    // one B fragment (word t % 2 of row block t / 2) interleaved with tile t's MFMAs (t < 8)
+    auto tiles = [&](int p, int g, Frag8 (&bw)[kSegRB][2], auto &&side) {
+      const uint8_t *xs = seg_lds + (p & 1) * kSegStageBytes + frow;
+      const int pa = 8 * g + 2 * lg;
+      const int o0 = 16 * (pa ^ lr), o1 = 16 * ((pa + 1) ^ lr);
+      Frag8 xa[kSegAhead + 1][2];
 #pragma unroll
-      for (int i = 0; i < kSegTT; i++) {
-        const int row = (tid >> 4) + 16 * i;
-        if (row < 16 * ntiles) *(u32x4 *)(xs + row * kXStride + 8 * (tid & 15)) = xv[i];
+      for (int t = 0; t < kSegAhead; t++) {
+        xa[t][0].q = *(const uint4 *)(xs + t * 16 * 256 + o0);
+        xa[t][1].q = *(const uint4 *)(xs + t * 16 * 256 + o1);
       }
-      __syncthreads();
-      uint4 cq[kSegRB];
-      uint2 csb[kSegRB];
 #pragma unroll
-      for (int r = 0; r < kSegRB; r++) {
-        cq[r] = wq[r];
-        csb[r] = wsb[r];
-      }
-      if (p + 1 < GP) SEG_LOAD_STEP(p + 1);  // the next step's loads fly while this one computes
-#pragma unroll
-      for (int g = 0; g < 2; g++) {
-        // B fragments of group g of the pair: row block r, half hf (k 16 lg + 8 hf .. + 8)
-        Frag8 bw[kSegRB][2];
+      for (int t = 0; t < kSegTT; t++) {
+        if (t + kSegAhead < kSegTT) {
+          Frag8 *n = xa[(t + kSegAhead) % (kSegAhead + 1)];
+          n[0].q = *(const uint4 *)(xs + (t + kSegAhead) * 16 * 256 + o0);
+          n[1].q = *(const uint4 *)(xs + (t + kSegAhead) * 16 * 256 + o1);
+        }
+        const Frag8 *c = xa[t % (kSegAhead + 1)];
 #pragma unroll
         for (int r = 0; r < kSegRB; r++) {
-          const float sc = g ? bf2f_hi(csb[r].x) : bf2f(csb[r].x & 0xffffu);
-          const float bi = g ? bf2f_hi(csb[r].y) : bf2f(csb[r].y & 0xffffu);
-          bw[r][0] = dequant_word(g ? cq[r].z : cq[r].x, sc, bi);
-          bw[r][1] = dequant_word(g ? cq[r].w : cq[r].y, sc, bi);
+          acc[t][r] = mfma16x16x32(c[0], bw[r][0], acc[t][r]);
+          acc[t][r] = mfma16x16x32(c[1], bw[r][1], acc[t][r]);
         }
+        if (t < 2 * kSegRB) side(t);
+#if JIT_SEG_IGLP
+        // one MFMA, then three VALU instructions of the side dequantization, eight times: the
+        // VALU work issues while the matrix core runs instead of between bursts of MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-        for (int t = 0; t < kSegTT; t++) {
-          if (t < ntiles) {
-            const uint16_t *xr = xs + (16 * t + lr) * kXStride + 64 * g + 16 * lg;
-            Frag8 xa[2];
-            xa[0].q = *(const uint4 *)xr;
-            xa[1].q = *(const uint4 *)(xr + 8);
-#pragma unroll
-            for (int r = 0; r < kSegRB; r++) {
-              acc[t][r] = mfma16x16x32(xa[0], bw[r][0], acc[t][r]);
-              acc[t][r] = mfma16x16x32(xa[1], bw[r][1], acc[t][r]);
-            }
-          }
-          // at most the next tile's activation reads ahead of its MFMAs (each tile's
-          // fragments are 8 registers)
-          __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < 2 * kSegRB; i++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
+#endif
       }
+    };
+
+    // prologue: step 0's activations and weights, step 1's weights; group 0 of step 0
+    load_x(0);
+    load_w(0);
+    if (GP > 1) load_w(1);
+    if (GP > 1)
+      seg_wait_vm<5>();
+    else
+      seg_wait_vm<0>();
+    seg_barrier();
+#pragma unroll
+    for (int r = 0; r < kSegRB; r++) dequant_rb(0, 0, r, bw0);
+    for (int p = 0; p < GP; p++) {
+      if (p > 0) {
+        // step p's activations: the loads issued after them are step p + 1's weights (5)
+        if (p + 1 < GP)
+          seg_wait_vm<5>();
+        else
+          seg_wait_vm<0>();
+        seg_barrier();
+      }
+      if (p + 1 < GP) load_x(p + 1);
+      if (p + 2 < GP) load_w(p + 2);
+      tiles(p, 0, bw0, [&](int t) { dequant_word_at(p, 1, t >> 1, t & 1, bw1); });
+      // step p + 1's weights: issued after them, step p + 1's activations (10) and step p + 2's
+      // weights (5), as far as those exist
+      if (p + 2 < GP)
+        seg_wait_vm<15>();
+      else if (p + 1 < GP)
+        seg_wait_vm<10>();
+      // (after the last step the dequantization below reads a stale stage and is unused)
+      tiles(p, 1, bw1, [&](int t) { dequant_word_at(p + 1, 0, t >> 1, t & 1, bw0); });
     }
-#undef SEG_LOAD_STEP
 
     // lane l holds C[token 16 t + 4 lg + i][row 16 rbk[r] + lr]
 #pragma unroll
@@ -219,6 +321,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
 }
 
+// The kernels take more LDS than the static limit: raise their dynamic limit once.
+template <bool SWIGLU, bool DENSE>
+void seg_prepare() {
+  static const bool done = [] {
+    (void)hipFuncSetAttribute((const void *)&seg_kernel<SWIGLU, DENSE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              kSegLdsBytes);
+    return true;
+  }();
+  (void)done;
+}
+
 }  // namespace
 
 extern "C" int jit_moe_gate_up_swiglu_seg(const uint16_t *x, int K, const int32_t *pair_row,
@@ -234,7 +347,8 @@ extern "C" int jit_moe_gate_up_swiglu_seg(const uint16_t *x, int K, const int32_
     return jit::fail(JIT_EINVAL, "moe_gate_up_seg: null pointer");
   SegArgs a{x, pair_row, expert_cnt, expert_off, (const uint8_t *)packed, h, jit_q4_packed_bytes(1, 2 * I, K), K, I, 0,
             I / 128, E};
-  seg_kernel<true><<<seg_grid(a.nx, E), 256, 0, (hipStream_t)stream>>>(a);
+  seg_prepare<true, false>();
+  seg_kernel<true><<<seg_grid(a.nx, E), 256, kSegLdsBytes, (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_moe_gate_up_swiglu_seg");
 }
 
@@ -249,7 +363,8 @@ extern "C" int jit_moe_down_seg(const uint16_t *h, int I, const int32_t *expert_
   if (!h || !expert_cnt || !expert_off || !packed || !r) return jit::fail(JIT_EINVAL, "moe_down_seg: null pointer");
   SegArgs a{h, nullptr, expert_cnt, expert_off, (const uint8_t *)packed, r, jit_q4_packed_bytes(1, D, I), I, D, 0,
             D / kSegRows, E};
-  seg_kernel<false><<<seg_grid(a.nx, E), 256, 0, (hipStream_t)stream>>>(a);
+  seg_prepare<false, false>();
+  seg_kernel<false><<<seg_grid(a.nx, E), 256, kSegLdsBytes, (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_moe_down_seg");
 }
 
@@ -262,6 +377,7 @@ extern "C" int jit_qmm_seg(const uint16_t *x, int T, int K, const void *packed, 
   if (!x || !packed || !y) return jit::fail(JIT_EINVAL, "qmm_seg: null pointer");
   const int chunks = (T + kSegTokens - 1) / kSegTokens;
   SegArgs a{x, nullptr, nullptr, nullptr, (const uint8_t *)packed, y, 0, K, N, T, N / kSegRows, chunks};
-  seg_kernel<false, true><<<seg_grid(a.nx, chunks), 256, 0, (hipStream_t)stream>>>(a);
+  seg_prepare<false, true>();
+  seg_kernel<false, true><<<seg_grid(a.nx, chunks), 256, kSegLdsBytes, (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_qmm_seg");
 }
