@@ -41,6 +41,9 @@ struct QmmArgs {
   int rows_w;                      // weight rows per expert (2N with SWIGLU)
 };
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kXOutOfRange = 0x80000000u;  // a byte offset past the activation buffer's range
+
 using qtile::kNibbleBytes;
 using qtile::kScaleBytes;
 using qtile::kTileBytes;
@@ -79,10 +82,16 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   // x rows of the first pass's tokens, requested before the weights: vector loads
   // complete in order, so a row index loaded after the weights would hold the
   // activation loads back until every weight load had landed
+  // (as a byte offset into x for the activation loads; a token past the expert's count gets an
+  // offset past the buffer's range, whose loads return zeros without reading memory)
   auto x_row = [&](int tok) {
     const int pos = off + (tok < cnt ? tok : 0);
-    return a.row_index ? a.row_index[pos] : pos;
+    const int row = a.row_index ? a.row_index[pos] : pos;
+    return tok < cnt ? (int)((uint32_t)row * (uint32_t)a.K * 2u) : (int)kXOutOfRange;
   };
+  // activations through a buffer resource (2 GiB range: x holds fewer bytes), so that the lanes
+  // of padding tokens (a 16-token tile over an expert's ~2 decode tokens) fetch nothing
+  const __amdgpu_buffer_rsrc_t xbuf = __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, 0x00020000);
   int xrow0[TT];
 #pragma unroll
   for (int tt = 0; tt < TT; tt++) xrow0[tt] = x_row(tfirst + 16 * tt + lr);
@@ -146,17 +155,18 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   // with no merge of load paths in front of its activation loads)
   auto pass = [&](const int t0, const int (&xrows)[TT]) {
     // activation fragments (natural k order, as the unpacked weights); lanes past the
-    // last token load a valid row (no branch around the loads): they only feed output
-    // rows of tokens that are never stored
+    // last token load from outside the buffer's range (no branch around the loads): zeros,
+    // which feed only output rows of tokens that are never stored
     Frag8 xa[TT][GPW][2];
 #pragma unroll
     for (int tt = 0; tt < TT; tt++) {
-      const int xrow = xrows[tt];
-      const uint16_t *xr = a.x + (long long)xrow * a.K + 64 * g0 + 16 * lg;
+      const uint32_t xo = (uint32_t)xrows[tt] + 2u * (64 * g0 + 16 * lg);  // (out of range stays out)
 #pragma unroll
       for (int g = 0; g < GPW; g++) {
-        xa[tt][g][0].q = *(const uint4 *)(xr + 64 * g);
-        xa[tt][g][1].q = *(const uint4 *)(xr + 64 * g + 8);
+        const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(xbuf, xo + 128 * g, 0, 0);
+        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(xbuf, xo + 128 * g + 16, 0, 0);
+        xa[tt][g][0].q = make_uint4(v0.x, v0.y, v0.z, v0.w);
+        xa[tt][g][1].q = make_uint4(v1.x, v1.y, v1.z, v1.w);
       }
     }
     f32x4 acc[TT][NBW];
@@ -336,12 +346,17 @@ extern "C" int jit_q4_prepack(const uint32_t *w, const uint16_t *scales, const u
   return jit::check_launch("jit_q4_prepack");
 }
 
+// The kernels read activations through a buffer resource of a 2 GiB range (byte offsets in 32
+// bits, past-the-end offsets for padding tokens).
+static bool x_in_range(long long rows, int K) { return rows * K * 2 + 4096 < 0x7fffffffLL; }
+
 static int qmm_common(const uint16_t *x, int T, int K, int N, uint16_t *y, const char *what) {
   if (T < 0 || K <= 0 || N <= 0) return jit::fail(JIT_EINVAL, "%s: bad dims T=%d K=%d N=%d", what, T, K, N);
   if (K % 256 != 0 || N % 16 != 0 || K > 4096)
     return jit::fail(JIT_EUNSUPPORTED, "%s covers K %% 256 == 0, K <= 4096 and N %% 16 == 0, got K=%d N=%d",
                      what, K, N);
   if (T > 0 && (!x || !y)) return jit::fail(JIT_EINVAL, "%s: null pointer", what);
+  if (!x_in_range(T, K)) return jit::fail(JIT_EUNSUPPORTED, "%s: x of %d x %d bf16 exceeds 2 GiB", what, T, K);
   return JIT_OK;
 }
 
@@ -384,6 +399,8 @@ static int gate_up_check(const uint16_t *x, int K, const int32_t *pair_row, cons
     return jit::fail(JIT_EUNSUPPORTED, "moe_gate_up covers K %% 512 == 0, K <= 4096 and I %% 16 == 0, got K=%d I=%d",
                      K, I);
   if (P > 0 && (!x || !pair_row || !cnt || !off || !h)) return jit::fail(JIT_EINVAL, "moe_gate_up: null pointer");
+  if (!x_in_range(P, K))  // x has at most P rows (every row routes at least one pair)
+    return jit::fail(JIT_EUNSUPPORTED, "moe_gate_up: %d pairs of K=%d exceed the 2 GiB activation range", P, K);
   return JIT_OK;
 }
 
@@ -419,6 +436,7 @@ static int down_check(const uint16_t *h, int I, const int32_t *cnt, const int32_
     return jit::fail(JIT_EUNSUPPORTED, "moe_down covers I %% 256 == 0, I <= 2048 and D %% 16 == 0, got I=%d D=%d",
                      I, D);
   if (P > 0 && (!h || !cnt || !off || !r)) return jit::fail(JIT_EINVAL, "moe_down: null pointer");
+  if (!x_in_range(P, I)) return jit::fail(JIT_EUNSUPPORTED, "moe_down: h of %d x %d bf16 exceeds 2 GiB", P, I);
   return JIT_OK;
 }
 
