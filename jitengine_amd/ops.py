@@ -93,10 +93,17 @@ def moe_pack(inds: torch.Tensor, n_experts: int) -> Packing:
     """inds [B, k] int32 -> Packing: Q36/model/moe.py:151-159 (_sort_pairs) and
     FN/model/moe/expert_mlp.py:39-49,147-163 (segment tables) in one launch."""
     _need(inds, torch.int32, "inds")
-    k = inds.shape[-1]
-    P = inds.numel()
-    E = int(n_experts)
-    pk = _packing_buffers(P, k, E, inds.device)
+    pk = _packing_buffers(inds.numel(), inds.shape[-1], int(n_experts), inds.device)
+    moe_pack_into(inds, pk)
+    return pk
+
+
+def moe_pack_into(inds: torch.Tensor, pk: Packing) -> None:
+    """moe_pack into the tables pk (sized for inds: P = inds.numel(), k = inds.shape[-1])."""
+    _need(inds, torch.int32, "inds")
+    k, P, E = pk.k, pk.P, pk.E
+    if inds.numel() != P or inds.shape[-1] != k:
+        raise ValueError(f"packing tables of {P} pairs x k={k} do not fit inds {tuple(inds.shape)}")
     _lib.check(
         _lib.lib().jit_moe_pack(
             _p(inds), P, k, E, _p(pk.order), _p(pk.pair_row), _p(pk.inv), _p(pk.expert_cnt),
@@ -105,7 +112,6 @@ def moe_pack(inds: torch.Tensor, n_experts: int) -> Packing:
         ),
         "moe_pack",
     )
-    return pk
 
 
 ROUTE_PACK_MAX_ROWS = 4

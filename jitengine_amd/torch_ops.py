@@ -1,0 +1,213 @@
+"""The hot path's operators registered with torch as torch.ops.jitengine.* (torch.library custom
+ops), the form the survey of the reference names for this boundary: the same C-ABI calls as
+jitengine_amd.ops, each with a fake kernel that gives its output shapes and dtypes without
+running it, so that torch.compile traces through the operators instead of breaking its graph at
+an opaque ctypes call, and meta/fake tensors propagate through them.
+
+Host-side structures of jitengine_amd.ops are passed as their tensors and sizes:
+  * a packed 4-bit matrix or expert stack (ops.PackedQ4) as its uint8 tensor and (E, N, K);
+  * the packing tables (ops.Packing) as the single int32 buffer moe_pack returns, with (k, E);
+  * a decode attention plan (ops.AttnPlan) as its three int32 tensors, its chunk count and the
+    longest sequence.
+Importing this module registers the operators; it needs the HIP library only when one runs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import ops
+
+_NS = "jitengine"
+
+
+def _packed(data: torch.Tensor, E: int, N: int, K: int) -> ops.PackedQ4:
+    return ops.PackedQ4(data, E, N, K, E > 1)
+
+
+def packing_from_buffer(buf: torch.Tensor, k: int, E: int) -> ops.Packing:
+    """The packing tables over moe_pack's int32 buffer [3 P + 5 E + 4] (views, no copy)."""
+    P = (buf.shape[0] - 5 * E - 4) // 3
+    parts = torch.split(buf, [P, P, P, E, E, E, E, E, 4])
+    return ops.Packing(*parts, P=P, k=k, E=E)
+
+
+# ----------------------------------------------------------------------------- router
+@torch.library.custom_op(f"{_NS}::router_topk", mutates_args=())
+def router_topk(logits: torch.Tensor, k: int, norm: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """(inds int32 [B, k], scores bf16 [B, k]) of router logits [B, E] (jit_router_topk)."""
+    return ops.router_topk(logits, k, norm)
+
+
+@router_topk.register_fake
+def _(logits, k, norm):
+    B = logits.shape[0]
+    return logits.new_empty((B, k), dtype=torch.int32), logits.new_empty((B, k), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{_NS}::moe_pack", mutates_args=())
+def moe_pack(inds: torch.Tensor, n_experts: int) -> torch.Tensor:
+    """The packing tables of inds [B, k] as one int32 buffer [3 P + 5 E + 4] (jit_moe_pack;
+    packing_from_buffer splits it)."""
+    P, E = inds.numel(), int(n_experts)
+    buf = torch.empty(3 * P + 5 * E + 4, dtype=torch.int32, device=inds.device)
+    ops.moe_pack_into(inds, packing_from_buffer(buf, inds.shape[-1], E))
+    return buf
+
+
+@moe_pack.register_fake
+def _(inds, n_experts):
+    P = inds.shape[0] * inds.shape[1]
+    return inds.new_empty((3 * P + 5 * n_experts + 4,), dtype=torch.int32)
+
+
+# ----------------------------------------------------------------------------- experts
+@torch.library.custom_op(f"{_NS}::expert_gate_up", mutates_args=())
+def expert_gate_up(x: torch.Tensor, packed: torch.Tensor, E: int, N: int, K: int, pack_buf: torch.Tensor,
+                   k: int, seg: bool) -> torch.Tensor:
+    """h bf16 [P, N / 2] of the fused gate||up stack [E, N, K] with SwiGLU, in sorted pair order
+    (jit_moe_gate_up_swiglu_packed, or the segment GEMM with seg)."""
+    return ops.expert_gate_up(x, _packed(packed, E, N, K), packing_from_buffer(pack_buf, k, E), seg=seg)
+
+
+@expert_gate_up.register_fake
+def _(x, packed, E, N, K, pack_buf, k, seg):
+    P = (pack_buf.shape[0] - 5 * E - 4) // 3
+    return x.new_empty((P, N // 2), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{_NS}::expert_down", mutates_args=())
+def expert_down(h: torch.Tensor, packed: torch.Tensor, E: int, N: int, K: int, pack_buf: torch.Tensor, k: int,
+                seg: bool) -> torch.Tensor:
+    """r bf16 [P, N] of the down stack [E, N, K] in sorted pair order (jit_moe_down_packed, or
+    the segment GEMM with seg)."""
+    return ops.expert_down(h, _packed(packed, E, N, K), packing_from_buffer(pack_buf, k, E), seg=seg)
+
+
+@expert_down.register_fake
+def _(h, packed, E, N, K, pack_buf, k, seg):
+    return h.new_empty((h.shape[0], N), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{_NS}::moe_combine", mutates_args=())
+def moe_combine(r: torch.Tensor, pack_buf: torch.Tensor, k: int, E: int, scores: torch.Tensor,
+                resid: torch.Tensor | None) -> torch.Tensor:
+    """y bf16 [B, D]: the slot-order weighted sum of the pair rows r, plus resid (jit_moe_combine)."""
+    return ops.moe_combine(r, packing_from_buffer(pack_buf, k, E), scores, resid)
+
+
+@moe_combine.register_fake
+def _(r, pack_buf, k, E, scores, resid):
+    return r.new_empty((scores.shape[0], r.shape[1]), dtype=torch.bfloat16)
+
+
+# ----------------------------------------------------------------------------- dense, norms
+@torch.library.custom_op(f"{_NS}::qmm", mutates_args=())
+def qmm(x: torch.Tensor, packed: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    """x [T, K] bf16 against a packed 4-bit matrix [N, K] (jit_qmm_packed, or jit_qmm_seg for a
+    long batch)."""
+    return ops.qmm(x, _packed(packed, 1, N, K))
+
+
+@qmm.register_fake
+def _(x, packed, N, K):
+    return x.new_empty((x.shape[0], N), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{_NS}::rmsnorm", mutates_args=())
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm rows of x (jit_rmsnorm)."""
+    return ops.rmsnorm(x, w, eps)
+
+
+@rmsnorm.register_fake
+def _(x, w, eps):
+    return torch.empty_like(x)
+
+
+# ----------------------------------------------------------------------------- attention
+@torch.library.custom_op(f"{_NS}::qk_norm_rope_append", mutates_args=("pool",))
+def qk_norm_rope_append(qkv: torch.Tensor, H: int, Hkv: int, q_norm: torch.Tensor, k_norm: torch.Tensor,
+                        eps: float, inv_freq: torch.Tensor, pos: torch.Tensor, page_table: torch.Tensor,
+                        pool: torch.Tensor) -> torch.Tensor:
+    """q bf16 [B, H, 128] (normed, rotated); k and v of every row written into the pool
+    (jit_qk_norm_rope_append)."""
+    return ops.qk_norm_rope_append(qkv, H, Hkv, q_norm, k_norm, eps, inv_freq, pos, page_table, pool)
+
+
+@qk_norm_rope_append.register_fake
+def _(qkv, H, Hkv, q_norm, k_norm, eps, inv_freq, pos, page_table, pool):
+    return qkv.new_empty((qkv.shape[0], H, ops.HEAD_DIM), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{_NS}::paged_decode_attention", mutates_args=("workspace",))
+def paged_decode_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor, lens: torch.Tensor,
+                           chunk_start: torch.Tensor, chunk_seq: torch.Tensor, total: int, max_len: int,
+                           scale: float, workspace: torch.Tensor) -> torch.Tensor:
+    """out bf16 [B, H, 128] of split-K paged decode attention under an attention plan given by its
+    tensors (jit_paged_decode_attn; workspace of attn_workspace_bytes(total, H) bytes)."""
+    plan = ops.AttnPlan(lens, chunk_start, chunk_seq, int(total), np.array([int(max_len)], np.int32))
+    return ops.paged_decode_attention(q, pool, page_table, plan, scale, workspace)
+
+
+@paged_decode_attention.register_fake
+def _(q, pool, page_table, lens, chunk_start, chunk_seq, total, max_len, scale, workspace):
+    return torch.empty_like(q)
+
+
+def plan_args(plan: ops.AttnPlan) -> tuple:
+    """(lens, chunk_start, chunk_seq, total, max_len) of an attention plan, for
+    torch.ops.jitengine.paged_decode_attention."""
+    mx = int(plan.lens_host.max()) if plan.lens_host.size else 0
+    return plan.lens, plan.chunk_start, plan.chunk_seq, plan.total, mx
+
+
+# ----------------------------------------------------------------------------- sampler
+@torch.library.custom_op(f"{_NS}::logprobs_rows", mutates_args=())
+def logprobs_rows(logits: torch.Tensor) -> torch.Tensor:
+    """bf16 [B, V] log-probabilities (jit_logprobs_rows)."""
+    return ops.logprobs_rows(logits)
+
+
+@logprobs_rows.register_fake
+def _(logits):
+    return torch.empty_like(logits)
+
+
+@torch.library.custom_op(f"{_NS}::argmax_rows", mutates_args=())
+def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
+    """int32 [B] greedy draws (jit_argmax_rows)."""
+    return ops.argmax_rows(logits)
+
+
+@argmax_rows.register_fake
+def _(logits):
+    return logits.new_empty((logits.shape[0],), dtype=torch.int32)
+
+
+@torch.library.custom_op(f"{_NS}::sample_rows", mutates_args=())
+def sample_rows(logits: torch.Tensor, temperature: float, top_p: float, top_k: int, u: torch.Tensor) -> torch.Tensor:
+    """int32 [B] draws under shared temperature / top-p / top-k given uniforms u [B] (jit_sample_rows)."""
+    return ops.sample_rows(logits, temperature, top_p, top_k, u)
+
+
+@sample_rows.register_fake
+def _(logits, temperature, top_p, top_k, u):
+    return logits.new_empty((logits.shape[0],), dtype=torch.int32)
+
+
+@torch.library.custom_op(f"{_NS}::threefry_uniform", mutates_args=())
+def threefry_uniform(keys: torch.Tensor) -> torch.Tensor:
+    """fp32 [B] uniforms of uint32 key pairs [B, 2] (jit_threefry_uniform)."""
+    return ops.threefry_uniform(keys)
+
+
+@threefry_uniform.register_fake
+def _(keys):
+    return keys.new_empty((keys.shape[0],), dtype=torch.float32)
+
+
+OPS = ("router_topk", "moe_pack", "expert_gate_up", "expert_down", "moe_combine", "qmm", "rmsnorm",
+       "qk_norm_rope_append", "paged_decode_attention", "logprobs_rows", "argmax_rows", "sample_rows",
+       "threefry_uniform")

@@ -1,0 +1,74 @@
+"""torch.ops.jitengine.* registration (jitengine_amd/torch_ops.py) on the CPU: every operator is
+registered, and its fake kernel propagates shapes and dtypes through meta tensors without the
+HIP library (what torch.compile's tracing relies on)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from jitengine_amd import torch_ops
+
+J = None
+
+
+def setup_module():
+    global J
+    J = torch.ops.jitengine
+
+
+def _m(shape, dtype):
+    return torch.empty(shape, dtype=dtype, device="meta")
+
+
+def test_every_operator_is_registered():
+    for name in torch_ops.OPS:
+        assert hasattr(J, name), name
+
+
+def test_router_pack_and_experts_propagate_shapes():
+    B, E, k, D, I = 32, 128, 8, 2048, 768
+    inds, scores = J.router_topk(_m((B, E), torch.bfloat16), k, True)
+    assert inds.shape == (B, k) and inds.dtype == torch.int32 and scores.dtype == torch.bfloat16
+    buf = J.moe_pack(inds, E)
+    P = B * k
+    assert buf.shape == (3 * P + 5 * E + 4,) and buf.dtype == torch.int32
+    pk = torch_ops.packing_from_buffer(buf, k, E)
+    assert pk.P == P and pk.order.shape == (P,) and pk.expert_cnt.shape == (E,) and pk.meta.shape == (4,)
+    h = J.expert_gate_up(_m((B, D), torch.bfloat16), _m((1000,), torch.uint8), E, 2 * I, D, buf, k, False)
+    assert h.shape == (P, I) and h.dtype == torch.bfloat16
+    r = J.expert_down(h, _m((1000,), torch.uint8), E, D, I, buf, k, True)
+    assert r.shape == (P, D)
+    y = J.moe_combine(r, buf, k, E, scores, _m((B, D), torch.bfloat16))
+    assert y.shape == (B, D) and y.dtype == torch.bfloat16
+
+
+def test_dense_attention_and_sampler_propagate_shapes():
+    B, H, Hkv, D, V = 4, 32, 4, 2048, 1000
+    assert J.qmm(_m((B, D), torch.bfloat16), _m((10,), torch.uint8), 5120, D).shape == (B, 5120)
+    assert J.rmsnorm(_m((B, D), torch.bfloat16), _m((D,), torch.bfloat16), 1e-6).shape == (B, D)
+    pool = _m((64, Hkv, 2, 2048), torch.bfloat16)
+    q = J.qk_norm_rope_append(_m((B, (H + 2 * Hkv) * 128), torch.bfloat16), H, Hkv, _m((128,), torch.bfloat16),
+                              _m((128,), torch.bfloat16), 1e-6, _m((64,), torch.float32), _m((B,), torch.int32),
+                              _m((B, 16), torch.int32), pool)
+    assert q.shape == (B, H, 128)
+    out = J.paged_decode_attention(q, pool, _m((B, 16), torch.int32), _m((B,), torch.int32),
+                                   _m((B + 1,), torch.int32), _m((8,), torch.int32), 8, 200, 128 ** -0.5,
+                                   _m((1 << 16,), torch.uint8))
+    assert out.shape == (B, H, 128) and out.dtype == torch.bfloat16
+    x = _m((B, V), torch.bfloat16)
+    assert J.logprobs_rows(x).shape == (B, V)
+    assert J.argmax_rows(x).dtype == torch.int32
+    assert J.sample_rows(x, 0.7, 0.9, 40, _m((B,), torch.float32)).shape == (B,)
+    assert J.threefry_uniform(_m((B, 2), torch.int32)).dtype == torch.float32
+
+
+def test_packing_buffer_split_matches_the_library_layout():
+    from jitengine_amd import ops
+
+    buf = torch.arange(3 * 24 + 5 * 16 + 4, dtype=torch.int32)
+    pk = torch_ops.packing_from_buffer(buf, 8, 16)
+    ref = ops._packing_buffers(24, 8, 16, "cpu")
+    for name in ("order", "pair_row", "inv", "expert_cnt", "expert_off", "seg_expert", "seg_start", "seg_cnt", "meta"):
+        assert getattr(pk, name).shape == getattr(ref, name).shape, name
+    assert int(pk.expert_cnt[0]) == 3 * 24 and int(pk.meta[0]) == 3 * 24 + 5 * 16
