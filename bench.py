@@ -657,7 +657,7 @@ def probe(dev: str, parts=("read", "launch", "barrier")) -> int:
         torch.cuda.synchronize()
         return s.elapsed_time(e) / reps  # ms
 
-    out = {"read": {}, "launch": {}, "barrier": {}, "lds_ring": {}}
+    out = {"read": {}, "launch": {}, "barrier": {}, "lds_ring": {}, "gemv": {}}
     if "lds" in parts:
         # streaming through an LDS ring by direct loads, one persistent workgroup per CU, over 48
         # rotating 196 MB windows (the expert weights' volume)
@@ -703,6 +703,41 @@ def probe(dev: str, parts=("read", "launch", "barrier")) -> int:
             out["read"][f"{name}_2048waves"] = round(waves * run * 8192 / (ms * 1e-3) / 1e9, 1)
         del buf, perm
         torch.cuda.empty_cache()
+
+    if "gemv" in parts:
+        # the gate||up expert GEMV's load shape without its arithmetic, against the kernel itself, on
+        # config 2's routing regime (32 tokens x top-8 over 128 experts), rotating over 4 layers'
+        # stacks so that HBM serves the weights
+        from jitengine_amd import ops
+        from jitengine_amd.quant import random_quantized
+
+        lib.probe_gemv.argtypes = [P, P, LL, I, I, I, P, I, P, P]
+        E, N, K, B, k = 128, 768, 2048, 32, 8
+        stacks = [ops.prepack(random_quantized((E, 2 * N, K), 900 + i, device=dev)) for i in range(4)]
+        estride = stacks[0].nbytes // E
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(7)
+        inds = torch.randn((B, E), generator=gen, device=dev).topk(k, dim=1).indices.to(torch.int32).contiguous()
+        pk = ops.moe_pack(inds, E)
+        cnt = pk.expert_cnt
+        active = int((cnt > 0).sum())
+        x = (torch.randn((B, K), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+        sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+        alg = active * estride
+        res = {"active_experts": active, "MB_per_launch": round(alg / 1e6, 1)}
+        for mode, name in ((0, "weights_only"), (1, "weights_and_x")):
+            def rot(mode=mode):
+                for st_ in stacks:
+                    lib.probe_gemv(ctypes.c_void_p(st_.data.data_ptr()), ctypes.c_void_p(cnt.data_ptr()), estride, E,
+                                   N, K, ctypes.c_void_p(x.data_ptr()), mode, ctypes.c_void_p(sink.data_ptr()), sp)
+            ms = timed(rot, 20) / len(stacks)
+            res[f"{name}_us"] = round(ms * 1e3, 2)
+            res[f"{name}_GB_s"] = round(alg / (ms * 1e-3) / 1e9, 1)
+        ms = timed(lambda: [ops.expert_gate_up(x, st_, pk) for st_ in stacks], 20) / len(stacks)
+        res["kernel_us"] = round(ms * 1e3, 2)
+        res["kernel_GB_s"] = round(alg / (ms * 1e-3) / 1e9, 1)
+        out["gemv"] = res
+        del stacks
 
     if "launch" in parts:
         g = torch.cuda.CUDAGraph()

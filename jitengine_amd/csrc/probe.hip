@@ -1,5 +1,6 @@
 // Measurement kernels of the benchmark (not part of the hot path's C-ABI): the HBM
-// streaming-read ceiling the hot-path kernels are rated against, the device cost of an empty
+// streaming-read ceiling the hot-path kernels are rated against, the expert GEMV's load shape
+// without its arithmetic, the device cost of an empty
 // launch inside a HIP graph, and the cost of a grid-wide barrier between the phases of one
 // persistent launch (the alternative to a launch per phase).  Built into their own library,
 // libjit_probe.so, which only bench.py loads.
@@ -171,7 +172,70 @@ __global__ __launch_bounds__(64 * L) void probe_lds_ring_kernel(const uint8_t *_
   if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;  // keeps the reads alive
 }
 
+// The gate||up expert GEMV's loads without its arithmetic: the grid, waves and per-wave slices
+// of the packed-layout gate||up kernel (one workgroup per 16 output columns and expert, 4 waves
+// splitting K into slices of 8 groups; per wave the gate block's and the up block's 4 nibble
+// tiles and their scale pieces, 9 KB), workgroups of inactive experts exiting at once.  MODE 1
+// also loads each wave's activation fragments of one 16-token tile (the rows of `cnt` tokens,
+// zeros past them) as the kernel does.
+template <int MODE>
+__global__ __launch_bounds__(256) void probe_gemv_kernel(const uint8_t *__restrict__ w, const int *__restrict__ cnt,
+                                                          long long estride, int N, int K, const uint16_t *x,
+                                                          uint32_t *__restrict__ sink) {
+  constexpr int GPW = 8, kNib = 1024, kScl = 128;
+  const int e = blockIdx.y;
+  const int c = cnt[e];
+  if (c <= 0) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
+  const int lr = l & 15, lg = l >> 4;
+  const int GP = K >> 7, g0 = wave * GPW;
+  uint32_t acc = 0;
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  u32x4 q[2][GPW / 2];
+  u32x2 sb[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; rb++) {
+    const int rowb = (rb ? N : 0) + blockIdx.x * 16;
+    const uint8_t *blk = w + (long long)e * estride + (long long)(rowb >> 4) * GP * (kNib + kScl);
+    sb[rb] = __builtin_nontemporal_load((const u32x2 *)(blk + (long long)GP * kNib + ((g0 >> 1) + min(lg, GPW / 2 - 1)) * kScl + 8 * lr));
+#pragma unroll
+    for (int j = 0; j < GPW / 2; j++)
+      q[rb][j] = __builtin_nontemporal_load((const u32x4 *)(blk + ((g0 >> 1) + j) * kNib + 16 * l));
+  }
+  if (MODE == 1) {
+    const __amdgpu_buffer_rsrc_t xb = __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, 0x7fffffff, 0x00020000);
+    const uint32_t xo = lr < c ? (uint32_t)(lr * K * 2 + 2 * (64 * g0 + 16 * lg)) : 0x80000000u;
+#pragma unroll
+    for (int g = 0; g < GPW; g++) {
+      const u32x4 a0 = __builtin_amdgcn_raw_buffer_load_b128(xb, xo + 128 * g, 0, 0);
+      const u32x4 a1 = __builtin_amdgcn_raw_buffer_load_b128(xb, xo + 128 * g + 16, 0, 0);
+      acc ^= a0.x ^ a1.w;
+    }
+  }
+#pragma unroll
+  for (int rb = 0; rb < 2; rb++) {
+    acc ^= sb[rb].x ^ sb[rb].y;
+#pragma unroll
+    for (int j = 0; j < GPW / 2; j++) acc ^= q[rb][j].x ^ q[rb][j].y ^ q[rb][j].z ^ q[rb][j].w;
+  }
+  if (acc == 0x9e3779b9u) sink[blockIdx.y] = acc;  // keeps the loads alive
+}
+
 }  // namespace
+
+// One launch of the gate||up GEMV's load shape over a packed stack [E, 2N, K] (estride bytes per
+// expert), the expert token counts cnt[E] (device), x [16, K] bf16 for MODE 1.
+extern "C" int probe_gemv(const void *w, const int *cnt, long long estride, int E, int N, int K, const void *x,
+                          int mode, uint32_t *sink, void *stream) {
+  if (!w || !cnt || !sink || E <= 0 || N % 16 || K % 1024 || mode < 0 || mode > 1 || (mode == 1 && !x)) return -1;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(N / 16, E);
+  if (mode == 0)
+    probe_gemv_kernel<0><<<grid, 256, 0, st>>>((const uint8_t *)w, cnt, estride, N, K, (const uint16_t *)x, sink);
+  else
+    probe_gemv_kernel<1><<<grid, 256, 0, st>>>((const uint8_t *)w, cnt, estride, N, K, (const uint16_t *)x, sink);
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
 
 extern "C" int probe_read(const void *p, long long bytes, int mode, int blocks, uint32_t *sink, void *stream) {
   if (!p || !sink || bytes < 16 || blocks <= 0 || mode < 0 || mode > 3) return -1;
