@@ -39,9 +39,16 @@ struct QmmArgs {
   long long w_estride, g_estride;  // per expert: 32-bit words and bf16 entries (MLX layout), or
                                    // bytes of tiles (packed layout; g_estride unused)
   int rows_w;                      // weight rows per expert (2N with SWIGLU)
+  int E;                           // experts of the stack (the grid may have fewer rows)
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
 constexpr uint32_t kXOutOfRange = 0x80000000u;  // a byte offset past the activation buffer's range
 
 using qtile::kNibbleBytes;
@@ -53,7 +60,7 @@ using qtile::unpack_nibbles;
 
 using qtile::swiglu_bf16;
 
-template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1>
+template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false>
 __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   static_assert(!PACKED || GPW % 2 == 0, "packed tiles hold pairs of groups");
   constexpr int NBW = SWIGLU ? 2 * NB : NB;  // weight row blocks (gate and up blocks with SWIGLU)
@@ -61,11 +68,36 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   const int ksplit = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
   const int lr = l & 15, lg = l >> 4;
-  const int e = blockIdx.y;
-  int cnt, off;
-  if (a.cnt) {
+  int e = 0, cnt, off;
+  if (a.cnt && !COMPACT) {
+    e = blockIdx.y;
     cnt = a.cnt[e];
     off = a.off[e];
+  } else if (a.cnt) {
+    // COMPACT (a step of P < E pairs, min(E, P) grid rows): workgroup row y takes the y-th
+    // expert that has pairs (experts in id order), so such a step launches no workgroups for
+    // idle experts.  Its offset is the pairs of the experts before it (the packing sorts pairs
+    // by expert).  (A grid of E rows keeps the direct lookup: every wave of a full grid reading
+    // all the counts would crowd the one L2 channel that holds them.)
+    const int y = blockIdx.y;
+    int seen = 0, before = 0;
+    e = -1;
+    for (int base = 0; base < a.E; base += 64) {  // uniform loop
+      const int c = base + l < a.E ? a.cnt[base + l] : 0;
+      const unsigned long long m = __ballot(c > 0);
+      const int n = __popcll(m);
+      if (y < seen + n) {
+        const int rank = __popcll(m & ((1ull << l) - 1ull));
+        const int bit = __ffsll((long long)__ballot(c > 0 && rank == y - seen)) - 1;
+        e = base + bit;
+        cnt = __builtin_amdgcn_readlane(c, bit);
+        off = before + wave_sum_i(l < bit ? c : 0);
+        break;
+      }
+      seen += n;
+      before += wave_sum_i(c);
+    }
+    if (e < 0) return;  // fewer experts with pairs than grid rows (uniform over the workgroup)
   } else {
     cnt = a.T;
     off = 0;
@@ -238,7 +270,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   }
 }
 
-template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1>
+template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false>
 int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what, int zsplit = 1) {
   constexpr int NBW = SWIGLU ? 2 * NB : NB;
   const int G = a.K / 64;
@@ -247,7 +279,7 @@ int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what, int zs
     return jit::fail(JIT_EUNSUPPORTED, "%s: K=%d does not split into %d-group wave slices", what, a.K, GPW);
   const dim3 grid((a.N + 16 * NB - 1) / (16 * NB), E, zsplit), block(64 * ksplit);
   const size_t lds = (size_t)ksplit * TT * NBW * 4 * 64 * sizeof(float);
-  qmm_kernel<NB, GPW, SWIGLU, PACKED, TT><<<grid, block, lds, st>>>(a);
+  qmm_kernel<NB, GPW, SWIGLU, PACKED, TT, COMPACT><<<grid, block, lds, st>>>(a);
   return jit::check_launch(what);
 }
 
@@ -413,7 +445,8 @@ extern "C" int jit_moe_gate_up_swiglu(const uint16_t *x, int K, const int32_t *p
   if (P == 0) return JIT_OK;
   if (!w || !scales || !biases) return jit::fail(JIT_EINVAL, "moe_gate_up: null pointer");
   QmmArgs a{x, pair_row, expert_cnt, expert_off, w, scales, biases, h, K, I, 0,
-            (long long)2 * I * (K / 8), (long long)2 * I * (K / 64), 2 * I};
+            (long long)2 * I * (K / 8), (long long)2 * I * (K / 64), 2 * I, E};
+  if (P < E) return launch_qmm<1, kGuGpw, true, false, 1, true>(a, P, (hipStream_t)stream, "jit_moe_gate_up_swiglu");
   return launch_qmm<1, kGuGpw, true, false>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu");
 }
 
@@ -424,7 +457,8 @@ extern "C" int jit_moe_gate_up_swiglu_packed(const uint16_t *x, int K, const int
   if (P == 0) return JIT_OK;
   if (!packed) return jit::fail(JIT_EINVAL, "moe_gate_up_packed: null pointer");
   QmmArgs a{x, pair_row, expert_cnt, expert_off, (const uint32_t *)packed, nullptr, nullptr, h, K, I, 0,
-            jit_q4_packed_bytes(1, 2 * I, K), 0, 2 * I};
+            jit_q4_packed_bytes(1, 2 * I, K), 0, 2 * I, E};
+  if (P < E) return launch_qmm<1, kGuGpw, true, true, 1, true>(a, P, (hipStream_t)stream, "jit_moe_gate_up_swiglu_packed");
   return launch_qmm<1, kGuGpw, true, true>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu_packed");
 }
 
@@ -448,7 +482,8 @@ extern "C" int jit_moe_down(const uint16_t *h, int I, const int32_t *expert_cnt,
   if (P == 0) return JIT_OK;
   if (!w || !scales || !biases) return jit::fail(JIT_EINVAL, "moe_down: null pointer");
   QmmArgs a{h, nullptr, expert_cnt, expert_off, w, scales, biases, r, I, D, 0,
-            (long long)D * (I / 8), (long long)D * (I / 64), D};
+            (long long)D * (I / 8), (long long)D * (I / 64), D, E};
+  if (P < E) return launch_qmm<kDnNb, kDnGpw, false, false, 1, true>(a, P, (hipStream_t)stream, "jit_moe_down");
   return launch_qmm<kDnNb, kDnGpw, false, false>(a, E, (hipStream_t)stream, "jit_moe_down");
 }
 
@@ -459,6 +494,7 @@ extern "C" int jit_moe_down_packed(const uint16_t *h, int I, const int32_t *expe
   if (P == 0) return JIT_OK;
   if (!packed) return jit::fail(JIT_EINVAL, "moe_down_packed: null pointer");
   QmmArgs a{h, nullptr, expert_cnt, expert_off, (const uint32_t *)packed, nullptr, nullptr, r, I, D, 0,
-            jit_q4_packed_bytes(1, D, I), 0, D};
+            jit_q4_packed_bytes(1, D, I), 0, D, E};
+  if (P < E) return launch_qmm<kDnNb, kDnGpw, false, true, 1, true>(a, P, (hipStream_t)stream, "jit_moe_down_packed");
   return launch_qmm<kDnNb, kDnGpw, false, true>(a, E, (hipStream_t)stream, "jit_moe_down_packed");
 }
