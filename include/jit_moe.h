@@ -91,6 +91,20 @@ int jit_moe_pack(const uint32_t *inds, int P, int k, int E, int32_t *order, int3
                  int32_t *inv, int32_t *expert_cnt, int32_t *expert_off, int32_t *seg_expert,
                  int32_t *seg_start, int32_t *seg_cnt, int32_t *meta, void *stream);
 
+/* Bytes of device workspace jit_moe_pack_ws takes for P pairs over E experts: 4 (E + 1) per tile of
+ * 1024 pairs when P > 2048 and E < 1024, else 0 (no workspace needed). */
+long long jit_moe_pack_workspace_bytes(int P, int E);
+
+/* jit_moe_pack with a device workspace of jit_moe_pack_workspace_bytes(P, E) bytes (contents on
+ * entry do not matter): a long batch (a chunked-prefill step's B * k pairs,
+ * Q36/model/moe.py:151-159 over the prefill rows) is packed by many workgroups in three launches
+ * -- per-tile expert counts, one scan, per-tile placement -- instead of one workgroup walking every
+ * tile.  The same tables, bit for bit (the stable order is unique).  With a workspace of 0 bytes
+ * needed it is jit_moe_pack; a smaller workspace than needed returns JIT_EINVAL. */
+int jit_moe_pack_ws(const uint32_t *inds, int P, int k, int E, int32_t *order, int32_t *pair_row, int32_t *inv,
+                    int32_t *expert_cnt, int32_t *expert_off, int32_t *seg_expert, int32_t *seg_start,
+                    int32_t *seg_cnt, int32_t *meta, void *workspace, long long workspace_bytes, void *stream);
+
 /* The router top-k of at most 4 rows followed by their packing, in one launch: the same
  * outputs, bit for bit, as jit_router_topk (inds [rows, k], scores) then jit_moe_pack over
  * P = rows * k pairs of E = N experts (their two contracts, plus rows <= 4 and N <= 128:

@@ -28,6 +28,8 @@ _SIGNATURES = {
     "jit_router_topk": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "jit_topk": [_P, _I, _I, _I, _P, _P],
     "jit_moe_pack": [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "jit_moe_pack_workspace_bytes": [_I, _I],
+    "jit_moe_pack_ws": [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int64, _P],
     "jit_route_pack": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "jit_q4_packed_bytes": [_I, _I, _I],
     "jit_q4_prepack": [_P, _P, _P, _I, _I, _I, _P, _P],
@@ -61,7 +63,7 @@ _SIGNATURES = {
     "jit_kv_copy_pages": [_P, _I, _I, _P, _P, _I, _P],
 }
 _RESTYPES = {"jit_last_error": ctypes.c_char_p, "jit_attn_workspace_bytes": ctypes.c_int64,
-             "jit_q4_packed_bytes": ctypes.c_int64}
+             "jit_q4_packed_bytes": ctypes.c_int64, "jit_moe_pack_workspace_bytes": ctypes.c_int64}
 
 _lib = None
 

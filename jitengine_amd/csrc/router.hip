@@ -167,13 +167,6 @@ int launch_router(const uint16_t *src, int rows, int N, int k, int norm, uint32_
 }
 
 // --------------------------------------------------------------- packing
-// One workgroup (128, 256 or 1024 threads).  (1) per-expert counts in LDS; (2) exclusive
-// scans give each expert's first sorted position and the ascending list of
-// non-empty experts; (3) pairs are placed in tiles of the workgroup's size in flat order: within
-// a wave, lanes holding the same expert id find each other with ballots over
-// the id's bits, so a pair's position is its expert's running offset plus the
-// pairs of that expert in earlier waves of the tile plus its rank among its own
-// wave's lanes -- a stable counting sort.
 constexpr int kPackThreads = 1024;  // the largest workgroup (and expert count) of the packing
 
 __device__ __forceinline__ int wave_incl_scan(int x, int l) {
@@ -185,32 +178,17 @@ __device__ __forceinline__ int wave_incl_scan(int x, int l) {
   return x;
 }
 
-// The packing, run by one workgroup of TH threads (TH >= E); ind(p) is flat pair p's
-// expert id.
-template <int TH, typename IndFn>
-__device__ __forceinline__ void pack_body(IndFn ind, int P, int k, int E, int32_t *__restrict__ order,
-                                          int32_t *__restrict__ pair_row, int32_t *__restrict__ inv,
-                                          int32_t *__restrict__ expert_cnt, int32_t *__restrict__ expert_off,
-                                          int32_t *__restrict__ seg_expert, int32_t *__restrict__ seg_start,
-                                          int32_t *__restrict__ seg_cnt, int32_t *__restrict__ meta) {
-  __shared__ int cnt[TH];
-  __shared__ int nxt[TH];
-  __shared__ unsigned short wcnt[(TH / 64)][TH];
+// The per-expert tables from each expert's pair count c (thread t: expert t, t < E; threads past
+// E pass c = 0): counts, first sorted positions, the ascending list of non-empty experts (their
+// segments) and meta = (segments, largest segment, bad pairs, 0).  nxt[t] receives expert t's
+// first position.  One workgroup of TH >= E threads.
+template <int TH>
+__device__ __forceinline__ void pack_tables(int c, int bad, int E, int *nxt, int32_t *__restrict__ expert_cnt,
+                                            int32_t *__restrict__ expert_off, int32_t *__restrict__ seg_expert,
+                                            int32_t *__restrict__ seg_start, int32_t *__restrict__ seg_cnt,
+                                            int32_t *__restrict__ meta) {
   __shared__ int wsum[(TH / 64)], wflag[(TH / 64)], wmax[(TH / 64)];
-  __shared__ int bad;
   const int t = threadIdx.x, w = t >> 6, l = t & 63;
-  cnt[t] = 0;
-  if (t == 0) bad = 0;
-  __syncthreads();
-  for (int p = t; p < P; p += TH) {
-    const uint32_t e = ind(p);
-    if (e < (uint32_t)E)
-      atomicAdd(&cnt[e], 1);
-    else
-      atomicAdd(&bad, 1);
-  }
-  __syncthreads();
-  const int c = cnt[t];
   const int f = c > 0 ? 1 : 0;
   const int cs = wave_incl_scan(c, l);
   const int fs = wave_incl_scan(f, l);
@@ -250,42 +228,141 @@ __device__ __forceinline__ void pack_body(IndFn ind, int P, int k, int E, int32_
     meta[2] = bad;
     meta[3] = 0;
   }
-  const int nbits = 32 - __clz(E);  // enough bits for ids 0..E (E = "no expert")
-  for (int base = 0; base < P; base += TH) {
-    const int p = base + t;
-    uint32_t e = p < P ? ind(p) : (uint32_t)E;
-    if (e > (uint32_t)E) e = (uint32_t)E;
-    unsigned long long m = ~0ull;
-    for (int bt = 0; bt < nbits; bt++) {
-      const int bit = (e >> bt) & 1u;
-      const unsigned long long bal = __ballot(bit);
-      m &= bit ? bal : ~bal;
-    }
-    const int rank = __popcll(m & ((1ull << l) - 1ull));
-    const int total = __popcll(m);
-    for (int idx = t; idx < (TH / 64) * E; idx += TH) wcnt[idx / E][idx % E] = 0;
-    __syncthreads();
-    if (e < (uint32_t)E && rank == total - 1) wcnt[w][e] = (unsigned short)total;
-    __syncthreads();
-    if (e < (uint32_t)E) {
-      int pos = nxt[e] + rank;
-      for (int ww = 0; ww < w; ww++) pos += wcnt[ww][e];
-      order[pos] = p;
-      pair_row[pos] = p / k;
-      inv[p] = pos;
-    } else if (p < P) {
-      inv[p] = -1;
-    }
-    __syncthreads();
-    if (t < E) {
-      int s = 0;
-      for (int ww = 0; ww < (TH / 64); ww++) s += wcnt[ww][t];
-      nxt[t] += s;
-    }
-    __syncthreads();
-  }
 }
 
+// Placement of the pairs base .. base + TH - 1 (flat order) at their sorted positions, given each
+// expert's next free position in nxt (advanced past the tile's pairs on return): within a wave,
+// lanes holding the same expert id find each other with ballots over the id's bits, so a pair's
+// position is its expert's running offset plus the pairs of that expert in earlier waves of the
+// tile plus its rank among its own wave's lanes -- a stable counting sort.  A pair with an id
+// past E gets inv = -1 and no position.
+template <int TH, typename IndFn>
+__device__ __forceinline__ void pack_place_tile(IndFn ind, int base, int P, int k, int E, int *nxt,
+                                                unsigned short (*wcnt)[TH], int32_t *__restrict__ order,
+                                                int32_t *__restrict__ pair_row, int32_t *__restrict__ inv) {
+  const int t = threadIdx.x, w = t >> 6, l = t & 63;
+  const int nbits = 32 - __clz(E);  // enough bits for ids 0..E (E = "no expert")
+  const int p = base + t;
+  uint32_t e = p < P ? ind(p) : (uint32_t)E;
+  if (e > (uint32_t)E) e = (uint32_t)E;
+  unsigned long long m = ~0ull;
+  for (int bt = 0; bt < nbits; bt++) {
+    const int bit = (e >> bt) & 1u;
+    const unsigned long long bal = __ballot(bit);
+    m &= bit ? bal : ~bal;
+  }
+  const int rank = __popcll(m & ((1ull << l) - 1ull));
+  const int total = __popcll(m);
+  for (int idx = t; idx < (TH / 64) * E; idx += TH) wcnt[idx / E][idx % E] = 0;
+  __syncthreads();
+  if (e < (uint32_t)E && rank == total - 1) wcnt[w][e] = (unsigned short)total;
+  __syncthreads();
+  if (e < (uint32_t)E) {
+    int pos = nxt[e] + rank;
+    for (int ww = 0; ww < w; ww++) pos += wcnt[ww][e];
+    order[pos] = p;
+    pair_row[pos] = p / k;
+    inv[p] = pos;
+  } else if (p < P) {
+    inv[p] = -1;
+  }
+  __syncthreads();
+  if (t < E) {
+    int s = 0;
+    for (int ww = 0; ww < (TH / 64); ww++) s += wcnt[ww][t];
+    nxt[t] += s;
+  }
+  __syncthreads();
+}
+
+// The packing, run by one workgroup of TH threads (TH >= E): (1) per-expert counts in LDS; (2)
+// the tables; (3) the pairs placed in tiles of TH in flat order.  ind(p) is flat pair p's expert id.
+template <int TH, typename IndFn>
+__device__ __forceinline__ void pack_body(IndFn ind, int P, int k, int E, int32_t *__restrict__ order,
+                                          int32_t *__restrict__ pair_row, int32_t *__restrict__ inv,
+                                          int32_t *__restrict__ expert_cnt, int32_t *__restrict__ expert_off,
+                                          int32_t *__restrict__ seg_expert, int32_t *__restrict__ seg_start,
+                                          int32_t *__restrict__ seg_cnt, int32_t *__restrict__ meta) {
+  __shared__ int cnt[TH];
+  __shared__ int nxt[TH];
+  __shared__ unsigned short wcnt[(TH / 64)][TH];
+  __shared__ int bad;
+  const int t = threadIdx.x;
+  cnt[t] = 0;
+  if (t == 0) bad = 0;
+  __syncthreads();
+  for (int p = t; p < P; p += TH) {
+    const uint32_t e = ind(p);
+    if (e < (uint32_t)E)
+      atomicAdd(&cnt[e], 1);
+    else
+      atomicAdd(&bad, 1);
+  }
+  __syncthreads();
+  pack_tables<TH>(cnt[t], bad, E, nxt, expert_cnt, expert_off, seg_expert, seg_start, seg_cnt, meta);
+  for (int base = 0; base < P; base += TH)
+    pack_place_tile<TH>(ind, base, P, k, E, nxt, wcnt, order, pair_row, inv);
+}
+
+// The packing of a long batch over many workgroups (the one-workgroup kernel walks its tiles one
+// after another), in three launches over a workspace of per-tile counts ws[tiles][E + 1] (slot E:
+// the tile's bad pairs), tiles of kPackThreads pairs:
+//   pack_count_kernel: each tile's expert counts;
+//   pack_scan_kernel (one workgroup): each expert's total, the tables, and in ws each tile's
+//     pairs of each expert before it (the tile's offset within the expert's segment);
+//   pack_place_kernel: each tile placed from its experts' first positions plus those offsets.
+// The result is the stable order (expert, flat index) itself, so the same tables as the one
+// workgroup's, bit for bit.
+__global__ __launch_bounds__(kPackThreads) void pack_count_kernel(const uint32_t *__restrict__ inds, int P, int E,
+                                                                  int32_t *__restrict__ ws) {
+  __shared__ int cnt[kPackThreads + 1];
+  const int t = threadIdx.x, tile = blockIdx.x;
+  for (int e = t; e <= E; e += kPackThreads) cnt[e] = 0;
+  __syncthreads();
+  const int p = tile * kPackThreads + t;
+  if (p < P) {
+    const uint32_t e = inds[p];
+    atomicAdd(&cnt[e < (uint32_t)E ? e : (uint32_t)E], 1);
+  }
+  __syncthreads();
+  for (int e = t; e <= E; e += kPackThreads) ws[(long long)tile * (E + 1) + e] = cnt[e];
+}
+
+template <int TH>
+__global__ __launch_bounds__(TH) void pack_scan_kernel(int tiles, int E, int32_t *__restrict__ ws,
+                                                       int32_t *__restrict__ expert_cnt, int32_t *__restrict__ expert_off,
+                                                       int32_t *__restrict__ seg_expert, int32_t *__restrict__ seg_start,
+                                                       int32_t *__restrict__ seg_cnt, int32_t *__restrict__ meta) {
+  __shared__ int nxt[TH];
+  const int t = threadIdx.x;
+  int run = 0;
+  if (t <= E)  // experts, and slot E (the bad pairs)
+    for (int i = 0; i < tiles; i++) {
+      int32_t *q = ws + (long long)i * (E + 1) + t;
+      const int v = *q;
+      *q = run;
+      run += v;
+    }
+  __shared__ int bad;
+  if (t == E) bad = run;
+  __syncthreads();
+  pack_tables<TH>(t < E ? run : 0, bad, E, nxt, expert_cnt, expert_off, seg_expert, seg_start, seg_cnt, meta);
+}
+
+__global__ __launch_bounds__(kPackThreads) void pack_place_kernel(const uint32_t *__restrict__ inds, int P, int k,
+                                                                  int E, const int32_t *__restrict__ ws,
+                                                                  const int32_t *__restrict__ expert_off,
+                                                                  int32_t *__restrict__ order,
+                                                                  int32_t *__restrict__ pair_row,
+                                                                  int32_t *__restrict__ inv) {
+  __shared__ int nxt[kPackThreads];
+  __shared__ unsigned short wcnt[kPackThreads / 64][kPackThreads];
+  const int t = threadIdx.x, tile = blockIdx.x;
+  for (int e = t; e < E; e += kPackThreads) nxt[e] = expert_off[e] + ws[(long long)tile * (E + 1) + e];
+  __syncthreads();
+  pack_place_tile<kPackThreads>([&](int p) { return inds[p]; }, tile * kPackThreads, P, k, E, nxt, wcnt, order,
+                                pair_row, inv);
+}
 
 template <int TH>
 __global__ __launch_bounds__(TH) void moe_pack_kernel(
@@ -390,4 +467,38 @@ extern "C" int jit_moe_pack(const uint32_t *inds, int P, int k, int E, int32_t *
     JIT_PACK(1024);
 #undef JIT_PACK
   return jit::check_launch("jit_moe_pack");
+}
+
+// Long batches take the three-launch packing over a workspace of per-tile counts.
+static bool pack_multi(int P, int E) { return P > 2 * kPackThreads && E < kPackThreads; }
+
+extern "C" long long jit_moe_pack_workspace_bytes(int P, int E) {
+  if (P <= 0 || E <= 0 || !pack_multi(P, E)) return 0;
+  return (long long)((P + kPackThreads - 1) / kPackThreads) * (E + 1) * (long long)sizeof(int32_t);
+}
+
+extern "C" int jit_moe_pack_ws(const uint32_t *inds, int P, int k, int E, int32_t *order, int32_t *pair_row,
+                               int32_t *inv, int32_t *expert_cnt, int32_t *expert_off, int32_t *seg_expert,
+                               int32_t *seg_start, int32_t *seg_cnt, int32_t *meta, void *workspace,
+                               long long workspace_bytes, void *stream) {
+  const long long need = jit_moe_pack_workspace_bytes(P, E);
+  if (need == 0)
+    return jit_moe_pack(inds, P, k, E, order, pair_row, inv, expert_cnt, expert_off, seg_expert, seg_start, seg_cnt,
+                        meta, stream);
+  if (k <= 0 || P % k != 0)
+    return jit::fail(JIT_EINVAL, "moe_pack takes P >= 0 pairs in rows of k > 0 and E > 0, got P=%d k=%d E=%d",
+                     P, k, E);
+  if (!inds || !order || !pair_row || !inv || !expert_cnt || !expert_off || !seg_expert || !seg_start ||
+      !seg_cnt || !meta)
+    return jit::fail(JIT_EINVAL, "moe_pack: null pointer");
+  if (!workspace || workspace_bytes < need)
+    return jit::fail(JIT_EINVAL, "moe_pack: workspace of %lld bytes, %lld needed", workspace_bytes, need);
+  const hipStream_t st = (hipStream_t)stream;
+  const int tiles = (P + kPackThreads - 1) / kPackThreads;
+  int32_t *ws = (int32_t *)workspace;
+  pack_count_kernel<<<tiles, kPackThreads, 0, st>>>(inds, P, E, ws);
+  pack_scan_kernel<kPackThreads><<<1, kPackThreads, 0, st>>>(tiles, E, ws, expert_cnt, expert_off, seg_expert,
+                                                             seg_start, seg_cnt, meta);
+  pack_place_kernel<<<tiles, kPackThreads, 0, st>>>(inds, P, k, E, ws, expert_off, order, pair_row, inv);
+  return jit::check_launch("jit_moe_pack_ws");
 }

@@ -104,11 +104,25 @@ def moe_pack_into(inds: torch.Tensor, pk: Packing) -> None:
     k, P, E = pk.k, pk.P, pk.E
     if inds.numel() != P or inds.shape[-1] != k:
         raise ValueError(f"packing tables of {P} pairs x k={k} do not fit inds {tuple(inds.shape)}")
+    L = _lib.lib()
+    ws_bytes = int(L.jit_moe_pack_workspace_bytes(P, E))
+    if ws_bytes == 0:
+        _lib.check(
+            L.jit_moe_pack(
+                _p(inds), P, k, E, _p(pk.order), _p(pk.pair_row), _p(pk.inv), _p(pk.expert_cnt),
+                _p(pk.expert_off), _p(pk.seg_expert), _p(pk.seg_start), _p(pk.seg_cnt), _p(pk.meta),
+                _stream(),
+            ),
+            "moe_pack",
+        )
+        return
+    # a long batch: three launches over a workspace of per-tile counts (jit_moe_pack_ws)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=inds.device)
     _lib.check(
-        _lib.lib().jit_moe_pack(
+        L.jit_moe_pack_ws(
             _p(inds), P, k, E, _p(pk.order), _p(pk.pair_row), _p(pk.inv), _p(pk.expert_cnt),
             _p(pk.expert_off), _p(pk.seg_expert), _p(pk.seg_start), _p(pk.seg_cnt), _p(pk.meta),
-            _stream(),
+            _p(ws), ws_bytes, _stream(),
         ),
         "moe_pack",
     )

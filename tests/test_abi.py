@@ -96,3 +96,8 @@ def test_attn_plan_is_a_function_of_each_length():
 def test_workspace_bytes():
     lib = _lib.lib()
     assert lib.jit_attn_workspace_bytes(10, 32) == 10 * 32 * 130 * 4
+    # packing: no workspace up to two tiles of 1024 pairs, then 4 (E + 1) bytes a tile
+    assert lib.jit_moe_pack_workspace_bytes(2048, 128) == 0
+    assert lib.jit_moe_pack_workspace_bytes(16864, 128) == 17 * 129 * 4
+    assert lib.jit_moe_pack_workspace_bytes(16864, 1024) == 0
+    assert lib.jit_moe_pack_ws(None, 16864, 8, 128, *([None] * 9), None, 17 * 129 * 4 - 1, None) == _lib.JIT_EINVAL

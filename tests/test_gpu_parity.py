@@ -100,6 +100,39 @@ def test_pack_bit_exact(B, k, E):
     assert meta[0] == U and meta[1] == want["meta"][1] and meta[2] == 0
 
 
+@pytest.mark.parametrize("P,k,E,skew,bad", [(2056, 8, 128, False, 0), (16864, 8, 128, True, 0),
+                                             (50000, 5, 1023, True, 37), (3072, 1, 64, False, 5)])
+def test_pack_many_workgroups_equal_one(P, k, E, skew, bad):
+    """A long batch's three-launch packing (jit_moe_pack_ws) gives the one-workgroup kernel's
+    tables bit for bit: skewed routing (segments of thousands of pairs), ids past E (dropped,
+    inv = -1, counted in meta[2]), tiles that do not divide P."""
+    from jitengine_amd import _lib
+
+    rng = np.random.default_rng(P + E)
+    w = 1.0 / (1.0 + np.arange(E)) ** (1.2 if skew else 0.0)
+    inds = rng.choice(E, P, p=w / w.sum()).astype(np.uint32)
+    inds[rng.permutation(P)[:bad]] = E + rng.integers(0, 50, bad).astype(np.uint32)
+    t = _i32(inds.reshape(-1, k))
+    assert _lib.lib().jit_moe_pack_workspace_bytes(P, E) > 0
+    multi = ops.moe_pack(t, E)
+    one = ops._packing_buffers(P, k, E, DEV)
+    _lib.check(_lib.lib().jit_moe_pack(ops._p(t), P, k, E, *[ops._p(getattr(one, n)) for n in (
+        "order", "pair_row", "inv", "expert_cnt", "expert_off", "seg_expert", "seg_start", "seg_cnt", "meta")],
+        ops._stream()), "moe_pack")
+    U = int(one.meta[0])
+    valid = int(one.expert_cnt.sum())
+    assert valid == P - bad and int(one.meta[2]) == bad
+    for name in ("pair_row", "order"):
+        assert torch.equal(getattr(multi, name)[:valid], getattr(one, name)[:valid]), name
+    for name in ("inv", "expert_cnt", "expert_off", "meta"):
+        assert torch.equal(getattr(multi, name), getattr(one, name)), name
+    for name in ("seg_expert", "seg_start", "seg_cnt"):
+        assert torch.equal(getattr(multi, name)[:U], getattr(one, name)[:U]), name
+    if bad == 0:  # (the oracle rejects ids past E)
+        want = oracle.moe_pack(inds.reshape(-1, k), E)
+        assert np.array_equal(multi.inv.cpu().numpy(), want["inv"])
+
+
 # ----------------------------------------------------------------------------- projections
 def _fn_criterion(got_u16, x, w, s, b, f64):
     stock = oracle.f32_to_bf16(oracle.qmv_mlx_f32(x, w, s, b))
