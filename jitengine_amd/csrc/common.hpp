@@ -113,4 +113,6 @@ namespace jit {
 void set_error(const char *fmt, ...);
 int fail(int code, const char *fmt, ...);
 int check_launch(const char *what);
+// Compute units of the current device (queried once per device, at most 64 devices).
+int cu_count();
 }  // namespace jit

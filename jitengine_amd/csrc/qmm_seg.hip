@@ -23,8 +23,9 @@ namespace {
 constexpr int kSegWaves = 4;
 constexpr int kSegRB = 4;                 // row blocks per wave
 constexpr int kSegRows = 16 * kSegRB * kSegWaves;  // weight rows per workgroup
-constexpr int kSegTT = 10;                // token tiles per chunk (160 tokens)
-constexpr int kSegTokens = 16 * kSegTT;
+constexpr int kSegTT = 10;                // token tiles per chunk of an expert segment (160 tokens)
+// (a dense batch, one matrix with its token chunks spread over workgroups, sizes its chunks to the
+// CUs: jit_qmm_seg)
 #ifndef JIT_SEG_AHEAD
 #define JIT_SEG_AHEAD 1
 #endif
@@ -86,7 +87,7 @@ __device__ __forceinline__ Frag8 dequant_word(uint32_t w, float s, float b) {
 }
 
 // LDS of a workgroup:
-//   two activation stages: one K step's activations, kSegTokens rows of 128 k (256 B, no
+//   two activation stages: one K step's activations, 16 TTS token rows of 128 k (256 B, no
 //     padding).  Row r's 16 B piece c sits in slot c ^ (r % 16), so the 16 rows one fragment
 //     read touches (same piece, rows 16 t .. 16 t + 15) fall in 16 different slots: the reads
 //     are free of bank conflicts without the padding the direct global->LDS loads (1 KB = 4
@@ -94,13 +95,14 @@ __device__ __forceinline__ Frag8 dequant_word(uint32_t w, float s, float b) {
 //   three weight stages: per wave its 4 row blocks' nibble tiles of one K step (4 x 1 KB) and
 //     their scale tiles (4 x 128 B, then a copy of them: the instruction writes 1 KB);
 //   the chunk's activation row indices.
-constexpr int kSegStageBytes = kSegTokens * 256;
+// (per chunk of TTS token tiles: the expert segments take kSegTT, dense batches 5, 8 or 10, jit_qmm_seg)
+constexpr int seg_stage_bytes(int tts) { return 16 * tts * 256; }
 constexpr int kSegWWave = 5 * 1024;
 constexpr int kSegWStageBytes = kSegWaves * kSegWWave;
-constexpr int kSegWOff = 2 * kSegStageBytes;
-constexpr int kSegRowOff = kSegWOff + 3 * kSegWStageBytes;
-constexpr int kSegLdsBytes = kSegRowOff + kSegTokens * (int)sizeof(int);
-static_assert(kSegLdsBytes <= 160 * 1024, "gfx950 gives a workgroup at most 160 KB of LDS");
+constexpr int seg_w_off(int tts) { return 2 * seg_stage_bytes(tts); }
+constexpr int seg_row_off(int tts) { return seg_w_off(tts) + 3 * kSegWStageBytes; }
+constexpr int seg_lds_bytes(int tts) { return seg_row_off(tts) + 16 * tts * (int)sizeof(int); }
+static_assert(seg_lds_bytes(kSegTT) <= 160 * 1024, "gfx950 gives a workgroup at most 160 KB of LDS");
 
 // s_waitcnt vmcnt(N), nothing else.  Direct loads are counted by hand: the compiler does not see
 // the ones issued by inline assembly.
@@ -135,10 +137,11 @@ __device__ __forceinline__ void seg_load_lds(const void *src, uint32_t dst) {
 // Each tile's activation fragments are read kSegAhead tiles ahead of its MFMAs.  Weights are
 // requested one and a half steps before they are dequantized, activations (mostly L2 hits:
 // an expert's column blocks run on one XCD) a step before they are read.
-template <bool SWIGLU, bool DENSE = false>
+template <bool SWIGLU, bool DENSE = false, int TTS = kSegTT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void seg_kernel(const SegArgs a) {
+  constexpr int kTokens = 16 * TTS, kStage = seg_stage_bytes(TTS);
   extern __shared__ __attribute__((aligned(16))) uint8_t seg_lds[];
-  int *xrow = (int *)(seg_lds + kSegRowOff);
+  int *xrow = (int *)(seg_lds + seg_row_off(TTS));
   int grp, cb;
   if (!seg_block(a, grp, cb)) return;  // grid padding (uniform over the workgroup)
   const int e = DENSE ? 0 : grp;
@@ -168,8 +171,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int srb = (l >> 3) & 3;
   const int rb_s = srb == 0 ? rbk[0] : srb == 1 ? rbk[1] : srb == 2 ? rbk[2] : rbk[3];
   const uint8_t *wscl = wexp + rb_s * tile_row + (long long)GP * qtile::kNibbleBytes + 16 * (l & 7);
-  const uint32_t wlds = lds0 + kSegWOff + wave * kSegWWave;  // + stage * kSegWStageBytes
-  const uint8_t *wmine = seg_lds + kSegWOff + wave * kSegWWave;
+  const uint32_t wlds = lds0 + seg_w_off(TTS) + wave * kSegWWave;  // + stage * kSegWStageBytes
+  const uint8_t *wmine = seg_lds + seg_w_off(TTS) + wave * kSegWWave;
   auto load_w = [&](int p) {
     const uint32_t st = wlds + (p % 3) * kSegWStageBytes;
 #pragma unroll
@@ -198,39 +201,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // fragment reads: lane (lr, lg) reads pieces 8 g + 2 lg and + 1 of row 16 t + lr
   const int frow = lr * 256;
 
-  const int cend = DENSE ? min(cnt, (grp + 1) * kSegTokens) : cnt;
-  for (int c0 = DENSE ? grp * kSegTokens : 0; c0 < cend; c0 += kSegTokens) {
-    const int nt = min(kSegTokens, cnt - c0);
+  const int cend = DENSE ? min(cnt, (grp + 1) * kTokens) : cnt;
+  for (int c0 = DENSE ? grp * kTokens : 0; c0 < cend; c0 += kTokens) {
+    const int nt = min(kTokens, cnt - c0);
     const int ntiles = (nt + 15) >> 4;
     __syncthreads();  // the previous chunk's reads of the stages and of xrow are done
-    for (int j = tid; j < kSegTokens; j += 256) {
+    for (int j = tid; j < kTokens; j += 256) {
       const int pos = off + c0 + min(j, nt - 1);  // rows past the segment re-read its last row
       xrow[j] = a.row_index ? a.row_index[pos] : pos;
     }
     __syncthreads();
-    uint32_t xsrc[kSegTT];  // element offsets of this lane's pieces (x holds < 2^32 elements)
+    uint32_t xsrc[TTS];  // element offsets of this lane's pieces (x holds < 2^32 elements)
 #pragma unroll
-    for (int j = 0; j < kSegTT; j++) xsrc[j] = (uint32_t)xrow[16 * j + srow] * (uint32_t)a.K + 8 * spiece;
+    for (int j = 0; j < TTS; j++) xsrc[j] = (uint32_t)xrow[16 * j + srow] * (uint32_t)a.K + 8 * spiece;
     auto load_x = [&](int p) {
-      const uint32_t st = lds0 + (p & 1) * kSegStageBytes + 4 * wave * 256;
+      const uint32_t st = lds0 + (p & 1) * kStage + 4 * wave * 256;
 #pragma unroll
-      for (int j = 0; j < kSegTT; j++)
+      for (int j = 0; j < TTS; j++)
         seg_load_lds(a.x + xsrc[j] + 128 * p, __builtin_amdgcn_readfirstlane(st + 16 * j * 256));
     };
 
-    f32x4 acc[kSegTT][kSegRB];
+    f32x4 acc[TTS][kSegRB];
 #pragma unroll
-    for (int t = 0; t < kSegTT; t++)
+    for (int t = 0; t < TTS; t++)
 #pragma unroll
       for (int r = 0; r < kSegRB; r++) acc[t][r] = f32x4{0.f, 0.f, 0.f, 0.f};
     Frag8 bw0[kSegRB][2], bw1[kSegRB][2];
 
-    // all kSegTT token tiles of group g of step p against bw, with no branch (tiles past the
+    // all TTS token tiles of group g of step p against bw, with no branch (tiles past the
     // chunk compute on rows that are never stored: a branch per tile would keep the
     // dequantization from being scheduled between the MFMAs); side(t) is the dequantization of
     // one B fragment (word t % 2 of row block t / 2) interleaved with tile t's MFMAs (t < 8)
     auto tiles = [&](int p, int g, Frag8 (&bw)[kSegRB][2], auto &&side) {
-      const uint8_t *xs = seg_lds + (p & 1) * kSegStageBytes + frow;
+      const uint8_t *xs = seg_lds + (p & 1) * kStage + frow;
       const int pa = 8 * g + 2 * lg;
       const int o0 = 16 * (pa ^ lr), o1 = 16 * ((pa + 1) ^ lr);
       Frag8 xa[kSegAhead + 1][2];
@@ -240,8 +243,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         xa[t][1].q = *(const uint4 *)(xs + t * 16 * 256 + o1);
       }
 #pragma unroll
-      for (int t = 0; t < kSegTT; t++) {
-        if (t + kSegAhead < kSegTT) {
+      for (int t = 0; t < TTS; t++) {
+        if (t + kSegAhead < TTS) {
           Frag8 *n = xa[(t + kSegAhead) % (kSegAhead + 1)];
           n[0].q = *(const uint4 *)(xs + (t + kSegAhead) * 16 * 256 + o0);
           n[1].q = *(const uint4 *)(xs + (t + kSegAhead) * 16 * 256 + o1);
@@ -265,6 +268,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         __builtin_amdgcn_sched_barrier(0);
 #endif
       }
+      // (a chunk of fewer tiles than B fragments runs the rest of them after its tiles)
+#pragma unroll
+      for (int t = TTS; t < 2 * kSegRB; t++) side(t);
     };
 
     // prologue: step 0's activations and weights, step 1's weights; group 0 of step 0
@@ -302,7 +308,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     // lane l holds C[token 16 t + 4 lg + i][row 16 rbk[r] + lr]
 #pragma unroll
-    for (int t = 0; t < kSegTT; t++) {
+    for (int t = 0; t < TTS; t++) {
       if (t >= ntiles) continue;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -322,11 +328,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 }
 
 // The kernels take more LDS than the static limit: raise their dynamic limit once.
-template <bool SWIGLU, bool DENSE>
+template <bool SWIGLU, bool DENSE, int TTS>
 void seg_prepare() {
   static const bool done = [] {
-    (void)hipFuncSetAttribute((const void *)&seg_kernel<SWIGLU, DENSE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kSegLdsBytes);
+    (void)hipFuncSetAttribute((const void *)&seg_kernel<SWIGLU, DENSE, TTS>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, seg_lds_bytes(TTS));
     return true;
   }();
   (void)done;
@@ -347,8 +353,8 @@ extern "C" int jit_moe_gate_up_swiglu_seg(const uint16_t *x, int K, const int32_
     return jit::fail(JIT_EINVAL, "moe_gate_up_seg: null pointer");
   SegArgs a{x, pair_row, expert_cnt, expert_off, (const uint8_t *)packed, h, jit_q4_packed_bytes(1, 2 * I, K), K, I, 0,
             I / 128, E};
-  seg_prepare<true, false>();
-  seg_kernel<true><<<seg_grid(a.nx, E), 256, kSegLdsBytes, (hipStream_t)stream>>>(a);
+  seg_prepare<true, false, kSegTT>();
+  seg_kernel<true><<<seg_grid(a.nx, E), 256, seg_lds_bytes(kSegTT), (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_moe_gate_up_swiglu_seg");
 }
 
@@ -363,8 +369,8 @@ extern "C" int jit_moe_down_seg(const uint16_t *h, int I, const int32_t *expert_
   if (!h || !expert_cnt || !expert_off || !packed || !r) return jit::fail(JIT_EINVAL, "moe_down_seg: null pointer");
   SegArgs a{h, nullptr, expert_cnt, expert_off, (const uint8_t *)packed, r, jit_q4_packed_bytes(1, D, I), I, D, 0,
             D / kSegRows, E};
-  seg_prepare<false, false>();
-  seg_kernel<false><<<seg_grid(a.nx, E), 256, kSegLdsBytes, (hipStream_t)stream>>>(a);
+  seg_prepare<false, false, kSegTT>();
+  seg_kernel<false><<<seg_grid(a.nx, E), 256, seg_lds_bytes(kSegTT), (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_moe_down_seg");
 }
 
@@ -375,9 +381,27 @@ extern "C" int jit_qmm_seg(const uint16_t *x, int T, int K, const void *packed, 
                      N);
   if (T == 0) return JIT_OK;
   if (!x || !packed || !y) return jit::fail(JIT_EINVAL, "qmm_seg: null pointer");
-  const int chunks = (T + kSegTokens - 1) / kSegTokens;
-  SegArgs a{x, nullptr, nullptr, nullptr, (const uint8_t *)packed, y, 0, K, N, T, N / kSegRows, chunks};
-  seg_prepare<false, true>();
-  seg_kernel<false, true><<<seg_grid(a.nx, chunks), 256, kSegLdsBytes, (hipStream_t)stream>>>(a);
+  // The chunk (token tiles per workgroup) is the smallest of 5, 8, 10 whose workgroups fill the CUs
+  // in one round: chunks of 10 can leave most CUs idle (config 3's o_proj, N = 2048 over 2,108
+  // tokens: 112 workgroups, 89 us, against 216 of 5 tiles, 67 us), while smaller chunks only add
+  // dequantization.  Batches too long for one round take chunks of 10 (12 tiles would fit the LDS,
+  // but their accumulators push the kernel past its registers: 106 us against 96 for qkv, N = 5120,
+  // in two rounds of 10).
+  const int nx = N / kSegRows, cus = jit::cu_count();
+  auto groups = [&](int tts) { return (T + 16 * tts - 1) / (16 * tts); };
+  const hipStream_t st = (hipStream_t)stream;
+#define JIT_QMM_SEG(TTS)                                                                                       \
+  {                                                                                                            \
+    SegArgs a{x, nullptr, nullptr, nullptr, (const uint8_t *)packed, y, 0, K, N, T, nx, groups(TTS)};          \
+    seg_prepare<false, true, TTS>();                                                                           \
+    seg_kernel<false, true, TTS><<<seg_grid(nx, groups(TTS)), 256, seg_lds_bytes(TTS), st>>>(a);              \
+  }
+  if (nx * groups(5) <= cus)
+    JIT_QMM_SEG(5)
+  else if (nx * groups(8) <= cus)
+    JIT_QMM_SEG(8)
+  else
+    JIT_QMM_SEG(10)
+#undef JIT_QMM_SEG
   return jit::check_launch("jit_qmm_seg");
 }

@@ -317,12 +317,14 @@ def test_qmm_packed_equals_direct(T, N, K):
 
 
 @pytest.mark.parametrize("T,N,K", [(192, 256, 2048), (300, 5120, 2048), (2108, 2048, 4096), (161, 512, 768),
-                                   (200, 256, 384), (17, 256, 128)])
+                                   (200, 256, 384), (17, 256, 128), (1200, 5120, 2048), (1800, 5120, 2048),
+                                   (2108, 5120, 2048)])
 def test_qmm_prefill_tile_gemm(T, N, K):
     """A long batch on the prefill tile GEMM (jit_qmm_seg): the reference's prefill arithmetic,
     bf16-dequantized weights with fp32 sums, restated by the oracle's bf16-weight mode (a dense
     matrix is a one-expert stack whose pairs are the rows in order); 161 rows: a partial token
-    chunk; K = 384 and 128: an odd number of K steps, and a single one."""
+    chunk; K = 384 and 128: an odd number of K steps, and a single one; N = 5120 over 1,200, 1,800
+    and 2,108 rows: chunks of 8 and 10 token tiles (the launch sizes them to the CUs)."""
     q = make_stack((N, K), seed=T + K)
     x = normal_bf16((T, K), seed=T)
     y = ops.qmm(bf16_tensor(x, DEV), ops.prepack(_dev(q)), seg=True)
