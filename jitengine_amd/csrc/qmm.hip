@@ -29,7 +29,7 @@ namespace {
 
 struct QmmArgs {
   const uint16_t *x;          // activations, row stride K (bf16)
-  const int32_t *row_index;   // x row of each sorted position (null: the position itself)
+  const int32_t *row_index;   // x row of each sorted position (gate||up; null: the position itself)
   const int32_t *cnt;         // pairs per expert (null: dense, T tokens)
   const int32_t *off;         // first sorted position per expert
   const uint32_t *w;          // weight stack [E, rows_w, K / 8]
@@ -111,26 +111,35 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   const int tfirst = 16 * TT * blockIdx.z, tstride = 16 * TT * gridDim.z;
   if (tfirst >= cnt) return;  // uniform over the workgroup
 
-  // x rows of the first pass's tokens, requested before the weights: vector loads
-  // complete in order, so a row index loaded after the weights would hold the
-  // activation loads back until every weight load had landed
-  // (as a byte offset into x for the activation loads; a token past the expert's count gets an
-  // offset past the buffer's range, whose loads return zeros without reading memory)
-  auto x_row = [&](int tok) {
+  // The prologue issues every load of the first pass before its first wait: the row indices of
+  // the first pass's tokens (before the weights: vector loads complete in order, so an index
+  // loaded after the weights would hold the activation loads back until every weight load had
+  // landed), the weight slice, then the activations, whose offsets need the indices.  The scale
+  // shuffles, which need the scale loads, come after all of them; the scheduling barriers keep
+  // the compiler from hoisting an offset or a shuffle (and the wait it implies) above a load.
+  // Only the gate||up instances (SWIGLU) gather token rows through a row index (launch_qmm checks
+  // it); down and the dense projections read their rows in place, with no load and no wait.
+  auto row_of = [&](int tok) {
     const int pos = off + (tok < cnt ? tok : 0);
-    const int row = a.row_index ? a.row_index[pos] : pos;
+    if constexpr (SWIGLU) return a.row_index[pos];
+    else return pos;
+  };
+  // a row as a byte offset into x for the activation loads; a token past the expert's count gets
+  // an offset past the buffer's range, whose loads return zeros without reading memory
+  auto x_off = [&](int tok, int row) {
     return tok < cnt ? (int)((uint32_t)row * (uint32_t)a.K * 2u) : (int)kXOutOfRange;
   };
   // activations through a buffer resource (2 GiB range: x holds fewer bytes), so that the lanes
   // of padding tokens (a 16-token tile over an expert's ~2 decode tokens) fetch nothing
   const __amdgpu_buffer_rsrc_t xbuf = __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 0x7fffffff, 0x00020000);
-  int xrow0[TT];
+  int row0[TT];
 #pragma unroll
-  for (int tt = 0; tt < TT; tt++) xrow0[tt] = x_row(tfirst + 16 * tt + lr);
+  for (int tt = 0; tt < TT; tt++) row0[tt] = row_of(tfirst + 16 * tt + lr);
 
   // ---- the wave's whole weight slice: GPW groups x NBW row blocks
   uint2 wv[GPW][NBW];
   uint32_t sv[NBW][(GPW + 1) / 2], bv[NBW][(GPW + 1) / 2];  // bf16 pairs (groups 2j, 2j+1)
+  uint2 sbl[NBW];  // packed layout: the lane's 8 bytes of its block's scale tile, shuffled later
 #pragma unroll
   for (int rb = 0; rb < NBW; rb++) {
     // rows past N (a partial last tile) read row block n0 instead; only stores are guarded
@@ -143,18 +152,13 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
       const uint8_t *blk = (const uint8_t *)a.w + (long long)e * a.w_estride + (long long)(rowb >> 4) * GP * kTileBytes;
       const uint8_t *nb = blk + (g0 >> 1) * kNibbleBytes;
       // lane group lg fetches pair min(lg, GPW/2 - 1) (lanes past the slice re-read its last pair)
-      const uint2 sbl = ld_stream8(blk + (long long)GP * kNibbleBytes +
-                                   ((g0 >> 1) + min(lg, GPW / 2 - 1)) * kScaleBytes + 8 * lr);
+      sbl[rb] = ld_stream8(blk + (long long)GP * kNibbleBytes +
+                           ((g0 >> 1) + min(lg, GPW / 2 - 1)) * kScaleBytes + 8 * lr);
 #pragma unroll
       for (int j = 0; j < GPW / 2; j++) {
         const uint4 q = ld_stream16(nb + j * kNibbleBytes + 16 * l);
         wv[2 * j][rb] = make_uint2(q.x, q.y);
         wv[2 * j + 1][rb] = make_uint2(q.z, q.w);
-      }
-#pragma unroll
-      for (int j = 0; j < GPW / 2; j++) {
-        sv[rb][j] = (uint32_t)__shfl((int)sbl.x, 16 * j + lr, 64);
-        bv[rb][j] = (uint32_t)__shfl((int)sbl.y, 16 * j + lr, 64);
       }
     } else {
       const long long row = (long long)rowb + lr;
@@ -183,16 +187,15 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
 
   // TT token tiles of 16 per pass: their activations are loaded together, their
   // partial sums meet in LDS once (one barrier round and one epilogue per pass)
-  // (the first pass is peeled off so that its x rows are the ones requested up front,
-  // with no merge of load paths in front of its activation loads)
-  auto pass = [&](const int t0, const int (&xrows)[TT]) {
-    // activation fragments (natural k order, as the unpacked weights); lanes past the
-    // last token load from outside the buffer's range (no branch around the loads): zeros,
-    // which feed only output rows of tokens that are never stored
-    Frag8 xa[TT][GPW][2];
+  // (the first pass is peeled off so that its activation loads follow the weight loads
+  // directly, with no merge of load paths in front of them)
+  // activation fragments (natural k order, as the unpacked weights); lanes past the
+  // last token load from outside the buffer's range (no branch around the loads): zeros,
+  // which feed only output rows of tokens that are never stored
+  auto load_x = [&](const int t0, const int (&rows)[TT], Frag8 (&xa)[TT][GPW][2]) {
 #pragma unroll
     for (int tt = 0; tt < TT; tt++) {
-      const uint32_t xo = (uint32_t)xrows[tt] + 2u * (64 * g0 + 16 * lg);  // (out of range stays out)
+      const uint32_t xo = (uint32_t)x_off(t0 + 16 * tt + lr, rows[tt]) + 2u * (64 * g0 + 16 * lg);  // (out of range stays out)
 #pragma unroll
       for (int g = 0; g < GPW; g++) {
         const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(xbuf, xo + 128 * g, 0, 0);
@@ -201,6 +204,8 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
         xa[tt][g][1].q = make_uint4(v1.x, v1.y, v1.z, v1.w);
       }
     }
+  };
+  auto pass = [&](const int t0, const Frag8 (&xa)[TT][GPW][2]) {
     f32x4 acc[TT][NBW];
 #pragma unroll
     for (int tt = 0; tt < TT; tt++)
@@ -261,12 +266,29 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     }
     __syncthreads();
   };
-  pass(tfirst, xrow0);
-  for (int t0 = tfirst + tstride; t0 < cnt; t0 += tstride) {
-    int xr[TT];
+  {
+    Frag8 xa[TT][GPW][2];
+    __builtin_amdgcn_sched_barrier(0);
+    load_x(tfirst, row0, xa);
+    __builtin_amdgcn_sched_barrier(0);
+    if (PACKED) {
 #pragma unroll
-    for (int tt = 0; tt < TT; tt++) xr[tt] = x_row(t0 + 16 * tt + lr);
-    pass(t0, xr);
+      for (int rb = 0; rb < NBW; rb++)
+#pragma unroll
+        for (int j = 0; j < GPW / 2; j++) {
+          sv[rb][j] = (uint32_t)__shfl((int)sbl[rb].x, 16 * j + lr, 64);
+          bv[rb][j] = (uint32_t)__shfl((int)sbl[rb].y, 16 * j + lr, 64);
+        }
+    }
+    pass(tfirst, xa);
+  }
+  for (int t0 = tfirst + tstride; t0 < cnt; t0 += tstride) {
+    int rows[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) rows[tt] = row_of(t0 + 16 * tt + lr);
+    Frag8 xa[TT][GPW][2];
+    load_x(t0, rows, xa);
+    pass(t0, xa);
   }
 }
 
@@ -277,6 +299,8 @@ int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what, int zs
   const int ksplit = G / GPW;
   if (ksplit * GPW != G || ksplit < 1 || ksplit > 8)
     return jit::fail(JIT_EUNSUPPORTED, "%s: K=%d does not split into %d-group wave slices", what, a.K, GPW);
+  if (SWIGLU != (a.row_index != nullptr))
+    return jit::fail(JIT_EINVAL, "%s: a row index goes with the gate||up instances only", what);
   const dim3 grid((a.N + 16 * NB - 1) / (16 * NB), E, zsplit), block(64 * ksplit);
   const size_t lds = (size_t)ksplit * TT * NBW * 4 * 64 * sizeof(float);
   qmm_kernel<NB, GPW, SWIGLU, PACKED, TT, COMPACT><<<grid, block, lds, st>>>(a);
