@@ -507,13 +507,10 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
 #pragma unroll
     for (int cc = 0; cc < 8; cc++) o[j][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  // the first and last positions among each tile's rows (uniform over the wave)
-  int tile_first[kPfTiles], tile_last[kPfTiles];
+  // the first position among each tile's rows (uniform over the wave)
+  int tile_first[kPfTiles];
 #pragma unroll
-  for (int j = 0; j < kPfTiles; j++) {
-    tile_first[j] = ctx + min(q0 + wave * tpw + j * TR, len - 1);
-    tile_last[j] = ctx + min(q0 + wave * tpw + j * TR + TR - 1, len - 1);
-  }
+  for (int j = 0; j < kPfTiles; j++) tile_first[j] = ctx + min(q0 + wave * tpw + j * TR, len - 1);
   __syncthreads();
 
   // staging of step st into stage st % kPfStages: chunk c = kPfChunks * wave + u (1 KB, one
@@ -566,6 +563,20 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
     pv_next = pages_of_step(st + 2);
     const uint16_t *kvst = kvs[st % kPfStages];
     const int k0 = 32 * kPfHalves * st;
+    // the step's slots past the workgroup's keys (its last step only) may hold stale bits, which a
+    // p of 0 would not cancel (0 x NaN): their V is zeroed in the stage before any wave reads it
+    // (one more barrier, on that step only)
+    if (k0 + 32 * kPfHalves > kend) {
+      uint16_t *vst = kvs[st % kPfStages];
+      for (int e = tid; e < kPfHalves * 2 * kPageHead; e += 64 * kPfWaves) {
+        const int slot = e % kPage, dim = (e / kPage) % kD, pgh = e / kPageHead;  // pgh: page 2 h + p of the step
+        if (k0 + kPage * pgh + slot >= kend) vst[(2 * pgh + 1) * kPageHead + dim * kPage + slot] = 0;
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
     // Key order within each 32-key half h (keys k0 + 32 h ..): the P.V MFMA's k index 8 lg + j
     // (lane group lg) is key 8 lg + j of the half (page lg / 2, slot 8 (lg % 2) + j), so a
     // lane's V operand is 8 consecutive slots of one page -- 16 contiguous bytes of the page's
@@ -594,18 +605,14 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
         __builtin_amdgcn_sched_barrier(0);
       }
     // online softmax of every tile over the step's keys: the masked scores' running max first
-    // (the o rescale happens before the step's first P.V MFMA), then, half by half, the
-    // probabilities, their sum and the P.V products, so that only one half's P fragments are live
+    // (the o rescale happens before the step's first P.V MFMA).  Keys past a row's position are
+    // masked on the steps that reach into the tile's rows (a tile whose rows all precede the
+    // step's keys is masked whole: its p are 0 and its state is left as it was); the scale is
+    // applied inside the exponent (max of the raw scores times the positive scale is the max of
+    // the scaled ones).
     float m_step[kPfTiles], alpha[kPfTiles], psum[kPfTiles];
 #pragma unroll
     for (int j = 0; j < kPfTiles; j++) {
-      psum[j] = 0.0f;
-      alpha[j] = 1.0f;
-      m_step[j] = m_run[j];
-      if (k0 > tile_last[j]) continue;  // every key of the step is past the tile's rows
-      // keys past a row's position are masked on the steps that reach into the tile's rows;
-      // the scale is applied inside the exponent (max of the raw scores times the positive
-      // scale is the max of the scaled ones)
       if (k0 + 32 * kPfHalves - 1 > tile_first[j]) {
         const int pos = ctx + tok[j];
 #pragma unroll
@@ -628,6 +635,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
       tmax = max_xor32(max_xor16(tmax)) * a.qk_scale;
       m_step[j] = fmaxf(m_run[j], tmax);  // finite: key 0 is in every row's first step
       alpha[j] = __builtin_amdgcn_exp2f(m_run[j] - m_step[j]);
+      psum[j] = 0.0f;
       if (__any(alpha[j] != 1.0f)) {
 #pragma unroll
         for (int cc = 0; cc < 8; cc++)
@@ -635,18 +643,18 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
           for (int i = 0; i < 4; i++) o[j][cc][i] *= alpha[j];
       }
     }
-    // O^T += V^T . P^T for every tile and half, a quarter of the V fragments (32 dims of a half)
-    // at a time; the lane's 8 keys are slots 8 (lg % 2) .. + 7 of page lg / 2
-#pragma unroll
-    for (int h = 0; h < kPfHalves; h++) {
-      // the half's P^T fragments: bf16 high parts (pw) and, with JIT_PF_PSPLIT, bf16 residuals (pl)
-      uint32_t pw[kPfTiles][4];
+    // O^T += V^T . P^T, software-pipelined over the halves: the probabilities of half h + 1 are
+    // computed (vector ALU) while the P.V MFMAs of half h run on the matrix cores.  P^T
+    // fragments of a half are bf16 high parts (pw) and, with JIT_PF_PSPLIT, bf16 residuals (pl),
+    // in two buffers by the half's parity; the lane's 8 keys of a half are slots 8 (lg % 2) .. + 7
+    // of page lg / 2.
+    uint32_t pw[2][kPfTiles][4];
 #if JIT_PF_PSPLIT
-      uint32_t pl[kPfTiles][4];
+    uint32_t pl[2][kPfTiles][4];
 #endif
+    auto probs = [&](const int h) {
 #pragma unroll
       for (int j = 0; j < kPfTiles; j++) {
-        if (k0 > tile_last[j]) continue;
         float p[2][4];
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -656,19 +664,24 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
             psum[j] += p[t][i];
           }
 #if JIT_PF_PSPLIT
-        split_bf16x2(p[0][0], p[0][1], pw[j][0], pl[j][0]);
-        split_bf16x2(p[0][2], p[0][3], pw[j][1], pl[j][1]);
-        split_bf16x2(p[1][0], p[1][1], pw[j][2], pl[j][2]);
-        split_bf16x2(p[1][2], p[1][3], pw[j][3], pl[j][3]);
+        split_bf16x2(p[0][0], p[0][1], pw[h & 1][j][0], pl[h & 1][j][0]);
+        split_bf16x2(p[0][2], p[0][3], pw[h & 1][j][1], pl[h & 1][j][1]);
+        split_bf16x2(p[1][0], p[1][1], pw[h & 1][j][2], pl[h & 1][j][2]);
+        split_bf16x2(p[1][2], p[1][3], pw[h & 1][j][3], pl[h & 1][j][3]);
 #else
-        pw[j][0] = pack_bf16x2_rne(p[0][0], p[0][1]);
-        pw[j][1] = pack_bf16x2_rne(p[0][2], p[0][3]);
-        pw[j][2] = pack_bf16x2_rne(p[1][0], p[1][1]);
-        pw[j][3] = pack_bf16x2_rne(p[1][2], p[1][3]);
+        pw[h & 1][j][0] = pack_bf16x2_rne(p[0][0], p[0][1]);
+        pw[h & 1][j][1] = pack_bf16x2_rne(p[0][2], p[0][3]);
+        pw[h & 1][j][2] = pack_bf16x2_rne(p[1][0], p[1][1]);
+        pw[h & 1][j][3] = pack_bf16x2_rne(p[1][2], p[1][3]);
 #endif
       }
+    };
+    probs(0);
+#pragma unroll
+    for (int h = 0; h < kPfHalves; h++) {
+      // (one region per half: its P.V MFMAs and the next half's probabilities)
+      if (h + 1 < kPfHalves) probs(h + 1);
       const uint16_t *kvsc = kvst + h * 4 * kPageHead;
-      const int kh = k0 + 32 * h;
 #pragma unroll
       for (int hv = 0; hv < 2; hv++) {
         Frag8 vf[4];
@@ -676,34 +689,25 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
         for (int c4 = 0; c4 < 4; c4++)
           vf[c4].q = *(const uint4 *)(kvsc + (2 * (lg >> 1) + 1) * kPageHead + (16 * (4 * hv + c4) + lr) * kPage +
                                       8 * (lg & 1));
-        if (kh + 32 > kend) {  // slots past the keys may hold stale bits: their V is made 0
-          const int kb = kh + 8 * lg;
-#pragma unroll
-          for (int c4 = 0; c4 < 4; c4++)
-#pragma unroll
-            for (int w2 = 0; w2 < 4; w2++) vf[c4].u[w2] = mask_pair(vf[c4].u[w2], kb + 2 * w2, kend);
-        }
 #pragma unroll
         for (int j = 0; j < kPfTiles; j++) {
-          if (k0 > tile_last[j]) continue;
           Frag8 pf;
 #pragma unroll
-          for (int i = 0; i < 4; i++) pf.u[i] = pw[j][i];
+          for (int i = 0; i < 4; i++) pf.u[i] = pw[h & 1][j][i];
 #pragma unroll
           for (int c4 = 0; c4 < 4; c4++) o[j][4 * hv + c4] = mfma16x16x32(vf[c4], pf, o[j][4 * hv + c4]);
 #if JIT_PF_PSPLIT
 #pragma unroll
-          for (int i = 0; i < 4; i++) pf.u[i] = pl[j][i];
+          for (int i = 0; i < 4; i++) pf.u[i] = pl[h & 1][j][i];
 #pragma unroll
           for (int c4 = 0; c4 < 4; c4++) o[j][4 * hv + c4] = mfma16x16x32(vf[c4], pf, o[j][4 * hv + c4]);
 #endif
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int j = 0; j < kPfTiles; j++) {
-      if (k0 > tile_last[j]) continue;
       l_run[j] = l_run[j] * alpha[j] + psum[j];
       m_run[j] = m_step[j];
     }
