@@ -788,9 +788,9 @@ OP_KERNELS = {  # the kernels one op launches (rocprofv3 kernel names contain th
     "paged_attention": ["paged_attn_kernel", "attn_merge_kernel"],
     "gate_up_swiglu": ["qmm_kernel<1, 8, true, true"],
     "down": ["qmm_kernel<4, 4, false, true"],
-    "gate_up_swiglu_seg": ["seg_kernel<true, false>"],
-    "down_seg": ["seg_kernel<false, false>"],
-    "qkv_proj_seg": ["seg_kernel<false, true>"],
+    "gate_up_swiglu_seg": ["seg_kernel<true, false,"],  # (any token-chunk length)
+    "down_seg": ["seg_kernel<false, false,"],
+    "qkv_proj_seg": ["seg_kernel<false, true, 10>"],  # (config 3's 2,108 rows: the 10-tile chunk; o_proj takes 5)
     "prefill_attention": ["prefill_attn_kernel"],
 }
 
