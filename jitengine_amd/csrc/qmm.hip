@@ -56,6 +56,7 @@ using qtile::kScaleBytes;
 using qtile::kTileBytes;
 using qtile::nibbles_natural;
 using qtile::unpack_nibbles;
+using qtile::unpack_nibbles2;
 #define UNPACK_CONSTANTS(m, c) QTILE_UNPACK_CONSTANTS(m, c)
 
 using qtile::swiglu_bf16;
@@ -225,7 +226,16 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
         // constraint keeps their unpacking here instead of hoisted (8 VGPRs per word pair)
         uint32_t w0 = wv[g][rb].x, w1 = wv[g][rb].y;
         asm volatile("" : "+v"(w0), "+v"(w1));
-        const Frag8 B0 = unpack_nibbles(w0, um, uc), B1 = unpack_nibbles(w1, um, uc);
+        // (the paired 64-bit shifts save 3 instructions a word pair; the other instances keep the
+        // 32-bit shifts, which need no adjacent register pair: down would pass 168 VGPRs and lose a
+        // wave per SIMD)
+        Frag8 B0, B1;
+        if constexpr (SWIGLU) {
+          unpack_nibbles2(w0, w1, um, uc, B0, B1);
+        } else {
+          B0 = unpack_nibbles(w0, um, uc);
+          B1 = unpack_nibbles(w1, um, uc);
+        }
         const float sc = (g & 1) ? bf2f_hi(sv[rb][g >> 1]) : bf2f(sv[rb][g >> 1] & 0xffffu);
         const float bi = (g & 1) ? bf2f_hi(bv[rb][g >> 1]) : bf2f(bv[rb][g >> 1] & 0xffffu);
         const float bq = fmaf(-128.0f, sc, bi);

@@ -50,6 +50,24 @@ __device__ __forceinline__ Frag8 unpack_nibbles(uint32_t w, uint32_t m, uint32_t
   return f;
 }
 
+// Both words of a lane's group (w0, w1) at once: the shifts by 4, 8 and 12 are 64-bit shifts of
+// the pair (one v_lshrrev_b64 each instead of one shift a word; written out, as the compiler
+// splits a 64-bit shift into two 32-bit ones).  The low word of (w1:w0) >> s takes w1's low bits
+// into its bits 32 - s .. 31, which the mask (bits 0-3 and 16-19) never keeps.
+__device__ __forceinline__ void unpack_nibbles2(uint32_t w0, uint32_t w1, uint32_t m, uint32_t c, Frag8 &b0,
+                                                Frag8 &b1) {
+  const uint64_t w = ((uint64_t)w1 << 32) | w0;
+  b0.u[0] = (w0 & m) | c;
+  b1.u[0] = (w1 & m) | c;
+#pragma unroll
+  for (int j = 1; j < 4; j++) {
+    uint64_t t;
+    asm("v_lshrrev_b64 %0, %1, %2" : "=v"(t) : "n"(4 * j), "v"(w));
+    b0.u[j] = ((uint32_t)t & m) | c;
+    b1.u[j] = ((uint32_t)(t >> 32) & m) | c;
+  }
+}
+
 // The unpack masks as register values the compiler cannot fold back into literals.
 #define QTILE_UNPACK_CONSTANTS(m, c)         \
   uint32_t m = 0x000F000Fu, c = 0x43004300u; \
