@@ -296,12 +296,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       if (p + 1 < GP) load_x(p + 1);
       if (p + 2 < GP) load_w(p + 2);
       tiles(p, 0, bw0, [&](int t) { dequant_word_at(p, 1, t >> 1, t & 1, bw1); });
-      // step p + 1's weights: issued after them, step p + 1's activations (10) and step p + 2's
-      // weights (5), as far as those exist
+      // step p + 1's weights: issued after them, step p + 1's activations (TTS loads, one per
+      // token tile) and step p + 2's weights (5), as far as those exist
       if (p + 2 < GP)
-        seg_wait_vm<15>();
+        seg_wait_vm<TTS + 5>();
       else if (p + 1 < GP)
-        seg_wait_vm<10>();
+        seg_wait_vm<TTS>();
       // (after the last step the dequantization below reads a stale stage and is unused)
       tiles(p, 1, bw1, [&](int t) { dequant_word_at(p + 1, 0, t >> 1, t & 1, bw0); });
     }
