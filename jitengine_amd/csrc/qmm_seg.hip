@@ -6,22 +6,25 @@
 // products in fp32.  Rows are independent, so a row's result does not depend on
 // how many rows its expert has.
 //
-// Work split: a workgroup of 4 waves owns 256 weight rows of one expert (down:
-// 16 row blocks; gate||up: 8 gate blocks and the 8 up blocks of the same output
-// columns, so SwiGLU is fused) and every token of the expert's segment, in
-// chunks of up to 16 * TTMAX tokens.  Each wave owns 4 row blocks.  K is walked in
-// steps of one group pair (128 k): the wave dequantizes its 4 row blocks' pair
-// into bf16 MFMA B fragments once (one fma and half a convert per weight) and uses
-// them against every token tile of the chunk, whose activations the workgroup
-// stages in LDS (gathered through pair_row for gate||up).  The next step's packed
-// weights and activations are loaded while the current step computes.  fp32
-// accumulators: TTMAX x 4 tiles of 16 x 16 per wave.
+// Work split: a workgroup of 8 waves (two a SIMD) owns 256 weight rows of one expert
+// (down: 16 row blocks; gate||up: 8 gate blocks and the 8 up blocks of the same
+// output columns, so SwiGLU is fused) and every token of the expert's segment, in
+// chunks of up to 16 * TTS tokens.  Each wave owns 2 row blocks (gate||up: a gate
+// block and its up block).  K is walked in steps of one group pair (128 k): the wave
+// dequantizes its 2 row blocks' pair into bf16 MFMA B fragments once (one fma and
+// half a convert per weight) and uses them against every token tile of the chunk,
+// whose activations the workgroup stages in LDS (gathered through pair_row for
+// gate||up).  The next step's packed weights and activations are loaded while the
+// current step computes.  Two waves a SIMD let one wave's dequantization (vector ALU)
+// run while the other's MFMAs keep the matrix core busy.  fp32 accumulators: TTS x 2
+// tiles of 16 x 16 per wave.
 #include "qtile.hpp"
 
 namespace {
 
-constexpr int kSegWaves = 4;
-constexpr int kSegRB = 4;                 // row blocks per wave
+constexpr int kSegWaves = 8;
+constexpr int kSegRB = 2;                 // row blocks per wave
+constexpr int kSegThreads = 64 * kSegWaves;
 constexpr int kSegRows = 16 * kSegRB * kSegWaves;  // weight rows per workgroup
 constexpr int kSegTT = 10;                // token tiles per chunk of an expert segment (160 tokens)
 // (a dense batch, one matrix with its token chunks spread over workgroups, sizes its chunks to the
@@ -92,12 +95,13 @@ __device__ __forceinline__ Frag8 dequant_word(uint32_t w, float s, float b) {
 //     read touches (same piece, rows 16 t .. 16 t + 15) fall in 16 different slots: the reads
 //     are free of bank conflicts without the padding the direct global->LDS loads (1 KB = 4
 //     whole rows per wave instruction) could not insert;
-//   three weight stages: per wave its 4 row blocks' nibble tiles of one K step (4 x 1 KB) and
-//     their scale tiles (4 x 128 B, then a copy of them: the instruction writes 1 KB);
+//   three weight stages: per wave its 2 row blocks' nibble tiles of one K step (2 x 1 KB) and
+//     their scale tiles (2 x 128 B, then copies of them: the instruction writes 1 KB);
 //   the chunk's activation row indices.
 // (per chunk of TTS token tiles: the expert segments take kSegTT, dense batches 5, 8 or 10, jit_qmm_seg)
 constexpr int seg_stage_bytes(int tts) { return 16 * tts * 256; }
-constexpr int kSegWWave = 5 * 1024;
+constexpr int kSegWLoads = kSegRB + 1;  // direct loads of a wave's weights per K step
+constexpr int kSegWWave = kSegWLoads * 1024;
 constexpr int kSegWStageBytes = kSegWaves * kSegWWave;
 constexpr int seg_w_off(int tts) { return 2 * seg_stage_bytes(tts); }
 constexpr int seg_row_off(int tts) { return seg_w_off(tts) + 3 * kSegWStageBytes; }
@@ -126,8 +130,9 @@ __device__ __forceinline__ void seg_load_lds(const void *src, uint32_t dst) {
 
 // DENSE: one dense matrix (E = 1, cnt null), one token chunk per group.
 //
-// Pipeline over the K steps p (one group pair each).  Per wave and step, 15 direct loads:
-// 10 of activations (the wave's 4 rows of each token tile) and 5 of its packed weights.
+// Pipeline over the K steps p (one group pair each).  Per wave and step, TTS / 2 + 3 direct
+// loads: TTS / 2 of activations (4 rows of each of half the token tiles: waves 0-3 stage the
+// even tiles, 4-7 the odd ones) and 3 of its packed weights.
 //   top of step p: wait for step p's activations (requested at the top of step p - 1), one
 //     barrier; request step p + 1's activations into the other stage and step p + 2's weights;
 //   group 0's token tiles against B fragments dequantized during step p - 1, with the
@@ -138,8 +143,9 @@ __device__ __forceinline__ void seg_load_lds(const void *src, uint32_t dst) {
 // requested one and a half steps before they are dequantized, activations (mostly L2 hits:
 // an expert's column blocks run on one XCD) a step before they are read.
 template <bool SWIGLU, bool DENSE = false, int TTS = kSegTT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void seg_kernel(const SegArgs a) {
-  constexpr int kTokens = 16 * TTS, kStage = seg_stage_bytes(TTS);
+__global__ __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void seg_kernel(const SegArgs a) {
+  static_assert(TTS % 2 == 0 && TTS >= 2 * kSegRB, "the halves of the waves stage alternate token tiles");
+  constexpr int kTokens = 16 * TTS, kStage = seg_stage_bytes(TTS), kXLoads = TTS / 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t seg_lds[];
   int *xrow = (int *)(seg_lds + seg_row_off(TTS));
   int grp, cb;
@@ -154,22 +160,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)seg_lds);
 
-  // the wave's 4 row blocks (index of the first row / 16 inside the expert's stack)
+  // the wave's 2 row blocks (index of the first row / 16 inside the expert's stack)
   int rbk[kSegRB];
 #pragma unroll
   for (int r = 0; r < kSegRB; r++) {
-    if (SWIGLU)  // gate blocks 8 cb + 2 wave + r (r < 2), and the up blocks of the same columns
-      rbk[r] = (r >= 2 ? a.N / 16 : 0) + cb * 8 + 2 * wave + (r & 1);
+    if (SWIGLU)  // gate block 8 cb + wave, and the up block of the same columns
+      rbk[r] = (r ? a.N / 16 : 0) + cb * 8 + wave;
     else
-      rbk[r] = cb * 16 + 4 * wave + r;
+      rbk[r] = cb * 16 + kSegRB * wave + r;
   }
   const uint8_t *wexp = a.w + (long long)e * a.w_estride;
   const long long tile_row = (long long)GP * qtile::kTileBytes;  // bytes of one row block's tiles
   // weight staging: nibble instruction r moves row block r's tile (lane l: its 16 B piece); the
-  // scale instruction's lane l moves piece l % 8 of row block (l / 8) % 4's scale tile
+  // scale instruction's lane l moves piece l % 8 of row block (l / 8) % 2's scale tile
   const uint8_t *wnib = wexp + 16 * l;
-  const int srb = (l >> 3) & 3;
-  const int rb_s = srb == 0 ? rbk[0] : srb == 1 ? rbk[1] : srb == 2 ? rbk[2] : rbk[3];
+  const int rb_s = (l >> 3) & 1 ? rbk[1] : rbk[0];
   const uint8_t *wscl = wexp + rb_s * tile_row + (long long)GP * qtile::kNibbleBytes + 16 * (l & 7);
   const uint32_t wlds = lds0 + seg_w_off(TTS) + wave * kSegWWave;  // + stage * kSegWStageBytes
   const uint8_t *wmine = seg_lds + seg_w_off(TTS) + wave * kSegWWave;
@@ -178,14 +183,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int r = 0; r < kSegRB; r++)
       seg_load_lds(wnib + rbk[r] * tile_row + p * qtile::kNibbleBytes, __builtin_amdgcn_readfirstlane(st + r * 1024));
-    seg_load_lds(wscl + p * qtile::kScaleBytes, __builtin_amdgcn_readfirstlane(st + 4096));
+    seg_load_lds(wscl + p * qtile::kScaleBytes, __builtin_amdgcn_readfirstlane(st + kSegRB * 1024));
   };
   // B fragment h of group g, row block r, from the staged step p: bf16(s q + b) of the lane's
   // word h of the group (the nibble tile's 16 B piece holds group 0's two words, then group 1's)
   auto dequant_word_at = [&](int p, int g, int r, int h, Frag8 (&bw)[kSegRB][2]) {
     const uint8_t *st = wmine + (p % 3) * kSegWStageBytes;
     const uint32_t q = *(const uint32_t *)(st + r * 1024 + 16 * l + 8 * g + 4 * h);
-    const uint2 sb = *(const uint2 *)(st + 4096 + r * 128 + 8 * lr);
+    const uint2 sb = *(const uint2 *)(st + kSegRB * 1024 + r * 128 + 8 * lr);
     const float sc = g ? bf2f_hi(sb.x) : bf2f(sb.x & 0xffffu);
     const float bi = g ? bf2f_hi(sb.y) : bf2f(sb.y & 0xffffu);
     bw[r][h] = dequant_word(q, sc, bi);
@@ -194,9 +199,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     dequant_word_at(p, g, r, 0, bw);
     dequant_word_at(p, g, r, 1, bw);
   };
-  // activation staging: the wave's instruction j moves rows 16 j + 4 wave .. + 3 (1 KB); lane l
-  // fetches the piece its slot l % 16 holds in row 16 j + srow
-  const int srow = 4 * wave + (l >> 4);
+  // activation staging: the wave's instruction i moves rows 4 (wave % 4) .. + 3 (1 KB) of token
+  // tile j = 2 i + wave / 4; lane l fetches the piece its slot l % 16 holds in row 16 j + srow
+  const int srow = 4 * (wave & 3) + (l >> 4), jhalf = wave >> 2;
   const int spiece = (l & 15) ^ srow;
   // fragment reads: lane (lr, lg) reads pieces 8 g + 2 lg and + 1 of row 16 t + lr
   const int frow = lr * 256;
@@ -206,19 +211,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int nt = min(kTokens, cnt - c0);
     const int ntiles = (nt + 15) >> 4;
     __syncthreads();  // the previous chunk's reads of the stages and of xrow are done
-    for (int j = tid; j < kTokens; j += 256) {
+    for (int j = tid; j < kTokens; j += kSegThreads) {
       const int pos = off + c0 + min(j, nt - 1);  // rows past the segment re-read its last row
       xrow[j] = a.row_index ? a.row_index[pos] : pos;
     }
     __syncthreads();
-    uint32_t xsrc[TTS];  // element offsets of this lane's pieces (x holds < 2^32 elements)
+    uint32_t xsrc[kXLoads];  // element offsets of this lane's pieces (x holds < 2^32 elements)
 #pragma unroll
-    for (int j = 0; j < TTS; j++) xsrc[j] = (uint32_t)xrow[16 * j + srow] * (uint32_t)a.K + 8 * spiece;
+    for (int i = 0; i < kXLoads; i++)
+      xsrc[i] = (uint32_t)xrow[16 * (2 * i + jhalf) + srow] * (uint32_t)a.K + 8 * spiece;
     auto load_x = [&](int p) {
-      const uint32_t st = lds0 + (p & 1) * kStage + 4 * wave * 256;
+      const uint32_t st = lds0 + (p & 1) * kStage + 4 * (wave & 3) * 256;
 #pragma unroll
-      for (int j = 0; j < TTS; j++)
-        seg_load_lds(a.x + xsrc[j] + 128 * p, __builtin_amdgcn_readfirstlane(st + 16 * j * 256));
+      for (int i = 0; i < kXLoads; i++)
+        seg_load_lds(a.x + xsrc[i] + 128 * p, __builtin_amdgcn_readfirstlane(st + 16 * (2 * i + jhalf) * 256));
     };
 
     f32x4 acc[TTS][kSegRB];
@@ -278,7 +284,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     load_w(0);
     if (GP > 1) load_w(1);
     if (GP > 1)
-      seg_wait_vm<5>();
+      seg_wait_vm<kSegWLoads>();
     else
       seg_wait_vm<0>();
     seg_barrier();
@@ -286,9 +292,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int r = 0; r < kSegRB; r++) dequant_rb(0, 0, r, bw0);
     for (int p = 0; p < GP; p++) {
       if (p > 0) {
-        // step p's activations: the loads issued after them are step p + 1's weights (5)
+        // step p's activations: the loads issued after them are step p + 1's weights
         if (p + 1 < GP)
-          seg_wait_vm<5>();
+          seg_wait_vm<kSegWLoads>();
         else
           seg_wait_vm<0>();
         seg_barrier();
@@ -296,12 +302,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       if (p + 1 < GP) load_x(p + 1);
       if (p + 2 < GP) load_w(p + 2);
       tiles(p, 0, bw0, [&](int t) { dequant_word_at(p, 1, t >> 1, t & 1, bw1); });
-      // step p + 1's weights: issued after them, step p + 1's activations (TTS loads, one per
-      // token tile) and step p + 2's weights (5), as far as those exist
+      // step p + 1's weights: issued after them, step p + 1's activations (TTS / 2 loads) and
+      // step p + 2's weights, as far as those exist
       if (p + 2 < GP)
-        seg_wait_vm<TTS + 5>();
+        seg_wait_vm<kXLoads + kSegWLoads>();
       else if (p + 1 < GP)
-        seg_wait_vm<TTS>();
+        seg_wait_vm<kXLoads>();
       // (after the last step the dequantization below reads a stale stage and is unused)
       tiles(p, 1, bw1, [&](int t) { dequant_word_at(p + 1, 0, t >> 1, t & 1, bw0); });
     }
@@ -316,8 +322,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         if (tok >= nt) continue;
         uint16_t *o = a.out + (long long)(off + c0 + tok) * a.N;
         if (SWIGLU) {
-#pragma unroll
-          for (int r = 0; r < 2; r++) o[16 * rbk[r] + lr] = (uint16_t)qtile::swiglu_bf16(acc[t][r][i], acc[t][r + 2][i]);
+          o[16 * rbk[0] + lr] = (uint16_t)qtile::swiglu_bf16(acc[t][0][i], acc[t][1][i]);
         } else {
 #pragma unroll
           for (int r = 0; r < kSegRB; r++) o[16 * rbk[r] + lr] = (uint16_t)f2bf(acc[t][r][i]);
@@ -354,7 +359,7 @@ extern "C" int jit_moe_gate_up_swiglu_seg(const uint16_t *x, int K, const int32_
   SegArgs a{x, pair_row, expert_cnt, expert_off, (const uint8_t *)packed, h, jit_q4_packed_bytes(1, 2 * I, K), K, I, 0,
             I / 128, E};
   seg_prepare<true, false, kSegTT>();
-  seg_kernel<true><<<seg_grid(a.nx, E), 256, seg_lds_bytes(kSegTT), (hipStream_t)stream>>>(a);
+  seg_kernel<true><<<seg_grid(a.nx, E), kSegThreads, seg_lds_bytes(kSegTT), (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_moe_gate_up_swiglu_seg");
 }
 
@@ -370,7 +375,7 @@ extern "C" int jit_moe_down_seg(const uint16_t *h, int I, const int32_t *expert_
   SegArgs a{h, nullptr, expert_cnt, expert_off, (const uint8_t *)packed, r, jit_q4_packed_bytes(1, D, I), I, D, 0,
             D / kSegRows, E};
   seg_prepare<false, false, kSegTT>();
-  seg_kernel<false><<<seg_grid(a.nx, E), 256, seg_lds_bytes(kSegTT), (hipStream_t)stream>>>(a);
+  seg_kernel<false><<<seg_grid(a.nx, E), kSegThreads, seg_lds_bytes(kSegTT), (hipStream_t)stream>>>(a);
   return jit::check_launch("jit_moe_down_seg");
 }
 
@@ -381,12 +386,11 @@ extern "C" int jit_qmm_seg(const uint16_t *x, int T, int K, const void *packed, 
                      N);
   if (T == 0) return JIT_OK;
   if (!x || !packed || !y) return jit::fail(JIT_EINVAL, "qmm_seg: null pointer");
-  // The chunk (token tiles per workgroup) is the smallest of 5, 8, 10 whose workgroups fill the CUs
-  // in one round: chunks of 10 can leave most CUs idle (config 3's o_proj, N = 2048 over 2,108
-  // tokens: 112 workgroups, 89 us, against 216 of 5 tiles, 67 us), while smaller chunks only add
-  // dequantization.  Batches too long for one round take chunks of 10 (12 tiles would fit the LDS,
-  // but their accumulators push the kernel past its registers: 106 us against 96 for qkv, N = 5120,
-  // in two rounds of 10).
+  // The chunk (token tiles per workgroup, even: the two halves of the waves stage alternate
+  // tiles) is the smallest of 4, 6, 8, 10 whose workgroups fill the CUs in one round: chunks of
+  // 10 can leave most CUs idle (config 3's o_proj, N = 2048 over 2,108 tokens: 112 workgroups),
+  // while smaller chunks only add dequantization.  Batches too long for one round take chunks of
+  // 10.
   const int nx = N / kSegRows, cus = jit::cu_count();
   auto groups = [&](int tts) { return (T + 16 * tts - 1) / (16 * tts); };
   const hipStream_t st = (hipStream_t)stream;
@@ -394,10 +398,12 @@ extern "C" int jit_qmm_seg(const uint16_t *x, int T, int K, const void *packed, 
   {                                                                                                            \
     SegArgs a{x, nullptr, nullptr, nullptr, (const uint8_t *)packed, y, 0, K, N, T, nx, groups(TTS)};          \
     seg_prepare<false, true, TTS>();                                                                           \
-    seg_kernel<false, true, TTS><<<seg_grid(nx, groups(TTS)), 256, seg_lds_bytes(TTS), st>>>(a);              \
+    seg_kernel<false, true, TTS><<<seg_grid(nx, groups(TTS)), kSegThreads, seg_lds_bytes(TTS), st>>>(a);      \
   }
-  if (nx * groups(5) <= cus)
-    JIT_QMM_SEG(5)
+  if (nx * groups(4) <= cus)
+    JIT_QMM_SEG(4)
+  else if (nx * groups(6) <= cus)
+    JIT_QMM_SEG(6)
   else if (nx * groups(8) <= cus)
     JIT_QMM_SEG(8)
   else
