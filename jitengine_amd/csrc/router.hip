@@ -336,13 +336,22 @@ __global__ __launch_bounds__(TH) void pack_scan_kernel(int tiles, int E, int32_t
   __shared__ int nxt[TH];
   const int t = threadIdx.x;
   int run = 0;
-  if (t <= E)  // experts, and slot E (the bad pairs)
-    for (int i = 0; i < tiles; i++) {
-      int32_t *q = ws + (long long)i * (E + 1) + t;
-      const int v = *q;
-      *q = run;
-      run += v;
+  if (t <= E) {  // experts, and slot E (the bad pairs)
+    // the tiles' counts in batches whose loads are all issued before the first store (a store
+    // between them would order each load behind the previous one's round trip)
+    constexpr int kBatch = 16;
+    for (int i0 = 0; i0 < tiles; i0 += kBatch) {
+      int v[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; j++) v[j] = i0 + j < tiles ? ws[(long long)(i0 + j) * (E + 1) + t] : 0;
+#pragma unroll
+      for (int j = 0; j < kBatch; j++)
+        if (i0 + j < tiles) {
+          ws[(long long)(i0 + j) * (E + 1) + t] = run;
+          run += v[j];
+        }
     }
+  }
   __shared__ int bad;
   if (t == E) bad = run;
   __syncthreads();
