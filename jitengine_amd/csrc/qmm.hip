@@ -80,11 +80,22 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     // idle experts.  Its offset is the pairs of the experts before it (the packing sorts pairs
     // by expert).  (A grid of E rows keeps the direct lookup: every wave of a full grid reading
     // all the counts would crowd the one L2 channel that holds them.)
+    // The counts of up to kScanAhead * 64 experts are requested together before the first ballot
+    // (one round trip instead of one per 64 experts; a stack of more experts reads the rest as
+    // it goes).
+    constexpr int kScanAhead = 4;
     const int y = blockIdx.y;
     int seen = 0, before = 0;
+    int cpre[kScanAhead];
+#pragma unroll
+    for (int j = 0; j < kScanAhead; j++) cpre[j] = 64 * j + l < a.E ? a.cnt[64 * j + l] : 0;
     e = -1;
     for (int base = 0; base < a.E; base += 64) {  // uniform loop
-      const int c = base + l < a.E ? a.cnt[base + l] : 0;
+      int c = cpre[0];
+#pragma unroll
+      for (int j = 1; j < kScanAhead; j++)
+        if (base == 64 * j) c = cpre[j];
+      if (base >= 64 * kScanAhead) c = base + l < a.E ? a.cnt[base + l] : 0;
       const unsigned long long m = __ballot(c > 0);
       const int n = __popcll(m);
       if (y < seen + n) {

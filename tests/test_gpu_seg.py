@@ -131,10 +131,11 @@ def test_moe_block_prefill_switch():
     assert_close_bf16(u16(y), want, what="prefill experts")
 
 
-@pytest.mark.parametrize("T,N,K", [(512, 2048, 4096), (1200, 5120, 2048), (2108, 5120, 2048)])
+@pytest.mark.parametrize("T,N,K", [(512, 2048, 4096), (2108, 2048, 4096), (1200, 5120, 2048), (2108, 5120, 2048)])
 def test_dense_segment_gemm_repeats_bit_for_bit(T, N, K):
-    """A dense batch sized to each token chunk the launch picks (5, 8 and 10 tiles: a 512-row prompt
-    chunk's o_proj, and config 3's qkv at 1,200 and 2,108 rows) gives the same bits on every call.
+    """A dense batch sized to each token chunk the launch picks on 256 CUs (4, 6, 8 and 10 tiles: the
+    o_proj of a 512-row prompt chunk and of config 3's 2,108 rows, and qkv at 1,200 and 2,108 rows)
+    gives the same bits on every call.
     A regression test: the kernel's waits for its direct global->LDS loads count the loads issued
     after the awaited ones, and with a count fixed for 10-tile chunks the shorter chunks read a
     weight stage before it had landed, now and then."""
