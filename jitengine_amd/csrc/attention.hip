@@ -105,6 +105,9 @@ struct AttnArgs {
   uint16_t *out;
   int max_pages, H, Hkv, G;
   float qk_scale;  // scale * log2(e)
+  int hb;          // kv heads per workgroup (a kernel argument: blockDim.x lives in the implicit
+                   // arguments, whose 16-bit fields the kernel would fetch with a vector load and
+                   // wait for before anything else)
 };
 
 // xor-16 / xor-32 lane exchanges, one VALU op each (gfx950 permlane swaps): with both
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
   extern __shared__ float xstate[];  // [WS - 1][hb][kStateFloats][64]
   const int gc = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
-  const int hb = (blockDim.x >> 6) / WS;  // kv heads per workgroup
+  const int hb = a.hb;
   const int kvl = wave % hb, split = wave / hb;
   const int kvh = blockIdx.y * hb + kvl;
   const bool live = kvh < a.Hkv;  // (dead waves still meet the barrier of the merge)
@@ -806,10 +809,10 @@ int decode_attn_launch(const uint16_t *q, const uint16_t *pool, const int32_t *p
                        const char *what) {
   float *part_o = (float *)workspace;
   float *part_ml = part_o + (long long)total_chunks * H * kD;
-  AttnArgs a{q, pool, page_table, lens, chunk_start, chunk_seq, part_o, part_ml, out,
-             max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f};
   constexpr int WS = kAttnSplits;
   const int hb = Hkv < kAttnHeadsPerBlock ? Hkv : kAttnHeadsPerBlock;  // kv heads per workgroup (WS waves each)
+  AttnArgs a{q, pool, page_table, lens, chunk_start, chunk_seq, part_o, part_ml, out,
+             max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f, hb};
   const size_t lds = (size_t)(WS - 1) * hb * kStateFloats * 64 * sizeof(float);
   paged_attn_kernel<WS><<<dim3(total_chunks, (Hkv + hb - 1) / hb), 64 * hb * WS, lds, st>>>(a);
   int rc = jit::check_launch(what);
