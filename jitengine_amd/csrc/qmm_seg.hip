@@ -209,7 +209,6 @@ __global__ __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(2, 
   const int cend = DENSE ? min(cnt, (grp + 1) * kTokens) : cnt;
   for (int c0 = DENSE ? grp * kTokens : 0; c0 < cend; c0 += kTokens) {
     const int nt = min(kTokens, cnt - c0);
-    const int ntiles = (nt + 15) >> 4;
     __syncthreads();  // the previous chunk's reads of the stages and of xrow are done
     for (int j = tid; j < kTokens; j += kSegThreads) {
       const int pos = off + c0 + min(j, nt - 1);  // rows past the segment re-read its last row
@@ -312,20 +311,27 @@ __global__ __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(2, 
       tiles(p, 1, bw1, [&](int t) { dequant_word_at(p + 1, 0, t >> 1, t & 1, bw0); });
     }
 
-    // lane l holds C[token 16 t + 4 lg + i][row 16 rbk[r] + lr]
+    // lane l holds C[token 16 t + 4 lg + i][row 16 rbk[r] + lr].  No branch per token: the
+    // stores go through a buffer resource (the launch checks that the output spans less than
+    // 2 GiB), and a token past the chunk gets an offset past its range, whose store is dropped.
+    // (Whole tiles past the chunk are skipped: a branch uniform over the wave.)
+    const __amdgpu_buffer_rsrc_t obuf = __builtin_amdgcn_make_buffer_rsrc((void *)a.out, (short)0, 0x7fffffff, 0x00020000);
+    const int ntiles = (nt + 15) >> 4;
 #pragma unroll
     for (int t = 0; t < TTS; t++) {
       if (t >= ntiles) continue;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int tok = 16 * t + 4 * lg + i;
-        if (tok >= nt) continue;
-        uint16_t *o = a.out + (long long)(off + c0 + tok) * a.N;
+        const uint32_t ro = tok < nt ? (uint32_t)(off + c0 + tok) * (uint32_t)a.N * 2u : 0x80000000u;
         if (SWIGLU) {
-          o[16 * rbk[0] + lr] = (uint16_t)qtile::swiglu_bf16(acc[t][0][i], acc[t][1][i]);
+          __builtin_amdgcn_raw_buffer_store_b16((unsigned short)qtile::swiglu_bf16(acc[t][0][i], acc[t][1][i]), obuf,
+                                                (int)(ro + 2u * (16 * rbk[0] + lr)), 0, 0);
         } else {
 #pragma unroll
-          for (int r = 0; r < kSegRB; r++) o[16 * rbk[r] + lr] = (uint16_t)f2bf(acc[t][r][i]);
+          for (int r = 0; r < kSegRB; r++)
+            __builtin_amdgcn_raw_buffer_store_b16((unsigned short)f2bf(acc[t][r][i]), obuf,
+                                                  (int)(ro + 2u * (16 * rbk[r] + lr)), 0, 0);
         }
       }
     }
@@ -356,6 +362,8 @@ extern "C" int jit_moe_gate_up_swiglu_seg(const uint16_t *x, int K, const int32_
   if (P == 0) return JIT_OK;
   if (!x || !pair_row || !expert_cnt || !expert_off || !packed || !h)
     return jit::fail(JIT_EINVAL, "moe_gate_up_seg: null pointer");
+  if ((long long)P * I * 2 >= (1LL << 31))
+    return jit::fail(JIT_EUNSUPPORTED, "moe_gate_up_seg: h of %d x %d bf16 exceeds 2 GiB", P, I);
   SegArgs a{x, pair_row, expert_cnt, expert_off, (const uint8_t *)packed, h, jit_q4_packed_bytes(1, 2 * I, K), K, I, 0,
             I / 128, E};
   seg_prepare<true, false, kSegTT>();
@@ -372,6 +380,8 @@ extern "C" int jit_moe_down_seg(const uint16_t *h, int I, const int32_t *expert_
                      I, D);
   if (P == 0) return JIT_OK;
   if (!h || !expert_cnt || !expert_off || !packed || !r) return jit::fail(JIT_EINVAL, "moe_down_seg: null pointer");
+  if ((long long)P * D * 2 >= (1LL << 31))
+    return jit::fail(JIT_EUNSUPPORTED, "moe_down_seg: r of %d x %d bf16 exceeds 2 GiB", P, D);
   SegArgs a{h, nullptr, expert_cnt, expert_off, (const uint8_t *)packed, r, jit_q4_packed_bytes(1, D, I), I, D, 0,
             D / kSegRows, E};
   seg_prepare<false, false, kSegTT>();
@@ -386,6 +396,8 @@ extern "C" int jit_qmm_seg(const uint16_t *x, int T, int K, const void *packed, 
                      N);
   if (T == 0) return JIT_OK;
   if (!x || !packed || !y) return jit::fail(JIT_EINVAL, "qmm_seg: null pointer");
+  if ((long long)T * N * 2 >= (1LL << 31))
+    return jit::fail(JIT_EUNSUPPORTED, "qmm_seg: y of %d x %d bf16 exceeds 2 GiB", T, N);
   // The chunk (token tiles per workgroup, even: the two halves of the waves stage alternate
   // tiles) is the smallest of 4, 6, 8, 10 whose workgroups fill the CUs in one round: chunks of
   // 10 can leave most CUs idle (config 3's o_proj, N = 2048 over 2,108 tokens: 112 workgroups),

@@ -130,7 +130,10 @@ __device__ __forceinline__ f32x4 group_xsum(const Frag8 (&xa)[2]) {
 // the identical operation sequence, so the sigmoid below rounds the same fp32 value to bf16.
 __device__ __forceinline__ float exp_pos(float x) {
 #pragma clang fp contract(off)
-  if (!(x <= 89.0f)) return x * __builtin_inff();
+  // (no branch: the polynomial runs for every x, and x > 89 or NaN selects x * inf at the end)
+  const float x0 = x;
+  const bool big = !(x <= 89.0f);
+  x = big ? 0.0f : x;
   const float t = x * 1.44269504088896341f;
   const float n = __builtin_rintf(t);
   float r = __builtin_fmaf(-n, 0.693145751953125f, x);
@@ -145,7 +148,8 @@ __device__ __forceinline__ float exp_pos(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
   const int e = (int)n;
   const float sc = __uint_as_float((uint32_t)(e - 1 + 127) << 23);
-  return (p * sc) * 2.0f;
+  const float y = (p * sc) * 2.0f;
+  return big ? x0 * __builtin_inff() : y;
 }
 
 // bf16 round trip of a float (round to nearest even, v_cvt_pk_bf16_f32): exact for every
