@@ -600,8 +600,9 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
 def bench_sampler(dev: str) -> int:
     """The sampler's kernels (csrc/sampler.hip) on the reference's vocabulary (248,320) for 1 and
     32 rows of N(0, 3) logits: log-probabilities, the greedy draw, and draws under the settings of
-    the reference's sampler checks (Q36/sampler.py:575).  One workgroup per row reads its row
-    about six times from L2 (max, log-sum-exp, histogram, weights, the draw's walk); the
+    the reference's sampler checks (Q36/sampler.py:575).  Log-probabilities and greedy split each
+    row over slices, one workgroup a slice, and read it three times; a draw's workgroup reads its
+    row about six times from L2 (max, log-sum-exp, histogram, weights, the draw's walk).  The
     algorithmic bytes are the row's 2 V once."""
     from jitengine_amd import ops
 

@@ -468,6 +468,183 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
   }
 }
 
+// ---- log-probabilities and the greedy draw of a few rows, each row split over workgroups ----
+// One workgroup walks a whole row in the kernel above, so a batch of a few rows leaves most CUs
+// idle (a 248,320-entry row: ~80 us on one CU).  For up to kSplitRows rows each row is cut into
+// slices of whole 8-value steps, one workgroup each, and the row's reductions become launches:
+//   slice maxima -> the row max m0 and the slices' exact integer sums S -> lse, lpmax, and the
+//   slices' log-probabilities or first indices of lpmax -> (greedy) the smallest of those.
+// The partials pass between launches through plain stores to a static buffer and are combined in
+// slice order; max, the integer sum and min do not depend on the order, so every result has the
+// bits of the one-workgroup kernel.  Calls that overlap on one device share the buffer and race.
+constexpr int kSplitThreads = 256, kSplitWaves = kSplitThreads / 64;
+constexpr int kSplitRows = 64, kSplitMax = 64;  // rows, slices per row
+constexpr int kSplitMin = 2048;                  // values a slice holds at least
+
+struct SplitScratch {
+  float max[kSplitRows][kSplitMax];
+  unsigned long long sum[kSplitRows][kSplitMax];
+  int idx[kSplitRows][kSplitMax];
+};
+__device__ SplitScratch g_split;
+
+struct SplitArgs {
+  const uint16_t *logits;
+  int V, ns, len;  // slices per row, values per slice (a multiple of 8)
+  int32_t *tok;
+  uint16_t *lp;
+};
+
+template <bool kVec, typename F>
+__device__ __forceinline__ void slice_steps(const uint16_t *row, int lo, int hi, F &&f) {
+  for (int i0 = lo + 8 * (int)threadIdx.x; i0 < hi; i0 += 8 * kSplitThreads)
+    f(i0, load8<kVec>(row, i0, hi), min(8, hi - i0));
+}
+
+template <bool kVec, typename F>
+__device__ __forceinline__ void slice_each(const uint16_t *row, int lo, int hi, F &&f) {
+  slice_steps<kVec>(row, lo, hi, [&](int i0, const Raw8 &q, int n) {
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      if (j < n) f(i0 + j, val(q, j));
+  });
+}
+
+__device__ __forceinline__ float split_max(float v, float *sh) {
+  v = wave_max(v);
+  __syncthreads();
+  if (lane_id() == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float m = sh[0];
+#pragma unroll
+  for (int w = 1; w < kSplitWaves; w++) m = fmaxf(m, sh[w]);
+  return m;
+}
+
+__device__ __forceinline__ unsigned long long split_sum(unsigned long long v, unsigned long long *sh) {
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane_id() == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  unsigned long long t = 0;
+#pragma unroll
+  for (int w = 0; w < kSplitWaves; w++) t += sh[w];
+  return t;
+}
+
+__device__ __forceinline__ int split_min(int v, int *sh) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if (lane_id() == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int m = sh[0];
+#pragma unroll
+  for (int w = 1; w < kSplitWaves; w++) m = min(m, sh[w]);
+  return m;
+}
+
+// the row max from the slice maxima (thread t < ns reads slice t's)
+__device__ __forceinline__ float split_row_max(int b, int ns, float *sh) {
+  return split_max((int)threadIdx.x < ns ? g_split.max[b][threadIdx.x] : -INFINITY, sh);
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kSplitThreads) void split_max_kernel(const SplitArgs a) {
+  __shared__ float sh[kSplitWaves];
+  const int s = blockIdx.x, b = blockIdx.y;
+  const uint16_t *row = a.logits + (long long)b * a.V;
+  const int lo = s * a.len, hi = min(a.V, lo + a.len);
+  float m = -INFINITY;
+  slice_each<kVec>(row, lo, hi, [&](int, float x) { m = fmaxf(m, x); });
+  m = split_max(m, sh);
+  if (threadIdx.x == 0) g_split.max[b][s] = m;
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kSplitThreads) void split_sum_kernel(const SplitArgs a) {
+  __shared__ float shf[kSplitWaves];
+  __shared__ unsigned long long shq[kSplitWaves];
+  const int s = blockIdx.x, b = blockIdx.y;
+  const uint16_t *row = a.logits + (long long)b * a.V;
+  const int lo = s * a.len, hi = min(a.V, lo + a.len);
+  const float m0 = split_row_max(b, a.ns, shf);
+  uint64_t S = 0;
+  slice_each<kVec>(row, lo, hi, [&](int, float x) { S += fix42(exp_neg(x - m0)); });
+  S = split_sum(S, shq);
+  if (threadIdx.x == 0) g_split.sum[b][s] = S;
+}
+
+template <int kMode, bool kVec>
+__global__ __launch_bounds__(kSplitThreads) void split_final_kernel(const SplitArgs a) {
+  __shared__ float shf[kSplitWaves];
+  __shared__ unsigned long long shq[kSplitWaves];
+  __shared__ int shi[kSplitWaves];
+  const int s = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const uint16_t *row = a.logits + (long long)b * a.V;
+  const int lo = s * a.len, hi = min(a.V, lo + a.len);
+  const float m0 = split_row_max(b, a.ns, shf);
+  const uint64_t S = split_sum(t < a.ns ? g_split.sum[b][t] : 0ull, shq);
+  const float lse = bf16r(m0 + log_ge1(fix42_to_f32(S)));
+  if constexpr (kMode == kLogprobs) {
+    uint16_t *out = a.lp + (long long)b * a.V;
+    slice_steps<kVec>(row, lo, hi, [&](int i0, const Raw8 &q, int n) {
+      uint32_t h[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) h[j] = f2bf(val(q, j) - lse);
+      if (kVec) {
+        if (n == 8)
+          *(uint4 *)(out + i0) = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                            h[6] | (h[7] << 16));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+          if (j < n) out[i0 + j] = (uint16_t)h[j];
+      }
+    });
+  } else {
+    const float lpmax = bf16r(m0 - lse);
+    int best = a.V;
+    slice_each<kVec>(row, lo, hi, [&](int i, float x) {
+      if (bf16r(x - lse) == lpmax && i < best) best = i;
+    });
+    best = split_min(best, shi);
+    if (t == 0) g_split.idx[b][s] = best;
+  }
+}
+
+__global__ __launch_bounds__(64) void split_argmin_kernel(int ns, int V, int32_t *__restrict__ tok) {
+  const int b = blockIdx.x;
+  int m = (int)threadIdx.x < ns ? g_split.idx[b][threadIdx.x] : V;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = min(m, __shfl_xor(m, o, 64));
+  if (threadIdx.x == 0) tok[b] = m < V ? m : 0;  // (a row without a number: 0)
+}
+
+// The split launches of log-probabilities (kLogprobs) or the greedy draw (kGreedy) of B <=
+// kSplitRows rows.
+template <int kMode, bool kVec>
+int launch_split_vec(const SplitArgs &a, int B, hipStream_t st) {
+  const dim3 grid(a.ns, B);
+  split_max_kernel<kVec><<<grid, kSplitThreads, 0, st>>>(a);
+  split_sum_kernel<kVec><<<grid, kSplitThreads, 0, st>>>(a);
+  split_final_kernel<kMode, kVec><<<grid, kSplitThreads, 0, st>>>(a);
+  if (kMode == kGreedy) split_argmin_kernel<<<B, 64, 0, st>>>(a.ns, a.V, a.tok);
+  return jit::check_launch(kMode == kGreedy ? "jit_argmax_rows" : "jit_logprobs_rows");
+}
+
+template <int kMode>
+int launch_split(const uint16_t *logits, int B, int V, int32_t *tok, uint16_t *lp, void *stream) {
+  // about 1024 workgroups in all, at least kSplitMin values each
+  int ns = min(kSplitMax, max(1, 1024 / B));
+  ns = min(ns, (V + kSplitMin - 1) / kSplitMin);
+  const int len = ((V + ns - 1) / ns + 7) / 8 * 8;
+  ns = (V + len - 1) / len;
+  const SplitArgs a{logits, V, ns, len, tok, lp};
+  if ((V & 7) == 0 && ((uintptr_t)logits & 15) == 0) return launch_split_vec<kMode, true>(a, B, (hipStream_t)stream);
+  return launch_split_vec<kMode, false>(a, B, (hipStream_t)stream);
+}
+
 int check_rows(const char *what, const void *logits, int B, int V, const void *out) {
   if (B < 0 || V <= 0) return jit::fail(JIT_EINVAL, "%s: bad dims B=%d V=%d", what, B, V);
   if (V > kMaxV) return jit::fail(JIT_EUNSUPPORTED, "%s covers V <= %d, got %d", what, kMaxV, V);
@@ -501,6 +678,7 @@ float host_bf16(float f) {
 extern "C" int jit_logprobs_rows(const uint16_t *logits, int B, int V, uint16_t *lp, void *stream) {
   if (int rc = check_rows("logprobs_rows", logits, B, V, lp)) return rc;
   if (B == 0) return JIT_OK;
+  if (B <= kSplitRows) return launch_split<kLogprobs>(logits, B, V, nullptr, lp, stream);
   SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, nullptr, lp};
   return launch<kLogprobs>(a, B, stream);
 }
@@ -508,6 +686,7 @@ extern "C" int jit_logprobs_rows(const uint16_t *logits, int B, int V, uint16_t 
 extern "C" int jit_argmax_rows(const uint16_t *logits, int B, int V, int32_t *out, void *stream) {
   if (int rc = check_rows("argmax_rows", logits, B, V, out)) return rc;
   if (B == 0) return JIT_OK;
+  if (B <= kSplitRows) return launch_split<kGreedy>(logits, B, V, out, nullptr, stream);
   SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, out, nullptr};
   return launch<kGreedy>(a, B, stream);
 }
@@ -519,6 +698,7 @@ extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temp
     return jit::fail(JIT_EINVAL, "sample_rows: bad settings T=%g top_p=%g top_k=%d", temperature, top_p, top_k);
   if (B == 0) return JIT_OK;
   if (temperature <= 0.0) {
+    if (B <= kSplitRows) return launch_split<kGreedy>(logits, B, V, tokens, nullptr, stream);
     SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, tokens, nullptr};
     return launch<kGreedy>(a, B, stream);
   }

@@ -47,6 +47,34 @@ def test_greedy_first_max_of_lp():
         assert np.array_equal(ops.sample_rows(t, 0.0, 0.9, 20, None).cpu().numpy(), want), kind
 
 
+def test_split_rows_and_one_workgroup_rows_agree():
+    """Log-probabilities and the greedy draw of up to 64 rows run over slices of each row, one
+    workgroup a slice; 65 rows take one workgroup a row.  Both against the oracle, with ties of the
+    largest lp in different slices, a row whose numbers sit in the last slice only, an all -inf
+    row, one-slice rows and an unaligned vocabulary."""
+    def bf(v):
+        return f32_to_bf16(np.array([v], np.float32))[0]
+
+    for V in (V_REF, 7007, 2000):
+        x = sampler_logits(0, 65, V, 180 + V % 97, scale=3.0).astype(np.uint16)
+        ninf = np.uint16(0xFF80)
+        x[1, :] = f32_to_bf16(np.full(V, -1.0, np.float32))
+        x[1, V // 2], x[1, V - 3] = bf(5.0), bf(5.0)
+        x[2, :] = ninf
+        x[2, V - 1] = bf(-7.5)
+        x[3, :] = ninf
+        x[4, :] = f32_to_bf16(np.full(V, -0.5, np.float32))
+        x[4, V // 3], x[4, V - 5] = bf(0.0), bf(2.0**-8)
+        want_tok = oracle.argmax_rows(x)
+        want_lp = oracle.logprobs_rows(x)
+        assert list(want_tok[1:5]) == [V // 2, V - 1, 0, V // 3]
+        for B in (1, 5, 64, 65):
+            t = bf16_tensor(x[:B], DEV)
+            assert np.array_equal(ops.argmax_rows(t).cpu().numpy(), want_tok[:B]), (V, B)
+            assert np.array_equal(ops.sample_rows(t, 0.0, 1.0, 0, None).cpu().numpy(), want_tok[:B]), (V, B)
+            assert np.array_equal(u16(ops.logprobs_rows(t)), want_lp[:B]), (V, B)
+
+
 SETTINGS = [(0.7, 0.95, 40), (1.0, 0.9, 20), (0.6, 0.8, 64), (1.3, 1.0, 5), (0.3, 1.0, 0), (1.0, 0.95, 0),
             (1.0, 0.8, 0), (0.7, 1.0, 20), (1.0, 1.0, 1), (1.0, 0.5, 1000), (1.0, 0.02, 40), (2.0, 1.0, V_REF),
             (1.0, 0.95, V_REF - 1)]
