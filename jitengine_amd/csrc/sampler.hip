@@ -49,6 +49,7 @@ struct SampleArgs {
   const float *u;
   int32_t *tok;
   uint16_t *lp;
+  int ns;  // > 0: the row's max and integer sum come as ns slice partials from the split launches
 };
 
 // ascending-order key of a log-probability (a bf16 value <= 0): 0x7fff - magnitude, so that
@@ -222,6 +223,17 @@ __global__ __launch_bounds__(kThreads) void threefry_uniform_kernel(const uint32
   u[b] = fminf((float)x0 / 4294967296.0f, 0x1.fffffep-1f);
 }
 
+constexpr int kSplitThreads = 256, kSplitWaves = kSplitThreads / 64;
+constexpr int kSplitRows = 64, kSplitMax = 64;  // rows, slices per row
+constexpr int kSplitMin = 2048;                  // values a slice holds at least
+
+struct SplitScratch {
+  float max[kSplitRows][kSplitMax];
+  unsigned long long sum[kSplitRows][kSplitMax];
+  int idx[kSplitRows][kSplitMax];
+};
+__device__ SplitScratch g_split;
+
 template <int kMode, bool kVec>
 __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs a) {
   __shared__ Shared sh;
@@ -230,12 +242,18 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
   const uint16_t *row = a.logits + (long long)b * V;
 
   // log-sum-exp: the largest logit, then the exact integer sum of the 2^42-scaled exponentials
+  // (a.ns > 0: combined from the slice partials of split_max_kernel / split_sum_kernel)
   float m0 = -INFINITY;
-  for_each<kVec>(row, V, [&](int, float x) { m0 = fmaxf(m0, x); });
-  m0 = wg_max(m0, sh);
   uint64_t S = 0;
-  for_each<kVec>(row, V, [&](int, float x) { S += fix42(exp_neg(x - m0)); });
-  S = wg_sum(S, sh);
+  if (a.ns > 0) {
+    m0 = wg_max(t < a.ns ? g_split.max[b][t] : -INFINITY, sh);
+    S = wg_sum(t < a.ns ? g_split.sum[b][t] : 0ull, sh);
+  } else {
+    for_each<kVec>(row, V, [&](int, float x) { m0 = fmaxf(m0, x); });
+    m0 = wg_max(m0, sh);
+    for_each<kVec>(row, V, [&](int, float x) { S += fix42(exp_neg(x - m0)); });
+    S = wg_sum(S, sh);
+  }
   const float lse = bf16r(m0 + log_ge1(fix42_to_f32(S)));
   const float lpmax = bf16r(m0 - lse);
 
@@ -477,17 +495,6 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
 // The partials pass between launches through plain stores to a static buffer and are combined in
 // slice order; max, the integer sum and min do not depend on the order, so every result has the
 // bits of the one-workgroup kernel.  Calls that overlap on one device share the buffer and race.
-constexpr int kSplitThreads = 256, kSplitWaves = kSplitThreads / 64;
-constexpr int kSplitRows = 64, kSplitMax = 64;  // rows, slices per row
-constexpr int kSplitMin = 2048;                  // values a slice holds at least
-
-struct SplitScratch {
-  float max[kSplitRows][kSplitMax];
-  unsigned long long sum[kSplitRows][kSplitMax];
-  int idx[kSplitRows][kSplitMax];
-};
-__device__ SplitScratch g_split;
-
 struct SplitArgs {
   const uint16_t *logits;
   int V, ns, len;  // slices per row, values per slice (a multiple of 8)
@@ -621,27 +628,33 @@ __global__ __launch_bounds__(64) void split_argmin_kernel(int ns, int V, int32_t
   if (threadIdx.x == 0) tok[b] = m < V ? m : 0;  // (a row without a number: 0)
 }
 
-// The split launches of log-probabilities (kLogprobs) or the greedy draw (kGreedy) of B <=
-// kSplitRows rows.
+// The split launches of B <= kSplitRows rows: log-probabilities (kLogprobs), the greedy draw
+// (kGreedy), or only the slice maxima and sums that sample_rows_kernel then combines (kSample).
 template <int kMode, bool kVec>
 int launch_split_vec(const SplitArgs &a, int B, hipStream_t st) {
   const dim3 grid(a.ns, B);
   split_max_kernel<kVec><<<grid, kSplitThreads, 0, st>>>(a);
   split_sum_kernel<kVec><<<grid, kSplitThreads, 0, st>>>(a);
-  split_final_kernel<kMode, kVec><<<grid, kSplitThreads, 0, st>>>(a);
-  if (kMode == kGreedy) split_argmin_kernel<<<B, 64, 0, st>>>(a.ns, a.V, a.tok);
-  return jit::check_launch(kMode == kGreedy ? "jit_argmax_rows" : "jit_logprobs_rows");
+  if constexpr (kMode != kSample) split_final_kernel<kMode, kVec><<<grid, kSplitThreads, 0, st>>>(a);
+  if constexpr (kMode == kGreedy) split_argmin_kernel<<<B, 64, 0, st>>>(a.ns, a.V, a.tok);
+  return jit::check_launch(kMode == kGreedy ? "jit_argmax_rows" : kMode == kLogprobs ? "jit_logprobs_rows"
+                                                                                       : "jit_sample_rows");
 }
 
-template <int kMode>
-int launch_split(const uint16_t *logits, int B, int V, int32_t *tok, uint16_t *lp, void *stream) {
-  // about 1024 workgroups in all, at least kSplitMin values each
+// The slices of a row: about 1024 workgroups in all, at most kSplitMax a row, at least kSplitMin
+// values each, whole 8-value steps.
+SplitArgs split_args(const uint16_t *logits, int B, int V, int32_t *tok, uint16_t *lp) {
   int ns = min(kSplitMax, max(1, 1024 / B));
   ns = min(ns, (V + kSplitMin - 1) / kSplitMin);
   const int len = ((V + ns - 1) / ns + 7) / 8 * 8;
   ns = (V + len - 1) / len;
-  const SplitArgs a{logits, V, ns, len, tok, lp};
-  if ((V & 7) == 0 && ((uintptr_t)logits & 15) == 0) return launch_split_vec<kMode, true>(a, B, (hipStream_t)stream);
+  return SplitArgs{logits, V, ns, len, tok, lp};
+}
+
+template <int kMode>
+int launch_split(const SplitArgs &a, int B, void *stream) {
+  if ((a.V & 7) == 0 && ((uintptr_t)a.logits & 15) == 0)
+    return launch_split_vec<kMode, true>(a, B, (hipStream_t)stream);
   return launch_split_vec<kMode, false>(a, B, (hipStream_t)stream);
 }
 
@@ -678,7 +691,7 @@ float host_bf16(float f) {
 extern "C" int jit_logprobs_rows(const uint16_t *logits, int B, int V, uint16_t *lp, void *stream) {
   if (int rc = check_rows("logprobs_rows", logits, B, V, lp)) return rc;
   if (B == 0) return JIT_OK;
-  if (B <= kSplitRows) return launch_split<kLogprobs>(logits, B, V, nullptr, lp, stream);
+  if (B <= kSplitRows) return launch_split<kLogprobs>(split_args(logits, B, V, nullptr, lp), B, stream);
   SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, nullptr, lp};
   return launch<kLogprobs>(a, B, stream);
 }
@@ -686,7 +699,7 @@ extern "C" int jit_logprobs_rows(const uint16_t *logits, int B, int V, uint16_t 
 extern "C" int jit_argmax_rows(const uint16_t *logits, int B, int V, int32_t *out, void *stream) {
   if (int rc = check_rows("argmax_rows", logits, B, V, out)) return rc;
   if (B == 0) return JIT_OK;
-  if (B <= kSplitRows) return launch_split<kGreedy>(logits, B, V, out, nullptr, stream);
+  if (B <= kSplitRows) return launch_split<kGreedy>(split_args(logits, B, V, out, nullptr), B, stream);
   SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, out, nullptr};
   return launch<kGreedy>(a, B, stream);
 }
@@ -698,7 +711,7 @@ extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temp
     return jit::fail(JIT_EINVAL, "sample_rows: bad settings T=%g top_p=%g top_k=%d", temperature, top_p, top_k);
   if (B == 0) return JIT_OK;
   if (temperature <= 0.0) {
-    if (B <= kSplitRows) return launch_split<kGreedy>(logits, B, V, tokens, nullptr, stream);
+    if (B <= kSplitRows) return launch_split<kGreedy>(split_args(logits, B, V, tokens, nullptr), B, stream);
     SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, tokens, nullptr};
     return launch<kGreedy>(a, B, stream);
   }
@@ -711,6 +724,11 @@ extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temp
     return jit::fail(JIT_EUNSUPPORTED, "sample_rows: 1 / T = %g is not a finite positive bf16", 1.0 / temperature);
   const int k = top_k >= V ? 0 : top_k;
   SampleArgs a{logits, V, inv_t, thr, k, u, tokens, nullptr};
+  if (B <= kSplitRows) {  // the row's log-sum-exp from slices, the selection and draw in one workgroup
+    const SplitArgs sa = split_args(logits, B, V, nullptr, nullptr);
+    if (int rc = launch_split<kSample>(sa, B, stream)) return rc;
+    a.ns = sa.ns;
+  }
   return launch<kSample>(a, B, stream);
 }
 
