@@ -227,10 +227,18 @@ constexpr int kSplitThreads = 256, kSplitWaves = kSplitThreads / 64;
 constexpr int kSplitRows = 64, kSplitMax = 64;  // rows, slices per row
 constexpr int kSplitMin = 2048;                  // values a slice holds at least
 
+// a draw's cut, from sample_rows_kernel to the slice launches (done: the token is written)
+struct SplitCut {
+  int key_t, r_lo, r_hi, partial, done;
+  float lse, m;
+};
+
 struct SplitScratch {
   float max[kSplitRows][kSplitMax];
   unsigned long long sum[kSplitRows][kSplitMax];
-  int idx[kSplitRows][kSplitMax];
+  int idx[kSplitRows][kSplitMax];             // greedy: first index; draws: members of key_t
+  unsigned long long wsum[kSplitRows][kSplitMax];  // draws: the slice's total weight
+  SplitCut cut[kSplitRows];
 };
 __device__ SplitScratch g_split;
 
@@ -349,7 +357,10 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
     const int key_p = sh.cut[0], j0 = sh.cut[1];
     if (key_p < 0) {  // nothing survives top-p: the greedy token
       const int i = first_max();
-      if (t == 0) a.tok[b] = i;
+      if (t == 0) {
+        a.tok[b] = i;
+        if (a.ns > 0) g_split.cut[b] = SplitCut{0, 0, 0, 0, 1, 0.0f, 0.0f};
+      }
       return;
     }
     auto surv = [&](int key, uint32_t c) -> uint32_t {
@@ -382,6 +393,10 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
     const int key_t = sh.cut[2], r_lo = sh.cut[3], r_hi = sh.cut[4];
     const bool partial = r_lo > 0 || r_hi < (int)hist[key_t];
     const float m = bf16r(lpmax * a.inv_t);
+    if (a.ns > 0) {  // the ranks, weights and the draw run over the row's slices
+      if (t == 0) g_split.cut[b] = SplitCut{key_t, r_lo, r_hi, (int)partial, 0, lse, m};
+      return;
+    }
 
     // ranks of key_t's members: the members in the waves below
     uint32_t tie_base = 0;
@@ -628,6 +643,159 @@ __global__ __launch_bounds__(64) void split_argmin_kernel(int ns, int V, int32_t
   if (threadIdx.x == 0) tok[b] = m < V ? m : 0;  // (a row without a number: 0)
 }
 
+// ---- a draw's weights and walk over the slices (after sample_rows_kernel has set the cut) ----
+struct DrawArgs {
+  const uint16_t *logits;
+  int V, ns, len;
+  float inv_t;
+  const float *u;
+  int32_t *tok;
+};
+
+// exclusive prefix over the workgroup's threads in thread order, and the workgroup's total
+template <typename T>
+__device__ __forceinline__ T split_excl(T v, T *sh, T &total) {
+  const T inc = wave_incl(v);
+  __syncthreads();
+  if (lane_id() == 63) sh[threadIdx.x >> 6] = inc;
+  __syncthreads();
+  T base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSplitWaves; w++) {
+    if (w < (int)(threadIdx.x >> 6)) base += sh[w];
+    tot += sh[w];
+  }
+  total = tot;
+  return base + inc - v;
+}
+
+// the members of key_t in slice s (partial cuts only)
+template <bool kVec>
+__global__ __launch_bounds__(kSplitThreads) void split_ties_kernel(const DrawArgs a) {
+  __shared__ unsigned long long sh[kSplitWaves];
+  const int s = blockIdx.x, b = blockIdx.y;
+  const SplitCut c = g_split.cut[b];
+  if (c.done || !c.partial) return;
+  const uint16_t *row = a.logits + (long long)b * a.V;
+  const int lo = s * a.len, hi = min(a.V, lo + a.len);
+  unsigned long long n = 0;
+  slice_each<kVec>(row, lo, hi, [&](int, float x) { n += key_of(bf16r(x - c.lse)) == c.key_t; });
+  n = split_sum(n, sh);
+  if (threadIdx.x == 0) g_split.idx[b][s] = (int)n;
+}
+
+// The weights of one 2048-value step of a slice from i0s (thread t: the 8 values from i0s + 8 t),
+// the ranks of key_t's members running on from `rank0` in vocabulary order; returns the step's
+// members.  W and the kept rule are sample_rows_kernel's.
+template <bool kVec>
+__device__ __forceinline__ uint32_t split_step_weights(const uint16_t *row, int i0s, int hi, const SplitCut &c,
+                                                       float inv_t, uint32_t rank0, uint32_t *shu, uint64_t W[8],
+                                                       int &n) {
+  const int i0 = i0s + 8 * (int)threadIdx.x;
+  const Raw8 q = load8<kVec>(row, i0, hi);
+  n = max(0, min(8, hi - i0));
+  int key[8];
+  uint32_t ties = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    key[j] = j < n ? key_of(bf16r(val(q, j) - c.lse)) : -1;
+    ties += key[j] == c.key_t;
+  }
+  uint32_t total = 0;
+  uint32_t rank = c.partial ? rank0 + split_excl(ties, shu, total) : 0u;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    bool kept = key[j] > c.key_t;
+    if (key[j] == c.key_t) {
+      kept = !c.partial || ((int)rank >= c.r_lo && (int)rank < c.r_hi);
+      rank++;
+    }
+    W[j] = kept ? fix42(exp_neg(bf16r(bf16r(val(q, j) - c.lse) * inv_t) - c.m)) : 0ull;
+  }
+  return total;
+}
+
+// the members of key_t in the slices before s (partial cuts only)
+__device__ __forceinline__ uint32_t split_tie_base(int b, int s, const SplitCut &c, unsigned long long *sh) {
+  if (!c.partial) return 0u;
+  const int t = threadIdx.x;
+  return (uint32_t)split_sum(t < s ? (unsigned long long)g_split.idx[b][t] : 0ull, sh);
+}
+
+// the slice's total weight
+template <bool kVec>
+__global__ __launch_bounds__(kSplitThreads) void split_weights_kernel(const DrawArgs a) {
+  __shared__ unsigned long long shq[kSplitWaves];
+  __shared__ uint32_t shu[kSplitWaves];
+  const int s = blockIdx.x, b = blockIdx.y;
+  const SplitCut c = g_split.cut[b];
+  if (c.done) return;
+  const uint16_t *row = a.logits + (long long)b * a.V;
+  const int lo = s * a.len, hi = min(a.V, lo + a.len);
+  uint32_t rank = split_tie_base(b, s, c, shq);
+  unsigned long long tw = 0;
+  for (int i0s = lo; i0s < hi; i0s += 8 * kSplitThreads) {
+    uint64_t W[8];
+    int n;
+    rank += split_step_weights<kVec>(row, i0s, hi, c, a.inv_t, rank, shu, W, n);
+#pragma unroll
+    for (int j = 0; j < 8; j++) tw += W[j];
+  }
+  tw = split_sum(tw, shq);
+  if (threadIdx.x == 0) g_split.wsum[b][s] = tw;
+}
+
+// The draw: U = floor(u * total weight); the token is the number of i with C_i = sum_{j<i} W_j
+// <= U, less one.  The slices before the first slice whose prefix passes U count whole, the
+// slices after it none, and that slice is walked.
+template <bool kVec>
+__global__ __launch_bounds__(kSplitThreads) void split_draw_kernel(const DrawArgs a) {
+  __shared__ unsigned long long shq[kSplitWaves];
+  __shared__ uint32_t shu[kSplitWaves];
+  __shared__ unsigned long long pick[2];
+  const int b = blockIdx.x, t = threadIdx.x;
+  const SplitCut c = g_split.cut[b];
+  if (c.done) return;
+  const unsigned long long T = t < a.ns ? g_split.wsum[b][t] : 0ull;
+  unsigned long long total;
+  const unsigned long long P = split_excl(T, shq, total);
+  float u = a.u[b];
+  u = fminf(fmaxf(u, 0.0f), 0x1.fffffep-1f);  // (NaN -> 0)
+  const uint64_t U = mul_u32_u64_hi((uint64_t)(u * 4294967296.0f), total);
+  if (t == 0) pick[0] = (unsigned long long)a.ns;
+  __syncthreads();
+  // the first slice whose prefix with it passes U (the prefixes grow with the slice)
+  if (t < a.ns && P <= U && U < P + T) pick[0] = t, pick[1] = P;
+  __syncthreads();
+  const int s = (int)pick[0];
+  if (s >= a.ns) {  // (a total of 0: every C_i is 0)
+    if (t == 0) a.tok[b] = a.V - 1;
+    return;
+  }
+  const uint16_t *row = a.logits + (long long)b * a.V;
+  const int lo = s * a.len, hi = min(a.V, lo + a.len);
+  uint32_t rank = split_tie_base(b, s, c, shq);
+  unsigned long long run = pick[1], cnt = 0;
+  for (int i0s = lo; i0s < hi; i0s += 8 * kSplitThreads) {
+    uint64_t W[8];
+    int n;
+    rank += split_step_weights<kVec>(row, i0s, hi, c, a.inv_t, rank, shu, W, n);
+    unsigned long long lt = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) lt += W[j];
+    unsigned long long st;
+    unsigned long long cc = run + split_excl(lt, shq, st);  // C of the thread's first value
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      if (j < n && cc <= U) cnt++;
+      cc += W[j];
+    }
+    run += st;
+  }
+  cnt = split_sum(cnt, shq);
+  if (t == 0) a.tok[b] = (int32_t)((unsigned long long)lo + cnt - 1);
+}
+
 // The split launches of B <= kSplitRows rows: log-probabilities (kLogprobs), the greedy draw
 // (kGreedy), or only the slice maxima and sums that sample_rows_kernel then combines (kSample).
 template <int kMode, bool kVec>
@@ -724,12 +892,26 @@ extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temp
     return jit::fail(JIT_EUNSUPPORTED, "sample_rows: 1 / T = %g is not a finite positive bf16", 1.0 / temperature);
   const int k = top_k >= V ? 0 : top_k;
   SampleArgs a{logits, V, inv_t, thr, k, u, tokens, nullptr};
-  if (B <= kSplitRows) {  // the row's log-sum-exp from slices, the selection and draw in one workgroup
-    const SplitArgs sa = split_args(logits, B, V, nullptr, nullptr);
-    if (int rc = launch_split<kSample>(sa, B, stream)) return rc;
-    a.ns = sa.ns;
+  if (B > kSplitRows) return launch<kSample>(a, B, stream);
+  // the row's log-sum-exp over slices, the histogram and the cut in one workgroup a row, then the
+  // ranks, weights and the draw over slices again
+  const SplitArgs sa = split_args(logits, B, V, nullptr, nullptr);
+  if (int rc = launch_split<kSample>(sa, B, stream)) return rc;
+  a.ns = sa.ns;
+  if (int rc = launch<kSample>(a, B, stream)) return rc;
+  const DrawArgs da{logits, V, sa.ns, sa.len, inv_t, u, tokens};
+  const dim3 grid(sa.ns, B);
+  const hipStream_t st = (hipStream_t)stream;
+  if ((V & 7) == 0 && ((uintptr_t)logits & 15) == 0) {
+    split_ties_kernel<true><<<grid, kSplitThreads, 0, st>>>(da);
+    split_weights_kernel<true><<<grid, kSplitThreads, 0, st>>>(da);
+    split_draw_kernel<true><<<B, kSplitThreads, 0, st>>>(da);
+  } else {
+    split_ties_kernel<false><<<grid, kSplitThreads, 0, st>>>(da);
+    split_weights_kernel<false><<<grid, kSplitThreads, 0, st>>>(da);
+    split_draw_kernel<false><<<B, kSplitThreads, 0, st>>>(da);
   }
-  return launch<kSample>(a, B, stream);
+  return jit::check_launch("jit_sample_rows");
 }
 
 extern "C" int jit_threefry_uniform(const uint32_t *keys, int B, float *u, void *stream) {
