@@ -650,7 +650,19 @@ struct DrawArgs {
   float inv_t;
   const float *u;
   int32_t *tok;
+  int nocut;  // no top-p and no top-k: every value is kept, and no histogram or cut ran
 };
+
+// The row's cut: sample_rows_kernel's, or without top-p and top-k the one that keeps every value
+// (key_t 0, no partial tie group) with lse and m from the slice partials.
+__device__ __forceinline__ SplitCut split_cut(const DrawArgs &a, int b, float *shf, unsigned long long *shq) {
+  if (!a.nocut) return g_split.cut[b];
+  const int t = threadIdx.x;
+  const float m0 = split_max(t < a.ns ? g_split.max[b][t] : -INFINITY, shf);
+  const uint64_t S = split_sum(t < a.ns ? g_split.sum[b][t] : 0ull, shq);
+  const float lse = bf16r(m0 + log_ge1(fix42_to_f32(S)));
+  return SplitCut{0, 0, 0, 0, 0, lse, bf16r(bf16r(m0 - lse) * a.inv_t)};
+}
 
 // exclusive prefix over the workgroup's threads in thread order, and the workgroup's total
 template <typename T>
@@ -725,10 +737,11 @@ __device__ __forceinline__ uint32_t split_tie_base(int b, int s, const SplitCut 
 // the slice's total weight
 template <bool kVec>
 __global__ __launch_bounds__(kSplitThreads) void split_weights_kernel(const DrawArgs a) {
+  __shared__ float shf[kSplitWaves];
   __shared__ unsigned long long shq[kSplitWaves];
   __shared__ uint32_t shu[kSplitWaves];
   const int s = blockIdx.x, b = blockIdx.y;
-  const SplitCut c = g_split.cut[b];
+  const SplitCut c = split_cut(a, b, shf, shq);
   if (c.done) return;
   const uint16_t *row = a.logits + (long long)b * a.V;
   const int lo = s * a.len, hi = min(a.V, lo + a.len);
@@ -750,11 +763,12 @@ __global__ __launch_bounds__(kSplitThreads) void split_weights_kernel(const Draw
 // slices after it none, and that slice is walked.
 template <bool kVec>
 __global__ __launch_bounds__(kSplitThreads) void split_draw_kernel(const DrawArgs a) {
+  __shared__ float shf[kSplitWaves];
   __shared__ unsigned long long shq[kSplitWaves];
   __shared__ uint32_t shu[kSplitWaves];
   __shared__ unsigned long long pick[2];
   const int b = blockIdx.x, t = threadIdx.x;
-  const SplitCut c = g_split.cut[b];
+  const SplitCut c = split_cut(a, b, shf, shq);
   if (c.done) return;
   const unsigned long long T = t < a.ns ? g_split.wsum[b][t] : 0ull;
   unsigned long long total;
@@ -895,19 +909,22 @@ extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temp
   if (B > kSplitRows) return launch<kSample>(a, B, stream);
   // the row's log-sum-exp over slices, the histogram and the cut in one workgroup a row, then the
   // ranks, weights and the draw over slices again
+  // (without top-p and top-k every value is kept: no histogram, no cut)
   const SplitArgs sa = split_args(logits, B, V, nullptr, nullptr);
   if (int rc = launch_split<kSample>(sa, B, stream)) return rc;
   a.ns = sa.ns;
-  if (int rc = launch<kSample>(a, B, stream)) return rc;
-  const DrawArgs da{logits, V, sa.ns, sa.len, inv_t, u, tokens};
+  const int nocut = thr == 0.0f && k == 0;
+  if (!nocut)
+    if (int rc = launch<kSample>(a, B, stream)) return rc;
+  const DrawArgs da{logits, V, sa.ns, sa.len, inv_t, u, tokens, nocut};
   const dim3 grid(sa.ns, B);
   const hipStream_t st = (hipStream_t)stream;
   if ((V & 7) == 0 && ((uintptr_t)logits & 15) == 0) {
-    split_ties_kernel<true><<<grid, kSplitThreads, 0, st>>>(da);
+    if (!nocut) split_ties_kernel<true><<<grid, kSplitThreads, 0, st>>>(da);
     split_weights_kernel<true><<<grid, kSplitThreads, 0, st>>>(da);
     split_draw_kernel<true><<<B, kSplitThreads, 0, st>>>(da);
   } else {
-    split_ties_kernel<false><<<grid, kSplitThreads, 0, st>>>(da);
+    if (!nocut) split_ties_kernel<false><<<grid, kSplitThreads, 0, st>>>(da);
     split_weights_kernel<false><<<grid, kSplitThreads, 0, st>>>(da);
     split_draw_kernel<false><<<B, kSplitThreads, 0, st>>>(da);
   }

@@ -107,12 +107,12 @@ def test_sample_rows_grid_of_uniforms():
 
 def test_sample_rows_split_over_slices():
     """Draws of up to 64 rows run their weights and walk over slices of each row: 64 rows whose
-    tie groups (integer logits) span every slice, cut inside a tie group by top-k and top-p, and
-    uniforms across (0, 1)."""
+    tie groups (integer logits) span every slice, cut inside a tie group by top-k and top-p or not
+    cut at all, and uniforms across (0, 1)."""
     for kind in (1, 0):
         x = sampler_logits(kind, 64, V_REF, 190 + kind, scale=3.0)
         u = ((np.arange(64) + 0.5) / 64).astype(np.float32)
-        for T, p, k in [(1.0, 0.9, 20), (0.7, 1.0, 5000), (1.0, 0.5, 0)]:
+        for T, p, k in [(1.0, 0.9, 20), (0.7, 1.0, 5000), (1.0, 0.5, 0), (1.3, 1.0, 0)]:
             got = ops.sample_rows(bf16_tensor(x, DEV), T, p, k, torch.from_numpy(u).to(DEV)).cpu().numpy()
             assert np.array_equal(got, oracle.sample_rows(x, T, p, k, u)), (kind, T, p, k)
 
