@@ -49,7 +49,8 @@ struct SampleArgs {
   const float *u;
   int32_t *tok;
   uint16_t *lp;
-  int ns;  // > 0: the row's max and integer sum come as ns slice partials from the split launches
+  int ns;    // > 0: the row's max and integer sum come as ns slice partials from the split launches
+  int hist;  // (ns > 0) the row's histogram comes from split_hist_kernel
 };
 
 // ascending-order key of a log-probability (a bf16 value <= 0): 0x7fff - magnitude, so that
@@ -239,8 +240,9 @@ struct SplitScratch {
   int idx[kSplitRows][kSplitMax];             // greedy: first index; draws: members of key_t
   unsigned long long wsum[kSplitRows][kSplitMax];  // draws: the slice's total weight
   SplitCut cut[kSplitRows];
+  uint32_t hist[kSplitRows][kKeys];  // draws with a cut: the row's histogram of lp keys
 };
-__device__ SplitScratch g_split;
+__device__ __align__(16) SplitScratch g_split;
 
 template <int kMode, bool kVec>
 __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs a) {
@@ -312,15 +314,27 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
   }
 
   if constexpr (kMode == kSample) {
-    __shared__ uint32_t hist[kKeys];
-    for (int j = t; j < kKeys; j += kThreads) hist[j] = 0u;
-    __syncthreads();
-    for_each<kVec>(row, V, [&](int, float x) { atomicAdd(&hist[key_of(bf16r(x - lse))], 1u); });
+    __shared__ __align__(16) uint32_t hist[kKeys];
+    if (a.hist) {  // the row's histogram from split_hist_kernel
+      for (int j = t; j < kKeys / 4; j += kThreads) ((uint4 *)hist)[j] = ((const uint4 *)g_split.hist[b])[j];
+    } else {
+      for (int j = t; j < kKeys; j += kThreads) hist[j] = 0u;
+      __syncthreads();
+      for_each<kVec>(row, V, [&](int, float x) { atomicAdd(&hist[key_of(bf16r(x - lse))], 1u); });
+    }
     __syncthreads();
 
-    // thread t owns the bins [32 t, 32 t + 32)
+    // thread t owns the bins [32 t, 32 t + 32), held in registers (read from LDS once, 16 bytes
+    // at a time: the lanes' bins lie 128 bytes apart, and element reads of them conflict in
+    // every bank)
     const int k0 = t * kBinsPerThread;
     auto mass_of = [&](int key) { return fix42(bf16r(exp_neg(value_of(key)))); };
+    uint32_t bins[kBinsPerThread];
+#pragma unroll
+    for (int j = 0; j < kBinsPerThread / 4; j++) {
+      const uint4 q = ((const uint4 *)hist)[k0 / 4 + j];
+      bins[4 * j] = q.x, bins[4 * j + 1] = q.y, bins[4 * j + 2] = q.z, bins[4 * j + 3] = q.w;
+    }
 
     // top-p: the boundary bin key_p and the number j0 of its (lowest-index) members cut
     const bool topp = a.thr > 0.0f;
@@ -329,28 +343,32 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
       sh.cut[1] = 0;              // j0
     }
     if (topp) {
-      uint64_t mass = 0;
+      uint64_t F[kBinsPerThread], mass = 0;
+#pragma unroll
       for (int j = 0; j < kBinsPerThread; j++) {
-        const uint32_t c = hist[k0 + j];
-        if (c) mass += (uint64_t)c * mass_of(k0 + j);
+        F[j] = bins[j] ? mass_of(k0 + j) : 0ull;
+        mass += (uint64_t)bins[j] * F[j];
       }
       uint64_t cb = wg_excl<false>(mass, sh);  // (its barriers order the writes above)
+      int jc = -1;                             // the thread's bin where the kept mass starts
+      uint64_t cbc = 0;
+#pragma unroll
       for (int j = 0; j < kBinsPerThread; j++) {
-        const uint32_t c = hist[k0 + j];
-        if (!c) continue;
-        const uint64_t F = mass_of(k0 + j), ce = cb + (uint64_t)c * F;
-        if (fix42_to_bf16(cb) <= a.thr && fix42_to_bf16(ce) > a.thr) {
-          // the smallest j0 whose member (rank j0, cum cb + (j0 + 1) F) survives
-          uint32_t lo = 0, hi = c - 1;
-          while (lo < hi) {
-            const uint32_t mid = (lo + hi) >> 1;
-            if (fix42_to_bf16(cb + (uint64_t)(mid + 1) * F) > a.thr) hi = mid;
-            else lo = mid + 1;
-          }
-          sh.cut[0] = k0 + j;
-          sh.cut[1] = (int)lo;
-        }
+        const uint64_t ce = cb + (uint64_t)bins[j] * F[j];
+        if (bins[j] && fix42_to_bf16(cb) <= a.thr && fix42_to_bf16(ce) > a.thr) jc = j, cbc = cb;
         cb = ce;
+      }
+      if (jc >= 0) {
+        // the smallest j0 whose member (rank j0, cum cbc + (j0 + 1) Fc) survives
+        const uint64_t Fc = mass_of(k0 + jc);
+        uint32_t lo = 0, hi = hist[k0 + jc] - 1;
+        while (lo < hi) {
+          const uint32_t mid = (lo + hi) >> 1;
+          if (fix42_to_bf16(cbc + (uint64_t)(mid + 1) * Fc) > a.thr) hi = mid;
+          else lo = mid + 1;
+        }
+        sh.cut[0] = k0 + jc;
+        sh.cut[1] = (int)lo;
       }
     }
     __syncthreads();
@@ -369,7 +387,8 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
 
     // the kept set: keys above key_t, and the members of key_t's group of rank [r_lo, r_hi)
     uint64_t nt = 0;
-    for (int j = 0; j < kBinsPerThread; j++) nt += surv(k0 + j, hist[k0 + j]);
+#pragma unroll
+    for (int j = 0; j < kBinsPerThread; j++) nt += surv(k0 + j, bins[j]);
     const uint64_t n_surv = wg_sum(nt, sh);
     if (t == 0) {
       sh.cut[2] = key_p;                    // key_t
@@ -378,8 +397,9 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
     }
     if (a.k > 0 && n_surv > (uint64_t)a.k) {
       uint64_t above = wg_excl<true>(nt, sh);  // survivors in the bins of the threads above
+#pragma unroll
       for (int j = kBinsPerThread - 1; j >= 0; j--) {
-        const uint32_t s = surv(k0 + j, hist[k0 + j]);
+        const uint32_t s = surv(k0 + j, bins[j]);
         if (above < (uint64_t)a.k && (uint64_t)a.k <= above + s) {
           const int lo = (k0 + j == key_p) ? j0 : 0;
           sh.cut[2] = k0 + j;
@@ -515,6 +535,7 @@ struct SplitArgs {
   int V, ns, len;  // slices per row, values per slice (a multiple of 8)
   int32_t *tok;
   uint16_t *lp;
+  int hist;  // draws with a cut: split_sum_kernel clears the row's histogram, split_hist_kernel fills it
 };
 
 template <bool kVec, typename F>
@@ -595,6 +616,36 @@ __global__ __launch_bounds__(kSplitThreads) void split_sum_kernel(const SplitArg
   slice_each<kVec>(row, lo, hi, [&](int, float x) { S += fix42(exp_neg(x - m0)); });
   S = split_sum(S, shq);
   if (threadIdx.x == 0) g_split.sum[b][s] = S;
+  if (a.hist) {  // the row's slices clear its histogram for split_hist_kernel
+    uint4 *h = (uint4 *)g_split.hist[b];
+    for (int i = s * kSplitThreads + threadIdx.x; i < kKeys / 4; i += a.ns * kSplitThreads)
+      h[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+// The row's histogram of lp keys (sample_rows_kernel's, which then only copies it): each slice
+// counts its values in LDS and adds its non-empty bins to the row's.  The adds are system-scope
+// atomics (performed past the XCDs' L2s, so slices on different XCDs add to one copy); integer
+// adds, so the counts do not depend on their order.
+template <bool kVec>
+__global__ __launch_bounds__(kSplitThreads) void split_hist_kernel(const SplitArgs a) {
+  __shared__ __align__(16) uint32_t hist[kKeys];
+  __shared__ float shf[kSplitWaves];
+  __shared__ unsigned long long shq[kSplitWaves];
+  const int s = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const uint16_t *row = a.logits + (long long)b * a.V;
+  const int lo = s * a.len, hi = min(a.V, lo + a.len);
+  for (int i = t; i < kKeys / 4; i += kSplitThreads) ((uint4 *)hist)[i] = make_uint4(0u, 0u, 0u, 0u);
+  const float m0 = split_row_max(b, a.ns, shf);
+  const uint64_t S = split_sum(t < a.ns ? g_split.sum[b][t] : 0ull, shq);
+  const float lse = bf16r(m0 + log_ge1(fix42_to_f32(S)));
+  __syncthreads();
+  slice_each<kVec>(row, lo, hi, [&](int, float x) { atomicAdd(&hist[key_of(bf16r(x - lse))], 1u); });
+  __syncthreads();
+  for (int k = t; k < kKeys; k += kSplitThreads) {
+    const uint32_t c = hist[k];
+    if (c) __hip_atomic_fetch_add(&g_split.hist[b][k], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 template <int kMode, bool kVec>
@@ -817,6 +868,8 @@ int launch_split_vec(const SplitArgs &a, int B, hipStream_t st) {
   const dim3 grid(a.ns, B);
   split_max_kernel<kVec><<<grid, kSplitThreads, 0, st>>>(a);
   split_sum_kernel<kVec><<<grid, kSplitThreads, 0, st>>>(a);
+  if constexpr (kMode == kSample)
+    if (a.hist) split_hist_kernel<kVec><<<grid, kSplitThreads, 0, st>>>(a);
   if constexpr (kMode != kSample) split_final_kernel<kMode, kVec><<<grid, kSplitThreads, 0, st>>>(a);
   if constexpr (kMode == kGreedy) split_argmin_kernel<<<B, 64, 0, st>>>(a.ns, a.V, a.tok);
   return jit::check_launch(kMode == kGreedy ? "jit_argmax_rows" : kMode == kLogprobs ? "jit_logprobs_rows"
@@ -910,10 +963,14 @@ extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temp
   // the row's log-sum-exp over slices, the histogram and the cut in one workgroup a row, then the
   // ranks, weights and the draw over slices again
   // (without top-p and top-k every value is kept: no histogram, no cut)
-  const SplitArgs sa = split_args(logits, B, V, nullptr, nullptr);
+  const int nocut = thr == 0.0f && k == 0;
+  SplitArgs sa = split_args(logits, B, V, nullptr, nullptr);
+  // the histogram over slices up to 4 rows (at most 256 workgroups; beyond, the LDS clears and the
+  // adds of more slices cost more than one workgroup a row building its own)
+  sa.hist = !nocut && B <= 4;
   if (int rc = launch_split<kSample>(sa, B, stream)) return rc;
   a.ns = sa.ns;
-  const int nocut = thr == 0.0f && k == 0;
+  a.hist = sa.hist;
   if (!nocut)
     if (int rc = launch<kSample>(a, B, stream)) return rc;
   const DrawArgs da{logits, V, sa.ns, sa.len, inv_t, u, tokens, nocut};
