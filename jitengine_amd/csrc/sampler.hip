@@ -36,6 +36,7 @@ constexpr int kThreads = 1024, kWaves = 16;
 constexpr int kStep = 512;        // values a wave covers per step: 64 lanes x 8
 constexpr int kKeys = 32768;      // histogram bins: the magnitudes of values <= 0
 constexpr int kBinsPerThread = kKeys / kThreads;
+constexpr int kHistSlots = kKeys + kKeys / kBinsPerThread;  // the LDS histogram with its pad words
 constexpr int kMaxV = 1 << 19;    // (2^42-scaled sums of at most 2^20 terms stay below 2^62)
 constexpr int kMaxSteps = (kMaxV / (kWaves * 8) * 8 + kStep - 1) / kStep;  // steps of a wave's range
 
@@ -59,6 +60,9 @@ __device__ __forceinline__ int key_of(float lp) { return 0x7fff - (int)((__float
 __device__ __forceinline__ float value_of(int key) { return __uint_as_float((0x8000u | (uint32_t)(0x7fff - key)) << 16); }
 
 __device__ __forceinline__ float bf16r(float x) { return bf2f(f2bf(x)); }
+
+// the LDS slot of histogram bin k (one pad word after every kBinsPerThread bins)
+__device__ __forceinline__ int hslot(int k) { return k + k / kBinsPerThread; }
 
 // ---- workgroup reductions and scans (every thread of the workgroup calls them) ----
 template <typename T>
@@ -314,27 +318,26 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
   }
 
   if constexpr (kMode == kSample) {
-    __shared__ __align__(16) uint32_t hist[kKeys];
+    // bin k sits in slot hslot(k): a pad word after every 32 bins, so that the 32 bins of thread
+    // t start at word 33 t and the lanes' element reads of them fall in distinct banks
+    __shared__ uint32_t hist[kHistSlots];
     if (a.hist) {  // the row's histogram from split_hist_kernel
-      for (int j = t; j < kKeys / 4; j += kThreads) ((uint4 *)hist)[j] = ((const uint4 *)g_split.hist[b])[j];
+      for (int j = t; j < kKeys / 4; j += kThreads) {
+        const uint4 q = ((const uint4 *)g_split.hist[b])[j];
+        uint32_t *d = hist + hslot(4 * j);  // (4 j .. 4 j + 3 lie in one run of 32)
+        d[0] = q.x, d[1] = q.y, d[2] = q.z, d[3] = q.w;
+      }
     } else {
-      for (int j = t; j < kKeys; j += kThreads) hist[j] = 0u;
+      for (int j = t; j < kHistSlots; j += kThreads) hist[j] = 0u;
       __syncthreads();
-      for_each<kVec>(row, V, [&](int, float x) { atomicAdd(&hist[key_of(bf16r(x - lse))], 1u); });
+      for_each<kVec>(row, V, [&](int, float x) { atomicAdd(&hist[hslot(key_of(bf16r(x - lse)))], 1u); });
     }
     __syncthreads();
 
-    // thread t owns the bins [32 t, 32 t + 32), held in registers (read from LDS once, 16 bytes
-    // at a time: the lanes' bins lie 128 bytes apart, and element reads of them conflict in
-    // every bank)
+    // thread t owns the bins [32 t, 32 t + 32), in the slots from 33 t
     const int k0 = t * kBinsPerThread;
+    const uint32_t *bins = hist + hslot(k0);
     auto mass_of = [&](int key) { return fix42(bf16r(exp_neg(value_of(key)))); };
-    uint32_t bins[kBinsPerThread];
-#pragma unroll
-    for (int j = 0; j < kBinsPerThread / 4; j++) {
-      const uint4 q = ((const uint4 *)hist)[k0 / 4 + j];
-      bins[4 * j] = q.x, bins[4 * j + 1] = q.y, bins[4 * j + 2] = q.z, bins[4 * j + 3] = q.w;
-    }
 
     // top-p: the boundary bin key_p and the number j0 of its (lowest-index) members cut
     const bool topp = a.thr > 0.0f;
@@ -343,25 +346,23 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
       sh.cut[1] = 0;              // j0
     }
     if (topp) {
-      uint64_t F[kBinsPerThread], mass = 0;
-#pragma unroll
-      for (int j = 0; j < kBinsPerThread; j++) {
-        F[j] = bins[j] ? mass_of(k0 + j) : 0ull;
-        mass += (uint64_t)bins[j] * F[j];
-      }
+      uint64_t mass = 0;
+      for (int j = 0; j < kBinsPerThread; j++)
+        if (bins[j]) mass += (uint64_t)bins[j] * mass_of(k0 + j);
       uint64_t cb = wg_excl<false>(mass, sh);  // (its barriers order the writes above)
       int jc = -1;                             // the thread's bin where the kept mass starts
       uint64_t cbc = 0;
-#pragma unroll
       for (int j = 0; j < kBinsPerThread; j++) {
-        const uint64_t ce = cb + (uint64_t)bins[j] * F[j];
-        if (bins[j] && fix42_to_bf16(cb) <= a.thr && fix42_to_bf16(ce) > a.thr) jc = j, cbc = cb;
+        const uint32_t c = bins[j];
+        if (!c) continue;
+        const uint64_t ce = cb + (uint64_t)c * mass_of(k0 + j);
+        if (fix42_to_bf16(cb) <= a.thr && fix42_to_bf16(ce) > a.thr) jc = j, cbc = cb;
         cb = ce;
       }
       if (jc >= 0) {
         // the smallest j0 whose member (rank j0, cum cbc + (j0 + 1) Fc) survives
         const uint64_t Fc = mass_of(k0 + jc);
-        uint32_t lo = 0, hi = hist[k0 + jc] - 1;
+        uint32_t lo = 0, hi = bins[jc] - 1;
         while (lo < hi) {
           const uint32_t mid = (lo + hi) >> 1;
           if (fix42_to_bf16(cbc + (uint64_t)(mid + 1) * Fc) > a.thr) hi = mid;
@@ -387,17 +388,15 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
 
     // the kept set: keys above key_t, and the members of key_t's group of rank [r_lo, r_hi)
     uint64_t nt = 0;
-#pragma unroll
     for (int j = 0; j < kBinsPerThread; j++) nt += surv(k0 + j, bins[j]);
     const uint64_t n_surv = wg_sum(nt, sh);
     if (t == 0) {
       sh.cut[2] = key_p;                    // key_t
       sh.cut[3] = j0;                       // r_lo
-      sh.cut[4] = (int)hist[key_p];         // r_hi
+      sh.cut[4] = (int)hist[hslot(key_p)];  // r_hi
     }
     if (a.k > 0 && n_surv > (uint64_t)a.k) {
       uint64_t above = wg_excl<true>(nt, sh);  // survivors in the bins of the threads above
-#pragma unroll
       for (int j = kBinsPerThread - 1; j >= 0; j--) {
         const uint32_t s = surv(k0 + j, bins[j]);
         if (above < (uint64_t)a.k && (uint64_t)a.k <= above + s) {
@@ -411,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
     }
     __syncthreads();
     const int key_t = sh.cut[2], r_lo = sh.cut[3], r_hi = sh.cut[4];
-    const bool partial = r_lo > 0 || r_hi < (int)hist[key_t];
+    const bool partial = r_lo > 0 || r_hi < (int)hist[hslot(key_t)];
     const float m = bf16r(lpmax * a.inv_t);
     if (a.ns > 0) {  // the ranks, weights and the draw run over the row's slices
       if (t == 0) g_split.cut[b] = SplitCut{key_t, r_lo, r_hi, (int)partial, 0, lse, m};
