@@ -37,6 +37,7 @@ constexpr int kStep = 512;        // values a wave covers per step: 64 lanes x 8
 constexpr int kKeys = 32768;      // histogram bins: the magnitudes of values <= 0
 constexpr int kBinsPerThread = kKeys / kThreads;
 constexpr int kHistSlots = kKeys + kKeys / kBinsPerThread;  // the LDS histogram with its pad words
+static_assert(kKeys % (4 * kThreads) == 0, "the histogram copy takes whole 16-byte words a thread");
 constexpr int kMaxV = 1 << 19;    // (2^42-scaled sums of at most 2^20 terms stay below 2^62)
 constexpr int kMaxSteps = (kMaxV / (kWaves * 8) * 8 + kStep - 1) / kStep;  // steps of a wave's range
 
@@ -321,11 +322,15 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
     // bin k sits in slot hslot(k): a pad word after every 32 bins, so that the 32 bins of thread
     // t start at word 33 t and the lanes' element reads of them fall in distinct banks
     __shared__ uint32_t hist[kHistSlots];
-    if (a.hist) {  // the row's histogram from split_hist_kernel
-      for (int j = t; j < kKeys / 4; j += kThreads) {
-        const uint4 q = ((const uint4 *)g_split.hist[b])[j];
-        uint32_t *d = hist + hslot(4 * j);  // (4 j .. 4 j + 3 lie in one run of 32)
-        d[0] = q.x, d[1] = q.y, d[2] = q.z, d[3] = q.w;
+    if (a.hist) {  // the row's histogram from split_hist_kernel (all loads issued before the stores)
+      constexpr int kCopy = kKeys / 4 / kThreads;
+      uint4 q[kCopy];
+#pragma unroll
+      for (int i = 0; i < kCopy; i++) q[i] = ((const uint4 *)g_split.hist[b])[t + i * kThreads];
+#pragma unroll
+      for (int i = 0; i < kCopy; i++) {
+        uint32_t *d = hist + hslot(4 * (t + i * kThreads));  // (4 j .. 4 j + 3 lie in one run of 32)
+        d[0] = q[i].x, d[1] = q[i].y, d[2] = q[i].z, d[3] = q[i].w;
       }
     } else {
       for (int j = t; j < kHistSlots; j += kThreads) hist[j] = 0u;
