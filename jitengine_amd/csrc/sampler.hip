@@ -339,9 +339,31 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
     }
     __syncthreads();
 
-    // thread t owns the bins [32 t, 32 t + 32), in the slots from 33 t
-    const int k0 = t * kBinsPerThread;
-    const uint32_t *bins = hist + hslot(k0);
+    // The row's values sit in a narrow range of keys (a few hundred bins for logits of any
+    // spread), so the scans below give each thread a contiguous share of the range of non-empty
+    // keys [kl, kh], in key order, rather than of all 32,768: the prefixes are the same (the
+    // empty bins add nothing), and the exp and roundings of the bins run in all 16 waves rather
+    // than in the one whose 32-bin stretches cover them.
+    int kl = kKeys, kh = -1;
+    {
+      const uint32_t *own = hist + hslot(t * kBinsPerThread);  // (slots from 33 t: distinct banks)
+      for (int j = 0; j < kBinsPerThread; j++)
+        if (own[j]) kl = min(kl, t * kBinsPerThread + j), kh = max(kh, t * kBinsPerThread + j);
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        kl = min(kl, __shfl_xor(kl, o, 64));
+        kh = max(kh, __shfl_xor(kh, o, 64));
+      }
+      __shared__ int shk[2][kWaves];
+      if (l == 0) shk[0][t >> 6] = kl, shk[1][t >> 6] = kh;
+      __syncthreads();
+#pragma unroll
+      for (int w = 0; w < kWaves; w++) kl = min(kl, shk[0][w]), kh = max(kh, shk[1][w]);
+    }
+    const int span = kh >= kl ? kh - kl + 1 : 0;
+    const int per = (span + kThreads - 1) / kThreads;  // keys a thread scans (1 for most rows)
+    const int kb = min(kl + t * per, kh + 1), ke = min(kb + per, kh + 1);  // the thread's keys [kb, ke)
+    auto bin = [&](int key) { return hist[hslot(key)]; };
     auto mass_of = [&](int key) { return fix42(bf16r(exp_neg(value_of(key)))); };
 
     // top-p: the boundary bin key_p and the number j0 of its (lowest-index) members cut
@@ -352,28 +374,28 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
     }
     if (topp) {
       uint64_t mass = 0;
-      for (int j = 0; j < kBinsPerThread; j++)
-        if (bins[j]) mass += (uint64_t)bins[j] * mass_of(k0 + j);
+      for (int k = kb; k < ke; k++)
+        if (const uint32_t c = bin(k)) mass += (uint64_t)c * mass_of(k);
       uint64_t cb = wg_excl<false>(mass, sh);  // (its barriers order the writes above)
-      int jc = -1;                             // the thread's bin where the kept mass starts
+      int kc = -1;                             // the thread's bin where the kept mass starts
       uint64_t cbc = 0;
-      for (int j = 0; j < kBinsPerThread; j++) {
-        const uint32_t c = bins[j];
+      for (int k = kb; k < ke; k++) {
+        const uint32_t c = bin(k);
         if (!c) continue;
-        const uint64_t ce = cb + (uint64_t)c * mass_of(k0 + j);
-        if (fix42_to_bf16(cb) <= a.thr && fix42_to_bf16(ce) > a.thr) jc = j, cbc = cb;
+        const uint64_t ce = cb + (uint64_t)c * mass_of(k);
+        if (fix42_to_bf16(cb) <= a.thr && fix42_to_bf16(ce) > a.thr) kc = k, cbc = cb;
         cb = ce;
       }
-      if (jc >= 0) {
+      if (kc >= 0) {
         // the smallest j0 whose member (rank j0, cum cbc + (j0 + 1) Fc) survives
-        const uint64_t Fc = mass_of(k0 + jc);
-        uint32_t lo = 0, hi = bins[jc] - 1;
+        const uint64_t Fc = mass_of(kc);
+        uint32_t lo = 0, hi = bin(kc) - 1;
         while (lo < hi) {
           const uint32_t mid = (lo + hi) >> 1;
           if (fix42_to_bf16(cbc + (uint64_t)(mid + 1) * Fc) > a.thr) hi = mid;
           else lo = mid + 1;
         }
-        sh.cut[0] = k0 + jc;
+        sh.cut[0] = kc;
         sh.cut[1] = (int)lo;
       }
     }
@@ -393,7 +415,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
 
     // the kept set: keys above key_t, and the members of key_t's group of rank [r_lo, r_hi)
     uint64_t nt = 0;
-    for (int j = 0; j < kBinsPerThread; j++) nt += surv(k0 + j, bins[j]);
+    for (int k = kb; k < ke; k++) nt += surv(k, bin(k));
     const uint64_t n_surv = wg_sum(nt, sh);
     if (t == 0) {
       sh.cut[2] = key_p;                    // key_t
@@ -402,11 +424,11 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
     }
     if (a.k > 0 && n_surv > (uint64_t)a.k) {
       uint64_t above = wg_excl<true>(nt, sh);  // survivors in the bins of the threads above
-      for (int j = kBinsPerThread - 1; j >= 0; j--) {
-        const uint32_t s = surv(k0 + j, bins[j]);
+      for (int k = ke - 1; k >= kb; k--) {
+        const uint32_t s = surv(k, bin(k));
         if (above < (uint64_t)a.k && (uint64_t)a.k <= above + s) {
-          const int lo = (k0 + j == key_p) ? j0 : 0;
-          sh.cut[2] = k0 + j;
+          const int lo = (k == key_p) ? j0 : 0;
+          sh.cut[2] = k;
           sh.cut[3] = lo;
           sh.cut[4] = lo + (a.k - (int)above);
         }
