@@ -562,6 +562,7 @@ struct SplitArgs {
   int32_t *tok;
   uint16_t *lp;
   int hist;  // draws with a cut: split_sum_kernel clears the row's histogram, split_hist_kernel fills it
+  int hg;    // slices a split_hist_kernel workgroup counts
 };
 
 template <bool kVec, typename F>
@@ -649,8 +650,8 @@ __global__ __launch_bounds__(kSplitThreads) void split_sum_kernel(const SplitArg
   }
 }
 
-// The row's histogram of lp keys (sample_rows_kernel's, which then only copies it): each slice
-// counts its values in LDS and adds its non-empty bins to the row's.  The adds are system-scope
+// The row's histogram of lp keys (sample_rows_kernel's, which then only copies it): each workgroup
+// counts the values of hg consecutive slices in LDS and adds its non-empty bins to the row's.  The adds are system-scope
 // atomics (performed past the XCDs' L2s, so slices on different XCDs add to one copy); integer
 // adds, so the counts do not depend on their order.
 template <bool kVec>
@@ -660,7 +661,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_hist_kernel(const SplitAr
   __shared__ unsigned long long shq[kSplitWaves];
   const int s = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const uint16_t *row = a.logits + (long long)b * a.V;
-  const int lo = s * a.len, hi = min(a.V, lo + a.len);
+  const int lo = s * a.hg * a.len, hi = min(a.V, lo + a.hg * a.len);
   for (int i = t; i < kKeys / 4; i += kSplitThreads) ((uint4 *)hist)[i] = make_uint4(0u, 0u, 0u, 0u);
   const float m0 = split_row_max(b, a.ns, shf);
   const uint64_t S = split_sum(t < a.ns ? g_split.sum[b][t] : 0ull, shq);
@@ -895,7 +896,7 @@ int launch_split_vec(const SplitArgs &a, int B, hipStream_t st) {
   split_max_kernel<kVec><<<grid, kSplitThreads, 0, st>>>(a);
   split_sum_kernel<kVec><<<grid, kSplitThreads, 0, st>>>(a);
   if constexpr (kMode == kSample)
-    if (a.hist) split_hist_kernel<kVec><<<grid, kSplitThreads, 0, st>>>(a);
+    if (a.hist) split_hist_kernel<kVec><<<dim3((a.ns + a.hg - 1) / a.hg, B), kSplitThreads, 0, st>>>(a);
   if constexpr (kMode != kSample) split_final_kernel<kMode, kVec><<<grid, kSplitThreads, 0, st>>>(a);
   if constexpr (kMode == kGreedy) split_argmin_kernel<<<B, 64, 0, st>>>(a.ns, a.V, a.tok);
   return jit::check_launch(kMode == kGreedy ? "jit_argmax_rows" : kMode == kLogprobs ? "jit_logprobs_rows"
@@ -991,9 +992,10 @@ extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temp
   // (without top-p and top-k every value is kept: no histogram, no cut)
   const int nocut = thr == 0.0f && k == 0;
   SplitArgs sa = split_args(logits, B, V, nullptr, nullptr);
-  // the histogram over slices up to 4 rows (at most 256 workgroups; beyond, the LDS clears and the
-  // adds of more slices cost more than one workgroup a row building its own)
-  sa.hist = !nocut && B <= 4;
+  // the histogram over runs of slices, about 256 workgroups in all (each clears and scans 128 KB
+  // of LDS, so more of them with fewer values each cost more than they save)
+  sa.hist = !nocut;
+  sa.hg = max(1, (sa.ns * B + 255) / 256);
   if (int rc = launch_split<kSample>(sa, B, stream)) return rc;
   a.ns = sa.ns;
   a.hist = sa.hist;
