@@ -346,9 +346,10 @@ int jit_embed_q4(const int32_t *ids, int B, const uint32_t *weight, const uint16
                  const uint16_t *biases, int V, int D, uint16_t *out, void *stream);
 
 /* Token sampling over rows of bf16 logits [B, V] (Q36/sampler.py).  Up to 64 rows are split
- * over slices of each row, one workgroup a slice, with partials in a static device buffer: calls
- * of these three functions that overlap on one device race (issue them on one stream); more rows
- * take one workgroup a row.
+ * over slices of each row, one workgroup a slice, with partials and the draws' histograms in a
+ * static device buffer (8.1 MiB, held on each device the library runs on until the process ends):
+ * calls of these three functions that overlap on one device race (issue them on one stream); more
+ * rows take one workgroup a row.
  * Shared definitions:
  *   lse  = bf16(m0 + ln(S 2^-42)), m0 the row's largest logit and S = sum floor(e^(x - m0) 2^42);
  *   lp   = bf16(x - lse) (logprobs_from_logits, Q36/sampler.py:295-297).
