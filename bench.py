@@ -781,7 +781,142 @@ def probe(dev: str, parts=("read", "launch", "barrier")) -> int:
                     res[phases] = timed(run, 10)
                 out["barrier"][f"{blocks}wg_{words * 4}B_per_wg_us"] = round((res[64] - res[0]) * 1e3 / 64, 3)
         out["barrier"]["timeouts"] = int(status[0])
+
+    if "handoff" in parts:
+        # cross-XCD handoff without cache-wide operations (device-coherent stores, a completion wait,
+        # a device-scope counter; the last workgroup of a group reads its group's words back
+        # device-coherent and checks each against this launch's values), against the same launch
+        # without the handoff and against a second launch doing the read-back; 48 launches with
+        # distinct values per HIP graph
+        lib.probe_handoff.argtypes = [I, I, I, I, I, P, P, P, P]
+        lib.probe_barrier2.argtypes = [I, I, I, P, P, I, P, P]
+        res = {}
+        status = torch.zeros(2, dtype=torch.int32, device=dev)
+        handoff_shapes = ((32, 16, 2048), (256, 2, 2048), (128, 4, 4096), (1, 256, 1024), (1, 32, 4096))
+        for groups, per, words in handoff_shapes:
+            counters = torch.zeros(groups, dtype=torch.int32, device=dev)
+            data = torch.zeros(groups * per * words, dtype=torch.int32, device=dev)
+            ms = {}
+            for mode in range(4):
+                def launches(mode=mode, s=None):
+                    for i in range(48):
+                        rc = lib.probe_handoff(groups, per, words, 1000 * mode + i, mode,
+                                               ctypes.c_void_p(counters.data_ptr()), ctypes.c_void_p(data.data_ptr()),
+                                               ctypes.c_void_p(status.data_ptr()),
+                                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                        assert rc == 0, rc
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    launches()
+                ms[mode] = timed(g.replay, 10) / 48
+                del g
+            key = f"{groups}x{per}wg_{words * 4 // 1024}KB"
+            res[key] = {"write_only_us": round(ms[0] * 1e3, 3),
+                        "handoff_device_scope_us": round(ms[1] * 1e3, 3),
+                        "handoff_system_scope_us": round(ms[2] * 1e3, 3),
+                        "write_then_readback_launch_us": round(ms[3] * 1e3, 3)}
+        torch.cuda.synchronize()
+        res["mismatched_words"] = int(status[0])
+        # every handoff launch must have found exactly one last member per group
+        res["readbacks"] = int(status[1])
+        res["readbacks_expected"] = sum(g * 48 * 11 * 2 for g, _, _ in handoff_shapes)
+        status.zero_()
+        cnt = torch.zeros(1, dtype=torch.int32, device=dev)
+        max_blocks = int(lib.probe_barrier2_max_blocks())
+        for blocks in sorted({256, min(512, max_blocks)}):
+            data = torch.zeros(2 * blocks * 1024, dtype=torch.int32, device=dev)
+            for words in (0, 1024):
+                t_ = {}
+                for phases in (0, 64):
+                    def run(phases=phases, words=words, blocks=blocks, data=data):
+                        cnt.zero_()
+                        rc = lib.probe_barrier2(blocks, phases, words, ctypes.c_void_p(cnt.data_ptr()),
+                                                ctypes.c_void_p(data.data_ptr()), 1 << 22,
+                                                ctypes.c_void_p(status.data_ptr()), sp)
+                        assert rc == 0, rc
+                    t_[phases] = timed(run, 10)
+                res[f"grid_barrier_{blocks}wg_{words * 4}B_per_wg_us"] = round((t_[64] - t_[0]) * 1e3 / 64, 3)
+        torch.cuda.synchronize()
+        res["grid_barrier_mismatched_words"] = int(status[0])
+        res["grid_barrier_timeouts"] = int(status[1])
+        out["handoff"] = res
     print(json.dumps({"probe": out}), flush=True)
+    return 0
+
+
+def gemv_phases(dev: str) -> int:
+    """Where the expert GEMVs' time goes: the gate||up and down kernels of the stamps build
+    (libjit_stamps.so, JIT_QMM_STAMPS=1) on config 2's routing regime (32 tokens x top-8 over 128
+    experts), rotating over 4 layers' stacks so that HBM serves the weights; per workgroup with work,
+    s_memrealtime stamps at entry, once its expert's count is known, once its first pass's loads have
+    landed, after the arithmetic, after the LDS reduction and at its end (csrc/qmm.hip)."""
+    import ctypes
+
+    from jitengine_amd import _lib
+    from jitengine_amd import build as hip_build
+    from jitengine_amd import ops
+    from jitengine_amd.quant import random_quantized
+
+    lib = ctypes.CDLL(hip_build.STAMPS_LIB)
+    for name in ("jit_moe_gate_up_swiglu_packed", "jit_moe_down_packed"):
+        getattr(lib, name).argtypes = _lib._SIGNATURES[name]
+    lib.jit_qmm_stamps_clear.argtypes = [ctypes.c_void_p]
+    lib.jit_qmm_stamps_read.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    E, I, D, B, k = 128, 768, 2048, 32, 8
+    gus = [ops.prepack(random_quantized((E, 2 * I, D), 900 + i, device=dev)) for i in range(4)]
+    dns = [ops.prepack(random_quantized((E, D, I), 950 + i, device=dev)) for i in range(4)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    inds = torch.randn((B, E), generator=gen, device=dev).topk(k, dim=1).indices.to(torch.int32).contiguous()
+    pk = ops.moe_pack(inds, E)
+    P = B * k
+    x = (torch.randn((B, D), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    h = (torch.randn((P, I), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    hout = torch.empty((P, I), dtype=torch.bfloat16, device=dev)
+    rout = torch.empty((P, D), dtype=torch.bfloat16, device=dev)
+    active = int((pk.expert_cnt > 0).sum())
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def gate_up(i):
+        return lib.jit_moe_gate_up_swiglu_packed(p(x), D, p(pk.pair_row), p(pk.expert_cnt), p(pk.expert_off), E,
+                                                 p(gus[i].data), I, P, p(hout), sp)
+
+    def down(i):
+        return lib.jit_moe_down_packed(p(h), I, p(pk.expert_cnt), p(pk.expert_off), E, p(dns[i].data), D, P,
+                                       p(rout), sp)
+
+    out = {"active_experts": active}
+    names = ("count_known", "loads_landed", "arithmetic", "lds_reduction", "epilogue")
+    for kname, fn, per_expert in (("gate_up_swiglu", gate_up, 1769472), ("down", down, 884736)):
+        for rep in range(8):
+            assert fn(rep % 4) == 0
+        torch.cuda.synchronize()
+        assert lib.jit_qmm_stamps_clear(sp) == 0
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_ev.record()
+        assert fn(0) == 0
+        e_ev.record()
+        torch.cuda.synchronize()
+        buf = np.zeros((1 << 16, 8), np.uint64)
+        assert lib.jit_qmm_stamps_read(buf.ctypes.data_as(ctypes.c_void_p), 1 << 16) == 0
+        st = buf[buf[:, 6] == 1][:, :6].astype(np.int64)
+        t0 = st[:, 0].min()
+        span = int(st[:, 5].max() - t0)
+        tick_us = 0.01  # s_memrealtime counts at 100 MHz
+        d = np.diff(st, axis=1) * tick_us
+        life = (st[:, 5] - st[:, 0]) * tick_us
+        res = {"workgroups_with_work": int(st.shape[0]), "event_us": round(s_ev.elapsed_time(e_ev) * 1e3, 2),
+               "stamp_span_us": round(span * tick_us, 2), "wg_life_mean_us": round(float(life.mean()), 3),
+               "mean_resident_wgs": round(float(life.sum()) / (span * tick_us), 1),
+               "alg_MB": round(active * per_expert / 1e6, 1)}
+        for j, n in enumerate(names):
+            res[f"{n}_mean_us"] = round(float(d[:, j].mean()), 3)
+            res[f"{n}_p90_us"] = round(float(np.percentile(d[:, j], 90)), 3)
+        # when the workgroups start, in tenths of the span: how the grid drains
+        res["starts_by_tenth_of_span"] = np.histogram((st[:, 0] - t0) / max(span, 1), bins=10, range=(0, 1))[0].tolist()
+        out[kname] = res
+    print(json.dumps({"gemv_phases": out}), flush=True)
     return 0
 
 
@@ -978,12 +1113,15 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph replay")
+    ap.add_argument("--no-cpu", action="store_true", help="leave out the CPU baseline (quick device-only runs)")
     ap.add_argument("--no-bs1", action="store_true",
                     help="config 2 only: skip the bs=1 (config 4) measurement reported beside it")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--sampler", action="store_true", help="time the sampler's kernels (vocabulary 248,320)")
     ap.add_argument("--probe", action="store_true",
                     help="measure the streaming-read ceiling, the empty-launch floor and the grid-barrier cost")
+    ap.add_argument("--gemv-phases", action="store_true",
+                    help="per-phase stamps of the expert GEMVs (the stamps build of csrc/qmm.hip)")
     ap.add_argument("--probe-parts", default="read,launch,barrier",
                     help="which probe measurements to run (the barrier's cooperative launch ends rocprofv3 badly)")
     ap.add_argument("--rocprof-summary", metavar="DIR",
@@ -1008,13 +1146,15 @@ def main() -> int:
         return copy_calibration(dev)
     if args.probe:
         return probe(dev, set(args.probe_parts.split(",")))
+    if args.gemv_phases:
+        return gemv_phases(dev)
     if args.sampler:
         return bench_sampler(dev)
     if args.config == 1:
         res = bench_config1(args.steps, args.warmup, dev)
     elif args.config in (0, 2, 4):
         res = bench_decode(args.config, args.steps, args.warmup, dev, graph=not args.no_graph,
-                           n_layers=args.layers)
+                           n_layers=args.layers, cpu=not args.no_cpu)
         if args.config == 2 and not args.no_bs1:
             # the metric's bs=1 half: config 4 on the same model, reported beside config 2
             model = res.pop("_model")
@@ -1038,7 +1178,7 @@ def main() -> int:
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
             "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to MLX 4-bit g64)",
-            "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"]}
+            "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res.get("cpu_baseline")}
     for key in ("arithmetic", "step_hbm", "hot_path_hbm", "step_tflops", "op_us", "op_us_per_step", "op_us_sum_per_step", "kernels_us",
                 "bs1"):
         if key in res:

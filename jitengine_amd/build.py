@@ -24,6 +24,8 @@ INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(OUT_DIR, "libjit_moe.so")
 PROBE_LIB = os.path.join(OUT_DIR, "libjit_probe.so")  # bench.py's measurement kernels (csrc/probe.hip)
+# the quantized projections with per-workgroup phase stamps (JIT_QMM_STAMPS=1), for bench.py --gemv-phases
+STAMPS_LIB = os.path.join(OUT_DIR, "libjit_stamps.so")
 ARCH = "gfx950"
 
 SOURCES = {
@@ -51,8 +53,8 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: str, extra: list, verbose: bool) -> str:
-    obj = os.path.join(OUT_DIR, src + ".o")
+def _compile(src: str, extra: list, verbose: bool, tag: str = "") -> str:
+    obj = os.path.join(OUT_DIR, src + tag + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else []
     cmd = [hipcc(), *lang, *_COMMON, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
@@ -66,8 +68,11 @@ def _compile(src: str, extra: list, verbose: bool) -> str:
 def build(verbose: bool = False) -> str:
     """Compile every source and link the shared library; returns its path."""
     os.makedirs(OUT_DIR, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
-        objs = list(ex.map(lambda kv: _compile(kv[0], kv[1], verbose), SOURCES.items()))
+    jobs = [(src, extra, "") for src, extra in SOURCES.items()]
+    jobs += [(src, SOURCES[src] + ["-DJIT_QMM_STAMPS=1"], ".stamps") for src in ("errors.cpp", "qmm.hip")]
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        built = list(ex.map(lambda j: _compile(j[0], j[1], verbose, j[2]), jobs))
+    objs, stamp_objs = built[:len(SOURCES)], built[len(SOURCES):]
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
@@ -76,10 +81,22 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
-    for o in objs:
+    _link(stamp_objs, STAMPS_LIB, verbose)
+    for o in objs + stamp_objs:
         os.remove(o)
     _build_probe(verbose)
     return LIB
+
+
+def _link(objs: list, out: str, verbose: bool) -> None:
+    tmp = out + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(tmp, out)
 
 
 def _build_probe(verbose: bool) -> None:

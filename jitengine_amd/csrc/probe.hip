@@ -133,6 +133,137 @@ __global__ __launch_bounds__(256) void probe_barrier_kernel(int phases, int word
   if (acc == 0x9e3779b9u) status[1] = 1;  // keeps the reads alive
 }
 
+// ------------------------------------------------------------------ cross-XCD handoff
+// Words exchanged between workgroups on different XCDs without any cache-wide operation: the
+// writer stores them device-coherent (the sc1 bit: write-through past its XCD's L2), waits for
+// its stores to complete (s_waitcnt vmcnt(0): a completed sc1 store has reached the device's
+// coherence point), and only then counts itself on a device-scope atomic; a reader issues
+// device-coherent loads (sc1: served from the coherence point, not from a stale line of its own
+// L2) after the atomic has told it every writer finished.  No buffer_wbl2 (write-back of the
+// whole L2) and no buffer_inv (invalidation of it) is issued.  Mode 2 of probe_handoff uses the
+// system-scope bits (sc0 sc1) instead of the device-scope ones, for comparison.
+constexpr int kSc1 = 16, kSc0Sc1 = 17;  // cache-policy operand of the buffer intrinsics
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t probe_rsrc(const void *p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ uint32_t probe_word(int tag, int g, int m, int w) {
+  uint32_t h = (uint32_t)tag * 0x9e3779b1u ^ (uint32_t)g * 0x85ebca77u ^ (uint32_t)m * 0xc2b2ae3du ^ (uint32_t)w;
+  return h * 0x27d4eb2fu + 1u;
+}
+
+// groups x per workgroups; workgroup b is member m = b % per of group g = b / per (consecutive
+// workgroups, so a group spans every XCD).  Each writes `words` words (multiple of 1024) of its
+// own slot, 16 bytes a thread per pass.  MODE 0: plain stores, no handoff (the write-only
+// baseline).  MODE 1: the handoff above -- the member that arrives last on counters[g] reads
+// all per x words of its group back, checks every word against the value its writer stored in
+// this launch (tag), adds the mismatches to status[0], counts its read-back in status[1] and puts
+// the counter back to 0.
+template <int MODE, int POL>
+__global__ __launch_bounds__(256) void probe_handoff_kernel(int per, int words, int tag, uint32_t *counters,
+                                                            uint32_t *data, int *status) {
+  const int b = blockIdx.x, g = b / per, m = b % per, t = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t rs = probe_rsrc(data);
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  const uint32_t slot = (uint32_t)b * (uint32_t)words * 4u;
+  for (int w = 4 * t; w < words; w += 1024) {
+    const u32x4v v = {probe_word(tag, g, m, w), probe_word(tag, g, m, w + 1), probe_word(tag, g, m, w + 2),
+                      probe_word(tag, g, m, w + 3)};
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, slot + 4u * w, 0, MODE ? POL : 0);
+  }
+  if (MODE == 0) return;
+  __shared__ int last;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are complete
+  __syncthreads();
+  if (t == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(counters + g, 1u, __ATOMIC_RELAXED,
+                                                POL == kSc1 ? __HIP_MEMORY_SCOPE_AGENT : __HIP_MEMORY_SCOPE_SYSTEM);
+    last = old == (uint32_t)per - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  int bad = 0;
+  for (int mm = 0; mm < per; mm++) {
+    const uint32_t s = (uint32_t)(g * per + mm) * (uint32_t)words * 4u;
+    for (int w = 4 * t; w < words; w += 1024) {
+      const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(rs, s + 4u * w, 0, POL);
+      bad += (v.x != probe_word(tag, g, mm, w)) + (v.y != probe_word(tag, g, mm, w + 1)) +
+             (v.z != probe_word(tag, g, mm, w + 2)) + (v.w != probe_word(tag, g, mm, w + 3));
+    }
+  }
+  if (bad) atomicAdd(status, bad);
+  if (t == 0) {
+    __hip_atomic_store(counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    atomicAdd(status + 1, 1);  // read-backs done: one per group and launch when every handoff found its last member
+  }
+}
+
+// The same read-back as a launch of its own (the two-launch alternative to the handoff): one
+// workgroup per group reads and checks its group's words with plain loads.
+__global__ __launch_bounds__(256) void probe_readback_kernel(int per, int words, int tag, const uint32_t *data,
+                                                             int *status) {
+  const int g = blockIdx.x, t = threadIdx.x;
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  int bad = 0;
+  for (int mm = 0; mm < per; mm++) {
+    const u32x4v *s = (const u32x4v *)(data + (long long)(g * per + mm) * words);
+    for (int w = 4 * t; w < words; w += 1024) {
+      const u32x4v v = s[w / 4];
+      bad += (v.x != probe_word(tag, g, mm, w)) + (v.y != probe_word(tag, g, mm, w + 1)) +
+             (v.z != probe_word(tag, g, mm, w + 2)) + (v.w != probe_word(tag, g, mm, w + 3));
+    }
+  }
+  if (bad) atomicAdd(status, bad);
+}
+
+// A grid barrier built from the same pieces: per phase each workgroup stores `words` words
+// device-coherent, waits for them, arrives on a device-scope atomic, polls the counter with
+// device-coherent loads (no sleep, no fence) until every workgroup has arrived or spin_limit
+// polls have passed (then it counts itself in status[1] and leaves: every wave ends), and reads
+// its neighbour's words of the phase back device-coherent, counting mismatches in status[0].
+// Every workgroup must be resident at once (the host launches it cooperatively).
+__global__ __launch_bounds__(256) void probe_barrier2_kernel(int phases, int words, uint32_t *counter, uint32_t *data,
+                                                             int spin_limit, int *status) {
+  const int nb = gridDim.x, b = blockIdx.x, t = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t rs = probe_rsrc(data);
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  __shared__ int give_up;
+  int bad = 0;
+  for (int ph = 0; ph < phases; ph++) {
+    const uint32_t slot = (uint32_t)(b + (ph & 1) * nb) * (uint32_t)words * 4u;  // two sets: phases alternate
+    for (int w = 4 * t; w < words; w += 1024) {
+      const u32x4v v = {probe_word(ph, b, 0, w), probe_word(ph, b, 0, w + 1), probe_word(ph, b, 0, w + 2),
+                        probe_word(ph, b, 0, w + 3)};
+      __builtin_amdgcn_raw_buffer_store_b128(v, rs, slot + 4u * w, 0, kSc1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0) {
+      __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t target = (uint32_t)(ph + 1) * (uint32_t)nb;
+      int spins = 0;
+      while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        if (++spins > spin_limit) break;
+      }
+      give_up = spins > spin_limit;
+    }
+    __syncthreads();
+    if (give_up) {
+      if (t == 0) atomicAdd(status + 1, 1);
+      return;
+    }
+    const int nbr = (b + 1) % nb;
+    const uint32_t ns = (uint32_t)(nbr + (ph & 1) * nb) * (uint32_t)words * 4u;
+    for (int w = 4 * t; w < words; w += 1024) {
+      const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(rs, ns + 4u * w, 0, kSc1);
+      bad += (v.x != probe_word(ph, nbr, 0, w)) + (v.y != probe_word(ph, nbr, 0, w + 1)) +
+             (v.z != probe_word(ph, nbr, 0, w + 2)) + (v.w != probe_word(ph, nbr, 0, w + 3));
+    }
+  }
+  if (bad) atomicAdd(status, bad);
+}
+
 // Streaming through an LDS ring by direct global->LDS loads, the shape of a persistent streaming
 // kernel without its arithmetic: each workgroup reads one contiguous run of the buffer in stages
 // of NL KB x L waves (each wave NL loads of 1 KB per stage), S stages of LDS, the loads of S - 2
@@ -281,6 +412,48 @@ extern "C" int probe_barrier(int blocks, int phases, int words, uint32_t *counte
   if (blocks <= 0 || blocks > cap || phases < 0 || words < 0 || !counter || !data || !status) return -1;
   void *args[] = {&phases, &words, &counter, &data, &spin_limit, &status};
   const hipError_t e = hipLaunchCooperativeKernel((const void *)probe_barrier_kernel, dim3(blocks), dim3(256), args,
+                                                  0, (hipStream_t)stream);
+  return e == hipSuccess ? 0 : -3;
+}
+
+// mode 0: write only; 1: device-scope handoff; 2: system-scope handoff; 3: write only, then a
+// read-back launch.  groups * per * words * 4 bytes of data (words a multiple of 1024), groups
+// counters (zero before the first call; every handoff call leaves them zero).
+extern "C" int probe_handoff(int groups, int per, int words, int tag, int mode, uint32_t *counters, uint32_t *data,
+                             int *status, void *stream) {
+  if (groups <= 0 || per <= 0 || words <= 0 || words % 1024 || mode < 0 || mode > 3 || !counters || !data || !status ||
+      (long long)groups * per * words * 4 > 0x7fffffffLL)
+    return -1;
+  hipStream_t st = (hipStream_t)stream;
+  const int n = groups * per;
+  switch (mode) {
+    case 0: probe_handoff_kernel<0, 0><<<n, 256, 0, st>>>(per, words, tag, counters, data, status); break;
+    case 1: probe_handoff_kernel<1, kSc1><<<n, 256, 0, st>>>(per, words, tag, counters, data, status); break;
+    case 2: probe_handoff_kernel<1, kSc0Sc1><<<n, 256, 0, st>>>(per, words, tag, counters, data, status); break;
+    default:
+      probe_handoff_kernel<0, 0><<<n, 256, 0, st>>>(per, words, tag, counters, data, status);
+      probe_readback_kernel<<<groups, 256, 0, st>>>(per, words, tag, data, status);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int probe_barrier2_max_blocks(void) {
+  int dev = 0, per_cu = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -3;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, probe_barrier2_kernel, 256, 0) != hipSuccess) return -3;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -3;
+  return per_cu * cus;
+}
+
+// data: 2 * blocks * words words (words a multiple of 1024, or 0)
+extern "C" int probe_barrier2(int blocks, int phases, int words, uint32_t *counter, uint32_t *data, int spin_limit,
+                              int *status, void *stream) {
+  const int cap = probe_barrier2_max_blocks();
+  if (blocks <= 0 || blocks > cap || phases < 0 || words < 0 || words % 1024 || !counter || !data || !status ||
+      2LL * blocks * words * 4 > 0x7fffffffLL)
+    return -1;
+  void *args[] = {&phases, &words, &counter, &data, &spin_limit, &status};
+  const hipError_t e = hipLaunchCooperativeKernel((const void *)probe_barrier2_kernel, dim3(blocks), dim3(256), args,
                                                   0, (hipStream_t)stream);
   return e == hipSuccess ? 0 : -3;
 }

@@ -61,8 +61,45 @@ using qtile::unpack_nibbles2;
 
 using qtile::swiglu_bf16;
 
+// The outputs of a workgroup of 4 or more row blocks without SwiGLU (down) leave the LDS reduction
+// as 16-byte stores of 8 adjacent outputs per thread: each thread's one item instead of a wave's
+// 5-6 rounds of 2-byte stores per lane (config 2: down 23.5 -> 21.2 us, the same bits).  Narrower
+// workgroups keep the per-lane stores (the dense projections' 32 items would sit on one wave:
+// o_proj 6.8 -> 7.1 us).  JIT_QMM_VEC_EPILOGUE=0 builds the per-lane stores everywhere.
+#ifndef JIT_QMM_VEC_EPILOGUE
+#define JIT_QMM_VEC_EPILOGUE 1
+#endif
+constexpr bool kVecEpilogue = JIT_QMM_VEC_EPILOGUE;
+constexpr int kVecEpilogueMinNb = 4;
+
+// Phase stamps (a build with JIT_QMM_STAMPS=1 only, bench.py --gemv-phases): wave 0 of every
+// workgroup that has work records s_memrealtime (a constant 100 MHz clock shared by the device) at
+// kernel entry (0), once its expert's count is known and its first loads go out (1), once every load
+// of its first pass has landed (2; that build waits for all of them there instead of group by group),
+// when the pass's arithmetic is done (3), after the K-split partial sums have met in LDS (4) and at
+// its end (5).
+#ifndef JIT_QMM_STAMPS
+#define JIT_QMM_STAMPS 0
+#endif
+#if JIT_QMM_STAMPS
+constexpr int kStampSlots = 1 << 16;
+__device__ uint64_t g_qmm_stamps[kStampSlots][8];
+#define QMM_STAMP(i)                                        \
+  do {                                                      \
+    if (stamp_pass == 0) ts[i] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define QMM_STAMP(i) \
+  do {               \
+  } while (0)
+#endif
+
 template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false>
 __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
+#if JIT_QMM_STAMPS
+  uint64_t ts[6] = {__builtin_amdgcn_s_memrealtime(), 0, 0, 0, 0, 0};
+  int stamp_pass = 0;
+#endif
   static_assert(!PACKED || GPW % 2 == 0, "packed tiles hold pairs of groups");
   constexpr int NBW = SWIGLU ? 2 * NB : NB;  // weight row blocks (gate and up blocks with SWIGLU)
   extern __shared__ float red[];             // [KSPLIT][TT][NBW][4][64]
@@ -115,6 +152,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     off = 0;
   }
   if (cnt <= 0) return;  // uniform over the workgroup
+  QMM_STAMP(1);
   const int n0 = blockIdx.x * (16 * NB);
   const int G = a.K >> 6, KW = a.K >> 3;
   const int g0 = wave * GPW;
@@ -262,6 +300,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
       // unpacked fragments ahead would cost 8 registers per (group, block))
       __builtin_amdgcn_sched_barrier(0);
     }
+    QMM_STAMP(3);
     // ---- the waves' partial sums meet in LDS; lane l holds C[token 4*lg + i][row lr]
 #pragma unroll
     for (int tt = 0; tt < TT; tt++)
@@ -270,6 +309,38 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) red[(((wave * TT + tt) * NBW + rb) * 4 + i) * 64 + l] = acc[tt][rb][i];
     __syncthreads();
+    QMM_STAMP(4);
+    if constexpr (!SWIGLU && kVecEpilogue && NB >= kVecEpilogueMinNb) {
+      // each thread owns 8 adjacent outputs of one token: (tile, token, row octet) items spread over
+      // the threads, the partial sums read as two 16-byte LDS reads per wave slice and added in wave
+      // order as below, the outputs stored as one 16-byte store
+      const int nthr = ksplit * 64;
+      for (int it = threadIdx.x; it < TT * 16 * 2 * NB; it += nthr) {
+        const int half = it & 1, tok = (it >> 1) & 15, rest = it >> 5;
+        const int ob = rest % NB, tt = rest / NB;
+        const int t = t0 + 16 * tt + tok;
+        if (n0 + 16 * ob >= a.N || t >= cnt) continue;
+        const int lane0 = 16 * (tok >> 2) + 8 * half;
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int ks = 0; ks < ksplit; ks++) {
+          const float *pr = red + (((ks * TT + tt) * NBW + ob) * 4 + (tok & 3)) * 64 + lane0;
+          const float4 p0 = *(const float4 *)pr, p1 = *(const float4 *)(pr + 4);
+          v[0] += p0.x;
+          v[1] += p0.y;
+          v[2] += p0.z;
+          v[3] += p0.w;
+          v[4] += p1.x;
+          v[5] += p1.y;
+          v[6] += p1.z;
+          v[7] += p1.w;
+        }
+        const uint4 w = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                                   pack_bf16x2(v[6], v[7]));
+        *(uint4 *)(a.out + (long long)(off + t) * a.N + n0 + 16 * ob + 8 * half) = w;
+      }
+      __syncthreads();
+      return;
+    }
     // (tile, output block, token row i) triples are spread over the waves
     for (int idx = wave; idx < TT * 4 * NB; idx += ksplit) {
       const int tt = idx / (4 * NB), ob = (idx >> 2) % NB, i = idx & 3;
@@ -301,7 +372,15 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
           bv[rb][j] = (uint32_t)__shfl((int)sbl[rb].y, 16 * j + lr, 64);
         }
     }
+#if JIT_QMM_STAMPS
+    __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("" ::: "memory");
+#endif
+    QMM_STAMP(2);
     pass(tfirst, xa);
+#if JIT_QMM_STAMPS
+    stamp_pass = 1;
+#endif
   }
   for (int t0 = tfirst + tstride; t0 < cnt; t0 += tstride) {
     int rows[TT];
@@ -311,6 +390,17 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     load_x(t0, rows, xa);
     pass(t0, xa);
   }
+#if JIT_QMM_STAMPS
+  ts[5] = __builtin_amdgcn_s_memrealtime();
+  const long long slot = blockIdx.x + (long long)gridDim.x * (blockIdx.y + (long long)gridDim.y * blockIdx.z);
+  if (threadIdx.x < 6 && slot < kStampSlots) {
+    uint64_t v = ts[0];
+#pragma unroll
+    for (int i = 1; i < 6; i++) v = threadIdx.x == i ? ts[i] : v;
+    g_qmm_stamps[slot][threadIdx.x] = v;
+  }
+  if (threadIdx.x == 6 && slot < kStampSlots) g_qmm_stamps[slot][6] = 1;  // (a workgroup with work)
+#endif
 }
 
 template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false>
@@ -543,3 +633,17 @@ extern "C" int jit_moe_down_packed(const uint16_t *h, int I, const int32_t *expe
   if (P < E) return launch_qmm<kDnNb, kDnGpw, false, true, 1, true>(a, P, (hipStream_t)stream, "jit_moe_down_packed");
   return launch_qmm<kDnNb, kDnGpw, false, true>(a, E, (hipStream_t)stream, "jit_moe_down_packed");
 }
+
+#if JIT_QMM_STAMPS
+// The stamps of the last launches (bench.py --gemv-phases): clear, then copy out kStampSlots x 8 words.
+extern "C" int jit_qmm_stamps_clear(void *stream) {
+  void *p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_qmm_stamps)) != hipSuccess) return JIT_ELAUNCH;
+  return hipMemsetAsync(p, 0, sizeof(g_qmm_stamps), (hipStream_t)stream) == hipSuccess ? 0 : JIT_ELAUNCH;
+}
+extern "C" int jit_qmm_stamps_read(uint64_t *host, int slots) {
+  if (!host || slots < 0 || slots > kStampSlots) return JIT_EINVAL;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_qmm_stamps), (size_t)slots * 8 * sizeof(uint64_t), 0,
+                             hipMemcpyDeviceToHost) == hipSuccess ? 0 : JIT_ELAUNCH;
+}
+#endif
