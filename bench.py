@@ -56,12 +56,27 @@ HOT_OPS = ("paged_attention", "gate_up_swiglu", "down")  # the ops that move the
 
 
 def hot_path_hbm(step_us: dict, alg_bytes: int) -> dict:
-    """The north-star measure of a decode step: its quantized-expert and KV-pool bytes (alg_bytes)
-    over the summed live time of the ops that move them (step_us: microseconds per step by op)."""
+    """A kernel-level diagnostic, not the north-star measure: a decode step's quantized-expert and
+    KV-pool bytes (alg_bytes) over the summed live time of only the ops that move them (step_us:
+    microseconds per step by op), leaving out the rest of the step."""
     us = sum(step_us[n] for n in HOT_OPS if n in step_us)
     gbs = alg_bytes / (us * 1e-6) / 1e9 if us > 0 else None
-    return {"ops": list(HOT_OPS), "alg_bytes": alg_bytes, "us_per_step": us, "GB_s": gbs,
-            "frac": gbs / HBM_PEAK_GBS if gbs else None, "target_frac": 0.6}
+    return {"label": "diagnostic: hot ops' live time only (not the whole step)", "ops": list(HOT_OPS),
+            "alg_bytes": alg_bytes, "us_per_step": us, "GB_s": gbs, "frac": gbs / HBM_PEAK_GBS if gbs else None}
+
+
+NORTH_STAR_FRAC = 0.6  # BASELINE.json: >= 60% of HBM peak on the combined expert + KV-pool traffic
+
+
+def north_star(alg_bytes: int, ms_per_step: float, rows: int) -> dict:
+    """The north-star measure as BASELINE defines it: the step's quantized-expert and KV-pool bytes
+    over the whole step's time (every launch of the step included), as a fraction of the 8 TB/s peak,
+    and the tokens/s a step meeting the 60% target would give on these bytes."""
+    gbs = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    target_ms = alg_bytes / (NORTH_STAR_FRAC * HBM_PEAK_GBS * 1e9) * 1e3
+    return {"alg_bytes": alg_bytes, "ms_per_step": ms_per_step, "GB_s": gbs, "frac": gbs / HBM_PEAK_GBS,
+            "target_frac": NORTH_STAR_FRAC, "met": gbs / HBM_PEAK_GBS >= NORTH_STAR_FRAC,
+            "tokens_s": rows / (ms_per_step * 1e-3), "tokens_s_at_target": rows / (target_ms * 1e-3)}
 
 
 def time_ops(launches: dict, reps: int = 5) -> dict:
@@ -553,6 +568,7 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
                      "split": {"experts": sum(U) * per_expert, "kv": n_layers * kv, "dense": n_layers * dense}},
         # the target's own measure: the quantized-expert and KV-pool bytes of a step over the time of
         # the ops that move them (attention with its merge, gate||up, down), each timed live
+        "north_star": north_star(sum(U) * per_expert + n_layers * kv, ms, B),
         "hot_path_hbm": hot_path_hbm(step_us, sum(U) * per_expert + n_layers * kv),
         "op_us": kus,
         "op_us_per_step": step_us,
@@ -1162,7 +1178,8 @@ def main() -> int:
             r4 = bench_decode(4, args.steps, args.warmup, dev, graph=not args.no_graph, model=model, cpu=False)
             res["bs1"] = {"workload": r4["config"]["workload"] + " (config 2's weights)",
                           "value": r4["value"], "unit": "tokens/s", "ms_per_step": r4["ms_per_step"],
-                          "step_hbm": r4["step_hbm"], "hot_path_hbm": r4["hot_path_hbm"],
+                          "step_hbm": r4["step_hbm"], "north_star": r4["north_star"],
+                          "hot_path_hbm": r4["hot_path_hbm"],
                           "op_us_per_step": r4["op_us_per_step"],
                           "attention": {k: r4["roofline"][k] for k in ("achieved", "alg_bytes_per_launch",
                                                                         "launch_us")} | {"unit": "GB/s"}}
@@ -1179,7 +1196,7 @@ def main() -> int:
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
             "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to MLX 4-bit g64)",
             "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res.get("cpu_baseline")}
-    for key in ("arithmetic", "step_hbm", "hot_path_hbm", "step_tflops", "op_us", "op_us_per_step", "op_us_sum_per_step", "kernels_us",
+    for key in ("arithmetic", "step_hbm", "north_star", "hot_path_hbm", "step_tflops", "op_us", "op_us_per_step", "op_us_sum_per_step", "kernels_us",
                 "bs1"):
         if key in res:
             line[key] = res[key]

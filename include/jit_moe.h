@@ -347,9 +347,12 @@ int jit_embed_q4(const int32_t *ids, int B, const uint32_t *weight, const uint16
 
 /* Token sampling over rows of bf16 logits [B, V] (Q36/sampler.py).  Up to 64 rows are split
  * over slices of each row, one workgroup a slice, with partials and the draws' histograms in a
- * static device buffer (8.1 MiB, held on each device the library runs on until the process ends):
- * calls of these three functions that overlap on one device race (issue them on one stream); more
- * rows take one workgroup a row.
+ * workspace: the caller's (the _ws entry points, jit_sampler_workspace_bytes() bytes, 16-byte
+ * aligned, contents on entry do not matter) or, for the entry points without one, a static device
+ * buffer of the same size (8.1 MiB, held on each device the library runs on until the process
+ * ends).  Calls that share a workspace -- or the static buffer -- and overlap in time race: give
+ * concurrent streams workspaces of their own.  More than 64 rows take one workgroup a row and
+ * use no workspace.
  * Shared definitions:
  *   lse  = bf16(m0 + ln(S 2^-42)), m0 the row's largest logit and S = sum floor(e^(x - m0) 2^42);
  *   lp   = bf16(x - lse) (logprobs_from_logits, Q36/sampler.py:295-297).
@@ -360,6 +363,21 @@ int jit_embed_q4(const int32_t *ids, int B, const uint32_t *weight, const uint16
 
 /* lp [B, V] bf16 = the rows' log-probabilities as defined above. */
 int jit_logprobs_rows(const uint16_t *logits, int B, int V, uint16_t *lp, void *stream);
+
+/* Bytes of the workspace the _ws sampling entry points take (the split launches' partials). */
+long long jit_sampler_workspace_bytes(void);
+
+/* jit_logprobs_rows, jit_argmax_rows and jit_sample_rows with a caller's workspace of at least
+ * jit_sampler_workspace_bytes() bytes (JIT_EINVAL if smaller or not 16-byte aligned; NULL takes the
+ * static buffer): the same kernels and the same results, for callers that run samplers on several
+ * streams at once.  No counterpart in the reference, whose MLX ops allocate per call. */
+int jit_logprobs_rows_ws(const uint16_t *logits, int B, int V, uint16_t *lp, void *workspace,
+                         long long workspace_bytes, void *stream);
+int jit_argmax_rows_ws(const uint16_t *logits, int B, int V, int32_t *out, void *workspace,
+                       long long workspace_bytes, void *stream);
+int jit_sample_rows_ws(const uint16_t *logits, int B, int V, double temperature, double top_p, int top_k,
+                       const float *u, int32_t *tokens, void *workspace, long long workspace_bytes,
+                       void *stream);
 
 /* Greedy choice: out[b] = the first index of the largest lp of row b (Sampler.__call__ with
  * temperature 0: mx.argmax of the log-probabilities, Q36/sampler.py:371-374).  The bf16

@@ -60,10 +60,15 @@ _SIGNATURES = {
     "jit_argmax_rows": [_P, _I, _I, _P, _P],
     "jit_sample_rows": [_P, _I, _I, ctypes.c_double, ctypes.c_double, _I, _P, _P, _P],
     "jit_threefry_uniform": [_P, _I, _P, _P],
+    "jit_sampler_workspace_bytes": [],
+    "jit_logprobs_rows_ws": [_P, _I, _I, _P, _P, ctypes.c_int64, _P],
+    "jit_argmax_rows_ws": [_P, _I, _I, _P, _P, ctypes.c_int64, _P],
+    "jit_sample_rows_ws": [_P, _I, _I, ctypes.c_double, ctypes.c_double, _I, _P, _P, _P, ctypes.c_int64, _P],
     "jit_kv_copy_pages": [_P, _I, _I, _P, _P, _I, _P],
 }
 _RESTYPES = {"jit_last_error": ctypes.c_char_p, "jit_attn_workspace_bytes": ctypes.c_int64,
-             "jit_q4_packed_bytes": ctypes.c_int64, "jit_moe_pack_workspace_bytes": ctypes.c_int64}
+             "jit_q4_packed_bytes": ctypes.c_int64, "jit_moe_pack_workspace_bytes": ctypes.c_int64,
+             "jit_sampler_workspace_bytes": ctypes.c_int64}
 
 _lib = None
 

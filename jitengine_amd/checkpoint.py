@@ -35,6 +35,12 @@ class CheckpointError(ValueError):
     """The checkpoint is not one this build can serve (the message says why)."""
 
 
+# The reference config's RoPE defaults, used when config.json names neither key
+# (Qwen3_5MoeConfig.rope_theta / partial_rotary_factor, Q36/model/config.py:22-23).
+REF_ROPE_THETA = 1e7
+REF_PARTIAL_ROTARY = 0.25
+
+
 @dataclass(frozen=True)
 class CheckpointConfig:
     model: MoEConfig
@@ -98,12 +104,15 @@ def read_config(model_path: str) -> CheckpointConfig:
     if int(t.get("shared_expert_intermediate_size", 0) or 0):
         raise CheckpointError("shared experts are not served")
     # RoPE as the reference reads it (Q36/model/config.py:91-95): rope_parameters first, then the
-    # top-level keys; the kernels rotate the whole head with plain frequencies only
+    # top-level keys, then the reference config's defaults (rope_theta 1e7, partial_rotary_factor
+    # 0.25; Q36/model/config.py:22-23) -- so a config.json that names neither key means a quarter-head
+    # rotation at 1e7, which the kernels do not serve.  They rotate the whole head with plain
+    # frequencies only.
     rp = t.get("rope_parameters") or {}
     if not isinstance(rp, dict):
         raise CheckpointError("rope_parameters is not an object")
-    theta = float(rp.get("rope_theta", t.get("rope_theta", 1e6)))
-    prf = float(rp.get("partial_rotary_factor", t.get("partial_rotary_factor", 1.0)))
+    theta = float(rp.get("rope_theta", t.get("rope_theta", REF_ROPE_THETA)))
+    prf = float(rp.get("partial_rotary_factor", t.get("partial_rotary_factor", REF_PARTIAL_ROTARY)))
     if prf != 1.0:
         raise CheckpointError(f"partial_rotary_factor {prf}: the kernels rotate the whole head (1.0)")
     scaling = t.get("rope_scaling") or rp.get("rope_scaling")

@@ -24,6 +24,7 @@
 // tie group at the top-k / top-p cut needs the vocabulary order: its members' ranks come from a
 // counting pass.
 #include <cstring>
+#include <mutex>
 
 #include "common.hpp"
 #include "fmath.hpp"
@@ -43,6 +44,8 @@ constexpr int kMaxSteps = (kMaxV / (kWaves * 8) * 8 + kStep - 1) / kStep;  // st
 
 enum Mode { kLogprobs = 0, kGreedy = 1, kSample = 2 };
 
+struct SplitScratch;  // the split launches' partials (below)
+
 struct SampleArgs {
   const uint16_t *logits;
   int V;
@@ -53,6 +56,7 @@ struct SampleArgs {
   uint16_t *lp;
   int ns;    // > 0: the row's max and integer sum come as ns slice partials from the split launches
   int hist;  // (ns > 0) the row's histogram comes from split_hist_kernel
+  SplitScratch *sp;  // the partials of the split launches (a caller's workspace or the library's array)
 };
 
 // ascending-order key of a log-probability (a bf16 value <= 0): 0x7fff - magnitude, so that
@@ -247,6 +251,9 @@ struct SplitScratch {
   SplitCut cut[kSplitRows];
   uint32_t hist[kSplitRows][kKeys];  // draws with a cut: the row's histogram of lp keys
 };
+// The library's own partials, for the entry points without a workspace: every device holds its copy
+// until the process ends.  On the host `g_split` names a stand-in, never device memory: host code
+// only passes the per-device address hipGetSymbolAddress returns (split_scratch_of_current_device).
 __device__ __align__(16) SplitScratch g_split;
 
 template <int kMode, bool kVec>
@@ -261,8 +268,8 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
   float m0 = -INFINITY;
   uint64_t S = 0;
   if (a.ns > 0) {
-    m0 = wg_max(t < a.ns ? g_split.max[b][t] : -INFINITY, sh);
-    S = wg_sum(t < a.ns ? g_split.sum[b][t] : 0ull, sh);
+    m0 = wg_max(t < a.ns ? a.sp->max[b][t] : -INFINITY, sh);
+    S = wg_sum(t < a.ns ? a.sp->sum[b][t] : 0ull, sh);
   } else {
     for_each<kVec>(row, V, [&](int, float x) { m0 = fmaxf(m0, x); });
     m0 = wg_max(m0, sh);
@@ -326,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
       constexpr int kCopy = kKeys / 4 / kThreads;
       uint4 q[kCopy];
 #pragma unroll
-      for (int i = 0; i < kCopy; i++) q[i] = ((const uint4 *)g_split.hist[b])[t + i * kThreads];
+      for (int i = 0; i < kCopy; i++) q[i] = ((const uint4 *)a.sp->hist[b])[t + i * kThreads];
 #pragma unroll
       for (int i = 0; i < kCopy; i++) {
         uint32_t *d = hist + hslot(4 * (t + i * kThreads));  // (4 j .. 4 j + 3 lie in one run of 32)
@@ -405,7 +412,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
       const int i = first_max();
       if (t == 0) {
         a.tok[b] = i;
-        if (a.ns > 0) g_split.cut[b] = SplitCut{0, 0, 0, 0, 1, 0.0f, 0.0f};
+        if (a.ns > 0) a.sp->cut[b] = SplitCut{0, 0, 0, 0, 1, 0.0f, 0.0f};
       }
       return;
     }
@@ -440,7 +447,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const SampleArgs 
     const bool partial = r_lo > 0 || r_hi < (int)hist[hslot(key_t)];
     const float m = bf16r(lpmax * a.inv_t);
     if (a.ns > 0) {  // the ranks, weights and the draw run over the row's slices
-      if (t == 0) g_split.cut[b] = SplitCut{key_t, r_lo, r_hi, (int)partial, 0, lse, m};
+      if (t == 0) a.sp->cut[b] = SplitCut{key_t, r_lo, r_hi, (int)partial, 0, lse, m};
       return;
     }
 
@@ -563,6 +570,7 @@ struct SplitArgs {
   uint16_t *lp;
   int hist;  // draws with a cut: split_sum_kernel clears the row's histogram, split_hist_kernel fills it
   int hg;    // slices a split_hist_kernel workgroup counts
+  SplitScratch *sp;
 };
 
 template <bool kVec, typename F>
@@ -615,8 +623,8 @@ __device__ __forceinline__ int split_min(int v, int *sh) {
 }
 
 // the row max from the slice maxima (thread t < ns reads slice t's)
-__device__ __forceinline__ float split_row_max(int b, int ns, float *sh) {
-  return split_max((int)threadIdx.x < ns ? g_split.max[b][threadIdx.x] : -INFINITY, sh);
+__device__ __forceinline__ float split_row_max(const SplitScratch *sp, int b, int ns, float *sh) {
+  return split_max((int)threadIdx.x < ns ? sp->max[b][threadIdx.x] : -INFINITY, sh);
 }
 
 template <bool kVec>
@@ -628,7 +636,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_max_kernel(const SplitArg
   float m = -INFINITY;
   slice_each<kVec>(row, lo, hi, [&](int, float x) { m = fmaxf(m, x); });
   m = split_max(m, sh);
-  if (threadIdx.x == 0) g_split.max[b][s] = m;
+  if (threadIdx.x == 0) a.sp->max[b][s] = m;
 }
 
 template <bool kVec>
@@ -638,13 +646,13 @@ __global__ __launch_bounds__(kSplitThreads) void split_sum_kernel(const SplitArg
   const int s = blockIdx.x, b = blockIdx.y;
   const uint16_t *row = a.logits + (long long)b * a.V;
   const int lo = s * a.len, hi = min(a.V, lo + a.len);
-  const float m0 = split_row_max(b, a.ns, shf);
+  const float m0 = split_row_max(a.sp, b, a.ns, shf);
   uint64_t S = 0;
   slice_each<kVec>(row, lo, hi, [&](int, float x) { S += fix42(exp_neg(x - m0)); });
   S = split_sum(S, shq);
-  if (threadIdx.x == 0) g_split.sum[b][s] = S;
+  if (threadIdx.x == 0) a.sp->sum[b][s] = S;
   if (a.hist) {  // the row's slices clear its histogram for split_hist_kernel
-    uint4 *h = (uint4 *)g_split.hist[b];
+    uint4 *h = (uint4 *)a.sp->hist[b];
     for (int i = s * kSplitThreads + threadIdx.x; i < kKeys / 4; i += a.ns * kSplitThreads)
       h[i] = make_uint4(0u, 0u, 0u, 0u);
   }
@@ -663,15 +671,15 @@ __global__ __launch_bounds__(kSplitThreads) void split_hist_kernel(const SplitAr
   const uint16_t *row = a.logits + (long long)b * a.V;
   const int lo = s * a.hg * a.len, hi = min(a.V, lo + a.hg * a.len);
   for (int i = t; i < kKeys / 4; i += kSplitThreads) ((uint4 *)hist)[i] = make_uint4(0u, 0u, 0u, 0u);
-  const float m0 = split_row_max(b, a.ns, shf);
-  const uint64_t S = split_sum(t < a.ns ? g_split.sum[b][t] : 0ull, shq);
+  const float m0 = split_row_max(a.sp, b, a.ns, shf);
+  const uint64_t S = split_sum(t < a.ns ? a.sp->sum[b][t] : 0ull, shq);
   const float lse = bf16r(m0 + log_ge1(fix42_to_f32(S)));
   __syncthreads();
   slice_each<kVec>(row, lo, hi, [&](int, float x) { atomicAdd(&hist[key_of(bf16r(x - lse))], 1u); });
   __syncthreads();
   for (int k = t; k < kKeys; k += kSplitThreads) {
     const uint32_t c = hist[k];
-    if (c) __hip_atomic_fetch_add(&g_split.hist[b][k], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (c) __hip_atomic_fetch_add(&a.sp->hist[b][k], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -683,8 +691,8 @@ __global__ __launch_bounds__(kSplitThreads) void split_final_kernel(const SplitA
   const int s = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const uint16_t *row = a.logits + (long long)b * a.V;
   const int lo = s * a.len, hi = min(a.V, lo + a.len);
-  const float m0 = split_row_max(b, a.ns, shf);
-  const uint64_t S = split_sum(t < a.ns ? g_split.sum[b][t] : 0ull, shq);
+  const float m0 = split_row_max(a.sp, b, a.ns, shf);
+  const uint64_t S = split_sum(t < a.ns ? a.sp->sum[b][t] : 0ull, shq);
   const float lse = bf16r(m0 + log_ge1(fix42_to_f32(S)));
   if constexpr (kMode == kLogprobs) {
     uint16_t *out = a.lp + (long long)b * a.V;
@@ -709,13 +717,14 @@ __global__ __launch_bounds__(kSplitThreads) void split_final_kernel(const SplitA
       if (bf16r(x - lse) == lpmax && i < best) best = i;
     });
     best = split_min(best, shi);
-    if (t == 0) g_split.idx[b][s] = best;
+    if (t == 0) a.sp->idx[b][s] = best;
   }
 }
 
-__global__ __launch_bounds__(64) void split_argmin_kernel(int ns, int V, int32_t *__restrict__ tok) {
+__global__ __launch_bounds__(64) void split_argmin_kernel(const SplitScratch *sp, int ns, int V,
+                                                                    int32_t *__restrict__ tok) {
   const int b = blockIdx.x;
-  int m = (int)threadIdx.x < ns ? g_split.idx[b][threadIdx.x] : V;
+  int m = (int)threadIdx.x < ns ? sp->idx[b][threadIdx.x] : V;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) m = min(m, __shfl_xor(m, o, 64));
   if (threadIdx.x == 0) tok[b] = m < V ? m : 0;  // (a row without a number: 0)
@@ -729,15 +738,16 @@ struct DrawArgs {
   const float *u;
   int32_t *tok;
   int nocut;  // no top-p and no top-k: every value is kept, and no histogram or cut ran
+  SplitScratch *sp;
 };
 
 // The row's cut: sample_rows_kernel's, or without top-p and top-k the one that keeps every value
 // (key_t 0, no partial tie group) with lse and m from the slice partials.
 __device__ __forceinline__ SplitCut split_cut(const DrawArgs &a, int b, float *shf, unsigned long long *shq) {
-  if (!a.nocut) return g_split.cut[b];
+  if (!a.nocut) return a.sp->cut[b];
   const int t = threadIdx.x;
-  const float m0 = split_max(t < a.ns ? g_split.max[b][t] : -INFINITY, shf);
-  const uint64_t S = split_sum(t < a.ns ? g_split.sum[b][t] : 0ull, shq);
+  const float m0 = split_max(t < a.ns ? a.sp->max[b][t] : -INFINITY, shf);
+  const uint64_t S = split_sum(t < a.ns ? a.sp->sum[b][t] : 0ull, shq);
   const float lse = bf16r(m0 + log_ge1(fix42_to_f32(S)));
   return SplitCut{0, 0, 0, 0, 0, lse, bf16r(bf16r(m0 - lse) * a.inv_t)};
 }
@@ -764,14 +774,14 @@ template <bool kVec>
 __global__ __launch_bounds__(kSplitThreads) void split_ties_kernel(const DrawArgs a) {
   __shared__ unsigned long long sh[kSplitWaves];
   const int s = blockIdx.x, b = blockIdx.y;
-  const SplitCut c = g_split.cut[b];
+  const SplitCut c = a.sp->cut[b];
   if (c.done || !c.partial) return;
   const uint16_t *row = a.logits + (long long)b * a.V;
   const int lo = s * a.len, hi = min(a.V, lo + a.len);
   unsigned long long n = 0;
   slice_each<kVec>(row, lo, hi, [&](int, float x) { n += key_of(bf16r(x - c.lse)) == c.key_t; });
   n = split_sum(n, sh);
-  if (threadIdx.x == 0) g_split.idx[b][s] = (int)n;
+  if (threadIdx.x == 0) a.sp->idx[b][s] = (int)n;
 }
 
 // The weights of one 2048-value step of a slice from i0s (thread t: the 8 values from i0s + 8 t),
@@ -806,10 +816,11 @@ __device__ __forceinline__ uint32_t split_step_weights(const uint16_t *row, int 
 }
 
 // the members of key_t in the slices before s (partial cuts only)
-__device__ __forceinline__ uint32_t split_tie_base(int b, int s, const SplitCut &c, unsigned long long *sh) {
+__device__ __forceinline__ uint32_t split_tie_base(const SplitScratch *sp, int b, int s, const SplitCut &c,
+                                                   unsigned long long *sh) {
   if (!c.partial) return 0u;
   const int t = threadIdx.x;
-  return (uint32_t)split_sum(t < s ? (unsigned long long)g_split.idx[b][t] : 0ull, sh);
+  return (uint32_t)split_sum(t < s ? (unsigned long long)sp->idx[b][t] : 0ull, sh);
 }
 
 // the slice's total weight
@@ -823,7 +834,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_weights_kernel(const Draw
   if (c.done) return;
   const uint16_t *row = a.logits + (long long)b * a.V;
   const int lo = s * a.len, hi = min(a.V, lo + a.len);
-  uint32_t rank = split_tie_base(b, s, c, shq);
+  uint32_t rank = split_tie_base(a.sp, b, s, c, shq);
   unsigned long long tw = 0;
   for (int i0s = lo; i0s < hi; i0s += 8 * kSplitThreads) {
     uint64_t W[8];
@@ -833,7 +844,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_weights_kernel(const Draw
     for (int j = 0; j < 8; j++) tw += W[j];
   }
   tw = split_sum(tw, shq);
-  if (threadIdx.x == 0) g_split.wsum[b][s] = tw;
+  if (threadIdx.x == 0) a.sp->wsum[b][s] = tw;
 }
 
 // The draw: U = floor(u * total weight); the token is the number of i with C_i = sum_{j<i} W_j
@@ -848,7 +859,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_draw_kernel(const DrawArg
   const int b = blockIdx.x, t = threadIdx.x;
   const SplitCut c = split_cut(a, b, shf, shq);
   if (c.done) return;
-  const unsigned long long T = t < a.ns ? g_split.wsum[b][t] : 0ull;
+  const unsigned long long T = t < a.ns ? a.sp->wsum[b][t] : 0ull;
   unsigned long long total;
   const unsigned long long P = split_excl(T, shq, total);
   float u = a.u[b];
@@ -866,7 +877,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_draw_kernel(const DrawArg
   }
   const uint16_t *row = a.logits + (long long)b * a.V;
   const int lo = s * a.len, hi = min(a.V, lo + a.len);
-  uint32_t rank = split_tie_base(b, s, c, shq);
+  uint32_t rank = split_tie_base(a.sp, b, s, c, shq);
   unsigned long long run = pick[1], cnt = 0;
   for (int i0s = lo; i0s < hi; i0s += 8 * kSplitThreads) {
     uint64_t W[8];
@@ -898,19 +909,19 @@ int launch_split_vec(const SplitArgs &a, int B, hipStream_t st) {
   if constexpr (kMode == kSample)
     if (a.hist) split_hist_kernel<kVec><<<dim3((a.ns + a.hg - 1) / a.hg, B), kSplitThreads, 0, st>>>(a);
   if constexpr (kMode != kSample) split_final_kernel<kMode, kVec><<<grid, kSplitThreads, 0, st>>>(a);
-  if constexpr (kMode == kGreedy) split_argmin_kernel<<<B, 64, 0, st>>>(a.ns, a.V, a.tok);
+  if constexpr (kMode == kGreedy) split_argmin_kernel<<<B, 64, 0, st>>>(a.sp, a.ns, a.V, a.tok);
   return jit::check_launch(kMode == kGreedy ? "jit_argmax_rows" : kMode == kLogprobs ? "jit_logprobs_rows"
                                                                                        : "jit_sample_rows");
 }
 
 // The slices of a row: about 1024 workgroups in all, at most kSplitMax a row, at least kSplitMin
 // values each, whole 8-value steps.
-SplitArgs split_args(const uint16_t *logits, int B, int V, int32_t *tok, uint16_t *lp) {
+SplitArgs split_args(const uint16_t *logits, int B, int V, int32_t *tok, uint16_t *lp, SplitScratch *sp) {
   int ns = min(kSplitMax, max(1, 1024 / B));
   ns = min(ns, (V + kSplitMin - 1) / kSplitMin);
   const int len = ((V + ns - 1) / ns + 7) / 8 * 8;
   ns = (V + len - 1) / len;
-  return SplitArgs{logits, V, ns, len, tok, lp};
+  return SplitArgs{logits, V, ns, len, tok, lp, 0, 0, sp};
 }
 
 template <int kMode>
@@ -948,32 +959,49 @@ float host_bf16(float f) {
   return r;
 }
 
+// The current device's address of g_split (looked up on the first call on that device).
+constexpr int kMaxDevices = 64;
+std::mutex g_split_mu;
+SplitScratch *g_split_dev[kMaxDevices];
+
+int split_scratch_of_current_device(SplitScratch **sp, const char *what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return jit::fail(JIT_ELAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return jit::fail(JIT_EUNSUPPORTED, "%s: device %d is past the %d devices the scratch table covers", what, dev,
+                     kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_split_mu);
+  if (!g_split_dev[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_split));
+    if (e != hipSuccess || !p)
+      return jit::fail(JIT_ELAUNCH, "%s: hipGetSymbolAddress(g_split) failed on device %d: %s", what, dev,
+                       hipGetErrorString(e));
+    g_split_dev[dev] = (SplitScratch *)p;
+  }
+  *sp = g_split_dev[dev];
+  return JIT_OK;
+}
+
 }  // namespace
 
-extern "C" int jit_logprobs_rows(const uint16_t *logits, int B, int V, uint16_t *lp, void *stream) {
-  if (int rc = check_rows("logprobs_rows", logits, B, V, lp)) return rc;
-  if (B == 0) return JIT_OK;
-  if (B <= kSplitRows) return launch_split<kLogprobs>(split_args(logits, B, V, nullptr, lp), B, stream);
+static int logprobs_rows(const uint16_t *logits, int B, int V, uint16_t *lp, SplitScratch *sp, void *stream) {
+  if (B <= kSplitRows) return launch_split<kLogprobs>(split_args(logits, B, V, nullptr, lp, sp), B, stream);
   SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, nullptr, lp};
   return launch<kLogprobs>(a, B, stream);
 }
 
-extern "C" int jit_argmax_rows(const uint16_t *logits, int B, int V, int32_t *out, void *stream) {
-  if (int rc = check_rows("argmax_rows", logits, B, V, out)) return rc;
-  if (B == 0) return JIT_OK;
-  if (B <= kSplitRows) return launch_split<kGreedy>(split_args(logits, B, V, out, nullptr), B, stream);
+static int argmax_rows(const uint16_t *logits, int B, int V, int32_t *out, SplitScratch *sp, void *stream) {
+  if (B <= kSplitRows) return launch_split<kGreedy>(split_args(logits, B, V, out, nullptr, sp), B, stream);
   SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, out, nullptr};
   return launch<kGreedy>(a, B, stream);
 }
 
-extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temperature, double top_p, int top_k,
-                               const float *u, int32_t *tokens, void *stream) {
-  if (int rc = check_rows("sample_rows", logits, B, V, tokens)) return rc;
-  if (!(temperature == temperature) || !(top_p == top_p) || top_k < 0)
-    return jit::fail(JIT_EINVAL, "sample_rows: bad settings T=%g top_p=%g top_k=%d", temperature, top_p, top_k);
-  if (B == 0) return JIT_OK;
+static int sample_rows(const uint16_t *logits, int B, int V, double temperature, double top_p, int top_k,
+                       const float *u, int32_t *tokens, SplitScratch *sp, void *stream) {
   if (temperature <= 0.0) {
-    if (B <= kSplitRows) return launch_split<kGreedy>(split_args(logits, B, V, tokens, nullptr), B, stream);
+    if (B <= kSplitRows) return launch_split<kGreedy>(split_args(logits, B, V, tokens, nullptr, sp), B, stream);
     SampleArgs a{logits, V, 0.0f, 0.0f, 0, nullptr, tokens, nullptr};
     return launch<kGreedy>(a, B, stream);
   }
@@ -985,13 +1013,13 @@ extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temp
   if (!(inv_t > 0.0f) || !(inv_t < INFINITY))
     return jit::fail(JIT_EUNSUPPORTED, "sample_rows: 1 / T = %g is not a finite positive bf16", 1.0 / temperature);
   const int k = top_k >= V ? 0 : top_k;
-  SampleArgs a{logits, V, inv_t, thr, k, u, tokens, nullptr};
+  SampleArgs a{logits, V, inv_t, thr, k, u, tokens, nullptr, 0, 0, sp};
   if (B > kSplitRows) return launch<kSample>(a, B, stream);
   // the row's log-sum-exp over slices, the histogram and the cut in one workgroup a row, then the
   // ranks, weights and the draw over slices again
   // (without top-p and top-k every value is kept: no histogram, no cut)
   const int nocut = thr == 0.0f && k == 0;
-  SplitArgs sa = split_args(logits, B, V, nullptr, nullptr);
+  SplitArgs sa = split_args(logits, B, V, nullptr, nullptr, sp);
   // the histogram over runs of slices, about 256 workgroups in all (each clears and scans 128 KB
   // of LDS, so more of them with fewer values each cost more than they save)
   sa.hist = !nocut;
@@ -1001,7 +1029,7 @@ extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temp
   a.hist = sa.hist;
   if (!nocut)
     if (int rc = launch<kSample>(a, B, stream)) return rc;
-  const DrawArgs da{logits, V, sa.ns, sa.len, inv_t, u, tokens, nocut};
+  const DrawArgs da{logits, V, sa.ns, sa.len, inv_t, u, tokens, nocut, sp};
   const dim3 grid(sa.ns, B);
   const hipStream_t st = (hipStream_t)stream;
   if ((V & 7) == 0 && ((uintptr_t)logits & 15) == 0) {
@@ -1014,6 +1042,70 @@ extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temp
     split_draw_kernel<false><<<B, kSplitThreads, 0, st>>>(da);
   }
   return jit::check_launch("jit_sample_rows");
+}
+
+// The split launches' partials: the library's own array (the entry points without a workspace) or a
+// caller's workspace of jit_sampler_workspace_bytes() bytes.
+static int scratch_arg(void *workspace, long long bytes, const char *what, SplitScratch **sp) {
+  if (workspace) {
+    if (bytes < (long long)sizeof(SplitScratch) || ((uintptr_t)workspace & 15))
+      return jit::fail(JIT_EINVAL, "%s: workspace of %lld bytes at %p; %lld bytes, 16-byte aligned, needed", what,
+                       bytes, workspace, (long long)sizeof(SplitScratch));
+    *sp = (SplitScratch *)workspace;
+    return JIT_OK;
+  }
+  return split_scratch_of_current_device(sp, what);
+}
+
+extern "C" long long jit_sampler_workspace_bytes(void) { return (long long)sizeof(SplitScratch); }
+
+extern "C" int jit_logprobs_rows_ws(const uint16_t *logits, int B, int V, uint16_t *lp, void *workspace,
+                                    long long workspace_bytes, void *stream) {
+  if (int rc = check_rows("logprobs_rows", logits, B, V, lp)) return rc;
+  if (B == 0) return JIT_OK;
+  SplitScratch *sp = nullptr;
+  if (int rc = scratch_arg(workspace, workspace_bytes, "logprobs_rows", &sp)) return rc;
+  return logprobs_rows(logits, B, V, lp, sp, stream);
+}
+
+extern "C" int jit_logprobs_rows(const uint16_t *logits, int B, int V, uint16_t *lp, void *stream) {
+  return jit_logprobs_rows_ws(logits, B, V, lp, nullptr, 0, stream);
+}
+
+extern "C" int jit_argmax_rows_ws(const uint16_t *logits, int B, int V, int32_t *out, void *workspace,
+                                  long long workspace_bytes, void *stream) {
+  if (int rc = check_rows("argmax_rows", logits, B, V, out)) return rc;
+  if (B == 0) return JIT_OK;
+  SplitScratch *sp = nullptr;
+  if (int rc = scratch_arg(workspace, workspace_bytes, "argmax_rows", &sp)) return rc;
+  return argmax_rows(logits, B, V, out, sp, stream);
+}
+
+extern "C" int jit_argmax_rows(const uint16_t *logits, int B, int V, int32_t *out, void *stream) {
+  return jit_argmax_rows_ws(logits, B, V, out, nullptr, 0, stream);
+}
+
+extern "C" int jit_sample_rows_ws(const uint16_t *logits, int B, int V, double temperature, double top_p, int top_k,
+                                  const float *u, int32_t *tokens, void *workspace, long long workspace_bytes,
+                                  void *stream) {
+  if (int rc = check_rows("sample_rows", logits, B, V, tokens)) return rc;
+  if (!(temperature == temperature) || !(top_p == top_p) || top_k < 0)
+    return jit::fail(JIT_EINVAL, "sample_rows: bad settings T=%g top_p=%g top_k=%d", temperature, top_p, top_k);
+  if (B == 0) return JIT_OK;
+  if (temperature > 0.0) {  // (the draw's own contract, before the workspace is looked up)
+    if (!u) return jit::fail(JIT_EINVAL, "sample_rows: null uniforms");
+    const float inv_t = host_bf16((float)(1.0 / temperature));
+    if (!(inv_t > 0.0f) || !(inv_t < INFINITY))
+      return jit::fail(JIT_EUNSUPPORTED, "sample_rows: 1 / T = %g is not a finite positive bf16", 1.0 / temperature);
+  }
+  SplitScratch *sp = nullptr;
+  if (int rc = scratch_arg(workspace, workspace_bytes, "sample_rows", &sp)) return rc;
+  return sample_rows(logits, B, V, temperature, top_p, top_k, u, tokens, sp, stream);
+}
+
+extern "C" int jit_sample_rows(const uint16_t *logits, int B, int V, double temperature, double top_p, int top_k,
+                               const float *u, int32_t *tokens, void *stream) {
+  return jit_sample_rows_ws(logits, B, V, temperature, top_p, top_k, u, tokens, nullptr, 0, stream);
 }
 
 extern "C" int jit_threefry_uniform(const uint32_t *keys, int B, float *u, void *stream) {

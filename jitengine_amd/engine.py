@@ -37,6 +37,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
+from . import ops
 from .kvpool import KVPool, PoolExhausted, PrefixStore, pages_for
 from .ops import PAGE
 from .model import CausalLM, make_mixed_state, make_step_state
@@ -178,7 +179,7 @@ class Engine:
         for i, k in enumerate(keys):
             groups.setdefault(k, []).append(i)
         for members in groups.values():
-            idx = torch.tensor(members, dtype=torch.int64, device=logits.device)
+            idx = ops.upload(members, logits.device, torch.int64)
             sel = logits if len(members) == len(rows) else logits.index_select(0, idx).contiguous()
             tok = sample_rows(sel, [samplers[i] for i in members], [steps[i] for i in members])
             out.index_copy_(0, idx, tok)
@@ -190,7 +191,7 @@ class Engine:
         read)."""
         lm = self.lm
         st = make_step_state(lm.cfg, pos, self.pool.page_table([r.rid for r in rows]))
-        ids_t = ids if torch.is_tensor(ids) else torch.tensor(ids, dtype=torch.int32, device=self.device)
+        ids_t = ids if torch.is_tensor(ids) else ops.upload(ids, self.device, torch.int32)
         h = lm.model.decode_step(lm.embed_tokens(ids_t), self.pool.pools, st)
         return self._draw(rows, h, [len(r.tokens) + ahead for r in rows])
 
@@ -247,14 +248,21 @@ class Engine:
             return self._pump()
         self._admit()
         decode = [r for r in self.rows if r.state == "decode"]
+        pending = [r for r in self.rows if r.state == "prefill"]
+        if pending:
+            # the oldest pending prompt's next chunk always runs: when the decode rows leave it no
+            # room, the step serves only as many of them as fit beside it (the others decode in the
+            # next step; a row's tokens do not depend on the step it runs in), so a prompt's first
+            # token never waits on the decode load
+            n0 = self._chunk_len(pending[0])
+            if len(decode) + n0 > self.max_step_tokens:
+                decode = decode[:self.max_step_tokens - n0]
         budget = self.max_step_tokens - len(decode)
         chunks = []
-        for r in self.rows:
-            if r.state != "prefill":
-                continue
+        for r in pending:
             # the chunk up to the next multiple of prefill_chunk (or the prompt's end); a chunk that
             # does not fit the step's budget waits (strict FIFO), it is never cut short
-            n = min(self.prefill_chunk - r.done_prompt % self.prefill_chunk, len(r.prompt) - r.done_prompt)
+            n = self._chunk_len(r)
             if n > budget:
                 break
             chunks.append((r, r.done_prompt, n))
@@ -282,6 +290,11 @@ class Engine:
         self.steps += 1
         self._consume(drawn)
         return drawn
+
+    def _chunk_len(self, r: Request) -> int:
+        """Rows of r's next prompt chunk: up to the next multiple of prefill_chunk (an absolute grid)
+        or the prompt's end."""
+        return min(self.prefill_chunk - r.done_prompt % self.prefill_chunk, len(r.prompt) - r.done_prompt)
 
     def _prefill_chunk(self, r: Request, c: int, n: int):
         """Prompt positions c .. c + n - 1 of request r as a forward of their own (the chunked-prefill

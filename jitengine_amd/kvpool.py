@@ -150,7 +150,7 @@ class KVPool:
 
     def page_table(self, seq_ids, width: int | None = None) -> torch.Tensor:
         """int32 [B, width] page ids of the given sequences (unused entries 0, never read)."""
-        return torch.from_numpy(self.page_table_host(seq_ids, width)).to(self.device)
+        return ops.upload(self.page_table_host(seq_ids, width), self.device)
 
     def page_table_host(self, seq_ids, width: int | None = None) -> np.ndarray:
         rows = [self.pages.get(s, []) for s in seq_ids]

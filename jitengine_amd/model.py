@@ -91,7 +91,7 @@ def make_step_state(cfg: MoEConfig, pos_host, page_table: torch.Tensor) -> StepS
     dev = page_table.device
     plan = ops.attn_plan(pos_host + 1, dev)
     ws = torch.empty(max(ops.attn_workspace_bytes(plan.total, cfg.heads), 4), dtype=torch.uint8, device=dev)
-    return StepState(torch.from_numpy(pos_host).to(dev), page_table, plan, ws)
+    return StepState(ops.upload(pos_host, dev), page_table, plan, ws)
 
 
 @dataclass

@@ -29,6 +29,20 @@ def _p(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def upload(a, device, dtype=None) -> torch.Tensor:
+    """A host array (numpy or list) as a device tensor without a host wait: staged in pinned host
+    memory and copied asynchronously on the current stream (torch's caching host allocator keeps the
+    staging block until the copy has run), so a step's small inputs can be queued while earlier steps
+    still run.  A pageable copy would make the host wait for the stream."""
+    t = torch.from_numpy(np.ascontiguousarray(a)) if isinstance(a, np.ndarray) else torch.tensor(a, dtype=dtype)
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        return t.to(dev)
+    return t.pin_memory().to(dev, non_blocking=True)
+
+
 def _need(t: torch.Tensor, dtype, name: str) -> None:
     if t.dtype != dtype:
         raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
@@ -484,7 +498,7 @@ def attn_plan(lens_host, device) -> AttnPlan:
         ),
         "attn_plan",
     )
-    dev = torch.from_numpy(np.concatenate([ln, cs, seq])).to(device)
+    dev = upload(np.concatenate([ln, cs, seq]), device)
     return AttnPlan(dev[:B], dev[B:2 * B + 1], dev[2 * B + 1:], int(total), ln)
 
 
@@ -630,28 +644,44 @@ def embed_q4(ids: torch.Tensor, table: QLinear) -> torch.Tensor:
     return out
 
 
-def logprobs_rows(logits: torch.Tensor) -> torch.Tensor:
+def sampler_workspace(device) -> torch.Tensor:
+    """A workspace for the sampling ops (jit_sampler_workspace_bytes bytes): a stream that samples
+    while others do passes one of its own; without one the library's static buffer serves, and calls
+    on several streams at once would race on it."""
+    return torch.empty(int(_lib.lib().jit_sampler_workspace_bytes()), dtype=torch.uint8, device=device)
+
+
+def _ws_args(workspace):
+    if workspace is None:
+        return None, 0
+    _need(workspace, torch.uint8, "workspace")
+    return _p(workspace), workspace.numel()
+
+
+def logprobs_rows(logits: torch.Tensor, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """bf16 [B, V]: lp = bf16(x - lse) per row with lse = bf16(m0 + ln(S 2^-42)), S the exact
     integer sum of floor(e^(x - m0) 2^42) (logprobs_from_logits, Q36/sampler.py:295-297)."""
     _need(logits, torch.bfloat16, "logits")
     B, V = logits.shape
     out = torch.empty_like(logits)
-    _lib.check(_lib.lib().jit_logprobs_rows(_p(logits), B, V, _p(out), _stream()), "logprobs_rows")
+    ws, nb = _ws_args(workspace)
+    _lib.check(_lib.lib().jit_logprobs_rows_ws(_p(logits), B, V, _p(out), ws, nb, _stream()), "logprobs_rows")
     return out
 
 
-def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
+def argmax_rows(logits: torch.Tensor, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """int32 [B]: the first index of each row's largest log-probability (the greedy draw,
     Q36/sampler.py:371-374)."""
     _need(logits, torch.bfloat16, "logits")
     B, V = logits.shape
     out = torch.empty(B, dtype=torch.int32, device=logits.device)
-    _lib.check(_lib.lib().jit_argmax_rows(_p(logits), B, V, _p(out), _stream()), "argmax_rows")
+    ws, nb = _ws_args(workspace)
+    _lib.check(_lib.lib().jit_argmax_rows_ws(_p(logits), B, V, _p(out), ws, nb, _stream()), "argmax_rows")
     return out
 
 
 def sample_rows(logits: torch.Tensor, temperature: float, top_p: float, top_k: int,
-                u: torch.Tensor | None) -> torch.Tensor:
+                u: torch.Tensor | None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """int32 [B]: one draw per row of bf16 logits [B, V] under shared settings, given fp32
     uniforms u [B] (Sampler._sample_exact_full / sample_rows, Q36/sampler.py:451-476, 486-543;
     the definitions are jit_sample_rows'); temperature <= 0 is the greedy draw."""
@@ -664,8 +694,10 @@ def sample_rows(logits: torch.Tensor, temperature: float, top_p: float, top_k: i
         if u.shape != (B,):
             raise ValueError(f"u must be [{B}], got {tuple(u.shape)}")
     out = torch.empty(B, dtype=torch.int32, device=logits.device)
-    _lib.check(_lib.lib().jit_sample_rows(_p(logits), B, V, float(temperature), float(top_p), int(top_k),
-                                          _p(u) if u is not None else None, _p(out), _stream()), "sample_rows")
+    ws, nb = _ws_args(workspace)
+    _lib.check(_lib.lib().jit_sample_rows_ws(_p(logits), B, V, float(temperature), float(top_p), int(top_k),
+                                             _p(u) if u is not None else None, _p(out), ws, nb, _stream()),
+               "sample_rows")
     return out
 
 

@@ -111,5 +111,5 @@ def sample_rows(logits: torch.Tensor, samplers: list, steps: list) -> torch.Tens
     if s0.greedy:
         return ops.argmax_rows(logits)
     keys = np.stack([s.key(st) for s, st in zip(samplers, steps)]).view(np.int32)
-    u = ops.threefry_uniform(torch.from_numpy(keys).to(logits.device))
+    u = ops.threefry_uniform(ops.upload(keys, logits.device))
     return ops.sample_rows(logits, s0.temperature, s0.top_p, s0.top_k, u)

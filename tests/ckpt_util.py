@@ -15,8 +15,8 @@ from jitengine_amd.quant import random_quantized
 def config_dict(D=256, H=2, Hkv=1, E=4, k=2, I=64, V=64, L=2, tie=False, **extra):
     c = {"model_type": "qwen3_moe", "hidden_size": D, "num_attention_heads": H, "num_key_value_heads": Hkv,
          "head_dim": 128, "num_experts": E, "num_experts_per_tok": k, "moe_intermediate_size": I,
-         "rope_theta": 1000000.0, "rms_norm_eps": 1e-6, "num_hidden_layers": L, "vocab_size": V,
-         "norm_topk_prob": True, "tie_word_embeddings": tie, "decoder_sparse_step": 1, "mlp_only_layers": [],
+         "rope_theta": 1000000.0, "partial_rotary_factor": 1.0, "rms_norm_eps": 1e-6, "num_hidden_layers": L,
+         "vocab_size": V, "norm_topk_prob": True, "tie_word_embeddings": tie, "decoder_sparse_step": 1, "mlp_only_layers": [],
          "eos_token_id": [V - 1], "quantization": {"group_size": 64, "bits": 4}}
     c.update(extra)
     return c

@@ -5,6 +5,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
+import oracle
 from jitengine_amd.quant import QLinear, random_quantized
 from oracle import bf16_to_f32, f32_to_bf16  # noqa: F401
 
@@ -147,6 +148,19 @@ def assert_attention_parity(got_u16: np.ndarray, exact: np.ndarray, stock_u16: n
                                f"arithmetic's {e_stock[bad[0]]:.3g}")
         out["err_vs_stock"] = float((e_got / np.maximum(e_stock, 1e-300)).max())
     return out
+
+
+def assert_fn_criterion(got_u16, x, w, s, b, f64) -> None:
+    """The reference's criterion for a quantized projection (FN/kernels/selfcheck.py:313-331): the
+    largest error of the result against the float64 product f64 is at most 8x that of the reference's
+    own fp32 arithmetic (oracle.qmv_mlx_f32, rounded to bf16 as the reference returns it) plus 4 fp32
+    ulps of the result's scale."""
+    stock = f32_to_bf16(oracle.qmv_mlx_f32(x, w, s, b))
+    e_got = np.abs(bf16_to_f32(got_u16) - f64).max()
+    e_stock = np.abs(bf16_to_f32(stock) - f64).max()
+    scale = np.abs(f64).max()
+    assert e_stock <= 2.0**-6 * scale
+    assert e_got <= 8 * e_stock + 4 * 2.0**-24 * scale, (e_got, e_stock)
 
 
 def sampler_logits(kind: int, B: int, V: int, seed: int, scale: float = 1.0) -> np.ndarray:

@@ -63,6 +63,13 @@ def test_contract_breaks_return_einval_before_launch():
     assert lib.jit_sample_rows(dummy, 2, 64, 1.0, 0.9, 5, None, dummy, None) == _lib.JIT_EINVAL
     assert lib.jit_sample_rows(dummy, 2, 64, 1e-300, 0.9, 5, dummy, dummy, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_logprobs_rows(None, -1, 64, None, None) == _lib.JIT_EINVAL
+    need = lib.jit_sampler_workspace_bytes()
+    assert need > 64 * 32768 * 4  # the per-row histograms of the split draws, and the partials
+    ws = ctypes.c_void_p(256)
+    assert lib.jit_logprobs_rows_ws(dummy, 2, 64, dummy, ws, need - 1, None) == _lib.JIT_EINVAL
+    assert lib.jit_argmax_rows_ws(dummy, 2, 64, dummy, ctypes.c_void_p(264), need, None) == _lib.JIT_EINVAL
+    assert b"16-byte aligned" in lib.jit_last_error()
+    assert lib.jit_sample_rows_ws(dummy, 2, 64, 1.0, 0.9, 5, dummy, dummy, ws, 16, None) == _lib.JIT_EINVAL
     assert lib.jit_threefry_uniform(None, -1, None, None) == _lib.JIT_EINVAL
     # empty work is a no-op, not an error
     assert lib.jit_router_topk(None, 0, 128, 8, 1, None, None, None, None) == _lib.JIT_OK

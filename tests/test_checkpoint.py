@@ -49,6 +49,28 @@ def test_tied_head_and_layer_limit(tmp_path):
     assert lm.lm_head is lm.embed and len(lm.layers) == 1 and lm.cfg.layers == 1
 
 
+@pytest.mark.parametrize("drop", [("partial_rotary_factor",), ("partial_rotary_factor", "rope_theta")])
+def test_config_without_rope_keys_takes_the_reference_defaults(tmp_path, drop):
+    """A config.json that leaves out the RoPE keys means the reference config's defaults
+    (partial_rotary_factor 0.25, rope_theta 1e7): a quarter-head rotation, rejected, never silently
+    read as a whole-head rotation at 1e6."""
+    cfg = config_dict()
+    for key in drop:
+        del cfg[key]
+    with open(os.path.join(tmp_path, "config.json"), "w") as f:
+        json.dump(cfg, f)
+    with pytest.raises(CheckpointError, match="partial_rotary_factor 0.25"):
+        checkpoint.read_config(str(tmp_path))
+
+
+def test_config_theta_default_is_the_reference_one(tmp_path):
+    cfg = config_dict()
+    del cfg["rope_theta"]
+    with open(os.path.join(tmp_path, "config.json"), "w") as f:
+        json.dump(cfg, f)
+    assert checkpoint.read_config(str(tmp_path)).model.rope_theta == checkpoint.REF_ROPE_THETA == 1e7
+
+
 @pytest.mark.parametrize("change, what", [
     ({"quantization": {"group_size": 64, "bits": 8}}, "bits=8"),
     ({"quantization": {"group_size": 32, "bits": 4}}, "group_size=32"),

@@ -9,7 +9,10 @@ import torch
 import oracle
 from jitengine_amd import ops
 from jitengine_amd.model import DecoderLayer, MoEConfig, Model, make_step_state, random_layer_weights, rope_inv_freq
-from tests.helpers import assert_close_bf16, bf16_tensor, bf16_to_f32, normal_bf16, u16
+from tests.helpers import (
+    assert_attention_parity, assert_close_bf16, assert_fn_criterion, bf16_tensor, bf16_to_f32, f32_to_bf16,
+    normal_bf16, u16,
+)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -91,11 +94,48 @@ def _ctx(lens, cfg, seed):
     return table, pools
 
 
+def _stages_on_gpu_inputs(cfg, lens, table, pool_after, w, dbg, what):
+    """Each stage of the attention and MoE halves against the oracle on the GPU's own inputs to that
+    stage (so a stage's error is not hidden under the drift of the stages before it):
+    * attention: the attention bar (tests.helpers.assert_attention_parity: the reference's 8x-stock
+      criterion, one ulp + 2^-14 of the row, >= 98% correctly rounded) on the GPU's q over the pool
+      the GPU's append left, through the layer's plan, page table and pos + 1 lengths;
+    * router logits: the reference's criterion for quantized projections and >= 95% bit-equal;
+    * gate||up + SwiGLU (h) and down (r): the north-star tolerance (h at 4 ulps, as its SwiGLU
+      may flip with one ulp of g or u) and >= 95% bit-equal, under the GPU's routing;
+    * the closing combine: y = bf16(h + combine(r, scores)) bit for bit."""
+    lens1 = np.asarray(lens, np.int64) + 1
+    q = u16(dbg["q"])
+    _, exact = oracle.paged_decode_attn(q, pool_after, table, lens1, 128 ** -0.5, exact=True)
+    stock, _ = oracle.sdpa_mlx_f32(q, pool_after, table, lens1, 128 ** -0.5)
+    assert_attention_parity(u16(dbg["attn"]), exact, stock, what=f"{what}: attention stage")
+    hn = u16(dbg["hn"])
+    wr, sr, br = _layer_numpy(w)["router"]
+    f64, want_l = oracle.qmm(hn, wr, sr, br)
+    got_l = u16(dbg["logits"])
+    assert_fn_criterion(got_l, hn, wr, sr, br, f64)
+    st = assert_close_bf16(got_l, want_l, what=f"{what}: router logits")
+    assert st["bit_equal"] >= 0.95, (what, "logits", st)
+    gi = dbg["inds"].cpu().numpy().view(np.uint32)
+    opk = oracle.moe_pack(gi, cfg.experts)
+    lw = _layer_numpy(w)
+    want_h = oracle.moe_gate_up(hn, gi, opk, *lw["gate_up"])
+    st = assert_close_bf16(u16(dbg["hh"]), want_h, what=f"{what}: gate_up", ulps=4.0)
+    assert st["bit_equal"] >= 0.95, (what, "gate_up", st)
+    want_r = oracle.moe_down(u16(dbg["hh"]), gi, opk, *lw["down"])
+    st = assert_close_bf16(u16(dbg["r"]), want_r, what=f"{what}: down")
+    assert st["bit_equal"] >= 0.95, (what, "down", st)
+    moe = oracle.moe_combine(u16(dbg["r"]), opk["inv"], u16(dbg["scores"]))
+    want_y = f32_to_bf16(bf16_to_f32(u16(dbg["h"])) + bf16_to_f32(moe))
+    assert np.array_equal(u16(dbg["y"]), want_y), f"{what}: y != bf16(h + combine(r))"
+
+
 def _layer_vs_oracle(cfg, lens, table, pool, x, w, what, max_flips):
     """One layer step on the GPU against oracle.decoder_layer on the same inputs, stage by stage
     (the MoE half under the GPU's routing, which is bit-exact given the logits); rows whose float64
     routing differs are counted.  The layer output composes ~6 bf16 rounding stages (attention,
-    o_proj, residual, experts, combine, residual): up to 4 ulps where that exceeds the absolute 2e-2."""
+    o_proj, residual, experts, combine, residual): up to 4 ulps where that exceeds the absolute 2e-2.
+    Then each stage against the oracle on the GPU's own inputs (_stages_on_gpu_inputs)."""
     layer = DecoderLayer(cfg, w)
     pool_t = bf16_tensor(pool, DEV)
     st = make_step_state(cfg, np.array(lens), _i32(table))
@@ -113,6 +153,7 @@ def _layer_vs_oracle(cfg, lens, table, pool, x, w, what, max_flips):
     flips = int(np.sum(np.any(np.sort(own, -1) != np.sort(gi, -1), -1)))
     assert flips <= max_flips, f"{what}: {flips} rows routed differently from the float64 logits"
     assert_close_bf16(u16(y), ref["y"], what=f"{what}: layer output", ulps=4.0)
+    _stages_on_gpu_inputs(cfg, lens, table, u16(pool_t), w, dbg, what)
     return dbg, ref
 
 
@@ -180,6 +221,7 @@ def test_decoder_layer_parity():
     # combine, residual): up to 4 ulps where that exceeds the absolute 2e-2 (|y| in [2, 4) has
     # an ulp of 1.6e-2)
     assert_close_bf16(u16(y), ref["y"], what="layer output", ulps=4.0)
+    _stages_on_gpu_inputs(cfg, lens, table, u16(pool_t), w, dbg, "12 ragged rows")
 
 
 @pytest.mark.parametrize("B,resid", [(1, True), (32, True), (33, False)])

@@ -17,8 +17,8 @@ from jitengine_amd import ops
 from jitengine_amd.moe import MoEBlock
 from jitengine_amd.quant import QLinear
 from tests.helpers import (
-    assert_attention_parity, assert_close_bf16, bf16_tensor, bf16_to_f32, f32_to_bf16, make_stack, normal_bf16,
-    router_logits, stack_np, tie_gates, u16,
+    assert_attention_parity, assert_close_bf16, assert_fn_criterion, bf16_tensor, bf16_to_f32, f32_to_bf16, make_stack,
+    normal_bf16, router_logits, stack_np, tie_gates, u16,
 )
 
 pytestmark = pytest.mark.gpu
@@ -134,15 +134,6 @@ def test_pack_many_workgroups_equal_one(P, k, E, skew, bad):
 
 
 # ----------------------------------------------------------------------------- projections
-def _fn_criterion(got_u16, x, w, s, b, f64):
-    stock = oracle.f32_to_bf16(oracle.qmv_mlx_f32(x, w, s, b))
-    e_got = np.abs(bf16_to_f32(got_u16) - f64).max()
-    e_stock = np.abs(bf16_to_f32(stock) - f64).max()
-    scale = np.abs(f64).max()
-    assert e_stock <= 2.0**-6 * scale
-    assert e_got <= 8 * e_stock + 4 * 2.0**-24 * scale, (e_got, e_stock)
-
-
 @pytest.mark.parametrize("T", [1, 3, 16, 17, 40])
 @pytest.mark.parametrize("N,K", [(128, 2048), (512, 2048), (256, 4096), (2048, 768 + 256)])
 def test_qmm_parity(T, N, K):
@@ -153,7 +144,7 @@ def test_qmm_parity(T, N, K):
     f64, want = oracle.qmm(x, w, s, b)
     assert_close_bf16(u16(y), want, what="qmm")
     if K % 512 == 0:
-        _fn_criterion(u16(y), x, w, s, b, f64)
+        assert_fn_criterion(u16(y), x, w, s, b, f64)
 
 
 def _moe_inputs(B, E, D, I, seed):

@@ -117,6 +117,35 @@ def test_sample_rows_split_over_slices():
             assert np.array_equal(got, oracle.sample_rows(x, T, p, k, u)), (kind, T, p, k)
 
 
+def test_workspace_variants_equal_the_static_buffer_and_run_on_two_streams():
+    """The _ws entry points (a caller's workspace) give the static buffer's results, and two streams
+    sampling at once, each with a workspace of its own, both get the oracle's draws."""
+    x1 = sampler_logits(1, 32, V_REF, 201, scale=3.0)
+    x2 = sampler_logits(0, 8, V_REF, 202, scale=3.0)
+    u1 = ((np.arange(32) + 0.5) / 32).astype(np.float32)
+    u2 = ((np.arange(8) + 0.25) / 8).astype(np.float32)
+    t1, t2 = bf16_tensor(x1, DEV), bf16_tensor(x2, DEV)
+    d1, d2 = torch.from_numpy(u1).to(DEV), torch.from_numpy(u2).to(DEV)
+    ws1, ws2 = ops.sampler_workspace(DEV), ops.sampler_workspace(DEV)
+    assert torch.equal(ops.logprobs_rows(t1, ws1), ops.logprobs_rows(t1))
+    assert torch.equal(ops.argmax_rows(t2, ws2), ops.argmax_rows(t2))
+    want1 = oracle.sample_rows(x1, 1.0, 0.9, 20, u1)
+    want2 = oracle.sample_rows(x2, 0.8, 1.0, 40, u2)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    outs = []
+    for rep in range(4):
+        with torch.cuda.stream(s1):
+            a = ops.sample_rows(t1, 1.0, 0.9, 20, d1, ws1)
+        with torch.cuda.stream(s2):
+            b = ops.sample_rows(t2, 0.8, 1.0, 40, d2, ws2)
+        outs.append((a, b))
+    torch.cuda.synchronize()
+    for a, b in outs:
+        assert np.array_equal(a.cpu().numpy(), want1)
+        assert np.array_equal(b.cpu().numpy(), want2)
+
+
 def test_sample_rows_unaligned_vocabulary():
     for V in (1001, 7, 4096 + 3):
         x = sampler_logits(0, 3, V, V, scale=3.0)

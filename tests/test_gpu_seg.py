@@ -15,7 +15,7 @@ import oracle
 from jitengine_amd import ops
 from jitengine_amd.moe import MoEBlock
 from jitengine_amd.quant import QLinear, random_quantized
-from tests.helpers import assert_close_bf16, bf16_tensor, normal_bf16, stack_np, u16
+from tests.helpers import assert_close_bf16, bf16_tensor, normal_bf16, router_logits, stack_np, u16
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -65,6 +65,50 @@ def test_segment_gemm_parity(seg_case):
     r = ops.expert_down(h, dn, pk, seg=True)
     want_r = oracle.moe_down(u16(h), inds.view(np.uint32), opk, *stack_np(dn_h), bf16w=True)
     st = assert_close_bf16(u16(r), want_r, what="seg down")
+    assert st["bit_equal"] > 0.9, st
+
+
+def _pairs_of(inds_flat, order, pair_row, sel):
+    """(expert ids, pack) for the sorted positions `sel` alone, in the oracle's calling form: the
+    oracle computes pair j of the returned table as the pair at sorted position sel[j]."""
+    ids = np.ascontiguousarray(inds_flat[order[sel]]).astype(np.uint32)
+    return ids, {"order": np.arange(sel.size, dtype=np.int32), "pair_row": np.ascontiguousarray(pair_row[sel])}
+
+
+def test_segment_gemm_config3_geometry():
+    """BASELINE configs[3]'s MoE half at full size: 2,108 rows (four 512-token prefill chunks and 60
+    decode rows) routed top-8 over 128 experts -- 16,864 pairs, ~132 per expert, 160-row token
+    chunks, every expert's column blocks on the XCD of its expert -- through the segment GEMMs,
+    against the oracle's bf16-weight restatement on every pair of 16 experts (the largest segment
+    among them) with the seg tests' >= 90% bit-equal floor."""
+    B, E = 2108, 128
+    gu_d = random_quantized((E, 2 * I, D), 61, device=DEV)
+    dn_d = random_quantized((E, D, I), 62, device=DEV)
+    gu, dn = ops.prepack(gu_d), ops.prepack(dn_d)
+    gu_h, dn_h = gu_d.to("cpu"), dn_d.to("cpu")
+    del gu_d, dn_d
+    x = normal_bf16((B, D), seed=63)
+    inds, _, _ = oracle.router_topk(router_logits(0, B, E, seed=64), K_TOP, True)
+    pk = ops.moe_pack(torch.from_numpy(inds.view(np.int32)).to(DEV), E)
+    h = ops.expert_gate_up(bf16_tensor(x, DEV), gu, pk, seg=True)
+    r = ops.expert_down(h, dn, pk, seg=True)
+    torch.cuda.synchronize()
+    cnt = pk.expert_cnt.cpu().numpy()
+    order, pair_row = pk.order.cpu().numpy(), pk.pair_row.cpu().numpy()
+    by_count = np.argsort(cnt, kind="stable")
+    pick = set(by_count[np.linspace(0, E - 1, 15).astype(int)].tolist()) | {int(cnt.argmax())}
+    while len(pick) < 16:
+        pick.add(int(by_count[len(pick)]))
+    flat = inds.reshape(-1)
+    sel = np.flatnonzero(np.isin(flat[order], sorted(pick)))
+    assert cnt.max() >= 150 and sel.size > 16 * 64, (cnt.max(), sel.size)  # a whole 160-row chunk; ~2,100 pairs
+    ids, spk = _pairs_of(flat, order, pair_row, sel)
+    want_h = oracle.moe_gate_up(x, ids, spk, *stack_np(gu_h), bf16w=True)
+    st = assert_close_bf16(u16(h)[sel], want_h, what="config 3 seg gate_up")
+    assert st["bit_equal"] > 0.9, st
+    h_sel = np.ascontiguousarray(u16(h)[sel])
+    want_r = oracle.moe_down(h_sel, ids, {"order": spk["order"]}, *stack_np(dn_h), bf16w=True)
+    st = assert_close_bf16(u16(r)[sel], want_r, what="config 3 seg down")
     assert st["bit_equal"] > 0.9, st
 
 

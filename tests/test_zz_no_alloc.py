@@ -77,6 +77,27 @@ def test_noalloc_equals_workspace_entry_two_calls():
     assert torch.equal(got2.view(torch.int16), want.view(torch.int16))
 
 
+def test_noalloc_allocates_no_device_memory():
+    """After one warm call, further calls (inputs and `out` allocated beforehand) change neither the
+    device's free memory (an allocation inside the library would take at least a 2 MiB page of it)
+    nor torch's count of allocations."""
+    lens = [262144, 5000, 17]
+    q, pool, table, plan = _case(lens, seed=93)
+    out = torch.empty_like(q)
+    scale = 128 ** -0.5
+    ops.paged_decode_attention_noalloc(q, pool, table, plan, scale, out)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    allocs0 = torch.cuda.memory_stats().get("allocation.all.allocated", 0)
+    for _ in range(5):
+        ops.paged_decode_attention_noalloc(q, pool, table, plan, scale, out)
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    allocs1 = torch.cuda.memory_stats().get("allocation.all.allocated", 0)
+    assert abs(free1 - free0) < (2 << 20), (free0, free1)
+    assert allocs1 == allocs0, (allocs0, allocs1)
+
+
 def test_noalloc_rejects_partials_past_the_scratch():
     lib = _lib.lib()
     per_chunk = lib.jit_attn_workspace_bytes(1, 32)
