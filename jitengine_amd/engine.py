@@ -38,6 +38,7 @@ import numpy as np
 import torch
 
 from . import ops
+from . import selfcheck as _selfcheck
 from .kvpool import KVPool, PoolExhausted, PrefixStore, pages_for
 from .ops import PAGE
 from .model import CausalLM, make_mixed_state, make_step_state
@@ -69,7 +70,7 @@ class Engine:
 
     def __init__(self, lm: CausalLM, num_pages: int, prefill_chunk: int = 512, max_step_tokens: int = 2048,
                  prefix_store: bool = True, page_seed: int | None = None, device=None, allocate: bool = True,
-                 pipeline: bool = True):
+                 pipeline: bool = True, selfcheck: bool = False):
         if prefill_chunk <= 0 or max_step_tokens <= 0:
             raise ValueError("prefill_chunk and max_step_tokens must be positive")
         if prefill_chunk > max_step_tokens:
@@ -78,6 +79,8 @@ class Engine:
         cfg = lm.cfg
         dev = device if device is not None else lm.final_norm.device
         self.device = torch.device(dev)
+        if selfcheck or _selfcheck.enabled_by_env():  # the kernels against torch, once per device
+            _selfcheck.run(self.device)
         self.pool = KVPool(len(lm.layers), num_pages, cfg.kv_heads, self.device, seed=page_seed, allocate=allocate)
         self.store = PrefixStore(self.pool) if prefix_store else None
         self.prefill_chunk = int(prefill_chunk)

@@ -104,7 +104,7 @@ def _solo(lm, prompt, max_tokens, **kw):
 
 def test_engine_batched_equals_solo(lm):
     prompts = _prompts(1, [5, 17, 33, 40, 9])
-    e = Engine(lm, 128, prefill_chunk=16, max_step_tokens=48, page_seed=7)
+    e = Engine(lm, 128, prefill_chunk=16, max_step_tokens=48, page_seed=7, selfcheck=True)
     reqs = [e.submit(p, 6, eos=()) for p in prompts[:2]]
     e.step()
     e.step()
