@@ -936,6 +936,88 @@ def gemv_phases(dev: str) -> int:
     return 0
 
 
+def attn_phases(dev: str) -> int:
+    """Where decode attention's time goes (the stamps build, libjit_stamps.so with JIT_ATTN_STAMPS=1):
+    config 2's 32 ragged sequences and config 4's 262,144 keys, each over 3 pools in turn (so HBM
+    serves the pages); per workgroup, s_memrealtime stamps at entry, once its first K has landed,
+    at the end of its key loop, after its splits' states met in LDS and at its end."""
+    import ctypes
+
+    from jitengine_amd import _lib
+    from jitengine_amd import build as hip_build
+    from jitengine_amd import ops
+
+    lib = ctypes.CDLL(hip_build.STAMPS_LIB)
+    lib.jit_paged_decode_attn.argtypes = _lib._SIGNATURES["jit_paged_decode_attn"]
+    lib.jit_attn_stamps_clear.argtypes = [ctypes.c_void_p]
+    lib.jit_attn_stamps_read.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {}
+    for config in (2, 4):
+        rng = np.random.default_rng(seed_for(config))
+        if config == 2:
+            lens = np.round(np.exp(rng.uniform(np.log(128), np.log(32768), 32))).astype(np.int32) + 1
+        else:
+            lens = np.array([CONFIG4_KEYS], np.int32)
+        B, H, Hkv = lens.size, 32, 4
+        npg = (lens + 15) // 16
+        num_pages = int(npg.sum())
+        perm = rng.permutation(num_pages)
+        table = np.zeros((B, int(npg.max())), np.int32)
+        at = 0
+        for b in range(B):
+            table[b, :npg[b]] = perm[at:at + npg[b]]
+            at += npg[b]
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(5)
+        pools = [torch.randn((num_pages, Hkv, 2, 2048), generator=gen, device=dev, dtype=torch.bfloat16)
+                 for _ in range(3)]
+        q = torch.randn((B, H, 128), generator=gen, device=dev, dtype=torch.bfloat16)
+        tt = torch.from_numpy(table).to(dev)
+        plan = ops.attn_plan(lens, dev)
+        ws = torch.empty(ops.attn_workspace_bytes(plan.total, H), dtype=torch.uint8, device=dev)
+        o = torch.empty_like(q)
+
+        def run(i):
+            return lib.jit_paged_decode_attn(p(q), p(pools[i]), p(tt), table.shape[1], p(plan.lens),
+                                             p(plan.chunk_start), p(plan.chunk_seq), B, H, Hkv, 128 ** -0.5,
+                                             plan.total, p(ws), p(o), sp)
+        for rep in range(6):
+            assert run(rep % 3) == 0
+        torch.cuda.synchronize()
+        assert lib.jit_attn_stamps_clear(sp) == 0
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_ev.record()
+        assert run(0) == 0
+        e_ev.record()
+        torch.cuda.synchronize()
+        buf = np.zeros((1 << 14, 8), np.uint64)
+        assert lib.jit_attn_stamps_read(buf.ctypes.data_as(ctypes.c_void_p), 1 << 14) == 0
+        slots = np.flatnonzero(buf[:, 7] == 1)
+        st = buf[slots][:, :5].astype(np.int64)
+        t0 = st[:, 0].min()
+        rel = (st - t0) * 0.01  # microseconds (s_memrealtime counts at 100 MHz)
+        xcd = slots % 8  # workgroups are dealt to the 8 XCDs round-robin in launch order
+        d = np.diff(st, axis=1) * 0.01
+        kv = int(lens.astype(np.int64).sum()) * 2048
+
+        def q_(v):
+            return [round(float(np.percentile(v, x)), 2) for x in (0, 10, 50, 90, 100)]
+        out[f"config{config}"] = {
+            "workgroups": int(st.shape[0]), "event_us_kernel_plus_merge": round(s_ev.elapsed_time(e_ev) * 1e3, 2),
+            "span_us": round(float(rel[:, 4].max()), 2), "kv_MB": round(kv / 1e6, 1),
+            "start_us_pctl_0_10_50_90_100": q_(rel[:, 0]), "end_us_pctl_0_10_50_90_100": q_(rel[:, 4]),
+            "first_k_landed_us_mean": round(float(d[:, 0].mean()), 2), "key_loop_us_pctl": q_(d[:, 1]),
+            "split_merge_wait_us_mean": round(float(d[:, 2].mean()), 3), "tail_us_mean": round(float(d[:, 3].mean()), 3),
+            "end_us_mean_by_xcd": [round(float(rel[xcd == x, 4].mean()), 2) for x in range(8)],
+            "end_us_max_by_xcd": [round(float(rel[xcd == x, 4].max()), 2) for x in range(8)],
+            # every workgroup of config 4 streams an equal share at once: the bytes over the median key loop
+            "steady_rate_GB_s": round(kv / (float(np.median(d[:, 1])) * 1e-6) / 1e9, 1) if config == 4 else None}
+    print(json.dumps({"attn_phases": out}), flush=True)
+    return 0
+
+
 OP_KERNELS = {  # the kernels one op launches (rocprofv3 kernel names contain these)
     "paged_attention": ["paged_attn_kernel", "attn_merge_kernel"],
     "gate_up_swiglu": ["qmm_kernel<1, 8, true, true"],
@@ -1136,6 +1218,8 @@ def main() -> int:
     ap.add_argument("--sampler", action="store_true", help="time the sampler's kernels (vocabulary 248,320)")
     ap.add_argument("--probe", action="store_true",
                     help="measure the streaming-read ceiling, the empty-launch floor and the grid-barrier cost")
+    ap.add_argument("--attn-phases", action="store_true",
+                    help="per-phase stamps of decode attention (the stamps build of csrc/attention.hip)")
     ap.add_argument("--gemv-phases", action="store_true",
                     help="per-phase stamps of the expert GEMVs (the stamps build of csrc/qmm.hip)")
     ap.add_argument("--probe-parts", default="read,launch,barrier",
@@ -1164,6 +1248,8 @@ def main() -> int:
         return probe(dev, set(args.probe_parts.split(",")))
     if args.gemv_phases:
         return gemv_phases(dev)
+    if args.attn_phases:
+        return attn_phases(dev)
     if args.sampler:
         return bench_sampler(dev)
     if args.config == 1:

@@ -24,7 +24,8 @@ INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(OUT_DIR, "libjit_moe.so")
 PROBE_LIB = os.path.join(OUT_DIR, "libjit_probe.so")  # bench.py's measurement kernels (csrc/probe.hip)
-# the quantized projections with per-workgroup phase stamps (JIT_QMM_STAMPS=1), for bench.py --gemv-phases
+# the quantized projections and decode attention with per-workgroup phase stamps (JIT_QMM_STAMPS=1,
+# JIT_ATTN_STAMPS=1), for bench.py --gemv-phases and --attn-phases
 STAMPS_LIB = os.path.join(OUT_DIR, "libjit_stamps.so")
 ARCH = "gfx950"
 
@@ -69,7 +70,8 @@ def build(verbose: bool = False) -> str:
     """Compile every source and link the shared library; returns its path."""
     os.makedirs(OUT_DIR, exist_ok=True)
     jobs = [(src, extra, "") for src, extra in SOURCES.items()]
-    jobs += [(src, SOURCES[src] + ["-DJIT_QMM_STAMPS=1"], ".stamps") for src in ("errors.cpp", "qmm.hip")]
+    jobs += [(src, SOURCES[src] + ["-DJIT_QMM_STAMPS=1", "-DJIT_ATTN_STAMPS=1"], ".stamps")
+             for src in ("errors.cpp", "qmm.hip", "attention.hip")]
     with ThreadPoolExecutor(max_workers=4) as ex:
         built = list(ex.map(lambda j: _compile(j[0], j[1], verbose, j[2]), jobs))
     objs, stamp_objs = built[:len(SOURCES)], built[len(SOURCES):]

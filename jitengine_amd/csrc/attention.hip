@@ -170,8 +170,38 @@ __device__ __forceinline__ uint32_t mask_pair(uint32_t w, int k, int L) {
 // loads in flight than one wave per kv head walking the whole chunk.
 constexpr int kStateFloats = 32 + 2;  // o[8][4], max, sum per lane
 
+// Stamps (a build with JIT_ATTN_STAMPS=1 only, bench.py --attn-phases): wave 0 of every workgroup
+// records s_memrealtime (100 MHz) at entry (0), once its first step's K has landed (1; that build
+// waits for it there), at the end of its key loop (2), after the splits' states have met in LDS (3)
+// and at its end (4).
+#ifndef JIT_ATTN_STAMPS
+#define JIT_ATTN_STAMPS 0
+#endif
+#if JIT_ATTN_STAMPS
+constexpr int kAttnStampSlots = 1 << 14;
+__device__ uint64_t g_attn_stamps[kAttnStampSlots][8];
+#define ATTN_STAMP(i) ts[i] = __builtin_amdgcn_s_memrealtime()
+#else
+#define ATTN_STAMP(i) \
+  do {                \
+  } while (0)
+#endif
+
 template <int WS>
 __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
+#if JIT_ATTN_STAMPS
+  uint64_t ts[5] = {__builtin_amdgcn_s_memrealtime(), 0, 0, 0, 0};
+  auto stamp_out = [&]() {
+    ts[4] = __builtin_amdgcn_s_memrealtime();
+    const int slot = blockIdx.x + gridDim.x * blockIdx.y;
+    if (threadIdx.x < 5 && slot < kAttnStampSlots) {
+      uint64_t v = ts[0];
+      for (int i = 1; i < 5; i++) v = threadIdx.x == i ? ts[i] : v;
+      g_attn_stamps[slot][threadIdx.x] = v;
+      if (threadIdx.x == 0) g_attn_stamps[slot][7] = 1;
+    }
+  };
+#endif
   static_assert(WS == kAttnSplits, "the chunk rule rounds to whole 32-key steps of each of WS waves");
   extern __shared__ float xstate[];  // [WS - 1][hb][kStateFloats][64]
   const int gc = blockIdx.x;
@@ -223,6 +253,11 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
     asm volatile("" ::: "memory");
     load_v2(vv, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
   }
+#if JIT_ATTN_STAMPS
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("" ::: "memory");
+  ATTN_STAMP(1);
+#endif
   for (int st = 0; st < nst; st++) {
     const int k0 = wk0 + 32 * st;
     f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -312,6 +347,7 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
     // issued once that step's K has arrived
     asm volatile("" ::: "memory");
   }
+  ATTN_STAMP(2);
   if (WS > 1) {  // the splits' states meet: split 0 of each kv head adds splits 1.. in order
     if (split > 0) {
       float *st = xstate + (((split - 1) * hb + kvl) * kStateFloats) * 64 + l;
@@ -323,6 +359,7 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
       st[33 * 64] = l_run;
     }
     __syncthreads();
+    ATTN_STAMP(3);
     if (split > 0 || !live) return;
 #pragma unroll
     for (int sp = 1; sp < WS; sp++) {
@@ -340,6 +377,9 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
   } else if (!live) {
     return;
   }
+#if JIT_ATTN_STAMPS
+  if (wave == 0) stamp_out();
+#endif
   // per-head sum over the four lane groups
   const float l_tot = sum_xor32(sum_xor16(l_run));
   if (lr >= G) return;
@@ -900,3 +940,17 @@ extern "C" int jit_paged_decode_attn_noalloc(const uint16_t *q, const uint16_t *
   return decode_attn_launch(q, pool, page_table, max_pages, lens, chunk_start, chunk_seq, B, H, Hkv, scale,
                             total_chunks, ws, out, (hipStream_t)stream, "jit_paged_decode_attn_noalloc");
 }
+
+#if JIT_ATTN_STAMPS
+// The stamps of the last decode-attention launch (bench.py --attn-phases).
+extern "C" int jit_attn_stamps_clear(void *stream) {
+  void *p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_attn_stamps)) != hipSuccess) return JIT_ELAUNCH;
+  return hipMemsetAsync(p, 0, sizeof(g_attn_stamps), (hipStream_t)stream) == hipSuccess ? 0 : JIT_ELAUNCH;
+}
+extern "C" int jit_attn_stamps_read(uint64_t *host, int slots) {
+  if (!host || slots < 0 || slots > kAttnStampSlots) return JIT_EINVAL;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_attn_stamps), (size_t)slots * 8 * sizeof(uint64_t), 0,
+                             hipMemcpyDeviceToHost) == hipSuccess ? 0 : JIT_ELAUNCH;
+}
+#endif
