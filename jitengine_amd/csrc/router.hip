@@ -193,12 +193,18 @@ int launch_router(const uint16_t *src, int rows, int N, int k, int norm, uint32_
 constexpr int kPackThreads = 1024;  // the largest workgroup (and expert count) of the packing
 
 __device__ __forceinline__ int wave_incl_scan(int x, int l) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (l >= o) x += y;
-  }
-  return x;
+  // within each 16-lane row by row shifts 1, 2, 4, 8 (lanes past a row's start add 0), then the
+  // rows' totals (integers: any order gives the same sums)
+#define JIT_SCAN_STEP(ctrl) x += __builtin_amdgcn_update_dpp(0, x, ctrl, 0xF, 0xF, true)
+  JIT_SCAN_STEP(0x111);
+  JIT_SCAN_STEP(0x112);
+  JIT_SCAN_STEP(0x114);
+  JIT_SCAN_STEP(0x118);
+#undef JIT_SCAN_STEP
+  const int t0 = __builtin_amdgcn_readlane(x, 15), t1 = __builtin_amdgcn_readlane(x, 31);
+  const int t2 = __builtin_amdgcn_readlane(x, 47);
+  const int row = l >> 4;
+  return x + (row >= 1 ? t0 : 0) + (row >= 2 ? t1 : 0) + (row >= 3 ? t2 : 0);
 }
 
 // The per-expert tables from each expert's pair count c (thread t: expert t, t < E; threads past
@@ -216,8 +222,7 @@ __device__ __forceinline__ void pack_tables(int c, int bad, int E, int *nxt, int
   const int cs = wave_incl_scan(c, l);
   const int fs = wave_incl_scan(f, l);
   int mx = c;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mx = max(mx, __shfl_xor(mx, o, 64));
+  mx = (int)wave_max_u32((uint32_t)mx);  // (counts are >= 0)
   if (l == 63) {
     wsum[w] = cs;
     wflag[w] = fs;
