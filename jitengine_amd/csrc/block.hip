@@ -26,8 +26,7 @@ constexpr int kD = JIT_HEAD_DIM;
 constexpr int kPage = JIT_PAGE_TOKENS;
 
 __device__ __forceinline__ float block_sum_256(float v, float *red) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += shfl_xor_f(v, o);
+  v = wave_butterfly<false>(v);  // (the pairs of a shuffle butterfly over offsets 32..1)
   const int w = threadIdx.x >> 6;
   if (lane_id() == 0) red[w] = v;
   __syncthreads();
@@ -219,8 +218,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
   }
   const uint16_t *nw = head < H ? qn_w : kn_w;
   float ss = fmaf(x1, x1, x2 * x2);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += shfl_xor_f(ss, o);
+  ss = wave_butterfly<false>(ss);  // (the pairs of a shuffle butterfly over offsets 32..1)
   const float r = rsqrtf(ss / (float)kD + eps);
   x1 = bf2f(f2bf(bf2f(nw[l]) * bf2f(f2bf(x1 * r))));
   x2 = bf2f(f2bf(bf2f(nw[l + 64]) * bf2f(f2bf(x2 * r))));

@@ -64,28 +64,6 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // slots rank-(N-k) in ascending (value, index) order.  The wave finds them as k
 // rounds of a maximum over (value, index) keys, round t filling slot k-1-t -- the
 // same slots the ranks give, with no pairwise comparison.
-// The butterfly over lane offsets 32, 16, 8, 4, 2, 1 (in that order; after step o every lane
-// holds the combination of its own value and lane l ^ o's), in VALU lane exchanges instead of LDS
-// permutes: the permlane swaps for 32 and 16, a row rotation by 8 (lane l ^ 8 within its 16-lane
-// row), two bank-masked row shifts for 4, quad permutes for 2 and 1.  Each step pairs the same
-// lanes as a shuffle by l ^ o would, and the combination is commutative, so the results are the
-// shuffle butterfly's bit for bit.
-template <bool MAX>
-__device__ __forceinline__ float wave_butterfly(float v) {
-  auto op = [](float a, float b) { return MAX ? (b > a ? b : a) : a + b; };
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  const int vi = __float_as_int(v);
-  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(vi, vi, 0x128, 0xF, 0xF, false)));  // row_ror:8
-  int x4 = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x104, 0xF, 0x5, false);  // row_shl:4, banks 0, 2
-  x4 = __builtin_amdgcn_update_dpp(x4, __float_as_int(v), 0x114, 0xF, 0xA, false);               // row_shr:4, banks 1, 3
-  v = op(v, __int_as_float(x4));
-  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x4E, 0xF, 0xF, false)));
-  return op(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xF, 0xF, false)));
-}
-
 // One row on one wave: softmax (unless FROM_GATES) and the top-k slots, written to
 // inds / scores.  `skey` is the wave's LDS scratch of k entries.
 template <int NPL, bool FROM_GATES>
