@@ -44,9 +44,17 @@ struct QmmArgs {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// The wave's integer sum (exact, so the pairing does not matter), by VALU lane exchanges: the
+// permlane swaps across rows, then DPP row rotations within each 16-lane row.
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  v = (int)(r[0] + r[1]);
+  r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  v = (int)(r[0] + r[1]);
+  v += __builtin_amdgcn_update_dpp(v, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  v += __builtin_amdgcn_update_dpp(v, v, 0x124, 0xF, 0xF, false);  // row_ror:4
+  v += __builtin_amdgcn_update_dpp(v, v, 0x122, 0xF, 0xF, false);  // row_ror:2
+  v += __builtin_amdgcn_update_dpp(v, v, 0x121, 0xF, 0xF, false);  // row_ror:1
   return v;
 }
 constexpr uint32_t kXOutOfRange = 0x80000000u;  // a byte offset past the activation buffer's range
