@@ -414,17 +414,16 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
 // merged in lane order: a fixed order that depends only on the sequence's chunk count.
 constexpr int kMergeLanes = 16;
 
-__global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restrict__ lens,
-                                                         const int32_t *__restrict__ chunk_start,
+__global__ __launch_bounds__(512) void attn_merge_kernel(const int32_t *__restrict__ chunk_start,
                                                          const float *__restrict__ part_o,
                                                          const float *__restrict__ part_ml, int H,
                                                          uint16_t *__restrict__ out) {
   const int b = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
-  const int L = lens[b];
-  const int ck = chunk_tokens(L);
-  const int n = (L + ck - 1) / ck;
-  if (n <= 1) return;
+  // the sequence's chunks from the plan's prefix alone (one load of two adjacent words, where
+  // lens[b] and then the prefix were two round trips in a row; the plan is lens' chunk split)
   const long long c0 = chunk_start[b];
+  const int n = chunk_start[b + 1] - (int)c0;
+  if (n <= 1) return;
   __shared__ float4 s_o[kMergeLanes][32];
   __shared__ float s_m[kMergeLanes], s_l[kMergeLanes];
   const int cl = t >> 5, dq = t & 31;
@@ -857,7 +856,7 @@ int decode_attn_launch(const uint16_t *q, const uint16_t *pool, const int32_t *p
   paged_attn_kernel<WS><<<dim3(total_chunks, (Hkv + hb - 1) / hb), 64 * hb * WS, lds, st>>>(a);
   int rc = jit::check_launch(what);
   if (rc) return rc;
-  attn_merge_kernel<<<dim3(B, H), 512, 0, st>>>(lens, chunk_start, part_o, part_ml, H, out);
+  attn_merge_kernel<<<dim3(B, H), 512, 0, st>>>(chunk_start, part_o, part_ml, H, out);
   return jit::check_launch(what);
 }
 
