@@ -323,17 +323,29 @@ int jit_paged_decode_attn_noalloc(const uint16_t *q, const uint16_t *pool, const
  * Chunk c owns q rows chunk_row[c] .. + chunk_len[c] - 1 of q [T, H, 128] (normed,
  * rotated); its token t sits at position chunk_ctx[c] + t of sequence chunk_seq[c]
  * and attends keys 0 .. chunk_ctx[c] + t (the pool must hold them: the chunk's own
- * keys appended).  Work items: nblk (chunk, first token) pairs blk_chunk, blk_q0 of
- * jit_prefill_block_tokens(H, Hkv) tokens each, covering every chunk (any order;
- * longest first balances best).  out [T, H, 128] bf16; fp32 online softmax.
- * Contract: H % Hkv == 0 (JIT_EINVAL), H / Hkv divides 16 (JIT_EUNSUPPORTED).  Any context
- * length: the first 4,096 page ids of a work item are staged in LDS, later ones read from the table. */
+ * keys appended).  A token's keys are cut into parts at multiples of
+ * jit_prefill_part_keys() (6,144): a token at position pos has pos / 6144 + 1 parts.
+ * Work items: nblk (chunk, first token, part) triples blk_chunk, blk_q0, blk_part --
+ * row blocks of jit_prefill_block_tokens(H, Hkv) tokens, each with one item per part
+ * that holds a key of its last token -- covering every chunk (any order; longest
+ * first balances best).  pmax = the most parts of any token; max_len = the longest
+ * chunk.  Tokens of one part are written by their item; the others leave fp32
+ * partials in workspace (jit_prefill_workspace_bytes(T, pmax, H) bytes, T = the q
+ * rows; unused and may be null when pmax == 1), which a second launch merges in part
+ * order.  out [T, H, 128] bf16; fp32 online softmax.
+ * Contract: H % Hkv == 0, pmax >= 1 (JIT_EINVAL), H / Hkv divides 16, H <= 64 when
+ * pmax > 1 (JIT_EUNSUPPORTED).  Any context length. */
 int jit_prefill_block_tokens(int H, int Hkv);
+int jit_prefill_part_keys(void);
+/* Bytes of the partials' workspace: T * pmax * H * 132 * 4 when pmax > 1, 0 when pmax == 1,
+ * -1 for T < 0, pmax < 1 or H <= 0. */
+long long jit_prefill_workspace_bytes(int T, int pmax, int H);
 int jit_paged_prefill_attn(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,
                            int max_pages, const int32_t *chunk_seq, const int32_t *chunk_ctx,
                            const int32_t *chunk_len, const int32_t *chunk_row, int C,
-                           const int32_t *blk_chunk, const int32_t *blk_q0, int nblk, int H, int Hkv,
-                           float scale, uint16_t *out, void *stream);
+                           const int32_t *blk_chunk, const int32_t *blk_q0, const int32_t *blk_part,
+                           int nblk, int pmax, int max_len, int H, int Hkv, float scale,
+                           void *workspace, uint16_t *out, void *stream);
 
 /* ------------------------------------------------------------------ step ends and KV pages */
 

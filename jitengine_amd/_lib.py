@@ -54,7 +54,9 @@ _SIGNATURES = {
     "jit_paged_decode_attn": [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P, _P],
     "jit_paged_decode_attn_noalloc": [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P],
     "jit_prefill_block_tokens": [_I, _I],
-    "jit_paged_prefill_attn": [_P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _F, _P, _P],
+    "jit_paged_prefill_attn": [_P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P],
+    "jit_prefill_part_keys": [],
+    "jit_prefill_workspace_bytes": [_I, _I, _I],
     "jit_embed_q4": [_P, _I, _P, _P, _P, _I, _I, _P, _P],
     "jit_logprobs_rows": [_P, _I, _I, _P, _P],
     "jit_argmax_rows": [_P, _I, _I, _P, _P],
@@ -67,6 +69,7 @@ _SIGNATURES = {
     "jit_kv_copy_pages": [_P, _I, _I, _P, _P, _I, _P],
 }
 _RESTYPES = {"jit_last_error": ctypes.c_char_p, "jit_attn_workspace_bytes": ctypes.c_int64,
+             "jit_prefill_workspace_bytes": ctypes.c_int64,
              "jit_q4_packed_bytes": ctypes.c_int64, "jit_moe_pack_workspace_bytes": ctypes.c_int64,
              "jit_sampler_workspace_bytes": ctypes.c_int64}
 

@@ -496,15 +496,32 @@ constexpr int kPfChunks = kPfHalves * 4 * kPageHead * 2 / 1024 / kPfWaves;  // 1
 static_assert(kPfChunks == 8 && kPfWaves == 2 * kPfHalves, "one page per wave per step");
 static_assert(kPfStages == 2, "the page-id prefetch below runs one step ahead of the staging");
 
+// Key parts.  A token's keys are cut at the fixed positions kPfPartKeys, 2 kPfPartKeys, ...
+// (whole 128-key steps), and each part of a row block is a work item of its own, so a chunk
+// deep into a long context becomes several items of at most kPfPartSteps steps that the
+// dispatcher can place beside the short ones (config 3: the longest item falls from 68 steps to
+// 48, against a mean of 46).  A token whose keys all precede kPfPartKeys is finished by its one
+// item; the others leave fp32 partials (m, l, o) per part, which prefill_merge_kernel combines in
+// part order.  The cuts depend only on key positions, so a token's bits still depend only on its
+// q row and its keys.
+#ifndef JIT_PF_PART_STEPS
+#define JIT_PF_PART_STEPS 48
+#endif
+constexpr int kPfPartSteps = JIT_PF_PART_STEPS;
+constexpr int kPfPartKeys = kPfPartSteps * 32 * kPfHalves;
+constexpr int kPfSlot = kD + 4;  // floats of one (token, part, head) partial: o, max, sum, 2 pad (16 B rows)
+
 struct PrefillArgs {
   const uint16_t *q;          // [T, H, 128] bf16 (normed, rotated)
   const uint16_t *pool;
   const int32_t *page_table;  // [S, max_pages]
   const int32_t *blk_chunk;   // [nblk] chunk of each workgroup
   const int32_t *blk_q0;      // [nblk] first token (within the chunk) of each workgroup
+  const int32_t *blk_part;    // [nblk] key part of each workgroup
   const int32_t *chunk_seq, *chunk_ctx, *chunk_len, *chunk_row;  // [C]
   uint16_t *out;              // [T, H, 128] bf16
-  int max_pages, H, Hkv, G;
+  float *part;                // [T][pmax][H][kPfSlot] fp32: o[128], max, sum (tokens of several parts)
+  int max_pages, H, Hkv, G, pmax;
   float qk_scale;             // scale * log2(e)
 };
 
@@ -513,8 +530,11 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   // (4 KB each), filled by direct global->LDS loads kPfStages - 1 steps ahead of the step
   // being computed
   __shared__ __attribute__((aligned(16))) uint16_t kvs[kPfStages][kPfHalves * 4 * kPageHead];
-  const int ch = a.blk_chunk[blockIdx.x], q0 = a.blk_q0[blockIdx.x];
-  const int kvh = blockIdx.y;
+  // one dimension, the kv heads of an item adjacent: the hardware dispatches workgroups in index
+  // order, so the plan's longest-first order holds across the kv heads (a (item, kv head) grid
+  // dispatched every item of kv head 0 before any of kv head 1)
+  const int item = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
+  const int ch = a.blk_chunk[item], q0 = a.blk_q0[item], part = a.blk_part[item];
   const int seq = a.chunk_seq[ch], ctx = a.chunk_ctx[ch], len = a.chunk_len[ch], row0 = a.chunk_row[ch];
   const int G = a.G, TR = 16 / G, tpw = kPfTiles * TR;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = lane_id();
@@ -522,6 +542,9 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   const int tlast = min(q0 + kPfWaves * tpw, len) - 1;  // the workgroup's last token
   const int kend = ctx + tlast + 1;                     // its keys: [0, kend)
   const int nst = (kend + 32 * kPfHalves - 1) / (32 * kPfHalves), npages = (kend + 15) >> 4;
+  // this item's steps: part `part` of the keys (the plan makes an item only for parts that hold a
+  // key of the block's last token)
+  const int st0 = part * kPfPartSteps, st1 = min(nst, st0 + kPfPartSteps);
   const int32_t *prow = a.page_table + (long long)seq * a.max_pages;
   // wave w stages on step st page 2 kPfHalves st + w of the workgroup's keys (a page past the keys
   // repeats the last one); lane i reads the page of wave i % kPfWaves, so that the ids stay in a
@@ -583,15 +606,15 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
 #pragma unroll
     for (int cc = 0; cc < 4; cc++)
       asm volatile("" ::"v"(qf[j][cc].u[0]), "v"(qf[j][cc].u[1]), "v"(qf[j][cc].u[2]), "v"(qf[j][cc].u[3]));
-  PF_STAGE(0, pages_of_step(0));
+  PF_STAGE(st0, pages_of_step(st0));
   // the pages of the next step to stage, read one step ahead so that their latency hides behind a
   // step's arithmetic (the wait for them is the loop's own wait for the staging)
-  int pv_next = pages_of_step(1);
+  int pv_next = pages_of_step(st0 + 1);
   // the wait that leaves the loads of the next kPfStages - 2 steps in flight, and no lgkm or
   // export wait (vmcnt is split over bits 3:0 and 15:14)
   constexpr int kPfVm = (kPfStages - 2) * kPfChunks;
   constexpr int kPfWait = (kPfVm & 15) | ((kPfVm >> 4) << 14) | (7 << 4) | (15 << 8);
-  for (int st = 0; st < nst; st++) {
+  for (int st = st0; st < st1; st++) {
     // this wave's loads of step st have landed and its reads of step st - 1 are done; after
     // the barrier so are every wave's, and stage (st - 1) % kPfStages may be refilled
     // (the empty asm statements keep the compiler from moving LDS accesses across the barrier,
@@ -675,7 +698,10 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
 #pragma unroll
           for (int i = 0; i < 4; i++) tmax = fmaxf(tmax, sc[j][h][t][i]);
       tmax = max_xor32(max_xor16(tmax)) * a.qk_scale;
-      m_step[j] = fmaxf(m_run[j], tmax);  // finite: key 0 is in every row's first step
+      // finite for every row with a key in this part (its first key is in the part's first step);
+      // a row without one (a token before the part's first key) turns NaN in its own column only
+      // and is never stored
+      m_step[j] = fmaxf(m_run[j], tmax);
       alpha[j] = __builtin_amdgcn_exp2f(m_run[j] - m_step[j]);
       psum[j] = 0.0f;
       if (__any(alpha[j] != 1.0f)) {
@@ -760,16 +786,72 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_attn_kernel(const Prefi
   for (int j = 0; j < kPfTiles; j++) {
     const float l_tot = sum_xor32(sum_xor16(l_run[j]));
     if (!store[j]) continue;
-    const float inv = 1.0f / l_tot;
-    uint16_t *op = a.out + ((long long)(row0 + tok[j]) * a.H + kvh * G + lr % G) * kD + 4 * lg;
+    const int parts = (ctx + tok[j]) / kPfPartKeys + 1;  // the token's key parts
+    const long long hrow = (long long)(row0 + tok[j]) * a.H + kvh * G + lr % G;
+    if (parts == 1) {  // (then part == 0): the token's whole result
+      const float inv = 1.0f / l_tot;
+      uint16_t *op = a.out + hrow * kD + 4 * lg;
 #pragma unroll
-    for (int cc = 0; cc < 8; cc++) {
-      uint2 w;
-      w.x = pack_bf16x2(o[j][cc][0] * inv, o[j][cc][1] * inv);
-      w.y = pack_bf16x2(o[j][cc][2] * inv, o[j][cc][3] * inv);
-      *(uint2 *)(op + 16 * cc) = w;
+      for (int cc = 0; cc < 8; cc++) {
+        uint2 w;
+        w.x = pack_bf16x2(o[j][cc][0] * inv, o[j][cc][1] * inv);
+        w.y = pack_bf16x2(o[j][cc][2] * inv, o[j][cc][3] * inv);
+        *(uint2 *)(op + 16 * cc) = w;
+      }
+    } else if (part < parts) {  // this part's (max, sum, unnormalised o) of the token
+      float *ps = a.part + (((long long)(row0 + tok[j]) * a.pmax + part) * a.H + kvh * G + lr % G) * kPfSlot;
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++)
+        *(float4 *)(ps + 16 * cc + 4 * lg) = make_float4(o[j][cc][0], o[j][cc][1], o[j][cc][2], o[j][cc][3]);
+      if (lg == 0) *(float2 *)(ps + kD) = make_float2(m_run[j], l_tot);
     }
   }
+}
+
+// Merge of a token's key parts (tokens at or past kPfPartKeys): one workgroup of 8 H threads per
+// token, thread (h, d) owning 16 dims of head h; the parts are combined online in part order
+// (running max in the exp2 domain, as the parts were formed), then normalised and rounded as a
+// whole-token result is.  Grid: (the longest chunk, chunks); other tokens exit at once.
+__global__ __launch_bounds__(512) void prefill_merge_kernel(const int32_t *__restrict__ chunk_ctx,
+                                                            const int32_t *__restrict__ chunk_len,
+                                                            const int32_t *__restrict__ chunk_row,
+                                                            const float *__restrict__ part, int H, int pmax,
+                                                            uint16_t *__restrict__ out) {
+  const int c = blockIdx.y, t = blockIdx.x;
+  if (t >= chunk_len[c]) return;
+  const int parts = (chunk_ctx[c] + t) / kPfPartKeys + 1;
+  if (parts < 2) return;
+  const long long row = chunk_row[c] + t;
+  const int h = threadIdx.x >> 3, d0 = 16 * (threadIdx.x & 7);
+  float M = -INFINITY, Ls = 0.0f;
+  float O[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) O[i] = 0.0f;
+  for (int p = 0; p < parts; p++) {
+    const float *ps = part + ((row * pmax + p) * H + h) * kPfSlot;
+    const float2 ml = *(const float2 *)(ps + kD);
+    const float4 *po = (const float4 *)(ps + d0);
+    const float mn = fmaxf(M, ml.x);
+    const float fa = exp2f(M - mn), fb = exp2f(ml.x - mn);
+    Ls = Ls * fa + ml.y * fb;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float4 v = po[q];
+      O[4 * q] = O[4 * q] * fa + v.x * fb;
+      O[4 * q + 1] = O[4 * q + 1] * fa + v.y * fb;
+      O[4 * q + 2] = O[4 * q + 2] * fa + v.z * fb;
+      O[4 * q + 3] = O[4 * q + 3] * fa + v.w * fb;
+    }
+    M = mn;
+  }
+  const float inv = 1.0f / Ls;
+  uint4 w[2];
+  uint32_t *wu = (uint32_t *)w;
+#pragma unroll
+  for (int i = 0; i < 8; i++) wu[i] = pack_bf16x2(O[2 * i] * inv, O[2 * i + 1] * inv);
+  uint4 *op = (uint4 *)(out + (row * H + h) * kD + d0);
+  op[0] = w[0];
+  op[1] = w[1];
 }
 
 }  // namespace
@@ -779,23 +861,38 @@ extern "C" int jit_prefill_block_tokens(int H, int Hkv) {
   return kPfWaves * kPfTiles * 16 / (H / Hkv);
 }
 
+extern "C" int jit_prefill_part_keys(void) { return kPfPartKeys; }
+
+extern "C" long long jit_prefill_workspace_bytes(int T, int pmax, int H) {
+  if (T < 0 || pmax < 1 || H <= 0) return -1;
+  return pmax > 1 ? (long long)T * pmax * H * kPfSlot * (long long)sizeof(float) : 0;
+}
+
 extern "C" int jit_paged_prefill_attn(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,
                                       int max_pages, const int32_t *chunk_seq, const int32_t *chunk_ctx,
                                       const int32_t *chunk_len, const int32_t *chunk_row, int C,
-                                      const int32_t *blk_chunk, const int32_t *blk_q0, int nblk, int H, int Hkv,
-                                      float scale, uint16_t *out, void *stream) {
-  if (C < 0 || nblk < 0 || H <= 0 || Hkv <= 0 || max_pages <= 0)
-    return jit::fail(JIT_EINVAL, "paged_prefill_attn: bad dims C=%d nblk=%d H=%d Hkv=%d", C, nblk, H, Hkv);
+                                      const int32_t *blk_chunk, const int32_t *blk_q0, const int32_t *blk_part,
+                                      int nblk, int pmax, int max_len, int H, int Hkv, float scale,
+                                      void *workspace, uint16_t *out, void *stream) {
+  if (C < 0 || nblk < 0 || H <= 0 || Hkv <= 0 || max_pages <= 0 || pmax < 1 || max_len < 0)
+    return jit::fail(JIT_EINVAL, "paged_prefill_attn: bad dims C=%d nblk=%d H=%d Hkv=%d pmax=%d max_len=%d", C,
+                     nblk, H, Hkv, pmax, max_len);
   if (H % Hkv != 0) return jit::fail(JIT_EINVAL, "%d query heads do not share %d KV heads evenly", H, Hkv);
   if (16 % (H / Hkv) != 0)
     return jit::fail(JIT_EUNSUPPORTED, "paged_prefill_attn covers H / Hkv in {1, 2, 4, 8, 16}, got %d", H / Hkv);
+  if (pmax > 1 && H > 64)
+    return jit::fail(JIT_EUNSUPPORTED, "paged_prefill_attn merges key parts of up to 64 query heads, got %d", H);
   if (C == 0 || nblk == 0) return JIT_OK;
   if (!q || !pool || !page_table || !chunk_seq || !chunk_ctx || !chunk_len || !chunk_row || !blk_chunk ||
-      !blk_q0 || !out)
+      !blk_q0 || !blk_part || !out || (pmax > 1 && !workspace))
     return jit::fail(JIT_EINVAL, "paged_prefill_attn: null pointer");
-  const PrefillArgs a{q, pool, page_table, blk_chunk, blk_q0, chunk_seq, chunk_ctx, chunk_len, chunk_row, out,
-                      max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f};
-  prefill_attn_kernel<<<dim3(nblk, Hkv), 64 * kPfWaves, 0, (hipStream_t)stream>>>(a);
+  const PrefillArgs a{q, pool, page_table, blk_chunk, blk_q0, blk_part, chunk_seq, chunk_ctx, chunk_len, chunk_row,
+                      out, (float *)workspace, max_pages, H, Hkv, H / Hkv, pmax, scale * 1.44269504088896341f};
+  prefill_attn_kernel<<<dim3(nblk * Hkv), 64 * kPfWaves, 0, (hipStream_t)stream>>>(a);
+  int rc = jit::check_launch("jit_paged_prefill_attn");
+  if (rc || pmax == 1 || max_len == 0) return rc;
+  prefill_merge_kernel<<<dim3(max_len, C), 8 * H, 0, (hipStream_t)stream>>>(chunk_ctx, chunk_len, chunk_row,
+                                                                              (const float *)workspace, H, pmax, out);
   return jit::check_launch("jit_paged_prefill_attn");
 }
 

@@ -513,34 +513,52 @@ class PrefillPlan:
 
     chunks: list
     tables: torch.Tensor  # [4, C] chunk_seq, chunk_ctx, chunk_len, chunk_row
-    blocks: torch.Tensor  # [2, nblk] blk_chunk, blk_q0
+    blocks: torch.Tensor  # [3, nblk] blk_chunk, blk_q0, blk_part
     rows: int
+    pmax: int = 1  # most key parts of a token (jit_prefill_part_keys keys a part)
+    max_len: int = 0  # the longest chunk
 
 
 def prefill_plan(chunks, H: int, Hkv: int, device) -> PrefillPlan:
     """Plan of causal prefill attention over chunks [(seq, ctx, length), ...]: every chunk cut
-    into work items of jit_prefill_block_tokens tokens, the items with the most keys first."""
-    bt = int(_lib.lib().jit_prefill_block_tokens(H, Hkv))
+    into row blocks of jit_prefill_block_tokens tokens, each block's keys cut at multiples of
+    jit_prefill_part_keys, one work item per (block, part), the items with the most key steps first."""
+    lib = _lib.lib()
+    bt = int(lib.jit_prefill_block_tokens(H, Hkv))
     if bt <= 0:
         raise _lib.UnsupportedShape(f"prefill attention covers H / Hkv in (1, 2, 4, 8, 16), got {H}/{Hkv}")
-    rows, tab, items = 0, [], []
+    part_keys = int(lib.jit_prefill_part_keys())
+    step = 128
+    part_steps = part_keys // step
+    rows, tab, items, pmax, max_len = 0, [], [], 1, 0
     for c, (seq, ctx, length) in enumerate(chunks):
         if seq < 0 or ctx < 0 or length < 1:
             raise ValueError(f"chunk {c}: seq {seq}, ctx {ctx}, length {length}")
         tab.append((seq, ctx, length, rows))
         rows += length
-        items += [(ctx + min(q0 + bt, length), c, q0) for q0 in range(0, length, bt)]
-    items.sort(key=lambda it: -it[0])
+        max_len = max(max_len, length)
+        pmax = max(pmax, (ctx + length - 1) // part_keys + 1)
+        for q0 in range(0, length, bt):
+            keys = ctx + min(q0 + bt, length)
+            nst = (keys + step - 1) // step
+            for p in range((nst - 1) // part_steps + 1):
+                items.append((min(nst, (p + 1) * part_steps) - p * part_steps, keys, c, q0, p))
+    items.sort(key=lambda it: (-it[0], -it[1]))
     tables = torch.tensor(np.array(tab, np.int32).T.copy() if tab else np.zeros((4, 0), np.int32), device=device)
-    blocks = torch.tensor(np.array([(c, q0) for _, c, q0 in items], np.int32).T.copy() if items
-                          else np.zeros((2, 0), np.int32), device=device)
-    return PrefillPlan(list(chunks), tables.contiguous(), blocks.contiguous(), rows)
+    blocks = torch.tensor(np.array([it[2:] for it in items], np.int32).T.copy() if items
+                          else np.zeros((3, 0), np.int32), device=device)
+    return PrefillPlan(list(chunks), tables.contiguous(), blocks.contiguous(), rows, pmax, max_len)
+
+
+def prefill_workspace_bytes(plan: PrefillPlan, H: int) -> int:
+    return int(_lib.lib().jit_prefill_workspace_bytes(plan.rows, plan.pmax, H))
 
 
 def paged_prefill_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor, plan: PrefillPlan,
-                            scale: float) -> torch.Tensor:
+                            scale: float, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """q [T, H, 128] bf16 (the plan's chunk rows) -> out [T, H, 128]: causal attention of each chunk
-    token over its sequence's keys up to its own position (jit_paged_prefill_attn)."""
+    token over its sequence's keys up to its own position (jit_paged_prefill_attn); tokens of
+    several key parts go through a workspace of prefill_workspace_bytes (allocated when not given)."""
     _need(q, torch.bfloat16, "q")
     _need(pool, torch.bfloat16, "pool")
     _need(page_table, torch.int32, "page_table")
@@ -553,12 +571,16 @@ def paged_prefill_attention(q: torch.Tensor, pool: torch.Tensor, page_table: tor
     for seq, ctx, length in plan.chunks:
         if seq >= page_table.shape[0] or (ctx + length + PAGE - 1) // PAGE > page_table.shape[1]:
             raise ValueError(f"chunk ({seq}, {ctx}, {length}) is outside page_table {tuple(page_table.shape)}")
+    need = prefill_workspace_bytes(plan, H)
+    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     out = torch.empty_like(q)
     tb, bl = plan.tables, plan.blocks
     _lib.check(
         _lib.lib().jit_paged_prefill_attn(
             _p(q), _p(pool), _p(page_table), page_table.shape[1], _p(tb[0]), _p(tb[1]), _p(tb[2]), _p(tb[3]),
-            tb.shape[1], _p(bl[0]), _p(bl[1]), bl.shape[1], H, Hkv, float(scale), _p(out), _stream(),
+            tb.shape[1], _p(bl[0]), _p(bl[1]), _p(bl[2]), bl.shape[1], plan.pmax, plan.max_len, H, Hkv,
+            float(scale), _p(workspace) if need > 0 else None, _p(out), _stream(),
         ),
         "paged_prefill_attn",
     )

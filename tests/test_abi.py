@@ -49,15 +49,24 @@ def test_contract_breaks_return_einval_before_launch():
     assert lib.jit_paged_decode_attn(None, None, None, 4, None, None, None, 2, 30, 4, 0.1, 4, None, None, None) == _lib.JIT_EINVAL
     assert lib.jit_paged_decode_attn(None, None, None, 4, None, None, None, 2, 64, 2, 0.1, 4, None, None, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_prefill_block_tokens(32, 4) == 32 and lib.jit_prefill_block_tokens(24, 8) == -1
-    assert lib.jit_paged_prefill_attn(*([None] * 3), 16, *([None] * 4), 1, None, None, 1, 32, 3, 0.1, None,
-                                      None) == _lib.JIT_EINVAL
-    assert lib.jit_paged_prefill_attn(*([None] * 3), 16, *([None] * 4), 1, None, None, 1, 24, 8, 0.1, None,
-                                      None) == _lib.JIT_EUNSUPPORTED
+    assert lib.jit_paged_prefill_attn(*([None] * 3), 16, *([None] * 4), 1, None, None, None, 1, 1, 1, 32, 3, 0.1,
+                                      None, None, None) == _lib.JIT_EINVAL
+    assert lib.jit_paged_prefill_attn(*([None] * 3), 16, *([None] * 4), 1, None, None, None, 1, 1, 1, 24, 8, 0.1,
+                                      None, None, None) == _lib.JIT_EUNSUPPORTED
+    # key parts: 48 steps of 128 keys; partials of 132 floats per (token, part, head); none for one part
+    assert lib.jit_prefill_part_keys() == 6144
+    assert lib.jit_prefill_workspace_bytes(10, 2, 32) == 10 * 2 * 32 * 132 * 4
+    assert lib.jit_prefill_workspace_bytes(10, 1, 32) == 0 and lib.jit_prefill_workspace_bytes(10, 0, 32) == -1
+    assert lib.jit_paged_prefill_attn(*([None] * 3), 16, *([None] * 4), 1, None, None, None, 1, 0, 1, 32, 4, 0.1,
+                                      None, None, None) == _lib.JIT_EINVAL  # pmax < 1
     assert lib.jit_qmm_seg(None, 4, 2048, None, 128, None, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_moe_combine_rmsnorm(None, None, None, 2, 8, 4096, None, None, None, 1e-6, None, None) == _lib.JIT_EUNSUPPORTED
     assert lib.jit_sample_rows(None, 2, 0, 1.0, 0.9, 5, None, None, None) == _lib.JIT_EINVAL
     assert lib.jit_sample_rows(None, 2, (1 << 19) + 1, 1.0, 0.9, 5, None, None, None) == _lib.JIT_EUNSUPPORTED
     dummy = ctypes.c_void_p(16)  # (never dereferenced: every call below returns before a launch)
+    # tokens of two key parts need the partials' workspace
+    assert lib.jit_paged_prefill_attn(dummy, dummy, dummy, 16, dummy, dummy, dummy, dummy, 1, dummy, dummy, dummy, 1,
+                                      2, 1, 32, 4, 0.1, None, dummy, None) == _lib.JIT_EINVAL
     assert lib.jit_sample_rows(dummy, 2, 64, 1.0, 0.9, -1, dummy, dummy, None) == _lib.JIT_EINVAL
     assert lib.jit_sample_rows(dummy, 2, 64, float("nan"), 0.9, 5, dummy, dummy, None) == _lib.JIT_EINVAL
     assert lib.jit_sample_rows(dummy, 2, 64, 1.0, 0.9, 5, None, dummy, None) == _lib.JIT_EINVAL

@@ -72,6 +72,42 @@ def test_prefill_token_result_is_independent_of_the_chunking():
     assert np.array_equal(single[0], whole[57])
 
 
+def test_prefill_key_parts_keep_results_independent_of_the_chunking():
+    """Keys are cut into parts at multiples of jit_prefill_part_keys (6,144): tokens past a cut are
+    merged from per-part partials.  The cuts sit at key positions, so a token's bits still do not
+    depend on the chunking: positions 6,100 .. 6,229 (around the first cut) as one chunk, as two
+    chunks split at the cut and off it, and as one-token chunks agree; and the oracle agrees."""
+    assert int(ops._lib.lib().jit_prefill_part_keys()) == 6144
+    pool, table = _pool([6230], seed=81)
+    q = normal_bf16((130, 32, 128), seed=82)
+    whole = _run(q, pool, table, [(0, 6100, 130)])
+    assert np.array_equal(whole, _run(q, pool, table, [(0, 6100, 44), (0, 6144, 86)]))
+    assert np.array_equal(whole, _run(q, pool, table, [(0, 6100, 71), (0, 6171, 59)]))
+    for i in (0, 43, 44, 45, 129):
+        assert np.array_equal(_run(q[i:i + 1], pool, table, [(0, 6100 + i, 1)])[0], whole[i]), i
+    sel = np.r_[40:48, 120:130]
+    want, exact = oracle.paged_decode_attn(q[sel], pool, table[np.zeros(sel.size, int)], 6100 + sel + 1, SCALE,
+                                           exact=True)
+    assert_attention_parity(whole[sel], exact, what="prefill across the first key cut")
+    assert_close_bf16(whole[sel], want, what="prefill across the first key cut")
+
+
+def test_prefill_three_key_parts_and_a_mixed_plan():
+    """Tokens of three key parts (past 12,288) beside a chunk of one part in the same launch."""
+    chunks = [(0, 12270, 40), (1, 30, 50)]
+    pool, table = _pool([12310, 80], seed=91)
+    q = normal_bf16((90, 32, 128), seed=92)
+    plan = ops.prefill_plan(chunks, 32, 4, DEV)
+    assert plan.pmax == 3
+    got = _run(q, pool, table, chunks)
+    sel = np.r_[0:4, 16:22, 36:40, 40:44, 86:90]
+    seqs = np.where(sel < 40, 0, 1)
+    lens = np.where(sel < 40, 12270 + sel + 1, 30 + (sel - 40) + 1)
+    want, exact = oracle.paged_decode_attn(q[sel], pool, table[seqs], lens.astype(np.int32), SCALE, exact=True)
+    assert_attention_parity(got[sel], exact, what="prefill of three key parts")
+    assert_close_bf16(got[sel], want, what="prefill of three key parts")
+
+
 def test_prefill_one_token_matches_decode_attention():
     """A one-token chunk at position p is decode attention over p + 1 keys (both within the
     tolerance of the same oracle row, and close to each other)."""
