@@ -311,6 +311,15 @@ __global__ __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(2, 
       tiles(p, 1, bw1, [&](int t) { dequant_word_at(p + 1, 0, t >> 1, t & 1, bw0); });
     }
 
+    // SwiGLU's sigmoid by table (qtile::swiglu_bf16_tab, exhaustively equal to the bf16 steps): every
+    // wave is done with the stages, so the table (7.7 KB) takes the start of the LDS, one entry
+    // or so a thread instead of ~45 instructions for each of a lane's ~40 outputs
+    const uint16_t *sig_tab = (const uint16_t *)seg_lds;
+    if constexpr (SWIGLU) {
+      __syncthreads();
+      for (int i = tid; i < qtile::kSigEntries; i += kSegThreads) ((uint16_t *)seg_lds)[i] = qtile::sigmoid_entry(i);
+      __syncthreads();
+    }
     // lane l holds C[token 16 t + 4 lg + i][row 16 rbk[r] + lr].  No branch per token: the
     // stores go through a buffer resource (the launch checks that the output spans less than
     // 2 GiB), and a token past the chunk gets an offset past its range, whose store is dropped.
@@ -325,7 +334,7 @@ __global__ __launch_bounds__(kSegThreads) __attribute__((amdgpu_waves_per_eu(2, 
         const int tok = 16 * t + 4 * lg + i;
         const uint32_t ro = tok < nt ? (uint32_t)(off + c0 + tok) * (uint32_t)a.N * 2u : 0x80000000u;
         if (SWIGLU) {
-          __builtin_amdgcn_raw_buffer_store_b16((unsigned short)qtile::swiglu_bf16(acc[t][0][i], acc[t][1][i]), obuf,
+          __builtin_amdgcn_raw_buffer_store_b16((unsigned short)qtile::swiglu_bf16_tab(acc[t][0][i], acc[t][1][i], sig_tab), obuf,
                                                 (int)(ro + 2u * (16 * rbk[0] + lr)), 0, 0);
         } else {
 #pragma unroll

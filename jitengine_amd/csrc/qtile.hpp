@@ -180,4 +180,31 @@ __device__ __forceinline__ uint32_t swiglu_bf16(float gacc, float uacc) {
   return f2bf(sl * u);
 }
 
+// sigmoid_bf16 as a table over the bf16 bits of g, for kernels with many SwiGLU outputs per lane
+// (the segment GEMM's epilogue: ~40 a lane, each ~45 instructions by the steps above).  The
+// function is constant outside 2^-8 <= |g| < 2^7: below, bf16(e^|g|) = 1 (e^|g| < 1 + 2^-8, the
+// rounding midpoint), so d = 2 and the result is 0.5 on both sides; from 2^7 on, e^|g| overflows
+// (exp_pos(x > 89) = inf), y = 0 and the result is 0 for g < 0 and 1 otherwise (a NaN g lands here
+// too and keeps a NaN product below).  Entry 2 i + s: sign s and magnitude index i -- 0 for the
+// small ones, 1 + (bits - 0x3B80) for the 1,920 bf16 magnitudes of the middle, 1,921 for the large
+// ones -- as bf16 bits; the table is exhaustively equal to sigmoid_bf16.
+constexpr int kSigLo = 0x3B80, kSigMid = 0x4300 - 0x3B80;
+constexpr int kSigEntries = 2 * (kSigMid + 2);
+__device__ __forceinline__ uint16_t sigmoid_entry(int e) {
+  const int i = e >> 1, sgn = e & 1;
+  if (i == 0) return 0x3F00;                     // 0.5
+  if (i == kSigMid + 1) return sgn ? 0 : 0x3F80;  // 0 or 1
+  const float g = __uint_as_float((uint32_t)((sgn << 15) | (kSigLo + i - 1)) << 16);
+  return (uint16_t)(__float_as_uint(sigmoid_bf16(g)) >> 16);
+}
+__device__ __forceinline__ uint32_t swiglu_bf16_tab(float gacc, float uacc, const uint16_t *tab) {
+#pragma clang fp contract(off)
+  const float g = rne_bf16(gacc), u = rne_bf16(uacc);
+  const uint32_t b = __float_as_uint(g) >> 16;
+  const int i = min(max((int)(b & 0x7fffu) - kSigLo, -1), kSigMid) + 1;
+  const float sig = __uint_as_float((uint32_t)tab[2 * i + (int)(b >> 15)] << 16);
+  const float sl = rne_bf16(g * sig);
+  return f2bf(sl * u);
+}
+
 }  // namespace qtile
