@@ -1025,7 +1025,7 @@ OP_KERNELS = {  # the kernels one op launches (rocprofv3 kernel names contain th
     "gate_up_swiglu_seg": ["seg_kernel<true, false,"],  # (any token-chunk length)
     "down_seg": ["seg_kernel<false, false,"],
     "qkv_proj_seg": ["seg_kernel<false, true, 10>"],  # (config 3's 2,108 rows: the 10-tile chunk; o_proj takes 5)
-    "prefill_attention": ["prefill_attn_kernel"],
+    "prefill_attention": ["prefill_attn_kernel", "prefill_merge_kernel"],
 }
 
 
