@@ -54,7 +54,10 @@ constexpr int kAttnHeadsPerBlock = JIT_ATTN_HB;  // kv heads per workgroup
 // sequence still fills the chip in one even wave of workgroups (262,144 keys: 128 chunks of
 // 2048, 100 us a layer against 116 us for 171 chunks of 1536).  A wave's run stays at most
 // 64 pages (one page id per lane), hence the cap.
-constexpr int kLongChunks = 128;
+#ifndef JIT_ATTN_LONG_CHUNKS
+#define JIT_ATTN_LONG_CHUNKS 128
+#endif
+constexpr int kLongChunks = JIT_ATTN_LONG_CHUNKS;
 constexpr int kChunkMax = 64 * kPage * kAttnSplits;
 static_assert(kChunk % (32 * kAttnSplits) == 0 && kChunk <= kChunkMax, "a wave's run is whole 32-key steps");
 
