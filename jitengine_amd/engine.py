@@ -306,7 +306,7 @@ class Engine:
         seq_table = self.pool.page_table_host([r.rid])
         ms = make_mixed_state(lm.cfg, [(0, c, n)], seq_table, np.zeros(0, np.int32),
                               np.zeros((0, seq_table.shape[1]), np.int32), dev)
-        x = lm.embed_tokens(torch.tensor(r.prompt[c:c + n], dtype=torch.int32, device=dev))
+        x = lm.embed_tokens(ops.upload(np.asarray(r.prompt[c:c + n], np.int32), dev))
         for layer, pool in zip(lm.layers, self.pool.pools):
             x = layer.mixed(x, pool, ms)
         if c + n < len(r.prompt):

@@ -94,8 +94,8 @@ class KVPool:
         """Device copy of pages src[i] -> dst[i] in every layer."""
         if not src or not self.pools:
             return
-        s = torch.tensor(src, dtype=torch.int32, device=self.device)
-        d = torch.tensor(dst, dtype=torch.int32, device=self.device)
+        s = ops.upload(np.asarray(src, np.int32), self.device)
+        d = ops.upload(np.asarray(dst, np.int32), self.device)
         for pool in self.pools:
             ops.kv_copy_pages(pool, s, d)
 

@@ -127,9 +127,10 @@ def make_mixed_state(cfg: MoEConfig, chunks, seq_table_host, dec_pos_host, dec_t
                                  dec_table_host]).astype(np.int32)
     dplan = ops.attn_plan(dec_pos + 1, device)
     ws = torch.empty(max(ops.attn_workspace_bytes(dplan.total, cfg.heads), 4), dtype=torch.uint8, device=device)
-    return MixedState(P, torch.from_numpy(pos_rows).to(device), torch.from_numpy(table_rows).to(device),
-                      torch.from_numpy(seq_table_host).to(device), ops.prefill_plan(chunks, cfg.heads, cfg.kv_heads, device),
-                      torch.from_numpy(dec_table_host).to(device), dplan, ws)
+    # (pinned, asynchronous uploads: the host does not wait for the steps still queued)
+    return MixedState(P, ops.upload(pos_rows, device), ops.upload(table_rows, device),
+                      ops.upload(seq_table_host, device), ops.prefill_plan(chunks, cfg.heads, cfg.kv_heads, device),
+                      ops.upload(dec_table_host, device), dplan, ws)
 
 
 class DecoderLayer:

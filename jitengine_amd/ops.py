@@ -544,9 +544,9 @@ def prefill_plan(chunks, H: int, Hkv: int, device) -> PrefillPlan:
             for p in range((nst - 1) // part_steps + 1):
                 items.append((min(nst, (p + 1) * part_steps) - p * part_steps, keys, c, q0, p))
     items.sort(key=lambda it: (-it[0], -it[1]))
-    tables = torch.tensor(np.array(tab, np.int32).T.copy() if tab else np.zeros((4, 0), np.int32), device=device)
-    blocks = torch.tensor(np.array([it[2:] for it in items], np.int32).T.copy() if items
-                          else np.zeros((3, 0), np.int32), device=device)
+    tables = upload(np.array(tab, np.int32).T.copy() if tab else np.zeros((4, 0), np.int32), device)
+    blocks = upload(np.array([it[2:] for it in items], np.int32).T.copy() if items
+                    else np.zeros((3, 0), np.int32), device)
     return PrefillPlan(list(chunks), tables.contiguous(), blocks.contiguous(), rows, pmax, max_len)
 
 
