@@ -100,28 +100,82 @@ def _norm_and_attention(dev) -> None:
     xf = x.float()
     _close("rmsnorm", ops.rmsnorm(x, wn, 1e-6), xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6) * wn.float())
     H, Hkv, lens = 8, 2, [5, 40, 1600]
-    npg = [-(-L // ops.PAGE) for L in lens]
-    pool = torch.randn((sum(npg) + 1, Hkv, 2, ops.PAGE * ops.HEAD_DIM), generator=g, device=dev).to(torch.bfloat16)
-    perm = torch.randperm(sum(npg), device=dev).to(torch.int32)
-    table = torch.zeros((len(lens), max(npg)), dtype=torch.int32, device=dev)
-    at = 0
-    for b, n in enumerate(npg):
-        table[b, :n] = perm[at:at + n]
-        at += n
+    pool, table, npg, K, V = _paged_kv(g, dev, lens, Hkv)
     q = torch.randn((len(lens), H, ops.HEAD_DIM), generator=g, device=dev).to(torch.bfloat16)
     out = ops.paged_decode_attention(q, pool, table, ops.attn_plan(lens, dev), ops.HEAD_DIM ** -0.5)
-    pf = pool.float()
-    K = pf[:, :, 0].reshape(-1, Hkv, 4, ops.PAGE, 32).permute(0, 1, 3, 2, 4).reshape(-1, Hkv, ops.PAGE, ops.HEAD_DIM)
-    V = pf[:, :, 1].reshape(-1, Hkv, ops.HEAD_DIM, ops.PAGE).transpose(2, 3)
     want = torch.empty((len(lens), H, ops.HEAD_DIM), device=dev)
     for b, L in enumerate(lens):
-        pages = table[b, :npg[b]].long()
-        kb = K[pages].permute(1, 0, 2, 3).reshape(Hkv, -1, ops.HEAD_DIM)[:, :L]
-        vb = V[pages].permute(1, 0, 2, 3).reshape(Hkv, -1, ops.HEAD_DIM)[:, :L]
+        kb, vb = _keys_of(K, V, table, npg, b, L, Hkv)
         qb = q[b].float().reshape(Hkv, H // Hkv, ops.HEAD_DIM)
         p = torch.softmax(qb @ kb.transpose(1, 2) * ops.HEAD_DIM ** -0.5, dim=-1)
         want[b] = (p @ vb).reshape(H, ops.HEAD_DIM)
     _close("paged decode attention", out, want)
+
+
+def _paged_kv(g, dev, keys, Hkv):
+    """A pool holding each sequence's keys in permuted pages, its table, and the K and V views
+    [pages, Hkv, 16, 128] (fp32) of its two parts (K chunk-major, V dim-major)."""
+    npg = [-(-n // ops.PAGE) for n in keys]
+    pool = torch.randn((sum(npg) + 1, Hkv, 2, ops.PAGE * ops.HEAD_DIM), generator=g, device=dev).to(torch.bfloat16)
+    perm = torch.randperm(sum(npg), device=dev).to(torch.int32)
+    table = torch.zeros((len(keys), max(npg)), dtype=torch.int32, device=dev)
+    at = 0
+    for b, n in enumerate(npg):
+        table[b, :n] = perm[at:at + n]
+        at += n
+    pf = pool.float()
+    K = pf[:, :, 0].reshape(-1, Hkv, 4, ops.PAGE, 32).permute(0, 1, 3, 2, 4).reshape(-1, Hkv, ops.PAGE, ops.HEAD_DIM)
+    V = pf[:, :, 1].reshape(-1, Hkv, ops.HEAD_DIM, ops.PAGE).transpose(2, 3)
+    return pool, table, npg, K, V
+
+
+def _keys_of(K, V, table, npg, b, L, Hkv):
+    pages = table[b, :npg[b]].long()
+    kb = K[pages].permute(1, 0, 2, 3).reshape(Hkv, -1, ops.HEAD_DIM)[:, :L]
+    vb = V[pages].permute(1, 0, 2, 3).reshape(Hkv, -1, ops.HEAD_DIM)[:, :L]
+    return kb, vb
+
+
+def _prefill(dev) -> None:
+    """Causal prefill attention of two chunks, one across the first key cut (partials and merge)."""
+    g = torch.Generator(device=dev).manual_seed(7)
+    H, Hkv, cut = 8, 2, int(ops._lib.lib().jit_prefill_part_keys())
+    chunks = [(0, 0, 20), (1, cut - 10, 24)]
+    pool, table, npg, K, V = _paged_kv(g, dev, [ctx + n for _, ctx, n in chunks], Hkv)
+    T = sum(n for *_, n in chunks)
+    q = torch.randn((T, H, ops.HEAD_DIM), generator=g, device=dev).to(torch.bfloat16)
+    scale = ops.HEAD_DIM ** -0.5
+    out = ops.paged_prefill_attention(q, pool, table, ops.prefill_plan(chunks, H, Hkv, dev), scale)
+    want = torch.empty((T, H, ops.HEAD_DIM), device=dev)
+    row = 0
+    for seq, ctx, n in chunks:
+        kb, vb = _keys_of(K, V, table, npg, seq, ctx + n, Hkv)
+        qb = q[row:row + n].float().reshape(n, Hkv, H // Hkv, ops.HEAD_DIM).permute(1, 0, 2, 3)
+        s = torch.einsum("hngd,hkd->hngk", qb, kb) * scale
+        pos = ctx + torch.arange(n, device=dev)
+        s = s.masked_fill(torch.arange(ctx + n, device=dev)[None, None, None, :] > pos[None, :, None, None], -torch.inf)
+        o = torch.einsum("hngk,hkd->hngd", torch.softmax(s, dim=-1), vb)
+        want[row:row + n] = o.permute(1, 0, 2, 3).reshape(n, H, ops.HEAD_DIM)
+        row += n
+    _close("paged prefill attention", out, want)
+
+
+def _segment(dev) -> None:
+    """The segment GEMMs of long expert segments (bf16 weights, bf16(s q + b)) with SwiGLU."""
+    g = torch.Generator(device=dev).manual_seed(8)
+    E, D, I, k, B = 8, 512, 256, 2, 48
+    gu, dn = random_quantized((E, 2 * I, D), 9, device=dev), random_quantized((E, D, I), 10, device=dev)
+    inds = torch.stack([torch.randperm(E, device=dev)[:k] for _ in range(B)]).to(torch.int32)
+    pk = ops.moe_pack(inds, E)
+    xe = torch.randn((B, D), generator=g, device=dev).to(torch.bfloat16)
+    h = ops.expert_gate_up(xe, ops.prepack(gu), pk, seg=True)
+    wgu = dequantize4(gu).to(torch.bfloat16).float()
+    wdn = dequantize4(dn).to(torch.bfloat16).float()
+    e_of = inds.reshape(-1)[pk.order.long()].long()
+    gu_out = torch.einsum("pk,pnk->pn", xe[pk.pair_row.long()].float(), wgu[e_of])
+    _close("segment gate_up + SwiGLU", h, torch.nn.functional.silu(gu_out[:, :I]) * gu_out[:, I:])
+    r = ops.expert_down(h, ops.prepack(dn), pk, seg=True)
+    _close("segment down", r, torch.einsum("pk,pnk->pn", h.float(), wdn[e_of]))
 
 
 def _sampler(dev) -> None:
@@ -131,7 +185,8 @@ def _sampler(dev) -> None:
 
 
 CASES = (("router + packing", _router_and_pack), ("projections + experts", _projections),
-         ("rmsnorm + attention", _norm_and_attention), ("sampler", _sampler))
+         ("rmsnorm + attention", _norm_and_attention), ("prefill attention", _prefill),
+         ("segment GEMMs", _segment), ("sampler", _sampler))
 
 
 def run(device=None, force: bool = False) -> list:
