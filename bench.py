@@ -501,11 +501,11 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
     per_layer = {
         "rmsnorm": lambda l: ops.rmsnorm(dbg[l]["x"], L_[l].input_norm, cfg.eps),
         "qkv_proj": lambda l: ops.qmm(dbg[l]["xn"], L_[l].qkv),
-        "qk_norm_rope_append": lambda l: ops.qk_norm_rope_append(
-            dbg[l]["qkv"], cfg.heads, cfg.kv_heads, L_[l].q_norm, L_[l].k_norm, cfg.eps, L_[l].inv_freq, st.pos,
-            st.page_table, pools[l]),
-        "paged_attention": lambda l: ops.paged_decode_attention(
-            dbg[l]["q"], pools[l], st.page_table, st.plan, cfg.head_dim ** -0.5, st.workspace),
+        # (the step's attention launch norms, rotates and appends the token itself: the fused entry; its
+        # append rewrites the same slot with the same bits)
+        "paged_attention": lambda l: ops.paged_decode_attention_qkv(
+            dbg[l]["qkv"], cfg.heads, cfg.kv_heads, L_[l].q_norm, L_[l].k_norm, cfg.eps, L_[l].inv_freq, pools[l],
+            st.page_table, st.plan, cfg.head_dim ** -0.5, st.workspace),
         "o_proj": lambda l: ops.qmm(dbg[l]["attn"].view(B, -1), L_[l].o),
         "add_rmsnorm": lambda l: ops.rmsnorm(dbg[l]["o"], L_[l].post_norm, cfg.eps, resid=dbg[l]["x"],
                                              return_sum=True),

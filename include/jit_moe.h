@@ -300,6 +300,20 @@ int jit_paged_decode_attn(const uint16_t *q, const uint16_t *pool, const int32_t
                           const int32_t *chunk_seq, int B, int H, int Hkv, float scale,
                           int total_chunks, void *workspace, uint16_t *out, void *stream);
 
+/* jit_paged_decode_attn fused with the step's own token's jit_qk_norm_rope_append: qkv holds
+ * the step's raw rows [B, (H + 2 Hkv) * 128] (the qkv projection's output) instead of q.  Row b's
+ * token sits at position lens[b] - 1: its q heads are normed and rotated inside the attention
+ * kernel, and its K (normed, rotated) and V are written into the pool at that position through
+ * page_table row b before any read of that slot -- the bits of jit_qk_norm_rope_append followed
+ * by jit_paged_decode_attn, one launch fewer.  Replaces the same reference calls as the two
+ * (Q36/model/attention.py:99-119, Q36/kvcache/kv_cache.py:27-85, Q36/kernels/sdpa_decode.py:448-476).
+ * inv_freq [64] fp32; q_norm_w, k_norm_w [128] bf16.  Contract as jit_paged_decode_attn. */
+int jit_paged_decode_attn_qkv(const uint16_t *qkv, const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                              float eps, const float *inv_freq, uint16_t *pool, const int32_t *page_table,
+                              int max_pages, const int32_t *lens, const int32_t *chunk_start,
+                              const int32_t *chunk_seq, int B, int H, int Hkv, float scale,
+                              int total_chunks, void *workspace, uint16_t *out, void *stream);
+
 /* jit_paged_decode_attn without a workspace argument: the same kernels and the same bits,
  * with the fp32 split-K partials in a file-scope device array of JIT_ATTN_SCRATCH_BYTES
  * (16 MiB) that each GPU holds from the library's first call on it until the process ends.

@@ -52,6 +52,7 @@ _SIGNATURES = {
     "jit_attn_plan": [_P, _I, _P, _P, _I],
     "jit_attn_workspace_bytes": [_I, _I],
     "jit_paged_decode_attn": [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P, _P],
+    "jit_paged_decode_attn_qkv": [_P, _P, _P, _F, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P, _P],
     "jit_paged_decode_attn_noalloc": [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _F, _I, _P, _P],
     "jit_prefill_block_tokens": [_I, _I],
     "jit_paged_prefill_attn": [_P, _P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P],

@@ -111,6 +111,12 @@ struct AttnArgs {
   int hb;          // kv heads per workgroup (a kernel argument: blockDim.x lives in the implicit
                    // arguments, whose 16-bit fields the kernel would fetch with a vector load and
                    // wait for before anything else)
+  // jit_paged_decode_attn_qkv: the step's raw q/k/v rows [B, (H + 2 Hkv) * 128] instead of q, the
+  // q and k norm weights, RoPE's inverse frequencies and the norm's eps (null qkv: q as given)
+  const uint16_t *qkv;
+  const uint16_t *qn_w, *kn_w;
+  const float *inv_freq;
+  float eps;
 };
 
 // xor-16 / xor-32 lane exchanges, one VALU op each (gfx950 permlane swaps): with both
@@ -231,15 +237,71 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
   // masked, so prefetches need no branch)
   auto page = [&](int i) { return __builtin_amdgcn_readlane(my_page, min(i, last)); };
 
+  Frag8 kf[2][4];
+  uint2 vv[2][8];
+  // K before V, as in the loop, so a step's K wait leaves its V loads in flight
+  auto first_loads = [&]() {
+    if (nst > 0) {
+      load_k2(kf, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
+      asm volatile("" ::: "memory");
+      load_v2(vv, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
+    }
+  };
   // Q^T fragments (B operand of S^T = K . Q^T): q head lr, dims 8*lg.. of each chunk
   Frag8 qf[4];
-  if (lr < G) {
-    const uint16_t *qp = a.q + ((long long)b * a.H + kvh * G + lr) * kD + 8 * lg;
 #pragma unroll
-    for (int cc = 0; cc < 4; cc++) qf[cc].q = *(const uint4 *)(qp + 32 * cc);
+  for (int cc = 0; cc < 4; cc++) qf[cc].q = make_uint4(0, 0, 0, 0);
+  if (a.qkv == nullptr) {
+    if (lr < G) {
+      const uint16_t *qp = a.q + ((long long)b * a.H + kvh * G + lr) * kD + 8 * lg;
+#pragma unroll
+      for (int cc = 0; cc < 4; cc++) qf[cc].q = *(const uint4 *)(qp + 32 * cc);
+    }
+    first_loads();
   } else {
+    // The step's own token (position L - 1) from its raw q/k/v row: every workgroup norms and
+    // rotates its q heads (qk_head_norm_rope, as jit_qk_norm_rope_append does: the same bits) into
+    // LDS, and the workgroup of the sequence's last chunk first writes the token's K and V of its
+    // kv heads into the pool.  The barrier's fence orders those stores before this workgroup's
+    // reads of the token's page; other workgroups never read it.  A wave whose first step holds
+    // that page issues its first loads after the barrier, the others before the q work.
+    const int tok = L - 1;
+    const bool defer = wk1 == L && tok < wk0 + 32;
+    if (!defer) first_loads();
+    const int nh = a.H + 2 * a.Hkv;
+    const uint16_t *row = a.qkv + (long long)b * nh * kD;
+    uint16_t *qs = (uint16_t *)(xstate + (WS - 1) * hb * kStateFloats * 64);  // [hb][G][128], past the states
+    if (live) {
+      const float ang = (float)tok * a.inv_freq[l];
+      if (c == nchunks - 1 && split < 2) {
+        const int pg = a.page_table[(long long)b * a.max_pages + (tok >> 4)], slot = tok & (kPage - 1);
+        uint16_t *hp = (uint16_t *)a.pool + ((long long)pg * a.Hkv + kvh) * 2 * kPageHead;
+        if (split == 0) {  // K: normed and rotated, into the chunk-major K part
+          const uint16_t *src = row + (a.H + kvh) * kD;
+          uint32_t o1, o2;
+          qk_head_norm_rope(bf2f(src[l]), bf2f(src[l + 64]), bf2f(a.kn_w[l]), bf2f(a.kn_w[l + 64]), a.eps, ang, o1, o2);
+          hp[k_page_offset(slot, l)] = (uint16_t)o1;
+          hp[k_page_offset(slot, l + 64)] = (uint16_t)o2;
+        } else {  // V: as it is, into the dim-major V part
+          const uint16_t *src = row + (a.H + a.Hkv + kvh) * kD;
+          hp[kPageHead + l * kPage + slot] = src[l];
+          hp[kPageHead + (l + 64) * kPage + slot] = src[l + 64];
+        }
+      }
+      for (int hq = split; hq < G; hq += WS) {  // (uniform over the wave)
+        const uint16_t *src = row + (kvh * G + hq) * kD;
+        uint32_t o1, o2;
+        qk_head_norm_rope(bf2f(src[l]), bf2f(src[l + 64]), bf2f(a.qn_w[l]), bf2f(a.qn_w[l + 64]), a.eps, ang, o1, o2);
+        qs[(kvl * G + hq) * kD + l] = (uint16_t)o1;
+        qs[(kvl * G + hq) * kD + l + 64] = (uint16_t)o2;
+      }
+    }
+    __syncthreads();
+    if (live && lr < G) {
 #pragma unroll
-    for (int cc = 0; cc < 4; cc++) qf[cc].q = make_uint4(0, 0, 0, 0);
+      for (int cc = 0; cc < 4; cc++) qf[cc].q = *(const uint4 *)(qs + (kvl * G + lr) * kD + 8 * lg + 32 * cc);
+    }
+    if (defer) first_loads();
   }
   // Lane (lr, lg) owns q head lr throughout: scores S^T[key 4*lg + i][head lr], the
   // running max / sum of head lr, and O^T[dim 16*cc + 4*lg + i][head lr].
@@ -248,14 +310,6 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
 #pragma unroll
   for (int cc = 0; cc < 8; cc++) o[cc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  Frag8 kf[2][4];
-  uint2 vv[2][8];
-  // K before V, as in the loop, so a step's K wait leaves its V loads in flight
-  if (nst > 0) {
-    load_k2(kf, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
-    asm volatile("" ::: "memory");
-    load_v2(vv, a.pool, a.Hkv, kvh, page(0), page(1), lr, lg);
-  }
 #if JIT_ATTN_STAMPS
   __builtin_amdgcn_s_waitcnt(0);
   asm volatile("" ::: "memory");
@@ -942,17 +996,28 @@ namespace {
 // The two launches of a decode-attention call: the split-K chunks, then the chunk-order merge.
 // `workspace` holds the fp32 partials of multi-chunk sequences (every partial the merge reads
 // is written by the first launch of the same call, so nothing in it has to start at zero).
+// The raw-row inputs of the fused entry (jit_paged_decode_attn_qkv).
+struct FusedQkv {
+  const uint16_t *qkv, *q_norm_w, *k_norm_w;
+  const float *inv_freq;
+  float eps;
+};
+
 int decode_attn_launch(const uint16_t *q, const uint16_t *pool, const int32_t *page_table, int max_pages,
                        const int32_t *lens, const int32_t *chunk_start, const int32_t *chunk_seq, int B, int H,
                        int Hkv, float scale, int total_chunks, void *workspace, uint16_t *out, hipStream_t st,
-                       const char *what) {
+                       const char *what, const FusedQkv *fq = nullptr) {
   float *part_o = (float *)workspace;
   float *part_ml = part_o + (long long)total_chunks * H * kD;
   constexpr int WS = kAttnSplits;
   const int hb = Hkv < kAttnHeadsPerBlock ? Hkv : kAttnHeadsPerBlock;  // kv heads per workgroup (WS waves each)
   AttnArgs a{q, pool, page_table, lens, chunk_start, chunk_seq, part_o, part_ml, out,
-             max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f, hb};
-  const size_t lds = (size_t)(WS - 1) * hb * kStateFloats * 64 * sizeof(float);
+             max_pages, H, Hkv, H / Hkv, scale * 1.44269504088896341f, hb,
+             fq ? fq->qkv : nullptr, fq ? fq->q_norm_w : nullptr, fq ? fq->k_norm_w : nullptr,
+             fq ? fq->inv_freq : nullptr, fq ? fq->eps : 0.0f};
+  // the splits' states, and with fq the staged q heads of the workgroup's kv heads
+  const size_t lds = (size_t)(WS - 1) * hb * kStateFloats * 64 * sizeof(float) +
+                     (fq ? (size_t)hb * (H / Hkv) * kD * sizeof(uint16_t) : 0);
   paged_attn_kernel<WS><<<dim3(total_chunks, (Hkv + hb - 1) / hb), 64 * hb * WS, lds, st>>>(a);
   int rc = jit::check_launch(what);
   if (rc) return rc;
@@ -1016,6 +1081,22 @@ extern "C" int jit_paged_decode_attn(const uint16_t *q, const uint16_t *pool,
     return jit::fail(JIT_EINVAL, "paged_decode_attn: null pointer");
   return decode_attn_launch(q, pool, page_table, max_pages, lens, chunk_start, chunk_seq, B, H, Hkv, scale,
                             total_chunks, workspace, out, (hipStream_t)stream, "jit_paged_decode_attn");
+}
+
+extern "C" int jit_paged_decode_attn_qkv(const uint16_t *qkv, const uint16_t *q_norm_w, const uint16_t *k_norm_w,
+                                         float eps, const float *inv_freq, uint16_t *pool, const int32_t *page_table,
+                                         int max_pages, const int32_t *lens, const int32_t *chunk_start,
+                                         const int32_t *chunk_seq, int B, int H, int Hkv, float scale,
+                                         int total_chunks, void *workspace, uint16_t *out, void *stream) {
+  int rc = decode_attn_contract(B, H, Hkv, max_pages, total_chunks, "paged_decode_attn_qkv");
+  if (rc) return rc;
+  if (B == 0 || total_chunks == 0) return JIT_OK;
+  if (!qkv || !q_norm_w || !k_norm_w || !inv_freq || !pool || !page_table || !lens || !chunk_start || !chunk_seq ||
+      !workspace || !out)
+    return jit::fail(JIT_EINVAL, "paged_decode_attn_qkv: null pointer");
+  const FusedQkv fq{qkv, q_norm_w, k_norm_w, inv_freq, eps};
+  return decode_attn_launch(nullptr, pool, page_table, max_pages, lens, chunk_start, chunk_seq, B, H, Hkv, scale,
+                            total_chunks, workspace, out, (hipStream_t)stream, "jit_paged_decode_attn_qkv", &fq);
 }
 
 extern "C" int jit_paged_decode_attn_noalloc(const uint16_t *q, const uint16_t *pool, const int32_t *page_table,

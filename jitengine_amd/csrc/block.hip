@@ -217,15 +217,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
     return;
   }
   const uint16_t *nw = head < H ? qn_w : kn_w;
-  float ss = fmaf(x1, x1, x2 * x2);
-  ss = wave_butterfly<false>(ss);  // (the pairs of a shuffle butterfly over offsets 32..1)
-  const float r = rsqrtf(ss / (float)kD + eps);
-  x1 = bf2f(f2bf(bf2f(nw[l]) * bf2f(f2bf(x1 * r))));
-  x2 = bf2f(f2bf(bf2f(nw[l + 64]) * bf2f(f2bf(x2 * r))));
-  const float ang = (float)p * inv_freq[l];
-  float sn, cs;
-  sincosf(ang, &sn, &cs);
-  const uint32_t o1 = f2bf(x1 * cs - x2 * sn), o2 = f2bf(x1 * sn + x2 * cs);
+  uint32_t o1, o2;
+  qk_head_norm_rope(x1, x2, bf2f(nw[l]), bf2f(nw[l + 64]), eps, (float)p * inv_freq[l], o1, o2);
   if (head < H) {
     uint16_t *qo = q_out + ((long long)b * H + head) * kD;
     qo[l] = (uint16_t)o1;

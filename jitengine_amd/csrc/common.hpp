@@ -130,6 +130,26 @@ __device__ __forceinline__ int k_page_offset(int slot, int d) {
   return (d >> 5) * (JIT_PAGE_TOKENS * 32) + slot * 32 + (d & 31);
 }
 
+// ------------------------------------------------------------------ q/k norm + RoPE of one head
+// One head of one token, on the 64 lanes of a wave (lane l: dims l and l + 64, RoPE's pairs):
+// RMSNorm over the head's 128 dims with the norm weight (w1, w2 = dims l, l + 64), each step
+// rounded to bf16 as the reference's bf16 arithmetic does, then the rotation by ang = pos *
+// inv_freq[l] (Q36/model/attention.py:99-119).  Every kernel that norms and rotates a head calls
+// this, so their bits agree; the expression is fixed (no contraction).
+__device__ __forceinline__ void qk_head_norm_rope(float x1, float x2, float w1, float w2, float eps, float ang,
+                                                  uint32_t &o1, uint32_t &o2) {
+#pragma clang fp contract(off)
+  float ss = __builtin_fmaf(x1, x1, x2 * x2);
+  ss = wave_butterfly<false>(ss);  // (the pairs of a shuffle butterfly over offsets 32..1)
+  const float r = rsqrtf(ss / 128.0f + eps);
+  x1 = bf2f(f2bf(w1 * bf2f(f2bf(x1 * r))));
+  x2 = bf2f(f2bf(w2 * bf2f(f2bf(x2 * r))));
+  float sn, cs;
+  sincosf(ang, &sn, &cs);
+  o1 = f2bf(x1 * cs - x2 * sn);
+  o2 = f2bf(x1 * sn + x2 * cs);
+}
+
 // ------------------------------------------------------------------ host error plumbing
 namespace jit {
 void set_error(const char *fmt, ...);

@@ -166,9 +166,15 @@ class DecoderLayer:
         # decode rows take the decode kernels at any batch size (seg=False): a row's bits never
         # depend on how many other rows the step carries
         qkv = ops.qmm(xn, self.qkv, seg=False)
-        q = ops.qk_norm_rope_append(qkv, cfg.heads, cfg.kv_heads, self.q_norm, self.k_norm, cfg.eps,
-                                    self.inv_freq, st.pos, st.page_table, pool)
-        attn = ops.paged_decode_attention(q, pool, st.page_table, st.plan, cfg.head_dim ** -0.5, st.workspace)
+        scale = cfg.head_dim ** -0.5
+        if debug is None:  # q/k norm + RoPE + append inside the attention launch (the same bits)
+            q = None
+            attn = ops.paged_decode_attention_qkv(qkv, cfg.heads, cfg.kv_heads, self.q_norm, self.k_norm, cfg.eps,
+                                                  self.inv_freq, pool, st.page_table, st.plan, scale, st.workspace)
+        else:  # the two launches, which also show q
+            q = ops.qk_norm_rope_append(qkv, cfg.heads, cfg.kv_heads, self.q_norm, self.k_norm, cfg.eps,
+                                        self.inv_freq, st.pos, st.page_table, pool)
+            attn = ops.paged_decode_attention(q, pool, st.page_table, st.plan, scale, st.workspace)
         o = ops.qmm(attn.view(B, -1), self.o, seg=False)
         hn, h = ops.rmsnorm(o, self.post_norm, cfg.eps, resid=x, return_sum=True)
         logits = ops.qmm(hn, moe.router, seg=False)

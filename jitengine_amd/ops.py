@@ -619,6 +619,39 @@ def paged_decode_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torc
     return out
 
 
+def paged_decode_attention_qkv(qkv: torch.Tensor, H: int, Hkv: int, q_norm: torch.Tensor, k_norm: torch.Tensor,
+                               eps: float, inv_freq: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor,
+                               plan: AttnPlan, scale: float, workspace: torch.Tensor | None = None):
+    """qkv [B, (H + 2 Hkv) * 128] (the step's raw rows) -> out [B, H, 128]: qk_norm_rope_append of each
+    row's token at position lens[b] - 1 and paged_decode_attention in one launch (the same bits);
+    the token's K and V are written into the pool."""
+    _need(qkv, torch.bfloat16, "qkv")
+    _need(pool, torch.bfloat16, "pool")
+    _need(page_table, torch.int32, "page_table")
+    _need(inv_freq, torch.float32, "inv_freq")
+    B = qkv.shape[0]
+    if qkv.shape[1] != (H + 2 * Hkv) * HEAD_DIM or _pool_heads(pool) != Hkv or inv_freq.numel() != HEAD_DIM // 2:
+        raise ValueError("qkv / pool / inv_freq do not match the head geometry")
+    if plan.lens.shape[0] != B or page_table.shape[0] != B:
+        raise ValueError("qkv, page_table and plan disagree on the number of sequences")
+    if B and int((plan.lens_host.max() + PAGE - 1) // PAGE) > page_table.shape[1]:
+        raise ValueError(f"page_table has {page_table.shape[1]} columns, the longest sequence needs "
+                         f"{int((plan.lens_host.max() + PAGE - 1) // PAGE)}")
+    need = attn_workspace_bytes(plan.total, H)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=qkv.device)
+    out = torch.empty((B, H, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
+    _lib.check(
+        _lib.lib().jit_paged_decode_attn_qkv(
+            _p(qkv), _p(q_norm), _p(k_norm), float(eps), _p(inv_freq), _p(pool), _p(page_table), page_table.shape[1],
+            _p(plan.lens), _p(plan.chunk_start), _p(plan.chunk_seq), B, H, Hkv, float(scale), plan.total,
+            _p(workspace), _p(out), _stream(),
+        ),
+        "paged_decode_attn_qkv",
+    )
+    return out
+
+
 def paged_decode_attention_noalloc(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor,
                                    plan: AttnPlan, scale: float, out: torch.Tensor):
     """paged_decode_attention into a caller-given `out` [B, H, 128] bf16, with the split-K partials in
