@@ -522,6 +522,10 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
     # a step of at most ROUTE_PACK_MAX_ROWS rows routes and packs in one launch, a larger one in two
     for name in (("router_topk", "moe_pack") if B <= ops.ROUTE_PACK_MAX_ROWS else ("route_pack",)):
         del per_layer[name]
+    if B == 1:  # one token routes itself inside the gate||up launch (DecoderLayer.run's choice)
+        del per_layer["route_pack"]
+        per_layer["gate_up_swiglu"] = lambda l: ops.route_gate_up(dbg[l]["hn"], dbg[l]["logits"], L_[l].moe.gate_up,
+                                                                  cfg.top_k, cfg.norm_topk)[3]
     launches = {name: step_layers.get(name, list(range(n_layers))) for name in per_layer}
     launches = {name: ls for name, ls in launches.items() if ls}  # (a one-layer step has no combine_rmsnorm)
     per_layer = {name: f for name, f in per_layer.items() if name in launches}

@@ -166,6 +166,20 @@ int jit_moe_gate_up_swiglu_packed(const uint16_t *x, int K, const int32_t *pair_
                                   const int32_t *expert_cnt, const int32_t *expert_off, int E,
                                   const void *packed, int I, int P, uint16_t *h, void *stream);
 
+/* One token's routing and its gate||up in one launch: jit_route_pack for one row (the top-k of
+ * logits [E] with renormalisation when norm != 0, Q36/kernels/router_topk.py:72-192, and the
+ * packing of its k pairs, Q36/model/moe.py:129-159) followed by jit_moe_gate_up_swiglu_packed of
+ * x [1, K] -- the same bits, one launch fewer.  Every workgroup takes the top-k itself (no
+ * exchange); the launch also writes jit_route_pack's outputs (inds [k], scores [k] and the packing
+ * tables, as for one row) for the down and combine launches that read them.  h [k, I] in sorted
+ * pair order.  Contract: K % 512 == 0, K <= 4096, I % 16 == 0, E % 32 == 0, E <= 128, 0 < k < E,
+ * k <= 64 (JIT_EINVAL / JIT_EUNSUPPORTED). */
+int jit_moe_gate_up_swiglu_routed_packed(const uint16_t *x, int K, const uint16_t *logits, int E, int k,
+                                         int norm, const void *packed, int I, uint16_t *h, uint32_t *inds,
+                                         uint16_t *scores, int32_t *order, int32_t *pair_row, int32_t *inv,
+                                         int32_t *expert_cnt, int32_t *expert_off, int32_t *seg_expert,
+                                         int32_t *seg_start, int32_t *seg_cnt, int32_t *meta, void *stream);
+
 /* Elementwise SwiGLU of bf16 gate and up values: h[i] = bf16(bf16(g[i] * SigmoidX(g[i])) * u[i]),
  * SigmoidX's steps each rounded to bf16 (e = bf16(exp|g|), d = bf16(1 + e), y = bf16(1 / d),
  * g < 0 ? y : bf16(1 - y)) -- exactly the epilogue of jit_moe_gate_up_swiglu* on given operands.

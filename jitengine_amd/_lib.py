@@ -37,6 +37,8 @@ _SIGNATURES = {
     "jit_qmm_packed": [_P, _I, _I, _P, _I, _P, _P],
     "jit_moe_gate_up_swiglu": [_P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _P, _P],
     "jit_moe_gate_up_swiglu_packed": [_P, _I, _P, _P, _P, _I, _P, _I, _I, _P, _P],
+    "jit_moe_gate_up_swiglu_routed_packed": [_P, _I, _P, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                             _P, _P, _P],
     "jit_swiglu": [_P, _P, ctypes.c_int64, _P, _P],
     "jit_moe_down": [_P, _I, _P, _P, _I, _P, _P, _P, _I, _I, _P, _P],
     "jit_moe_down_packed": [_P, _I, _P, _P, _I, _P, _I, _I, _P, _P],

@@ -24,6 +24,7 @@
 // The waves' partial sums meet in LDS and are added in wave order (a fixed
 // order: results do not depend on the batch).
 #include "qtile.hpp"
+#include "route.hpp"
 
 namespace {
 
@@ -40,6 +41,13 @@ struct QmmArgs {
                                    // bytes of tiles (packed layout; g_estride unused)
   int rows_w;                      // weight rows per expert (2N with SWIGLU)
   int E;                           // experts of the stack (the grid may have fewer rows)
+  // ROUTED (a one-token step routing itself): the token's router logits [E], top-k and renorm,
+  // and the packing tables the launch writes for the later launches (down, combine)
+  const uint16_t *logits;
+  int k, norm;
+  uint32_t *inds;
+  uint16_t *scores;
+  int32_t *order, *pair_row, *inv, *t_cnt, *t_off, *seg_expert, *seg_start, *seg_cnt, *meta;
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -102,7 +110,7 @@ __device__ uint64_t g_qmm_stamps[kStampSlots][8];
   } while (0)
 #endif
 
-template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false>
+template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false, bool ROUTED = false>
 __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
 #if JIT_QMM_STAMPS
   uint64_t ts[6] = {__builtin_amdgcn_s_memrealtime(), 0, 0, 0, 0, 0};
@@ -114,8 +122,48 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   const int ksplit = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
   const int lr = l & 15, lg = l >> 4;
+  static_assert(!ROUTED || (COMPACT && TT == 1), "a routed step is one token over the compact grid");
   int e = 0, cnt, off;
-  if (a.cnt && !COMPACT) {
+  if constexpr (ROUTED) {
+    // One token routes itself (the router's top-k on every wave: route::topk_slot_key, the
+    // router kernels' own arithmetic): grid row y takes the y-th smallest of the token's k expert
+    // ids -- the packing's order, one pair each at position y.  Workgroup (0, 0) also writes the
+    // packing tables (jit_route_pack's, for one token) that the later launches read.
+    const uint32_t slot = route::topk_slot_key<2>(a.logits, a.E, a.k, l);  // lane j < k: slot j
+    const int id = (int)(slot & 0xffffu);
+    int rank = 0;  // among the k distinct ids
+    for (int j = 0; j < a.k; j++) rank += __builtin_amdgcn_readlane(id, j) < id ? 1 : 0;
+    const int y = blockIdx.y;
+    const unsigned long long at = __ballot(l < a.k && rank == y);
+    e = __builtin_amdgcn_readlane(id, __ffsll((long long)at) - 1);
+    cnt = 1;
+    off = y;
+    if (blockIdx.x == 0 && y == 0 && wave == 0) {
+      const float tot = route::slots_total(slot, a.k);
+      if (l < a.k) {
+        const float sc = bf2f(route::key_bf16(slot));
+        a.inds[l] = (uint32_t)id;
+        a.scores[l] = (uint16_t)(a.norm ? f2bf(sc / tot) : f2bf(sc));
+        a.inv[l] = rank;
+        a.order[rank] = l;
+        a.pair_row[rank] = 0;
+        a.seg_expert[rank] = id;
+        a.seg_start[rank] = rank;
+        a.seg_cnt[rank] = 1;
+      }
+      for (int x = l; x < a.E; x += 64) {
+        int c = 0, below = 0;
+        for (int j = 0; j < a.k; j++) {
+          const int o = __builtin_amdgcn_readlane(id, j);
+          c += o == x ? 1 : 0;
+          below += o < x ? 1 : 0;
+        }
+        a.t_cnt[x] = c;
+        a.t_off[x] = below;
+      }
+      if (l < 4) a.meta[l] = l == 0 ? a.k : (l == 1 ? 1 : 0);  // segments, largest, bad pairs, 0
+    }
+  } else if (a.cnt && !COMPACT) {
     e = blockIdx.y;
     cnt = a.cnt[e];
     off = a.off[e];
@@ -179,7 +227,8 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   // it); down and the dense projections read their rows in place, with no load and no wait.
   auto row_of = [&](int tok) {
     const int pos = off + (tok < cnt ? tok : 0);
-    if constexpr (SWIGLU) return a.row_index[pos];
+    if constexpr (ROUTED) return 0;  // (the one token's row)
+    else if constexpr (SWIGLU) return a.row_index[pos];
     else return pos;
   };
   // a row as a byte offset into x for the activation loads; a token past the expert's count gets
@@ -411,18 +460,18 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
 #endif
 }
 
-template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false>
+template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false, bool ROUTED = false>
 int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what, int zsplit = 1) {
   constexpr int NBW = SWIGLU ? 2 * NB : NB;
   const int G = a.K / 64;
   const int ksplit = G / GPW;
   if (ksplit * GPW != G || ksplit < 1 || ksplit > 8)
     return jit::fail(JIT_EUNSUPPORTED, "%s: K=%d does not split into %d-group wave slices", what, a.K, GPW);
-  if (SWIGLU != (a.row_index != nullptr))
+  if (SWIGLU != (a.row_index != nullptr || ROUTED))
     return jit::fail(JIT_EINVAL, "%s: a row index goes with the gate||up instances only", what);
   const dim3 grid((a.N + 16 * NB - 1) / (16 * NB), E, zsplit), block(64 * ksplit);
   const size_t lds = (size_t)ksplit * TT * NBW * 4 * 64 * sizeof(float);
-  qmm_kernel<NB, GPW, SWIGLU, PACKED, TT, COMPACT><<<grid, block, lds, st>>>(a);
+  qmm_kernel<NB, GPW, SWIGLU, PACKED, TT, COMPACT, ROUTED><<<grid, block, lds, st>>>(a);
   return jit::check_launch(what);
 }
 
@@ -603,6 +652,31 @@ extern "C" int jit_moe_gate_up_swiglu_packed(const uint16_t *x, int K, const int
             jit_q4_packed_bytes(1, 2 * I, K), 0, 2 * I, E};
   if (P < E) return launch_qmm<1, kGuGpw, true, true, 1, true>(a, P, (hipStream_t)stream, "jit_moe_gate_up_swiglu_packed");
   return launch_qmm<1, kGuGpw, true, true>(a, E, (hipStream_t)stream, "jit_moe_gate_up_swiglu_packed");
+}
+
+// A one-token step routed inside the gate||up launch (jit_route_pack + jit_moe_gate_up_swiglu_packed
+// for one token, one launch): every workgroup takes the token's top-k from its router logits, and
+// the packing tables are written for the down and combine launches that follow.
+extern "C" int jit_moe_gate_up_swiglu_routed_packed(const uint16_t *x, int K, const uint16_t *logits, int E, int k,
+                                                    int norm, const void *packed, int I, uint16_t *h, uint32_t *inds,
+                                                    uint16_t *scores, int32_t *order, int32_t *pair_row, int32_t *inv,
+                                                    int32_t *expert_cnt, int32_t *expert_off, int32_t *seg_expert,
+                                                    int32_t *seg_start, int32_t *seg_cnt, int32_t *meta,
+                                                    void *stream) {
+  if (K <= 0 || I <= 0 || E <= 0 || !(0 < k && k <= E))
+    return jit::fail(JIT_EINVAL, "moe_gate_up_routed: bad dims K=%d I=%d E=%d k=%d", K, I, E, k);
+  if (K % 512 != 0 || K > 4096 || I % 16 != 0 || E % 32 != 0 || E > 128 || k >= E || k > 64)
+    return jit::fail(JIT_EUNSUPPORTED,
+                     "moe_gate_up_routed covers K %% 512 == 0, K <= 4096, I %% 16 == 0, E %% 32 == 0, E <= 128 and "
+                     "k < E, k <= 64, got K=%d I=%d E=%d k=%d", K, I, E, k);
+  if (!x || !logits || !packed || !h || !inds || !scores || !order || !pair_row || !inv || !expert_cnt ||
+      !expert_off || !seg_expert || !seg_start || !seg_cnt || !meta)
+    return jit::fail(JIT_EINVAL, "moe_gate_up_routed: null pointer");
+  QmmArgs a{x, nullptr, nullptr, nullptr, (const uint32_t *)packed, nullptr, nullptr, h, K, I, 0,
+            jit_q4_packed_bytes(1, 2 * I, K), 0, 2 * I, E, logits, k, norm ? 1 : 0, inds, scores, order, pair_row,
+            inv, expert_cnt, expert_off, seg_expert, seg_start, seg_cnt, meta};
+  return launch_qmm<1, kGuGpw, true, true, 1, true, true>(a, k, (hipStream_t)stream,
+                                                          "jit_moe_gate_up_swiglu_routed_packed");
 }
 
 static int down_check(const uint16_t *h, int I, const int32_t *cnt, const int32_t *off, int E, int D, int P,

@@ -9,52 +9,18 @@
 
 #include "common.hpp"
 #include "fmath.hpp"
+#include "route.hpp"
 
 namespace {
 
 using fmath::exp_neg;
+using route::key_bf16;
+using route::order_key;
+using route::row_keys;
+using route::wave_max_u32;
 
 constexpr int kRowsPerBlock = 4;  // one wave64 per token row
 constexpr int kMaxN = 1024;
-
-// Key of a bf16 value in the ascending (value, index) order of the rank rule: the
-// value's bits made monotonic as an unsigned integer (-0 ties +0, as the float
-// comparison does) above a 16-bit index.  Gates must not be NaN.
-__device__ __forceinline__ uint32_t order_key(uint32_t b, int i) {
-  b = b == 0x8000u ? 0u : b;
-  const uint32_t o = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
-  return (o << 16) | (uint32_t)i;
-}
-__device__ __forceinline__ uint32_t key_bf16(uint32_t key) {
-  const uint32_t o = key >> 16;
-  return (o & 0x8000u) ? (o & 0x7fffu) : (~o & 0xffffu);
-}
-
-// Wave maximum with no LDS round trip: DPP quad permutes (lane ^ 1, lane ^ 2), row
-// half-mirror and row mirror (every lane of a 16-lane row then holds the row's
-// maximum), then the permlane swaps across rows.  A maximum needs no fixed pairing,
-// so the mirrors serve where an xor butterfly would.
-__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v, int ctrl) {
-  uint32_t y;
-  switch (ctrl) {  // the DPP control is an immediate
-    case 0: y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false); break;   // [1,0,3,2]
-    case 1: y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false); break;   // [2,3,0,1]
-    case 2: y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false); break;  // half mirror
-    default: y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false); break; // mirror
-  }
-  return y > v ? y : v;
-}
-
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = dpp_max_u32(v, 0);
-  v = dpp_max_u32(v, 1);
-  v = dpp_max_u32(v, 2);
-  v = dpp_max_u32(v, 3);
-  auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  v = r[0] > r[1] ? r[0] : r[1];
-  r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return r[0] > r[1] ? r[0] : r[1];
-}
 
 // One wave per row.  Lane l owns experts l, l+64, ...: it sums their exps in that
 // order, the wave adds the 64 partial sums by a butterfly over offsets 32..1
@@ -71,45 +37,7 @@ __device__ __forceinline__ void topk_row(const uint16_t *__restrict__ lg, int ro
                                          uint32_t *__restrict__ inds, uint16_t *__restrict__ scores,
                                          uint16_t *__restrict__ gates_out, uint32_t *skey, int l) {
   uint32_t key[NPL];
-  if (FROM_GATES) {
-    uint32_t raw[NPL];
-#pragma unroll
-    for (int j = 0; j < NPL; j++) raw[j] = lg[min(l + 64 * j, N - 1)];
-#pragma unroll
-    for (int j = 0; j < NPL; j++) {
-      const int i = l + 64 * j;
-      key[j] = i < N ? order_key(raw[j], i) : 0u;
-    }
-  } else {
-    float v[NPL], e[NPL];
-    float mx = -INFINITY;
-    uint32_t raw[NPL];
-#pragma unroll
-    for (int j = 0; j < NPL; j++) raw[j] = lg[min(l + 64 * j, N - 1)];  // (every load issued before any is used)
-#pragma unroll
-    for (int j = 0; j < NPL; j++) {
-      const int i = l + 64 * j;
-      v[j] = i < N ? bf2f(raw[j]) : -INFINITY;
-      mx = v[j] > mx ? v[j] : mx;
-    }
-    mx = wave_butterfly<true>(mx);
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NPL; j++) {
-      const int i = l + 64 * j;
-      e[j] = (i < N) ? exp_neg(v[j] - mx) : 0.0f;
-      s = s + e[j];
-    }
-    s = wave_butterfly<false>(s);
-    const float inv = 1.0f / s;
-#pragma unroll
-    for (int j = 0; j < NPL; j++) {
-      const int i = l + 64 * j;
-      const uint32_t g = f2bf(e[j] * inv);
-      key[j] = i < N ? order_key(g, i) : 0u;
-      if (gates_out && i < N) gates_out[(size_t)row * N + i] = (uint16_t)g;
-    }
-  }
+  row_keys<NPL, FROM_GATES>(lg, row, N, l, key, gates_out);
   // every valid key is > 0 (its value field is >= 0x007f); a taken key becomes 0
   for (int t = 0; t < k; t++) {
     uint32_t m = key[0];

@@ -178,12 +178,18 @@ class DecoderLayer:
         o = ops.qmm(attn.view(B, -1), self.o, seg=False)
         hn, h = ops.rmsnorm(o, self.post_norm, cfg.eps, resid=x, return_sum=True)
         logits = ops.qmm(hn, moe.router, seg=False)
-        if B <= ops.ROUTE_PACK_MAX_ROWS and moe.num_experts <= 128:  # one launch for a small step
-            inds, scores, pk = ops.route_pack(logits, moe.top_k, moe.norm_topk)
+        E, k = moe.num_experts, moe.top_k
+        if B == 1 and isinstance(moe.gate_up, ops.PackedQ4) and E % 32 == 0 and E <= 128 and k < E and k <= 64:
+            # one token: its top-k and packing inside the gate||up launch (the same bits)
+            inds, scores, pk, hh = ops.route_gate_up(hn, logits, moe.gate_up, k, moe.norm_topk)
+            r = ops.expert_down(hh, moe.down, pk)
         else:
-            inds, scores = ops.router_topk(logits, moe.top_k, moe.norm_topk)
-            pk = ops.moe_pack(inds, moe.num_experts)
-        hh, r = moe.expert_mlp(hn, pk)
+            if B <= ops.ROUTE_PACK_MAX_ROWS and E <= 128:  # one launch for a small step
+                inds, scores, pk = ops.route_pack(logits, k, moe.norm_topk)
+            else:
+                inds, scores = ops.router_topk(logits, k, moe.norm_topk)
+                pk = ops.moe_pack(inds, E)
+            hh, r = moe.expert_mlp(hn, pk)
         if next_norm is None:
             y, xn_next = ops.moe_combine(r, pk, scores, h), None
         else:

@@ -164,6 +164,34 @@ def route_pack(logits: torch.Tensor, k: int, norm: bool):
     return inds, scores, pk
 
 
+def route_gate_up(x: torch.Tensor, logits: torch.Tensor, gate_up, k: int, norm: bool):
+    """One token's route_pack and expert_gate_up in one launch (jit_moe_gate_up_swiglu_routed_packed):
+    x [1, K] bf16, logits [1, E] bf16, a packed [E, 2I, K] stack -> (inds, scores, Packing, h), bit
+    for bit the two launches' results."""
+    _need(x, torch.bfloat16, "x")
+    _need(logits, torch.bfloat16, "logits")
+    _need_packed(gate_up, "route_gate_up")
+    if x.shape[0] != 1 or logits.shape[0] != 1:
+        raise _lib.UnsupportedShape("route_gate_up takes one token")
+    E = logits.shape[1]
+    if E != _experts_of(gate_up) or x.shape[-1] != gate_up.in_dims:
+        raise ValueError("x / logits / stack disagree on K or E")
+    I = gate_up.out_dims // 2
+    inds = torch.empty((1, k), dtype=torch.int32, device=x.device)
+    scores = torch.empty((1, k), dtype=torch.bfloat16, device=x.device)
+    pk = _packing_buffers(k, k, E, x.device)
+    h = torch.empty((k, I), dtype=torch.bfloat16, device=x.device)
+    _lib.check(
+        _lib.lib().jit_moe_gate_up_swiglu_routed_packed(
+            _p(x), x.shape[-1], _p(logits), E, int(k), int(bool(norm)), _p(gate_up.data), I, _p(h), _p(inds),
+            _p(scores), _p(pk.order), _p(pk.pair_row), _p(pk.inv), _p(pk.expert_cnt), _p(pk.expert_off),
+            _p(pk.seg_expert), _p(pk.seg_start), _p(pk.seg_cnt), _p(pk.meta), _stream(),
+        ),
+        "route_gate_up",
+    )
+    return inds, scores, pk, h
+
+
 def _packing_buffers(P: int, k: int, E: int, device) -> Packing:
     buf = torch.empty(3 * P + 5 * E + 4, dtype=torch.int32, device=device)
     parts = torch.split(buf, [P, P, P, E, E, E, E, E, 4])
