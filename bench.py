@@ -526,6 +526,17 @@ def bench_decode(config: int, steps: int, warmup: int, dev: str, graph: bool, n_
         del per_layer["route_pack"]
         per_layer["gate_up_swiglu"] = lambda l: ops.route_gate_up(dbg[l]["hn"], dbg[l]["logits"], L_[l].moe.gate_up,
                                                                   cfg.top_k, cfg.norm_topk)[3]
+        # ... layer l's combine and layer l + 1's input norm run inside that layer's qkv launch, and the
+        # post-attention add + norm inside the router launch (Model.decode_step, DecoderLayer.run)
+        # (the geometry's layers all take the prologues or none does)
+        if all(ops.row_prologue_fits(m, cfg.hidden) for lay in L_ for m in (lay.qkv, lay.moe.router)):
+            step_layers.update(qkv_proj=[0], combine_qkv=list(range(last)), combine_rmsnorm=[])
+            del per_layer["add_rmsnorm"]
+            per_layer["router_proj"] = lambda l: ops.qmm_add_rmsnorm(dbg[l]["o"], dbg[l]["x"], L_[l].post_norm,
+                                                                     cfg.eps, L_[l].moe.router)[0]
+            per_layer["combine_qkv"] = lambda l: ops.qmm_combine_rmsnorm(dbg[l]["r"], dbg[l]["pk"], dbg[l]["scores"],
+                                                                         dbg[l]["h"], L_[l + 1].input_norm, cfg.eps,
+                                                                         L_[l + 1].qkv)[1]
     launches = {name: step_layers.get(name, list(range(n_layers))) for name in per_layer}
     launches = {name: ls for name, ls in launches.items() if ls}  # (a one-layer step has no combine_rmsnorm)
     per_layer = {name: f for name, f in per_layer.items() if name in launches}

@@ -253,6 +253,28 @@ int jit_moe_combine_rmsnorm(const uint16_t *r, const int32_t *inv, const uint16_
 int jit_rmsnorm(const uint16_t *x, const uint16_t *resid, int rows, int D, const uint16_t *w,
                 float eps, uint16_t *h_out, uint16_t *y, void *stream);
 
+/* One row's residual add and RMSNorm in front of a packed projection, in one launch
+ * (jit_rmsnorm with resid followed by jit_qmm_packed of its output, for a one-token step; the
+ * post-attention norm and the router projection, Q36/model/model.py:65-80 and
+ * Q36/model/moe.py:161-165): h_out = bf16(a_row + resid), hn_out = rmsnorm(h_out) * w and
+ * y = hn_out . W^T, each bit for bit what the two calls write.  a_row, resid, w, h_out,
+ * hn_out: D bf16; W packed [N, D] (jit_q4_prepack); y: N bf16.
+ * Contract: D % 256 == 0, D <= 2048, N % 16 == 0 (JIT_EUNSUPPORTED). */
+int jit_qmm_packed_add_rmsnorm(const uint16_t *a_row, const uint16_t *resid, const uint16_t *w, float eps, int D,
+                               const void *packed, int N, uint16_t *h_out, uint16_t *hn_out, uint16_t *y,
+                               void *stream);
+
+/* One row's MoE combine and the next layer's input RMSNorm in front of that layer's packed qkv
+ * projection, in one launch (jit_moe_combine_rmsnorm for B = 1 followed by jit_qmm_packed of its
+ * normed row; Q36/model/moe.py:119-123,286, Q36/model/model.py:65-80, Q36/model/attention.py:99):
+ * y_out = the combined row as jit_moe_combine writes it (resid may be NULL) and
+ * out = rmsnorm(y_out) * w . W^T, each bit for bit what the two calls write.  r, inv, scores, k:
+ * as jit_moe_combine with B = 1; W packed [N, D].
+ * Contract: D % 256 == 0, D <= 2048, N % 16 == 0, k > 0 (JIT_EUNSUPPORTED / JIT_EINVAL). */
+int jit_qmm_packed_combine_rmsnorm(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int k,
+                                   const uint16_t *resid, const uint16_t *w, float eps, int D, const void *packed,
+                                   int N, uint16_t *y_out, uint16_t *out, void *stream);
+
 /* The attention block between the qkv projection and attention
  * (Qwen3_5MoeAttention.step, Q36/model/attention.py:99-119, without the output
  * gate, which the BASELINE geometry does not have): qkv [B, (H + 2 Hkv) * 128]

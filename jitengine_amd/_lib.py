@@ -48,6 +48,8 @@ _SIGNATURES = {
     "jit_moe_combine": [_P, _P, _P, _I, _I, _I, _P, _P, _P],
     "jit_moe_combine_rmsnorm": [_P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P],
     "jit_rmsnorm": [_P, _P, _I, _I, _P, _F, _P, _P, _P],
+    "jit_qmm_packed_add_rmsnorm": [_P, _P, _P, _F, _I, _P, _I, _P, _P, _P, _P],
+    "jit_qmm_packed_combine_rmsnorm": [_P, _P, _P, _I, _P, _P, _F, _I, _P, _I, _P, _P, _P],
     "jit_qk_norm_rope_append": [_P, _I, _I, _I, _P, _P, _F, _P, _P, _P, _I, _P, _P, _P],
     "jit_kv_append_paged": [_P, _P, _I, _I, _P, _P, _I, _P, _P],
     "jit_attn_chunk_tokens": [_I],

@@ -9,31 +9,17 @@
 // rotates the pairs (x[i], x[i + D/2]) by pos * inv_freq[i] in fp32.
 #include "common.hpp"
 #include "qtile.hpp"
+#include "rowops.hpp"
 
 namespace {
 
-// Eight floats to eight bf16 (round-to-nearest-even), packed.
-__device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
-  uint4 o;
-  o.x = pack_bf16x2_rne(v[0], v[1]);
-  o.y = pack_bf16x2_rne(v[2], v[3]);
-  o.z = pack_bf16x2_rne(v[4], v[5]);
-  o.w = pack_bf16x2_rne(v[6], v[7]);
-  return o;
-}
+using rowops::block_sum_256;
+using rowops::combine8;
+using rowops::norm8;
+using rowops::pack8;
 
 constexpr int kD = JIT_HEAD_DIM;
 constexpr int kPage = JIT_PAGE_TOKENS;
-
-__device__ __forceinline__ float block_sum_256(float v, float *red) {
-  v = wave_butterfly<false>(v);  // (the pairs of a shuffle butterfly over offsets 32..1)
-  const int w = threadIdx.x >> 6;
-  if (lane_id() == 0) red[w] = v;
-  __syncthreads();
-  const float s = (red[0] + red[1]) + (red[2] + red[3]);
-  __syncthreads();
-  return s;
-}
 
 // One workgroup (256 threads) per row; each thread owns 8 consecutive elements.
 // With `resid`, the row is h = bf16(x + resid) (written to h_out) and h is normed.
@@ -42,7 +28,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
                                                       const uint16_t *__restrict__ w, float eps,
                                                       uint16_t *__restrict__ h_out,
                                                       uint16_t *__restrict__ y) {
-  __shared__ float red[4];
+  __shared__ float red[8];
   const long long row = blockIdx.x;
   float v[8];
   float ss = 0.0f;
@@ -73,69 +59,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
   const float tot = block_sum_256(ss, red);
   const float r = rsqrtf(tot / (float)D + eps);
   if (on) {
-    const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
     float o[8];
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      float n0 = v[i] * r, n1 = v[i + 1] * r;
-      round_bf2(n0, n1);
-      o[i] = bf2f(ww[i >> 1] & 0xffffu) * n0;
-      o[i + 1] = bf2f_hi(ww[i >> 1]) * n1;
-    }
+    norm8(v, r, wq, o);
     *(uint4 *)(y + row * D + n) = pack8(o);
   }
 }
-
-// Weighted combine of one row's 8 consecutive outputs n..n+7 (slot order, each
-// product and each partial sum rounded to bf16; a dropped pair, inv < 0,
-// contributes nothing), plus the residual when given.  Every slot's loads are
-// issued before any is used.
-__device__ __forceinline__ void combine8(const uint16_t *__restrict__ r, const int32_t *__restrict__ inv,
-                                         const uint16_t *__restrict__ scores, int k, int D,
-                                         const uint16_t *__restrict__ resid, long long bt, int n, float (&acc)[8]) {
-#pragma clang fp contract(off)
-#pragma unroll
-  for (int i = 0; i < 8; i++) acc[i] = 0.0f;
-  const uint4 res = resid ? *(const uint4 *)(resid + bt * D + n) : make_uint4(0u, 0u, 0u, 0u);
-  for (int j0 = 0; j0 < k; j0 += 8) {
-    uint4 rv[8];
-    float sc[8];
-    bool use[8];
-#pragma unroll
-    for (int jj = 0; jj < 8; jj++) {
-      const int j = min(j0 + jj, k - 1);
-      const int p = inv[bt * k + j];
-      use[jj] = j0 + jj < k && p >= 0;
-      sc[jj] = bf2f(scores[bt * k + j]);
-      rv[jj] = *(const uint4 *)(r + (long long)(p < 0 ? 0 : p) * D + n);
-    }
-#pragma unroll
-    for (int jj = 0; jj < 8; jj++) {
-      if (!use[jj]) continue;
-      const uint32_t wds[4] = {rv[jj].x, rv[jj].y, rv[jj].z, rv[jj].w};
-#pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        float p0 = bf2f(wds[i >> 1] & 0xffffu) * sc[jj], p1 = bf2f_hi(wds[i >> 1]) * sc[jj];
-        round_bf2(p0, p1);
-        float a0 = acc[i] + p0, a1 = acc[i + 1] + p1;
-        round_bf2(a0, a1);
-        acc[i] = a0;
-        acc[i + 1] = a1;
-      }
-    }
-  }
-  if (resid) {
-    const uint32_t wds[4] = {res.x, res.y, res.z, res.w};
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      float a0 = bf2f(wds[i >> 1] & 0xffffu) + acc[i], a1 = bf2f_hi(wds[i >> 1]) + acc[i + 1];
-      round_bf2(a0, a1);
-      acc[i] = a0;
-      acc[i + 1] = a1;
-    }
-  }
-}
-
 
 // Weighted combine: one workgroup per token row, 8 outputs per thread.
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict__ r,
@@ -158,7 +86,7 @@ __global__ __launch_bounds__(256) void combine_rmsnorm_kernel(
     const uint16_t *__restrict__ r, const int32_t *__restrict__ inv, const uint16_t *__restrict__ scores, int k,
     int D, const uint16_t *__restrict__ resid, uint16_t *__restrict__ y, const uint16_t *__restrict__ w, float eps,
     uint16_t *__restrict__ xn) {
-  __shared__ float red[4];
+  __shared__ float red[8];
   const long long bt = blockIdx.x;
   const int n = threadIdx.x * 8;
   const bool on = n < D;
@@ -174,15 +102,8 @@ __global__ __launch_bounds__(256) void combine_rmsnorm_kernel(
   const float tot = block_sum_256(ss, red);
   const float rs = rsqrtf(tot / (float)D + eps);
   if (on) {
-    const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
     float o[8];
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      float n0 = v[i] * rs, n1 = v[i + 1] * rs;
-      round_bf2(n0, n1);
-      o[i] = bf2f(ww[i >> 1] & 0xffffu) * n0;
-      o[i + 1] = bf2f_hi(ww[i >> 1]) * n1;
-    }
+    norm8(v, rs, wq, o);
     *(uint4 *)(xn + bt * D + n) = pack8(o);
   }
 }

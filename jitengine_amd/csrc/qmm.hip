@@ -25,6 +25,7 @@
 // order: results do not depend on the batch).
 #include "qtile.hpp"
 #include "route.hpp"
+#include "rowops.hpp"
 
 namespace {
 
@@ -48,6 +49,15 @@ struct QmmArgs {
   uint32_t *inds;
   uint16_t *scores;
   int32_t *order, *pair_row, *inv, *t_cnt, *t_off, *seg_expert, *seg_start, *seg_cnt, *meta;
+  // PRO (a one-row dense projection that builds its own input row; x unused): 1 = bf16(pr_a +
+  // pr_resid) then RMSNorm with pr_w (workgroup 0 writes the sum to pr_sum and the normed row to
+  // pr_norm); 2 = the MoE combine of the expert outputs pr_a through pr_inv / pr_scores plus
+  // pr_resid, then RMSNorm (workgroup 0 writes the combined row to pr_sum)
+  const uint16_t *pr_a, *pr_resid, *pr_w, *pr_scores;
+  const int32_t *pr_inv;
+  int pr_k;
+  float pr_eps;
+  uint16_t *pr_sum, *pr_norm;
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -110,7 +120,8 @@ __device__ uint64_t g_qmm_stamps[kStampSlots][8];
   } while (0)
 #endif
 
-template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false, bool ROUTED = false>
+template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false, bool ROUTED = false,
+          int PRO = 0>
 __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
 #if JIT_QMM_STAMPS
   uint64_t ts[6] = {__builtin_amdgcn_s_memrealtime(), 0, 0, 0, 0, 0};
@@ -123,6 +134,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
   const int lr = l & 15, lg = l >> 4;
   static_assert(!ROUTED || (COMPACT && TT == 1), "a routed step is one token over the compact grid");
+  static_assert(PRO == 0 || (!SWIGLU && TT == 1 && !COMPACT), "a row prologue goes with a one-row dense projection");
   int e = 0, cnt, off;
   if constexpr (ROUTED) {
     // One token routes itself (the router's top-k on every wave: route::topk_slot_key, the
@@ -299,7 +311,19 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   // activation fragments (natural k order, as the unpacked weights); lanes past the
   // last token load from outside the buffer's range (no branch around the loads): zeros,
   // which feed only output rows of tokens that are never stored
+  // PRO: the row, after the K-split partials' region of the LDS (8 floats of reduction, then K bf16)
+  float *pro_red = red + ksplit * TT * NBW * 4 * 64;
+  const uint8_t *pro_row = (const uint8_t *)(pro_red + 8);
   auto load_x = [&](const int t0, const int (&rows)[TT], Frag8 (&xa)[TT][GPW][2]) {
+    if constexpr (PRO != 0) {  // the one token's lanes read the row from LDS, the padding lanes zeros
+#pragma unroll
+      for (int g = 0; g < GPW; g++) {
+        const uint8_t *xp = pro_row + 2 * (64 * g0 + 16 * lg) + 128 * g;
+        xa[0][g][0].q = lr == 0 ? *(const uint4 *)xp : make_uint4(0u, 0u, 0u, 0u);
+        xa[0][g][1].q = lr == 0 ? *(const uint4 *)(xp + 16) : make_uint4(0u, 0u, 0u, 0u);
+      }
+      return;
+    }
 #pragma unroll
     for (int tt = 0; tt < TT; tt++) {
       const uint32_t xo = (uint32_t)x_off(t0 + 16 * tt + lr, rows[tt]) + 2u * (64 * g0 + 16 * lg);  // (out of range stays out)
@@ -415,6 +439,45 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     }
     __syncthreads();
   };
+  if constexpr (PRO != 0) {
+    // The input row, built as rmsnorm_kernel (PRO 1) or combine_rmsnorm_kernel (PRO 2) builds it
+    // (rowops: thread t < 256 owns elements 8t .. 8t + 7), while the weight loads above are in
+    // flight; every workgroup builds it (no exchange), workgroup 0 also writes it out.
+    const int D = a.K, n = threadIdx.x * 8;
+    const bool on = threadIdx.x < 256 && n < D, first = blockIdx.x == 0 && blockIdx.z == 0;
+    const uint4 wq = on ? *(const uint4 *)(a.pr_w + n) : make_uint4(0u, 0u, 0u, 0u);
+    float v[8];
+    float ss = 0.0f;
+    if (on) {
+      if constexpr (PRO == 1) {
+        const uint4 av = *(const uint4 *)(a.pr_a + n), rv = *(const uint4 *)(a.pr_resid + n);
+        const uint32_t aw[4] = {av.x, av.y, av.z, av.w}, rw[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          v[i] = bf2f(aw[i >> 1] & 0xffffu);
+          v[i + 1] = bf2f_hi(aw[i >> 1]);
+          v[i] += bf2f(rw[i >> 1] & 0xffffu);
+          v[i + 1] += bf2f_hi(rw[i >> 1]);
+          round_bf2(v[i], v[i + 1]);
+        }
+      } else {
+        rowops::combine8(a.pr_a, a.pr_inv, a.pr_scores, a.pr_k, D, a.pr_resid, 0, n, v);
+      }
+      if (first) *(uint4 *)(a.pr_sum + n) = rowops::pack8(v);
+#pragma unroll
+      for (int i = 0; i < 8; i++) ss = fmaf(v[i], v[i], ss);
+    }
+    const float tot = rowops::block_sum_256(ss, pro_red);
+    const float rs = rsqrtf(tot / (float)D + a.pr_eps);
+    if (on) {
+      float o[8];
+      rowops::norm8(v, rs, wq, o);
+      const uint4 q = rowops::pack8(o);
+      *(uint4 *)(pro_row + 2 * n) = q;
+      if (PRO == 1 && first) *(uint4 *)(a.pr_norm + n) = q;
+    }
+    __syncthreads();
+  }
   {
     Frag8 xa[TT][GPW][2];
     __builtin_amdgcn_sched_barrier(0);
@@ -460,7 +523,8 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
 #endif
 }
 
-template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false, bool ROUTED = false>
+template <int NB, int GPW, bool SWIGLU, bool PACKED, int TT = 1, bool COMPACT = false, bool ROUTED = false,
+          int PRO = 0>
 int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what, int zsplit = 1) {
   constexpr int NBW = SWIGLU ? 2 * NB : NB;
   const int G = a.K / 64;
@@ -470,8 +534,9 @@ int launch_qmm(const QmmArgs &a, int E, hipStream_t st, const char *what, int zs
   if (SWIGLU != (a.row_index != nullptr || ROUTED))
     return jit::fail(JIT_EINVAL, "%s: a row index goes with the gate||up instances only", what);
   const dim3 grid((a.N + 16 * NB - 1) / (16 * NB), E, zsplit), block(64 * ksplit);
-  const size_t lds = (size_t)ksplit * TT * NBW * 4 * 64 * sizeof(float);
-  qmm_kernel<NB, GPW, SWIGLU, PACKED, TT, COMPACT, ROUTED><<<grid, block, lds, st>>>(a);
+  const size_t lds = (size_t)ksplit * TT * NBW * 4 * 64 * sizeof(float) +
+                     (PRO ? 8 * sizeof(float) + (size_t)a.K * sizeof(uint16_t) : 0);
+  qmm_kernel<NB, GPW, SWIGLU, PACKED, TT, COMPACT, ROUTED, PRO><<<grid, block, lds, st>>>(a);
   return jit::check_launch(what);
 }
 
@@ -600,6 +665,69 @@ extern "C" int jit_qmm_packed(const uint16_t *x, int T, int K, const void *packe
   if (!packed) return jit::fail(JIT_EINVAL, "qmm_packed: null pointer");
   QmmArgs a{x, nullptr, nullptr, nullptr, (const uint32_t *)packed, nullptr, nullptr, y, K, N, T, 0, 0, N};
   return launch_dense<true>(a, (hipStream_t)stream);
+}
+
+// One row's dense projection with its input row built in the launch (PRO 1 / 2): the launch shape of
+// jit_qmm_packed for one token, so each output sums the same groups in the same order.
+template <int PRO, int GPW>
+int launch_dense_pro_gpw(const QmmArgs &a, hipStream_t st, const char *what) {
+  const bool wide = GPW <= 4 && a.N >= JIT_DENSE_WIDE_N;
+  return wide ? launch_qmm<2, GPW, false, true, 1, false, false, PRO>(a, 1, st, what, 1)
+              : launch_qmm<1, GPW, false, true, 1, false, false, PRO>(a, 1, st, what, 1);
+}
+
+template <int PRO>
+int launch_dense_pro(const QmmArgs &a, hipStream_t st, const char *what) {
+  if (a.K % 256 != 0 || a.K > 2048 || a.N % 16 != 0)
+    return jit::fail(JIT_EUNSUPPORTED, "%s covers D %% 256 == 0, D <= 2048 and N %% 16 == 0, got D=%d N=%d", what,
+                     a.K, a.N);
+  switch (dense_gpw(a.K)) {
+    case 2: return launch_dense_pro_gpw<PRO, 2>(a, st, what);
+    case 4: return launch_dense_pro_gpw<PRO, 4>(a, st, what);
+    case 6: return launch_dense_pro_gpw<PRO, 6>(a, st, what);
+    case 8: return launch_dense_pro_gpw<PRO, 8>(a, st, what);
+    default: return jit::fail(JIT_EUNSUPPORTED, "%s: no wave split for D=%d", what, a.K);
+  }
+}
+
+// rmsnorm of bf16(a + resid) (jit_rmsnorm with a residual, for one row) followed by jit_qmm_packed of the
+// normed row, in one launch: h_out = the sum, hn_out = the normed row, y = hn . W^T.
+extern "C" int jit_qmm_packed_add_rmsnorm(const uint16_t *a_row, const uint16_t *resid, const uint16_t *w, float eps,
+                                          int D, const void *packed, int N, uint16_t *h_out, uint16_t *hn_out,
+                                          uint16_t *y, void *stream) {
+  if (D <= 0 || N <= 0) return jit::fail(JIT_EINVAL, "qmm_packed_add_rmsnorm: bad dims D=%d N=%d", D, N);
+  if (!a_row || !resid || !w || !packed || !h_out || !hn_out || !y)
+    return jit::fail(JIT_EINVAL, "qmm_packed_add_rmsnorm: null pointer");
+  QmmArgs a{nullptr, nullptr, nullptr, nullptr, (const uint32_t *)packed, nullptr, nullptr, y, D, N, 1, 0, 0, N};
+  a.pr_a = a_row;
+  a.pr_resid = resid;
+  a.pr_w = w;
+  a.pr_eps = eps;
+  a.pr_sum = h_out;
+  a.pr_norm = hn_out;
+  return launch_dense_pro<1>(a, (hipStream_t)stream, "jit_qmm_packed_add_rmsnorm");
+}
+
+// jit_moe_combine_rmsnorm for one row followed by jit_qmm_packed of the normed row, in one launch:
+// y_out = the combined row (the next layer's residual), out = rmsnorm(y_out) . W^T.
+extern "C" int jit_qmm_packed_combine_rmsnorm(const uint16_t *r, const int32_t *inv, const uint16_t *scores, int k,
+                                              const uint16_t *resid, const uint16_t *w, float eps, int D,
+                                              const void *packed, int N, uint16_t *y_out, uint16_t *out,
+                                              void *stream) {
+  if (D <= 0 || N <= 0 || k <= 0)
+    return jit::fail(JIT_EINVAL, "qmm_packed_combine_rmsnorm: bad dims D=%d N=%d k=%d", D, N, k);
+  if (!r || !inv || !scores || !w || !packed || !y_out || !out)
+    return jit::fail(JIT_EINVAL, "qmm_packed_combine_rmsnorm: null pointer");
+  QmmArgs a{nullptr, nullptr, nullptr, nullptr, (const uint32_t *)packed, nullptr, nullptr, out, D, N, 1, 0, 0, N};
+  a.pr_a = r;
+  a.pr_inv = inv;
+  a.pr_scores = scores;
+  a.pr_k = k;
+  a.pr_resid = resid;
+  a.pr_w = w;
+  a.pr_eps = eps;
+  a.pr_sum = y_out;
+  return launch_dense_pro<2>(a, (hipStream_t)stream, "jit_qmm_packed_combine_rmsnorm");
 }
 
 // Expert GEMV shapes (groups of 64 per wave; row blocks of 16 per workgroup), chosen by timing

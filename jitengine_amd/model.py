@@ -153,19 +153,31 @@ class DecoderLayer:
         sub-block, residual, MoE sub-block, residual); `debug` receives every intermediate."""
         return self.run(x, pool, st, debug=debug)[0]
 
-    def run(self, x: torch.Tensor, pool: torch.Tensor, st: StepState, xn: torch.Tensor | None = None,
-            next_norm: torch.Tensor | None = None, debug: dict | None = None):
+    def run(self, x: torch.Tensor | None, pool: torch.Tensor, st: StepState, xn: torch.Tensor | None = None,
+            next_norm: torch.Tensor | None = None, debug: dict | None = None, carry: tuple | None = None,
+            defer: bool = False):
         """(y, xn_next): the layer on rows x whose input norm xn = rmsnorm(x) may come from the
         previous layer; with next_norm (the next layer's input-norm weight) the closing combine
-        also returns that layer's normed input in the same launch, else xn_next is None."""
+        also returns that layer's normed input in the same launch, else xn_next is None.
+
+        One-token steps (the same bits, fewer launches): carry = (r, pk, scores, h) is the previous
+        layer's combine left undone, run here with this layer's input norm inside the qkv
+        projection (x is None then: the launch writes it); defer=True leaves this layer's combine
+        undone and returns (None, carry) for the next layer to take in."""
         cfg = self.cfg
-        B = x.shape[0]
         moe = self.moe
-        if xn is None:
-            xn = ops.rmsnorm(x, self.input_norm, cfg.eps)
-        # decode rows take the decode kernels at any batch size (seg=False): a row's bits never
-        # depend on how many other rows the step carries
-        qkv = ops.qmm(xn, self.qkv, seg=False)
+        if carry is not None:
+            r0, pk0, sc0, h0 = carry
+            x, qkv = ops.qmm_combine_rmsnorm(r0, pk0, sc0, h0, self.input_norm, cfg.eps, self.qkv)
+        else:
+            if xn is None:
+                xn = ops.rmsnorm(x, self.input_norm, cfg.eps)
+            # decode rows take the decode kernels at any batch size (seg=False): a row's bits never
+            # depend on how many other rows the step carries
+            qkv = ops.qmm(xn, self.qkv, seg=False)
+        B = x.shape[0]
+        if defer and B != 1:
+            raise ValueError("defer takes a one-token step")
         scale = cfg.head_dim ** -0.5
         if debug is None:  # q/k norm + RoPE + append inside the attention launch (the same bits)
             q = None
@@ -176,8 +188,11 @@ class DecoderLayer:
                                         self.inv_freq, st.pos, st.page_table, pool)
             attn = ops.paged_decode_attention(q, pool, st.page_table, st.plan, scale, st.workspace)
         o = ops.qmm(attn.view(B, -1), self.o, seg=False)
-        hn, h = ops.rmsnorm(o, self.post_norm, cfg.eps, resid=x, return_sum=True)
-        logits = ops.qmm(hn, moe.router, seg=False)
+        if B == 1 and ops.row_prologue_fits(moe.router, cfg.hidden):  # the add + norm inside the router launch
+            logits, h, hn = ops.qmm_add_rmsnorm(o, x, self.post_norm, cfg.eps, moe.router)
+        else:
+            hn, h = ops.rmsnorm(o, self.post_norm, cfg.eps, resid=x, return_sum=True)
+            logits = ops.qmm(hn, moe.router, seg=False)
         E, k = moe.num_experts, moe.top_k
         if B == 1 and isinstance(moe.gate_up, ops.PackedQ4) and E % 32 == 0 and E <= 128 and k < E and k <= 64:
             # one token: its top-k and packing inside the gate||up launch (the same bits)
@@ -190,13 +205,17 @@ class DecoderLayer:
                 inds, scores = ops.router_topk(logits, k, moe.norm_topk)
                 pk = ops.moe_pack(inds, E)
             hh, r = moe.expert_mlp(hn, pk)
-        if next_norm is None:
+        if defer:
+            y, xn_next = None, None
+        elif next_norm is None:
             y, xn_next = ops.moe_combine(r, pk, scores, h), None
         else:
             y, xn_next = ops.moe_combine_rmsnorm(r, pk, scores, h, next_norm, cfg.eps)
         if debug is not None:
             debug.update(x=x, xn=xn, qkv=qkv, q=q, attn=attn, o=o, h=h, hn=hn, logits=logits, inds=inds,
                          scores=scores, pk=pk, hh=hh, r=r, y=y)
+        if defer:
+            return None, (r, pk, scores, h)
         return y, xn_next
 
 
@@ -244,10 +263,15 @@ class Model:
 
     def decode_step(self, x: torch.Tensor, pools: list, st: StepState) -> torch.Tensor:
         """x [B, D] bf16 hidden rows -> the last layer's output rows; pools[l] is layer l's KV pool."""
-        xn = None
+        one = x.shape[0] == 1
+        xn, carry = None, None
         for i, (layer, pool) in enumerate(zip(self.layers, pools)):
-            nxt = self.layers[i + 1].input_norm if i + 1 < len(self.layers) else None
-            x, xn = layer.run(x, pool, st, xn=xn, next_norm=nxt)
+            nxt = self.layers[i + 1] if i + 1 < len(self.layers) else None
+            # one token: the layer's combine runs inside the next layer's qkv launch
+            defer = one and nxt is not None and ops.row_prologue_fits(nxt.qkv, self.cfg.hidden)
+            y, out = layer.run(x, pool, st, xn=xn, carry=carry, defer=defer,
+                               next_norm=None if (defer or nxt is None) else nxt.input_norm)
+            x, xn, carry = (None, None, out) if defer else (y, out, None)
         return x
 
 

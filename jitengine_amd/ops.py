@@ -419,6 +419,67 @@ def moe_combine_rmsnorm(r: torch.Tensor, pk: Packing, scores: torch.Tensor, resi
     return y, xn
 
 
+def row_prologue_fits(lin, D: int) -> bool:
+    """Whether a one-row projection can build its own normed input row (qmm_add_rmsnorm,
+    qmm_combine_rmsnorm): a packed [N, D] matrix with D % 256 == 0, D <= 2048, N % 16 == 0."""
+    return (isinstance(lin, PackedQ4) and not lin.stacked and lin.K == D and D % 256 == 0 and D <= 2048
+            and lin.N % 16 == 0)
+
+
+def _need_row_prologue(lin, D: int, what: str) -> None:
+    if not row_prologue_fits(lin, D):
+        raise _lib.UnsupportedShape(f"{what} takes a packed [N, {D}] matrix, D % 256 == 0, D <= 2048, N % 16 == 0")
+
+
+def qmm_add_rmsnorm(a: torch.Tensor, resid: torch.Tensor, w: torch.Tensor, eps: float, lin):
+    """(y, h, hn) for one row in one launch (jit_qmm_packed_add_rmsnorm): h = bf16(a + resid),
+    hn = rmsnorm(h, w, eps), y = hn . W^T -- bit for bit rmsnorm(a, w, eps, resid, return_sum=True)
+    and qmm(hn, lin) (the post-attention norm and the router projection of a one-token step)."""
+    for t, name in ((a, "a"), (resid, "resid"), (w, "w")):
+        _need(t, torch.bfloat16, name)
+    D = a.shape[-1]
+    if a.shape != (1, D) or resid.shape != (1, D) or w.numel() != D:
+        raise ValueError("qmm_add_rmsnorm takes one row: a, resid [1, D], w [D]")
+    _need_row_prologue(lin, D, "qmm_add_rmsnorm")
+    y = torch.empty((1, lin.N), dtype=torch.bfloat16, device=a.device)
+    h, hn = torch.empty_like(a), torch.empty_like(a)
+    _lib.check(
+        _lib.lib().jit_qmm_packed_add_rmsnorm(_p(a), _p(resid), _p(w), float(eps), D, _p(lin.data), lin.N, _p(h),
+                                              _p(hn), _p(y), _stream()),
+        "qmm_add_rmsnorm",
+    )
+    return y, h, hn
+
+
+def qmm_combine_rmsnorm(r: torch.Tensor, pk: Packing, scores: torch.Tensor, resid: torch.Tensor | None,
+                        w: torch.Tensor, eps: float, lin):
+    """(y, out) for one row in one launch (jit_qmm_packed_combine_rmsnorm): y = moe_combine(r, pk,
+    scores, resid) and out = rmsnorm(y, w, eps) . W^T -- bit for bit moe_combine_rmsnorm and qmm of its
+    normed row (a layer's output and the next layer's qkv projection in a one-token step)."""
+    _need(r, torch.bfloat16, "r")
+    _need(scores, torch.bfloat16, "scores")
+    _need(w, torch.bfloat16, "w")
+    B, k = scores.shape
+    D = r.shape[-1]
+    if B != 1:
+        raise _lib.UnsupportedShape("qmm_combine_rmsnorm takes one row")
+    if resid is not None:
+        _need(resid, torch.bfloat16, "resid")
+        if resid.shape != (1, D):
+            raise ValueError("resid must be [1, D]")
+    if w.numel() != D:
+        raise ValueError(f"norm weight of {w.numel()} for rows of {D}")
+    _need_row_prologue(lin, D, "qmm_combine_rmsnorm")
+    y = torch.empty((1, D), dtype=torch.bfloat16, device=r.device)
+    out = torch.empty((1, lin.N), dtype=torch.bfloat16, device=r.device)
+    _lib.check(
+        _lib.lib().jit_qmm_packed_combine_rmsnorm(_p(r), _p(pk.inv), _p(scores), k, _p(resid), _p(w), float(eps), D,
+                                                  _p(lin.data), lin.N, _p(y), _p(out), _stream()),
+        "qmm_combine_rmsnorm",
+    )
+    return y, out
+
+
 # ----------------------------------------------------------------------------- decoder block glue
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, resid: torch.Tensor | None = None,
             return_sum: bool = False):
