@@ -264,36 +264,69 @@ __global__ __launch_bounds__(512) void paged_attn_kernel(const AttnArgs a) {
     // LDS, and the workgroup of the sequence's last chunk first writes the token's K and V of its
     // kv heads into the pool.  The barrier's fence orders those stores before this workgroup's
     // reads of the token's page; other workgroups never read it.  A wave whose first step holds
-    // that page issues its first loads after the barrier, the others before the q work.
+    // that page issues its first loads after the barrier, the others right after requesting the
+    // token's values: vector loads complete in order, so values requested behind the first K/V
+    // loads would be waited for only once those had landed.
     const int tok = L - 1;
     const bool defer = wk1 == L && tok < wk0 + 32;
-    if (!defer) first_loads();
     const int nh = a.H + 2 * a.Hkv;
     const uint16_t *row = a.qkv + (long long)b * nh * kD;
     uint16_t *qs = (uint16_t *)(xstate + (WS - 1) * hb * kStateFloats * 64);  // [hb][G][128], past the states
+    constexpr int kQHeads = (16 + WS - 1) / WS;  // q heads a wave norms (G <= 16)
+    const bool writer = live && c == nchunks - 1 && split < 2;  // the token's K (split 0) or V (split 1)
+    uint16_t qx[kQHeads][2], tx[2] = {0, 0}, qw[2] = {0, 0}, kw[2] = {0, 0};
+    float fr = 0.0f;
+    int pg = 0;
     if (live) {
-      const float ang = (float)tok * a.inv_freq[l];
-      if (c == nchunks - 1 && split < 2) {
-        const int pg = a.page_table[(long long)b * a.max_pages + (tok >> 4)], slot = tok & (kPage - 1);
+      fr = a.inv_freq[l];
+      qw[0] = a.qn_w[l];
+      qw[1] = a.qn_w[l + 64];
+#pragma unroll
+      for (int i = 0; i < kQHeads; i++) {
+        const int hq = split + WS * i;
+        if (hq < G) {  // (uniform over the wave)
+          const uint16_t *src = row + (kvh * G + hq) * kD;
+          qx[i][0] = src[l];
+          qx[i][1] = src[l + 64];
+        }
+      }
+      if (writer) {
+        pg = a.page_table[(long long)b * a.max_pages + (tok >> 4)];
+        const uint16_t *src = row + (a.H + (split ? a.Hkv : 0) + kvh) * kD;
+        tx[0] = src[l];
+        tx[1] = src[l + 64];
+        if (split == 0) {
+          kw[0] = a.kn_w[l];
+          kw[1] = a.kn_w[l + 64];
+        }
+      }
+    }
+    asm volatile("" ::: "memory");  // (the token's loads stay ahead of the first K/V)
+    if (!defer) first_loads();
+    if (live) {
+      const float ang = (float)tok * fr;
+      if (writer) {
+        const int slot = tok & (kPage - 1);
         uint16_t *hp = (uint16_t *)a.pool + ((long long)pg * a.Hkv + kvh) * 2 * kPageHead;
         if (split == 0) {  // K: normed and rotated, into the chunk-major K part
-          const uint16_t *src = row + (a.H + kvh) * kD;
           uint32_t o1, o2;
-          qk_head_norm_rope(bf2f(src[l]), bf2f(src[l + 64]), bf2f(a.kn_w[l]), bf2f(a.kn_w[l + 64]), a.eps, ang, o1, o2);
+          qk_head_norm_rope(bf2f(tx[0]), bf2f(tx[1]), bf2f(kw[0]), bf2f(kw[1]), a.eps, ang, o1, o2);
           hp[k_page_offset(slot, l)] = (uint16_t)o1;
           hp[k_page_offset(slot, l + 64)] = (uint16_t)o2;
         } else {  // V: as it is, into the dim-major V part
-          const uint16_t *src = row + (a.H + a.Hkv + kvh) * kD;
-          hp[kPageHead + l * kPage + slot] = src[l];
-          hp[kPageHead + (l + 64) * kPage + slot] = src[l + 64];
+          hp[kPageHead + l * kPage + slot] = tx[0];
+          hp[kPageHead + (l + 64) * kPage + slot] = tx[1];
         }
       }
-      for (int hq = split; hq < G; hq += WS) {  // (uniform over the wave)
-        const uint16_t *src = row + (kvh * G + hq) * kD;
-        uint32_t o1, o2;
-        qk_head_norm_rope(bf2f(src[l]), bf2f(src[l + 64]), bf2f(a.qn_w[l]), bf2f(a.qn_w[l + 64]), a.eps, ang, o1, o2);
-        qs[(kvl * G + hq) * kD + l] = (uint16_t)o1;
-        qs[(kvl * G + hq) * kD + l + 64] = (uint16_t)o2;
+#pragma unroll
+      for (int i = 0; i < kQHeads; i++) {
+        const int hq = split + WS * i;
+        if (hq < G) {  // (uniform over the wave)
+          uint32_t o1, o2;
+          qk_head_norm_rope(bf2f(qx[i][0]), bf2f(qx[i][1]), bf2f(qw[0]), bf2f(qw[1]), a.eps, ang, o1, o2);
+          qs[(kvl * G + hq) * kD + l] = (uint16_t)o1;
+          qs[(kvl * G + hq) * kD + l + 64] = (uint16_t)o2;
+        }
       }
     }
     __syncthreads();
