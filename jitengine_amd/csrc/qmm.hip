@@ -255,6 +255,22 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
 #pragma unroll
   for (int tt = 0; tt < TT; tt++) row0[tt] = row_of(tfirst + 16 * tt + lr);
 
+  // PRO 1: the input row's operands requested before the weight slice (vector loads complete in
+  // order: requested behind it, they would land only once all of it had; router launch 3.67 ->
+  // 3.25 us at bs = 1).  PRO 2's combine reads its rows through the slots' positions, after the
+  // weights: requesting all of the token's rows ahead instead was slower (6.6 -> 7.9 us).
+  const int pro_n = threadIdx.x * 8;
+  const bool pro_on = PRO != 0 && threadIdx.x < 256 && pro_n < a.K;
+  uint4 pro_wq = make_uint4(0u, 0u, 0u, 0u), pro_av = make_uint4(0u, 0u, 0u, 0u), pro_rv = make_uint4(0u, 0u, 0u, 0u);
+  if constexpr (PRO == 1) {
+    if (pro_on) {
+      pro_wq = *(const uint4 *)(a.pr_w + pro_n);
+      pro_av = *(const uint4 *)(a.pr_a + pro_n);
+      pro_rv = *(const uint4 *)(a.pr_resid + pro_n);
+    }
+    asm volatile("" ::: "memory");
+  }
+
   // ---- the wave's whole weight slice: GPW groups x NBW row blocks
   uint2 wv[GPW][NBW];
   uint32_t sv[NBW][(GPW + 1) / 2], bv[NBW][(GPW + 1) / 2];  // bf16 pairs (groups 2j, 2j+1)
@@ -443,14 +459,14 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     // The input row, built as rmsnorm_kernel (PRO 1) or combine_rmsnorm_kernel (PRO 2) builds it
     // (rowops: thread t < 256 owns elements 8t .. 8t + 7), while the weight loads above are in
     // flight; every workgroup builds it (no exchange), workgroup 0 also writes it out.
-    const int D = a.K, n = threadIdx.x * 8;
-    const bool on = threadIdx.x < 256 && n < D, first = blockIdx.x == 0 && blockIdx.z == 0;
-    const uint4 wq = on ? *(const uint4 *)(a.pr_w + n) : make_uint4(0u, 0u, 0u, 0u);
+    const int D = a.K, n = pro_n;
+    const bool on = pro_on, first = blockIdx.x == 0 && blockIdx.z == 0;
+    const uint4 wq = PRO == 1 ? pro_wq : (on ? *(const uint4 *)(a.pr_w + n) : make_uint4(0u, 0u, 0u, 0u));
     float v[8];
     float ss = 0.0f;
     if (on) {
       if constexpr (PRO == 1) {
-        const uint4 av = *(const uint4 *)(a.pr_a + n), rv = *(const uint4 *)(a.pr_resid + n);
+        const uint4 av = pro_av, rv = pro_rv;
         const uint32_t aw[4] = {av.x, av.y, av.z, av.w}, rw[4] = {rv.x, rv.y, rv.z, rv.w};
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
