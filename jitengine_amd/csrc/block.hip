@@ -23,6 +23,9 @@ constexpr int kPage = JIT_PAGE_TOKENS;
 
 // One workgroup (256 threads) per row; each thread owns 8 consecutive elements.
 // With `resid`, the row is h = bf16(x + resid) (written to h_out) and h is normed.
+// Rows a kernel writes besides its last output are stored at its end: a vector store counts on the
+// same in-order counter as the loads, so a store issued before a later load wait (the norm weights'
+// after the barrier) would be waited for there as well.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict__ x,
                                                       const uint16_t *__restrict__ resid, int D,
                                                       const uint16_t *__restrict__ w, float eps,
@@ -51,7 +54,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
         v[i + 1] += bf2f_hi(rw[i >> 1]);
         round_bf2(v[i], v[i + 1]);
       }
-      if (h_out) *(uint4 *)(h_out + row * D + n) = pack8(v);
     }
 #pragma unroll
     for (int i = 0; i < 8; i++) ss = fmaf(v[i], v[i], ss);
@@ -62,6 +64,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
     float o[8];
     norm8(v, r, wq, o);
     *(uint4 *)(y + row * D + n) = pack8(o);
+    if (resid && h_out) *(uint4 *)(h_out + row * D + n) = pack8(v);
   }
 }
 
@@ -95,7 +98,6 @@ __global__ __launch_bounds__(256) void combine_rmsnorm_kernel(
   float ss = 0.0f;
   if (on) {
     combine8(r, inv, scores, k, D, resid, bt, n, v);
-    *(uint4 *)(y + bt * D + n) = pack8(v);
 #pragma unroll
     for (int i = 0; i < 8; i++) ss = fmaf(v[i], v[i], ss);
   }
@@ -105,6 +107,7 @@ __global__ __launch_bounds__(256) void combine_rmsnorm_kernel(
     float o[8];
     norm8(v, rs, wq, o);
     *(uint4 *)(xn + bt * D + n) = pack8(o);
+    *(uint4 *)(y + bt * D + n) = pack8(v);  // (stored last: see rmsnorm_kernel)
   }
 }
 

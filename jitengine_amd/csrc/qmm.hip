@@ -262,6 +262,10 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
   const int pro_n = threadIdx.x * 8;
   const bool pro_on = PRO != 0 && threadIdx.x < 256 && pro_n < a.K;
   uint4 pro_wq = make_uint4(0u, 0u, 0u, 0u), pro_av = make_uint4(0u, 0u, 0u, 0u), pro_rv = make_uint4(0u, 0u, 0u, 0u);
+  // workgroup 0's copies of the row (the sum, and for PRO 1 the normed row), stored at the kernel's
+  // end: a store counts on the same in-order counter as the loads, so one issued before the weights'
+  // wait would be waited for there as well
+  uint4 pro_sum_q = make_uint4(0u, 0u, 0u, 0u), pro_norm_q = make_uint4(0u, 0u, 0u, 0u);
   if constexpr (PRO == 1) {
     if (pro_on) {
       pro_wq = *(const uint4 *)(a.pr_w + pro_n);
@@ -460,7 +464,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     // (rowops: thread t < 256 owns elements 8t .. 8t + 7), while the weight loads above are in
     // flight; every workgroup builds it (no exchange), workgroup 0 also writes it out.
     const int D = a.K, n = pro_n;
-    const bool on = pro_on, first = blockIdx.x == 0 && blockIdx.z == 0;
+    const bool on = pro_on;
     const uint4 wq = PRO == 1 ? pro_wq : (on ? *(const uint4 *)(a.pr_w + n) : make_uint4(0u, 0u, 0u, 0u));
     float v[8];
     float ss = 0.0f;
@@ -479,7 +483,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
       } else {
         rowops::combine8(a.pr_a, a.pr_inv, a.pr_scores, a.pr_k, D, a.pr_resid, 0, n, v);
       }
-      if (first) *(uint4 *)(a.pr_sum + n) = rowops::pack8(v);
+      pro_sum_q = rowops::pack8(v);
 #pragma unroll
       for (int i = 0; i < 8; i++) ss = fmaf(v[i], v[i], ss);
     }
@@ -490,7 +494,7 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
       rowops::norm8(v, rs, wq, o);
       const uint4 q = rowops::pack8(o);
       *(uint4 *)(pro_row + 2 * n) = q;
-      if (PRO == 1 && first) *(uint4 *)(a.pr_norm + n) = q;
+      pro_norm_q = q;
     }
     __syncthreads();
   }
@@ -525,6 +529,12 @@ __global__ __launch_bounds__(512) void qmm_kernel(const QmmArgs a) {
     Frag8 xa[TT][GPW][2];
     load_x(t0, rows, xa);
     pass(t0, xa);
+  }
+  if constexpr (PRO != 0) {
+    if (pro_on && blockIdx.x == 0 && blockIdx.z == 0) {
+      *(uint4 *)(a.pr_sum + pro_n) = pro_sum_q;
+      if constexpr (PRO == 1) *(uint4 *)(a.pr_norm + pro_n) = pro_norm_q;
+    }
   }
 #if JIT_QMM_STAMPS
   ts[5] = __builtin_amdgcn_s_memrealtime();
