@@ -38,6 +38,27 @@ __device__ __forceinline__ void topk_row(const uint16_t *__restrict__ lg, int ro
                                          uint16_t *__restrict__ gates_out, uint32_t *skey, int l) {
   uint32_t key[NPL];
   row_keys<NPL, FROM_GATES>(lg, row, N, l, key, gates_out);
+  if (k <= 64) {  // (uniform) slot j's key stays in lane j: no LDS round trip per slot
+    uint32_t mine = 0;
+    for (int t = 0; t < k; t++) {  // (every valid key is > 0; a taken key becomes 0)
+      uint32_t m = key[0];
+#pragma unroll
+      for (int j = 1; j < NPL; j++) m = key[j] > m ? key[j] : m;
+      m = wave_max_u32(m);
+#pragma unroll
+      for (int j = 0; j < NPL; j++) key[j] = key[j] == m ? 0u : key[j];
+      mine = l == k - 1 - t ? m : mine;
+    }
+    const float tot = scores != nullptr ? route::slots_total(mine, k) : 0.0f;
+    if (l < k) {
+      inds[(size_t)row * k + l] = mine & 0xffffu;
+      if (scores != nullptr) {
+        const float sc = bf2f(key_bf16(mine));
+        scores[(size_t)row * k + l] = (uint16_t)(norm ? f2bf(sc / tot) : f2bf(sc));
+      }
+    }
+    return;
+  }
   // every valid key is > 0 (its value field is >= 0x007f); a taken key becomes 0
   for (int t = 0; t < k; t++) {
     uint32_t m = key[0];
