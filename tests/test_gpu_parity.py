@@ -56,7 +56,19 @@ def test_router_topk_config_rows(B):
     assert np.array_equal(u16(scores), ws)
 
 
-@pytest.mark.parametrize("N,k", [(256, 8), (128, 8), (1024, 16), (64, 64)])
+@pytest.mark.parametrize("N,k", [(128, 64), (128, 65), (256, 100), (1024, 200)])
+@pytest.mark.parametrize("norm", [True, False])
+def test_router_topk_wide_k_bit_exact(N, k, norm):
+    """Both slot paths of the top-k: k <= 64 keeps slot j in lane j, more slots go through LDS."""
+    for t in range(6):
+        lg = router_logits(t % 4, 1 + t % 3, N, seed=5000 + N + k + t)
+        inds, scores = ops.router_topk(bf16_tensor(lg, DEV), k, norm)
+        wi, ws, _ = oracle.router_topk(lg, k, norm)
+        assert np.array_equal(inds.cpu().numpy().view(np.uint32), wi), t
+        assert np.array_equal(u16(scores), ws), t
+
+
+@pytest.mark.parametrize("N,k", [(256, 8), (128, 8), (1024, 16), (64, 64), (1024, 100)])
 def test_topk_from_gates_bit_exact(N, k):
     for t in range(12):
         g = tie_gates(3, N, seed=400 + t) if t % 2 else oracle.softmax_bf16(router_logits(t % 4, 3, N, seed=400 + t))
