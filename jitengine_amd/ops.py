@@ -145,14 +145,25 @@ def moe_pack_into(inds: torch.Tensor, pk: Packing) -> None:
 ROUTE_PACK_MAX_ROWS = 4
 
 
-def route_pack(logits: torch.Tensor, k: int, norm: bool):
+def _tables_for(pk: Packing | None, P: int, k: int, E: int, device) -> Packing:
+    """pk when it is sized for P pairs of k slots over E experts (ValueError otherwise), new tables
+    when it is None."""
+    if pk is None:
+        return _packing_buffers(P, k, E, device)
+    if (pk.P, pk.k, pk.E) != (P, k, E):
+        raise ValueError(f"packing tables of (P, k, E) = {(pk.P, pk.k, pk.E)}, the call needs {(P, k, E)}")
+    return pk
+
+
+def route_pack(logits: torch.Tensor, k: int, norm: bool, pk: Packing | None = None):
     """router_topk then moe_pack of at most ROUTE_PACK_MAX_ROWS rows in one launch (jit_route_pack):
-    (inds, scores, Packing), bit for bit the two-launch result; the expert count is N."""
+    (inds, scores, Packing), bit for bit the two-launch result; the expert count is N.  The tables
+    go into pk when given."""
     _need(logits, torch.bfloat16, "logits")
     rows, n = logits.shape
     inds = torch.empty((rows, k), dtype=torch.int32, device=logits.device)
     scores = torch.empty((rows, k), dtype=torch.bfloat16, device=logits.device)
-    pk = _packing_buffers(rows * k, k, n, logits.device)
+    pk = _tables_for(pk, rows * k, k, n, logits.device)
     _lib.check(
         _lib.lib().jit_route_pack(
             _p(logits), rows, n, int(k), int(bool(norm)), _p(inds), _p(scores), _p(pk.order), _p(pk.pair_row),
@@ -164,10 +175,10 @@ def route_pack(logits: torch.Tensor, k: int, norm: bool):
     return inds, scores, pk
 
 
-def route_gate_up(x: torch.Tensor, logits: torch.Tensor, gate_up, k: int, norm: bool):
+def route_gate_up(x: torch.Tensor, logits: torch.Tensor, gate_up, k: int, norm: bool, pk: Packing | None = None):
     """One token's route_pack and expert_gate_up in one launch (jit_moe_gate_up_swiglu_routed_packed):
     x [1, K] bf16, logits [1, E] bf16, a packed [E, 2I, K] stack -> (inds, scores, Packing, h), bit
-    for bit the two launches' results."""
+    for bit the two launches' results.  The tables go into pk when given."""
     _need(x, torch.bfloat16, "x")
     _need(logits, torch.bfloat16, "logits")
     _need_packed(gate_up, "route_gate_up")
@@ -179,7 +190,7 @@ def route_gate_up(x: torch.Tensor, logits: torch.Tensor, gate_up, k: int, norm: 
     I = gate_up.out_dims // 2
     inds = torch.empty((1, k), dtype=torch.int32, device=x.device)
     scores = torch.empty((1, k), dtype=torch.bfloat16, device=x.device)
-    pk = _packing_buffers(k, k, E, x.device)
+    pk = _tables_for(pk, k, k, E, x.device)
     h = torch.empty((k, I), dtype=torch.bfloat16, device=x.device)
     _lib.check(
         _lib.lib().jit_moe_gate_up_swiglu_routed_packed(

@@ -8,7 +8,9 @@ Host-side structures of jitengine_amd.ops are passed as their tensors and sizes:
   * a packed 4-bit matrix or expert stack (ops.PackedQ4) as its uint8 tensor and (E, N, K);
   * the packing tables (ops.Packing) as the single int32 buffer moe_pack returns, with (k, E);
   * a decode attention plan (ops.AttnPlan) as its three int32 tensors, its chunk count and the
-    longest sequence.
+    longest sequence (plan_args);
+  * a prefill plan (ops.PrefillPlan) as its two int32 tables, its chunks flattened into (seq, ctx,
+    length) triples, its most key parts of a token and its longest chunk (prefill_plan_args).
 Importing this module registers the operators; it needs the HIP library only when one runs.
 """
 
@@ -62,6 +64,23 @@ def _(inds, n_experts):
     return inds.new_empty((3 * P + 5 * n_experts + 4,), dtype=torch.int32)
 
 
+@torch.library.custom_op(f"{_NS}::route_pack", mutates_args=())
+def route_pack(logits: torch.Tensor, k: int, norm: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(inds, scores, packing buffer) of at most 4 router rows in one launch (jit_route_pack): the
+    router_topk and moe_pack results."""
+    rows, E = logits.shape
+    buf = torch.empty(3 * rows * k + 5 * E + 4, dtype=torch.int32, device=logits.device)
+    inds, scores, _ = ops.route_pack(logits, k, norm, pk=packing_from_buffer(buf, k, E))
+    return inds, scores, buf
+
+
+@route_pack.register_fake
+def _(logits, k, norm):
+    rows, E = logits.shape
+    return (logits.new_empty((rows, k), dtype=torch.int32), logits.new_empty((rows, k), dtype=torch.bfloat16),
+            logits.new_empty((3 * rows * k + 5 * E + 4,), dtype=torch.int32))
+
+
 # ----------------------------------------------------------------------------- experts
 @torch.library.custom_op(f"{_NS}::expert_gate_up", mutates_args=())
 def expert_gate_up(x: torch.Tensor, packed: torch.Tensor, E: int, N: int, K: int, pack_buf: torch.Tensor,
@@ -75,6 +94,23 @@ def expert_gate_up(x: torch.Tensor, packed: torch.Tensor, E: int, N: int, K: int
 def _(x, packed, E, N, K, pack_buf, k, seg):
     P = (pack_buf.shape[0] - 5 * E - 4) // 3
     return x.new_empty((P, N // 2), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{_NS}::route_gate_up", mutates_args=())
+def route_gate_up(x: torch.Tensor, logits: torch.Tensor, packed: torch.Tensor, E: int, N: int, K: int, k: int,
+                  norm: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(inds, scores, packing buffer, h) of one token: route_pack and expert_gate_up in one launch
+    (jit_moe_gate_up_swiglu_routed_packed)."""
+    buf = torch.empty(3 * k + 5 * E + 4, dtype=torch.int32, device=x.device)
+    inds, scores, _, h = ops.route_gate_up(x, logits, _packed(packed, E, N, K), k, norm,
+                                           pk=packing_from_buffer(buf, k, E))
+    return inds, scores, buf, h
+
+
+@route_gate_up.register_fake
+def _(x, logits, packed, E, N, K, k, norm):
+    return (x.new_empty((1, k), dtype=torch.int32), x.new_empty((1, k), dtype=torch.bfloat16),
+            x.new_empty((3 * k + 5 * E + 4,), dtype=torch.int32), x.new_empty((k, N // 2), dtype=torch.bfloat16))
 
 
 @torch.library.custom_op(f"{_NS}::expert_down", mutates_args=())
@@ -102,6 +138,19 @@ def _(r, pack_buf, k, E, scores, resid):
     return r.new_empty((scores.shape[0], r.shape[1]), dtype=torch.bfloat16)
 
 
+@torch.library.custom_op(f"{_NS}::moe_combine_rmsnorm", mutates_args=())
+def moe_combine_rmsnorm(r: torch.Tensor, pack_buf: torch.Tensor, k: int, E: int, scores: torch.Tensor,
+                        resid: torch.Tensor | None, w: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(y, xn): moe_combine and the RMSNorm of its rows in one launch (jit_moe_combine_rmsnorm)."""
+    return ops.moe_combine_rmsnorm(r, packing_from_buffer(pack_buf, k, E), scores, resid, w, eps)
+
+
+@moe_combine_rmsnorm.register_fake
+def _(r, pack_buf, k, E, scores, resid, w, eps):
+    y = r.new_empty((scores.shape[0], r.shape[1]), dtype=torch.bfloat16)
+    return y, torch.empty_like(y)
+
+
 # ----------------------------------------------------------------------------- dense, norms
 @torch.library.custom_op(f"{_NS}::qmm", mutates_args=())
 def qmm(x: torch.Tensor, packed: torch.Tensor, N: int, K: int) -> torch.Tensor:
@@ -124,6 +173,45 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
 @rmsnorm.register_fake
 def _(x, w, eps):
     return torch.empty_like(x)
+
+
+@torch.library.custom_op(f"{_NS}::rmsnorm_add", mutates_args=())
+def rmsnorm_add(x: torch.Tensor, resid: torch.Tensor, w: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(RMSNorm of h, h) for h = x + resid, in one launch (jit_rmsnorm with a residual)."""
+    return ops.rmsnorm(x, w, eps, resid, return_sum=True)
+
+
+@rmsnorm_add.register_fake
+def _(x, resid, w, eps):
+    return torch.empty_like(x), torch.empty_like(x)
+
+
+@torch.library.custom_op(f"{_NS}::qmm_add_rmsnorm", mutates_args=())
+def qmm_add_rmsnorm(a: torch.Tensor, resid: torch.Tensor, w: torch.Tensor, eps: float, packed: torch.Tensor, N: int,
+                    K: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(y, h, hn) of one row: h = a + resid, hn its RMSNorm, y = hn against a packed 4-bit [N, K]
+    matrix, in one launch (jit_qmm_packed_add_rmsnorm)."""
+    return ops.qmm_add_rmsnorm(a, resid, w, eps, _packed(packed, 1, N, K))
+
+
+@qmm_add_rmsnorm.register_fake
+def _(a, resid, w, eps, packed, N, K):
+    return a.new_empty((1, N), dtype=torch.bfloat16), torch.empty_like(a), torch.empty_like(a)
+
+
+@torch.library.custom_op(f"{_NS}::qmm_combine_rmsnorm", mutates_args=())
+def qmm_combine_rmsnorm(r: torch.Tensor, pack_buf: torch.Tensor, k: int, E: int, scores: torch.Tensor,
+                        resid: torch.Tensor | None, w: torch.Tensor, eps: float, packed: torch.Tensor, N: int,
+                        K: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(y, out) of one row: y = moe_combine, out = its RMSNorm against a packed 4-bit [N, K] matrix,
+    in one launch (jit_qmm_packed_combine_rmsnorm)."""
+    return ops.qmm_combine_rmsnorm(r, packing_from_buffer(pack_buf, k, E), scores, resid, w, eps,
+                                   _packed(packed, 1, N, K))
+
+
+@qmm_combine_rmsnorm.register_fake
+def _(r, pack_buf, k, E, scores, resid, w, eps, packed, N, K):
+    return r.new_empty((1, r.shape[1]), dtype=torch.bfloat16), r.new_empty((1, N), dtype=torch.bfloat16)
 
 
 # ----------------------------------------------------------------------------- attention
@@ -154,6 +242,71 @@ def paged_decode_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torc
 @paged_decode_attention.register_fake
 def _(q, pool, page_table, lens, chunk_start, chunk_seq, total, max_len, scale, workspace):
     return torch.empty_like(q)
+
+
+@torch.library.custom_op(f"{_NS}::paged_decode_attention_qkv", mutates_args=("pool", "workspace"))
+def paged_decode_attention_qkv(qkv: torch.Tensor, H: int, Hkv: int, q_norm: torch.Tensor, k_norm: torch.Tensor,
+                               eps: float, inv_freq: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor,
+                               lens: torch.Tensor, chunk_start: torch.Tensor, chunk_seq: torch.Tensor, total: int,
+                               max_len: int, scale: float, workspace: torch.Tensor) -> torch.Tensor:
+    """out bf16 [B, H, 128] of the step's raw qkv rows: qk_norm_rope_append of each token at position
+    lens[b] - 1 and split-K paged decode attention in one launch (jit_paged_decode_attn_qkv)."""
+    plan = ops.AttnPlan(lens, chunk_start, chunk_seq, int(total), np.array([int(max_len)], np.int32))
+    return ops.paged_decode_attention_qkv(qkv, H, Hkv, q_norm, k_norm, eps, inv_freq, pool, page_table, plan, scale,
+                                          workspace)
+
+
+@paged_decode_attention_qkv.register_fake
+def _(qkv, H, Hkv, q_norm, k_norm, eps, inv_freq, pool, page_table, lens, chunk_start, chunk_seq, total, max_len,
+      scale, workspace):
+    return qkv.new_empty((qkv.shape[0], H, ops.HEAD_DIM), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{_NS}::paged_prefill_attention", mutates_args=("workspace",))
+def paged_prefill_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torch.Tensor, tables: torch.Tensor,
+                            blocks: torch.Tensor, chunks: list[int], pmax: int, max_len: int, scale: float,
+                            workspace: torch.Tensor) -> torch.Tensor:
+    """out bf16 [T, H, 128]: causal attention of prefill chunks over the paged pool, under a prefill
+    plan given by its tensors and its chunks flattened as (seq, ctx, length) triples
+    (jit_paged_prefill_attn; workspace of prefill_workspace_bytes bytes)."""
+    trip = [tuple(chunks[i:i + 3]) for i in range(0, len(chunks), 3)]
+    plan = ops.PrefillPlan(trip, tables, blocks, sum(c[2] for c in trip), int(pmax), int(max_len))
+    return ops.paged_prefill_attention(q, pool, page_table, plan, scale, workspace)
+
+
+@paged_prefill_attention.register_fake
+def _(q, pool, page_table, tables, blocks, chunks, pmax, max_len, scale, workspace):
+    return torch.empty_like(q)
+
+
+def prefill_plan_args(plan: ops.PrefillPlan) -> tuple:
+    """(tables, blocks, chunks, pmax, max_len) of a prefill plan, for
+    torch.ops.jitengine.paged_prefill_attention."""
+    return plan.tables, plan.blocks, [int(v) for c in plan.chunks for v in c], plan.pmax, plan.max_len
+
+
+# ----------------------------------------------------------------------------- paged KV
+@torch.library.custom_op(f"{_NS}::kv_append_paged", mutates_args=("pool",))
+def kv_append_paged(pool: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor,
+                    page_table: torch.Tensor) -> None:
+    """k, v [B, Hkv, 128] written at positions pos [B] of the paged pool (jit_kv_append_paged)."""
+    ops.kv_append_paged(pool, k, v, pos, page_table)
+
+
+@kv_append_paged.register_fake
+def _(pool, k, v, pos, page_table):
+    return None
+
+
+@torch.library.custom_op(f"{_NS}::kv_copy_pages", mutates_args=("pool",))
+def kv_copy_pages(pool: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) -> None:
+    """Pages src[i] copied to dst[i] inside one layer's pool (jit_kv_copy_pages)."""
+    ops.kv_copy_pages(pool, src, dst)
+
+
+@kv_copy_pages.register_fake
+def _(pool, src, dst):
+    return None
 
 
 def plan_args(plan: ops.AttnPlan) -> tuple:
@@ -208,6 +361,7 @@ def _(keys):
     return keys.new_empty((keys.shape[0],), dtype=torch.float32)
 
 
-OPS = ("router_topk", "moe_pack", "expert_gate_up", "expert_down", "moe_combine", "qmm", "rmsnorm",
-       "qk_norm_rope_append", "paged_decode_attention", "logprobs_rows", "argmax_rows", "sample_rows",
-       "threefry_uniform")
+OPS = ("router_topk", "moe_pack", "route_pack", "expert_gate_up", "route_gate_up", "expert_down", "moe_combine",
+       "moe_combine_rmsnorm", "qmm", "rmsnorm", "rmsnorm_add", "qmm_add_rmsnorm", "qmm_combine_rmsnorm",
+       "qk_norm_rope_append", "paged_decode_attention", "paged_decode_attention_qkv", "paged_prefill_attention",
+       "kv_append_paged", "kv_copy_pages", "logprobs_rows", "argmax_rows", "sample_rows", "threefry_uniform")

@@ -1,6 +1,7 @@
 """torch.ops.jitengine.* on MI355X: every registered operator gives the bits of the
-jitengine_amd.ops call it wraps, and torch.compile traces a decoder layer's MoE half through
-them in one graph (fullgraph, no graph break) with the eager result."""
+jitengine_amd.ops call it wraps, and torch.compile traces a decoder layer's MoE half -- the
+batched launches and the one-token fused ones -- through them in one graph (fullgraph, no graph
+break) with the eager result."""
 
 from __future__ import annotations
 
@@ -104,6 +105,113 @@ def test_dense_norm_attention_and_sampler_operators():
     assert torch.equal(J.sample_rows(logits, 0.7, 0.9, 20, u), ops.sample_rows(logits, 0.7, 0.9, 20, u))
     keys = _i32(np.arange(8, dtype=np.uint32).reshape(4, 2) * np.uint32(2654435761))
     assert torch.equal(J.threefry_uniform(keys), ops.threefry_uniform(keys))
+
+
+def _norm_w(n, seed):
+    return (1 + 0.05 * bf16_tensor(normal_bf16((n,), seed=seed), DEV).float()).to(torch.bfloat16)
+
+
+def _one_token_moe_half(gu, dn, x, logits, h, w, qkv_lin):
+    """A one-token layer's MoE half and the next layer's qkv projection: three launches."""
+    inds, scores, buf, hh = J.route_gate_up(x, logits, gu.data, gu.E, gu.N, gu.K, K_TOP, True)
+    r = J.expert_down(hh, dn.data, dn.E, dn.N, dn.K, buf, K_TOP, False)
+    return J.qmm_combine_rmsnorm(r, buf, K_TOP, E, scores, h, w, 1e-6, qkv_lin.data, qkv_lin.N, qkv_lin.K)
+
+
+def test_fused_moe_and_row_operators_equal_the_library_calls(moe):
+    gu, dn, x, logits, resid = moe
+    inds, scores, pk = ops.route_pack(logits[:4], K_TOP, True)
+    ji, js, jb = J.route_pack(logits[:4], K_TOP, True)
+    jpk = torch_ops.packing_from_buffer(jb, K_TOP, E)
+    assert torch.equal(ji, inds) and torch.equal(js, scores)
+    for name in ("order", "pair_row", "inv", "expert_cnt", "expert_off", "meta"):
+        assert torch.equal(getattr(jpk, name), getattr(pk, name)), name
+    nseg = int(pk.meta[0])  # the segment tables are defined up to the segment count
+    for name in ("seg_expert", "seg_start", "seg_cnt"):
+        assert torch.equal(getattr(jpk, name)[:nseg], getattr(pk, name)[:nseg]), name
+
+    x1, l1 = x[:1].contiguous(), logits[:1].contiguous()
+    inds, scores, pk, hh = ops.route_gate_up(x1, l1, gu, K_TOP, True)
+    ji, js, jb, jh = J.route_gate_up(x1, l1, gu.data, gu.E, gu.N, gu.K, K_TOP, True)
+    jpk = torch_ops.packing_from_buffer(jb, K_TOP, E)
+    assert torch.equal(ji, inds) and torch.equal(js, scores) and torch.equal(jh, hh)
+    assert torch.equal(jpk.inv, pk.inv) and torch.equal(jpk.order, pk.order)
+
+    r = ops.expert_down(hh, dn, pk)
+    w = _norm_w(D, 91)
+    y, xn = ops.moe_combine_rmsnorm(r, pk, scores, resid[:1], w, 1e-6)
+    jy, jxn = J.moe_combine_rmsnorm(r, jb, K_TOP, E, js, resid[:1], w, 1e-6)
+    assert torch.equal(jy, y) and torch.equal(jxn, xn)
+    lin = ops.prepack(make_stack((128, D), seed=92).to(DEV))
+    y, out = ops.qmm_combine_rmsnorm(r, pk, scores, resid[:1], w, 1e-6, lin)
+    jy, jout = J.qmm_combine_rmsnorm(r, jb, K_TOP, E, js, resid[:1], w, 1e-6, lin.data, lin.N, lin.K)
+    assert torch.equal(jy, y) and torch.equal(jout, out)
+    a = resid[1:2].contiguous()
+    want = ops.qmm_add_rmsnorm(a, x1, w, 1e-6, lin)
+    got = J.qmm_add_rmsnorm(a, x1, w, 1e-6, lin.data, lin.N, lin.K)
+    assert all(torch.equal(g, e) for g, e in zip(got, want))
+    want = ops.rmsnorm(x, w, 1e-6, resid, return_sum=True)
+    got = J.rmsnorm_add(x, resid, w, 1e-6)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+
+
+def test_one_token_moe_half_compiles_into_one_graph(moe):
+    gu, dn, x, logits, resid = moe
+    args = (gu, dn, x[:1].contiguous(), logits[:1].contiguous(), resid[:1].contiguous(), _norm_w(D, 93),
+            ops.prepack(make_stack((256, D), seed=94).to(DEV)))
+    eager = _one_token_moe_half(*args)
+    torch._dynamo.reset()
+    fn = torch.compile(_one_token_moe_half, fullgraph=True, backend="aot_eager")
+    for _ in range(2):
+        got = fn(*args)
+        assert torch.equal(got[0], eager[0]) and torch.equal(got[1], eager[1])
+
+
+def _paged(lens, seed, Hkv=4, extra=5):
+    rng = np.random.default_rng(seed)
+    npg = [-(-L // 16) for L in lens]
+    perm = rng.permutation(sum(npg) + extra)
+    table = np.zeros((len(lens), max(npg)), np.int32)
+    at = 0
+    for i, n in enumerate(npg):
+        table[i, :n] = perm[at:at + n]
+        at += n
+    return bf16_tensor(normal_bf16((sum(npg) + extra, Hkv, 2, 2048), seed=seed + 1), DEV), _i32(table)
+
+
+def test_fused_attention_prefill_and_kv_operators():
+    H, Hkv, scale = 32, 4, 128 ** -0.5
+    lens = [1, 300, 2000]
+    pool, table = _paged(lens, 95)
+    plan = ops.attn_plan(lens, DEV)
+    qkv = bf16_tensor(normal_bf16((3, (H + 2 * Hkv) * 128), seed=96, scale=1.5), DEV)
+    qn, kn = _norm_w(128, 97), _norm_w(128, 98)
+    inv = torch.from_numpy(_inv_freq()).to(DEV)
+    ws = torch.empty(ops.attn_workspace_bytes(plan.total, H), dtype=torch.uint8, device=DEV)
+    pool2 = pool.clone()
+    want = ops.paged_decode_attention_qkv(qkv, H, Hkv, qn, kn, 1e-6, inv, pool, table, plan, scale)
+    got = J.paged_decode_attention_qkv(qkv, H, Hkv, qn, kn, 1e-6, inv, pool2, table, *torch_ops.plan_args(plan),
+                                       scale, ws)
+    assert torch.equal(got, want) and torch.equal(pool2, pool)
+
+    chunks = [(0, 0, 37), (1, 100, 64), (2, 1900, 100)]
+    pp = ops.prefill_plan(chunks, H, Hkv, DEV)
+    q = bf16_tensor(normal_bf16((pp.rows, H, 128), seed=99), DEV)
+    pws = torch.empty(max(ops.prefill_workspace_bytes(pp, H), 4), dtype=torch.uint8, device=DEV)
+    want = ops.paged_prefill_attention(q, pool, table, pp, scale)
+    got = J.paged_prefill_attention(q, pool, table, *torch_ops.prefill_plan_args(pp), scale, pws)
+    assert torch.equal(got, want)
+
+    k = bf16_tensor(normal_bf16((3, Hkv, 128), seed=100), DEV)
+    v = bf16_tensor(normal_bf16((3, Hkv, 128), seed=101), DEV)
+    pos = _i32(np.array([0, 299, 1999], np.int32))
+    ops.kv_append_paged(pool, k, v, pos, table)
+    J.kv_append_paged(pool2, k, v, pos, table)
+    assert torch.equal(pool2, pool)
+    src, dst = _i32(np.array([0, 3], np.int32)), _i32(np.array([pool.shape[0] - 1, pool.shape[0] - 2], np.int32))
+    ops.kv_copy_pages(pool, src, dst)
+    J.kv_copy_pages(pool2, src, dst)
+    assert torch.equal(pool2, pool)
 
 
 def _inv_freq():

@@ -72,3 +72,40 @@ def test_packing_buffer_split_matches_the_library_layout():
     for name in ("order", "pair_row", "inv", "expert_cnt", "expert_off", "seg_expert", "seg_start", "seg_cnt", "meta"):
         assert getattr(pk, name).shape == getattr(ref, name).shape, name
     assert int(pk.expert_cnt[0]) == 3 * 24 and int(pk.meta[0]) == 3 * 24 + 5 * 16
+
+
+def test_fused_launches_propagate_shapes():
+    E, k, D, I, N = 128, 8, 2048, 768, 5120
+    bf, i32 = torch.bfloat16, torch.int32
+    inds, scores, buf = J.route_pack(_m((4, E), bf), k, True)
+    assert inds.shape == (4, k) and scores.dtype == bf and buf.shape == (3 * 4 * k + 5 * E + 4,)
+    inds, scores, buf, h = J.route_gate_up(_m((1, D), bf), _m((1, E), bf), _m((10,), torch.uint8), E, 2 * I, D, k,
+                                           True)
+    assert inds.shape == (1, k) and buf.shape == (3 * k + 5 * E + 4,) and h.shape == (k, I) and h.dtype == bf
+    r = _m((k, D), bf)
+    y, xn = J.moe_combine_rmsnorm(r, buf, k, E, scores, _m((1, D), bf), _m((D,), bf), 1e-6)
+    assert y.shape == xn.shape == (1, D)
+    y, out = J.qmm_combine_rmsnorm(r, buf, k, E, scores, None, _m((D,), bf), 1e-6, _m((10,), torch.uint8), N, D)
+    assert y.shape == (1, D) and out.shape == (1, N) and out.dtype == bf
+    y, h, hn = J.qmm_add_rmsnorm(_m((1, D), bf), _m((1, D), bf), _m((D,), bf), 1e-6, _m((10,), torch.uint8), E, D)
+    assert y.shape == (1, E) and h.shape == hn.shape == (1, D)
+    xn, h = J.rmsnorm_add(_m((3, D), bf), _m((3, D), bf), _m((D,), bf), 1e-6)
+    assert xn.shape == h.shape == (3, D)
+
+
+def test_attention_and_kv_operators_propagate_shapes():
+    B, H, Hkv = 3, 32, 4
+    bf, i32 = torch.bfloat16, torch.int32
+    pool = _m((64, Hkv, 2, 2048), bf)
+    out = J.paged_decode_attention_qkv(_m((B, (H + 2 * Hkv) * 128), bf), H, Hkv, _m((128,), bf), _m((128,), bf), 1e-6,
+                                       _m((64,), torch.float32), pool, _m((B, 16), i32), _m((B,), i32),
+                                       _m((B + 1,), i32), _m((8,), i32), 8, 200, 128 ** -0.5,
+                                       _m((1 << 16,), torch.uint8))
+    assert out.shape == (B, H, 128) and out.dtype == bf
+    q = _m((70, H, 128), bf)
+    o = J.paged_prefill_attention(q, pool, _m((2, 16), i32), _m((4, 2), i32), _m((3, 5), i32), [0, 0, 50, 1, 30, 20],
+                                  1, 50, 128 ** -0.5, _m((16,), torch.uint8))
+    assert o.shape == q.shape
+    assert J.kv_append_paged(pool, _m((B, Hkv, 128), bf), _m((B, Hkv, 128), bf), _m((B,), i32),
+                             _m((B, 16), i32)) is None
+    assert J.kv_copy_pages(pool, _m((2,), i32), _m((2,), i32)) is None
