@@ -214,6 +214,37 @@ def test_fused_attention_prefill_and_kv_operators():
     assert torch.equal(pool2, pool)
 
 
+def test_attention_half_compiles_into_one_graph():
+    """The attention half of a decode layer -- attention with the q/k/v rows (which writes the tokens'
+    K and V into the pool) and the o projection -- under torch.compile (fullgraph): the mutated pool
+    and the output equal the eager calls', on two calls in a row."""
+    H, Hkv, scale = 32, 4, 128 ** -0.5
+    lens = [7, 300, 1600]
+    pool0, table = _paged(lens, 120)
+    plan = ops.attn_plan(lens, DEV)
+    qkv = bf16_tensor(normal_bf16((3, (H + 2 * Hkv) * 128), seed=121, scale=1.5), DEV)
+    qn, kn = _norm_w(128, 122), _norm_w(128, 123)
+    inv = torch.from_numpy(_inv_freq()).to(DEV)
+    o_lin = ops.prepack(make_stack((512, H * 128), seed=124).to(DEV))
+    ws = torch.empty(ops.attn_workspace_bytes(plan.total, H), dtype=torch.uint8, device=DEV)
+    args = torch_ops.plan_args(plan)
+
+    def half(qkv, pool):
+        attn = J.paged_decode_attention_qkv(qkv, H, Hkv, qn, kn, 1e-6, inv, pool, table, *args, scale, ws)
+        return J.qmm(attn.view(attn.shape[0], -1), o_lin.data, o_lin.N, o_lin.K)
+
+    pool_e = pool0.clone()
+    want = half(qkv, pool_e)
+    torch._dynamo.reset()
+    fn = torch.compile(half, fullgraph=True, backend="aot_eager")
+    for _ in range(2):
+        pool_c = pool0.clone()
+        got = fn(qkv, pool_c)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+        assert torch.equal(pool_c, pool_e)  # the tokens' K and V written through the compiled graph
+
+
 def _inv_freq():
     from jitengine_amd.model import rope_inv_freq
 
