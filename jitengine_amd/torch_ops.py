@@ -35,6 +35,12 @@ def packing_from_buffer(buf: torch.Tensor, k: int, E: int) -> ops.Packing:
     return ops.Packing(*parts, P=P, k=k, E=E)
 
 
+def _packing_buffer(P: int, E: int, device) -> torch.Tensor:
+    """A zeroed packing buffer: the launches define the segment tables only up to the segment count
+    (meta[0]), and an operator's outputs must not depend on what the memory held before."""
+    return torch.zeros(3 * P + 5 * E + 4, dtype=torch.int32, device=device)
+
+
 # ----------------------------------------------------------------------------- router
 @torch.library.custom_op(f"{_NS}::router_topk", mutates_args=())
 def router_topk(logits: torch.Tensor, k: int, norm: bool) -> tuple[torch.Tensor, torch.Tensor]:
@@ -51,9 +57,9 @@ def _(logits, k, norm):
 @torch.library.custom_op(f"{_NS}::moe_pack", mutates_args=())
 def moe_pack(inds: torch.Tensor, n_experts: int) -> torch.Tensor:
     """The packing tables of inds [B, k] as one int32 buffer [3 P + 5 E + 4] (jit_moe_pack;
-    packing_from_buffer splits it)."""
+    packing_from_buffer splits it; segment entries past the segment count are zero)."""
     P, E = inds.numel(), int(n_experts)
-    buf = torch.empty(3 * P + 5 * E + 4, dtype=torch.int32, device=inds.device)
+    buf = _packing_buffer(P, E, inds.device)
     ops.moe_pack_into(inds, packing_from_buffer(buf, inds.shape[-1], E))
     return buf
 
@@ -69,7 +75,7 @@ def route_pack(logits: torch.Tensor, k: int, norm: bool) -> tuple[torch.Tensor, 
     """(inds, scores, packing buffer) of at most 4 router rows in one launch (jit_route_pack): the
     router_topk and moe_pack results."""
     rows, E = logits.shape
-    buf = torch.empty(3 * rows * k + 5 * E + 4, dtype=torch.int32, device=logits.device)
+    buf = _packing_buffer(rows * k, E, logits.device)
     inds, scores, _ = ops.route_pack(logits, k, norm, pk=packing_from_buffer(buf, k, E))
     return inds, scores, buf
 
@@ -101,7 +107,7 @@ def route_gate_up(x: torch.Tensor, logits: torch.Tensor, packed: torch.Tensor, E
                   norm: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """(inds, scores, packing buffer, h) of one token: route_pack and expert_gate_up in one launch
     (jit_moe_gate_up_swiglu_routed_packed)."""
-    buf = torch.empty(3 * k + 5 * E + 4, dtype=torch.int32, device=x.device)
+    buf = _packing_buffer(k, E, x.device)
     inds, scores, _, h = ops.route_gate_up(x, logits, _packed(packed, E, N, K), k, norm,
                                            pk=packing_from_buffer(buf, k, E))
     return inds, scores, buf, h

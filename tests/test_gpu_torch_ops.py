@@ -245,6 +245,67 @@ def test_attention_half_compiles_into_one_graph():
         assert torch.equal(pool_c, pool_e)  # the tokens' K and V written through the compiled graph
 
 
+def test_opcheck_schemas_fakes_and_mutations(moe):
+    """torch.library.opcheck on every registered operator with real inputs: the schema (declared
+    mutations match what the call writes), the fake kernel against the real outputs, and tracing
+    with dynamic shapes."""
+    gu, dn, x, logits, resid = moe
+    inds, scores = ops.router_topk(logits, K_TOP, True)
+    buf = J.moe_pack(inds, E)
+    h = J.expert_gate_up(x, gu.data, gu.E, gu.N, gu.K, buf, K_TOP, False)
+    w = _norm_w(D, 131)
+    cases = [
+        (J.router_topk, (logits, K_TOP, True)),
+        (J.moe_pack, (inds, E)),
+        (J.route_pack, (logits[:4].contiguous(), K_TOP, True)),
+        (J.expert_gate_up, (x, gu.data, gu.E, gu.N, gu.K, buf, K_TOP, False)),
+        (J.expert_down, (h, dn.data, dn.E, dn.N, dn.K, buf, K_TOP, True)),
+        (J.moe_combine_rmsnorm, (J.expert_down(h, dn.data, dn.E, dn.N, dn.K, buf, K_TOP, False), buf, K_TOP, E,
+                                 scores, resid, w, 1e-6)),
+        (J.rmsnorm_add, (x, resid, w, 1e-6)),
+    ]
+    H, Hkv = 32, 4
+    lens = [5, 300]
+    pool, table = _paged(lens, 132)
+    plan = ops.attn_plan(lens, DEV)
+    qkv = bf16_tensor(normal_bf16((2, (H + 2 * Hkv) * 128), seed=133), DEV)
+    ws = torch.empty(ops.attn_workspace_bytes(plan.total, H), dtype=torch.uint8, device=DEV)
+    cases.append((J.paged_decode_attention_qkv, (qkv, H, Hkv, _norm_w(128, 134), _norm_w(128, 135), 1e-6,
+                                                 torch.from_numpy(_inv_freq()).to(DEV), pool, table,
+                                                 *torch_ops.plan_args(plan), 128 ** -0.5, ws)))
+    kv = bf16_tensor(normal_bf16((2, Hkv, 128), seed=136), DEV)
+    cases.append((J.kv_append_paged, (pool, kv, kv, _i32(np.array([4, 299], np.int32)), table)))
+    q = bf16_tensor(normal_bf16((2, H, 128), seed=137), DEV)
+    cases.append((J.paged_decode_attention, (q, pool, table, *torch_ops.plan_args(plan), 128 ** -0.5, ws)))
+    inv = torch.from_numpy(_inv_freq()).to(DEV)
+    cases.append((J.qk_norm_rope_append, (qkv, H, Hkv, _norm_w(128, 138), _norm_w(128, 139), 1e-6, inv,
+                                          _i32(np.array([4, 299], np.int32)), table, pool)))
+    pp = ops.prefill_plan([(0, 0, 5), (1, 200, 40)], H, Hkv, DEV)
+    qp = bf16_tensor(normal_bf16((pp.rows, H, 128), seed=140), DEV)
+    pws = torch.empty(max(ops.prefill_workspace_bytes(pp, H), 4), dtype=torch.uint8, device=DEV)
+    cases.append((J.paged_prefill_attention, (qp, pool, table, *torch_ops.prefill_plan_args(pp), 128 ** -0.5, pws)))
+    cases.append((J.kv_copy_pages, (pool, _i32(np.array([0], np.int32)), _i32(np.array([pool.shape[0] - 1],
+                                                                                        np.int32)))))
+    lin = ops.prepack(make_stack((128, D), seed=141).to(DEV))
+    x1 = x[:1].contiguous()
+    cases.append((J.qmm, (x, lin.data, lin.N, lin.K)))
+    cases.append((J.rmsnorm, (x, w, 1e-6)))
+    cases.append((J.qmm_add_rmsnorm, (x1, resid[:1].contiguous(), w, 1e-6, lin.data, lin.N, lin.K)))
+    i1, s1, b1, h1 = J.route_gate_up(x1, logits[:1].contiguous(), gu.data, gu.E, gu.N, gu.K, K_TOP, True)
+    cases.append((J.route_gate_up, (x1, logits[:1].contiguous(), gu.data, gu.E, gu.N, gu.K, K_TOP, True)))
+    r1 = J.expert_down(h1, dn.data, dn.E, dn.N, dn.K, b1, K_TOP, False)
+    cases.append((J.qmm_combine_rmsnorm, (r1, b1, K_TOP, E, s1, resid[:1].contiguous(), w, 1e-6, lin.data, lin.N,
+                                          lin.K)))
+    cases.append((J.moe_combine, (r1, b1, K_TOP, E, s1, None)))
+    lg = bf16_tensor(sampler_logits(0, 3, 1001, 142, scale=3.0), DEV)
+    u = torch.tensor([0.2, 0.5, 0.9], dtype=torch.float32, device=DEV)
+    cases += [(J.logprobs_rows, (lg,)), (J.argmax_rows, (lg,)), (J.sample_rows, (lg, 0.7, 0.9, 20, u)),
+              (J.threefry_uniform, (_i32(np.arange(6, dtype=np.int32).reshape(3, 2)),))]
+    assert {op._qualified_op_name.split("::")[1] for op, _ in cases} == set(torch_ops.OPS)
+    for op, args in cases:
+        torch.library.opcheck(op, args)
+
+
 def _inv_freq():
     from jitengine_amd.model import rope_inv_freq
 
