@@ -83,7 +83,8 @@ int jit_topk(const uint16_t *gates, int rows, int N, int k, uint32_t *inds, void
  *   inv[P]        sorted position of flat pair f
  *   expert_cnt[E], expert_off[E]    pairs per expert and first sorted position
  *   seg_expert[E], seg_start[E], seg_cnt[E]   the first meta[0] entries list
- *                 the non-empty experts in ascending order
+ *                 the non-empty experts in ascending order (the entries past
+ *                 them are not written)
  *   meta[4]       {n_seg, max_cnt, bad_ids, 0}; bad_ids counts ids >= E (such
  *                 pairs are dropped: they appear in no segment)
  * Contract: P >= 0, k > 0, 0 < E <= 1024. */
