@@ -203,6 +203,15 @@ def route_gate_up(x: torch.Tensor, logits: torch.Tensor, gate_up, k: int, norm: 
     return inds, scores, pk, h
 
 
+def _need_pairs(pk: Packing, rows: int, k: int, r: torch.Tensor | None, what: str) -> None:
+    """The packing tables pk cover `rows` rows of k slots (P = rows k), and r (when given) holds their
+    P pair rows: the kernels index inv, pair_row and r by these counts."""
+    if pk.k != k or pk.P != rows * k:
+        raise ValueError(f"{what}: packing tables of P={pk.P}, k={pk.k} for {rows} rows of {k} slots")
+    if r is not None and (r.dim() != 2 or r.shape[0] != pk.P):
+        raise ValueError(f"{what}: r {tuple(r.shape)} must hold the {pk.P} pair rows")
+
+
 def _packing_buffers(P: int, k: int, E: int, device) -> Packing:
     buf = torch.empty(3 * P + 5 * E + 4, dtype=torch.int32, device=device)
     parts = torch.split(buf, [P, P, P, E, E, E, E, E, 4])
@@ -322,6 +331,7 @@ def expert_gate_up(x: torch.Tensor, gate_up, pk: Packing, seg: bool = False) -> 
     E = _experts_of(gate_up)
     if x.shape[-1] != gate_up.in_dims or E != pk.E:
         raise ValueError("x / stack / packing disagree on K or E")
+    _need_pairs(pk, x.shape[0], pk.k, None, "expert_gate_up")  # (the pairs' rows are rows of x)
     I = gate_up.out_dims // 2
     h = torch.empty((pk.P, I), dtype=torch.bfloat16, device=x.device)
     L = _lib.lib()
@@ -396,6 +406,7 @@ def moe_combine(r: torch.Tensor, pk: Packing, scores: torch.Tensor, resid: torch
         _need(resid, torch.bfloat16, "resid")
         if resid.shape != (B, D):
             raise ValueError("resid must be [B, D]")
+    _need_pairs(pk, B, k, r, "moe_combine")
     y = torch.empty((B, D), dtype=torch.bfloat16, device=r.device)
     _lib.check(
         _lib.lib().jit_moe_combine(_p(r), _p(pk.inv), _p(scores), B, k, D, _p(resid), _p(y), _stream()),
@@ -420,6 +431,7 @@ def moe_combine_rmsnorm(r: torch.Tensor, pk: Packing, scores: torch.Tensor, resi
             raise ValueError("resid must be [B, D]")
     if w.numel() != D:
         raise ValueError(f"norm weight of {w.numel()} for rows of {D}")
+    _need_pairs(pk, B, k, r, "moe_combine_rmsnorm")
     y = torch.empty((B, D), dtype=torch.bfloat16, device=r.device)
     xn = torch.empty_like(y)
     _lib.check(
@@ -481,6 +493,7 @@ def qmm_combine_rmsnorm(r: torch.Tensor, pk: Packing, scores: torch.Tensor, resi
     if w.numel() != D:
         raise ValueError(f"norm weight of {w.numel()} for rows of {D}")
     _need_row_prologue(lin, D, "qmm_combine_rmsnorm")
+    _need_pairs(pk, 1, k, r, "qmm_combine_rmsnorm")
     y = torch.empty((1, D), dtype=torch.bfloat16, device=r.device)
     out = torch.empty((1, lin.N), dtype=torch.bfloat16, device=r.device)
     _lib.check(

@@ -476,3 +476,28 @@ def test_empty_batches():
     assert ops.argmax_rows(torch.empty((0, 1000), dtype=torch.bfloat16, device=DEV)).shape == (0,)
     assert ops.embed_q4(torch.empty(0, dtype=torch.int32, device=DEV),
                         random_quantized((16, 128), 6, device=DEV)).shape == (0, 128)
+
+
+def test_expert_and_combine_calls_reject_mismatched_packing():
+    """Packing tables that do not match the rows they are used with are refused on the host, before a
+    kernel could index x, inv or r out of range: x with fewer rows than the tables' tokens, scores of
+    another slot count or row count, r of another row count."""
+    E, D, I, B, k = 16, 512, 256, 6, 4
+    rng = np.random.default_rng(90)
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(B)]).astype(np.int32)
+    pk = ops.moe_pack(_i32(inds), E)
+    gu = ops.prepack(make_stack((E, 2 * I, D), seed=91).to(DEV))
+    x = bf16_tensor(normal_bf16((B, D), seed=92), DEV)
+    with pytest.raises(ValueError):
+        ops.expert_gate_up(x[:B - 1].contiguous(), gu, pk)
+    r = bf16_tensor(normal_bf16((B * k, D), seed=93), DEV)
+    scores = bf16_tensor(normal_bf16((B, k), seed=94), DEV)
+    w = torch.ones(D, dtype=torch.bfloat16, device=DEV)
+    for sc, rr in ((scores[:, :k - 1].contiguous(), r), (scores[:B - 1].contiguous(), r),
+                   (torch.cat([scores, scores]), r), (scores, r[:B * k - 1].contiguous())):
+        with pytest.raises(ValueError):
+            ops.moe_combine(rr, pk, sc)
+        with pytest.raises(ValueError):
+            ops.moe_combine_rmsnorm(rr, pk, sc, None, w, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(ops.moe_combine(r, pk, scores), ops.moe_combine_rmsnorm(r, pk, scores, None, w, 1e-6)[0])
