@@ -243,6 +243,19 @@ class PackedQ4:
     def nbytes(self) -> int:
         return self.data.numel()
 
+    def __post_init__(self):
+        # the kernels read E * N * K / 2 nibbles and their scales from `data`: a tensor of another size
+        # (an operator handed a byte tensor and separate dims) is refused before anything reads it
+        if self.data.dtype != torch.uint8 or not self.data.is_contiguous():
+            raise ValueError("packed data must be a contiguous uint8 tensor")
+        need = packed_bytes(self.E, self.N, self.K)
+        if need <= 0:
+            raise _lib.UnsupportedShape(f"the packed layout takes N % 16 == 0 and K % 128 == 0, got "
+                                        f"[{self.E}, {self.N}, {self.K}]")
+        if self.data.numel() != need:
+            raise ValueError(f"packed data of {self.data.numel()} bytes for [{self.E}, {self.N}, {self.K}], "
+                             f"which takes {need}")
+
 
 def packed_bytes(E: int, N: int, K: int) -> int:
     return int(_lib.lib().jit_q4_packed_bytes(int(E), int(N), int(K)))

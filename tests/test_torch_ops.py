@@ -109,3 +109,19 @@ def test_attention_and_kv_operators_propagate_shapes():
     assert J.kv_append_paged(pool, _m((B, Hkv, 128), bf), _m((B, Hkv, 128), bf), _m((B,), i32),
                              _m((B, 16), i32)) is None
     assert J.kv_copy_pages(pool, _m((2,), i32), _m((2,), i32)) is None
+
+
+def test_packed_matrix_refuses_data_of_another_size():
+    """A PackedQ4 (what the operators build from a byte tensor and (E, N, K)) checks the byte count
+    against the layout before any kernel reads it."""
+    from jitengine_amd import ops
+
+    n = ops.packed_bytes(2, 32, 256)
+    assert n > 0
+    ops.PackedQ4(torch.zeros(n, dtype=torch.uint8), 2, 32, 256, True)
+    with pytest.raises(ValueError):
+        ops.PackedQ4(torch.zeros(n - 1, dtype=torch.uint8), 2, 32, 256, True)
+    with pytest.raises(ValueError):
+        ops.PackedQ4(torch.zeros(n // 4, dtype=torch.int32), 2, 32, 256, True)
+    with pytest.raises(ops._lib.UnsupportedShape):
+        ops.PackedQ4(torch.zeros(n, dtype=torch.uint8), 2, 33, 256, True)
