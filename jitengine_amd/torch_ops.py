@@ -240,7 +240,9 @@ def paged_decode_attention(q: torch.Tensor, pool: torch.Tensor, page_table: torc
                            chunk_start: torch.Tensor, chunk_seq: torch.Tensor, total: int, max_len: int,
                            scale: float, workspace: torch.Tensor) -> torch.Tensor:
     """out bf16 [B, H, 128] of split-K paged decode attention under an attention plan given by its
-    tensors (jit_paged_decode_attn; workspace of attn_workspace_bytes(total, H) bytes)."""
+    tensors (jit_paged_decode_attn; workspace of attn_workspace_bytes(total, H) bytes).  max_len is
+    the plan's longest sequence (plan_args gives it): the page table's width is checked against it,
+    the device tensors are not read on the host."""
     plan = ops.AttnPlan(lens, chunk_start, chunk_seq, int(total), np.array([int(max_len)], np.int32))
     return ops.paged_decode_attention(q, pool, page_table, plan, scale, workspace)
 
@@ -256,7 +258,8 @@ def paged_decode_attention_qkv(qkv: torch.Tensor, H: int, Hkv: int, q_norm: torc
                                lens: torch.Tensor, chunk_start: torch.Tensor, chunk_seq: torch.Tensor, total: int,
                                max_len: int, scale: float, workspace: torch.Tensor) -> torch.Tensor:
     """out bf16 [B, H, 128] of the step's raw qkv rows: qk_norm_rope_append of each token at position
-    lens[b] - 1 and split-K paged decode attention in one launch (jit_paged_decode_attn_qkv)."""
+    lens[b] - 1 and split-K paged decode attention in one launch (jit_paged_decode_attn_qkv).  The
+    plan's tensors and max_len as for paged_decode_attention."""
     plan = ops.AttnPlan(lens, chunk_start, chunk_seq, int(total), np.array([int(max_len)], np.int32))
     return ops.paged_decode_attention_qkv(qkv, H, Hkv, q_norm, k_norm, eps, inv_freq, pool, page_table, plan, scale,
                                           workspace)
