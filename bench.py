@@ -175,7 +175,9 @@ def bench_config1(steps: int, warmup: int, dev: str) -> dict:
     dn_bytes_e = D * I // 2 + 2 * D * (I // 64) * 2
     alg_gate_up = U * gu_bytes_e + B * D * 2 + P * I * 2
     alg_down = U * dn_bytes_e + P * I * 2 + P * D * 2
-    alg_step = U * (gu_bytes_e + dn_bytes_e) + B * D * 2 + 2 * P * I * 2 + B * D * 2  # SURVEY 8(d) config 1
+    # the expert step's algorithmic bytes: each distinct expert's weights once, x read, h written and
+    # read back, the combined rows written
+    alg_step = U * (gu_bytes_e + dn_bytes_e) + B * D * 2 + 2 * P * I * 2 + B * D * 2
     dom = "gate_up_swiglu"
     achieved = alg_gate_up / (kus[dom] * 1e-6) / 1e9
 
